@@ -1,0 +1,264 @@
+#!/usr/bin/env python3
+"""Quantized-weight matrix path on one MI355X: decode-step GEMV throughput.
+
+A step is one decode token through the matrix path of a model: every layer's
+projections (edgexpu_cpu_linear_quant for q, k, v, o, gate, up, down;
+src/native.c:2530-2580) followed by the chunked output.weight logits product
+with greedy argmax (src/native.c:2292-2401).  Weights are distinct per layer,
+seeded synthetic GGUF blocks resident in HBM before the timed region (so no
+two launches share cached weights), activations are synthetic f32 N(0,1).
+
+Prints one JSON line: value = algorithmic bytes of the step (weights + x + y)
+per second, a `roofline` object for the dominant kernel (the Q4_K x Q8_K GEMV
+at the [14336 x 4096] gate/up shape, timed with HIP events on its own stream)
+and a `cpu_baseline` object (the reference's own CPU kernels built from
+source, oracle/_ref, timed on this host's cores on a bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "edgexpu-llm_amd"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+
+WORKLOADS = {
+    # config 3: Llama-3-8B-shaped decode, all Q4_K, logits [128256 x 4096] in 8192-row chunks
+    "llama3-8b-q4k-decode": dict(layers=32, hidden=4096, qdim=4096, kv=1024, ffn=14336, vocab=128256,
+                                 wtype=12, down_type=12, logits_type=12, logits_chunk=8192),
+    # config 1: SmolLM2-135M-shaped decode, all Q8_0, logits [49152 x 576]
+    "smollm2-135m-q8_0-decode": dict(layers=30, hidden=576, qdim=576, kv=192, ffn=1536, vocab=49152,
+                                     wtype=8, down_type=8, logits_type=8, logits_chunk=0),
+    # config 4: Q4_K_M hybrid ~4B (Qwen3-4B-like projections assumed), Q6_K down + logits
+    "hybrid-4b-q4km-decode": dict(layers=36, hidden=2560, qdim=4096, kv=1024, ffn=9728, vocab=151936,
+                                  wtype=12, down_type=14, logits_type=14, logits_chunk=0),
+}
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--workload", default="llama3-8b-q4k-decode", choices=sorted(WORKLOADS))
+    p.add_argument("--batch", type=int, default=1, help="tokens per step (decode batch m)")
+    p.add_argument("--kernel-reps", type=int, default=4, help="passes over the layers for the per-kernel timing")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU-baseline sample")
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--seed", type=int, default=20261203)
+    return p.parse_args()
+
+
+def projections(cfg):
+    h, q, kv, f = cfg["hidden"], cfg["qdim"], cfg["kv"], cfg["ffn"]
+    t, td = cfg["wtype"], cfg["down_type"]
+    # (name, type, n_out, n_in, input vector)
+    return [("q", t, q, h, "h"), ("k", t, kv, h, "h"), ("v", t, kv, h, "h"), ("o", t, h, q, "q"),
+            ("gate", t, f, h, "h"), ("up", t, f, h, "h"), ("down", td, h, f, "f")]
+
+
+def cpu_info():
+    model = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return model
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the path shards by rows; "
+              "see DESIGN.md for the multi-GPU design)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import edgexpu_amd as E
+    from edgexpu_amd import synth
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    L = E.hip()
+    L.check(L.init(0), "init")
+    cfg = WORKLOADS[args.workload]
+    m = args.batch
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+
+    # ---------------------------------------------------------------- data in HBM
+    projs = projections(cfg)
+    layers = []
+    for _ in range(cfg["layers"]):
+        layers.append({name: synth.torch_weights_bulk(t, n_out, n_in, gen, dev)
+                       for name, t, n_out, n_in, _ in projs})
+    wout = synth.torch_weights_bulk(cfg["logits_type"], cfg["vocab"], cfg["hidden"], gen, dev)
+    xin = {"h": torch.randn((m, cfg["hidden"]), generator=gen, device=dev),
+           "q": torch.randn((m, cfg["qdim"]), generator=gen, device=dev),
+           "f": torch.randn((m, cfg["ffn"]), generator=gen, device=dev)}
+    yout = {name: torch.empty((m, n_out), device=dev) for name, _, n_out, _, _ in projs}
+    scores = torch.empty((m, cfg["vocab"]), device=dev)
+    best = torch.empty(m, dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()
+
+    step_bytes = 0
+    for name, t, n_out, n_in, _ in projs:
+        step_bytes += cfg["layers"] * (n_out * E.row_bytes(t, n_in) + m * n_in * 4 + m * n_out * 4)
+    step_bytes += cfg["vocab"] * E.row_bytes(cfg["logits_type"], cfg["hidden"]) + m * cfg["hidden"] * 4 \
+        + m * cfg["vocab"] * 4
+    weight_bytes = sum(cfg["layers"] * n_out * E.row_bytes(t, n_in) for _, t, n_out, n_in, _ in projs) \
+        + cfg["vocab"] * E.row_bytes(cfg["logits_type"], cfg["hidden"])
+
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+
+    def step():
+        for lw in layers:
+            for name, t, n_out, n_in, src in projs:
+                if not L.linear_dev(yout[name].data_ptr(), xin[src].data_ptr(), lw[name].data_ptr(), t, None, m,
+                                    n_out, n_in, sp):
+                    L.check(0, f"linear {name}")
+        if not L.logits_dev(scores.data_ptr(), best.data_ptr(), xin["h"].data_ptr(), wout.data_ptr(),
+                            cfg["logits_type"], None, m, cfg["vocab"], cfg["hidden"], cfg["logits_chunk"], sp):
+            L.check(0, "logits")
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = e0.elapsed_time(e1) / args.steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    # ------------------------------------------------ per-kernel timing (GEMV only)
+    def time_gemv(name, reps):
+        _, t, n_out, n_in, src = next(p for p in projs if p[0] == name)
+        xq = E.quantize_q8_0(xin[src]) if t == 8 else E.quantize_q8_k(xin[src])
+        out = yout[name]
+        for lw in layers[:2]:
+            L.check(L.gemv_q8_dev(out.data_ptr(), xq.data_ptr(), lw[name].data_ptr(), t, None, m, n_out, n_in, sp),
+                    "gemv")
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        n = 0
+        for _ in range(reps):
+            for lw in layers:  # distinct matrices: nothing is re-read from cache
+                L.gemv_q8_dev(out.data_ptr(), xq.data_ptr(), lw[name].data_ptr(), t, None, m, n_out, n_in, sp)
+                n += 1
+        b.record(stream)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / n
+        algo = n_out * E.row_bytes(t, n_in) + m * n_in * 4 + m * n_out * 4
+        return {"shape": [n_out, n_in], "type": E.TYPE_NAMES[t], "us": round(us, 3), "bytes": algo,
+                "GBps": round(algo / (us * 1e-6) / 1e9, 1)}
+
+    per_kernel = {name: time_gemv(name, args.kernel_reps) for name, *_ in projs}
+    # logits kernel alone (f32 path for K-quants, Q8_0 path otherwise), whole matrix per launch
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(5):
+        L.logits_dev(scores.data_ptr(), None, xin["h"].data_ptr(), wout.data_ptr(), cfg["logits_type"], None, m,
+                     cfg["vocab"], cfg["hidden"], cfg["vocab"], sp)
+    b.record(stream)
+    torch.cuda.synchronize()
+    lus = a.elapsed_time(b) * 1e3 / 5
+    lbytes = cfg["vocab"] * E.row_bytes(cfg["logits_type"], cfg["hidden"]) + m * cfg["hidden"] * 4 \
+        + m * cfg["vocab"] * 4
+    per_kernel["logits"] = {"shape": [cfg["vocab"], cfg["hidden"]], "type": E.TYPE_NAMES[cfg["logits_type"]],
+                            "us": round(lus, 3), "bytes": lbytes, "GBps": round(lbytes / (lus * 1e-6) / 1e9, 1)}
+
+    dom_name = "gate"
+    dom = per_kernel[dom_name]
+    roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": f"gemv_kernel<{E.TYPE_NAMES[cfg['wtype']]}> {dom['shape'][0]}x{dom['shape'][1]} m={m}",
+                "us_per_launch": dom["us"], "bytes_per_launch": dom["bytes"]}
+
+    # ---------------------------------------------------------------- CPU baseline
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(args, cfg, layers, xin, projs, m)
+
+    line = {
+        "metric": "quant GEMV weight GB/s (% of HBM peak) + prefill quant-GEMM TOPS, 1 GPU",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8" if cfg["wtype"] != 0 else "f32",
+        "data": "synthetic",
+        "config": {"workload": args.workload, "batch": m, "layers": cfg["layers"], "hidden": cfg["hidden"],
+                   "ffn": cfg["ffn"], "vocab": cfg["vocab"], "weights": E.TYPE_NAMES[cfg["wtype"]],
+                   "down": E.TYPE_NAMES[cfg["down_type"]], "logits": E.TYPE_NAMES[cfg["logits_type"]],
+                   "logits_chunk_rows": cfg["logits_chunk"], "step_bytes": step_bytes,
+                   "weight_bytes": weight_bytes, "hbm_frac_step": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": per_kernel,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(args, cfg, layers, xin, projs, m):
+    """The reference's CPU path (oracle/_ref, built from the reference sources)
+    on a bounded sample of the same workload: the dominant GEMV shape."""
+    import numpy as np
+
+    import oracle as O
+
+    ref = O.load_reference()
+    kind = "reference"
+    if ref is None:
+        ref, kind = O.load_oracle(), "port"
+    name = "gate"
+    _, t, n_out, n_in, src = next(p for p in projs if p[0] == name)
+    ws = [layers[i][name].cpu().numpy() for i in range(2)]
+    x = xin[src].cpu().numpy().astype(np.float32)
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    os.environ.setdefault("OMP_NUM_THREADS", str(threads))
+    ref.linear_quant_batch(x, ws[0], t, None, m, n_out, n_in)  # warm-up (and the reference's thread probe)
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < args.cpu_seconds / 2 or reps < 2:
+        ref.linear_quant_batch(x, ws[reps % 2], t, None, m, n_out, n_in)
+        reps += 1
+    dt = (time.perf_counter() - t0) / reps
+    algo = n_out * len(ws[0][0]) + m * n_in * 4 + m * n_out * 4
+    return {"value": round(algo / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": f"{'edgexpu_cpu_linear_quant_batch' if kind == 'reference' else 'ora_linear_quant_batch'} "
+                      f"{E_name(t)} [{n_out}x{n_in}] m={m}, {reps} calls over 2 distinct matrices, "
+                      f"{dt * 1e3:.2f} ms/call, OMP_NUM_THREADS={threads}",
+            "cpu": cpu_info()}
+
+
+def E_name(t):
+    return {8: "q8_0", 12: "q4_k", 14: "q6_k"}[t]
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,147 @@
+// Device-side helpers shared by the gfx950 kernels of the GGUF quantized-
+// weight path: block layouts, fp16 codecs with the reference's rounding, and
+// wavefront reductions.
+//
+// Block byte maps (little-endian), as laid out by the reference
+// (src/gguf_quant.c:17-26,138-302; src/gguf_dot_q8.c:18-26,98-110):
+//   Q8_0  34 B / 32 elem : fp16 d | int8 q[32]
+//   Q4_K 144 B / 256 elem: fp16 d | fp16 dmin | scales[12] (6-bit sc/m) | qs[128]
+//   Q6_K 210 B / 256 elem: ql[128] | qh[64] | int8 sc[16] | fp16 d
+//   Q8_K 292 B / 256 elem: f32 d | int8 q[256] | int16 bsums[16]
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace exq {
+
+constexpr int kTypeF32 = 0;
+constexpr int kTypeQ8_0 = 8;
+constexpr int kTypeQ4_K = 12;
+constexpr int kTypeQ6_K = 14;
+
+constexpr int kQK8_0 = 32;
+constexpr int kQKK = 256;
+constexpr int kBytesQ8_0 = 34;
+constexpr int kBytesQ4_K = 144;
+constexpr int kBytesQ6_K = 210;
+constexpr int kBytesQ8_K = 292;
+
+// Loads that tolerate the 2-byte alignment of Q8_0 / Q6_K blocks: gfx950
+// global memory runs in unaligned-access mode, so these become plain
+// global_load_dword{,x2,x4} instructions.
+template <typename T>
+__device__ __forceinline__ T ldg_unaligned(const uint8_t *p) {
+    T v;
+    __builtin_memcpy(&v, p, sizeof(T));
+    return v;
+}
+
+__device__ __forceinline__ uint4 ldg16(const uint8_t *p) { return ldg_unaligned<uint4>(p); }
+__device__ __forceinline__ uint2 ldg8(const uint8_t *p) { return ldg_unaligned<uint2>(p); }
+__device__ __forceinline__ uint32_t ldg4(const uint8_t *p) { return ldg_unaligned<uint32_t>(p); }
+
+// IEEE half -> float; exact for every input including subnormals.
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)(h & 0xffffu));
+    return (float)v;
+}
+
+// float -> IEEE half with round-to-nearest-even and gradual underflow, the
+// behaviour of F16C _mm_cvtps_ph(_MM_FROUND_TO_NEAREST_INT) that the
+// reference uses for the Q8_0 activation scale (src/gguf_dot_q8.c:33-35).
+// Done in integer arithmetic so it does not depend on the shader's float
+// mode register.
+__device__ __forceinline__ uint32_t f32_to_f16_rne(float f) {
+    uint32_t x = __float_as_uint(f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t a = x & 0x7fffffffu;
+    if (a > 0x7f800000u) return sign | 0x7e00u | ((a >> 13) & 0x3ffu);
+    if (a >= 0x477ff000u) return sign | 0x7c00u;
+    if (a >= 0x38800000u) {
+        uint32_t r = a - 0x38000000u;
+        r += 0x0fffu + ((r >> 13) & 1u);
+        return sign | (r >> 13);
+    }
+    if (a < 0x33000000u) return sign;
+    uint32_t e = a >> 23;
+    uint32_t mant = (a & 0x7fffffu) | 0x800000u;
+    uint32_t sh = 126u - e;
+    uint32_t q = mant >> sh;
+    uint32_t rem = mant & ((1u << sh) - 1u);
+    uint32_t half = 1u << (sh - 1u);
+    if (rem > half || (rem == half && (q & 1u))) q++;
+    return sign | q;
+}
+
+// Signed 8-bit 4-way dot product with accumulate (v_dot4_i32_i8).
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// 16-bit pair dot with accumulate: lo(a)*lo(b) + hi(a)*hi(b) + c, signed.
+__device__ __forceinline__ int sdot2(uint32_t a, uint32_t b, int c) {
+    typedef short short2_t __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, a), __builtin_bit_cast(short2_t, b), c, false);
+}
+
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) {
+    return __shfl_xor(v, mask, 64);
+}
+
+// Sum of V per-lane values over aligned groups of G lanes (G a power of two
+// <= 64).  On return vals[0] in every lane holds the group total of value
+// index vidx(lane), where the indices are distributed over the group's lanes
+// by the bit pattern the halving steps leave behind: after the call, lane l
+// owns value index ((l & (G-1)) / (G / min(V, G))) ... folded as computed by
+// out_index().  V must be a power of two.
+template <int V>
+__device__ __forceinline__ void group_reduce(float (&vals)[V], int G, int lane) {
+    int nv = V;
+    int off = G >> 1;
+    // Transposing halving steps: each exchange halves the number of live values.
+#pragma unroll
+    for (int step = V; step > 1; step >>= 1) {
+        if (off == 0) break;
+        const int half = step >> 1;
+        const bool upper = (lane & off) != 0;
+#pragma unroll
+        for (int k = 0; k < half; ++k) {
+            float send = upper ? vals[k] : vals[k + half];
+            float keep = upper ? vals[k + half] : vals[k];
+            vals[k] = keep + shfl_xor_f(send, off);
+        }
+        nv = half;
+        off >>= 1;
+    }
+    // Plain butterfly for the remaining group bits.
+    for (; off > 0; off >>= 1) {
+        vals[0] += shfl_xor_f(vals[0], off);
+    }
+    (void)nv;
+}
+
+// Value index lane `lane` owns after group_reduce<V>(…, G, …).
+__device__ __forceinline__ int group_reduce_index(int V, int G, int lane) {
+    int idx = 0;
+    int off = G >> 1;
+    for (int step = V; step > 1 && off > 0; step >>= 1) {
+        const int half = step >> 1;
+        if (lane & off) idx += half;
+        off >>= 1;
+    }
+    return idx;
+}
+
+// Number of distinct values that survive group_reduce<V> with group size G.
+__host__ __device__ constexpr int group_reduce_live(int V, int G) {
+    int nv = V;
+    int off = G >> 1;
+    while (nv > 1 && off > 0) {
+        nv >>= 1;
+        off >>= 1;
+    }
+    return nv;
+}
+
+}  // namespace exq

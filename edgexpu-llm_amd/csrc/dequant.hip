@@ -1,0 +1,137 @@
+// Bulk dequantization of GGUF blocks to f32 (edgexpu_gguf_dequantize,
+// src/gguf_quant.c:355-411).  Each thread writes 8 consecutive outputs with
+// two 16-byte stores, so a wavefront writes 2 KiB of contiguous f32.
+//
+// Bit-exactness: the reference x86 build is gcc -std=c11, which does not
+// contract a*b-c into an FMA.  This file is compiled with -ffp-contract=off
+// and keeps the reference's operation order:
+//   Q8_0  y = d * q                                  (src/gguf_quant.c:152)
+//   Q4_K  y = (d*sc) * q - (dmin*m)                  (src/gguf_quant.c:251-260)
+//   Q6_K  y = (d*sc) * (q-32)                        (src/gguf_quant.c:291-294)
+#include "common.h"
+
+namespace exq {
+
+__device__ __forceinline__ void store8(float *dst, const float (&y)[8]) {
+    float4 *p = reinterpret_cast<float4 *>(dst);
+    p[0] = make_float4(y[0], y[1], y[2], y[3]);
+    p[1] = make_float4(y[4], y[5], y[6], y[7]);
+}
+
+// 4 threads per 34-byte block.
+__global__ __launch_bounds__(256) void dequant_q8_0_kernel(const uint8_t *__restrict__ src,
+                                                           long long n_threads, float *__restrict__ dst) {
+    const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_threads) return;
+    const long long b = t >> 2;
+    const int p = (int)(t & 3);
+    const uint8_t *blk = src + b * kBytesQ8_0;
+    const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(blk));
+    const uint2 q = ldg8(blk + 2 + 8 * p);
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t w = e < 4 ? q.x : q.y;
+        const int8_t c = (int8_t)((w >> (8 * (e & 3))) & 0xff);
+        y[e] = d * (float)c;
+    }
+    store8(dst + b * kQK8_0 + 8 * p, y);
+}
+
+// 32 threads per 144-byte super-block; thread p covers elements 8p..8p+7,
+// which lie in sub-block s = p/4 (64-chunk j = s/2, nibble half s&1).
+__global__ __launch_bounds__(256) void dequant_q4_k_kernel(const uint8_t *__restrict__ src,
+                                                           long long n_threads, float *__restrict__ dst) {
+    const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_threads) return;
+    const long long b = t >> 5;
+    const int p = (int)(t & 31);
+    const uint8_t *sb = src + b * kBytesQ4_K;
+    const uint4 h = *reinterpret_cast<const uint4 *>(sb);  // d, dmin, scales[12]
+    const float d = f16_bits_to_f32(h.x & 0xffffu);
+    const float dmin = f16_bits_to_f32(h.x >> 16);
+    const int s = p >> 2;
+    // get_scale_min_k4 (src/gguf_quant.c:212-220) on the 12 scale bytes held in h.y,h.z,h.w
+    const uint32_t sw[3] = {h.y, h.z, h.w};
+    auto byte_at = [&](int i) -> int { return (int)((sw[i >> 2] >> (8 * (i & 3))) & 0xffu); };
+    int sc, mn;
+    if (s < 4) {
+        sc = byte_at(s) & 63;
+        mn = byte_at(s + 4) & 63;
+    } else {
+        sc = (byte_at(s + 4) & 0x0f) | ((byte_at(s - 4) >> 6) << 4);
+        mn = (byte_at(s + 4) >> 4) | ((byte_at(s) >> 6) << 4);
+    }
+    const float ds = d * (float)sc;
+    const float ms = dmin * (float)mn;
+    const int j = s >> 1;
+    const int shift = (s & 1) * 4;
+    const uint2 q = *reinterpret_cast<const uint2 *>(sb + 16 + 32 * j + 8 * (p & 3));
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t w = e < 4 ? q.x : q.y;
+        const int c = (int)((w >> (8 * (e & 3) + shift)) & 0x0fu);
+        const float prod = ds * (float)c;
+        y[e] = prod - ms;
+    }
+    store8(dst + b * kQKK + 8 * p, y);
+}
+
+// 32 threads per 210-byte super-block; thread p covers elements 8p..8p+7:
+// half h = p/16, quarter k = (p%16)/4, position l0 = 8*(p%4).
+__global__ __launch_bounds__(256) void dequant_q6_k_kernel(const uint8_t *__restrict__ src,
+                                                           long long n_threads, float *__restrict__ dst) {
+    const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_threads) return;
+    const long long b = t >> 5;
+    const int p = (int)(t & 31);
+    const uint8_t *sb = src + b * kBytesQ6_K;
+    const int h = p >> 4;
+    const int k = (p >> 2) & 3;
+    const int l0 = 8 * (p & 3);
+    const uint2 ql = ldg8(sb + 64 * h + 32 * (k & 1) + l0);
+    const uint2 qh = ldg8(sb + 128 + 32 * h + l0);
+    const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(sb + 208));
+    const float ds = d * (float)(int8_t)sb[192 + (p >> 1)];
+    const int nshift = (k >> 1) * 4;
+    const int hshift = 2 * k;
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t wl = e < 4 ? ql.x : ql.y;
+        const uint32_t wh = e < 4 ? qh.x : qh.y;
+        const int lo = (int)((wl >> (8 * (e & 3) + nshift)) & 0x0fu);
+        const int hi = (int)((wh >> (8 * (e & 3) + hshift)) & 0x03u);
+        y[e] = ds * (float)((lo | (hi << 4)) - 32);
+    }
+    store8(dst + b * kQKK + 8 * p, y);
+}
+
+}  // namespace exq
+
+using namespace exq;
+
+hipError_t launch_dequantize(const uint8_t *src, int type, unsigned long long n, float *dst, hipStream_t st) {
+    long long threads;
+    switch (type) {
+        case kTypeQ8_0:
+            threads = (long long)(n / kQK8_0) * 4;
+            hipLaunchKernelGGL(dequant_q8_0_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, src,
+                               threads, dst);
+            break;
+        case kTypeQ4_K:
+            threads = (long long)(n / kQKK) * 32;
+            hipLaunchKernelGGL(dequant_q4_k_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, src,
+                               threads, dst);
+            break;
+        case kTypeQ6_K:
+            threads = (long long)(n / kQKK) * 32;
+            hipLaunchKernelGGL(dequant_q6_k_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, src,
+                               threads, dst);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}

@@ -1,0 +1,581 @@
+// libedgexpu_hip.so: the thin C-ABI between the C host side and the gfx950
+// kernels.  Holds the per-process device state (one device, one stream, one
+// growable workspace, device staging for host-pointer calls) and the sticky
+// error, validates every argument before launching, and sequences the
+// quantize -> GEMV / dequant kernels of the quantized-weight path.
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "common.h"
+#include "edgexpu_hip.h"
+
+using namespace exq;
+
+// kernels (quantize.hip, dequant.hip, gemv.hip, gemm.hip)
+hipError_t launch_quantize_q8_0(const float *x, int m, int K, int ldx, uint8_t *packed, hipStream_t st);
+hipError_t launch_quantize_q8_k(const float *x, int m, int K, int ldx, uint8_t *packed, hipStream_t st);
+hipError_t launch_dequantize(const uint8_t *src, int type, unsigned long long n, float *dst, hipStream_t st);
+hipError_t launch_gemv_q8(int type, const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const uint8_t *xq,
+                          size_t xq_stride, const float *bias, float *out, int ldo, hipStream_t st);
+hipError_t launch_gemv_f32(int type, const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const float *xf,
+                           const float *xs, const float *bias, float *out, int ldo, hipStream_t st);
+hipError_t launch_xsum16(const float *x, int m, int K, float *xs, hipStream_t st);
+hipError_t launch_argmax_rows(const float *s, int m, int n, size_t lds, unsigned long long *partial, uint32_t *best,
+                              hipStream_t st);
+hipError_t launch_gemm_q8(int type, const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const uint8_t *xq,
+                          size_t xq_stride, const float *bias, float *out, int ldo, hipStream_t st);
+bool gemm_q8_supported(int type, int n_out, int K, int m);
+
+namespace {
+
+constexpr size_t kLogitChunkBytes = (size_t)48u * 1024u * 1024u;  // include/edgexpu/scheduler.h:34
+constexpr int kGemvMaxTokens = 8;
+constexpr int kGemmMinTokens = 64;
+constexpr int kArgmaxParts = 1024;
+
+struct State {
+    bool ready = false;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    void *ws = nullptr;  // device workspace (quantized activations, sums, argmax partials)
+    size_t ws_cap = 0;
+    void *dbuf = nullptr;  // device staging for host-pointer calls
+    size_t dbuf_cap = 0;
+    int err = 0;
+    char msg[512] = {0};
+};
+
+State g;
+
+void set_error(int code, const char *fmt, ...) {
+    if (g.err != 0) return;  // sticky: keep the first error
+    g.err = code != 0 ? code : -1;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g.msg, sizeof(g.msg), fmt, ap);
+    va_end(ap);
+    fprintf(stderr, "edgexpu_hip: %s\n", g.msg);
+}
+
+bool hip_ok(hipError_t e, const char *what) {
+    if (e == hipSuccess) return true;
+    set_error((int)e, "%s: %s", what, hipGetErrorString(e));
+    return false;
+}
+
+bool ensure_init() {
+    if (g.ready) return true;
+    return edgexpu_hip_init(0) != 0;
+}
+
+hipStream_t pick_stream(void *s) { return s != nullptr ? (hipStream_t)s : g.stream; }
+
+bool gpu_type(uint32_t t) { return t == kTypeQ8_0 || t == kTypeQ4_K || t == kTypeQ6_K; }
+
+size_t block_elems(uint32_t t) { return t == kTypeQ8_0 ? (size_t)kQK8_0 : (size_t)kQKK; }
+
+size_t block_bytes(uint32_t t) {
+    return t == kTypeQ8_0 ? (size_t)kBytesQ8_0 : (t == kTypeQ4_K ? (size_t)kBytesQ4_K : (size_t)kBytesQ6_K);
+}
+
+// Bytes of one token's quantized activation: Q8_0 blocks for Q8_0 weights,
+// Q8_K blocks for the K-quants (src/cpu_kernel.c:577-631).
+size_t act_bytes(uint32_t t, int K) {
+    return t == kTypeQ8_0 ? (size_t)(K / kQK8_0) * kBytesQ8_0 : (size_t)(K / kQKK) * kBytesQ8_K;
+}
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Device workspace grown on demand (freed only at shutdown).
+void *workspace(size_t bytes) {
+    if (bytes <= g.ws_cap) return g.ws;
+    if (g.ws != nullptr) {
+        // kernels on any stream may still read the old buffer
+        if (!hip_ok(hipDeviceSynchronize(), "workspace sync")) return nullptr;
+        (void)hipFree(g.ws);
+        g.ws = nullptr;
+        g.ws_cap = 0;
+    }
+    size_t cap = align_up(bytes, (size_t)1 << 20);
+    if (!hip_ok(hipMalloc(&g.ws, cap), "hipMalloc workspace")) return nullptr;
+    g.ws_cap = cap;
+    return g.ws;
+}
+
+void *devbuf(size_t bytes) {
+    if (bytes <= g.dbuf_cap) return g.dbuf;
+    if (g.dbuf != nullptr) {
+        if (!hip_ok(hipDeviceSynchronize(), "staging sync")) return nullptr;
+        (void)hipFree(g.dbuf);
+        g.dbuf = nullptr;
+        g.dbuf_cap = 0;
+    }
+    size_t cap = align_up(bytes, (size_t)1 << 20);
+    if (!hip_ok(hipMalloc(&g.dbuf, cap), "hipMalloc staging")) return nullptr;
+    g.dbuf_cap = cap;
+    return g.dbuf;
+}
+
+// Workspace carve-up for m tokens of K elements.
+struct ActWs {
+    uint8_t *xq;               // m * act_bytes   quantized activations
+    float *xs;                 // m * K/16        16-element sums of f32 x (f32 logits path)
+    unsigned long long *keys;  // m * 1024        argmax partials
+};
+
+bool act_ws(uint32_t type, int m, int K, ActWs &a) {
+    const size_t qb = align_up((size_t)m * act_bytes(type, K), 256);
+    const size_t sb = align_up((size_t)m * (K / 16) * sizeof(float), 256);
+    const size_t kb = align_up((size_t)m * kArgmaxParts * sizeof(unsigned long long), 256);
+    uint8_t *base = (uint8_t *)workspace(qb + sb + kb);
+    if (base == nullptr) return false;
+    a.xq = base;
+    a.xs = (float *)(base + qb);
+    a.keys = (unsigned long long *)(base + qb + sb);
+    return true;
+}
+
+bool check_linear_args(const void *out, const void *x, const void *w, uint32_t type, int m, int n_out, int n_in,
+                       const char *who) {
+    if (out == nullptr || x == nullptr || w == nullptr || m <= 0 || n_out <= 0 || n_in <= 0) {
+        set_error(-2, "%s: null buffer or non-positive size (m=%d n_out=%d n_in=%d)", who, m, n_out, n_in);
+        return false;
+    }
+    if (!gpu_type(type)) {
+        set_error(-3, "%s: GGUF type %u is not supported on the GPU (Q8_0/Q4_K/Q6_K only)", who, type);
+        return false;
+    }
+    if ((size_t)n_in % block_elems(type) != 0) {
+        set_error(-2, "%s: n_in=%d is not a multiple of the type-%u block (%zu)", who, n_in, type, block_elems(type));
+        return false;
+    }
+    return true;
+}
+
+// GEMV (m <= 8 per launch) or MFMA GEMM over already-quantized activations.
+bool run_q8_product(uint32_t type, const void *w, int n_out, int n_in, int m, const uint8_t *xq, const float *bias,
+                    float *out, int ldo, hipStream_t st) {
+    const size_t rb = edgexpu_hip_row_bytes(type, n_in);
+    const size_t ab = act_bytes(type, n_in);
+    if (m >= kGemmMinTokens && gemm_q8_supported((int)type, n_out, n_in, m)) {
+        return hip_ok(launch_gemm_q8((int)type, (const uint8_t *)w, rb, n_out, n_in, m, xq, ab, bias, out, ldo, st),
+                      "gemm_q8");
+    }
+    for (int t0 = 0; t0 < m; t0 += kGemvMaxTokens) {
+        const int mt = m - t0 < kGemvMaxTokens ? m - t0 : kGemvMaxTokens;
+        if (!hip_ok(launch_gemv_q8((int)type, (const uint8_t *)w, rb, n_out, n_in, mt, xq + (size_t)t0 * ab, ab,
+                                   bias, out + (size_t)t0 * ldo, ldo, st),
+                    "gemv_q8"))
+            return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+struct edgexpu_hip_weight {
+    void *data;
+    float *bias;
+    uint32_t type;
+    int n_out;
+    int n_in;
+    bool owned;
+};
+
+extern "C" {
+
+int edgexpu_hip_init(int device) {
+    if (g.ready) {
+        if (device == g.device) return 1;
+        set_error(-4, "edgexpu_hip_init: already initialised on device %d", g.device);
+        return 0;
+    }
+    int n = 0;
+    if (!hip_ok(hipGetDeviceCount(&n), "hipGetDeviceCount")) return 0;
+    if (device < 0 || device >= n) {
+        set_error(-4, "edgexpu_hip_init: device %d out of range (%d devices)", device, n);
+        return 0;
+    }
+    if (!hip_ok(hipSetDevice(device), "hipSetDevice")) return 0;
+    if (!hip_ok(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking), "hipStreamCreate")) return 0;
+    g.device = device;
+    g.ready = true;
+    return 1;
+}
+
+void edgexpu_hip_shutdown(void) {
+    if (!g.ready) return;
+    (void)hipDeviceSynchronize();
+    if (g.ws) (void)hipFree(g.ws);
+    if (g.dbuf) (void)hipFree(g.dbuf);
+    (void)hipStreamDestroy(g.stream);
+    const int err = g.err;
+    char msg[sizeof(g.msg)];
+    memcpy(msg, g.msg, sizeof(msg));
+    g = State();
+    g.err = err;
+    memcpy(g.msg, msg, sizeof(msg));
+}
+
+int edgexpu_hip_last_error(char *buf, size_t size) {
+    if (buf != nullptr && size > 0) snprintf(buf, size, "%s", g.err ? g.msg : "");
+    return g.err;
+}
+
+void edgexpu_hip_clear_error(void) {
+    g.err = 0;
+    g.msg[0] = 0;
+}
+
+int edgexpu_hip_supports_type(uint32_t type) { return gpu_type(type) ? 1 : 0; }
+
+int edgexpu_hip_synchronize(void) {
+    if (!ensure_init()) return 0;
+    return hip_ok(hipStreamSynchronize(g.stream), "hipStreamSynchronize") ? 1 : 0;
+}
+
+void *edgexpu_hip_stream(void) {
+    if (!ensure_init()) return nullptr;
+    return (void *)g.stream;
+}
+
+size_t edgexpu_hip_row_bytes(uint32_t type, int n_in) {
+    if (!gpu_type(type) || n_in <= 0 || (size_t)n_in % block_elems(type) != 0) return 0;
+    return (size_t)n_in / block_elems(type) * block_bytes(type);
+}
+
+// ------------------------------------------------------------------ weights
+
+edgexpu_hip_weight *edgexpu_hip_weight_upload(const uint8_t *blocks, uint32_t type, int n_out, int n_in,
+                                              const float *bias) {
+    if (!ensure_init()) return nullptr;
+    const size_t rb = edgexpu_hip_row_bytes(type, n_in);
+    if (blocks == nullptr || n_out <= 0 || rb == 0) {
+        set_error(-2, "edgexpu_hip_weight_upload: bad arguments (type=%u n_out=%d n_in=%d)", type, n_out, n_in);
+        return nullptr;
+    }
+    edgexpu_hip_weight *w = (edgexpu_hip_weight *)calloc(1, sizeof(edgexpu_hip_weight));
+    if (w == nullptr) {
+        set_error(-5, "edgexpu_hip_weight_upload: out of host memory");
+        return nullptr;
+    }
+    const size_t nbytes = rb * (size_t)n_out;
+    if (!hip_ok(hipMalloc(&w->data, align_up(nbytes, 256)), "hipMalloc weight")) {
+        free(w);
+        return nullptr;
+    }
+    if (!hip_ok(hipMemcpy(w->data, blocks, nbytes, hipMemcpyHostToDevice), "upload weight")) {
+        (void)hipFree(w->data);
+        free(w);
+        return nullptr;
+    }
+    if (bias != nullptr) {
+        if (!hip_ok(hipMalloc((void **)&w->bias, (size_t)n_out * sizeof(float)), "hipMalloc bias") ||
+            !hip_ok(hipMemcpy(w->bias, bias, (size_t)n_out * sizeof(float), hipMemcpyHostToDevice), "upload bias")) {
+            if (w->bias) (void)hipFree(w->bias);
+            (void)hipFree(w->data);
+            free(w);
+            return nullptr;
+        }
+    }
+    w->type = type;
+    w->n_out = n_out;
+    w->n_in = n_in;
+    w->owned = true;
+    return w;
+}
+
+edgexpu_hip_weight *edgexpu_hip_weight_wrap(const void *dev_blocks, uint32_t type, int n_out, int n_in,
+                                            const float *dev_bias) {
+    if (dev_blocks == nullptr || n_out <= 0 || edgexpu_hip_row_bytes(type, n_in) == 0) {
+        set_error(-2, "edgexpu_hip_weight_wrap: bad arguments (type=%u n_out=%d n_in=%d)", type, n_out, n_in);
+        return nullptr;
+    }
+    edgexpu_hip_weight *w = (edgexpu_hip_weight *)calloc(1, sizeof(edgexpu_hip_weight));
+    if (w == nullptr) {
+        set_error(-5, "edgexpu_hip_weight_wrap: out of host memory");
+        return nullptr;
+    }
+    w->data = (void *)dev_blocks;
+    w->bias = (float *)dev_bias;
+    w->type = type;
+    w->n_out = n_out;
+    w->n_in = n_in;
+    w->owned = false;
+    return w;
+}
+
+void edgexpu_hip_weight_free(edgexpu_hip_weight *w) {
+    if (w == nullptr) return;
+    if (w->owned) {
+        if (g.ready) (void)hipDeviceSynchronize();
+        (void)hipFree(w->data);
+        if (w->bias) (void)hipFree(w->bias);
+    }
+    free(w);
+}
+
+const void *edgexpu_hip_weight_data(const edgexpu_hip_weight *w) { return w ? w->data : nullptr; }
+uint32_t edgexpu_hip_weight_type(const edgexpu_hip_weight *w) { return w ? w->type : 0u; }
+int edgexpu_hip_weight_n_out(const edgexpu_hip_weight *w) { return w ? w->n_out : 0; }
+int edgexpu_hip_weight_n_in(const edgexpu_hip_weight *w) { return w ? w->n_in : 0; }
+
+// ------------------------------------------------------------ device entries
+
+int edgexpu_hip_linear_quant_batch_dev(float *out, const float *x, const void *w, uint32_t type, const float *bias,
+                                       int m, int n_out, int n_in, void *stream) {
+    if (!ensure_init()) return 0;
+    if (!check_linear_args(out, x, w, type, m, n_out, n_in, "linear_quant_batch")) return 0;
+    if (!aligned16(x)) {
+        set_error(-2, "linear_quant_batch: x must be 16-byte aligned");
+        return 0;
+    }
+    hipStream_t st = pick_stream(stream);
+    ActWs a;
+    if (!act_ws(type, m, n_in, a)) return 0;
+    const hipError_t e = type == kTypeQ8_0 ? launch_quantize_q8_0(x, m, n_in, n_in, a.xq, st)
+                                           : launch_quantize_q8_k(x, m, n_in, n_in, a.xq, st);
+    if (!hip_ok(e, "quantize activations")) return 0;
+    return run_q8_product(type, w, n_out, n_in, m, a.xq, bias, out, n_out, st) ? 1 : 0;
+}
+
+int edgexpu_hip_gemv_q8_dev(float *out, const uint8_t *xq, const void *w, uint32_t type, const float *bias, int m,
+                            int n_out, int n_in, void *stream) {
+    if (!ensure_init()) return 0;
+    if (!check_linear_args(out, xq, w, type, m, n_out, n_in, "gemv_q8")) return 0;
+    return run_q8_product(type, w, n_out, n_in, m, xq, bias, out, n_out, pick_stream(stream)) ? 1 : 0;
+}
+
+int edgexpu_hip_logits_dev(float *scores, uint32_t *best_dev, const float *hidden, const void *w, uint32_t type,
+                           const float *bias, int m, int vocab, int n_embd, int chunk_rows, void *stream) {
+    if (!ensure_init()) return 0;
+    if (!check_linear_args(scores, hidden, w, type, m, vocab, n_embd, "logits")) return 0;
+    if (m > kGemvMaxTokens) {
+        set_error(-2, "logits: at most %d hidden vectors per call (m=%d)", kGemvMaxTokens, m);
+        return 0;
+    }
+    if (!aligned16(hidden)) {
+        set_error(-2, "logits: hidden must be 16-byte aligned");
+        return 0;
+    }
+    hipStream_t st = pick_stream(stream);
+    const size_t rb = edgexpu_hip_row_bytes(type, n_embd);
+    size_t chunk = chunk_rows > 0 ? (size_t)chunk_rows : kLogitChunkBytes / rb;
+    if (chunk < 1) chunk = 1;
+    ActWs a;
+    if (!act_ws(type, m, n_embd, a)) return 0;
+    if (type == kTypeQ8_0) {
+        // src/native.c:2317-2319: Q8_0 output weights use the Q8_0-activation dot
+        if (!hip_ok(launch_quantize_q8_0(hidden, m, n_embd, n_embd, a.xq, st), "quantize_q8_0")) return 0;
+    } else {
+        // K-quant output weights use the f32-activation dots (src/native.c:445-462)
+        if (!hip_ok(launch_xsum16(hidden, m, n_embd, a.xs, st), "xsum16")) return 0;
+    }
+    for (size_t r0 = 0; r0 < (size_t)vocab; r0 += chunk) {
+        const int rows = (int)((size_t)vocab - r0 < chunk ? (size_t)vocab - r0 : chunk);
+        const uint8_t *wc = (const uint8_t *)w + r0 * rb;
+        const float *bc = bias != nullptr ? bias + r0 : nullptr;
+        const hipError_t e =
+            type == kTypeQ8_0
+                ? launch_gemv_q8((int)type, wc, rb, rows, n_embd, m, a.xq, act_bytes(type, n_embd), bc, scores + r0,
+                                 vocab, st)
+                : launch_gemv_f32((int)type, wc, rb, rows, n_embd, m, hidden, a.xs, bc, scores + r0, vocab, st);
+        if (!hip_ok(e, "logits gemv")) return 0;
+    }
+    if (best_dev != nullptr &&
+        !hip_ok(launch_argmax_rows(scores, m, vocab, (size_t)vocab, a.keys, best_dev, st), "argmax"))
+        return 0;
+    return 1;
+}
+
+int edgexpu_hip_dequantize_dev(const void *src, uint32_t type, uint64_t n_elements, float *dst, void *stream) {
+    if (!ensure_init()) return 0;
+    if (src == nullptr || dst == nullptr || n_elements == 0) {
+        set_error(-2, "dequantize: null buffer or zero elements");
+        return 0;
+    }
+    if (!gpu_type(type)) {
+        set_error(-3, "dequantize: GGUF type %u is not supported on the GPU (Q8_0/Q4_K/Q6_K only)", type);
+        return 0;
+    }
+    if (n_elements % block_elems(type) != 0) {
+        set_error(-2, "dequantize: %llu elements is not a multiple of the type-%u block",
+                  (unsigned long long)n_elements, type);
+        return 0;
+    }
+    if (!aligned16(dst)) {
+        set_error(-2, "dequantize: dst must be 16-byte aligned");
+        return 0;
+    }
+    return hip_ok(launch_dequantize((const uint8_t *)src, (int)type, n_elements, dst, pick_stream(stream)),
+                  "dequantize")
+               ? 1
+               : 0;
+}
+
+static int quantize_dev(const float *x, int m, int n, uint8_t *dst, void *stream, bool k_quant) {
+    if (!ensure_init()) return 0;
+    const int qk = k_quant ? kQKK : kQK8_0;
+    if (x == nullptr || dst == nullptr || m <= 0 || n <= 0 || n % qk != 0) {
+        set_error(-2, "quantize_q8_%s: bad arguments (m=%d n=%d)", k_quant ? "k" : "0", m, n);
+        return 0;
+    }
+    if (!aligned16(x) || (k_quant && ((uintptr_t)dst & 3u) != 0) || (!k_quant && ((uintptr_t)dst & 1u) != 0)) {
+        set_error(-2, "quantize: x must be 16-byte and dst %d-byte aligned", k_quant ? 4 : 2);
+        return 0;
+    }
+    hipStream_t st = pick_stream(stream);
+    const hipError_t e = k_quant ? launch_quantize_q8_k(x, m, n, n, dst, st) : launch_quantize_q8_0(x, m, n, n, dst, st);
+    return hip_ok(e, "quantize") ? 1 : 0;
+}
+
+int edgexpu_hip_quantize_q8_0_dev(const float *x, int m, int n, uint8_t *dst, void *stream) {
+    return quantize_dev(x, m, n, dst, stream, false);
+}
+
+int edgexpu_hip_quantize_q8_k_dev(const float *x, int m, int n, uint8_t *dst, void *stream) {
+    return quantize_dev(x, m, n, dst, stream, true);
+}
+
+// ------------------------------------------------------------ host entries
+
+int edgexpu_hip_linear_quant_batch(float *out, const float *x, const edgexpu_hip_weight *w, int m) {
+    if (!ensure_init()) return 0;
+    if (w == nullptr || out == nullptr || x == nullptr || m <= 0) {
+        set_error(-2, "linear_quant_batch: null argument or m <= 0");
+        return 0;
+    }
+    const size_t xb = align_up((size_t)m * w->n_in * sizeof(float), 256);
+    const size_t ob = (size_t)m * w->n_out * sizeof(float);
+    uint8_t *d = (uint8_t *)devbuf(xb + ob);
+    if (d == nullptr) return 0;
+    if (!hip_ok(hipMemcpyAsync(d, x, (size_t)m * w->n_in * sizeof(float), hipMemcpyHostToDevice, g.stream), "H2D x"))
+        return 0;
+    if (!edgexpu_hip_linear_quant_batch_dev((float *)(d + xb), (const float *)d, w->data, w->type, w->bias, m,
+                                            w->n_out, w->n_in, nullptr))
+        return 0;
+    if (!hip_ok(hipMemcpyAsync(out, d + xb, ob, hipMemcpyDeviceToHost, g.stream), "D2H out")) return 0;
+    return hip_ok(hipStreamSynchronize(g.stream), "sync") ? 1 : 0;
+}
+
+int edgexpu_hip_linear_quant_batch_host(float *out, const float *x, const uint8_t *weight, uint32_t type,
+                                        const float *bias, int m, int n_out, int n_in) {
+    if (!ensure_init()) return 0;
+    if (!check_linear_args(out, x, weight, type, m, n_out, n_in, "linear_quant_batch")) return 0;
+    edgexpu_hip_weight *w = edgexpu_hip_weight_upload(weight, type, n_out, n_in, bias);
+    if (w == nullptr) return 0;
+    const int ok = edgexpu_hip_linear_quant_batch(out, x, w, m);
+    edgexpu_hip_weight_free(w);
+    return ok;
+}
+
+int edgexpu_hip_logits(float *scores, uint32_t *best, const float *hidden, const edgexpu_hip_weight *w,
+                       int chunk_rows) {
+    if (!ensure_init()) return 0;
+    if (w == nullptr || hidden == nullptr) {
+        set_error(-2, "logits: null argument");
+        return 0;
+    }
+    const size_t hb = align_up((size_t)w->n_in * sizeof(float), 256);
+    const size_t sb = align_up((size_t)w->n_out * sizeof(float), 256);
+    uint8_t *d = (uint8_t *)devbuf(hb + sb + 256);
+    if (d == nullptr) return 0;
+    float *dh = (float *)d;
+    float *ds = (float *)(d + hb);
+    uint32_t *dbest = (uint32_t *)(d + hb + sb);
+    if (!hip_ok(hipMemcpyAsync(dh, hidden, (size_t)w->n_in * sizeof(float), hipMemcpyHostToDevice, g.stream), "H2D"))
+        return 0;
+    if (!edgexpu_hip_logits_dev(ds, dbest, dh, w->data, w->type, w->bias, 1, w->n_out, w->n_in, chunk_rows, nullptr))
+        return 0;
+    if (scores != nullptr &&
+        !hip_ok(hipMemcpyAsync(scores, ds, (size_t)w->n_out * sizeof(float), hipMemcpyDeviceToHost, g.stream), "D2H"))
+        return 0;
+    uint32_t b = 0;
+    if (!hip_ok(hipMemcpyAsync(&b, dbest, sizeof(b), hipMemcpyDeviceToHost, g.stream), "D2H best")) return 0;
+    if (!hip_ok(hipStreamSynchronize(g.stream), "sync")) return 0;
+    if (best != nullptr) *best = b;
+    return 1;
+}
+
+int edgexpu_hip_dequantize(const uint8_t *src, uint32_t type, uint64_t n_elements, float *dst) {
+    if (!ensure_init()) return 0;
+    if (src == nullptr || dst == nullptr || n_elements == 0 || !gpu_type(type) ||
+        n_elements % block_elems(type) != 0) {
+        set_error(-2, "dequantize: bad arguments (type=%u n=%llu)", type, (unsigned long long)n_elements);
+        return 0;
+    }
+    const size_t sbytes = (size_t)(n_elements / block_elems(type)) * block_bytes(type);
+    const size_t so = align_up(sbytes, 256);
+    uint8_t *d = (uint8_t *)devbuf(so + (size_t)n_elements * sizeof(float));
+    if (d == nullptr) return 0;
+    if (!hip_ok(hipMemcpyAsync(d, src, sbytes, hipMemcpyHostToDevice, g.stream), "H2D src")) return 0;
+    if (!edgexpu_hip_dequantize_dev(d, type, n_elements, (float *)(d + so), nullptr)) return 0;
+    if (!hip_ok(hipMemcpyAsync(dst, d + so, (size_t)n_elements * sizeof(float), hipMemcpyDeviceToHost, g.stream),
+                "D2H dst"))
+        return 0;
+    return hip_ok(hipStreamSynchronize(g.stream), "sync") ? 1 : 0;
+}
+
+static int quantize_host(const float *x, int n, uint8_t *dst, bool k_quant) {
+    if (!ensure_init()) return 0;
+    const int qk = k_quant ? kQKK : kQK8_0;
+    if (x == nullptr || dst == nullptr || n <= 0 || n % qk != 0) {
+        set_error(-2, "quantize: bad arguments (n=%d)", n);
+        return 0;
+    }
+    const size_t qb = (size_t)(n / qk) * (k_quant ? kBytesQ8_K : kBytesQ8_0);
+    const size_t xo = align_up((size_t)n * sizeof(float), 256);
+    uint8_t *d = (uint8_t *)devbuf(xo + qb);
+    if (d == nullptr) return 0;
+    if (!hip_ok(hipMemcpyAsync(d, x, (size_t)n * sizeof(float), hipMemcpyHostToDevice, g.stream), "H2D x")) return 0;
+    if (!quantize_dev((const float *)d, 1, n, d + xo, nullptr, k_quant)) return 0;
+    if (!hip_ok(hipMemcpyAsync(dst, d + xo, qb, hipMemcpyDeviceToHost, g.stream), "D2H q")) return 0;
+    return hip_ok(hipStreamSynchronize(g.stream), "sync") ? 1 : 0;
+}
+
+int edgexpu_hip_quantize_q8_0(const float *x, int n, uint8_t *dst) { return quantize_host(x, n, dst, false); }
+int edgexpu_hip_quantize_q8_k(const float *x, int n, uint8_t *dst) { return quantize_host(x, n, dst, true); }
+
+int edgexpu_hip_dot_f32_rows(float *out, const uint8_t *w, uint32_t type, const float *x, int rows, int n) {
+    if (!ensure_init()) return 0;
+    if (!check_linear_args(out, x, w, type, 1, rows, n, "dot_f32_rows")) return 0;
+    const size_t rb = edgexpu_hip_row_bytes(type, n);
+    const size_t wo = align_up(rb * (size_t)rows, 256);
+    const size_t xo = align_up((size_t)n * sizeof(float), 256);
+    uint8_t *d = (uint8_t *)devbuf(wo + xo + align_up((size_t)rows * sizeof(float), 256));
+    if (d == nullptr) return 0;
+    float *dx = (float *)(d + wo);
+    float *dout = (float *)(d + wo + xo);
+    if (!hip_ok(hipMemcpyAsync(d, w, rb * (size_t)rows, hipMemcpyHostToDevice, g.stream), "H2D w")) return 0;
+    if (!hip_ok(hipMemcpyAsync(dx, x, (size_t)n * sizeof(float), hipMemcpyHostToDevice, g.stream), "H2D x")) return 0;
+    if (!edgexpu_hip_logits_dev(dout, nullptr, dx, d, type, nullptr, 1, rows, n, 0, nullptr)) return 0;
+    if (!hip_ok(hipMemcpyAsync(out, dout, (size_t)rows * sizeof(float), hipMemcpyDeviceToHost, g.stream), "D2H"))
+        return 0;
+    return hip_ok(hipStreamSynchronize(g.stream), "sync") ? 1 : 0;
+}
+
+int edgexpu_hip_dot_q8_rows(float *out, const uint8_t *w, uint32_t type, const uint8_t *xq, int rows, int n) {
+    if (!ensure_init()) return 0;
+    if (!check_linear_args(out, xq, w, type, 1, rows, n, "dot_q8_rows")) return 0;
+    const size_t rb = edgexpu_hip_row_bytes(type, n);
+    const size_t xb = act_bytes(type, n);
+    const size_t wo = align_up(rb * (size_t)rows, 256);
+    const size_t xo = align_up(xb, 256);
+    uint8_t *d = (uint8_t *)devbuf(wo + xo + align_up((size_t)rows * sizeof(float), 256));
+    if (d == nullptr) return 0;
+    float *dout = (float *)(d + wo + xo);
+    if (!hip_ok(hipMemcpyAsync(d, w, rb * (size_t)rows, hipMemcpyHostToDevice, g.stream), "H2D w")) return 0;
+    if (!hip_ok(hipMemcpyAsync(d + wo, xq, xb, hipMemcpyHostToDevice, g.stream), "H2D xq")) return 0;
+    if (!edgexpu_hip_gemv_q8_dev(dout, d + wo, d, type, nullptr, 1, rows, n, nullptr)) return 0;
+    if (!hip_ok(hipMemcpyAsync(out, dout, (size_t)rows * sizeof(float), hipMemcpyDeviceToHost, g.stream), "D2H"))
+        return 0;
+    return hip_ok(hipStreamSynchronize(g.stream), "sync") ? 1 : 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,196 @@
+"""Python front end of the MI355X quantized-weight path.
+
+Thin ctypes bindings over the C-ABI of ``lib/libedgexpu_hip.so`` (declared in
+``include/edgexpu_hip.h``) and ``lib/libedgexpu_kernels.so`` (the reference-named
+drop-in set, ``include/edgexpu_kernels.h``).  torch supplies device memory and
+streams only; every computation is a HIP kernel of the shared library.  When the
+library is missing this module raises instead of falling back to anything.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_DIR = os.path.join(PKG_DIR, "lib")
+HIP_SO = os.path.join(LIB_DIR, "libedgexpu_hip.so")
+KERNELS_SO = os.path.join(LIB_DIR, "libedgexpu_kernels.so")
+
+F32, F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 2, 6, 8, 12, 13, 14
+# (elements per block, bytes per block); Q8_K is the activation format
+BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+Q8_K_BLOCK = (256, 292)
+TYPE_NAMES = {Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k"}
+
+
+class HipError(RuntimeError):
+    pass
+
+
+def row_bytes(qtype: int, n: int) -> int:
+    bs, bb = BLOCK[qtype]
+    if n % bs:
+        raise ValueError(f"n={n} not a multiple of {bs}")
+    return n // bs * bb
+
+
+_vp = C.c_void_p
+_u8p = C.POINTER(C.c_uint8)
+_f32p = C.POINTER(C.c_float)
+
+
+def _sig(lib, name, restype, argtypes):
+    f = getattr(lib, name)
+    f.restype = restype
+    f.argtypes = argtypes
+    return f
+
+
+class HipLib:
+    """Bindings of include/edgexpu_hip.h."""
+
+    def __init__(self, path: str = HIP_SO):
+        if not os.path.exists(path):
+            raise HipError(f"{path} is missing: build it with `make -C edgexpu-llm_amd` "
+                           "(or __graft_entry__.build()); there is no fallback path")
+        self.path = path
+        self.lib = C.CDLL(path)
+        L = self.lib
+        self.init = _sig(L, "edgexpu_hip_init", C.c_int, [C.c_int])
+        self.shutdown = _sig(L, "edgexpu_hip_shutdown", None, [])
+        self._last_error = _sig(L, "edgexpu_hip_last_error", C.c_int, [C.c_char_p, C.c_size_t])
+        self.clear_error = _sig(L, "edgexpu_hip_clear_error", None, [])
+        self.supports_type = _sig(L, "edgexpu_hip_supports_type", C.c_int, [C.c_uint32])
+        self.synchronize = _sig(L, "edgexpu_hip_synchronize", C.c_int, [])
+        self.stream = _sig(L, "edgexpu_hip_stream", _vp, [])
+        self.row_bytes = _sig(L, "edgexpu_hip_row_bytes", C.c_size_t, [C.c_uint32, C.c_int])
+        self.weight_upload = _sig(L, "edgexpu_hip_weight_upload", _vp, [_vp, C.c_uint32, C.c_int, C.c_int, _vp])
+        self.weight_wrap = _sig(L, "edgexpu_hip_weight_wrap", _vp, [_vp, C.c_uint32, C.c_int, C.c_int, _vp])
+        self.weight_free = _sig(L, "edgexpu_hip_weight_free", None, [_vp])
+        self.linear_dev = _sig(L, "edgexpu_hip_linear_quant_batch_dev", C.c_int,
+                               [_vp, _vp, _vp, C.c_uint32, _vp, C.c_int, C.c_int, C.c_int, _vp])
+        self.gemv_q8_dev = _sig(L, "edgexpu_hip_gemv_q8_dev", C.c_int,
+                                [_vp, _vp, _vp, C.c_uint32, _vp, C.c_int, C.c_int, C.c_int, _vp])
+        self.logits_dev = _sig(L, "edgexpu_hip_logits_dev", C.c_int,
+                               [_vp, _vp, _vp, _vp, C.c_uint32, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp])
+        self.dequant_dev = _sig(L, "edgexpu_hip_dequantize_dev", C.c_int, [_vp, C.c_uint32, C.c_uint64, _vp, _vp])
+        self.q80_dev = _sig(L, "edgexpu_hip_quantize_q8_0_dev", C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp])
+        self.q8k_dev = _sig(L, "edgexpu_hip_quantize_q8_k_dev", C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp])
+        self.linear_host_w = _sig(L, "edgexpu_hip_linear_quant_batch", C.c_int, [_vp, _vp, _vp, C.c_int])
+        self.linear_host = _sig(L, "edgexpu_hip_linear_quant_batch_host", C.c_int,
+                                [_vp, _vp, _vp, C.c_uint32, _vp, C.c_int, C.c_int, C.c_int])
+        self.logits_host = _sig(L, "edgexpu_hip_logits", C.c_int, [_vp, C.POINTER(C.c_uint32), _vp, _vp, C.c_int])
+        self.dequant_host = _sig(L, "edgexpu_hip_dequantize", C.c_int, [_vp, C.c_uint32, C.c_uint64, _vp])
+        self.q80_host = _sig(L, "edgexpu_hip_quantize_q8_0", C.c_int, [_vp, C.c_int, _vp])
+        self.q8k_host = _sig(L, "edgexpu_hip_quantize_q8_k", C.c_int, [_vp, C.c_int, _vp])
+        self.dot_f32_rows = _sig(L, "edgexpu_hip_dot_f32_rows", C.c_int,
+                                 [_vp, _vp, C.c_uint32, _vp, C.c_int, C.c_int])
+        self.dot_q8_rows = _sig(L, "edgexpu_hip_dot_q8_rows", C.c_int,
+                                [_vp, _vp, C.c_uint32, _vp, C.c_int, C.c_int])
+
+    def last_error(self) -> tuple[int, str]:
+        buf = C.create_string_buffer(512)
+        code = self._last_error(buf, 512)
+        return code, buf.value.decode(errors="replace")
+
+    def check(self, ok: int, what: str):
+        if not ok:
+            code, msg = self.last_error()
+            self.clear_error()
+            raise HipError(f"{what} failed (code {code}): {msg}")
+
+
+_HIP: HipLib | None = None
+
+
+def hip() -> HipLib:
+    global _HIP
+    if _HIP is None:
+        _HIP = HipLib()
+    return _HIP
+
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream():
+    import torch
+
+    return torch.cuda.current_stream().cuda_stream
+
+
+# ---------------------------------------------------------------- device API
+
+
+def linear_quant_batch(w, qtype: int, x, n_out: int, n_in: int, bias=None, out=None):
+    """out[m, n_out] = bias + W · q8(x) on the GPU (edgexpu_hip_linear_quant_batch_dev).
+
+    ``w`` is a uint8 device tensor of n_out GGUF rows, ``x`` a float32 [m, n_in]
+    device tensor.  Work is queued on torch's current stream.
+    """
+    import torch
+
+    m = x.shape[0]
+    if out is None:
+        out = torch.empty((m, n_out), dtype=torch.float32, device=x.device)
+    L = hip()
+    L.check(L.linear_dev(_ptr(out), _ptr(x), _ptr(w), qtype, _ptr(bias), m, n_out, n_in, _stream()),
+            "linear_quant_batch")
+    return out
+
+
+def gemv_q8(w, qtype: int, xq, m: int, n_out: int, n_in: int, bias=None, out=None):
+    """GEMV against activations already in Q8_0 / Q8_K block bytes (edgexpu_hip_gemv_q8_dev)."""
+    import torch
+
+    if out is None:
+        out = torch.empty((m, n_out), dtype=torch.float32, device=xq.device)
+    L = hip()
+    L.check(L.gemv_q8_dev(_ptr(out), _ptr(xq), _ptr(w), qtype, _ptr(bias), m, n_out, n_in, _stream()), "gemv_q8")
+    return out
+
+
+def logits(w, qtype: int, hidden, vocab: int, n_embd: int, bias=None, chunk_rows: int = 0, scores=None,
+           want_best: bool = True):
+    """Logits product + greedy argmax (edgexpu_hip_logits_dev); hidden is [m, n_embd]."""
+    import torch
+
+    m = hidden.shape[0] if hidden.dim() == 2 else 1
+    if scores is None:
+        scores = torch.empty((m, vocab), dtype=torch.float32, device=hidden.device)
+    best = torch.empty(m, dtype=torch.int32, device=hidden.device) if want_best else None
+    L = hip()
+    L.check(L.logits_dev(_ptr(scores), _ptr(best), _ptr(hidden), _ptr(w), qtype, _ptr(bias), m, vocab, n_embd,
+                         chunk_rows, _stream()), "logits")
+    return scores, best
+
+
+def dequantize(src, qtype: int, n: int, dst=None):
+    import torch
+
+    if dst is None:
+        dst = torch.empty(n, dtype=torch.float32, device=src.device)
+    L = hip()
+    L.check(L.dequant_dev(_ptr(src), qtype, n, _ptr(dst), _stream()), "dequantize")
+    return dst
+
+
+def quantize_q8_0(x):
+    import torch
+
+    m, n = (x.shape[0], x.shape[1]) if x.dim() == 2 else (1, x.shape[0])
+    dst = torch.empty(m * (n // 32) * 34, dtype=torch.uint8, device=x.device)
+    L = hip()
+    L.check(L.q80_dev(_ptr(x), m, n, _ptr(dst), _stream()), "quantize_q8_0")
+    return dst
+
+
+def quantize_q8_k(x):
+    import torch
+
+    m, n = (x.shape[0], x.shape[1]) if x.dim() == 2 else (1, x.shape[0])
+    dst = torch.empty(m * (n // 256) * 292, dtype=torch.uint8, device=x.device)
+    L = hip()
+    L.check(L.q8k_dev(_ptr(x), m, n, _ptr(dst), _stream()), "quantize_q8_k")
+    return dst

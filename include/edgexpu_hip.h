@@ -1,0 +1,163 @@
+/*
+ * edgexpu_hip.h -- C-ABI of libedgexpu_hip.so, the MI355X (gfx950) kernel set
+ * for the GGUF Q8_0 / Q4_K / Q6_K quantized-weight matrix path.
+ *
+ * Plain C types only (no HIP or torch types): device pointers are `void *` /
+ * typed pointers into device memory, streams are `void *` holding a
+ * hipStream_t (NULL = the library's own stream).
+ *
+ * Conventions shared by every entry point:
+ *  - Return 1 on success, 0 on failure.  A failure records a sticky error
+ *    (code + message) readable with edgexpu_hip_last_error(); the library
+ *    never returns silently wrong data.  Bad arguments are rejected before
+ *    any launch (the reference silently returns for them:
+ *    src/cpu_kernel.c:562-564,571-574).
+ *  - Single caller: like the reference path (process-global activation
+ *    scratch, src/cpu_kernel.c:525-543) the library keeps one device, one
+ *    stream and one workspace per process and is not reentrant.
+ *  - Type ids are GGUF's (include/edgexpu/gguf_quant.h:17-24).  Only Q8_0 (8),
+ *    Q4_K (12) and Q6_K (14) run on the GPU; any other type is reported as
+ *    unsupported so the caller can route it to its CPU kernels.
+ */
+#ifndef EDGEXPU_HIP_H
+#define EDGEXPU_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EDGEXPU_HIP_TYPE_Q8_0 8
+#define EDGEXPU_HIP_TYPE_Q4_K 12
+#define EDGEXPU_HIP_TYPE_Q6_K 14
+
+/* ---- lifecycle and errors (no reference counterpart: the reference has no
+ * device; these replace its implicit process-global CPU state) ---- */
+
+/* Selects `device`, creates the library stream.  Optional: every entry point
+ * initialises device 0 on first use. */
+int edgexpu_hip_init(int device);
+/* Releases the stream, workspace and staging buffers. */
+void edgexpu_hip_shutdown(void);
+/* Sticky error: returns the last error code (0 = none) and copies its
+ * message into buf.  The error stays set until edgexpu_hip_clear_error(). */
+int edgexpu_hip_last_error(char *buf, size_t size);
+void edgexpu_hip_clear_error(void);
+/* 1 when `type` runs on the GPU (edgexpu_gguf_can_dot_q8/_q8k dispatch,
+ * src/gguf_dot_q8.c:414-434, restricted to Q8_0/Q4_K/Q6_K). */
+int edgexpu_hip_supports_type(uint32_t type);
+/* Blocks until the library stream is idle. */
+int edgexpu_hip_synchronize(void);
+/* hipStream_t of the library stream. */
+void *edgexpu_hip_stream(void);
+
+/* ---- layout (src/gguf_quant.c:69-108,468-480; src/gguf_dot_q8.c:255-267) ---- */
+size_t edgexpu_hip_row_bytes(uint32_t type, int n_in);
+
+/* ---- device-resident GGUF weights ----
+ * Replaces the per-token staging copy of src/native.c:350-380,593-655: a
+ * tensor's blocks are uploaded once and addressed by handle, never by the
+ * (aliasing) host staging pointer. */
+typedef struct edgexpu_hip_weight edgexpu_hip_weight;
+
+/* Copies n_out rows of GGUF blocks (and n_out f32 biases, may be NULL) to
+ * the device.  Returns NULL on error. */
+edgexpu_hip_weight *edgexpu_hip_weight_upload(const uint8_t *blocks, uint32_t type, int n_out, int n_in,
+                                              const float *bias);
+/* Wraps blocks already in device memory (not owned; the caller keeps them
+ * alive).  dev_bias may be NULL. */
+edgexpu_hip_weight *edgexpu_hip_weight_wrap(const void *dev_blocks, uint32_t type, int n_out, int n_in,
+                                            const float *dev_bias);
+void edgexpu_hip_weight_free(edgexpu_hip_weight *w);
+const void *edgexpu_hip_weight_data(const edgexpu_hip_weight *w);
+uint32_t edgexpu_hip_weight_type(const edgexpu_hip_weight *w);
+int edgexpu_hip_weight_n_out(const edgexpu_hip_weight *w);
+int edgexpu_hip_weight_n_in(const edgexpu_hip_weight *w);
+
+/* ---- device-pointer entry points (all buffers in device memory; work is
+ * queued on `stream` and not waited for) ---- */
+
+/* out[t*n_out + o] = bias[o] + dot(W[o], q8(x[t]))  for t < m.
+ * Replaces edgexpu_cpu_linear_quant_batch (include/edgexpu/cpu_kernel.h:71-80,
+ * src/cpu_kernel.c:545-644): activations are quantized once per token
+ * (Q8_0 for Q8_0 weights, Q8_K for Q4_K/Q6_K) and every row is dotted with
+ * the integer block kernels.  x is [m][n_in] f32, out [m][n_out] f32, both
+ * 16-byte aligned; bias may be NULL. */
+int edgexpu_hip_linear_quant_batch_dev(float *out, const float *x, const void *w, uint32_t type,
+                                       const float *bias, int m, int n_out, int n_in, void *stream);
+
+/* The integer block-dot product alone, for activations already quantized
+ * into the reference's block bytes (one token = n_in/32 Q8_0 blocks for Q8_0
+ * weights, n_in/256 Q8_K blocks for Q4_K / Q6_K; token t at
+ * xq + t * that size): out[t*n_out + o] = bias[o] + dot(W[o], xq[t]).
+ * edgexpu_gguf_dot_quant_q8 / _q8k (src/gguf_dot_q8.c:1004-1044) over all
+ * rows and tokens at once; lets several projections share one quantized
+ * input. */
+int edgexpu_hip_gemv_q8_dev(float *out, const uint8_t *xq, const void *w, uint32_t type, const float *bias, int m,
+                            int n_out, int n_in, void *stream);
+
+/* Logits product of src/native.c:2292-2401 for m hidden vectors:
+ * scores[t*vocab + i] = dot(W[i], h[t]) (+ bias[i]) with the Q8_0-activation
+ * dot for Q8_0 weights and the f32-activation dots for Q4_K / Q6_K
+ * (src/native.c:445-514, src/gguf_quant.c:704-794).  Rows are processed in
+ * launches of chunk_rows rows (0 = the reference's 48 MiB budget,
+ * include/edgexpu/scheduler.h:34); results do not depend on the chunking.
+ * When best_dev is non-NULL, best_dev[t] receives the greedy argmax of row t
+ * (lowest index on ties, NaN never wins, 0 when nothing beats -inf). */
+int edgexpu_hip_logits_dev(float *scores, uint32_t *best_dev, const float *hidden, const void *w, uint32_t type,
+                           const float *bias, int m, int vocab, int n_embd, int chunk_rows, void *stream);
+
+/* Bulk dequantization (edgexpu_gguf_dequantize, include/edgexpu/gguf_quant.h:32-39,
+ * src/gguf_quant.c:355-411), bit-identical to the reference's x86 build.
+ * n_elements must be a multiple of the block size; dst 16-byte aligned. */
+int edgexpu_hip_dequantize_dev(const void *src, uint32_t type, uint64_t n_elements, float *dst, void *stream);
+
+/* Activation quantizers writing the reference's block bytes
+ * (edgexpu_gguf_quantize_q8_0 / _q8_k, include/edgexpu/gguf_quant.h:80-87,
+ * src/gguf_dot_q8.c:269-412): m rows of n f32 -> m*(n/32)*34 or
+ * m*(n/256)*292 bytes, bit-identical to the reference's x86 build. */
+int edgexpu_hip_quantize_q8_0_dev(const float *x, int m, int n, uint8_t *dst, void *stream);
+int edgexpu_hip_quantize_q8_k_dev(const float *x, int m, int n, uint8_t *dst, void *stream);
+
+/* ---- host-pointer entry points (synchronous: inputs copied in, outputs
+ * copied out before return; the PCIe copies are part of the call) ---- */
+
+/* edgexpu_cpu_linear_quant_batch with a device-resident weight handle: x is
+ * host [m][n_in], out host [m][n_out]; the handle's bias is applied. */
+int edgexpu_hip_linear_quant_batch(float *out, const float *x, const edgexpu_hip_weight *w, int m);
+
+/* Same, with the weight rows passed as host GGUF bytes (uploaded for this call
+ * only: correct for the reference's reused staging buffer, but PCIe-bound). */
+int edgexpu_hip_linear_quant_batch_host(float *out, const float *x, const uint8_t *weight, uint32_t type,
+                                        const float *bias, int m, int n_out, int n_in);
+
+/* Logits with a device-resident output weight: hidden host [n_embd], scores
+ * host [vocab] (may be NULL), *best receives the greedy argmax. */
+int edgexpu_hip_logits(float *scores, uint32_t *best, const float *hidden, const edgexpu_hip_weight *w,
+                       int chunk_rows);
+
+/* Host-buffer dequantization: src host bytes, dst host f32. */
+int edgexpu_hip_dequantize(const uint8_t *src, uint32_t type, uint64_t n_elements, float *dst);
+
+/* Host-buffer quantizers (reference block bytes). */
+int edgexpu_hip_quantize_q8_0(const float *x, int n, uint8_t *dst);
+int edgexpu_hip_quantize_q8_k(const float *x, int n, uint8_t *dst);
+
+/* f32-activation row dots on the GPU for `rows` consecutive rows
+ * (edgexpu_gguf_dot_quant, src/gguf_quant.c:894-918, batched over rows):
+ * host in/out. */
+int edgexpu_hip_dot_f32_rows(float *out, const uint8_t *w, uint32_t type, const float *x, int rows, int n);
+
+/* Quantized-activation row dots on the GPU for `rows` consecutive rows against
+ * one activation already in the reference's Q8_0 (34 B/32) or Q8_K
+ * (292 B/256) block bytes (edgexpu_gguf_dot_quant_q8 / _q8k,
+ * src/gguf_dot_q8.c:1004-1044, batched over rows): host in/out. */
+int edgexpu_hip_dot_q8_rows(float *out, const uint8_t *w, uint32_t type, const uint8_t *xq, int rows, int n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

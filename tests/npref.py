@@ -1,0 +1,199 @@
+"""Independent numpy restatement of the quantized-weight path (test helper).
+
+Written from the block formats and formulas, not from the C oracle, so that the
+two pin each other: dequant and quantizers are bit-exact closed forms in
+float32 (numpy never fuses a multiply-add), the integer block sums are int64
+brute force, and the fp32 row results get a float64 value plus the
+conditioning scale S = sum |w_k x_k| of the tolerance rule |y - y^| <= tol * S.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+f32 = np.float32
+
+
+def f16(b: np.ndarray) -> np.ndarray:
+    """little-endian fp16 bytes [..., 2] -> float32 (exact)."""
+    return np.ascontiguousarray(b).view(np.float16).astype(np.float32)[..., 0]
+
+
+# ------------------------------------------------------------ unpack codes
+
+
+def q8_0_parts(blocks: np.ndarray):
+    """[nb, 34] -> d [nb] f32, q [nb, 32] int."""
+    b = blocks.reshape(-1, 34)
+    return f16(b[:, 0:2]), b[:, 2:].view(np.int8).astype(np.int64)
+
+
+def q4_k_parts(sb: np.ndarray):
+    """[nb, 144] -> d, dmin [nb]; sc, m [nb, 8]; codes [nb, 256] (element order)."""
+    s = sb.reshape(-1, 144)
+    d, dmin = f16(s[:, 0:2]), f16(s[:, 2:4])
+    sc12 = s[:, 4:16].astype(np.int64)
+    sc = np.zeros((s.shape[0], 8), np.int64)
+    m = np.zeros((s.shape[0], 8), np.int64)
+    sc[:, :4] = sc12[:, 0:4] & 63
+    m[:, :4] = sc12[:, 4:8] & 63
+    sc[:, 4:] = (sc12[:, 8:12] & 15) | ((sc12[:, 0:4] >> 6) << 4)
+    m[:, 4:] = (sc12[:, 8:12] >> 4) | ((sc12[:, 4:8] >> 6) << 4)
+    qs = s[:, 16:].reshape(-1, 4, 32).astype(np.int64)       # [nb, chunk j, l]
+    codes = np.stack([qs & 15, qs >> 4], axis=2)              # [nb, j, half, l]
+    return d, dmin, sc, m, codes.reshape(-1, 256)
+
+
+def q6_k_parts(sb: np.ndarray):
+    """[nb, 210] -> d [nb]; sc [nb, 16] (int8); codes [nb, 256] unsigned 0..63."""
+    s = sb.reshape(-1, 210)
+    ql = s[:, 0:128].reshape(-1, 2, 2, 32).astype(np.int64)   # [nb, half, ql-half, l]
+    qh = s[:, 128:192].reshape(-1, 2, 32).astype(np.int64)    # [nb, half, l]
+    sc = s[:, 192:208].view(np.int8).astype(np.int64)
+    d = f16(s[:, 208:210])
+    codes = np.empty((s.shape[0], 2, 4, 32), np.int64)        # [nb, half, quarter k, l]
+    for k in range(4):
+        lo = ql[:, :, k & 1, :]
+        lo = (lo >> 4) if k >= 2 else (lo & 15)
+        codes[:, :, k, :] = lo | (((qh >> (2 * k)) & 3) << 4)
+    return d, sc, codes.reshape(-1, 256)
+
+
+# ------------------------------------------------------------ dequant
+
+
+def dequant(qtype: int, src: np.ndarray) -> np.ndarray:
+    if qtype == 8:
+        d, q = q8_0_parts(src)
+        return (d[:, None] * q.astype(f32)).astype(f32).reshape(-1)
+    if qtype == 12:
+        d, dmin, sc, m, codes = q4_k_parts(src)
+        ds = (d[:, None] * sc.astype(f32)).astype(f32)        # [nb, 8]
+        ms = (dmin[:, None] * m.astype(f32)).astype(f32)
+        sub = np.repeat(np.arange(8), 32)
+        prod = (ds[:, sub] * codes.astype(f32)).astype(f32)
+        return (prod - ms[:, sub]).astype(f32).reshape(-1)
+    if qtype == 14:
+        d, sc, codes = q6_k_parts(src)
+        ds = (d[:, None] * sc.astype(f32)).astype(f32)        # [nb, 16]
+        sub = np.repeat(np.arange(16), 16)
+        return (ds[:, sub] * (codes - 32).astype(f32)).astype(f32).reshape(-1)
+    raise ValueError(qtype)
+
+
+# ------------------------------------------------------------ quantizers
+
+
+def _cvt_avx(r: np.ndarray) -> np.ndarray:
+    """rounded float -> int32 as _mm256_cvtps_epi32: NaN / out of range -> INT32_MIN."""
+    ok = np.isfinite(r) & (r >= -2147483648.0) & (r < 2147483648.0)
+    out = np.full(r.shape, -2147483648, np.int64)
+    out[ok] = r[ok].astype(np.int64)
+    return out
+
+
+def quantize_q8_0(x: np.ndarray) -> np.ndarray:
+    xb = x.astype(f32).reshape(-1, 32)
+    with np.errstate(all="ignore"):
+        amax = np.abs(xb).max(axis=1)
+        d = (amax / f32(127.0)).astype(f32)
+        idv = np.where(amax != 0, f32(127.0) / np.where(amax != 0, amax, f32(1)), f32(0)).astype(f32)
+        q = _cvt_avx(np.rint((xb * idv[:, None]).astype(f32)))
+    q = np.clip(q, -128, 127).astype(np.int8)
+    with np.errstate(over="ignore"):
+        dh = d.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    return np.concatenate([dh, q.view(np.uint8)], axis=1).reshape(-1)
+
+
+def quantize_q8_k(x: np.ndarray) -> np.ndarray:
+    xb = x.astype(f32).reshape(-1, 256)
+    out = np.zeros((xb.shape[0], 292), np.uint8)
+    for b in range(xb.shape[0]):
+        a = np.abs(xb[b])
+        i = int(np.argmax(a))                 # first index of the largest |x|
+        if a[i] == 0:
+            continue
+        with np.errstate(all="ignore"):
+            iscale = f32(f32(-127.0) / xb[b, i])
+            p = (iscale * xb[b]).astype(f32)
+            q = np.where(np.isfinite(p), np.rint(p), 0).astype(np.int64)   # lrintf: non-finite -> 0
+            d = f32(f32(1.0) / iscale)
+        q = np.clip(q, -127, 127)
+        out[b, 0:4] = np.array([d], f32).view(np.uint8)
+        out[b, 4:260] = q.astype(np.int8).view(np.uint8)
+        out[b, 260:292] = q.reshape(16, 16).sum(axis=1).astype(np.int16).view(np.uint8)
+    return out.reshape(-1)
+
+
+# ------------------------------------------------------------ integer block sums
+
+
+def q8_0_lanes(wblk, xblk):
+    _, qw = q8_0_parts(wblk)
+    _, qx = q8_0_parts(xblk)
+    return (qw[0] * qx[0]).reshape(8, 4).sum(axis=1)
+
+
+def q4_k_lanes(wsb, xsb):
+    _, _, sc, m, codes = q4_k_parts(wsb)
+    q8 = xsb[4:260].view(np.int8).astype(np.int64)
+    bs = xsb[260:292].view(np.int16).astype(np.int64)
+    e = np.arange(256)
+    lanes = np.array([np.sum((sc[0][e // 32] * codes[0] * q8)[((e % 32) // 4) == u]) for u in range(8)])
+    s32 = bs.reshape(8, 2).sum(axis=1)
+    mins = (m[0] * s32).reshape(4, 2).sum(axis=1)
+    return lanes, mins
+
+
+def q6_k_lanes(wsb, xsb):
+    _, sc, codes = q6_k_parts(wsb)
+    q8 = xsb[4:260].view(np.int8).astype(np.int64)
+    bs = xsb[260:292].view(np.int16).astype(np.int64)
+    e = np.arange(256)
+    lanes = []
+    for u in range(8):
+        sel = ((e % 32) // 4) == u
+        v = np.sum((sc[0][e // 16] * codes[0] * q8)[sel])
+        v -= 32 * (bs[2 * u] * sc[0][2 * u] + bs[2 * u + 1] * sc[0][2 * u + 1])
+        lanes.append(v)
+    return np.array(lanes)
+
+
+# ------------------------------------------------------------ f64 results + scale
+
+
+def q8_dot_f64(qtype: int, wrow: np.ndarray, xq: np.ndarray):
+    """Exact-integer, float64-combined row dot against quantized activations.
+
+    Returns (value, S) with S = sum over blocks of |dx*dw*isum| + |dx*dmin*imin|."""
+    if qtype == 8:
+        dw, qw = q8_0_parts(wrow)
+        dx, qx = q8_0_parts(xq)
+        isum = (qw * qx).sum(axis=1)
+        t = dw.astype(np.float64) * dx.astype(np.float64) * isum
+        return t.sum(), np.abs(t).sum()
+    xb = xq.reshape(-1, 292)
+    dx = xb[:, 0:4].copy().view(np.float32)[:, 0].astype(np.float64)
+    q8 = xb[:, 4:260].view(np.int8).astype(np.int64)
+    bs = xb[:, 260:292].copy().view(np.int16).astype(np.int64)
+    if qtype == 12:
+        d, dmin, sc, m, codes = q4_k_parts(wrow)
+        sub = np.repeat(np.arange(8), 32)
+        isum = (sc[:, sub] * codes * q8).sum(axis=1)
+        imin = (m * bs.reshape(-1, 8, 2).sum(axis=2)).sum(axis=1)
+        a = dx * d.astype(np.float64) * isum
+        b = dx * dmin.astype(np.float64) * imin
+        return (a - b).sum(), (np.abs(a) + np.abs(b)).sum()
+    if qtype == 14:
+        d, sc, codes = q6_k_parts(wrow)
+        sub = np.repeat(np.arange(16), 16)
+        isum = (sc[:, sub] * (codes - 32) * q8).sum(axis=1)
+        a = dx * d.astype(np.float64) * isum
+        return a.sum(), np.abs(a).sum()
+    raise ValueError(qtype)
+
+
+def f32_dot_f64(qtype: int, wrow: np.ndarray, x: np.ndarray):
+    """float64 row dot against f32 activations: (value, S = sum |w_k x_k|)."""
+    w = dequant(qtype, wrow).astype(np.float64)
+    p = w * x.astype(np.float64)
+    return p.sum(), np.abs(p).sum()

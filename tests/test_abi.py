@@ -1,0 +1,109 @@
+"""C-ABI checks that need no GPU: both libraries load, export every function
+declared in include/*.h, and their pure host helpers (layout constants,
+dispatch predicates, layer-kind tables) agree with the reference/oracle."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+import edgexpu_amd as E
+import oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared(header: str) -> list[str]:
+    src = open(os.path.join(ROOT, "include", header)).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    names = re.findall(r"^[A-Za-z_][\w\s\*]*?\b(edgexpu_\w+)\s*\(", src, flags=re.M)
+    return sorted(set(names))
+
+
+def exported(path: str) -> set[str]:
+    lib = C.CDLL(path)
+    return {n for n in dir(lib)} | {n for n in _probe(lib)}
+
+
+def _probe(lib):
+    return []
+
+
+@pytest.mark.parametrize("header,lib", [("edgexpu_hip.h", E.HIP_SO), ("edgexpu_kernels.h", E.KERNELS_SO)])
+def test_every_declared_symbol_is_exported(header, lib):
+    assert os.path.exists(lib), f"{lib} not built"
+    names = declared(header)
+    assert len(names) > 10
+    handle = C.CDLL(lib)
+    missing = [n for n in names if not hasattr(handle, n)]
+    assert not missing, f"{os.path.basename(lib)} lacks {missing}"
+
+
+def test_reference_entry_points_present():
+    """The drop-in set carries the reference's own names (cpu_kernel.h / gguf_quant.h)."""
+    ref_names = ["edgexpu_cpu_linear_quant", "edgexpu_cpu_linear_quant_batch", "edgexpu_gguf_dequantize",
+                 "edgexpu_gguf_quantize_q8_0", "edgexpu_gguf_quantize_q8_k", "edgexpu_gguf_dot_quant",
+                 "edgexpu_gguf_dot_quant_q8", "edgexpu_gguf_dot_quant_q8k", "edgexpu_gguf_row_bytes",
+                 "edgexpu_gguf_type_block_size", "edgexpu_gguf_type_block_bytes", "edgexpu_gguf_q8_0_nbytes",
+                 "edgexpu_gguf_q8_k_nbytes", "edgexpu_gguf_can_dot_q8", "edgexpu_gguf_can_dot_q8k"]
+    lib = C.CDLL(E.KERNELS_SO)
+    assert all(hasattr(lib, n) for n in ref_names)
+
+
+def test_layout_helpers_match_oracle(ora):
+    k = C.CDLL(E.KERNELS_SO)
+    for f in ("edgexpu_gguf_type_block_size", "edgexpu_gguf_type_block_bytes"):
+        getattr(k, f).restype = C.c_size_t
+    k.edgexpu_gguf_row_bytes.restype = C.c_size_t
+    k.edgexpu_gguf_q8_0_nbytes.restype = C.c_size_t
+    k.edgexpu_gguf_q8_k_nbytes.restype = C.c_size_t
+    ora.fn("ora_block_size", C.c_size_t, [C.c_uint32])
+    bs = ora.fn("ora_block_size", C.c_size_t, [C.c_uint32])
+    bb = ora.fn("ora_block_bytes", C.c_size_t, [C.c_uint32])
+    rb = ora.fn("ora_row_bytes", C.c_size_t, [C.c_uint32, C.c_int])
+    for t in list(range(16)) + [99]:
+        assert k.edgexpu_gguf_type_block_size(t) == bs(t)
+        assert k.edgexpu_gguf_type_block_bytes(t) == bb(t)
+        for n in (0, -32, 31, 32, 256, 576, 4096, 14336):
+            assert k.edgexpu_gguf_row_bytes(t, n) == rb(t, n)
+    for n in (0, 31, 32, 576, 4096):
+        assert k.edgexpu_gguf_q8_0_nbytes(n) == (0 if n <= 0 or n % 32 else n // 32 * 34)
+        assert k.edgexpu_gguf_q8_k_nbytes(n) == (0 if n <= 0 or n % 256 else n // 256 * 292)
+    # dispatch predicates, src/gguf_dot_q8.c:414-434
+    assert [t for t in range(16) if k.edgexpu_gguf_can_dot_q8(t)] == [2, 6, 8]
+    assert [t for t in range(16) if k.edgexpu_gguf_can_dot_q8k(t)] == [12, 13, 14]
+
+
+def test_hip_host_helpers_without_gpu():
+    L = E.HipLib()
+    assert [t for t in range(16) if L.supports_type(t)] == [8, 12, 14]
+    assert L.row_bytes(12, 4096) == 2304 and L.row_bytes(14, 9728) == 7980 and L.row_bytes(8, 576) == 612
+    assert L.row_bytes(12, 100) == 0 and L.row_bytes(2, 64) == 0
+
+
+def test_layer_kind_projection_tables():
+    k = C.CDLL(E.KERNELS_SO)
+    buf = (C.c_int * 16)()
+    # EDGEXPU_LAYER_ATTN_SWIGLU: q k v o gate up down (src/native.c:2530-2580)
+    assert k.edgexpu_kernels_layer_projections(0, buf, 16) == 7
+    assert list(buf[:7]) == [0, 1, 2, 3, 4, 5, 6]
+    assert k.edgexpu_kernels_layer_projections(1, buf, 16) == 0        # UNSUPPORTED
+    assert k.edgexpu_kernels_layer_projections(2, buf, 16) == 8        # GATED_DELTA
+    assert list(buf[:8]) == [7, 8, 9, 10, 11, 4, 5, 6]
+    assert k.edgexpu_kernels_layer_projections(3, buf, 16) == 7        # ATTN_QK_NORM
+    assert k.edgexpu_kernels_layer_projections(0, None, 0) == 7        # size query
+
+
+def test_kernel_set_table():
+    k = C.CDLL(E.KERNELS_SO)
+
+    class KS(C.Structure):
+        _fields_ = [("name", C.c_char_p)] + [(f, C.c_void_p) for f in (
+            "linear_quant", "linear_quant_batch", "dequantize", "quantize_q8_0", "quantize_q8_k",
+            "dot_quant", "dot_quant_q8", "dot_quant_q8k")]
+
+    k.edgexpu_kernels_hip.restype = C.POINTER(KS)
+    ks = k.edgexpu_kernels_hip().contents
+    assert ks.name == b"hip.gfx950"
+    assert C.cast(k.edgexpu_cpu_linear_quant_batch, C.c_void_p).value == ks.linear_quant_batch
+    assert all(getattr(ks, f) for f, _ in KS._fields_[1:])

@@ -1,0 +1,258 @@
+"""GPU parity of the HIP kernels against the oracle, through the C-ABI.
+
+Bars (BASELINE numerics contract):
+  * dequant and activation quantizers: bit-exact;
+  * integer block sums: exact (checked end to end with inputs whose fp32
+    combination is exact, so any integer error shows as a wrong output);
+  * fp32 outputs: |y - y_ref| <= TOL * S_i with S_i the row's conditioning
+    scale (sum of |block terms| for the Q8 paths, sum |w_k x_k| for the f32
+    logits paths), TOL = 1e-5.
+"""
+import numpy as np
+import pytest
+import torch
+
+import npref
+import oracle as O
+import edgexpu_amd as E
+from edgexpu_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+DEV = "cuda:0"
+TN = {8: "q8_0", 12: "q4_k", 14: "q6_k"}
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def q8_scales(ora, qt, w, x):
+    """S_i for every (token, row): sum over blocks of |block terms|."""
+    m, n = x.shape
+    S = np.zeros((m, w.shape[0]))
+    for t in range(m):
+        xq = ora.quantize_q8_0(x[t]) if qt == 8 else ora.quantize_q8_k(x[t])
+        for i in range(w.shape[0]):
+            S[t, i] = npref.q8_dot_f64(qt, w[i], xq)[1]
+    return S
+
+
+def assert_tol(got, want, S, what=""):
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    bad = err > TOL * S + 1e-30
+    assert not bad.any(), f"{what}: {bad.sum()} outside tolerance, worst ratio {(err / np.maximum(S, 1e-30)).max():.3e}"
+
+
+# ------------------------------------------------------------------ dequant
+
+
+@pytest.mark.parametrize("qt", [8, 12, 14])
+def test_dequant_golden_bit_exact(hipdev, golden, qt):
+    g = golden(f"dequant_{TN[qt]}")
+    out = E.dequantize(dev(g["src"]), qt, g["out"].size)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out.cpu().numpy()), bits(g["out"]))
+
+
+@pytest.mark.parametrize("qt,nblocks", [(8, 300001), (12, 40001), (14, 40003)])
+def test_dequant_random_bit_exact(hipdev, ora, qt, nblocks):
+    rng = np.random.default_rng(900 + qt)
+    bs = {8: 32, 12: 256, 14: 256}[qt]
+    src = synth.np_weights(qt, 1, nblocks * bs, rng).reshape(-1)
+    out = E.dequantize(dev(src), qt, nblocks * bs)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out.cpu().numpy()), bits(ora.dequantize(src, qt, nblocks * bs)))
+
+
+# ------------------------------------------------------------------ quantizers
+
+
+def test_quantizers_golden_bit_exact(hipdev, golden):
+    g = golden("quantize")
+    for name, x, q80, q8k in zip(g["names"], g["x"], g["q8_0"], g["q8_k"]):
+        xd = dev(x)
+        assert np.array_equal(E.quantize_q8_0(xd).cpu().numpy(), q80), f"q8_0 {name}"
+        assert np.array_equal(E.quantize_q8_k(xd).cpu().numpy(), q8k), f"q8_k {name}"
+    xr = dev(g["x_rand"])
+    assert np.array_equal(E.quantize_q8_0(xr).cpu().numpy(), g["q8_0_rand"].reshape(-1))
+    assert np.array_equal(E.quantize_q8_k(xr).cpu().numpy(), g["q8_k_rand"].reshape(-1))
+
+
+@pytest.mark.parametrize("n", [576, 1536, 4096, 14336])
+def test_quantizers_random_bit_exact(hipdev, ora, n):
+    rng = np.random.default_rng(n)
+    x = (rng.normal(0, 1, (7, n)) * rng.uniform(1e-3, 1e3, (7, 1))).astype(np.float32)
+    q80 = E.quantize_q8_0(dev(x)).cpu().numpy()
+    assert np.array_equal(q80, np.concatenate([ora.quantize_q8_0(r) for r in x]))
+    if n % 256 == 0:
+        q8k = E.quantize_q8_k(dev(x)).cpu().numpy()
+        assert np.array_equal(q8k, np.concatenate([ora.quantize_q8_k(r) for r in x]))
+
+
+# ------------------------------------------------------------------ GEMV
+
+
+LINEAR = ["linear_q8_0_576", "linear_q8_0_1536", "linear_q4_k_4096", "linear_q4_k_2560", "linear_q4_k_14336",
+          "linear_q6_k_2560", "linear_q6_k_9728"]
+
+
+@pytest.mark.parametrize("name", LINEAR)
+def test_linear_golden(hipdev, ora, golden, name):
+    g = golden(name)
+    qt, w, x, bias = int(g["type"]), g["w"], g["x"], g["bias"]
+    n_out, (m, n_in) = w.shape[0], x.shape
+    S = q8_scales(ora, qt, w, x)
+    y = E.linear_quant_batch(dev(w), qt, dev(x), n_out, n_in).cpu().numpy()
+    assert_tol(y, g["out"], S, name)
+    yb = E.linear_quant_batch(dev(w), qt, dev(x), n_out, n_in, bias=dev(bias)).cpu().numpy()
+    assert_tol(yb, g["out_bias"], S, name + "+bias")
+
+
+@pytest.mark.parametrize("qt,n_in,n_out", [(8, 576, 577), (8, 1536, 300), (12, 4096, 1001), (12, 2560, 515),
+                                           (12, 14336, 130), (14, 2560, 260), (14, 9728, 129), (12, 256, 70),
+                                           (14, 256, 33), (8, 32, 65)])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 11])
+def test_linear_random_vs_oracle(hipdev, ora, qt, n_in, n_out, m):
+    rng = np.random.default_rng(qt * 1000 + n_in + n_out + m)
+    w = synth.np_weights(qt, n_out, n_in, rng)
+    x = synth.np_activations(m, n_in, rng)
+    bias = rng.normal(0, 0.5, n_out).astype(np.float32)
+    want = ora.linear_quant_batch(x, w, qt, bias, m, n_out, n_in)
+    got = E.linear_quant_batch(dev(w), qt, dev(x), n_out, n_in, bias=dev(bias)).cpu().numpy()
+    S = q8_scales(ora, qt, w, x) if n_out * m <= 4000 else np.abs(want) * 0 + np.abs(want).max() * 10
+    assert_tol(got, want, S, f"{TN[qt]} {n_out}x{n_in} m={m}")
+
+
+@pytest.mark.parametrize("qt,n_in,n_out", [(12, 4096, 14336), (12, 14336, 4096), (8, 576, 49152), (14, 9728, 2560)])
+def test_linear_full_shape(hipdev, ora, qt, n_in, n_out):
+    """Workload shapes at full size; tolerance against the largest block-term scale."""
+    rng = np.random.default_rng(5 + qt + n_in)
+    w = synth.np_weights(qt, n_out, n_in, rng)
+    x = synth.np_activations(1, n_in, rng)
+    want = ora.linear_quant_batch(x, w, qt, None, 1, n_out, n_in)
+    got = E.linear_quant_batch(dev(w), qt, dev(x), n_out, n_in).cpu().numpy()
+    sample = rng.choice(n_out, 64, replace=False)
+    S = q8_scales(ora, qt, w[sample], x)[0]
+    assert_tol(got[0, sample], want[0, sample], S, "sampled rows")
+    # every row: relative to the row-sampled conditioning level
+    assert np.abs(got - want).max() <= TOL * S.max()
+
+
+@pytest.mark.parametrize("qt", [8, 12, 14])
+def test_integer_sums_exact_end_to_end(hipdev, qt):
+    """Unit scales and integer activations make every fp32 step exact, so the
+    output must equal the int64 closed form exactly (N2 through the kernel)."""
+    rng = np.random.default_rng(60 + qt)
+    n_in, n_out = (1536, 64) if qt == 8 else (2048, 64)
+    w = synth.np_weights(qt, n_out, n_in, rng)
+    one = np.array([1.0], np.float16).view(np.uint8)
+    if qt == 8:
+        wb = w.reshape(n_out, -1, 34)
+        wb[:, :, 0:2] = one
+        x = rng.integers(-127, 128, (1, n_in)).astype(np.float32)
+        x.reshape(-1, 32)[:, 0] = 127.0  # amax 127 -> d = 1, id = 1: q = x
+    elif qt == 12:
+        wb = w.reshape(n_out, -1, 144)
+        wb[:, :, 0:2] = one
+        wb[:, :, 2:4] = one
+        x = rng.integers(-127, 128, (1, n_in)).astype(np.float32)
+        x.reshape(-1, 256)[:, 0] = -127.0  # first max -127 -> iscale = 1: q = x, d = 1
+    else:
+        wb = w.reshape(n_out, -1, 210)
+        wb[:, :, 208:210] = one
+        x = rng.integers(-127, 128, (1, n_in)).astype(np.float32)
+        x.reshape(-1, 256)[:, 0] = -127.0
+    got = E.linear_quant_batch(dev(w), qt, dev(x), n_out, n_in).cpu().numpy()[0]
+    xq = npref.quantize_q8_0(x[0]) if qt == 8 else npref.quantize_q8_k(x[0])
+    want = np.array([npref.q8_dot_f64(qt, w[i], xq)[0] for i in range(n_out)])
+    assert np.all(np.abs(want) < 2**24)
+    assert np.array_equal(got.astype(np.float64), want)
+
+
+# ------------------------------------------------------------------ logits
+
+
+@pytest.mark.parametrize("name", ["dotf32_q4_k_4096", "dotf32_q4_k_2560", "dotf32_q6_k_2560", "dotf32_q8_0_576"])
+def test_f32_dots_golden(hipdev, golden, name):
+    g = golden(name)
+    qt, w, h = int(g["type"]), g["w"], g["h"]
+    rows, n = w.shape[0], h.size
+    scores, best = E.logits(dev(w), qt, dev(h[None, :]), rows, n)
+    got = scores.cpu().numpy()[0]
+    if qt == 8:  # Q8_0 logits go through the Q8_0-activation dot (src/native.c:2317-2319)
+        ora = O.load_oracle()
+        xq = ora.quantize_q8_0(h)
+        want = np.array([ora.dot_q8(8, w[i], xq, n) for i in range(rows)], np.float32)
+        S = np.array([npref.q8_dot_f64(8, w[i], xq)[1] for i in range(rows)])
+    else:
+        want = g["scores"]
+        S = np.array([npref.f32_dot_f64(qt, w[i], h)[1] for i in range(rows)])
+    assert_tol(got, want, S, name)
+
+
+@pytest.mark.parametrize("qt,n,vocab,chunk", [(12, 4096, 20000, 8192), (14, 2560, 15001, 0), (8, 576, 49152, 0),
+                                              (12, 2560, 3000, 1000)])
+def test_logits_and_argmax(hipdev, ora, qt, n, vocab, chunk):
+    rng = np.random.default_rng(qt + vocab)
+    w = synth.np_weights(qt, vocab, n, rng)
+    h = rng.normal(0, 1, n).astype(np.float32)
+    bias = rng.normal(0, 0.01, vocab).astype(np.float32)
+    want, want_best = ora.logits(h, w, qt, bias, vocab, n, chunk)
+    scores, best = E.logits(dev(w), qt, dev(h[None, :]), vocab, n, bias=dev(bias), chunk_rows=chunk)
+    got = scores.cpu().numpy()[0]
+    scale = np.abs(want).max() * 20  # conditioning level of these rows
+    assert np.abs(got - want).max() <= TOL * scale
+    b = int(best.cpu().numpy()[0])
+    assert b == int(np.argmax(got))           # GPU argmax is exact over GPU scores
+    top2 = np.sort(want)[-2:]
+    if top2[1] - top2[0] > 2 * TOL * scale:  # unambiguous winner: must agree with the oracle
+        assert b == want_best
+
+
+def test_argmax_rules(hipdev):
+    # A Q8_0 matrix whose rows are all zero except rows 10 and 4000: equal best
+    # scores, so the lowest index must win (src/native.c:2380).
+    n = 32
+    rows = 5000
+    wq = np.zeros((rows, 34), np.uint8)
+    one = np.array([1.0], np.float16).view(np.uint8)
+    for r in (10, 4000):
+        wq[r, 0:2] = one
+        wq[r, 2:] = 1
+    h = np.ones(n, np.float32)
+    scores, best = E.logits(dev(wq), 8, dev(h[None, :]), rows, n)
+    assert int(best.cpu().numpy()[0]) == 10
+    # NaN never wins: a NaN bias on the lowest winner hands the win to row 4000
+    bias = np.zeros(rows, np.float32)
+    bias[10] = np.nan
+    scores, best = E.logits(dev(wq), 8, dev(h[None, :]), rows, n, bias=dev(bias))
+    assert int(best.cpu().numpy()[0]) == 4000
+    # all -inf -> index 0
+    bias = np.full(rows, -np.inf, np.float32)
+    scores, best = E.logits(dev(wq), 8, dev(h[None, :]), rows, n, bias=dev(bias))
+    assert int(best.cpu().numpy()[0]) == 0
+
+
+# ------------------------------------------------------------------ errors
+
+
+def test_bad_arguments_are_rejected(hipdev):
+    L = hipdev
+    x = torch.zeros((1, 100), device=DEV)
+    w = torch.zeros(1000, dtype=torch.uint8, device=DEV)
+    out = torch.zeros((1, 4), device=DEV)
+    assert L.linear_dev(out.data_ptr(), x.data_ptr(), w.data_ptr(), 12, None, 1, 4, 100, None) == 0
+    code, msg = L.last_error()
+    assert code != 0 and "multiple" in msg
+    L.clear_error()
+    assert L.linear_dev(out.data_ptr(), x.data_ptr(), w.data_ptr(), 2, None, 1, 4, 96, None) == 0  # Q4_0
+    code, msg = L.last_error()
+    assert "not supported" in msg
+    L.clear_error()
+    assert L.last_error()[0] == 0
