@@ -123,66 +123,100 @@ def main():
     weight_bytes = sum(cfg["layers"] * n_out * E.row_bytes(t, n_in) for _, t, n_out, n_in, _ in projs) \
         + cfg["vocab"] * E.row_bytes(cfg["logits_type"], cfg["hidden"])
 
-    stream = torch.cuda.current_stream()
-    sp = stream.cuda_stream
+    # launches of one decode step: projections sharing an input are one
+    # grouped launch (q/k/v, gate/up), as src/native.c:2530-2532,2576-2577
+    # issue them back to back on the same normed hidden state
+    groups = [(["q", "k", "v"], "h"), (["o"], "q"), (["gate", "up"], "h"), (["down"], "f")]
+    pinfo = {name: (t, n_out, n_in) for name, t, n_out, n_in, _ in projs}
+    arr = C.c_void_p * 4
+    launch_args = []
+    for lw in layers:
+        for names, src in groups:
+            t, _, n_in = pinfo[names[0]]
+            assert all(pinfo[nm][0] == t and pinfo[nm][2] == n_in for nm in names)
+            launch_args.append((len(names), arr(*[yout[nm].data_ptr() for nm in names]), xin[src].data_ptr(),
+                                arr(*[lw[nm].data_ptr() for nm in names]), t,
+                                (C.c_int * 4)(*[pinfo[nm][1] for nm in names]), n_in))
 
-    def step():
-        for lw in layers:
-            for name, t, n_out, n_in, src in projs:
-                if not L.linear_dev(yout[name].data_ptr(), xin[src].data_ptr(), lw[name].data_ptr(), t, None, m,
-                                    n_out, n_in, sp):
-                    L.check(0, f"linear {name}")
+    def step(sp):
+        for nmat, outs, x, ws, t, nouts, n_in in launch_args:
+            if not L.linear_group_dev(nmat, outs, x, ws, t, None, nouts, m, n_in, sp):
+                L.check(0, "linear group")
         if not L.logits_dev(scores.data_ptr(), best.data_ptr(), xin["h"].data_ptr(), wout.data_ptr(),
                             cfg["logits_type"], None, m, cfg["vocab"], cfg["hidden"], cfg["logits_chunk"], sp):
             L.check(0, "logits")
 
+    def capture(fn):
+        """HIP graph of fn(stream); the library's device entry points allocate
+        nothing once a warm-up call has sized the workspace."""
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn(side.cuda_stream)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn(torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        return graph
+
+    def timed(run, n):
+        """ms per run over n runs, HIP events on the stream the work is issued to."""
+        stream = torch.cuda.current_stream()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(stream)
+        for _ in range(n):
+            run()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n
+
+    cur = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
     for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(args.steps):
-        step()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms_per_step = e0.elapsed_time(e1) / args.steps
+        step(cur())
+    eager_ms = timed(lambda: step(cur()), max(1, min(args.steps, 5)))
+    graph = capture(step)
+    for _ in range(args.warmup):
+        graph.replay()
+    ms_per_step = timed(graph.replay, args.steps)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
     # ------------------------------------------------ per-kernel timing (GEMV only)
-    def time_gemv(name, reps):
-        _, t, n_out, n_in, src = next(p for p in projs if p[0] == name)
-        xq = E.quantize_q8_0(xin[src]) if t == 8 else E.quantize_q8_k(xin[src])
-        out = yout[name]
-        for lw in layers[:2]:
-            L.check(L.gemv_q8_dev(out.data_ptr(), xq.data_ptr(), lw[name].data_ptr(), t, None, m, n_out, n_in, sp),
-                    "gemv")
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        n = 0
-        for _ in range(reps):
-            for lw in layers:  # distinct matrices: nothing is re-read from cache
-                L.gemv_q8_dev(out.data_ptr(), xq.data_ptr(), lw[name].data_ptr(), t, None, m, n_out, n_in, sp)
-                n += 1
-        b.record(stream)
-        torch.cuda.synchronize()
-        us = a.elapsed_time(b) * 1e3 / n
-        algo = n_out * E.row_bytes(t, n_in) + m * n_in * 4 + m * n_out * 4
-        return {"shape": [n_out, n_in], "type": E.TYPE_NAMES[t], "us": round(us, 3), "bytes": algo,
-                "GBps": round(algo / (us * 1e-6) / 1e9, 1)}
+    def time_gemv(names, reps):
+        """One product launch (fused quantize + GEMV) per layer, distinct
+        matrices each time so nothing is re-read from cache."""
+        t, _, n_in = pinfo[names[0]]
+        src = next(p[4] for p in projs if p[0] == names[0])
+        nmat = len(names)
+        per_layer = [(arr(*[yout[nm].data_ptr() for nm in names]), arr(*[lw[nm].data_ptr() for nm in names]))
+                     for lw in layers]
+        nouts = (C.c_int * 4)(*[pinfo[nm][1] for nm in names])
 
-    per_kernel = {name: time_gemv(name, args.kernel_reps) for name, *_ in projs}
-    # logits kernel alone (f32 path for K-quants, Q8_0 path otherwise), whole matrix per launch
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record(stream)
-    for _ in range(5):
-        L.logits_dev(scores.data_ptr(), None, xin["h"].data_ptr(), wout.data_ptr(), cfg["logits_type"], None, m,
-                     cfg["vocab"], cfg["hidden"], cfg["vocab"], sp)
-    b.record(stream)
-    torch.cuda.synchronize()
-    lus = a.elapsed_time(b) * 1e3 / 5
+        def launches(sp):
+            for _ in range(reps):
+                for outs, ws in per_layer:
+                    L.linear_group_dev(nmat, outs, xin[src].data_ptr(), ws, t, None, nouts, m, n_in, sp)
+
+        g = capture(launches)
+        g.replay()
+        us = timed(g.replay, 3) * 1e3 / (reps * len(layers))
+        algo = sum(pinfo[nm][1] * E.row_bytes(t, n_in) + m * pinfo[nm][1] * 4 for nm in names) + m * n_in * 4
+        return {"shape": [sum(pinfo[nm][1] for nm in names), n_in], "type": E.TYPE_NAMES[t], "us": round(us, 3),
+                "bytes": algo, "GBps": round(algo / (us * 1e-6) / 1e9, 1)}
+
+    per_kernel = {name: time_gemv([name], args.kernel_reps) for name, *_ in projs}
+    per_kernel["qkv"] = time_gemv(["q", "k", "v"], args.kernel_reps)
+    per_kernel["gate_up"] = time_gemv(["gate", "up"], args.kernel_reps)
+
+    def logits_only(sp):
+        for _ in range(5):
+            L.logits_dev(scores.data_ptr(), None, xin["h"].data_ptr(), wout.data_ptr(), cfg["logits_type"], None, m,
+                         cfg["vocab"], cfg["hidden"], cfg["vocab"], sp)
+
+    lg = capture(logits_only)
+    lus = timed(lg.replay, 2) * 1e3 / 5
     lbytes = cfg["vocab"] * E.row_bytes(cfg["logits_type"], cfg["hidden"]) + m * cfg["hidden"] * 4 \
         + m * cfg["vocab"] * 4
     per_kernel["logits"] = {"shape": [cfg["vocab"], cfg["hidden"]], "type": E.TYPE_NAMES[cfg["logits_type"]],
@@ -192,7 +226,7 @@ def main():
     dom = per_kernel[dom_name]
     roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": f"gemv_kernel<{E.TYPE_NAMES[cfg['wtype']]}> {dom['shape'][0]}x{dom['shape'][1]} m={m}",
+                "kernel": f"gemv_fused_kernel<{E.TYPE_NAMES[cfg['wtype']]}> {dom['shape'][0]}x{dom['shape'][1]} m={m}",
                 "us_per_launch": dom["us"], "bytes_per_launch": dom["bytes"]}
 
     # ---------------------------------------------------------------- CPU baseline
@@ -208,6 +242,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
+        "eager_ms_per_step": round(eager_ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

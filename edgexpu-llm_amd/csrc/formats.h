@@ -1,0 +1,437 @@
+// Per-format pieces of the decode GEMV kernels: how a lane loads its slice of
+// a GGUF row ("unit") and of the activation, and the unit's contribution to
+// the row dot.  Shared by the generic kernel (gemv.hip) and the fused,
+// persistent kernel (gemv_fused.hip).
+//
+//   Q8_0 x Q8_0  -- dot_q8_0_q8_0  src/gguf_dot_q8.c:436-480
+//   Q4_K x Q8_K  -- dot_q4_k_q8_k  src/gguf_dot_q8.c:603-762
+//   Q6_K x Q8_K  -- dot_q6_k_q8_k  src/gguf_dot_q8.c:897-1002
+//   Q4_K/Q6_K/Q8_0 x f32 -- dot_q4_k / dot_q6_k / dot_q8_0, src/gguf_quant.c:539-794
+//
+// Integer block sums are exact (sdot4 on the int8 codes); their fp32
+// combination differs from the reference only in summation order.
+#pragma once
+
+#include "common.h"
+
+namespace exq {
+
+struct GemvArgs {
+    const uint8_t *w;        // n_out rows of row_bytes
+    size_t row_bytes;
+    int n_out;
+    int K;                   // n_in
+    int nblk;                // K / block elements (32 or 256)
+    int U;                   // units per row
+    int G;                   // lanes per slot (8, 16, 32 or 64)
+    int T;                   // ceil(U / G)
+    int m;                   // tokens in this launch (== M template)
+    // quantized activations in the reference's block bytes (Q8_0: 34 B per
+    // 32, Q8_K: 292 B per 256), token t at xq + t*xq_stride; or f32 activations
+    const uint8_t *xq;
+    size_t xq_stride;
+    const float *xf;         // [m][K] f32 activations (f32 path)
+    const float *xs;         // [m][K/16] 16-element sums of x (f32 path)
+    const float *bias;       // [n_out] or null
+    float *out;              // [m][ldo]
+    int ldo;
+};
+
+// Activation staged in LDS by the fused kernel (split layout, per token t):
+//   q8  int8  [K]        at q + t*K
+//   d   f32   [K/QK]     at d + t*nblk   (Q8_K d, or the fp16-rounded Q8_0 d)
+//   bs  int16 [K/16]     at bs + t*K/16  (16-element code sums; Q8_K only)
+struct ActLds {
+    const int8_t *q;
+    const float *d;
+    const int16_t *bs;
+    int K;
+    int nblk;
+};
+
+// ------------------------------------------------------------------ Q4_K
+
+struct FmtQ4K {
+    static constexpr int kUnitsPerBlock = 4;  // (super-block i, 64-chunk j)
+    struct Act {
+        uint32_t q[16];   // codes of elements 64j..64j+63 of super-block i
+        float dx;         // Q8_K block scale
+        uint32_t spair;   // int16 pair: sums of sub-blocks 2j and 2j+1
+    };
+    __device__ static void load_act(const GemvArgs &a, int unit, int tk, Act &x) {
+        const int i = unit >> 2, j = unit & 3;
+        const uint8_t *blk = a.xq + (size_t)tk * a.xq_stride + (size_t)i * kBytesQ8_K;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint4 t = ldg16(blk + 4 + 64 * j + 16 * v);
+            x.q[4 * v + 0] = t.x; x.q[4 * v + 1] = t.y; x.q[4 * v + 2] = t.z; x.q[4 * v + 3] = t.w;
+        }
+        x.dx = *reinterpret_cast<const float *>(blk);
+        const uint2 bs = ldg8(blk + 260 + 8 * j);  // bsums 4j..4j+3
+        const int s0 = (int)(int16_t)(bs.x & 0xffff) + (int)(int16_t)(bs.x >> 16);
+        const int s1 = (int)(int16_t)(bs.y & 0xffff) + (int)(int16_t)(bs.y >> 16);
+        x.spair = ((uint32_t)s0 & 0xffffu) | ((uint32_t)s1 << 16);
+    }
+    __device__ static void load_act_lds(const ActLds &s, int unit, int tk, Act &x) {
+        const int i = unit >> 2, j = unit & 3;
+        const uint4 *p = reinterpret_cast<const uint4 *>(s.q + (size_t)tk * s.K + 256 * i + 64 * j);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint4 t = p[v];
+            x.q[4 * v + 0] = t.x; x.q[4 * v + 1] = t.y; x.q[4 * v + 2] = t.z; x.q[4 * v + 3] = t.w;
+        }
+        x.dx = s.d[tk * s.nblk + i];
+        const uint2 bs = *reinterpret_cast<const uint2 *>(s.bs + (size_t)tk * (s.K / 16) + 16 * i + 4 * j);
+        const int s0 = (int)(int16_t)(bs.x & 0xffff) + (int)(int16_t)(bs.x >> 16);
+        const int s1 = (int)(int16_t)(bs.y & 0xffff) + (int)(int16_t)(bs.y >> 16);
+        x.spair = ((uint32_t)s0 & 0xffffu) | ((uint32_t)s1 << 16);
+    }
+    struct W {
+        uint4 h, q0, q1;
+    };
+    template <class A>
+    __device__ static void load_w(const A &a, int row, int unit, W &w) {
+        const int i = unit >> 2, j = unit & 3;
+        const uint8_t *sb = a.w + (size_t)row * a.row_bytes + (size_t)i * kBytesQ4_K;
+        w.h = *reinterpret_cast<const uint4 *>(sb);
+        w.q0 = *reinterpret_cast<const uint4 *>(sb + 16 + 32 * j);
+        w.q1 = *reinterpret_cast<const uint4 *>(sb + 32 + 32 * j);
+    }
+    __device__ static void dot1(const W &w, int unit, const Act &xa, float &acc) {
+        const int j = unit & 3;
+        const float d = f16_bits_to_f32(w.h.x & 0xffffu);
+        const float dmin = f16_bits_to_f32(w.h.x >> 16);
+        // Six-bit scale/min pairs of sub-blocks 2j, 2j+1 (unpack_k4_scales,
+        // src/gguf_dot_q8.c:112-124): bytes 0..3 hold sc0..3, 4..7 m0..3, and
+        // 8..11 the low nibbles of sc4..7 / m4..7 with the top bits of 0..7.
+        const int sh = 16 * (j & 1);
+        uint32_t scp, mp;
+        if (j < 2) {
+            scp = (w.h.y >> sh) & 0x3f3fu;
+            mp = (w.h.z >> sh) & 0x3f3fu;
+        } else {
+            scp = ((w.h.w >> sh) & 0x0f0fu) | (((w.h.y >> sh) >> 2) & 0x3030u);
+            mp = (((w.h.w >> sh) >> 4) & 0x0f0fu) | (((w.h.z >> sh) >> 2) & 0x3030u);
+        }
+        const int sc0 = (int)(scp & 0xffu), sc1 = (int)(scp >> 8);
+        const uint32_t mpair = (mp & 0xffu) | ((mp & 0xff00u) << 8);
+        const uint32_t qw[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+        uint32_t lo[8], hi[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            lo[k] = qw[k] & 0x0f0f0f0fu;
+            hi[k] = (qw[k] >> 4) & 0x0f0f0f0fu;
+        }
+        {
+            int dlo = 0, dhi = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                dlo = sdot4(lo[k], xa.q[k], dlo);
+                dhi = sdot4(hi[k], xa.q[8 + k], dhi);
+            }
+            const int isum = sc0 * dlo + sc1 * dhi;
+            const int imin = sdot2(mpair, xa.spair, 0);
+            const float dd = xa.dx * d;
+            const float dm = xa.dx * dmin;
+            acc = fmaf(dd, (float)isum, acc);
+            acc = fmaf(-dm, (float)imin, acc);
+        }
+    }
+};
+
+// ------------------------------------------------------------------ Q6_K
+
+struct FmtQ6K {
+    static constexpr int kUnitsPerBlock = 4;  // (super-block i, half h, l-half p)
+    struct Act {
+        uint32_t q[16];   // q8 of elements 128h+32k+16p..+15, k=0..3 (4 dwords each)
+        float dx;
+        int bs32[4];      // 32 * (16-element code sum) of sub-block 8h+2k+p
+    };
+    __device__ static void load_act(const GemvArgs &a, int unit, int tk, Act &x) {
+        const int i = unit >> 2, h = (unit >> 1) & 1, p = unit & 1;
+        const uint8_t *blk = a.xq + (size_t)tk * a.xq_stride + (size_t)i * kBytesQ8_K;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint4 t = ldg16(blk + 4 + 128 * h + 32 * k + 16 * p);
+            x.q[4 * k + 0] = t.x; x.q[4 * k + 1] = t.y; x.q[4 * k + 2] = t.z; x.q[4 * k + 3] = t.w;
+        }
+        x.dx = *reinterpret_cast<const float *>(blk);
+        const int16_t *bs = reinterpret_cast<const int16_t *>(blk + 260) + 8 * h + p;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) x.bs32[k] = 32 * (int)bs[2 * k];
+    }
+    __device__ static void load_act_lds(const ActLds &s, int unit, int tk, Act &x) {
+        const int i = unit >> 2, h = (unit >> 1) & 1, p = unit & 1;
+        const int8_t *base = s.q + (size_t)tk * s.K + 256 * i + 128 * h + 16 * p;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint4 t = *reinterpret_cast<const uint4 *>(base + 32 * k);
+            x.q[4 * k + 0] = t.x; x.q[4 * k + 1] = t.y; x.q[4 * k + 2] = t.z; x.q[4 * k + 3] = t.w;
+        }
+        x.dx = s.d[tk * s.nblk + i];
+        const int16_t *bs = s.bs + (size_t)tk * (s.K / 16) + 16 * i + 8 * h + p;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) x.bs32[k] = 32 * (int)bs[2 * k];
+    }
+    struct W {
+        uint4 A, B, H;
+        uint2 sc;
+        uint32_t d;
+    };
+    template <class A>
+    __device__ static void load_w(const A &a, int row, int unit, W &w) {
+        const int i = unit >> 2, h = (unit >> 1) & 1, p = unit & 1;
+        const uint8_t *sb = a.w + (size_t)row * a.row_bytes + (size_t)i * kBytesQ6_K;
+        w.A = ldg16(sb + 64 * h + 16 * p);
+        w.B = ldg16(sb + 64 * h + 32 + 16 * p);
+        w.H = ldg16(sb + 128 + 32 * h + 16 * p);
+        w.sc = ldg8(sb + 192 + 8 * h);
+        w.d = *reinterpret_cast<const uint16_t *>(sb + 208);
+    }
+    __device__ static void dot1(const W &w, int unit, const Act &xa, float &acc) {
+        const int p = unit & 1;
+        const float d = f16_bits_to_f32(w.d);
+        // sc[8h + 2k + p], k = 0..3: bytes p, 2+p of sc.x and p, 2+p of sc.y
+        int sc[4];
+        sc[0] = (int)(int8_t)((w.sc.x >> (8 * p)) & 0xffu);
+        sc[1] = (int)(int8_t)((w.sc.x >> (8 * (2 + p))) & 0xffu);
+        sc[2] = (int)(int8_t)((w.sc.y >> (8 * p)) & 0xffu);
+        sc[3] = (int)(int8_t)((w.sc.y >> (8 * (2 + p))) & 0xffu);
+        const uint32_t A[4] = {w.A.x, w.A.y, w.A.z, w.A.w};
+        const uint32_t B[4] = {w.B.x, w.B.y, w.B.z, w.B.w};
+        const uint32_t H[4] = {w.H.x, w.H.y, w.H.z, w.H.w};
+        uint32_t c[4][4];  // unsigned 6-bit codes, [quarter k][dword]
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            c[0][v] = (A[v] & 0x0f0f0f0fu) | ((H[v] << 4) & 0x30303030u);
+            c[1][v] = (B[v] & 0x0f0f0f0fu) | ((H[v] << 2) & 0x30303030u);
+            c[2][v] = ((A[v] >> 4) & 0x0f0f0f0fu) | (H[v] & 0x30303030u);
+            c[3][v] = ((B[v] >> 4) & 0x0f0f0f0fu) | ((H[v] >> 2) & 0x30303030u);
+        }
+        {
+            int isum = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                int dk = 0;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) dk = sdot4(c[k][v], xa.q[4 * k + v], dk);
+                isum += sc[k] * (dk - xa.bs32[k]);
+            }
+            acc = fmaf(xa.dx * d, (float)isum, acc);
+        }
+    }
+};
+
+// ------------------------------------------------------------------ Q8_0
+
+struct FmtQ80 {
+    static constexpr int kUnitsPerBlock = 1;  // one 32-element block
+    struct Act {
+        uint32_t q[8];
+        float dx;
+    };
+    __device__ static void load_act(const GemvArgs &a, int unit, int tk, Act &x) {
+        const uint8_t *blk = a.xq + (size_t)tk * a.xq_stride + (size_t)unit * kBytesQ8_0;
+        const uint4 t0 = ldg16(blk + 2), t1 = ldg16(blk + 18);
+        x.q[0] = t0.x; x.q[1] = t0.y; x.q[2] = t0.z; x.q[3] = t0.w;
+        x.q[4] = t1.x; x.q[5] = t1.y; x.q[6] = t1.z; x.q[7] = t1.w;
+        x.dx = f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(blk));
+    }
+    __device__ static void load_act_lds(const ActLds &s, int unit, int tk, Act &x) {
+        const uint4 *p = reinterpret_cast<const uint4 *>(s.q + (size_t)tk * s.K + 32 * unit);
+        const uint4 t0 = p[0], t1 = p[1];
+        x.q[0] = t0.x; x.q[1] = t0.y; x.q[2] = t0.z; x.q[3] = t0.w;
+        x.q[4] = t1.x; x.q[5] = t1.y; x.q[6] = t1.z; x.q[7] = t1.w;
+        x.dx = s.d[tk * s.nblk + unit];
+    }
+    struct W {
+        uint4 q0, q1;
+        uint32_t d;
+    };
+    template <class A>
+    __device__ static void load_w(const A &a, int row, int unit, W &w) {
+        const uint8_t *blk = a.w + (size_t)row * a.row_bytes + (size_t)unit * kBytesQ8_0;
+        w.d = *reinterpret_cast<const uint16_t *>(blk);
+        w.q0 = ldg16(blk + 2);
+        w.q1 = ldg16(blk + 18);
+    }
+    __device__ static void dot1(const W &w, int, const Act &xa, float &acc) {
+        const float d = f16_bits_to_f32(w.d);
+        const uint32_t q[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+        {
+            int s = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) s = sdot4(q[k], xa.q[k], s);
+            acc = fmaf(d * xa.dx, (float)s, acc);
+        }
+    }
+};
+
+// ------------------------------------------------------------ f32 activations
+
+// Q4_K weights against f32 activations (logits path, dot_q4_k).
+// Unit = (super-block i, 64-chunk j); the activation slice is 64 floats.
+struct FmtQ4KF32 {
+    static constexpr int kUnitsPerBlock = 4;
+    struct Act {
+        float x[64];
+        float sx0, sx1;   // sums of x over sub-blocks 2j and 2j+1
+    };
+    __device__ static void load_act(const GemvArgs &a, int unit, int tk, Act &x) {
+        const int i = unit >> 2, j = unit & 3;
+        const float4 *p = reinterpret_cast<const float4 *>(a.xf + (size_t)tk * a.K + 256 * i + 64 * j);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const float4 t = p[v];
+            x.x[4 * v] = t.x; x.x[4 * v + 1] = t.y; x.x[4 * v + 2] = t.z; x.x[4 * v + 3] = t.w;
+        }
+        const float *s = a.xs + (size_t)tk * (a.K / 16) + 16 * i + 4 * j;
+        x.sx0 = s[0] + s[1];
+        x.sx1 = s[2] + s[3];
+    }
+    using W = FmtQ4K::W;
+    template <class A>
+    __device__ static void load_w(const A &a, int row, int unit, W &w) { FmtQ4K::load_w(a, row, unit, w); }
+    __device__ static void dot1(const W &w, int unit, const Act &xa, float &acc) {
+        const int j = unit & 3;
+        const float d = f16_bits_to_f32(w.h.x & 0xffffu);
+        const float dmin = f16_bits_to_f32(w.h.x >> 16);
+        const int sh = 16 * (j & 1);
+        uint32_t scp, mp;
+        if (j < 2) {
+            scp = (w.h.y >> sh) & 0x3f3fu;
+            mp = (w.h.z >> sh) & 0x3f3fu;
+        } else {
+            scp = ((w.h.w >> sh) & 0x0f0fu) | (((w.h.y >> sh) >> 2) & 0x3030u);
+            mp = (((w.h.w >> sh) >> 4) & 0x0f0fu) | (((w.h.z >> sh) >> 2) & 0x3030u);
+        }
+        const float d1 = d * (float)(scp & 0xffu), d2 = d * (float)(scp >> 8);
+        const float m1 = dmin * (float)(mp & 0xffu), m2 = dmin * (float)(mp >> 8);
+        const uint32_t qw[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+        {
+            float qlo = 0.0f, qhi = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const uint32_t lo = qw[k] & 0x0f0f0f0fu;
+                const uint32_t hi = (qw[k] >> 4) & 0x0f0f0f0fu;
+                qlo = fmaf((float)(lo & 0xffu), xa.x[4 * k + 0], qlo);
+                qlo = fmaf((float)((lo >> 8) & 0xffu), xa.x[4 * k + 1], qlo);
+                qlo = fmaf((float)((lo >> 16) & 0xffu), xa.x[4 * k + 2], qlo);
+                qlo = fmaf((float)(lo >> 24), xa.x[4 * k + 3], qlo);
+                qhi = fmaf((float)(hi & 0xffu), xa.x[32 + 4 * k + 0], qhi);
+                qhi = fmaf((float)((hi >> 8) & 0xffu), xa.x[32 + 4 * k + 1], qhi);
+                qhi = fmaf((float)((hi >> 16) & 0xffu), xa.x[32 + 4 * k + 2], qhi);
+                qhi = fmaf((float)(hi >> 24), xa.x[32 + 4 * k + 3], qhi);
+            }
+            float r = d1 * qlo - m1 * xa.sx0;
+            r += d2 * qhi - m2 * xa.sx1;
+            acc += r;
+        }
+    }
+};
+
+// Q6_K weights against f32 activations (logits path, dot_q6_k).
+// Unit = (super-block i, half h, l-half p): 4 sub-blocks of 16 elements.
+struct FmtQ6KF32 {
+    static constexpr int kUnitsPerBlock = 4;
+    struct Act {
+        float x[64];      // [k][16]
+        float sx[4];      // sums of x per sub-block 8h+2k+p
+    };
+    __device__ static void load_act(const GemvArgs &a, int unit, int tk, Act &x) {
+        const int i = unit >> 2, h = (unit >> 1) & 1, p = unit & 1;
+        const float *base = a.xf + (size_t)tk * a.K + 256 * i + 128 * h + 16 * p;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 *q = reinterpret_cast<const float4 *>(base + 32 * k);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float4 t = q[v];
+                x.x[16 * k + 4 * v] = t.x; x.x[16 * k + 4 * v + 1] = t.y;
+                x.x[16 * k + 4 * v + 2] = t.z; x.x[16 * k + 4 * v + 3] = t.w;
+            }
+        }
+        const float *s = a.xs + (size_t)tk * (a.K / 16) + 16 * i + 8 * h + p;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) x.sx[k] = s[2 * k];
+    }
+    using W = FmtQ6K::W;
+    template <class A>
+    __device__ static void load_w(const A &a, int row, int unit, W &w) { FmtQ6K::load_w(a, row, unit, w); }
+    __device__ static void dot1(const W &w, int unit, const Act &xa, float &acc) {
+        const int p = unit & 1;
+        const float d = f16_bits_to_f32(w.d);
+        float ds[4];
+        ds[0] = d * (float)(int8_t)((w.sc.x >> (8 * p)) & 0xffu);
+        ds[1] = d * (float)(int8_t)((w.sc.x >> (8 * (2 + p))) & 0xffu);
+        ds[2] = d * (float)(int8_t)((w.sc.y >> (8 * p)) & 0xffu);
+        ds[3] = d * (float)(int8_t)((w.sc.y >> (8 * (2 + p))) & 0xffu);
+        const uint32_t A[4] = {w.A.x, w.A.y, w.A.z, w.A.w};
+        const uint32_t B[4] = {w.B.x, w.B.y, w.B.z, w.B.w};
+        const uint32_t H[4] = {w.H.x, w.H.y, w.H.z, w.H.w};
+        uint32_t c[4][4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            c[0][v] = (A[v] & 0x0f0f0f0fu) | ((H[v] << 4) & 0x30303030u);
+            c[1][v] = (B[v] & 0x0f0f0f0fu) | ((H[v] << 2) & 0x30303030u);
+            c[2][v] = ((A[v] >> 4) & 0x0f0f0f0fu) | (H[v] & 0x30303030u);
+            c[3][v] = ((B[v] >> 4) & 0x0f0f0f0fu) | ((H[v] >> 2) & 0x30303030u);
+        }
+        {
+            float r = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                float s = 0.0f;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const uint32_t cv = c[k][v];
+                    s = fmaf((float)(cv & 0xffu), xa.x[16 * k + 4 * v + 0], s);
+                    s = fmaf((float)((cv >> 8) & 0xffu), xa.x[16 * k + 4 * v + 1], s);
+                    s = fmaf((float)((cv >> 16) & 0xffu), xa.x[16 * k + 4 * v + 2], s);
+                    s = fmaf((float)(cv >> 24), xa.x[16 * k + 4 * v + 3], s);
+                }
+                // sum (q-32)*x = sum q*x - 32*sum x
+                r = fmaf(ds[k], fmaf(-32.0f, xa.sx[k], s), r);
+            }
+            acc += r;
+        }
+    }
+};
+
+// Q8_0 weights against f32 activations (dot_q8_0; used when the activation
+// cannot be quantized).  Unit = one block.
+struct FmtQ80F32 {
+    static constexpr int kUnitsPerBlock = 1;
+    struct Act {
+        float x[32];
+    };
+    __device__ static void load_act(const GemvArgs &a, int unit, int tk, Act &x) {
+        const float4 *p = reinterpret_cast<const float4 *>(a.xf + (size_t)tk * a.K + 32 * unit);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+            const float4 t = p[v];
+            x.x[4 * v] = t.x; x.x[4 * v + 1] = t.y; x.x[4 * v + 2] = t.z; x.x[4 * v + 3] = t.w;
+        }
+    }
+    using W = FmtQ80::W;
+    template <class A>
+    __device__ static void load_w(const A &a, int row, int unit, W &w) { FmtQ80::load_w(a, row, unit, w); }
+    __device__ static void dot1(const W &w, int, const Act &xa, float &acc) {
+        const float d = f16_bits_to_f32(w.d);
+        const uint32_t q[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+        {
+            float s = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                s = fmaf((float)(int8_t)(q[k] & 0xffu), xa.x[4 * k + 0], s);
+                s = fmaf((float)(int8_t)((q[k] >> 8) & 0xffu), xa.x[4 * k + 1], s);
+                s = fmaf((float)(int8_t)((q[k] >> 16) & 0xffu), xa.x[4 * k + 2], s);
+                s = fmaf((float)(int8_t)(q[k] >> 24), xa.x[4 * k + 3], s);
+            }
+            acc = fmaf(d, s, acc);
+        }
+    }
+};
+
+}  // namespace exq

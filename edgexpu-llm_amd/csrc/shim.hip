@@ -29,6 +29,9 @@ hipError_t launch_argmax_rows(const float *s, int m, int n, size_t lds, unsigned
 hipError_t launch_gemm_q8(int type, const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const uint8_t *xq,
                           size_t xq_stride, const float *bias, float *out, int ldo, hipStream_t st);
 bool gemm_q8_supported(int type, int n_out, int K, int m);
+bool gemv_fused_supported(int type, int K, int m);
+hipError_t launch_gemv_fused(int type, int nmat, const uint8_t *const *w, const int *n_out, const float *const *bias,
+                             float *const *out, size_t row_bytes, int K, int m, const float *x, hipStream_t st);
 
 namespace {
 
@@ -72,7 +75,9 @@ bool ensure_init() {
     return edgexpu_hip_init(0) != 0;
 }
 
-hipStream_t pick_stream(void *s) { return s != nullptr ? (hipStream_t)s : g.stream; }
+// A NULL handle is HIP's default (null) stream, as everywhere in HIP: work then
+// orders with the caller's other default-stream work.
+hipStream_t pick_stream(void *s) { return (hipStream_t)s; }
 
 bool gpu_type(uint32_t t) { return t == kTypeQ8_0 || t == kTypeQ4_K || t == kTypeQ6_K; }
 
@@ -91,6 +96,13 @@ size_t act_bytes(uint32_t t, int K) {
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Tuning override: EXQ_FUSED=0 routes decode products through the separate
+// quantize + GEMV kernels.
+bool use_fused() {
+    static const int v = getenv("EXQ_FUSED") ? atoi(getenv("EXQ_FUSED")) : 1;
+    return v != 0;
+}
 
 // Device workspace grown on demand (freed only at shutdown).
 void *workspace(size_t bytes) {
@@ -203,7 +215,7 @@ int edgexpu_hip_init(int device) {
         return 0;
     }
     if (!hip_ok(hipSetDevice(device), "hipSetDevice")) return 0;
-    if (!hip_ok(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking), "hipStreamCreate")) return 0;
+    if (!hip_ok(hipStreamCreate(&g.stream), "hipStreamCreate")) return 0;
     g.device = device;
     g.ready = true;
     return 1;
@@ -337,12 +349,52 @@ int edgexpu_hip_linear_quant_batch_dev(float *out, const float *x, const void *w
         return 0;
     }
     hipStream_t st = pick_stream(stream);
+    if (use_fused() && gemv_fused_supported((int)type, n_in, m)) {
+        // one launch: activation quantized in LDS, integer-dot GEMV
+        const uint8_t *wp = (const uint8_t *)w;
+        return hip_ok(launch_gemv_fused((int)type, 1, &wp, &n_out, &bias, &out, edgexpu_hip_row_bytes(type, n_in),
+                                        n_in, m, x, st),
+                      "gemv_fused")
+                   ? 1
+                   : 0;
+    }
     ActWs a;
     if (!act_ws(type, m, n_in, a)) return 0;
     const hipError_t e = type == kTypeQ8_0 ? launch_quantize_q8_0(x, m, n_in, n_in, a.xq, st)
                                            : launch_quantize_q8_k(x, m, n_in, n_in, a.xq, st);
     if (!hip_ok(e, "quantize activations")) return 0;
     return run_q8_product(type, w, n_out, n_in, m, a.xq, bias, out, n_out, st) ? 1 : 0;
+}
+
+int edgexpu_hip_linear_quant_group_dev(int nmat, float *const *out, const float *x, const void *const *w,
+                                       uint32_t type, const float *const *bias, const int *n_out, int m, int n_in,
+                                       void *stream) {
+    if (!ensure_init()) return 0;
+    if (nmat < 1 || nmat > 4 || out == nullptr || w == nullptr || n_out == nullptr) {
+        set_error(-2, "linear_quant_group: nmat must be 1..4 with out, w and n_out arrays");
+        return 0;
+    }
+    for (int z = 0; z < nmat; ++z) {
+        if (!check_linear_args(out[z], x, w[z], type, m, n_out[z], n_in, "linear_quant_group")) return 0;
+    }
+    if (!aligned16(x)) {
+        set_error(-2, "linear_quant_group: x must be 16-byte aligned");
+        return 0;
+    }
+    hipStream_t st = pick_stream(stream);
+    if (use_fused() && gemv_fused_supported((int)type, n_in, m)) {
+        return hip_ok(launch_gemv_fused((int)type, nmat, (const uint8_t *const *)w, n_out, bias, out,
+                                        edgexpu_hip_row_bytes(type, n_in), n_in, m, x, st),
+                      "gemv_fused")
+                   ? 1
+                   : 0;
+    }
+    for (int z = 0; z < nmat; ++z) {
+        if (!edgexpu_hip_linear_quant_batch_dev(out[z], x, w[z], type, bias != nullptr ? bias[z] : nullptr, m,
+                                                n_out[z], n_in, stream))
+            return 0;
+    }
+    return 1;
 }
 
 int edgexpu_hip_gemv_q8_dev(float *out, const uint8_t *xq, const void *w, uint32_t type, const float *bias, int m,
@@ -458,7 +510,7 @@ int edgexpu_hip_linear_quant_batch(float *out, const float *x, const edgexpu_hip
     if (!hip_ok(hipMemcpyAsync(d, x, (size_t)m * w->n_in * sizeof(float), hipMemcpyHostToDevice, g.stream), "H2D x"))
         return 0;
     if (!edgexpu_hip_linear_quant_batch_dev((float *)(d + xb), (const float *)d, w->data, w->type, w->bias, m,
-                                            w->n_out, w->n_in, nullptr))
+                                            w->n_out, w->n_in, g.stream))
         return 0;
     if (!hip_ok(hipMemcpyAsync(out, d + xb, ob, hipMemcpyDeviceToHost, g.stream), "D2H out")) return 0;
     return hip_ok(hipStreamSynchronize(g.stream), "sync") ? 1 : 0;
@@ -491,7 +543,8 @@ int edgexpu_hip_logits(float *scores, uint32_t *best, const float *hidden, const
     uint32_t *dbest = (uint32_t *)(d + hb + sb);
     if (!hip_ok(hipMemcpyAsync(dh, hidden, (size_t)w->n_in * sizeof(float), hipMemcpyHostToDevice, g.stream), "H2D"))
         return 0;
-    if (!edgexpu_hip_logits_dev(ds, dbest, dh, w->data, w->type, w->bias, 1, w->n_out, w->n_in, chunk_rows, nullptr))
+    if (!edgexpu_hip_logits_dev(ds, dbest, dh, w->data, w->type, w->bias, 1, w->n_out, w->n_in, chunk_rows,
+                                g.stream))
         return 0;
     if (scores != nullptr &&
         !hip_ok(hipMemcpyAsync(scores, ds, (size_t)w->n_out * sizeof(float), hipMemcpyDeviceToHost, g.stream), "D2H"))
@@ -515,7 +568,7 @@ int edgexpu_hip_dequantize(const uint8_t *src, uint32_t type, uint64_t n_element
     uint8_t *d = (uint8_t *)devbuf(so + (size_t)n_elements * sizeof(float));
     if (d == nullptr) return 0;
     if (!hip_ok(hipMemcpyAsync(d, src, sbytes, hipMemcpyHostToDevice, g.stream), "H2D src")) return 0;
-    if (!edgexpu_hip_dequantize_dev(d, type, n_elements, (float *)(d + so), nullptr)) return 0;
+    if (!edgexpu_hip_dequantize_dev(d, type, n_elements, (float *)(d + so), g.stream)) return 0;
     if (!hip_ok(hipMemcpyAsync(dst, d + so, (size_t)n_elements * sizeof(float), hipMemcpyDeviceToHost, g.stream),
                 "D2H dst"))
         return 0;
@@ -534,7 +587,7 @@ static int quantize_host(const float *x, int n, uint8_t *dst, bool k_quant) {
     uint8_t *d = (uint8_t *)devbuf(xo + qb);
     if (d == nullptr) return 0;
     if (!hip_ok(hipMemcpyAsync(d, x, (size_t)n * sizeof(float), hipMemcpyHostToDevice, g.stream), "H2D x")) return 0;
-    if (!quantize_dev((const float *)d, 1, n, d + xo, nullptr, k_quant)) return 0;
+    if (!quantize_dev((const float *)d, 1, n, d + xo, g.stream, k_quant)) return 0;
     if (!hip_ok(hipMemcpyAsync(dst, d + xo, qb, hipMemcpyDeviceToHost, g.stream), "D2H q")) return 0;
     return hip_ok(hipStreamSynchronize(g.stream), "sync") ? 1 : 0;
 }
@@ -554,7 +607,7 @@ int edgexpu_hip_dot_f32_rows(float *out, const uint8_t *w, uint32_t type, const 
     float *dout = (float *)(d + wo + xo);
     if (!hip_ok(hipMemcpyAsync(d, w, rb * (size_t)rows, hipMemcpyHostToDevice, g.stream), "H2D w")) return 0;
     if (!hip_ok(hipMemcpyAsync(dx, x, (size_t)n * sizeof(float), hipMemcpyHostToDevice, g.stream), "H2D x")) return 0;
-    if (!edgexpu_hip_logits_dev(dout, nullptr, dx, d, type, nullptr, 1, rows, n, 0, nullptr)) return 0;
+    if (!edgexpu_hip_logits_dev(dout, nullptr, dx, d, type, nullptr, 1, rows, n, 0, g.stream)) return 0;
     if (!hip_ok(hipMemcpyAsync(out, dout, (size_t)rows * sizeof(float), hipMemcpyDeviceToHost, g.stream), "D2H"))
         return 0;
     return hip_ok(hipStreamSynchronize(g.stream), "sync") ? 1 : 0;
@@ -572,7 +625,7 @@ int edgexpu_hip_dot_q8_rows(float *out, const uint8_t *w, uint32_t type, const u
     float *dout = (float *)(d + wo + xo);
     if (!hip_ok(hipMemcpyAsync(d, w, rb * (size_t)rows, hipMemcpyHostToDevice, g.stream), "H2D w")) return 0;
     if (!hip_ok(hipMemcpyAsync(d + wo, xq, xb, hipMemcpyHostToDevice, g.stream), "H2D xq")) return 0;
-    if (!edgexpu_hip_gemv_q8_dev(dout, d + wo, d, type, nullptr, 1, rows, n, nullptr)) return 0;
+    if (!edgexpu_hip_gemv_q8_dev(dout, d + wo, d, type, nullptr, 1, rows, n, g.stream)) return 0;
     if (!hip_ok(hipMemcpyAsync(out, dout, (size_t)rows * sizeof(float), hipMemcpyDeviceToHost, g.stream), "D2H"))
         return 0;
     return hip_ok(hipStreamSynchronize(g.stream), "sync") ? 1 : 0;

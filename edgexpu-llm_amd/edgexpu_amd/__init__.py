@@ -69,6 +69,8 @@ class HipLib:
         self.weight_free = _sig(L, "edgexpu_hip_weight_free", None, [_vp])
         self.linear_dev = _sig(L, "edgexpu_hip_linear_quant_batch_dev", C.c_int,
                                [_vp, _vp, _vp, C.c_uint32, _vp, C.c_int, C.c_int, C.c_int, _vp])
+        self.linear_group_dev = _sig(L, "edgexpu_hip_linear_quant_group_dev", C.c_int,
+                                     [C.c_int, _vp, _vp, _vp, C.c_uint32, _vp, _vp, C.c_int, C.c_int, _vp])
         self.gemv_q8_dev = _sig(L, "edgexpu_hip_gemv_q8_dev", C.c_int,
                                 [_vp, _vp, _vp, C.c_uint32, _vp, C.c_int, C.c_int, C.c_int, _vp])
         self.logits_dev = _sig(L, "edgexpu_hip_logits_dev", C.c_int,
@@ -138,6 +140,24 @@ def linear_quant_batch(w, qtype: int, x, n_out: int, n_in: int, bias=None, out=N
     L.check(L.linear_dev(_ptr(out), _ptr(x), _ptr(w), qtype, _ptr(bias), m, n_out, n_in, _stream()),
             "linear_quant_batch")
     return out
+
+
+def linear_quant_group(ws, qtype: int, x, n_outs, n_in: int, biases=None, outs=None):
+    """Several projections of one input in one launch (edgexpu_hip_linear_quant_group_dev)."""
+    import torch
+
+    m = x.shape[0]
+    nmat = len(ws)
+    if outs is None:
+        outs = [torch.empty((m, n), dtype=torch.float32, device=x.device) for n in n_outs]
+    arr_p = C.c_void_p * nmat
+    out_a = arr_p(*[o.data_ptr() for o in outs])
+    w_a = arr_p(*[w.data_ptr() for w in ws])
+    b_a = None if biases is None else arr_p(*[None if b is None else b.data_ptr() for b in biases])
+    n_a = (C.c_int * nmat)(*n_outs)
+    L = hip()
+    L.check(L.linear_group_dev(nmat, out_a, _ptr(x), w_a, qtype, b_a, n_a, m, n_in, _stream()), "linear_quant_group")
+    return outs
 
 
 def gemv_q8(w, qtype: int, xq, m: int, n_out: int, n_in: int, bias=None, out=None):

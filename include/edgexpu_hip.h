@@ -4,7 +4,9 @@
  *
  * Plain C types only (no HIP or torch types): device pointers are `void *` /
  * typed pointers into device memory, streams are `void *` holding a
- * hipStream_t (NULL = the library's own stream).
+ * hipStream_t; NULL is HIP's default (null) stream.  The host-pointer entry
+ * points run on the library's own stream (edgexpu_hip_stream()) and return
+ * only when their results are in host memory.
  *
  * Conventions shared by every entry point:
  *  - Return 1 on success, 0 on failure.  A failure records a sticky error
@@ -87,6 +89,15 @@ int edgexpu_hip_weight_n_in(const edgexpu_hip_weight *w);
  * 16-byte aligned; bias may be NULL. */
 int edgexpu_hip_linear_quant_batch_dev(float *out, const float *x, const void *w, uint32_t type,
                                        const float *bias, int m, int n_out, int n_in, void *stream);
+
+/* Several projections of the same input in one launch (q/k/v, or gate/up):
+ * out[z][t*n_out[z] + o] = bias[z][o] + dot(W_z[o], q8(x[t])) for z < nmat
+ * (1..4).  All matrices share type and n_in; bias may be NULL or hold NULL
+ * entries.  Equivalent to nmat edgexpu_hip_linear_quant_batch_dev calls
+ * (src/native.c:2530-2532 and :2576-2577 issue them back to back). */
+int edgexpu_hip_linear_quant_group_dev(int nmat, float *const *out, const float *x, const void *const *w,
+                                       uint32_t type, const float *const *bias, const int *n_out, int m, int n_in,
+                                       void *stream);
 
 /* The integer block-dot product alone, for activations already quantized
  * into the reference's block bytes (one token = n_in/32 Q8_0 blocks for Q8_0

@@ -164,13 +164,16 @@ def q6_k_lanes(wsb, xsb):
 def q8_dot_f64(qtype: int, wrow: np.ndarray, xq: np.ndarray):
     """Exact-integer, float64-combined row dot against quantized activations.
 
-    Returns (value, S) with S = sum over blocks of |dx*dw*isum| + |dx*dmin*imin|."""
+    Returns (value, S) with S the element-level conditioning scale
+    sum_k |dx*dw*sc*q_k*q8_k| (+ sum_k |dx*dmin*m*q8_k| for Q4_K): any fp32
+    summation order of the row, the reference's AVX2 lanes included, stays
+    within a few ulp of S."""
     if qtype == 8:
         dw, qw = q8_0_parts(wrow)
         dx, qx = q8_0_parts(xq)
         isum = (qw * qx).sum(axis=1)
-        t = dw.astype(np.float64) * dx.astype(np.float64) * isum
-        return t.sum(), np.abs(t).sum()
+        scale = dw.astype(np.float64) * dx.astype(np.float64)
+        return (scale * isum).sum(), (np.abs(scale)[:, None] * np.abs(qw * qx)).sum()
     xb = xq.reshape(-1, 292)
     dx = xb[:, 0:4].copy().view(np.float32)[:, 0].astype(np.float64)
     q8 = xb[:, 4:260].view(np.int8).astype(np.int64)
@@ -182,13 +185,15 @@ def q8_dot_f64(qtype: int, wrow: np.ndarray, xq: np.ndarray):
         imin = (m * bs.reshape(-1, 8, 2).sum(axis=2)).sum(axis=1)
         a = dx * d.astype(np.float64) * isum
         b = dx * dmin.astype(np.float64) * imin
-        return (a - b).sum(), (np.abs(a) + np.abs(b)).sum()
+        mag = (np.abs(dx * d.astype(np.float64))[:, None] * np.abs(sc[:, sub] * codes * q8)).sum() + \
+            (np.abs(dx * dmin.astype(np.float64))[:, None] * np.abs(m[:, sub] * q8)).sum()
+        return (a - b).sum(), mag
     if qtype == 14:
         d, sc, codes = q6_k_parts(wrow)
         sub = np.repeat(np.arange(16), 16)
-        isum = (sc[:, sub] * (codes - 32) * q8).sum(axis=1)
-        a = dx * d.astype(np.float64) * isum
-        return a.sum(), np.abs(a).sum()
+        terms = sc[:, sub] * (codes - 32) * q8
+        a = dx * d.astype(np.float64) * terms.sum(axis=1)
+        return a.sum(), (np.abs(dx * d.astype(np.float64))[:, None] * np.abs(terms)).sum()
     raise ValueError(qtype)
 
 

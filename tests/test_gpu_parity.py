@@ -111,7 +111,7 @@ def test_linear_golden(hipdev, ora, golden, name):
     y = E.linear_quant_batch(dev(w), qt, dev(x), n_out, n_in).cpu().numpy()
     assert_tol(y, g["out"], S, name)
     yb = E.linear_quant_batch(dev(w), qt, dev(x), n_out, n_in, bias=dev(bias)).cpu().numpy()
-    assert_tol(yb, g["out_bias"], S, name + "+bias")
+    assert_tol(yb, g["out_bias"], S + np.abs(bias)[None, :], name + "+bias")
 
 
 @pytest.mark.parametrize("qt,n_in,n_out", [(8, 576, 577), (8, 1536, 300), (12, 4096, 1001), (12, 2560, 515),
@@ -126,7 +126,8 @@ def test_linear_random_vs_oracle(hipdev, ora, qt, n_in, n_out, m):
     want = ora.linear_quant_batch(x, w, qt, bias, m, n_out, n_in)
     got = E.linear_quant_batch(dev(w), qt, dev(x), n_out, n_in, bias=dev(bias)).cpu().numpy()
     S = q8_scales(ora, qt, w, x) if n_out * m <= 4000 else np.abs(want) * 0 + np.abs(want).max() * 10
-    assert_tol(got, want, S, f"{TN[qt]} {n_out}x{n_in} m={m}")
+    # out = bias + dot: the final addition is conditioned by |bias| too
+    assert_tol(got, want, S + np.abs(bias)[None, :], f"{TN[qt]} {n_out}x{n_in} m={m}")
 
 
 @pytest.mark.parametrize("qt,n_in,n_out", [(12, 4096, 14336), (12, 14336, 4096), (8, 576, 49152), (14, 9728, 2560)])
@@ -256,3 +257,29 @@ def test_bad_arguments_are_rejected(hipdev):
     assert "not supported" in msg
     L.clear_error()
     assert L.last_error()[0] == 0
+
+
+# ------------------------------------------------------------------ grouped launches
+
+
+@pytest.mark.parametrize("qt,n_in,n_outs", [(12, 4096, (4096, 1024, 1024)), (12, 4096, (14336, 14336)),
+                                            (8, 576, (576, 192, 192)), (14, 2560, (300, 7)),
+                                            (12, 14336, (4096,)), (12, 2560, (4096, 1024, 1024, 33))])
+@pytest.mark.parametrize("m", [1, 3])
+def test_linear_group_matches_single(hipdev, ora, qt, n_in, n_outs, m):
+    """One grouped launch == the per-projection calls (and the oracle)."""
+    rng = np.random.default_rng(sum(n_outs) + n_in + m)
+    ws = [synth.np_weights(qt, n, n_in, rng) for n in n_outs]
+    x = synth.np_activations(m, n_in, rng)
+    biases = [rng.normal(0, 0.1, n).astype(np.float32) if z % 2 == 0 else None for z, n in enumerate(n_outs)]
+    outs = E.linear_quant_group([dev(w) for w in ws], qt, dev(x), list(n_outs), n_in,
+                                biases=[None if b is None else dev(b) for b in biases])
+    for z, (w, n) in enumerate(zip(ws, n_outs)):
+        got = outs[z].cpu().numpy()
+        single = E.linear_quant_batch(dev(w), qt, dev(x), n, n_in,
+                                      bias=None if biases[z] is None else dev(biases[z])).cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), single.view(np.uint32)), f"matrix {z}"
+        want = ora.linear_quant_batch(x, w, qt, biases[z], m, n, n_in)
+        sample = np.arange(min(n, 48))
+        S = q8_scales(ora, qt, w[sample], x) + (0 if biases[z] is None else np.abs(biases[z][sample]))
+        assert_tol(got[:, sample], want[:, sample], S, f"group matrix {z}")
