@@ -58,7 +58,8 @@ struct FmtQ4K {
         float dx;         // Q8_K block scale
         uint32_t spair;   // int16 pair: sums of sub-blocks 2j and 2j+1
     };
-    __device__ static void load_act(const GemvArgs &a, int unit, int tk, Act &x) {
+    template <class A>
+    __device__ static void load_act(const A &a, int unit, int tk, Act &x) {
         const int i = unit >> 2, j = unit & 3;
         const uint8_t *blk = a.xq + (size_t)tk * a.xq_stride + (size_t)i * kBytesQ8_K;
 #pragma unroll
@@ -148,7 +149,8 @@ struct FmtQ6K {
         float dx;
         int bs32[4];      // 32 * (16-element code sum) of sub-block 8h+2k+p
     };
-    __device__ static void load_act(const GemvArgs &a, int unit, int tk, Act &x) {
+    template <class A>
+    __device__ static void load_act(const A &a, int unit, int tk, Act &x) {
         const int i = unit >> 2, h = (unit >> 1) & 1, p = unit & 1;
         const uint8_t *blk = a.xq + (size_t)tk * a.xq_stride + (size_t)i * kBytesQ8_K;
 #pragma unroll
@@ -231,7 +233,8 @@ struct FmtQ80 {
         uint32_t q[8];
         float dx;
     };
-    __device__ static void load_act(const GemvArgs &a, int unit, int tk, Act &x) {
+    template <class A>
+    __device__ static void load_act(const A &a, int unit, int tk, Act &x) {
         const uint8_t *blk = a.xq + (size_t)tk * a.xq_stride + (size_t)unit * kBytesQ8_0;
         const uint4 t0 = ldg16(blk + 2), t1 = ldg16(blk + 18);
         x.q[0] = t0.x; x.q[1] = t0.y; x.q[2] = t0.z; x.q[3] = t0.w;

@@ -31,13 +31,19 @@ hipError_t launch_gemm_q8(int type, const uint8_t *w, size_t row_bytes, int n_ou
 bool gemm_q8_supported(int type, int n_out, int K, int m);
 bool gemv_fused_supported(int type, int K, int m);
 hipError_t launch_gemv_fused(int type, int nmat, const uint8_t *const *w, const int *n_out, const float *const *bias,
-                             float *const *out, size_t row_bytes, int K, int m, const float *x, hipStream_t st);
+                             float *const *out, size_t row_bytes, int K, int m, const float *x, const uint8_t *xq,
+                             size_t xq_stride, hipStream_t st);
 
 namespace {
 
 constexpr size_t kLogitChunkBytes = (size_t)48u * 1024u * 1024u;  // include/edgexpu/scheduler.h:34
 constexpr int kGemvMaxTokens = 8;
+constexpr int kFusedMaxTokens = 4;
 constexpr int kGemmMinTokens = 64;
+// Rows up to this many elements quantize the activation inside the GEMV
+// workgroups; longer rows quantize it once in its own launch (the in-kernel
+// staging costs one load latency per 8192 elements per workgroup).
+constexpr int kStageMaxK = 4096;
 constexpr int kArgmaxParts = 1024;
 
 struct State {
@@ -97,11 +103,24 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-// Tuning override: EXQ_FUSED=0 routes decode products through the separate
-// quantize + GEMV kernels.
-bool use_fused() {
-    static const int v = getenv("EXQ_FUSED") ? atoi(getenv("EXQ_FUSED")) : 1;
-    return v != 0;
+// Tuning overrides: EXQ_FUSED=0 never quantizes inside the GEMV, 2 always
+// does (where the kernel covers the shape), 1 (default) by row length;
+// EXQ_GENERIC=1 sends every quantized-activation GEMV to the generic kernel.
+int env_int(const char *name, int dflt) {
+    const char *e = getenv(name);
+    return e != nullptr ? atoi(e) : dflt;
+}
+
+bool stage_in_kernel(uint32_t type, int K, int m) {
+    static const int mode = env_int("EXQ_FUSED", 1);
+    static const int generic = env_int("EXQ_GENERIC", 0);
+    if (mode == 0 || generic != 0 || !gemv_fused_supported((int)type, K, m)) return false;
+    return mode == 2 || K <= kStageMaxK;
+}
+
+bool split_gemv(uint32_t type, int K, int m) {
+    static const int generic = env_int("EXQ_GENERIC", 0);
+    return generic == 0 && m <= kFusedMaxTokens && gemv_fused_supported((int)type, K, m);
 }
 
 // Device workspace grown on demand (freed only at shutdown).
@@ -179,11 +198,45 @@ bool run_q8_product(uint32_t type, const void *w, int n_out, int n_in, int m, co
         return hip_ok(launch_gemm_q8((int)type, (const uint8_t *)w, rb, n_out, n_in, m, xq, ab, bias, out, ldo, st),
                       "gemm_q8");
     }
+    if (ldo == n_out && split_gemv(type, n_in, m)) {
+        const uint8_t *wp = (const uint8_t *)w;
+        return hip_ok(launch_gemv_fused((int)type, 1, &wp, &n_out, &bias, &out, rb, n_in, m, nullptr, xq, ab, st),
+                      "gemv_split");
+    }
     for (int t0 = 0; t0 < m; t0 += kGemvMaxTokens) {
         const int mt = m - t0 < kGemvMaxTokens ? m - t0 : kGemvMaxTokens;
         if (!hip_ok(launch_gemv_q8((int)type, (const uint8_t *)w, rb, n_out, n_in, mt, xq + (size_t)t0 * ab, ab,
                                    bias, out + (size_t)t0 * ldo, ldo, st),
                     "gemv_q8"))
+            return false;
+    }
+    return true;
+}
+
+// nmat products over one input x (f32, [m][n_in]): either one launch that
+// quantizes x inside its workgroups, or one quantize launch followed by one
+// launch over all nmat matrices (m <= 4) or per-matrix products.
+bool run_linear_group(uint32_t type, int nmat, const void *const *w, const int *n_out, const float *const *bias,
+                      float *const *out, const float *x, int m, int n_in, hipStream_t st) {
+    const size_t rb = edgexpu_hip_row_bytes(type, n_in);
+    if (stage_in_kernel(type, n_in, m)) {
+        return hip_ok(launch_gemv_fused((int)type, nmat, (const uint8_t *const *)w, n_out, bias, out, rb, n_in, m, x,
+                                        nullptr, 0, st),
+                      "gemv_fused");
+    }
+    ActWs a;
+    if (!act_ws(type, m, n_in, a)) return false;
+    const hipError_t e = type == kTypeQ8_0 ? launch_quantize_q8_0(x, m, n_in, n_in, a.xq, st)
+                                           : launch_quantize_q8_k(x, m, n_in, n_in, a.xq, st);
+    if (!hip_ok(e, "quantize activations")) return false;
+    if (split_gemv(type, n_in, m) && m < kGemmMinTokens) {
+        return hip_ok(launch_gemv_fused((int)type, nmat, (const uint8_t *const *)w, n_out, bias, out, rb, n_in, m,
+                                        nullptr, a.xq, act_bytes(type, n_in), st),
+                      "gemv_split");
+    }
+    for (int z = 0; z < nmat; ++z) {
+        if (!run_q8_product(type, w[z], n_out[z], n_in, m, a.xq, bias != nullptr ? bias[z] : nullptr, out[z],
+                            n_out[z], st))
             return false;
     }
     return true;
@@ -348,22 +401,8 @@ int edgexpu_hip_linear_quant_batch_dev(float *out, const float *x, const void *w
         set_error(-2, "linear_quant_batch: x must be 16-byte aligned");
         return 0;
     }
-    hipStream_t st = pick_stream(stream);
-    if (use_fused() && gemv_fused_supported((int)type, n_in, m)) {
-        // one launch: activation quantized in LDS, integer-dot GEMV
-        const uint8_t *wp = (const uint8_t *)w;
-        return hip_ok(launch_gemv_fused((int)type, 1, &wp, &n_out, &bias, &out, edgexpu_hip_row_bytes(type, n_in),
-                                        n_in, m, x, st),
-                      "gemv_fused")
-                   ? 1
-                   : 0;
-    }
-    ActWs a;
-    if (!act_ws(type, m, n_in, a)) return 0;
-    const hipError_t e = type == kTypeQ8_0 ? launch_quantize_q8_0(x, m, n_in, n_in, a.xq, st)
-                                           : launch_quantize_q8_k(x, m, n_in, n_in, a.xq, st);
-    if (!hip_ok(e, "quantize activations")) return 0;
-    return run_q8_product(type, w, n_out, n_in, m, a.xq, bias, out, n_out, st) ? 1 : 0;
+    const void *wp = w;
+    return run_linear_group(type, 1, &wp, &n_out, &bias, &out, x, m, n_in, pick_stream(stream)) ? 1 : 0;
 }
 
 int edgexpu_hip_linear_quant_group_dev(int nmat, float *const *out, const float *x, const void *const *w,
@@ -381,20 +420,7 @@ int edgexpu_hip_linear_quant_group_dev(int nmat, float *const *out, const float 
         set_error(-2, "linear_quant_group: x must be 16-byte aligned");
         return 0;
     }
-    hipStream_t st = pick_stream(stream);
-    if (use_fused() && gemv_fused_supported((int)type, n_in, m)) {
-        return hip_ok(launch_gemv_fused((int)type, nmat, (const uint8_t *const *)w, n_out, bias, out,
-                                        edgexpu_hip_row_bytes(type, n_in), n_in, m, x, st),
-                      "gemv_fused")
-                   ? 1
-                   : 0;
-    }
-    for (int z = 0; z < nmat; ++z) {
-        if (!edgexpu_hip_linear_quant_batch_dev(out[z], x, w[z], type, bias != nullptr ? bias[z] : nullptr, m,
-                                                n_out[z], n_in, stream))
-            return 0;
-    }
-    return 1;
+    return run_linear_group(type, nmat, w, n_out, bias, out, x, m, n_in, pick_stream(stream)) ? 1 : 0;
 }
 
 int edgexpu_hip_gemv_q8_dev(float *out, const uint8_t *xq, const void *w, uint32_t type, const float *bias, int m,
