@@ -9,10 +9,16 @@ seeded synthetic GGUF blocks resident in HBM before the timed region (so no
 two launches share cached weights), activations are synthetic f32 N(0,1).
 
 Prints one JSON line: value = algorithmic bytes of the step (weights + x + y)
-per second, a `roofline` object for the dominant kernel (the Q4_K x Q8_K GEMV
-at the [14336 x 4096] gate/up shape, timed with HIP events on its own stream)
-and a `cpu_baseline` object (the reference's own CPU kernels built from
-source, oracle/_ref, timed on this host's cores on a bounded sample).
+per second, a `roofline` object for the dominant kernel (the grouped
+gate+up launch, [2 x 14336 x 4096] Q4_K x Q8_K for the default workload,
+timed with HIP events on the stream it is launched on) and a `cpu_baseline`
+object (the reference's own CPU kernels built from source, oracle/_ref, timed
+on this host's cores on a bounded sample).
+
+`roofline.traffic` is the HBM bytes per launch of that kernel as measured by
+rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, calibrated against a plain copy of
+known size (--calibrate-copy runs that copy before the timed region); the
+figures are read from profiles/traffic_<workload>.json when present.
 """
 from __future__ import annotations
 
@@ -54,7 +60,23 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU-baseline sample")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--seed", type=int, default=20261203)
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="first copy a 256 MiB buffer 4 times (device to device) for counter calibration")
     return p.parse_args()
+
+
+COPY_BYTES = 256 << 20
+
+
+def traffic_from_profile(workload):
+    """HBM bytes per launch of the dominant kernel, from a committed counter summary."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
+    try:
+        with open(path) as fh:
+            d = json.load(fh)
+        return d.get("bytes_per_launch"), d
+    except (OSError, ValueError):
+        return None, None
 
 
 def projections(cfg):
@@ -114,6 +136,13 @@ def main():
     scores = torch.empty((m, cfg["vocab"]), device=dev)
     best = torch.empty(m, dtype=torch.int32, device=dev)
     torch.cuda.synchronize()
+    if args.calibrate_copy:
+        src_buf = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+        dst_buf = torch.empty_like(src_buf)
+        for _ in range(4):
+            dst_buf.copy_(src_buf)
+        torch.cuda.synchronize()
+        del src_buf, dst_buf
 
     step_bytes = 0
     for name, t, n_out, n_in, _ in projs:
@@ -222,12 +251,16 @@ def main():
     per_kernel["logits"] = {"shape": [cfg["vocab"], cfg["hidden"]], "type": E.TYPE_NAMES[cfg["logits_type"]],
                             "us": round(lus, 3), "bytes": lbytes, "GBps": round(lbytes / (lus * 1e-6) / 1e9, 1)}
 
-    dom_name = "gate"
+    dom_name = "gate_up"
     dom = per_kernel[dom_name]
+    traffic, tinfo = traffic_from_profile(args.workload)
     roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": f"gemv_fused_kernel<{E.TYPE_NAMES[cfg['wtype']]}> {dom['shape'][0]}x{dom['shape'][1]} m={m}",
+                "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "kernel": f"gemv_fused_kernel ({E.TYPE_NAMES[cfg['wtype']]}, gate+up grouped) "
+                          f"{dom['shape'][0]}x{dom['shape'][1]} m={m}",
                 "us_per_launch": dom["us"], "bytes_per_launch": dom["bytes"]}
+    if tinfo is not None:
+        roofline["traffic_source"] = tinfo.get("source")
 
     # ---------------------------------------------------------------- CPU baseline
     cpu = None

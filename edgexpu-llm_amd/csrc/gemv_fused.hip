@@ -180,7 +180,7 @@ struct FusedLds {
         qbytes = ((size_t)m * K + 15) & ~(size_t)15;
         dbytes = (((size_t)m * nblk * 4) + 15) & ~(size_t)15;
         bbytes = q8k ? ((((size_t)m * (K / 16) * 2) + 15) & ~(size_t)15) : 0;
-        rbytes = (size_t)NW * S * NV * sizeof(float);
+        rbytes = 2 * (size_t)NW * S * NV * sizeof(float);  // two buffers, alternating by tile
     }
     __host__ __device__ size_t total() const { return qbytes + dbytes + bbytes + rbytes; }
 };
@@ -189,14 +189,16 @@ struct FusedLds {
 // weight matrix to be requested by one generation of workgroups, without
 // spilling (checked with -Rpass-analysis=kernel-resource-usage).
 template <class Fmt>
-constexpr int fused_occupancy(int nv) {
-    return nv <= 1 ? (sizeof(typename Fmt::W) > 48 ? 7 : 8) : nv <= 2 ? 6 : (sizeof(typename Fmt::W) > 48 ? 4 : 5);
+constexpr int fused_occupancy(int r, int m) {
+    return r * m <= 1   ? (sizeof(typename Fmt::W) > 48 ? 6 : 8)
+           : r * m <= 2 ? (sizeof(typename Fmt::W) > 48 ? (m > 1 ? 4 : 5) : 6)
+                        : 4;
 }
 
 // STAGE: quantize a.x into LDS inside the kernel; otherwise read the codes
 // of a.xq (quantized by an earlier launch) straight from global memory.
 template <class Fmt, int M, int R, int NW, bool STAGE>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(fused_occupancy<Fmt>(R * M)))) void
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(fused_occupancy<Fmt>(R, M)))) void
 gemv_fused_kernel(FusedArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     // wave-uniform values go through readfirstlane so that the tile, matrix
@@ -219,86 +221,115 @@ gemv_fused_kernel(FusedArgs a) {
     int8_t *lq = reinterpret_cast<int8_t *>(smem);
     float *ld = reinterpret_cast<float *>(smem + L.qbytes);
     int16_t *lbs = reinterpret_cast<int16_t *>(smem + L.qbytes + L.dbytes);
-    float *red = reinterpret_cast<float *>(smem + L.qbytes + L.dbytes + L.bbytes);  // [wave][slot][NV]
+    float *red = reinterpret_cast<float *>(smem + L.qbytes + L.dbytes + L.bbytes);  // [2][wave][slot][NV]
 
-    // 1. this wave's weight loads go out before the activation is staged;
-    //    they are unconditional (clamped tile, row and unit) so every path
-    //    issues the same loads
-    const int tile = blockIdx.x * RG + rg;
-    const bool have = tile < a.ntiles;
-    int z, row0;
-    locate(a, min(tile, a.ntiles - 1), rows_per_tile, z, row0);
-    const WSrc src{a.w[z], a.row_bytes};
+    // The one output value (if any) this lane stores: with G >= V the
+    // reduction leaves each lane at most one value.  KS == 1: writer lanes of
+    // every wave; KS > 1: the first S*NV lanes of the row group's first wave.
+    static_assert(V <= 16, "group_reduce leaves one value per lane only for V <= G (G >= 16)");
+    const int base = group_reduce_index(V, G, gl);
+    const int spread = V < G ? G / V : 1;
+    int o_slot, o_idx;
+    bool o_live;
+    if (KS == 1) {
+        o_slot = slot;
+        o_idx = base;
+        o_live = (gl & (spread - 1)) == 0 && base < NV;
+    } else {
+        o_slot = lane / NV;
+        o_idx = lane - o_slot * NV;
+        o_live = ks == 0 && lane < S * NV;
+    }
+    const int o_r = o_idx / M, o_t = o_idx - (o_idx / M) * M;
+
+    // Loads of one tile: weights (unconditional: clamped tile, row and unit,
+    // so every path issues the same loads) and the bias of this lane's output.
+    const int wg_tiles = (a.ntiles + RG - 1) / RG;
     typename Fmt::W w[R];
+    auto load_tile = [&](int wt_, int &z_, int &row0_, float &bias_) {
+        locate(a, min(wt_ * RG + rg, a.ntiles - 1), rows_per_tile, z_, row0_);
+        const WSrc src{a.w[z_], a.row_bytes};
 #pragma unroll
-    for (int r = 0; r < R; ++r) Fmt::load_w(src, min(row0 + slot + S * r, a.n_out[z] - 1), u, w[r]);
+        for (int r = 0; r < R; ++r) Fmt::load_w(src, min(row0_ + slot + S * r, a.n_out[z_] - 1), u, w[r]);
+        bias_ = 0.0f;
+        const float *bp = a.bias[z_];
+        if (bp != nullptr && o_live) bias_ = bp[min(row0_ + o_slot + S * o_r, a.n_out[z_] - 1)];
+    };
 
-    // 2. quantize the activation into LDS, then take this lane's slices
+    // 1. the first tile's loads go out before the activation is staged
+    int wt = blockIdx.x;
+    int z, row0;
+    float bias;
+    load_tile(wt, z, row0, bias);
+
+    // 2. quantize the activation into LDS once per workgroup
     if (STAGE) {
         if (kQ8K) stage_q8_k<NW * 64>(a, lq, ld, lbs);
         else stage_q8_0<NW * 64>(a, lq, ld);
         __syncthreads();
     }
     const ActLds act{lq, ld, lbs, a.K, a.nblk};
-
-    // 3. dot products, reduction over the G lanes of each slot
-    float vals[V];
-#pragma unroll
-    for (int k = 0; k < V; ++k) vals[k] = 0.0f;
-    if (unit < a.U) {
-#pragma unroll
-        for (int t = 0; t < M; ++t) {
-            typename Fmt::Act x;
-            if (STAGE) Fmt::load_act_lds(act, u, t, x);
-            else Fmt::load_act(a, u, t, x);
-#pragma unroll
-            for (int r = 0; r < R; ++r) Fmt::dot1(w[r], u, x, vals[r * M + t]);
-        }
+    // one token: the activation slice stays in registers for every tile
+    typename Fmt::Act x1;
+    if (M == 1) {
+        if (STAGE) Fmt::load_act_lds(act, u, 0, x1);
+        else Fmt::load_act(a, u, 0, x1);
     }
-    group_reduce<V>(vals, G, lane);
-    const int live = group_reduce_live(V, G);
-    const int base = group_reduce_index(V, G, gl);
-    const int spread = V < G ? G / V : 1;
-    const bool writer = (gl & (spread - 1)) == 0;
 
-    // 4. for KS > 1 the KS waves of a row group add their partials in LDS
-    //    (in wave order, so the result does not depend on timing)
-    if (KS > 1) {
-        if (writer) {
+    // 3. grid-stride loop over workgroup tiles (a uniform trip count, so the
+    //    barriers of the KS > 1 reduction line up).  The next tile's loads are
+    //    issued as soon as the current tile's weights have been consumed, so
+    //    the lane reduction and the store overlap them; the resident waves of
+    //    the CU hide the rest of the latency.
+    for (int iter = 0;; ++iter) {
+        const bool have = wt * RG + rg < a.ntiles;
+        float vals[V];
 #pragma unroll
-            for (int k = 0; k < V; ++k) {
-                if (k >= live) break;
-                const int idx = base + k;
-                if (idx < NV) red[(wave * S + slot) * NV + idx] = vals[k];
+        for (int k = 0; k < V; ++k) vals[k] = 0.0f;
+        if (unit < a.U) {
+#pragma unroll
+            for (int t = 0; t < M; ++t) {
+                typename Fmt::Act x;
+                if (M == 1) x = x1;
+                else if (STAGE) Fmt::load_act_lds(act, u, t, x);
+                else Fmt::load_act(a, u, t, x);
+#pragma unroll
+                for (int r = 0; r < R; ++r) Fmt::dot1(w[r], u, x, vals[r * M + t]);
             }
         }
-        __syncthreads();
-        if (ks != 0 || !have) return;
-        if (lane >= S * NV) return;
-        const int sl = lane / NV, idx = lane - sl * NV;
-        float sum = 0.0f;
-        for (int k2 = 0; k2 < KS; ++k2) sum += red[((rg * KS + k2) * S + sl) * NV + idx];
-        const int r = idx / M, t = idx - r * M;
-        const int row = row0 + sl + S * r;
-        if (row < a.n_out[z]) {
-            const float b = a.bias[z] != nullptr ? a.bias[z][row] : 0.0f;
-            a.out[z][(size_t)t * a.n_out[z] + row] = b + sum;
+        const int cz = z, crow0 = row0;
+        const float cbias = bias;
+        wt += gridDim.x;
+        const bool more = wt < wg_tiles;  // uniform over the workgroup
+        if (more) load_tile(wt, z, row0, bias);
+
+        group_reduce<V>(vals, G, lane);
+        float result = vals[0];
+        if (KS > 1) {
+            // the KS waves of a row group add their partials in LDS, in wave
+            // order; the buffer alternates by iteration, so one barrier per
+            // iteration keeps the next write away from this read
+            float *rb = red + (iter & 1) * (NW * S * NV);
+            if ((gl & (spread - 1)) == 0 && base < NV) rb[(wave * S + slot) * NV + base] = vals[0];
+            __syncthreads();
+            result = 0.0f;
+            if (o_live)
+                for (int k2 = 0; k2 < KS; ++k2) result += rb[((rg * KS + k2) * S + o_slot) * NV + o_idx];
         }
-        return;
-    }
-    if (!have || !writer) return;
-#pragma unroll
-    for (int k = 0; k < V; ++k) {
-        if (k >= live) break;
-        const int idx = base + k;
-        if (idx >= NV) break;  // padding
-        const int r = idx / M, t = idx - r * M;
-        const int row = row0 + slot + S * r;
-        if (row < a.n_out[z]) {
-            const float b = a.bias[z] != nullptr ? a.bias[z][row] : 0.0f;
-            a.out[z][(size_t)t * a.n_out[z] + row] = b + vals[k];
+        if (have && o_live) {
+            const int row = crow0 + o_slot + S * o_r;
+            if (row < a.n_out[cz]) a.out[cz][(size_t)o_t * a.n_out[cz] + row] = cbias + result;
         }
+        if (!more) break;
     }
+}
+
+// Tuning overrides: EXQ_FUSED_R (rows per slot at m = 1: 1, 2 or 4),
+// EXQ_FUSED_NW (waves per workgroup: 4 or 8), EXQ_FUSED_GRID (multiple of the
+// resident workgroup count).
+static int env_int(const char *name, int dflt) {
+    const char *e = getenv(name);
+    return e != nullptr ? atoi(e) : dflt;
 }
 
 template <class Fmt, int M, int R, int NW, bool STAGE>
@@ -313,17 +344,36 @@ static hipError_t launch_fused_fmt(FusedArgs a, hipStream_t st) {
     for (int z = a.nmat; z <= kFusedMaxMats; ++z) a.tile_start[z] = t;
     a.ntiles = t;
     const FusedLds L(a.m, a.K, a.nblk, Fmt::kUnitsPerBlock == 4, NW, S, R * M, STAGE);
-    const int grid = (t + RG - 1) / RG;
+    const int wg_tiles = (t + RG - 1) / RG;
+    // resident workgroups from the kernel's real occupancy (registers + LDS);
+    // the grid takes at most that many, each looping over the same number of
+    // tiles, so no second generation of workgroups forms a tail
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    static size_t cached_lds = (size_t)-1;
+    static int per_cu = 1;
+    if (L.total() != cached_lds) {
+        int v = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_fused_kernel<Fmt, M, R, NW, STAGE>, NW * 64,
+                                                         L.total()) != hipSuccess ||
+            v < 1)
+            v = 1;
+        per_cu = v;
+        cached_lds = L.total();
+    }
+    static const int grid_scale = env_int("EXQ_FUSED_GRID", 1);  // tuning override: resident multiple
+    const int resident = per_cu * cus * (grid_scale > 0 ? grid_scale : 1);
+    const int rounds = (wg_tiles + resident - 1) / resident;
+    const int grid = (wg_tiles + rounds - 1) / rounds;
     hipLaunchKernelGGL((gemv_fused_kernel<Fmt, M, R, NW, STAGE>), dim3(grid), dim3(NW * 64), L.total(), st, a);
     return hipGetLastError();
 }
 
-// Tuning overrides: EXQ_FUSED_R (rows per slot at m = 1: 1, 2 or 4) and
-// EXQ_FUSED_NW (waves per workgroup: 4 or 8).
-static int env_int(const char *name, int dflt) {
-    const char *e = getenv(name);
-    return e != nullptr ? atoi(e) : dflt;
-}
 
 template <class Fmt, int NW, bool STAGE>
 static hipError_t launch_fused_m(FusedArgs a, int r1, hipStream_t st) {
@@ -332,18 +382,25 @@ static hipError_t launch_fused_m(FusedArgs a, int r1, hipStream_t st) {
             if (r1 == 1) return launch_fused_fmt<Fmt, 1, 1, NW, STAGE>(a, st);
             if (r1 == 4) return launch_fused_fmt<Fmt, 1, 4, NW, STAGE>(a, st);
             return launch_fused_fmt<Fmt, 1, 2, NW, STAGE>(a, st);
-        case 2: return launch_fused_fmt<Fmt, 2, 2, NW, STAGE>(a, st);
+        case 2: return launch_fused_fmt<Fmt, 2, 1, NW, STAGE>(a, st);
         case 3: return launch_fused_fmt<Fmt, 3, 1, NW, STAGE>(a, st);
         case 4: return launch_fused_fmt<Fmt, 4, 1, NW, STAGE>(a, st);
         default: return hipErrorInvalidValue;
     }
 }
 
+// Tile shape: 8 waves per workgroup; R = 4 rows per slot at m = 1 unless
+// the launch is short and unsplit (<= 4096 rows), where R = 2 keeps more
+// workgroups in flight.  (Measured on [1024..28672 x 4096] and
+// [4096 x 14336] Q4_K.)  EXQ_FUSED_R / EXQ_FUSED_NW override.
 template <class Fmt>
 static hipError_t launch_fused_nw(FusedArgs a, bool stage, hipStream_t st) {
-    static const int r1 = env_int("EXQ_FUSED_R", 2);
+    static const int r_env = env_int("EXQ_FUSED_R", 0);
     static const int nw = env_int("EXQ_FUSED_NW", 8);
     if (a.KS > 4) return hipErrorInvalidValue;
+    int rows = 0;
+    for (int z = 0; z < a.nmat; ++z) rows += a.n_out[z];
+    const int r1 = r_env > 0 ? r_env : (a.KS == 1 && rows <= 4096 ? 2 : 4);
     if (stage) return nw == 4 ? launch_fused_m<Fmt, 4, true>(a, r1, st) : launch_fused_m<Fmt, 8, true>(a, r1, st);
     return nw == 4 ? launch_fused_m<Fmt, 4, false>(a, r1, st) : launch_fused_m<Fmt, 8, false>(a, r1, st);
 }
