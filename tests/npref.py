@@ -202,3 +202,36 @@ def f32_dot_f64(qtype: int, wrow: np.ndarray, x: np.ndarray):
     w = dequant(qtype, wrow).astype(np.float64)
     p = w * x.astype(np.float64)
     return p.sum(), np.abs(p).sum()
+
+
+def q4k_q8k_gemm_f64(w: np.ndarray, xq: np.ndarray):
+    """Many-token Q4_K x Q8_K product in float64 with exact integer block sums.
+
+    w: [n_out, row_bytes] Q4_K rows; xq: [m, nb*292] Q8_K rows.  Returns
+    (value [m, n_out], S [m, n_out]) with S the element-level conditioning
+    scale of q8_dot_f64, computed with matrix products (every partial sum is
+    an integer below 2**53, so float64 products are exact)."""
+    n_out = w.shape[0]
+    m = xq.shape[0]
+    nb = w.shape[1] // 144
+    d, dmin, sc, mn, codes = q4_k_parts(w.reshape(-1, 144))
+    d = d.astype(np.float64).reshape(n_out, nb)
+    dmin = dmin.astype(np.float64).reshape(n_out, nb)
+    sc = sc.reshape(n_out, nb, 8)
+    mn = mn.reshape(n_out, nb, 8)
+    codes = codes.reshape(n_out, nb, 256)
+    xb = xq.reshape(m, nb, 292)
+    dx = xb[:, :, 0:4].copy().view(np.float32)[:, :, 0].astype(np.float64)
+    q8 = xb[:, :, 4:260].copy().view(np.int8).astype(np.float64)
+    sub = np.repeat(np.arange(8), 32)
+    val = np.zeros((m, n_out))
+    mag = np.zeros((m, n_out))
+    for b in range(nb):
+        ws = (sc[:, b, sub] * codes[:, b, :]).astype(np.float64)     # [n_out, 256]
+        wm = mn[:, b, sub].astype(np.float64)                          # [n_out, 256]
+        isum = q8[:, b, :] @ ws.T                                      # [m, n_out]
+        imin = q8[:, b, :] @ wm.T
+        aq = np.abs(q8[:, b, :])
+        val += dx[:, b:b + 1] * (d[None, :, b] * isum - dmin[None, :, b] * imin)
+        mag += np.abs(dx[:, b:b + 1]) * (np.abs(d[None, :, b]) * (aq @ ws.T) + np.abs(dmin[None, :, b]) * (aq @ wm.T))
+    return val, mag

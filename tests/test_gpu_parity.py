@@ -176,6 +176,61 @@ def test_integer_sums_exact_end_to_end(hipdev, qt):
     assert np.array_equal(got.astype(np.float64), want)
 
 
+# ------------------------------------------------------------------ prefill GEMM (m >= 64)
+
+
+def _q8k_rows(ora, x):
+    return np.stack([ora.quantize_q8_k(x[t]) for t in range(x.shape[0])])
+
+
+@pytest.mark.parametrize("n_in,n_out,m", [(4096, 300, 64), (2560, 515, 100), (256, 70, 129), (14336, 130, 64),
+                                          (4096, 257, 200), (1024, 128, 128)])
+def test_prefill_gemm_vs_oracle(hipdev, ora, n_in, n_out, m):
+    """m >= 64 Q4_K products run on the int8 matrix cores; every output within
+    the fp32 bound of the reference (oracle) on its conditioning scale."""
+    rng = np.random.default_rng(900 + n_in + n_out + m)
+    w = synth.np_weights(12, n_out, n_in, rng)
+    x = synth.np_activations(m, n_in, rng)
+    bias = rng.normal(0, 0.5, n_out).astype(np.float32)
+    want = ora.linear_quant_batch(x, w, 12, bias, m, n_out, n_in)
+    got = E.linear_quant_batch(dev(w), 12, dev(x), n_out, n_in, bias=dev(bias)).cpu().numpy()
+    exact, S = npref.q4k_q8k_gemm_f64(w, _q8k_rows(ora, x))
+    # the float64 restatement agrees with the oracle to its own fp32 bound
+    assert_tol(want - bias[None, :], exact.astype(np.float32), S, "oracle vs float64")
+    assert_tol(got, want, S + np.abs(bias)[None, :], f"gemm {n_out}x{n_in} m={m}")
+
+
+@pytest.mark.parametrize("n_in,n_out", [(4096, 4096), (4096, 14336), (14336, 4096)])
+def test_prefill_gemm_full_shape(hipdev, ora, n_in, n_out):
+    """The three prefill shapes at m = 512 against the float64 restatement
+    (exact integers, float64 combine); a row sample also against the oracle."""
+    m = 512
+    rng = np.random.default_rng(77 + n_in + n_out)
+    w = synth.np_weights(12, n_out, n_in, rng)
+    x = synth.np_activations(m, n_in, rng)
+    got = E.linear_quant_batch(dev(w), 12, dev(x), n_out, n_in).cpu().numpy()
+    xq = _q8k_rows(ora, x)
+    rows = np.sort(rng.choice(n_out, 256, replace=False))
+    exact, S = npref.q4k_q8k_gemm_f64(w[rows], xq)
+    assert_tol(got[:, rows], exact.astype(np.float32), S, f"gemm {n_out}x{n_in} m=512 (sampled rows)")
+    tok = rng.choice(m, 4, replace=False)
+    want = ora.linear_quant_batch(x[tok], w[rows], 12, None, 4, rows.size, n_in)
+    assert_tol(got[tok][:, rows], want, S[tok], "vs oracle")
+
+
+def test_prefill_equals_decode_rows(hipdev, ora):
+    """Prefill (matrix cores) and decode (GEMV) agree per token to the bound."""
+    rng = np.random.default_rng(4242)
+    n_in, n_out, m = 4096, 512, 96
+    w = synth.np_weights(12, n_out, n_in, rng)
+    x = synth.np_activations(m, n_in, rng)
+    big = E.linear_quant_batch(dev(w), 12, dev(x), n_out, n_in).cpu().numpy()
+    _, S = npref.q4k_q8k_gemm_f64(w, _q8k_rows(ora, x))
+    for t in (0, 37, 95):
+        one = E.linear_quant_batch(dev(w), 12, dev(x[t:t + 1]), n_out, n_in).cpu().numpy()[0]
+        assert_tol(big[t], one, 2 * S[t], f"token {t}")
+
+
 # ------------------------------------------------------------------ logits
 
 
