@@ -60,6 +60,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU-baseline sample")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--seed", type=int, default=20261203)
+    p.add_argument("--no-extra", action="store_true", help="skip the prefill-GEMM and bulk-dequant legs")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="first copy a 256 MiB buffer 4 times (device to device) for counter calibration")
     return p.parse_args()
@@ -262,6 +263,11 @@ def main():
     if tinfo is not None:
         roofline["traffic_source"] = tinfo.get("source")
 
+    extra = {}
+    if not args.no_extra:
+        extra["prefill"] = prefill_leg(L, E, synth, gen, dev, capture, timed)
+        extra["dequant"] = dequant_leg(L, E, synth, gen, dev)
+
     # ---------------------------------------------------------------- CPU baseline
     cpu = None
     if not args.no_cpu:
@@ -290,7 +296,79 @@ def main():
         "cpu_baseline": cpu,
         "kernels": per_kernel,
     }
+    line.update(extra)
     print(json.dumps(line), flush=True)
+
+
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+
+
+def prefill_leg(L, E, synth, gen, dev, capture, timed):
+    """Prefill GEMM at m = 512 tokens on the 8B Q4_K shapes (activations
+    already quantized to Q8_K, weights distinct per launch): TOPS = 2*M*N*K
+    per second.  The int8 matrix-core work is 2.5x the useful product (high
+    and low scale halves plus the min term), so the MFMA pipes run at
+    2.5 x TOPS / peak of their capacity."""
+    import torch
+
+    M = 512
+    out = {}
+    for n_out, n_in in ((4096, 4096), (14336, 4096), (4096, 14336)):
+        ws = [synth.torch_weights_bulk(12, n_out, n_in, gen, dev) for _ in range(2)]
+        x = torch.randn((M, n_in), generator=gen, device=dev)
+        xq = torch.empty((M, n_in // 256 * 292), dtype=torch.uint8, device=dev)
+        L.check(L.q8k_dev(x.data_ptr(), M, n_in, xq.data_ptr(), torch.cuda.current_stream().cuda_stream), "q8k")
+        y = torch.empty((M, n_out), device=dev)
+
+        def launches(sp, ws=ws, xq=xq, y=y, n_out=n_out, n_in=n_in):
+            for _ in range(2):
+                for w in ws:
+                    if not L.gemv_q8_dev(y.data_ptr(), xq.data_ptr(), w.data_ptr(), 12, None, M, n_out, n_in, sp):
+                        L.check(0, "prefill gemm")
+
+        g = capture(launches)
+        g.replay()
+        us = timed(g.replay, 3) * 1e3 / 4
+        tops = 2.0 * M * n_out * n_in / (us * 1e-6) / 1e12
+        out[f"{n_out}x{n_in}"] = {"us": round(us, 2), "TOPS": round(tops, 1),
+                                  "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                                  "mfma_pipe_frac": round(2.5 * tops / INT8_PEAK_TOPS, 4)}
+        del ws, x, xq, y
+    return {"m": M, "weights": "q4_k", "peak_TOPS": INT8_PEAK_TOPS, "shapes": out}
+
+
+def dequant_leg(L, E, synth, gen, dev):
+    """Bulk dequantization of 1 GiB of blocks per format to f32 (the block
+    contents are a 16 MiB seeded tile repeated); GB/s = (src + dst bytes) / s."""
+    import torch
+
+    out = {}
+    tile_bytes = 16 << 20
+    for qt, name in ((8, "q8_0"), (12, "q4_k"), (14, "q6_k")):
+        bb = E.row_bytes(qt, 32 if qt == 8 else 256)
+        be = 32 if qt == 8 else 256
+        nblk = (1 << 30) // bb
+        tile_rows = tile_bytes // (bb * 64)
+        tile = synth.torch_weights_bulk(qt, tile_rows, 64 * be, gen, dev).reshape(-1)
+        src = tile.repeat((nblk * bb + tile.numel() - 1) // tile.numel())[: nblk * bb].contiguous()
+        n = nblk * be
+        dst = torch.empty(n, dtype=torch.float32, device=dev)
+        sp = torch.cuda.current_stream().cuda_stream
+        L.check(L.dequant_dev(src.data_ptr(), qt, n, dst.data_ptr(), sp), "dequant")
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(3):
+            L.dequant_dev(src.data_ptr(), qt, n, dst.data_ptr(), sp)
+        b.record()
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / 3
+        byts = nblk * bb + n * 4
+        out[name] = {"blocks": nblk, "src_bytes": nblk * bb, "dst_bytes": n * 4, "ms": round(ms, 3),
+                     "GBps": round(byts / (ms * 1e-3) / 1e9, 1)}
+        del tile, src, dst
+        torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(args, cfg, layers, xin, projs, m):
