@@ -5,8 +5,8 @@
 //  * The activation quantizer runs inside the kernel: every workgroup turns
 //    the f32 input into Q8_K (K-quant weights) or Q8_0 (Q8_0 weights) codes in
 //    LDS with exactly the arithmetic of quantize.hip (bit-identical to
-//    src/gguf_dot_q8.c:276-324,360-412), while the loads of its weight tile
-//    are already in flight.  No separate quantize launch.
+//    src/gguf_dot_q8.c:276-324,360-412), while the loads of its first weight
+//    tile are already in flight.  No separate quantize launch.
 //  * Lanes own fixed units of K (a unit is 64 elements of a super-block, or
 //    one Q8_0 block), so each lane reads its activation slice from LDS once
 //    and applies it to the R rows of its slot.  Long rows are split across
@@ -189,16 +189,17 @@ struct FusedLds {
 // weight matrix to be requested by one generation of workgroups, without
 // spilling (checked with -Rpass-analysis=kernel-resource-usage).
 template <class Fmt>
-constexpr int fused_occupancy(int r, int m) {
-    return r * m <= 1   ? (sizeof(typename Fmt::W) > 48 ? 6 : 8)
+constexpr int fused_occupancy(int r, int m, bool pipe) {
+    return pipe ? (r <= 1 ? (sizeof(typename Fmt::W) > 48 ? 4 : 5) : r <= 2 ? (sizeof(typename Fmt::W) > 48 ? 3 : 4) : 2)
+           : r * m <= 1 ? (sizeof(typename Fmt::W) > 48 ? 6 : 8)
            : r * m <= 2 ? (sizeof(typename Fmt::W) > 48 ? (m > 1 ? 4 : 5) : 6)
                         : 4;
 }
 
 // STAGE: quantize a.x into LDS inside the kernel; otherwise read the codes
 // of a.xq (quantized by an earlier launch) straight from global memory.
-template <class Fmt, int M, int R, int NW, bool STAGE>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(fused_occupancy<Fmt>(R, M)))) void
+template <class Fmt, int M, int R, int NW, bool STAGE, bool PIPE>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(fused_occupancy<Fmt>(R, M, PIPE)))) void
 gemv_fused_kernel(FusedArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     // wave-uniform values go through readfirstlane so that the tile, matrix
@@ -245,24 +246,32 @@ gemv_fused_kernel(FusedArgs a) {
     // Loads of one tile: weights (unconditional: clamped tile, row and unit,
     // so every path issues the same loads) and the bias of this lane's output.
     const int wg_tiles = (a.ntiles + RG - 1) / RG;
-    typename Fmt::W w[R];
-    auto load_tile = [&](int wt_, int &z_, int &row0_, float &bias_) {
+    // The bias word is loaded unconditionally (from the weights when there is
+    // no bias) and selected when used: a conditional write to the register
+    // of a load still in flight would make the compiler wait for every
+    // outstanding load first, which serialises the prefetch.
+    auto load_tile = [&](int wt_, int &z_, int &row0_, float &bias_, typename Fmt::W (&w_)[R]) {
         locate(a, min(wt_ * RG + rg, a.ntiles - 1), rows_per_tile, z_, row0_);
         const WSrc src{a.w[z_], a.row_bytes};
 #pragma unroll
-        for (int r = 0; r < R; ++r) Fmt::load_w(src, min(row0_ + slot + S * r, a.n_out[z_] - 1), u, w[r]);
-        bias_ = 0.0f;
+        for (int r = 0; r < R; ++r) Fmt::load_w(src, min(row0_ + slot + S * r, a.n_out[z_] - 1), u, w_[r]);
         const float *bp = a.bias[z_];
-        if (bp != nullptr && o_live) bias_ = bp[min(row0_ + o_slot + S * o_r, a.n_out[z_] - 1)];
+        const float *bsrc = bp != nullptr ? bp + min(row0_ + o_slot + S * o_r, a.n_out[z_] - 1)
+                                          : reinterpret_cast<const float *>(a.w[z_]);
+        bias_ = *bsrc;
     };
+    auto bias_of = [&](int z_, float raw) { return a.bias[z_] != nullptr ? raw : 0.0f; };
 
     // 1. the first tile's loads go out before the activation is staged
     int wt = blockIdx.x;
     int z, row0;
     float bias;
-    load_tile(wt, z, row0, bias);
+    typename Fmt::W wa[R];
+    load_tile(wt, z, row0, bias, wa);
 
-    // 2. quantize the activation into LDS once per workgroup
+    // 2. quantize the activation into LDS once per workgroup (the staging is
+    //    shared by the NW waves; quantizing per lane in registers instead
+    //    repeats it in every wave and measured slower)
     if (STAGE) {
         if (kQ8K) stage_q8_k<NW * 64>(a, lq, ld, lbs);
         else stage_q8_0<NW * 64>(a, lq, ld);
@@ -276,14 +285,8 @@ gemv_fused_kernel(FusedArgs a) {
         else Fmt::load_act(a, u, 0, x1);
     }
 
-    // 3. grid-stride loop over workgroup tiles (a uniform trip count, so the
-    //    barriers of the KS > 1 reduction line up).  The next tile's loads are
-    //    issued as soon as the current tile's weights have been consumed, so
-    //    the lane reduction and the store overlap them; the resident waves of
-    //    the CU hide the rest of the latency.
-    for (int iter = 0;; ++iter) {
-        const bool have = wt * RG + rg < a.ntiles;
-        float vals[V];
+    // dot products of one tile's weights into vals
+    auto dot = [&](const typename Fmt::W (&w_)[R], float (&vals)[V]) {
 #pragma unroll
         for (int k = 0; k < V; ++k) vals[k] = 0.0f;
         if (unit < a.U) {
@@ -294,15 +297,12 @@ gemv_fused_kernel(FusedArgs a) {
                 else if (STAGE) Fmt::load_act_lds(act, u, t, x);
                 else Fmt::load_act(a, u, t, x);
 #pragma unroll
-                for (int r = 0; r < R; ++r) Fmt::dot1(w[r], u, x, vals[r * M + t]);
+                for (int r = 0; r < R; ++r) Fmt::dot1(w_[r], u, x, vals[r * M + t]);
             }
         }
-        const int cz = z, crow0 = row0;
-        const float cbias = bias;
-        wt += gridDim.x;
-        const bool more = wt < wg_tiles;  // uniform over the workgroup
-        if (more) load_tile(wt, z, row0, bias);
-
+    };
+    // lane reduction, K-split sum and store of one tile
+    auto finish = [&](float (&vals)[V], int iter, bool have, int cz, int crow0, float cbias) {
         group_reduce<V>(vals, G, lane);
         float result = vals[0];
         if (KS > 1) {
@@ -320,7 +320,53 @@ gemv_fused_kernel(FusedArgs a) {
             const int row = crow0 + o_slot + S * o_r;
             if (row < a.n_out[cz]) a.out[cz][(size_t)o_t * a.n_out[cz] + row] = cbias + result;
         }
-        if (!more) break;
+    };
+
+    // 3. grid-stride loop over workgroup tiles (a uniform trip count, so the
+    //    barriers of the KS > 1 reduction line up).
+    if (PIPE) {
+        // Two register buffers in turn: the next tile's loads are issued
+        // before the current tile is computed, so each wave keeps a tile in
+        // flight while it works and the dot products overlap the stream.
+        typename Fmt::W wb[R];
+        for (int iter = 0;; iter += 2) {
+            int zb, rowb;
+            float biasb;
+            const int wt1 = wt + (int)gridDim.x;
+            const bool more1 = wt1 < wg_tiles;  // uniform over the workgroup
+            if (more1) load_tile(wt1, zb, rowb, biasb, wb);
+            float vals[V];
+            const float ba = bias_of(z, bias);  // older than the prefetch just issued
+            dot(wa, vals);
+            finish(vals, iter, wt * RG + rg < a.ntiles, z, row0, ba);
+            if (!more1) break;
+            const int wt2 = wt1 + (int)gridDim.x;
+            const bool more2 = wt2 < wg_tiles;
+            if (more2) load_tile(wt2, z, row0, bias, wa);
+            const float bb = bias_of(zb, biasb);
+            dot(wb, vals);
+            finish(vals, iter + 1, wt1 * RG + rg < a.ntiles, zb, rowb, bb);
+            if (!more2) break;
+            wt = wt2;
+        }
+    } else {
+        // One buffer: the next tile's loads are issued as soon as the
+        // current tile's weights have been consumed, so the lane reduction
+        // and the store overlap them.
+        for (int iter = 0;; ++iter) {
+            const bool have = wt * RG + rg < a.ntiles;
+            float vals[V];
+            dot(wa, vals);
+            const int cz = z, crow0 = row0;
+            // resolved before the next tile's loads go out, so the store
+            // below depends on no outstanding load
+            const float cbias = bias_of(z, bias);
+            wt += gridDim.x;
+            const bool more = wt < wg_tiles;  // uniform over the workgroup
+            if (more) load_tile(wt, z, row0, bias, wa);
+            finish(vals, iter, have, cz, crow0, cbias);
+            if (!more) break;
+        }
     }
 }
 
@@ -332,7 +378,7 @@ static int env_int(const char *name, int dflt) {
     return e != nullptr ? atoi(e) : dflt;
 }
 
-template <class Fmt, int M, int R, int NW, bool STAGE>
+template <class Fmt, int M, int R, int NW, bool STAGE, bool PIPE>
 static hipError_t launch_fused_fmt(FusedArgs a, hipStream_t st) {
     const int S = 64 / a.G, RG = NW / a.KS;
     const int rows_per_tile = S * R;
@@ -359,7 +405,7 @@ static hipError_t launch_fused_fmt(FusedArgs a, hipStream_t st) {
     static int per_cu = 1;
     if (L.total() != cached_lds) {
         int v = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_fused_kernel<Fmt, M, R, NW, STAGE>, NW * 64,
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_fused_kernel<Fmt, M, R, NW, STAGE, PIPE>, NW * 64,
                                                          L.total()) != hipSuccess ||
             v < 1)
             v = 1;
@@ -370,21 +416,26 @@ static hipError_t launch_fused_fmt(FusedArgs a, hipStream_t st) {
     const int resident = per_cu * cus * (grid_scale > 0 ? grid_scale : 1);
     const int rounds = (wg_tiles + resident - 1) / resident;
     const int grid = (wg_tiles + rounds - 1) / rounds;
-    hipLaunchKernelGGL((gemv_fused_kernel<Fmt, M, R, NW, STAGE>), dim3(grid), dim3(NW * 64), L.total(), st, a);
+    hipLaunchKernelGGL((gemv_fused_kernel<Fmt, M, R, NW, STAGE, PIPE>), dim3(grid), dim3(NW * 64), L.total(), st, a);
     return hipGetLastError();
 }
 
 
 template <class Fmt, int NW, bool STAGE>
-static hipError_t launch_fused_m(FusedArgs a, int r1, hipStream_t st) {
+static hipError_t launch_fused_m(FusedArgs a, int r1, bool pipe, hipStream_t st) {
     switch (a.m) {
         case 1:
-            if (r1 == 1) return launch_fused_fmt<Fmt, 1, 1, NW, STAGE>(a, st);
-            if (r1 == 4) return launch_fused_fmt<Fmt, 1, 4, NW, STAGE>(a, st);
-            return launch_fused_fmt<Fmt, 1, 2, NW, STAGE>(a, st);
-        case 2: return launch_fused_fmt<Fmt, 2, 1, NW, STAGE>(a, st);
-        case 3: return launch_fused_fmt<Fmt, 3, 1, NW, STAGE>(a, st);
-        case 4: return launch_fused_fmt<Fmt, 4, 1, NW, STAGE>(a, st);
+            if (pipe) {
+                if (r1 == 1) return launch_fused_fmt<Fmt, 1, 1, NW, STAGE, true>(a, st);
+                if (r1 == 4) return launch_fused_fmt<Fmt, 1, 4, NW, STAGE, true>(a, st);
+                return launch_fused_fmt<Fmt, 1, 2, NW, STAGE, true>(a, st);
+            }
+            if (r1 == 1) return launch_fused_fmt<Fmt, 1, 1, NW, STAGE, false>(a, st);
+            if (r1 == 4) return launch_fused_fmt<Fmt, 1, 4, NW, STAGE, false>(a, st);
+            return launch_fused_fmt<Fmt, 1, 2, NW, STAGE, false>(a, st);
+        case 2: return launch_fused_fmt<Fmt, 2, 1, NW, STAGE, false>(a, st);
+        case 3: return launch_fused_fmt<Fmt, 3, 1, NW, STAGE, false>(a, st);
+        case 4: return launch_fused_fmt<Fmt, 4, 1, NW, STAGE, false>(a, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -397,12 +448,14 @@ template <class Fmt>
 static hipError_t launch_fused_nw(FusedArgs a, bool stage, hipStream_t st) {
     static const int r_env = env_int("EXQ_FUSED_R", 0);
     static const int nw = env_int("EXQ_FUSED_NW", 8);
+    static const bool pipe = env_int("EXQ_FUSED_PIPE", 0) != 0;
     if (a.KS > 4) return hipErrorInvalidValue;
     int rows = 0;
     for (int z = 0; z < a.nmat; ++z) rows += a.n_out[z];
     const int r1 = r_env > 0 ? r_env : (a.KS == 1 && rows <= 4096 ? 2 : 4);
-    if (stage) return nw == 4 ? launch_fused_m<Fmt, 4, true>(a, r1, st) : launch_fused_m<Fmt, 8, true>(a, r1, st);
-    return nw == 4 ? launch_fused_m<Fmt, 4, false>(a, r1, st) : launch_fused_m<Fmt, 8, false>(a, r1, st);
+    if (stage)
+        return nw == 4 ? launch_fused_m<Fmt, 4, true>(a, r1, pipe, st) : launch_fused_m<Fmt, 8, true>(a, r1, pipe, st);
+    return nw == 4 ? launch_fused_m<Fmt, 4, false>(a, r1, pipe, st) : launch_fused_m<Fmt, 8, false>(a, r1, pipe, st);
 }
 
 // Lanes per slot G and waves per row KS for U units so that every unit is
