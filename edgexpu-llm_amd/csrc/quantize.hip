@@ -63,32 +63,29 @@ __global__ __launch_bounds__(256) void quantize_q8_k_kernel(
     const int b = (int)(blk % nb);
     const float4 v = *reinterpret_cast<const float4 *>(x + (size_t)tok * ldx + (size_t)b * kQKK + lane * 4);
     const float xs[4] = {v.x, v.y, v.z, v.w};
-    // First-index signed maximum of |x| (strict '>' within the lane's run,
-    // lowest index across lanes on equal magnitudes; NaN never wins).
-    float amax = 0.0f, maxv = 0.0f;
-    int idx = 0x7fffffff;
+    // First-index signed maximum of |x|: one 64-bit max over keys
+    // (|x| bits << 32) | (~index << 1) | sign -- equal magnitudes -> lowest
+    // index wins; zeros and NaN never enter (the reference's strict '>' from
+    // amax = 0).
+    unsigned long long key = 0ull;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        const float a = fabsf(xs[e]);
-        if (a > amax) {
-            amax = a;
-            maxv = xs[e];
-            idx = lane * 4 + e;
-        }
+        const float av = fabsf(xs[e]);
+        const uint32_t idx = (uint32_t)(lane * 4 + e);
+        unsigned long long k = ((unsigned long long)__float_as_uint(av) << 32) | (((~idx) & 0x7fffffffu) << 1) |
+                               (xs[e] < 0.0f ? 1u : 0u);
+        k = av > 0.0f ? k : 0ull;
+        key = k > key ? k : key;
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
-        const float oa = __shfl_xor(amax, off, 64);
-        const float ov = __shfl_xor(maxv, off, 64);
-        const int oi = __shfl_xor(idx, off, 64);
-        if (oa > amax || (oa == amax && oi < idx)) {
-            amax = oa;
-            maxv = ov;
-            idx = oi;
-        }
+        const unsigned long long o = __shfl_xor(key, off, 64);
+        key = o > key ? o : key;
     }
+    const float amax = __uint_as_float((uint32_t)(key >> 32));
+    const float maxv = (key & 1ull) ? -amax : amax;
     uint8_t *blkp = packed + ((size_t)tok * nb + b) * kBytesQ8_K;  // 4-byte aligned
-    if (amax == 0.0f) {
+    if (key == 0ull) {
         reinterpret_cast<uint32_t *>(blkp + 4)[lane] = 0u;
         if (lane < 8) reinterpret_cast<uint32_t *>(blkp + 260)[lane] = 0u;
         if (lane == 0) *reinterpret_cast<uint32_t *>(blkp) = 0u;

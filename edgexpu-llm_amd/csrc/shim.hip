@@ -36,7 +36,6 @@ hipError_t launch_gemv_fused(int type, int nmat, const uint8_t *const *w, const 
 
 namespace {
 
-constexpr size_t kLogitChunkBytes = (size_t)48u * 1024u * 1024u;  // include/edgexpu/scheduler.h:34
 constexpr int kGemvMaxTokens = 8;
 constexpr int kFusedMaxTokens = 4;
 constexpr int kGemmMinTokens = 64;
@@ -442,10 +441,12 @@ int edgexpu_hip_logits_dev(float *scores, uint32_t *best_dev, const float *hidde
         set_error(-2, "logits: hidden must be 16-byte aligned");
         return 0;
     }
+    if (chunk_rows < 0) {
+        set_error(-2, "logits: chunk_rows must be >= 0 (got %d)", chunk_rows);
+        return 0;
+    }
     hipStream_t st = pick_stream(stream);
     const size_t rb = edgexpu_hip_row_bytes(type, n_embd);
-    size_t chunk = chunk_rows > 0 ? (size_t)chunk_rows : kLogitChunkBytes / rb;
-    if (chunk < 1) chunk = 1;
     ActWs a;
     if (!act_ws(type, m, n_embd, a)) return 0;
     if (type == kTypeQ8_0) {
@@ -455,17 +456,15 @@ int edgexpu_hip_logits_dev(float *scores, uint32_t *best_dev, const float *hidde
         // K-quant output weights use the f32-activation dots (src/native.c:445-462)
         if (!hip_ok(launch_xsum16(hidden, m, n_embd, a.xs, st), "xsum16")) return 0;
     }
-    for (size_t r0 = 0; r0 < (size_t)vocab; r0 += chunk) {
-        const int rows = (int)((size_t)vocab - r0 < chunk ? (size_t)vocab - r0 : chunk);
-        const uint8_t *wc = (const uint8_t *)w + r0 * rb;
-        const float *bc = bias != nullptr ? bias + r0 : nullptr;
-        const hipError_t e =
-            type == kTypeQ8_0
-                ? launch_gemv_q8((int)type, wc, rb, rows, n_embd, m, a.xq, act_bytes(type, n_embd), bc, scores + r0,
-                                 vocab, st)
-                : launch_gemv_f32((int)type, wc, rb, rows, n_embd, m, hidden, a.xs, bc, scores + r0, vocab, st);
-        if (!hip_ok(e, "logits gemv")) return 0;
-    }
+    // The reference walks the rows in chunks of chunk_rows (its host-memory
+    // budget, src/native.c:2262-2274); every row's score is independent of
+    // the chunking, so one launch covers all chunks in row order.
+    const hipError_t e = type == kTypeQ8_0
+                             ? launch_gemv_q8((int)type, (const uint8_t *)w, rb, vocab, n_embd, m, a.xq,
+                                              act_bytes(type, n_embd), bias, scores, vocab, st)
+                             : launch_gemv_f32((int)type, (const uint8_t *)w, rb, vocab, n_embd, m, hidden, a.xs, bias,
+                                               scores, vocab, st);
+    if (!hip_ok(e, "logits gemv")) return 0;
     if (best_dev != nullptr &&
         !hip_ok(launch_argmax_rows(scores, m, vocab, (size_t)vocab, a.keys, best_dev, st), "argmax"))
         return 0;

@@ -112,9 +112,10 @@ int edgexpu_hip_gemv_q8_dev(float *out, const uint8_t *xq, const void *w, uint32
 /* Logits product of src/native.c:2292-2401 for m hidden vectors:
  * scores[t*vocab + i] = dot(W[i], h[t]) (+ bias[i]) with the Q8_0-activation
  * dot for Q8_0 weights and the f32-activation dots for Q4_K / Q6_K
- * (src/native.c:445-514, src/gguf_quant.c:704-794).  Rows are processed in
- * launches of chunk_rows rows (0 = the reference's 48 MiB budget,
- * include/edgexpu/scheduler.h:34); results do not depend on the chunking.
+ * (src/native.c:445-514, src/gguf_quant.c:704-794).  chunk_rows (>= 0) is the
+ * reference's row chunking (0 = its 48 MiB budget,
+ * include/edgexpu/scheduler.h:34); no score depends on it, and the GPU covers
+ * every chunk in one launch.
  * When best_dev is non-NULL, best_dev[t] receives the greedy argmax of row t
  * (lowest index on ties, NaN never wins, 0 when nothing beats -inf). */
 int edgexpu_hip_logits_dev(float *scores, uint32_t *best_dev, const float *hidden, const void *w, uint32_t type,
