@@ -67,6 +67,7 @@ def parse():
 
 
 COPY_BYTES = 256 << 20
+MIN_ROTATION_BYTES = 600e6  # weights in rotation per timed step sequence (MI355X MALL: 256 MB)
 
 
 def traffic_from_profile(workload):
@@ -125,11 +126,18 @@ def main():
 
     # ---------------------------------------------------------------- data in HBM
     projs = projections(cfg)
-    layers = []
-    for _ in range(cfg["layers"]):
-        layers.append({name: synth.torch_weights_bulk(t, n_out, n_in, gen, dev)
-                       for name, t, n_out, n_in, _ in projs})
-    wout = synth.torch_weights_bulk(cfg["logits_type"], cfg["vocab"], cfg["hidden"], gen, dev)
+    one_copy = sum(cfg["layers"] * n_out * E.row_bytes(t, n_in) for _, t, n_out, n_in, _ in projs) \
+        + cfg["vocab"] * E.row_bytes(cfg["logits_type"], cfg["hidden"])
+    # a model smaller than the 256 MB MALL is replicated so that consecutive
+    # steps read distinct weights (>= 600 MB in rotation): HBM, not cache
+    copies = max(1, -(-int(MIN_ROTATION_BYTES) // one_copy))
+    model = []
+    for _ in range(copies):
+        layers = [{name: synth.torch_weights_bulk(t, n_out, n_in, gen, dev) for name, t, n_out, n_in, _ in projs}
+                  for _ in range(cfg["layers"])]
+        wout = synth.torch_weights_bulk(cfg["logits_type"], cfg["vocab"], cfg["hidden"], gen, dev)
+        model.append((layers, wout))
+    layers, wout = model[0]
     xin = {"h": torch.randn((m, cfg["hidden"]), generator=gen, device=dev),
            "q": torch.randn((m, cfg["qdim"]), generator=gen, device=dev),
            "f": torch.randn((m, cfg["ffn"]), generator=gen, device=dev)}
@@ -159,22 +167,31 @@ def main():
     groups = [(["q", "k", "v"], "h"), (["o"], "q"), (["gate", "up"], "h"), (["down"], "f")]
     pinfo = {name: (t, n_out, n_in) for name, t, n_out, n_in, _ in projs}
     arr = C.c_void_p * 4
-    launch_args = []
-    for lw in layers:
-        for names, src in groups:
-            t, _, n_in = pinfo[names[0]]
-            assert all(pinfo[nm][0] == t and pinfo[nm][2] == n_in for nm in names)
-            launch_args.append((len(names), arr(*[yout[nm].data_ptr() for nm in names]), xin[src].data_ptr(),
-                                arr(*[lw[nm].data_ptr() for nm in names]), t,
-                                (C.c_int * 4)(*[pinfo[nm][1] for nm in names]), n_in))
+    copy_args = []
+    for c_layers, c_wout in model:
+        launch_args = []
+        for lw in c_layers:
+            for names, src in groups:
+                t, _, n_in = pinfo[names[0]]
+                assert all(pinfo[nm][0] == t and pinfo[nm][2] == n_in for nm in names)
+                launch_args.append((len(names), arr(*[yout[nm].data_ptr() for nm in names]), xin[src].data_ptr(),
+                                    arr(*[lw[nm].data_ptr() for nm in names]), t,
+                                    (C.c_int * 4)(*[pinfo[nm][1] for nm in names]), n_in))
+        copy_args.append((launch_args, c_wout))
 
-    def step(sp):
+    def one_step(sp, c):
+        launch_args, c_wout = copy_args[c]
         for nmat, outs, x, ws, t, nouts, n_in in launch_args:
             if not L.linear_group_dev(nmat, outs, x, ws, t, None, nouts, m, n_in, sp):
                 L.check(0, "linear group")
-        if not L.logits_dev(scores.data_ptr(), best.data_ptr(), xin["h"].data_ptr(), wout.data_ptr(),
+        if not L.logits_dev(scores.data_ptr(), best.data_ptr(), xin["h"].data_ptr(), c_wout.data_ptr(),
                             cfg["logits_type"], None, m, cfg["vocab"], cfg["hidden"], cfg["logits_chunk"], sp):
             L.check(0, "logits")
+
+    def step(sp):
+        """`copies` consecutive decode steps, one per weight copy."""
+        for c in range(copies):
+            one_step(sp, c)
 
     def capture(fn):
         """HIP graph of fn(stream); the library's device entry points allocate
@@ -210,7 +227,8 @@ def main():
     graph = capture(step)
     for _ in range(args.warmup):
         graph.replay()
-    ms_per_step = timed(graph.replay, args.steps)
+    ms_per_step = timed(graph.replay, args.steps) / copies
+    eager_ms /= copies
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
     # ------------------------------------------------ per-kernel timing (GEMV only)
@@ -291,7 +309,8 @@ def main():
                    "ffn": cfg["ffn"], "vocab": cfg["vocab"], "weights": E.TYPE_NAMES[cfg["wtype"]],
                    "down": E.TYPE_NAMES[cfg["down_type"]], "logits": E.TYPE_NAMES[cfg["logits_type"]],
                    "logits_chunk_rows": cfg["logits_chunk"], "step_bytes": step_bytes,
-                   "weight_bytes": weight_bytes, "hbm_frac_step": round(value / HBM_PEAK_GBS, 4)},
+                   "weight_bytes": weight_bytes, "weight_copies_rotated": copies,
+                   "hbm_frac_step": round(value / HBM_PEAK_GBS, 4)},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": per_kernel,
