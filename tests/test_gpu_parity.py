@@ -271,6 +271,26 @@ def test_logits_and_argmax(hipdev, ora, qt, n, vocab, chunk):
         assert b == want_best
 
 
+@pytest.mark.parametrize("qt,n,vocab", [(12, 4096, 3001), (14, 2560, 2050), (8, 576, 4000)])
+@pytest.mark.parametrize("m", [2, 3, 4, 8])
+def test_logits_multi_token(hipdev, ora, qt, n, vocab, m):
+    """m hidden vectors in one call: each row equals the one-token call (the
+    f32-activation formats unpack a row once for all tokens in the same
+    operation order, so bit-identical), within the bound of the oracle, and
+    the argmax is per row."""
+    rng = np.random.default_rng(7 * qt + vocab + m)
+    w = synth.np_weights(qt, vocab, n, rng)
+    h = rng.normal(0, 1, (m, n)).astype(np.float32)
+    scores, best = E.logits(dev(w), qt, dev(h), vocab, n)
+    got = scores.cpu().numpy()
+    for t in range(m):
+        one, _ = E.logits(dev(w), qt, dev(h[t:t + 1]), vocab, n)
+        assert np.array_equal(bits(got[t]), bits(one.cpu().numpy()[0])), f"token {t}"
+        want, _ = ora.logits(h[t], w, qt, None, vocab, n, 0)
+        assert np.abs(got[t] - want).max() <= TOL * np.abs(want).max() * 20
+    assert np.array_equal(best.cpu().numpy(), np.argmax(got, axis=1))
+
+
 def test_argmax_rules(hipdev):
     # A Q8_0 matrix whose rows are all zero except rows 10 and 4000: equal best
     # scores, so the lowest index must win (src/native.c:2380).
@@ -310,6 +330,11 @@ def test_bad_arguments_are_rejected(hipdev):
     assert L.linear_dev(out.data_ptr(), x.data_ptr(), w.data_ptr(), 2, None, 1, 4, 96, None) == 0  # Q4_0
     code, msg = L.last_error()
     assert "not supported" in msg
+    L.clear_error()
+    sc = torch.zeros((1, 4), device=DEV)
+    assert L.logits_dev(sc.data_ptr(), None, x.data_ptr(), w.data_ptr(), 12, None, 1, 4, 256, -1, None) == 0
+    code, msg = L.last_error()
+    assert code != 0 and "chunk_rows" in msg
     L.clear_error()
     assert L.last_error()[0] == 0
 
