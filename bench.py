@@ -320,18 +320,22 @@ def main():
 
 
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 
 
 def prefill_leg(L, E, synth, gen, dev, capture, timed):
     """Prefill GEMM at m = 512 tokens on the 8B Q4_K shapes (activations
     already quantized to Q8_K, weights distinct per launch): TOPS = 2*M*N*K
-    per second.  The int8 matrix-core work is 2.5x the useful product (high
-    and low scale halves plus the min term), so the MFMA pipes run at
-    2.5 x TOPS / peak of their capacity."""
+    per second, for both prefill modes.  Exact int8: the matrix-core work is
+    2.5x the useful product (high and low scale halves plus the min term), so
+    the MFMA pipes run at 2.5 x TOPS / peak of their capacity.  fp16: one
+    product per MAC; its launch includes the fp16 conversion of the
+    activation."""
     import torch
 
     M = 512
     out = {}
+    out_f16 = {}
     for n_out, n_in in ((4096, 4096), (14336, 4096), (4096, 14336)):
         ws = [synth.torch_weights_bulk(12, n_out, n_in, gen, dev) for _ in range(2)]
         x = torch.randn((M, n_in), generator=gen, device=dev)
@@ -345,15 +349,25 @@ def prefill_leg(L, E, synth, gen, dev, capture, timed):
                     if not L.gemv_q8_dev(y.data_ptr(), xq.data_ptr(), w.data_ptr(), 12, None, M, n_out, n_in, sp):
                         L.check(0, "prefill gemm")
 
-        g = capture(launches)
-        g.replay()
-        us = timed(g.replay, 3) * 1e3 / 4
-        tops = 2.0 * M * n_out * n_in / (us * 1e-6) / 1e12
-        out[f"{n_out}x{n_in}"] = {"us": round(us, 2), "TOPS": round(tops, 1),
-                                  "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
-                                  "mfma_pipe_frac": round(2.5 * tops / INT8_PEAK_TOPS, 4)}
+        for mode, res in ((0, out), (1, out_f16)):
+            L.check(L.set_prefill_mode(mode), "prefill mode")
+            g = capture(launches)
+            g.replay()
+            us = timed(g.replay, 3) * 1e3 / 4
+            tops = 2.0 * M * n_out * n_in / (us * 1e-6) / 1e12
+            if mode == 0:
+                res[f"{n_out}x{n_in}"] = {"us": round(us, 2), "TOPS": round(tops, 1),
+                                          "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                                          "mfma_pipe_frac": round(2.5 * tops / INT8_PEAK_TOPS, 4)}
+            else:
+                res[f"{n_out}x{n_in}"] = {"us": round(us, 2), "TOPS": round(tops, 1),
+                                          "frac_f16_peak": round(tops / F16_PEAK_TFLOPS, 4)}
+            del g
+        L.check(L.set_prefill_mode(0), "prefill mode")
         del ws, x, xq, y
-    return {"m": M, "weights": "q4_k", "peak_TOPS": INT8_PEAK_TOPS, "shapes": out}
+    return {"m": M, "weights": "q4_k",
+            "exact_int8": {"peak_TOPS": INT8_PEAK_TOPS, "tolerance": 1e-5, "shapes": out},
+            "f16": {"peak_TFLOPS": F16_PEAK_TFLOPS, "tolerance": 1e-3, "shapes": out_f16}}
 
 
 def dequant_leg(L, E, synth, gen, dev):

@@ -61,6 +61,8 @@ class HipLib:
         self._last_error = _sig(L, "edgexpu_hip_last_error", C.c_int, [C.c_char_p, C.c_size_t])
         self.clear_error = _sig(L, "edgexpu_hip_clear_error", None, [])
         self.supports_type = _sig(L, "edgexpu_hip_supports_type", C.c_int, [C.c_uint32])
+        self.set_prefill_mode = _sig(L, "edgexpu_hip_set_prefill_mode", C.c_int, [C.c_int])
+        self.prefill_mode = _sig(L, "edgexpu_hip_prefill_mode", C.c_int, [])
         self.synchronize = _sig(L, "edgexpu_hip_synchronize", C.c_int, [])
         self.stream = _sig(L, "edgexpu_hip_stream", _vp, [])
         self.row_bytes = _sig(L, "edgexpu_hip_row_bytes", C.c_size_t, [C.c_uint32, C.c_int])

@@ -50,6 +50,18 @@ void edgexpu_hip_clear_error(void);
 /* 1 when `type` runs on the GPU (edgexpu_gguf_can_dot_q8/_q8k dispatch,
  * src/gguf_dot_q8.c:414-434, restricted to Q8_0/Q4_K/Q6_K). */
 int edgexpu_hip_supports_type(uint32_t type);
+/* Prefill (m >= 64 tokens, Q4_K) arithmetic.  No reference counterpart: the
+ * reference has one CPU path.
+ *  EDGEXPU_HIP_PREFILL_EXACT_INT8 (default): int8 matrix cores with every
+ *    block integer exact, outputs within the 1e-5 bound of the reference;
+ *  EDGEXPU_HIP_PREFILL_F16: fp16 matrix cores on the Q8_K activation and the
+ *    dequantized weight (each rounded once to fp16), fp32 sums: outputs within
+ *    the 1e-3 prefill bound, several times the throughput.
+ * Decode (m < 64) is unaffected.  Returns 1, or 0 for an unknown mode. */
+#define EDGEXPU_HIP_PREFILL_EXACT_INT8 0
+#define EDGEXPU_HIP_PREFILL_F16 1
+int edgexpu_hip_set_prefill_mode(int mode);
+int edgexpu_hip_prefill_mode(void);
 /* Blocks until the library stream is idle. */
 int edgexpu_hip_synchronize(void);
 /* hipStream_t of the library stream. */

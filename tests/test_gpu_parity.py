@@ -218,6 +218,39 @@ def test_prefill_gemm_full_shape(hipdev, ora, n_in, n_out):
     assert_tol(got[tok][:, rows], want, S[tok], "vs oracle")
 
 
+F16_TOL = 1e-3  # prefill bound for the fp16 matrix-core path (each factor rounded once to fp16)
+
+
+@pytest.mark.parametrize("n_in,n_out,m", [(4096, 300, 64), (2560, 515, 100), (256, 70, 129), (14336, 130, 64),
+                                          (4096, 257, 200)])
+def test_prefill_gemm_f16_vs_oracle(hipdev, ora, n_in, n_out, m):
+    """EDGEXPU_HIP_PREFILL_F16: fp16 operands, fp32 sums; every output within
+    1e-3 of its conditioning scale, and typically ~2^-11 of it."""
+    L = hipdev
+    rng = np.random.default_rng(1900 + n_in + n_out + m)
+    w = synth.np_weights(12, n_out, n_in, rng)
+    x = synth.np_activations(m, n_in, rng)
+    bias = rng.normal(0, 0.5, n_out).astype(np.float32)
+    want = ora.linear_quant_batch(x, w, 12, bias, m, n_out, n_in)
+    assert L.set_prefill_mode(1) == 1
+    try:
+        got = E.linear_quant_batch(dev(w), 12, dev(x), n_out, n_in, bias=dev(bias)).cpu().numpy()
+    finally:
+        assert L.set_prefill_mode(0) == 1
+    _, S = npref.q4k_q8k_gemm_f64(w, _q8k_rows(ora, x))
+    err = np.abs(got.astype(np.float64) - want) / (S + np.abs(bias)[None, :])
+    assert err.max() <= F16_TOL, f"worst {err.max():.3e}"
+    assert np.median(err) < 1e-4
+
+
+def test_prefill_mode_switch(hipdev):
+    L = hipdev
+    assert L.prefill_mode() == 0
+    assert L.set_prefill_mode(7) == 0
+    L.clear_error()
+    assert L.prefill_mode() == 0
+
+
 def test_prefill_equals_decode_rows(hipdev, ora):
     """Prefill (matrix cores) and decode (GEMV) agree per token to the bound."""
     rng = np.random.default_rng(4242)
