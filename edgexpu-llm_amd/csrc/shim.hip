@@ -29,7 +29,8 @@ hipError_t launch_argmax_rows(const float *s, int m, int n, size_t lds, unsigned
 hipError_t launch_gemm_q8(int type, const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const uint8_t *xq,
                           size_t xq_stride, const float *bias, float *out, int ldo, hipStream_t st);
 hipError_t launch_gemm_f16(const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const uint8_t *xq,
-                           size_t xq_stride, _Float16 *a16, const float *bias, float *out, int ldo, hipStream_t st);
+                           size_t xq_stride, void *ws, const float *bias, float *out, int ldo, hipStream_t st);
+size_t gemm_f16_workspace(int m, int n_out, int K);
 bool gemm_q8_supported(int type, int n_out, int K, int m);
 bool gemv_fused_supported(int type, int K, int m);
 hipError_t launch_gemv_fused(int type, int nmat, const uint8_t *const *w, const int *n_out, const float *const *bias,
@@ -54,7 +55,7 @@ struct State {
     void *ws = nullptr;  // device workspace (quantized activations, sums, argmax partials)
     size_t ws_cap = 0;
     void *dbuf = nullptr;  // device staging for host-pointer calls
-    void *f16ws = nullptr;  // fp16 activations of the fp16 prefill GEMM
+    void *f16ws = nullptr;  // fp16 prefill GEMM workspace
     size_t f16ws_cap = 0;
     int prefill_mode = 0;   // EDGEXPU_HIP_PREFILL_EXACT_INT8 / _F16
     size_t dbuf_cap = 0;
@@ -157,10 +158,10 @@ void *devbuf(size_t bytes) {
     return g.dbuf;
 }
 
-// fp16 activation buffer of the fp16 prefill GEMM, grown on demand.
-_Float16 *f16ws(size_t elems) {
-    const size_t bytes = elems * sizeof(_Float16);
-    if (bytes <= g.f16ws_cap) return (_Float16 *)g.f16ws;
+// Workspace of the fp16 prefill GEMM (fp16 activations, split-K partials),
+// grown on demand.
+void *f16ws(size_t bytes) {
+    if (bytes <= g.f16ws_cap) return g.f16ws;
     if (g.f16ws != nullptr) {
         if (!hip_ok(hipDeviceSynchronize(), "f16 workspace sync")) return nullptr;
         (void)hipFree(g.f16ws);
@@ -170,7 +171,7 @@ _Float16 *f16ws(size_t elems) {
     size_t cap = align_up(bytes, (size_t)1 << 20);
     if (!hip_ok(hipMalloc(&g.f16ws, cap), "hipMalloc f16 workspace")) return nullptr;
     g.f16ws_cap = cap;
-    return (_Float16 *)g.f16ws;
+    return g.f16ws;
 }
 
 // Workspace carve-up for m tokens of K elements.
@@ -216,9 +217,9 @@ bool run_q8_product(uint32_t type, const void *w, int n_out, int n_in, int m, co
     const size_t ab = act_bytes(type, n_in);
     if (m >= kGemmMinTokens && gemm_q8_supported((int)type, n_out, n_in, m)) {
         if (g.prefill_mode == EDGEXPU_HIP_PREFILL_F16) {
-            _Float16 *a16 = f16ws((size_t)m * n_in);
-            if (a16 == nullptr) return false;
-            return hip_ok(launch_gemm_f16((const uint8_t *)w, rb, n_out, n_in, m, xq, ab, a16, bias, out, ldo, st),
+            void *ws = f16ws(gemm_f16_workspace(m, n_out, n_in));
+            if (ws == nullptr) return false;
+            return hip_ok(launch_gemm_f16((const uint8_t *)w, rb, n_out, n_in, m, xq, ab, ws, bias, out, ldo, st),
                           "gemm_f16");
         }
         return hip_ok(launch_gemm_q8((int)type, (const uint8_t *)w, rb, n_out, n_in, m, xq, ab, bias, out, ldo, st),
