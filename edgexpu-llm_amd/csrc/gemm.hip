@@ -325,18 +325,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         }
     }
 
-    // store: lane holds C[4*g + r][li] of each 16 x 16 tile
+    // store: lane holds C[4*g + r][li] of each 16 x 16 tile.  Bias is added
+    // before any store: a load still in flight at a conditional store makes
+    // every store wait for all earlier memory operations.
+#pragma unroll
+    for (int jo = 0; jo < 2; ++jo) {
+        const int o = min(o0 + 32 * wo + 16 * jo + li, a.n_out - 1);
+        const float b = a.bias != nullptr ? a.bias[o] : 0.0f;
+        asm volatile("" ::"v"(b));  // the load completes here, not at each store
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[jt][jo][r] += b;
+    }
+    const bool full = t0 + kGemmTileT <= a.m;
 #pragma unroll
     for (int jo = 0; jo < 2; ++jo) {
         const int o = o0 + 32 * wo + 16 * jo + li;
         if (o >= a.n_out) continue;
-        const float b = a.bias != nullptr ? a.bias[o] : 0.0f;
+        float *col = a.out + o;
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int t = t0 + 16 * jt + 4 * g + r;
-                if (t < a.m) a.out[(size_t)t * a.ldo + o] = b + acc[jt][jo][r];
+                if (full || t < a.m) col[(size_t)t * a.ldo] = acc[jt][jo][r];
             }
         }
     }

@@ -12,22 +12,26 @@
 // int8 path (gemm.hip), whose block integers are exact, this one trades the
 // last bits for a single accumulator and no per-super-block epilogue.
 //
-// Tiling: a workgroup of 4 waves computes 128 tokens x 128 output rows, each
-// wave 64 x 64 = 2 x 2 MFMA tiles of 32 x 32.  The K loop steps 64 elements
-// at a time: one pair of Q4_K sub-blocks, whose 64 weights per row are the low
-// and high nibbles of the same 32 bytes.  Every step the workgroup stages the
-// fp16 activation tile and dequantizes the 128 rows' sub-block pair into LDS
-// (two alternating LDS stages); the global loads of a step are issued two
-// steps ahead into two register sets, so a load has two step-times to land.
+// Tiling: a workgroup of 4 waves computes 128 tokens x 128 output rows; wave
+// w owns rows 32w .. 32w+31 for all 128 tokens (4 MFMA tiles of 32 x 32).
+// The K loop steps 64 elements at a time: one pair of Q4_K sub-blocks, whose
+// 64 weights per row are the low and high nibbles of the same 32 bytes.  The
+// weights never pass through LDS: each lane loads its row's 16 bytes of the
+// pair (and the block header) from global memory and dequantizes them
+// straight into its MFMA B operands, so every weight is read and converted
+// once per workgroup.  The fp16 activation tile, shared by the 4 waves, goes
+// from global memory straight into LDS (global_load_lds, no registers) in a
+// ring of four stages; each step issues the loads of the step three ahead.
 //
 // Split K: when the (token, row) tiles cannot fill the chip, grid.z slices
 // the K range; each slice writes its partial tile to a workspace and a second
 // kernel adds bias and the slices in a fixed order (the result does not
 // depend on scheduling).
 //
-// MFMA operand layout (both operands the same K permutation): lane l supplies
-// row/column l%32 and the 8 K indices 8*(l/32) .. 8*(l/32)+7 of a 16-wide K
-// slice; accumulator register r of lane l holds C[8*(r/4) + 4*(l/32) + r%4][l%32].
+// MFMA operand layout: lane l supplies row/column l%32 and 8 K indices of a
+// 16-wide K slice, chosen by l/32 (any permutation of K works when both
+// operands use the same one); accumulator register r of lane l holds
+// C[8*(r/4) + 4*(l/32) + r%4][l%32], C[token][row].
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -45,11 +49,10 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 constexpr int kF16TileT = 128;
 constexpr int kF16TileO = 128;
 constexpr int kF16KStep = 64;
-constexpr int kF16Pitch = kF16KStep + 8;  // halfs per LDS row (+8 spreads the banks)
-constexpr int kF16Stage = (kF16TileT + kF16TileO) * kF16Pitch * 2;  // 36864 bytes
-constexpr int kF16Lds = 2 * kF16Stage;
+constexpr int kF16Stage = kF16TileT * kF16KStep * 2;  // 16 KiB: the activation tile of one step
+constexpr int kF16Lds = 4 * kF16Stage;                 // four stages in flight
 constexpr int kF16MaxSplit = 8;
-constexpr int kF16TargetGroups = 512;  // two resident workgroups per CU (LDS-bound)
+constexpr int kF16TargetGroups = 512;  // two resident workgroups per CU
 
 // Q8_K activations (reference block bytes) -> fp16 dx*q8, [m][K].
 __global__ __launch_bounds__(256) void q8k_to_f16_kernel(const uint8_t *__restrict__ xq, size_t xq_stride, int m,
@@ -77,35 +80,40 @@ struct F16Args {
     float *out;   // [m][ldo]            (split == 1)
     float *part;  // [split][m][n_out]   (split > 1)
     int ldo, m, n_out, K;
-    int steps_per_split;  // even
+    int steps_per_split;  // a multiple of 4
 };
 
-// Registers between a step's global loads and its LDS stores: four 16-byte
-// chunks of the activation tile, and for weight row tid>>1 the 16 nibble
-// bytes of its half (tid&1) of the sub-block pair plus the block header.
-struct F16Stage {
-    v4u a0, a1, a2, a3;
+typedef __attribute__((address_space(3))) void lds_void;
+
+// This lane's weight loads of one step: its row's block header and the 16
+// nibble bytes of its half (lane/32) of the step's sub-block pair.
+struct F16W {
     v4u q, h;
 };
 
-__device__ __forceinline__ void f16_load(const F16Args &a, int step, int t0, int o0, F16Stage &st) {
-    const int tid = threadIdx.x;
-    const int k0 = kF16KStep * step;
-    // activation tile: 128 rows x 64 halfs = 1024 chunks of 8 halfs
-    // chunk c = tid + 256*i: row c/8 = tid/8 + 32*i, column 8*(tid%8)
-    const _Float16 *src = a.a + k0 + 8 * (tid & 7);
-    const int r = t0 + (tid >> 3);
-    st.a0 = *reinterpret_cast<const v4u *>(src + (size_t)min(r, a.m - 1) * a.K);
-    st.a1 = *reinterpret_cast<const v4u *>(src + (size_t)min(r + 32, a.m - 1) * a.K);
-    st.a2 = *reinterpret_cast<const v4u *>(src + (size_t)min(r + 64, a.m - 1) * a.K);
-    st.a3 = *reinterpret_cast<const v4u *>(src + (size_t)min(r + 96, a.m - 1) * a.K);
-    // weight row tid>>1: super-block step/4, pair step%4 = qs bytes
-    // 32*(step%4) .. +31, this thread's half 16*(tid&1) .. +15
-    const int sb = step >> 2, jp = step & 3;
-    const int o = min(o0 + (tid >> 1), a.n_out - 1);
-    const uint8_t *blk = a.w + (size_t)o * a.row_bytes + (size_t)sb * kBytesQ4_K;
-    st.h = *reinterpret_cast<const v4u *>(blk);
-    st.q = *reinterpret_cast<const v4u *>(blk + 16 + 32 * jp + 16 * (tid & 1));
+__device__ __forceinline__ void f16_load_w(const F16Args &a, int step, int orow, int g, F16W &w) {
+    // super-block step/4, pair step%4 = qs bytes 32*(step%4) .. +31
+    const uint8_t *blk = a.w + (size_t)orow * a.row_bytes + (size_t)(step >> 2) * kBytesQ4_K;
+    w.h = *reinterpret_cast<const v4u *>(blk);
+    w.q = *reinterpret_cast<const v4u *>(blk + 16 + 32 * (step & 3) + 16 * g);
+}
+
+// Activation tile of one step, global -> LDS without registers: wave w's
+// four 1 KiB loads fill tile rows 32w .. 32w+31 (8 rows of 128 bytes each);
+// lane L of load i writes 16-byte slot L%8 of row r = 32w + 8i + L/8.  Chunk
+// c (halfs 8c .. 8c+7) of row r sits in slot c ^ ((r/2) % 8): an MFMA read
+// of one chunk down 16 consecutive rows then covers all 64 LDS banks once
+// (rows of 128 bytes alternate between the two bank halves).
+__device__ __forceinline__ void f16_load_a(const F16Args &a, int step, int t0, int wave, int lane, uint8_t *stage) {
+    const int rl = lane >> 3, slot = lane & 7;
+    const _Float16 *src = a.a + kF16KStep * step;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = min(t0 + 32 * wave + 8 * i + rl, a.m - 1);
+        const int chunk = slot ^ ((4 * i + (rl >> 1)) & 7);  // ((32w + 8i + rl) / 2) % 8
+        __builtin_amdgcn_global_load_lds(src + (size_t)r * a.K + 8 * chunk,
+                                         (lds_void *)(stage + 1024 * (4 * wave + i)), 16, 0, 0);
+    }
 }
 
 __device__ __forceinline__ uint32_t f16_pack(float lo, float hi) {
@@ -113,24 +121,45 @@ __device__ __forceinline__ uint32_t f16_pack(float lo, float hi) {
     return (uint32_t)__builtin_bit_cast(uint16_t, l) | ((uint32_t)__builtin_bit_cast(uint16_t, h) << 16);
 }
 
-__device__ __forceinline__ void f16_store(const F16Stage &st, int step, uint8_t *stage) {
-    const int tid = threadIdx.x;
-    _Float16 *sA = reinterpret_cast<_Float16 *>(stage);
-    _Float16 *sB = sA + kF16TileT * kF16Pitch;
-    _Float16 *dstA = sA + (tid >> 3) * kF16Pitch + 8 * (tid & 7);
-    *reinterpret_cast<v4u *>(dstA) = st.a0;
-    *reinterpret_cast<v4u *>(dstA + 32 * kF16Pitch) = st.a1;
-    *reinterpret_cast<v4u *>(dstA + 64 * kF16Pitch) = st.a2;
-    *reinterpret_cast<v4u *>(dstA + 96 * kF16Pitch) = st.a3;
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+// Two weights d*q - m from nibbles q0, q1 (bytes 0 and 2 of nib) as an fp16
+// pair: the bytes 0x64 | q give the fp16 values 1024 + q, from which one
+// packed fp16 subtraction recovers q exactly; each d*q - m is then one
+// mixed-precision fma (fp16 q, f32 d and m) rounded once to fp16.
+__device__ __forceinline__ uint32_t f16_dequant2(uint32_t nib, uint32_t sel, float d, float negm) {
+    const uint32_t biased = __builtin_amdgcn_perm(0x64646464u, nib, sel);
+    const h2 q = __builtin_bit_cast(h2, biased) - h2{(_Float16)1024.0f, (_Float16)1024.0f};
+    const h2 r{(_Float16)__builtin_fmaf((float)q.x, d, negm), (_Float16)__builtin_fmaf((float)q.y, d, negm)};
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// 8 weights from the low (HI = 0) or high nibbles of two words, K order =
+// byte order
+template <int HI>
+__device__ __forceinline__ v8h f16_dequant8(uint32_t w0, uint32_t w1, float d, float negm) {
+    const uint32_t x = (w0 >> (4 * HI)) & 0x0f0f0f0fu, y = (w1 >> (4 * HI)) & 0x0f0f0f0fu;
+    // v_perm selectors: result bytes (byte 0 of nib, 0x64, byte 1, 0x64) and
+    // (byte 2, 0x64, byte 3, 0x64)
+    const v4u r{f16_dequant2(x, 0x04010400u, d, negm), f16_dequant2(x, 0x04030402u, d, negm),
+                f16_dequant2(y, 0x04010400u, d, negm), f16_dequant2(y, 0x04030402u, d, negm)};
+    return __builtin_bit_cast(v8h, r);
+}
+
+// The step's MFMA B operands for this lane's row and K half g: slice kk
+// holds the K indices 32*(kk/2) + 16*g + 8*(kk%2) .. +7 of the step, i.e.
+// the low (kk < 2, sub-block j0) or high (kk >= 2, sub-block j0+1) nibbles
+// of qs bytes 16*g + 8*(kk%2) .. +7 of the pair.
+template <int JP>
+__device__ __forceinline__ void f16_dequant(const F16W &st, v8h (&b)[4]) {
     // scales and mins of sub-blocks j0 = 2*(step%4) and j0 + 1
     // (get_scale_min_k4, src/gguf_quant.c:212-220): bytes j of the 12 packed
     // bytes (header words 1..3); for j < 4 sc = s[j]&63, m = s[j+4]&63, else
     // sc = (s[j+4]&15) | (s[j-4]>>6)<<4, m = (s[j+4]>>4) | (s[j]>>6)<<4
-    const int jp = step & 3;
-    const int sh = 16 * (jp & 1);  // byte (j0 & 3) of a word, j0 and j0+1 adjacent
+    constexpr int sh = 16 * (JP & 1);  // byte (j0 & 3) of a word, j0 and j0+1 adjacent
     const uint32_t w1 = st.h[1] >> sh, w2 = st.h[2] >> sh, w3 = st.h[3] >> sh;
     uint32_t sc0, mn0, sc1, mn1;
-    if (jp < 2) {
+    if constexpr (JP < 2) {
         sc0 = w1 & 63u;
         sc1 = (w1 >> 8) & 63u;
         mn0 = w2 & 63u;
@@ -142,102 +171,131 @@ __device__ __forceinline__ void f16_store(const F16Stage &st, int step, uint8_t 
         mn1 = ((w3 >> 12) & 15u) | (((w2 >> 14) & 3u) << 4);
     }
     const float d = f16_bits_to_f32(st.h[0] & 0xffffu), dm = f16_bits_to_f32(st.h[0] >> 16);
-    const float d0 = d * (float)sc0, m0 = dm * (float)mn0;
-    const float d1 = d * (float)sc1, m1 = dm * (float)mn1;
-    // w = d1*q - m1 in f32, rounded once to fp16: low nibbles -> sub-block j0,
-    // high nibbles -> j0 + 1, elements 16*(tid&1) + 4*i .. +3 from word i
-    const uint32_t qw[4] = {st.q[0], st.q[1], st.q[2], st.q[3]};
-    uint32_t lo[8], hi[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t l = qw[i] & 0x0f0f0f0fu, h = (qw[i] >> 4) & 0x0f0f0f0fu;
-        lo[2 * i] = f16_pack(d0 * (float)(l & 0xffu) - m0, d0 * (float)((l >> 8) & 0xffu) - m0);
-        lo[2 * i + 1] = f16_pack(d0 * (float)((l >> 16) & 0xffu) - m0, d0 * (float)(l >> 24) - m0);
-        hi[2 * i] = f16_pack(d1 * (float)(h & 0xffu) - m1, d1 * (float)((h >> 8) & 0xffu) - m1);
-        hi[2 * i + 1] = f16_pack(d1 * (float)((h >> 16) & 0xffu) - m1, d1 * (float)(h >> 24) - m1);
-    }
-    _Float16 *row = sB + (tid >> 1) * kF16Pitch + 16 * (tid & 1);
-    *reinterpret_cast<v4u *>(row) = v4u{lo[0], lo[1], lo[2], lo[3]};
-    *reinterpret_cast<v4u *>(row + 8) = v4u{lo[4], lo[5], lo[6], lo[7]};
-    *reinterpret_cast<v4u *>(row + 32) = v4u{hi[0], hi[1], hi[2], hi[3]};
-    *reinterpret_cast<v4u *>(row + 40) = v4u{hi[4], hi[5], hi[6], hi[7]};
+    const float d0 = d * (float)sc0, m0 = -(dm * (float)mn0);
+    const float d1 = d * (float)sc1, m1 = -(dm * (float)mn1);
+    b[0] = f16_dequant8<0>(st.q[0], st.q[1], d0, m0);
+    b[1] = f16_dequant8<0>(st.q[2], st.q[3], d0, m0);
+    b[2] = f16_dequant8<1>(st.q[0], st.q[1], d1, m1);
+    b[3] = f16_dequant8<1>(st.q[2], st.q[3], d1, m1);
 }
 
-__device__ __forceinline__ void f16_compute(const uint8_t *stage, int wt, int wo, int l32, int g, v16f (&acc)[2][2]) {
-    const _Float16 *sA = reinterpret_cast<const _Float16 *>(stage);
-    const _Float16 *sB = sA + kF16TileT * kF16Pitch;
+// 128 tokens x this wave's 32 rows: A operands from the LDS stage at the
+// matching K columns (swizzled slots), B from registers.
+__device__ __forceinline__ void f16_compute(const uint8_t *stage, int l32, int g, const v8h (&b)[4],
+                                            v16f (&acc)[4]) {
+    const uint8_t *row = stage + 128 * l32;
 #pragma unroll
-    for (int kk = 0; kk < kF16KStep / 16; ++kk) {
-        v8h av[2], bv[2];
+    for (int kk = 0; kk < 4; ++kk) {
+        const int chunk = 4 * (kk >> 1) + 2 * g + (kk & 1);  // columns 8*chunk .. +7
+        const int slot = chunk ^ ((l32 >> 1) & 7);           // row 32i + l32: (row / 2) % 8
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            av[i] = *reinterpret_cast<const v8h *>(sA + (64 * wt + 32 * i + l32) * kF16Pitch + 16 * kk + 8 * g);
-            bv[i] = *reinterpret_cast<const v8h *>(sB + (64 * wo + 32 * i + l32) * kF16Pitch + 16 * kk + 8 * g);
+        for (int i = 0; i < 4; ++i) {
+            const v8h av = *reinterpret_cast<const v8h *>(row + 4096 * i + 16 * slot);
+            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, b[kk], acc[i], 0, 0, 0);
         }
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int jj = 0; jj < 2; ++jj)
-                acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[jj], acc[i][jj], 0, 0, 0);
     }
 }
 
+// s_waitcnt vmcnt(N) (lgkmcnt and expcnt not waited on): gfx9 encoding,
+// vmcnt bits [3:0] and [15:14]
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// End of a step: this wave's loads of the next step have landed (the two
+// later steps' loads, kLoadsPerStep each, may stay in flight), its LDS reads
+// are done, then the workgroup barrier.  The barrier carries no memory fence:
+// a fence would wait for every load in flight, the prefetched ones included.
+constexpr int kLoadsPerStep = 6;  // 4 activation chunks + 2 weight loads
+__device__ __forceinline__ void f16_step_barrier() {
+    wait_vmcnt<2 * kLoadsPerStep>();
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Step s + J of the K loop (s a multiple of 4 from the slice start, which is
+// itself a multiple of 4, so the step's sub-block pair is J): dequantize its
+// weights from w[J], issue the loads of step s + J + 3 into w[(J+3)%4] and
+// LDS stage (J+3)%4, run its MFMAs on stage J, then the step barrier.
+template <int J>
+__device__ __forceinline__ void f16_step(const F16Args &a, int s, int last, int t0, int orow, int wave, int lane,
+                                         uint8_t *smem, F16W (&w)[4], v16f (&acc)[4]) {
+    const int l32 = lane & 31, g = lane >> 5;
+    v8h b[4];
+    f16_dequant<J>(w[J], b);
+    const int ahead = min(s + J + 3, last);
+    f16_load_w(a, ahead, orow, g, w[(J + 3) & 3]);
+    f16_load_a(a, ahead, t0, wave, lane, smem + ((J + 3) & 3) * kF16Stage);
+    __builtin_amdgcn_sched_barrier(0);  // issue the loads before the step's MFMAs
+    f16_compute(smem + J * kF16Stage, l32, g, b, acc);
+    f16_step_barrier();
+}
+
+// Workgroup of 4 waves: 128 tokens x 128 output rows, wave w owns rows
+// 32*w .. 32*w+31 (one per lane%32) for all 128 tokens (4 MFMA tiles).
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_f16_kernel(F16Args a) {
-    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ __align__(1024) uint8_t smem[kF16Lds];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wt = wave & 1, wo = wave >> 1;  // wave tile: tokens 64*wt.., rows 64*wo..
     const int t0 = blockIdx.y * kF16TileT, o0 = blockIdx.x * kF16TileO;
     const int l32 = lane & 31, g = lane >> 5;
+    const int orow = min(o0 + 32 * wave + l32, a.n_out - 1);
     const int total = a.K / kF16KStep;
     const int s0 = blockIdx.z * a.steps_per_split;
-    const int n = min(a.steps_per_split, total - s0);  // even, >= 2 (host sizing)
+    const int n = min(a.steps_per_split, total - s0);  // a multiple of 4 (host sizing)
     const int last = s0 + n - 1;
 
-    v16f acc[2][2];
+    v16f acc[4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i) acc[i] = v16f{};
+
+    // step s's weights in w[s%4], activations in LDS stage s%4; step s + 3
+    // is loaded while step s is computed (loads past the slice reload its
+    // last step, into a stage no later step reads)
+    F16W w[4];
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) acc[i][jj] = v16f{};
+    for (int j = 0; j < 3; ++j) {
+        f16_load_w(a, min(s0 + j, last), orow, g, w[j]);
+        f16_load_a(a, min(s0 + j, last), t0, wave, lane, smem + j * kF16Stage);
+    }
+    f16_step_barrier();
 
-    // ra holds the step after the one computed, rb the one after that; loads
-    // past the slice reload its last step (unconditional loads keep the
-    // staging registers in registers)
-    F16Stage ra, rb;
-    f16_load(a, s0, t0, o0, ra);
-    f16_store(ra, s0, smem);
-    f16_load(a, s0 + 1, t0, o0, ra);
-    f16_load(a, min(s0 + 2, last), t0, o0, rb);
-    __syncthreads();
-
-    for (int s = 0; s < n; s += 2) {
-        // step s from stage 0; step s + 1 (ra) into stage 1, last read before
-        // the previous barrier
-        f16_compute(smem, wt, wo, l32, g, acc);
-        f16_store(ra, s0 + s + 1, smem + kF16Stage);
-        f16_load(a, min(s0 + s + 3, last), t0, o0, ra);
-        __syncthreads();
-        // step s + 1 from stage 1; step s + 2 (rb) into stage 0
-        f16_compute(smem + kF16Stage, wt, wo, l32, g, acc);
-        if (s + 2 < n) f16_store(rb, s0 + s + 2, smem);
-        f16_load(a, min(s0 + s + 4, last), t0, o0, rb);
-        __syncthreads();
+    for (int s = s0; s <= last; s += 4) {
+        f16_step<0>(a, s, last, t0, orow, wave, lane, smem, w, acc);
+        f16_step<1>(a, s, last, t0, orow, wave, lane, smem, w, acc);
+        f16_step<2>(a, s, last, t0, orow, wave, lane, smem, w, acc);
+        f16_step<3>(a, s, last, t0, orow, wave, lane, smem, w, acc);
     }
 
     const bool split = gridDim.z > 1;
     float *dst = split ? a.part + (size_t)blockIdx.z * a.m * a.n_out : a.out;
     const int ld = split ? a.n_out : a.ldo;
+    // bias added before any store: a load still in flight at a conditional
+    // store makes every store wait for all earlier memory operations
+    const float bo = (!split && a.bias != nullptr) ? a.bias[orow] : 0.0f;
+    asm volatile("" ::"v"(bo));  // the load completes here, not at each store
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-        const int o = o0 + 64 * wo + 32 * jj + l32;
-        if (o >= a.n_out) continue;
-        const float b = (!split && a.bias != nullptr) ? a.bias[o] : 0.0f;
+    for (int i = 0; i < 4; ++i) acc[i] += bo;
+    const int o = o0 + 32 * wave + l32;
+    if (o >= a.n_out) return;
+    float *col = dst + o;
+    if (t0 + kF16TileT <= a.m) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                col[(size_t)(t0 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3)) * ld] = acc[i][r];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int t = t0 + 64 * wt + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
-                if (t < a.m) dst[(size_t)t * ld + o] = b + acc[i][jj][r];
+                const int t = t0 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+                if (t < a.m) col[(size_t)t * ld] = acc[i][r];
             }
     }
 }
@@ -264,7 +322,7 @@ void f16_split(int m, int n_out, int K, int &split, int &per) {
     s = s < 1 ? 1 : (s > kF16MaxSplit ? kF16MaxSplit : s);
     if (s > total / 2) s = total / 2;
     per = (total + s - 1) / s;
-    per += per & 1;
+    per = (per + 3) & ~3;  // whole super-blocks
     split = (total + per - 1) / per;
 }
 
@@ -307,11 +365,7 @@ hipError_t launch_gemm_f16(const uint8_t *w, size_t row_bytes, int n_out, int K,
     a.steps_per_split = per;
     const dim3 grid((unsigned)((n_out + kF16TileO - 1) / kF16TileO), (unsigned)((m + kF16TileT - 1) / kF16TileT),
                     (unsigned)split);
-    // more than 64 KiB of LDS per workgroup must be allowed first
-    static hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_f16_kernel),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, kF16Lds);
-    if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL(gemm_f16_kernel, grid, dim3(256), kF16Lds, st, a);
+    hipLaunchKernelGGL(gemm_f16_kernel, grid, dim3(256), 0, st, a);
     if (split > 1) {
         const long long plane = (long long)m * n_out;
         hipLaunchKernelGGL(f16_split_reduce_kernel, dim3((unsigned)((plane + 255) / 256)), dim3(256), 0, st, a.part,
