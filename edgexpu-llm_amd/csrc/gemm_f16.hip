@@ -54,22 +54,50 @@ constexpr int kF16Lds = 4 * kF16Stage;                 // four stages in flight
 constexpr int kF16MaxSplit = 8;
 constexpr int kF16TargetGroups = 512;  // two resident workgroups per CU
 
-// Q8_K activations (reference block bytes) -> fp16 dx*q8, [m][K].
-__global__ __launch_bounds__(256) void q8k_to_f16_kernel(const uint8_t *__restrict__ xq, size_t xq_stride, int m,
-                                                         int K, _Float16 *__restrict__ a16) {
-    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;  // 8 elements each
-    const long long total = (long long)m * K / 8;
-    if (i >= total) return;
-    const int t = (int)(i / (K / 8));
-    const int k = (int)(i - (long long)t * (K / 8)) * 8;
-    const uint8_t *blk = xq + (size_t)t * xq_stride + (size_t)(k / kQKK) * kBytesQ8_K;
-    const float dx = *reinterpret_cast<const float *>(blk);
-    const uint2 q = ldg8(blk + 4 + (k % kQKK));
-    const uint32_t qw[2] = {q.x, q.y};
-    v8h out;
+// Range: fp16 holds magnitudes up to 65504, the Q8_K activations and the
+// dequantized weights are f32.  Every token row t gets an exact power-of-two
+// prescale 2^-e_t, chosen so that the row's largest possible magnitude is at
+// most 2^15 (e_t = 0 for any row already below it).  Every weight row gets a
+// running exponent e_o, raised at a super-block whose header bound needs it,
+// with the row's partial sums rescaled by the same exact power of two (the
+// accumulators of one lane all belong to its one weight row).  The epilogue
+// multiplies the fp32 sums back by 2^(e_t + e_o).
+
+// Exponent e >= 0 with bound * 2^-e <= 2^15.
+__device__ __forceinline__ int f16_prescale_exp(float bound) {
+    int e;
+    (void)frexpf(bound, &e);  // bound = f * 2^e, 0.5 <= f < 1 (bound >= 0, finite)
+    return e > 15 ? e - 15 : 0;
+}
+
+// Q8_K activations (reference block bytes) -> fp16 2^-e_t * dx*q8, [m][K];
+// one workgroup per token row.  The row bound is 128 * max |dx| (|q8| <= 128).
+__global__ __launch_bounds__(256) void q8k_to_f16_kernel(const uint8_t *__restrict__ xq, size_t xq_stride, int K,
+                                                         _Float16 *__restrict__ a16, int *__restrict__ exp_t) {
+    __shared__ float wmax[4];
+    const int t = blockIdx.x;
+    const uint8_t *row = xq + (size_t)t * xq_stride;
+    const int nb = K / kQKK;
+    float mx = 0.0f;
+    for (int b = threadIdx.x; b < nb; b += 256)
+        mx = fmaxf(mx, fabsf(*reinterpret_cast<const float *>(row + (size_t)b * kBytesQ8_K)));
 #pragma unroll
-    for (int e = 0; e < 8; ++e) out[e] = (_Float16)(dx * (float)(int8_t)((qw[e >> 2] >> (8 * (e & 3))) & 0xffu));
-    *reinterpret_cast<v8h *>(a16 + (size_t)t * K + k) = out;
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, shfl_xor_f(mx, off));
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const int e = f16_prescale_exp(128.0f * mx);
+    if (threadIdx.x == 0) exp_t[t] = e;
+    for (int k = 8 * threadIdx.x; k < K; k += 8 * 256) {
+        const uint8_t *blk = row + (size_t)(k / kQKK) * kBytesQ8_K;
+        const float dx = ldexpf(*reinterpret_cast<const float *>(blk), -e);
+        const uint2 q = ldg8(blk + 4 + (k % kQKK));
+        const uint32_t qw[2] = {q.x, q.y};
+        v8h out;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) out[j] = (_Float16)(dx * (float)(int8_t)((qw[j >> 2] >> (8 * (j & 3))) & 0xffu));
+        *reinterpret_cast<v8h *>(a16 + (size_t)t * K + k) = out;
+    }
 }
 
 struct F16Args {
@@ -79,6 +107,7 @@ struct F16Args {
     const float *bias;
     float *out;   // [m][ldo]            (split == 1)
     float *part;  // [split][m][n_out]   (split > 1)
+    const int *exp_t;  // [m rounded up to 128] prescale exponents of the token rows
     int ldo, m, n_out, K;
     int steps_per_split;  // a multiple of 4
 };
@@ -151,7 +180,7 @@ __device__ __forceinline__ v8h f16_dequant8(uint32_t w0, uint32_t w1, float d, f
 // the low (kk < 2, sub-block j0) or high (kk >= 2, sub-block j0+1) nibbles
 // of qs bytes 16*g + 8*(kk%2) .. +7 of the pair.
 template <int JP>
-__device__ __forceinline__ void f16_dequant(const F16W &st, v8h (&b)[4]) {
+__device__ __forceinline__ void f16_dequant(const F16W &st, float wscale, v8h (&b)[4]) {
     // scales and mins of sub-blocks j0 = 2*(step%4) and j0 + 1
     // (get_scale_min_k4, src/gguf_quant.c:212-220): bytes j of the 12 packed
     // bytes (header words 1..3); for j < 4 sc = s[j]&63, m = s[j+4]&63, else
@@ -170,7 +199,8 @@ __device__ __forceinline__ void f16_dequant(const F16W &st, v8h (&b)[4]) {
         mn0 = ((w3 >> 4) & 15u) | (((w2 >> 6) & 3u) << 4);
         mn1 = ((w3 >> 12) & 15u) | (((w2 >> 14) & 3u) << 4);
     }
-    const float d = f16_bits_to_f32(st.h[0] & 0xffffu), dm = f16_bits_to_f32(st.h[0] >> 16);
+    // the row prescale 2^-e_o is exact: folded into d and dmin
+    const float d = f16_bits_to_f32(st.h[0] & 0xffffu) * wscale, dm = f16_bits_to_f32(st.h[0] >> 16) * wscale;
     const float d0 = d * (float)sc0, m0 = -(dm * (float)mn0);
     const float d1 = d * (float)sc1, m1 = -(dm * (float)mn1);
     b[0] = f16_dequant8<0>(st.q[0], st.q[1], d0, m0);
@@ -222,11 +252,24 @@ __device__ __forceinline__ void f16_step_barrier() {
 // weights from w[J], issue the loads of step s + J + 3 into w[(J+3)%4] and
 // LDS stage (J+3)%4, run its MFMAs on stage J, then the step barrier.
 template <int J>
-__device__ __forceinline__ void f16_step(const F16Args &a, int s, int last, int t0, int orow, int wave, int lane,
-                                         uint8_t *smem, F16W (&w)[4], v16f (&acc)[4]) {
+__device__ __forceinline__ void f16_step(const F16Args &a, int s, int last, int t0, int orow, int &eo, float &wscale,
+                                         int wave, int lane, uint8_t *smem, F16W (&w)[4], v16f (&acc)[4]) {
     const int l32 = lane & 31, g = lane >> 5;
+    if constexpr (J == 0) {
+        // new super-block: |d*sc*q - dmin*m| <= |d|*63*15 + |dmin|*63
+        const uint32_t h = w[0].h[0];
+        const int need = f16_prescale_exp(fabsf(f16_bits_to_f32(h & 0xffffu)) * 945.0f +
+                                          fabsf(f16_bits_to_f32(h >> 16)) * 63.0f);
+        if (need > eo) {  // rare: rescale the row's sums to the new exponent
+            const float f = ldexpf(1.0f, eo - need);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] *= f;
+            eo = need;
+            wscale = ldexpf(1.0f, -need);
+        }
+    }
     v8h b[4];
-    f16_dequant<J>(w[J], b);
+    f16_dequant<J>(w[J], wscale, b);
     const int ahead = min(s + J + 3, last);
     f16_load_w(a, ahead, orow, g, w[(J + 3) & 3]);
     f16_load_a(a, ahead, t0, wave, lane, smem + ((J + 3) & 3) * kF16Stage);
@@ -248,6 +291,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     const int s0 = blockIdx.z * a.steps_per_split;
     const int n = min(a.steps_per_split, total - s0);  // a multiple of 4 (host sizing)
     const int last = s0 + n - 1;
+    int eo = 0;  // running exponent of the weight row
+    float wscale = 1.0f;
 
     v16f acc[4];
 #pragma unroll
@@ -265,21 +310,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     f16_step_barrier();
 
     for (int s = s0; s <= last; s += 4) {
-        f16_step<0>(a, s, last, t0, orow, wave, lane, smem, w, acc);
-        f16_step<1>(a, s, last, t0, orow, wave, lane, smem, w, acc);
-        f16_step<2>(a, s, last, t0, orow, wave, lane, smem, w, acc);
-        f16_step<3>(a, s, last, t0, orow, wave, lane, smem, w, acc);
+        f16_step<0>(a, s, last, t0, orow, eo, wscale, wave, lane, smem, w, acc);
+        f16_step<1>(a, s, last, t0, orow, eo, wscale, wave, lane, smem, w, acc);
+        f16_step<2>(a, s, last, t0, orow, eo, wscale, wave, lane, smem, w, acc);
+        f16_step<3>(a, s, last, t0, orow, eo, wscale, wave, lane, smem, w, acc);
     }
 
     const bool split = gridDim.z > 1;
     float *dst = split ? a.part + (size_t)blockIdx.z * a.m * a.n_out : a.out;
     const int ld = split ? a.n_out : a.ldo;
-    // bias added before any store: a load still in flight at a conditional
-    // store makes every store wait for all earlier memory operations
+    // undo the prescales (slices of a split product each undo their own, so
+    // the partials add in one scale) and add bias before any store: a load
+    // still in flight at a conditional store makes every store wait for all
+    // earlier memory operations.  Tokens of register r of tile i:
+    // t0 + 32i + 8*(r/4) + 4g + r%4, four consecutive per (i, r/4).
     const float bo = (!split && a.bias != nullptr) ? a.bias[orow] : 0.0f;
-    asm volatile("" ::"v"(bo));  // the load completes here, not at each store
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] += bo;
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            // exp_t is padded to whole tiles; padded entries only reach rows
+            // t >= m, which are never stored
+            const int4 et = *reinterpret_cast<const int4 *>(a.exp_t + t0 + 32 * i + 8 * q + 4 * g);
+            const int e4[4] = {et.x, et.y, et.z, et.w};
+#pragma unroll
+            for (int p = 0; p < 4; ++p) acc[i][4 * q + p] = ldexpf(acc[i][4 * q + p], e4[p] + eo) + bo;
+        }
     const int o = o0 + 32 * wave + l32;
     if (o >= a.n_out) return;
     float *col = dst + o;
@@ -326,17 +382,31 @@ void f16_split(int m, int n_out, int K, int &split, int &per) {
     split = (total + per - 1) / per;
 }
 
+// Workspace of the fp16 prefill GEMM, 256-byte aligned pieces: fp16
+// activations [m][K], token exponents [m rounded up to 128] and, when the K
+// range is split, the partial tiles [split][m][n_out] (bytes).
+struct F16Ws {
+    size_t a16, exp_t, part, total;
+};
+
+F16Ws f16_ws_layout(int m, int n_out, int K, int split) {
+    auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    F16Ws l{};
+    l.a16 = 0;
+    l.exp_t = up((size_t)m * K * sizeof(_Float16));
+    l.part = l.exp_t + up((size_t)((m + kF16TileT - 1) / kF16TileT) * kF16TileT * sizeof(int));
+    l.total = l.part + (split > 1 ? (size_t)split * m * n_out * sizeof(float) : 0);
+    return l;
+}
+
 }  // namespace exq
 
 using namespace exq;
 
-// Workspace of the fp16 prefill GEMM: fp16 activations [m][K] and, when the
-// K range is split, the partial tiles [split][m][n_out] (bytes).
 size_t gemm_f16_workspace(int m, int n_out, int K) {
     int split, per;
     f16_split(m, n_out, K, split, per);
-    const size_t a16 = ((size_t)m * K * sizeof(_Float16) + 255) & ~(size_t)255;
-    return a16 + (split > 1 ? (size_t)split * m * n_out * sizeof(float) : 0);
+    return f16_ws_layout(m, n_out, K, split).total;
 }
 
 // ws: gemm_f16_workspace(m, n_out, K) bytes, 256-byte aligned.
@@ -346,23 +416,23 @@ hipError_t launch_gemm_f16(const uint8_t *w, size_t row_bytes, int n_out, int K,
     if (((uintptr_t)w & 15u) != 0 || (row_bytes & 15u) != 0 || ((uintptr_t)ws & 255u) != 0) return hipErrorInvalidValue;
     int split, per;
     f16_split(m, n_out, K, split, per);
-    _Float16 *a16 = (_Float16 *)ws;
-    const size_t a16_bytes = ((size_t)m * K * sizeof(_Float16) + 255) & ~(size_t)255;
-    const long long n8 = (long long)m * K / 8;
-    hipLaunchKernelGGL(q8k_to_f16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, xq, xq_stride, m, K,
-                       a16);
+    const F16Ws l = f16_ws_layout(m, n_out, K, split);
+    uint8_t *base = (uint8_t *)ws;
     F16Args a{};
     a.w = w;
     a.row_bytes = row_bytes;
-    a.a = a16;
+    a.a = (const _Float16 *)(base + l.a16);
     a.bias = bias;
     a.out = out;
-    a.part = split > 1 ? (float *)((uint8_t *)ws + a16_bytes) : nullptr;
+    a.part = split > 1 ? (float *)(base + l.part) : nullptr;
+    a.exp_t = (const int *)(base + l.exp_t);
     a.ldo = ldo;
     a.m = m;
     a.n_out = n_out;
     a.K = K;
     a.steps_per_split = per;
+    hipLaunchKernelGGL(q8k_to_f16_kernel, dim3((unsigned)m), dim3(256), 0, st, xq, xq_stride, K,
+                       (_Float16 *)(base + l.a16), (int *)(base + l.exp_t));
     const dim3 grid((unsigned)((n_out + kF16TileO - 1) / kF16TileO), (unsigned)((m + kF16TileT - 1) / kF16TileT),
                     (unsigned)split);
     hipLaunchKernelGGL(gemm_f16_kernel, grid, dim3(256), 0, st, a);

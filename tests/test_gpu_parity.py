@@ -243,6 +243,42 @@ def test_prefill_gemm_f16_vs_oracle(hipdev, ora, n_in, n_out, m):
     assert np.median(err) < 1e-4
 
 
+@pytest.mark.parametrize("split", [None, "1"])
+@pytest.mark.parametrize("n_in,n_out,m", [(4096, 300, 200), (2560, 130, 64)])
+def test_prefill_gemm_f16_range(hipdev, ora, monkeypatch, split, n_in, n_out, m):
+    """Activations and dequantized weights far beyond fp16's 65504 (token rows
+    of |x| ~ 1e7, weight rows with d = 300, dmin = 200 throughout or from the
+    middle of the row on): the exact per-row power-of-two prescales keep the
+    fp16 path within its bound, with the K range split over workgroups
+    (default here) and unsplit."""
+    L = hipdev
+    if split is not None:
+        monkeypatch.setenv("EXQ_F16_SPLIT", split)
+    rng = np.random.default_rng(2300 + n_in + m)
+    w = synth.np_weights(12, n_out, n_in, rng).copy()
+    rb = w.shape[1]
+    big = np.frombuffer(np.array([300.0, 200.0], dtype=np.float16).tobytes(), dtype=np.uint8)
+    nb = n_in // 256
+    for o, first in ((5, 0), (n_out - 1, nb // 2)):  # the second from mid-row on
+        for sb in range(first, nb):
+            w[o, sb * 144:sb * 144 + 4] = big
+    x = synth.np_activations(m, n_in, rng)
+    x[3] *= 5e6
+    x[m - 1] *= 2e6
+    bias = rng.normal(0, 0.5, n_out).astype(np.float32)
+    want = ora.linear_quant_batch(x, w, 12, bias, m, n_out, n_in)
+    assert np.isfinite(want).all()
+    assert L.set_prefill_mode(1) == 1
+    try:
+        got = E.linear_quant_batch(dev(w), 12, dev(x), n_out, n_in, bias=dev(bias)).cpu().numpy()
+    finally:
+        assert L.set_prefill_mode(0) == 1
+    assert np.isfinite(got).all()
+    _, S = npref.q4k_q8k_gemm_f64(w, _q8k_rows(ora, x))
+    err = np.abs(got.astype(np.float64) - want) / (S + np.abs(bias)[None, :])
+    assert err.max() <= F16_TOL, f"worst {err.max():.3e} at {np.unravel_index(err.argmax(), err.shape)}"
+
+
 def test_prefill_mode_switch(hipdev):
     L = hipdev
     assert L.prefill_mode() == 0
