@@ -61,6 +61,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--seed", type=int, default=20261203)
     p.add_argument("--no-extra", action="store_true", help="skip the prefill-GEMM and bulk-dequant legs")
+    p.add_argument("--prefill-only", action="store_true", help="run only the prefill-GEMM leg (one JSON line)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="first copy a 256 MiB buffer 4 times (device to device) for counter calibration")
     return p.parse_args()
@@ -102,6 +103,39 @@ def cpu_info():
     return model
 
 
+def capture(fn):
+    """HIP graph of fn(stream); the library's device entry points allocate
+    nothing once a warm-up call has sized the workspace."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn(side.cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return graph
+
+
+def timed(run, n):
+    """ms per run over n runs, HIP events on the stream the work is issued to."""
+    import torch
+
+    stream = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(n):
+        run()
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / n
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -123,6 +157,11 @@ def main():
     m = args.batch
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
+    if args.prefill_only:
+        # the prefill GEMM leg alone (for counter runs): one JSON line
+        res = prefill_leg(L, E, synth, gen, dev, capture, timed)
+        print(json.dumps({"metric": "prefill quant-GEMM TOPS, 1 GPU", "n_gpus": 1, "prefill": res}), flush=True)
+        return
 
     # ---------------------------------------------------------------- data in HBM
     projs = projections(cfg)
@@ -192,33 +231,6 @@ def main():
         """`copies` consecutive decode steps, one per weight copy."""
         for c in range(copies):
             one_step(sp, c)
-
-    def capture(fn):
-        """HIP graph of fn(stream); the library's device entry points allocate
-        nothing once a warm-up call has sized the workspace."""
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            fn(side.cuda_stream)
-        torch.cuda.current_stream().wait_stream(side)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            fn(torch.cuda.current_stream().cuda_stream)
-        torch.cuda.synchronize()
-        return graph
-
-    def timed(run, n):
-        """ms per run over n runs, HIP events on the stream the work is issued to."""
-        stream = torch.cuda.current_stream()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        a.record(stream)
-        for _ in range(n):
-            run()
-        b.record(stream)
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / n
 
     cur = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
     for _ in range(args.warmup):

@@ -356,17 +356,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     }
 }
 
-// out[t][o] = bias[o] + part[0][t][o] + part[1][t][o] + ... (fixed order)
+// out[t][o] = bias[o] + part[0][t][o] + part[1][t][o] + ... (fixed order);
+// VEC: four consecutive outputs of a row per thread (n_out and ldo multiples
+// of 4, out 16-byte aligned)
+template <bool VEC>
 __global__ __launch_bounds__(256) void f16_split_reduce_kernel(const float *__restrict__ part, int split, int m,
                                                                int n_out, const float *__restrict__ bias,
                                                                float *__restrict__ out, int ldo) {
-    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    constexpr int W = VEC ? 4 : 1;
+    const long long i = ((long long)blockIdx.x * blockDim.x + threadIdx.x) * W;
     const long long plane = (long long)m * n_out;
     if (i >= plane) return;
     const int t = (int)(i / n_out), o = (int)(i - (long long)t * n_out);
-    float v = bias != nullptr ? bias[o] : 0.0f;
-    for (int z = 0; z < split; ++z) v += part[(size_t)z * plane + i];
-    out[(size_t)t * ldo + o] = v;
+    if constexpr (VEC) {
+        float4 v = bias != nullptr ? *reinterpret_cast<const float4 *>(bias + o) : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int z = 0; z < split; ++z) {
+            const float4 p4 = *reinterpret_cast<const float4 *>(part + (size_t)z * plane + i);
+            v.x += p4.x;
+            v.y += p4.y;
+            v.z += p4.z;
+            v.w += p4.w;
+        }
+        *reinterpret_cast<float4 *>(out + (size_t)t * ldo + o) = v;
+    } else {
+        float v = bias != nullptr ? bias[o] : 0.0f;
+        for (int z = 0; z < split; ++z) v += part[(size_t)z * plane + i];
+        out[(size_t)t * ldo + o] = v;
+    }
 }
 
 // Split count and steps per split for an m x n_out x K product.
@@ -438,8 +454,14 @@ hipError_t launch_gemm_f16(const uint8_t *w, size_t row_bytes, int n_out, int K,
     hipLaunchKernelGGL(gemm_f16_kernel, grid, dim3(256), 0, st, a);
     if (split > 1) {
         const long long plane = (long long)m * n_out;
-        hipLaunchKernelGGL(f16_split_reduce_kernel, dim3((unsigned)((plane + 255) / 256)), dim3(256), 0, st, a.part,
-                           split, m, n_out, bias, out, ldo);
+        const bool vec = n_out % 4 == 0 && ldo % 4 == 0 && ((uintptr_t)out & 15u) == 0 &&
+                         ((uintptr_t)bias & 15u) == 0;
+        if (vec)
+            hipLaunchKernelGGL(f16_split_reduce_kernel<true>, dim3((unsigned)((plane / 4 + 255) / 256)), dim3(256), 0,
+                               st, a.part, split, m, n_out, bias, out, ldo);
+        else
+            hipLaunchKernelGGL(f16_split_reduce_kernel<false>, dim3((unsigned)((plane + 255) / 256)), dim3(256), 0,
+                               st, a.part, split, m, n_out, bias, out, ldo);
     }
     return hipGetLastError();
 }
