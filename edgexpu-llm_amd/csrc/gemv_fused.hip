@@ -109,22 +109,35 @@ __device__ __forceinline__ void quantize_q8_k_group(const float (&xs)[16], int b
     if (sub == 0) ld[tok * nb + b] = d;
 }
 
+// This thread's 16 elements of the round starting at block blk0 (clamped:
+// every thread issues the same loads).
 template <int NT>
-__device__ void stage_q8_k(const FusedArgs &a, int8_t *lq, float *ld, int16_t *lbs) {
+__device__ __forceinline__ void stage_q8_k_load(const FusedArgs &a, int blk0, float (&xs)[16]) {
+    const int tid = threadIdx.x, sub = tid & 15, bl = tid >> 4;
+    const int nb = a.K / kQKK, total = a.m * nb;
+    const int cb = min(blk0 + bl, total - 1);
+    const int tok = cb / nb;
+    const float4 *p =
+        reinterpret_cast<const float4 *>(a.x + (size_t)tok * a.K + (size_t)(cb - tok * nb) * kQKK + 16 * sub);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float4 u = p[k];
+        xs[4 * k] = u.x; xs[4 * k + 1] = u.y; xs[4 * k + 2] = u.z; xs[4 * k + 3] = u.w;
+    }
+}
+
+// Q8_K quantization of x into LDS, 16 threads per 256-block; the first
+// round's elements (xs0) were loaded by the caller before the first weight
+// tile, so they do not queue behind it.
+template <int NT>
+__device__ void stage_q8_k(const FusedArgs &a, const float (&xs0)[16], int8_t *lq, float *ld, int16_t *lbs) {
     constexpr int BPR = NT / 16;  // blocks per round
     const int tid = threadIdx.x, sub = tid & 15, bl = tid >> 4;
     const int nb = a.K / kQKK, total = a.m * nb;
-    for (int blk0 = 0; blk0 < total; blk0 += BPR) {
-        const int cb = min(blk0 + bl, total - 1);  // clamped: every thread issues the same loads
-        const int tok = cb / nb;
-        const float4 *p =
-            reinterpret_cast<const float4 *>(a.x + (size_t)tok * a.K + (size_t)(cb - tok * nb) * kQKK + 16 * sub);
+    quantize_q8_k_group<NT>(xs0, bl, total, nb, a.K, sub, lq, ld, lbs);
+    for (int blk0 = BPR; blk0 < total; blk0 += BPR) {
         float xs[16];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float4 u = p[k];
-            xs[4 * k] = u.x; xs[4 * k + 1] = u.y; xs[4 * k + 2] = u.z; xs[4 * k + 3] = u.w;
-        }
+        stage_q8_k_load<NT>(a, blk0, xs);
         quantize_q8_k_group<NT>(xs, blk0 + bl, total, nb, a.K, sub, lq, ld, lbs);
     }
 }
@@ -133,15 +146,26 @@ __device__ void stage_q8_k(const FusedArgs &a, int8_t *lq, float *ld, int16_t *l
 // 8 threads per 32-element block, NT/8 blocks per round; same arithmetic as
 // quantize_q8_0_kernel.
 template <int NT>
-__device__ void stage_q8_0(const FusedArgs &a, int8_t *lq, float *ld) {
+__device__ __forceinline__ float4 stage_q8_0_load(const FusedArgs &a, int blk0) {
+    const int tid = threadIdx.x, part = tid & 7, bl = tid >> 3;
+    const int nb = a.K / kQK8_0, total = a.m * nb;
+    const int cb = min(blk0 + bl, total - 1);  // clamped: every thread issues the same loads
+    const int tok = cb / nb, b = cb - tok * nb;
+    return *reinterpret_cast<const float4 *>(a.x + (size_t)tok * a.K + (size_t)b * kQK8_0 + part * 4);
+}
+
+// v0: this thread's elements of the first round, loaded by the caller before
+// the first weight tile.
+template <int NT>
+__device__ void stage_q8_0(const FusedArgs &a, float4 v0, int8_t *lq, float *ld) {
     constexpr int BPR = NT / 8;  // blocks per round
     const int tid = threadIdx.x, part = tid & 7, bl = tid >> 3;
     const int nb = a.K / kQK8_0, total = a.m * nb;
     for (int blk0 = 0; blk0 < total; blk0 += BPR) {
         const int blk = blk0 + bl;
-        const int cb = min(blk, total - 1);  // clamped: every thread issues the same loads
+        const int cb = min(blk, total - 1);
         const int tok = cb / nb, b = cb - tok * nb;
-        const float4 v = *reinterpret_cast<const float4 *>(a.x + (size_t)tok * a.K + (size_t)b * kQK8_0 + part * 4);
+        const float4 v = blk0 == 0 ? v0 : stage_q8_0_load<NT>(a, blk0);
         float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
         amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
         amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
@@ -262,19 +286,28 @@ gemv_fused_kernel(FusedArgs a) {
     };
     auto bias_of = [&](int z_, float raw) { return a.bias[z_] != nullptr ? raw : 0.0f; };
 
-    // 1. the first tile's loads go out before the activation is staged
+    // 1. the activation's first staging round, then the first tile's
+    //    weights: issued in this order, the activation does not wait behind
+    //    the tile (loads of one wave return in order)
+    float xs0[16];
+    float4 v0;
+    if constexpr (STAGE) {
+        if constexpr (kQ8K) stage_q8_k_load<NW * 64>(a, 0, xs0);
+        else v0 = stage_q8_0_load<NW * 64>(a, 0);
+    }
     int wt = blockIdx.x;
     int z, row0;
     float bias;
     typename Fmt::W wa[R];
     load_tile(wt, z, row0, bias, wa);
 
-    // 2. quantize the activation into LDS once per workgroup (the staging is
-    //    shared by the NW waves; quantizing per lane in registers instead
-    //    repeats it in every wave and measured slower)
-    if (STAGE) {
-        if (kQ8K) stage_q8_k<NW * 64>(a, lq, ld, lbs);
-        else stage_q8_0<NW * 64>(a, lq, ld);
+    // 2. quantize the activation into LDS once per workgroup while the tile
+    //    streams in (the staging is shared by the NW waves; quantizing per
+    //    lane in registers instead repeats it in every wave and measured
+    //    slower)
+    if constexpr (STAGE) {
+        if constexpr (kQ8K) stage_q8_k<NW * 64>(a, xs0, lq, ld, lbs);
+        else stage_q8_0<NW * 64>(a, v0, lq, ld);
         __syncthreads();
     }
     const ActLds act{lq, ld, lbs, a.K, a.nblk};
