@@ -213,8 +213,8 @@ struct FusedLds {
 // weight matrix to be requested by one generation of workgroups, without
 // spilling (checked with -Rpass-analysis=kernel-resource-usage).
 template <class Fmt>
-constexpr int fused_occupancy(int r, int m, bool pipe) {
-    return pipe ? (r <= 1 ? (sizeof(typename Fmt::W) > 48 ? 4 : 5) : r <= 2 ? (sizeof(typename Fmt::W) > 48 ? 3 : 4) : 2)
+constexpr int fused_occupancy(int r, int m, int loop) {
+    return loop == 1 ? (r <= 1 ? (sizeof(typename Fmt::W) > 48 ? 4 : 5) : r <= 2 ? (sizeof(typename Fmt::W) > 48 ? 3 : 4) : 2)
            : r * m <= 1 ? (sizeof(typename Fmt::W) > 48 ? 6 : 8)
            : r * m <= 2 ? (sizeof(typename Fmt::W) > 48 ? (m > 1 ? 4 : 5) : 6)
                         : 4;
@@ -222,8 +222,8 @@ constexpr int fused_occupancy(int r, int m, bool pipe) {
 
 // STAGE: quantize a.x into LDS inside the kernel; otherwise read the codes
 // of a.xq (quantized by an earlier launch) straight from global memory.
-template <class Fmt, int M, int R, int NW, bool STAGE, bool PIPE>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(fused_occupancy<Fmt>(R, M, PIPE)))) void
+template <class Fmt, int M, int R, int NW, bool STAGE, int LOOP>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(fused_occupancy<Fmt>(R, M, LOOP)))) void
 gemv_fused_kernel(FusedArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     // wave-uniform values go through readfirstlane so that the tile, matrix
@@ -276,13 +276,14 @@ gemv_fused_kernel(FusedArgs a) {
     // outstanding load first, which serialises the prefetch.
     auto load_tile = [&](int wt_, int &z_, int &row0_, float &bias_, typename Fmt::W (&w_)[R]) {
         locate(a, min(wt_ * RG + rg, a.ntiles - 1), rows_per_tile, z_, row0_);
-        const WSrc src{a.w[z_], a.row_bytes};
-#pragma unroll
-        for (int r = 0; r < R; ++r) Fmt::load_w(src, min(row0_ + slot + S * r, a.n_out[z_] - 1), u, w_[r]);
+        // the bias first: waiting for it then waits for no weight row
         const float *bp = a.bias[z_];
         const float *bsrc = bp != nullptr ? bp + min(row0_ + o_slot + S * o_r, a.n_out[z_] - 1)
                                           : reinterpret_cast<const float *>(a.w[z_]);
         bias_ = *bsrc;
+        const WSrc src{a.w[z_], a.row_bytes};
+#pragma unroll
+        for (int r = 0; r < R; ++r) Fmt::load_w(src, min(row0_ + slot + S * r, a.n_out[z_] - 1), u, w_[r]);
     };
     auto bias_of = [&](int z_, float raw) { return a.bias[z_] != nullptr ? raw : 0.0f; };
 
@@ -300,6 +301,7 @@ gemv_fused_kernel(FusedArgs a) {
     float bias;
     typename Fmt::W wa[R];
     load_tile(wt, z, row0, bias, wa);
+    __builtin_amdgcn_sched_barrier(0);  // every load issued before the staging arithmetic
 
     // 2. quantize the activation into LDS once per workgroup while the tile
     //    streams in (the staging is shared by the NW waves; quantizing per
@@ -357,7 +359,7 @@ gemv_fused_kernel(FusedArgs a) {
 
     // 3. grid-stride loop over workgroup tiles (a uniform trip count, so the
     //    barriers of the KS > 1 reduction line up).
-    if (PIPE) {
+    if constexpr (LOOP == 1) {
         // Two register buffers in turn: the next tile's loads are issued
         // before the current tile is computed, so each wave keeps a tile in
         // flight while it works and the dot products overlap the stream.
@@ -411,7 +413,7 @@ static int env_int(const char *name, int dflt) {
     return e != nullptr ? atoi(e) : dflt;
 }
 
-template <class Fmt, int M, int R, int NW, bool STAGE, bool PIPE>
+template <class Fmt, int M, int R, int NW, bool STAGE, int LOOP>
 static hipError_t launch_fused_fmt(FusedArgs a, hipStream_t st) {
     const int S = 64 / a.G, RG = NW / a.KS;
     const int rows_per_tile = S * R;
@@ -438,7 +440,7 @@ static hipError_t launch_fused_fmt(FusedArgs a, hipStream_t st) {
     static int per_cu = 1;
     if (L.total() != cached_lds) {
         int v = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_fused_kernel<Fmt, M, R, NW, STAGE, PIPE>, NW * 64,
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_fused_kernel<Fmt, M, R, NW, STAGE, LOOP>, NW * 64,
                                                          L.total()) != hipSuccess ||
             v < 1)
             v = 1;
@@ -449,26 +451,26 @@ static hipError_t launch_fused_fmt(FusedArgs a, hipStream_t st) {
     const int resident = per_cu * cus * (grid_scale > 0 ? grid_scale : 1);
     const int rounds = (wg_tiles + resident - 1) / resident;
     const int grid = (wg_tiles + rounds - 1) / rounds;
-    hipLaunchKernelGGL((gemv_fused_kernel<Fmt, M, R, NW, STAGE, PIPE>), dim3(grid), dim3(NW * 64), L.total(), st, a);
+    hipLaunchKernelGGL((gemv_fused_kernel<Fmt, M, R, NW, STAGE, LOOP>), dim3(grid), dim3(NW * 64), L.total(), st, a);
     return hipGetLastError();
 }
 
 
 template <class Fmt, int NW, bool STAGE>
-static hipError_t launch_fused_m(FusedArgs a, int r1, bool pipe, hipStream_t st) {
+static hipError_t launch_fused_m(FusedArgs a, int r1, int loop, hipStream_t st) {
     switch (a.m) {
         case 1:
-            if (pipe) {
-                if (r1 == 1) return launch_fused_fmt<Fmt, 1, 1, NW, STAGE, true>(a, st);
-                if (r1 == 4) return launch_fused_fmt<Fmt, 1, 4, NW, STAGE, true>(a, st);
-                return launch_fused_fmt<Fmt, 1, 2, NW, STAGE, true>(a, st);
+            if (loop == 1) {
+                if (r1 == 1) return launch_fused_fmt<Fmt, 1, 1, NW, STAGE, 1>(a, st);
+                if (r1 == 4) return launch_fused_fmt<Fmt, 1, 4, NW, STAGE, 1>(a, st);
+                return launch_fused_fmt<Fmt, 1, 2, NW, STAGE, 1>(a, st);
             }
-            if (r1 == 1) return launch_fused_fmt<Fmt, 1, 1, NW, STAGE, false>(a, st);
-            if (r1 == 4) return launch_fused_fmt<Fmt, 1, 4, NW, STAGE, false>(a, st);
-            return launch_fused_fmt<Fmt, 1, 2, NW, STAGE, false>(a, st);
-        case 2: return launch_fused_fmt<Fmt, 2, 1, NW, STAGE, false>(a, st);
-        case 3: return launch_fused_fmt<Fmt, 3, 1, NW, STAGE, false>(a, st);
-        case 4: return launch_fused_fmt<Fmt, 4, 1, NW, STAGE, false>(a, st);
+            if (r1 == 1) return launch_fused_fmt<Fmt, 1, 1, NW, STAGE, 0>(a, st);
+            if (r1 == 4) return launch_fused_fmt<Fmt, 1, 4, NW, STAGE, 0>(a, st);
+            return launch_fused_fmt<Fmt, 1, 2, NW, STAGE, 0>(a, st);
+        case 2: return launch_fused_fmt<Fmt, 2, 1, NW, STAGE, 0>(a, st);
+        case 3: return launch_fused_fmt<Fmt, 3, 1, NW, STAGE, 0>(a, st);
+        case 4: return launch_fused_fmt<Fmt, 4, 1, NW, STAGE, 0>(a, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -481,14 +483,14 @@ template <class Fmt>
 static hipError_t launch_fused_nw(FusedArgs a, bool stage, hipStream_t st) {
     static const int r_env = env_int("EXQ_FUSED_R", 0);
     static const int nw = env_int("EXQ_FUSED_NW", 8);
-    static const bool pipe = env_int("EXQ_FUSED_PIPE", 0) != 0;
+    static const int loop = env_int("EXQ_FUSED_PIPE", 0) != 0 ? 1 : 0;  // 1: two register buffers
     if (a.KS > 4) return hipErrorInvalidValue;
     int rows = 0;
     for (int z = 0; z < a.nmat; ++z) rows += a.n_out[z];
     const int r1 = r_env > 0 ? r_env : (a.KS == 1 && rows <= 4096 ? 2 : 4);
     if (stage)
-        return nw == 4 ? launch_fused_m<Fmt, 4, true>(a, r1, pipe, st) : launch_fused_m<Fmt, 8, true>(a, r1, pipe, st);
-    return nw == 4 ? launch_fused_m<Fmt, 4, false>(a, r1, pipe, st) : launch_fused_m<Fmt, 8, false>(a, r1, pipe, st);
+        return nw == 4 ? launch_fused_m<Fmt, 4, true>(a, r1, loop, st) : launch_fused_m<Fmt, 8, true>(a, r1, loop, st);
+    return nw == 4 ? launch_fused_m<Fmt, 4, false>(a, r1, loop, st) : launch_fused_m<Fmt, 8, false>(a, r1, loop, st);
 }
 
 // Lanes per slot G and waves per row KS for U units so that every unit is
