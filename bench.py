@@ -62,6 +62,8 @@ def parse():
     p.add_argument("--seed", type=int, default=20261203)
     p.add_argument("--no-extra", action="store_true", help="skip the prefill-GEMM and bulk-dequant legs")
     p.add_argument("--prefill-only", action="store_true", help="run only the prefill-GEMM leg (one JSON line)")
+    p.add_argument("--launch-sweep", action="store_true",
+                   help="time one Q4_K [rows x 4096] m=1 launch over row counts; fit fixed + marginal cost")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="first copy a 256 MiB buffer 4 times (device to device) for counter calibration")
     return p.parse_args()
@@ -157,6 +159,9 @@ def main():
     m = args.batch
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
+    if args.launch_sweep:
+        print(json.dumps(launch_sweep(L, E, synth, gen, dev)), flush=True)
+        return
     if args.prefill_only:
         # the prefill GEMM leg alone (for counter runs): one JSON line
         res = prefill_leg(L, E, synth, gen, dev, capture, timed)
@@ -380,6 +385,57 @@ def prefill_leg(L, E, synth, gen, dev, capture, timed):
     return {"m": M, "weights": "q4_k",
             "exact_int8": {"peak_TOPS": INT8_PEAK_TOPS, "tolerance": 1e-5, "shapes": out},
             "f16": {"peak_TFLOPS": F16_PEAK_TFLOPS, "tolerance": 1e-3, "shapes": out_f16}}
+
+
+def launch_sweep(L, E, synth, gen, dev):
+    """Per-launch time of the decode GEMV ([rows x 4096] Q4_K, m = 1, 32
+    distinct matrices per size so nothing is re-read from cache) against the
+    row count, and a least-squares fit time = fixed + bytes / rate over the
+    sizes of at least 4096 rows.  The empty-kernel time is a one-element torch
+    add in the same kind of graph."""
+    import numpy as np
+    import torch
+
+    K, NL = 4096, 32
+    x = torch.randn((1, K), generator=gen, device=dev)
+    arr = C.c_void_p * 4
+    rows_list = (64, 1024, 4096, 8192, 14336, 28672, 57344)
+    res = {}
+    for rows in rows_list:
+        ws = [synth.torch_weights_bulk(12, rows, K, gen, dev) for _ in range(NL)]
+        y = torch.empty((1, rows), device=dev)
+        nouts = (C.c_int * 4)(rows)
+
+        def launches(sp, ws=ws, y=y, nouts=nouts):
+            for _ in range(2):
+                for w in ws:
+                    if not L.linear_group_dev(1, arr(y.data_ptr()), x.data_ptr(), arr(w.data_ptr()), 12, None, nouts,
+                                              1, K, sp):
+                        L.check(0, "linear group")
+
+        g = capture(launches)
+        g.replay()
+        us = timed(g.replay, 3) * 1e3 / (2 * NL)
+        byts = rows * E.row_bytes(12, K)
+        res[rows] = {"us": round(us, 3), "bytes": byts, "GBps": round(byts / (us * 1e-6) / 1e9, 1)}
+        del ws, y, g
+    t = torch.zeros(1, device=dev)
+
+    def tiny(sp):
+        for _ in range(256):
+            t.add_(1.0)
+
+    g = capture(tiny)
+    g.replay()
+    empty_us = timed(g.replay, 3) * 1e3 / 256
+    big = [r for r in rows_list if r >= 4096]
+    A = np.array([[1.0, res[r]["bytes"]] for r in big])
+    b = np.array([res[r]["us"] for r in big])
+    (fixed, per_byte), *_ = np.linalg.lstsq(A, b, rcond=None)
+    return {"metric": "decode GEMV per-launch time vs rows, 1 GPU", "k": K, "type": "q4_k", "m": 1,
+            "launches": {str(r): v for r, v in res.items()}, "empty_kernel_us": round(empty_us, 3),
+            "fit": {"fixed_us": round(float(fixed), 3), "marginal_GBps": round(1e-3 / float(per_byte), 1),
+                    "rows_fitted": list(big)}}
 
 
 def dequant_leg(L, E, synth, gen, dev):
