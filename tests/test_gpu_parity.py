@@ -222,7 +222,7 @@ F16_TOL = 1e-3  # prefill bound for the fp16 matrix-core path (each factor round
 
 
 @pytest.mark.parametrize("n_in,n_out,m", [(4096, 300, 64), (2560, 515, 100), (256, 70, 129), (14336, 130, 64),
-                                          (4096, 257, 200)])
+                                          (4096, 257, 200), (2048, 260, 300), (1024, 384, 512), (1024, 136, 520)])
 def test_prefill_gemm_f16_vs_oracle(hipdev, ora, n_in, n_out, m):
     """EDGEXPU_HIP_PREFILL_F16: fp16 operands, fp32 sums; every output within
     1e-3 of its conditioning scale, and typically ~2^-11 of it."""
@@ -244,7 +244,7 @@ def test_prefill_gemm_f16_vs_oracle(hipdev, ora, n_in, n_out, m):
 
 
 @pytest.mark.parametrize("split", [None, "1"])
-@pytest.mark.parametrize("n_in,n_out,m", [(4096, 300, 200), (2560, 130, 64)])
+@pytest.mark.parametrize("n_in,n_out,m", [(4096, 300, 200), (2560, 130, 64), (2048, 140, 300)])
 def test_prefill_gemm_f16_range(hipdev, ora, monkeypatch, split, n_in, n_out, m):
     """Activations and dequantized weights far beyond fp16's 65504 (token rows
     of |x| ~ 1e7, weight rows with d = 300, dmin = 200 throughout or from the
