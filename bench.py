@@ -301,7 +301,7 @@ def main():
     extra = {}
     if not args.no_extra:
         extra["prefill"] = prefill_leg(L, E, synth, gen, dev, capture, timed)
-        extra["dequant"] = dequant_leg(L, E, synth, gen, dev)
+        extra["dequant"] = dequant_leg(L, E, synth, gen, dev, args.no_cpu)
 
     # ---------------------------------------------------------------- CPU baseline
     cpu = None
@@ -438,13 +438,21 @@ def launch_sweep(L, E, synth, gen, dev):
                     "rows_fitted": list(big)}}
 
 
-def dequant_leg(L, E, synth, gen, dev):
+def dequant_leg(L, E, synth, gen, dev, no_cpu=False):
     """Bulk dequantization of 1 GiB of blocks per format to f32 (the block
-    contents are a 16 MiB seeded tile repeated); GB/s = (src + dst bytes) / s."""
+    contents are a 16 MiB seeded tile repeated); GB/s = (src + dst bytes) / s.
+    Beside it, unless no_cpu, the reference's own dequant on one host core."""
     import torch
 
     out = {}
     tile_bytes = 16 << 20
+    ref, kind = None, None
+    if not no_cpu:
+        import oracle as O
+
+        ref, kind = O.load_reference(), "reference"
+        if ref is None:
+            ref, kind = O.load_oracle(), "port"
     for qt, name in ((8, "q8_0"), (12, "q4_k"), (14, "q6_k")):
         bb = E.row_bytes(qt, 32 if qt == 8 else 256)
         be = 32 if qt == 8 else 256
@@ -467,6 +475,19 @@ def dequant_leg(L, E, synth, gen, dev):
         byts = nblk * bb + n * 4
         out[name] = {"blocks": nblk, "src_bytes": nblk * bb, "dst_bytes": n * 4, "ms": round(ms, 3),
                      "GBps": round(byts / (ms * 1e-3) / 1e9, 1)}
+        if ref is not None:
+            # the reference's dequant is single-threaded (no OpenMP): a 16 MiB
+            # sample of the same blocks on one host core
+            sample = tile.cpu().numpy()
+            ns = sample.size // bb * be
+            ref.dequantize(sample, qt, ns)
+            reps, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < 0.5 or reps < 2:
+                ref.dequantize(sample, qt, ns)
+                reps += 1
+            dt = (time.perf_counter() - t0) / reps
+            out[name]["cpu_baseline"] = {"value": round((sample.size + ns * 4) / dt / 1e9, 2), "unit": "GB/s",
+                                         "cores": 1, "kind": kind, "sample": f"{sample.size >> 20} MiB of blocks"}
         del tile, src, dst
         torch.cuda.empty_cache()
     return out

@@ -429,7 +429,9 @@ size_t gemm_f16_workspace(int m, int n_out, int K) {
 hipError_t launch_gemm_f16(const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const uint8_t *xq,
                            size_t xq_stride, void *ws, const float *bias, float *out, int ldo, hipStream_t st) {
     if (K % kQKK != 0 || m < 1 || n_out < 1) return hipErrorInvalidValue;
-    if (((uintptr_t)w & 15u) != 0 || (row_bytes & 15u) != 0 || ((uintptr_t)ws & 255u) != 0) return hipErrorInvalidValue;
+    if (((uintptr_t)w & 15u) != 0 || (row_bytes & 15u) != 0 || ((uintptr_t)ws & 255u) != 0 ||
+        ((uintptr_t)xq & 3u) != 0 || (xq_stride & 3u) != 0)
+        return hipErrorInvalidValue;
     int split, per;
     f16_split(m, n_out, K, split, per);
     const F16Ws l = f16_ws_layout(m, n_out, K, split);

@@ -466,6 +466,11 @@ int edgexpu_hip_gemv_q8_dev(float *out, const uint8_t *xq, const void *w, uint32
                             int n_out, int n_in, void *stream) {
     if (!ensure_init()) return 0;
     if (!check_linear_args(out, xq, w, type, m, n_out, n_in, "gemv_q8")) return 0;
+    // the block scale heads every Q8_K (f32) / Q8_0 (f16) block
+    if (((uintptr_t)xq & (type == kTypeQ8_0 ? 1u : 3u)) != 0) {
+        set_error(-2, "gemv_q8: xq must be %d-byte aligned", type == kTypeQ8_0 ? 2 : 4);
+        return 0;
+    }
     return run_q8_product(type, w, n_out, n_in, m, xq, bias, out, n_out, pick_stream(stream)) ? 1 : 0;
 }
 

@@ -73,6 +73,40 @@ def test_dequant_random_bit_exact(hipdev, ora, qt, nblocks):
 # ------------------------------------------------------------------ quantizers
 
 
+# 1 GiB of blocks per format as whole rows: floor(2^30 / block bytes) blocks
+FULL_GIB = {8: (87481, 11552), 12: (372827, 5120), 14: (319566, 4096)}
+
+
+@pytest.mark.parametrize("qt", [8, 12, 14])
+def test_dequant_full_gib_bit_exact(hipdev, ora, qt):
+    """The bulk-dequant workload at full size: 1 GiB of distinct seeded
+    blocks per format dequantized on the GPU, every output word compared with
+    the oracle (in chunks of ~32 MB of output)."""
+    L = hipdev
+    rows, n_in = FULL_GIB[qt]
+    be = 32 if qt == 8 else 256
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(4000 + qt)
+    src = synth.torch_weights_bulk(qt, rows, n_in, gen, DEV)
+    assert rows * n_in // be == (1 << 30) // (src.shape[1] // (n_in // be))
+    n = rows * n_in
+    dst = torch.empty(n, dtype=torch.float32, device=DEV)
+    L.check(L.dequant_dev(src.data_ptr(), qt, n, dst.data_ptr(), torch.cuda.current_stream().cuda_stream), "dequant")
+    torch.cuda.synchronize()
+    src_h = src.cpu().numpy()
+    del src
+    rows_per = max(1, (1 << 25) // (n_in * 4))
+    for r0 in range(0, rows, rows_per):
+        r1 = min(rows, r0 + rows_per)
+        want = ora.dequantize(src_h[r0:r1].reshape(-1), qt, (r1 - r0) * n_in).view(np.uint32)
+        got = dst[r0 * n_in:r1 * n_in].cpu().numpy().view(np.uint32)
+        if not np.array_equal(got, want):
+            bad = np.nonzero(got != want)[0][:5]
+            raise AssertionError(f"type {qt}: rows {r0}..{r1} differ first at elements {bad.tolist()}")
+    del dst
+    torch.cuda.empty_cache()
+
+
 def test_quantizers_golden_bit_exact(hipdev, golden):
     g = golden("quantize")
     for name, x, q80, q8k in zip(g["names"], g["x"], g["q8_0"], g["q8_k"]):
@@ -404,6 +438,11 @@ def test_bad_arguments_are_rejected(hipdev):
     assert L.logits_dev(sc.data_ptr(), None, x.data_ptr(), w.data_ptr(), 12, None, 1, 4, 256, -1, None) == 0
     code, msg = L.last_error()
     assert code != 0 and "chunk_rows" in msg
+    L.clear_error()
+    xq = torch.zeros(2 * 292 + 8, dtype=torch.uint8, device=DEV)  # Q8_K codes, misaligned by one byte
+    assert L.gemv_q8_dev(out.data_ptr(), xq.data_ptr() + 1, w.data_ptr(), 12, None, 1, 4, 256, None) == 0
+    code, msg = L.last_error()
+    assert code != 0 and "aligned" in msg
     L.clear_error()
     assert L.last_error()[0] == 0
 
