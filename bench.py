@@ -37,13 +37,13 @@ sys.path.insert(0, os.path.join(ROOT, "oracle"))
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
 
 WORKLOADS = {
-    # config 3: Llama-3-8B-shaped decode, all Q4_K, logits [128256 x 4096] in 8192-row chunks
+    # Llama-3-8B-shaped decode, all Q4_K, logits [128256 x 4096] in 8192-row chunks
     "llama3-8b-q4k-decode": dict(layers=32, hidden=4096, qdim=4096, kv=1024, ffn=14336, vocab=128256,
                                  wtype=12, down_type=12, logits_type=12, logits_chunk=8192),
-    # config 1: SmolLM2-135M-shaped decode, all Q8_0, logits [49152 x 576]
+    # SmolLM2-135M-shaped decode, all Q8_0, logits [49152 x 576]
     "smollm2-135m-q8_0-decode": dict(layers=30, hidden=576, qdim=576, kv=192, ffn=1536, vocab=49152,
                                      wtype=8, down_type=8, logits_type=8, logits_chunk=0),
-    # config 4: Q4_K_M hybrid ~4B (Qwen3-4B-like projections assumed), Q6_K down + logits
+    # Q4_K_M hybrid ~4B (Qwen3-4B-like projections assumed), Q6_K down + logits
     "hybrid-4b-q4km-decode": dict(layers=36, hidden=2560, qdim=4096, kv=1024, ffn=9728, vocab=151936,
                                   wtype=12, down_type=14, logits_type=14, logits_chunk=0),
 }

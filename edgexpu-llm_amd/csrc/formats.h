@@ -281,7 +281,8 @@ struct FmtQ4KF32 {
         float x[64];
         float sx0, sx1;   // sums of x over sub-blocks 2j and 2j+1
     };
-    __device__ static void load_act(const GemvArgs &a, int unit, int tk, Act &x) {
+    template <class A>  // GemvArgs or FusedArgs: a.xf, a.xs, a.K
+    __device__ static void load_act(const A &a, int unit, int tk, Act &x) {
         const int i = unit >> 2, j = unit & 3;
         const float4 *p = reinterpret_cast<const float4 *>(a.xf + (size_t)tk * a.K + 256 * i + 64 * j);
 #pragma unroll
@@ -316,8 +317,12 @@ struct FmtQ4KF32 {
             float qlo = 0.0f, qhi = 0.0f;
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                const uint32_t lo = qw[k] & 0x0f0f0f0fu;
-                const uint32_t hi = (qw[k] >> 4) & 0x0f0f0f0fu;
+                uint32_t lo = qw[k] & 0x0f0f0f0fu;
+                uint32_t hi = (qw[k] >> 4) & 0x0f0f0f0fu;
+                // opaque to the compiler: it would otherwise fold each byte
+                // extraction back into a 4-bit field extract of qw, where one
+                // v_cvt_f32_ubyte{0..3} per byte of the masked word suffices
+                asm volatile("" : "+v"(lo), "+v"(hi));
                 qlo = fmaf((float)(lo & 0xffu), xa.x[4 * k + 0], qlo);
                 qlo = fmaf((float)((lo >> 8) & 0xffu), xa.x[4 * k + 1], qlo);
                 qlo = fmaf((float)((lo >> 16) & 0xffu), xa.x[4 * k + 2], qlo);
@@ -342,7 +347,8 @@ struct FmtQ6KF32 {
         float x[64];      // [k][16]
         float sx[4];      // sums of x per sub-block 8h+2k+p
     };
-    __device__ static void load_act(const GemvArgs &a, int unit, int tk, Act &x) {
+    template <class A>  // GemvArgs or FusedArgs: a.xf, a.xs, a.K
+    __device__ static void load_act(const A &a, int unit, int tk, Act &x) {
         const int i = unit >> 2, h = (unit >> 1) & 1, p = unit & 1;
         const float *base = a.xf + (size_t)tk * a.K + 256 * i + 128 * h + 16 * p;
 #pragma unroll
@@ -409,7 +415,8 @@ struct FmtQ80F32 {
     struct Act {
         float x[32];
     };
-    __device__ static void load_act(const GemvArgs &a, int unit, int tk, Act &x) {
+    template <class A>  // GemvArgs or FusedArgs: a.xf, a.xs, a.K
+    __device__ static void load_act(const A &a, int unit, int tk, Act &x) {
         const float4 *p = reinterpret_cast<const float4 *>(a.xf + (size_t)tk * a.K + 32 * unit);
 #pragma unroll
         for (int v = 0; v < 8; ++v) {

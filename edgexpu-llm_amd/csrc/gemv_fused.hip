@@ -43,6 +43,8 @@ struct FusedArgs {
     const float *x;        // [m][K] f32 activations (staged kernels)
     const uint8_t *xq;     // or: activations already quantized, reference block bytes
     size_t xq_stride;      //     (Q8_0: 34 B per 32, Q8_K: 292 B per 256), token t at xq + t*xq_stride
+    const float *xf;       // or (f32-activation formats): x [m][K] f32
+    const float *xs;       //     and its 16-element sums [m][K/16]
 };
 
 struct WSrc {
@@ -214,6 +216,9 @@ struct FusedLds {
 // spilling (checked with -Rpass-analysis=kernel-resource-usage).
 template <class Fmt>
 constexpr int fused_occupancy(int r, int m, int loop) {
+    // f32-activation formats: the activation slice (up to 66 floats) stays
+    // in registers
+    if (sizeof(typename Fmt::Act) > 128) return r <= 1 ? 4 : 3;
     return loop == 1 ? (r <= 1 ? (sizeof(typename Fmt::W) > 48 ? 4 : 5) : r <= 2 ? (sizeof(typename Fmt::W) > 48 ? 3 : 4) : 2)
            : loop == 2 ? (r <= 1 ? (sizeof(typename Fmt::W) > 48 ? 5 : 7)
                           : r <= 2 ? (sizeof(typename Fmt::W) > 48 ? 4 : 5)
@@ -319,7 +324,7 @@ gemv_fused_kernel(FusedArgs a) {
     // one token: the activation slice stays in registers for every tile
     typename Fmt::Act x1;
     if (M == 1) {
-        if (STAGE) Fmt::load_act_lds(act, u, 0, x1);
+        if constexpr (STAGE) Fmt::load_act_lds(act, u, 0, x1);
         else Fmt::load_act(a, u, 0, x1);
     }
 
@@ -331,8 +336,8 @@ gemv_fused_kernel(FusedArgs a) {
 #pragma unroll
             for (int t = 0; t < M; ++t) {
                 typename Fmt::Act x;
-                if (M == 1) x = x1;
-                else if (STAGE) Fmt::load_act_lds(act, u, t, x);
+                if constexpr (M == 1) x = x1;
+                else if constexpr (STAGE) Fmt::load_act_lds(act, u, t, x);
                 else Fmt::load_act(a, u, t, x);
 #pragma unroll
                 for (int r = 0; r < R; ++r) Fmt::dot1(w_[r], u, x, vals[r * M + t]);
@@ -587,6 +592,56 @@ bool gemv_fused_supported(int type, int K, int m) {
     if (!pick_fused_shape(U, G, KS)) return false;
     const FusedLds L(m, K, type == kTypeQ8_0 ? K / kQK8_0 : K / kQKK, type != kTypeQ8_0, 8, 64 / G, 4);
     return L.total() <= 64 * 1024;
+}
+
+// True when the fused kernel covers the f32-activation product (one token):
+// K-quant logits rows of type Q4_K / Q6_K, Q8_0 when its quantization fails.
+bool gemv_fused_f32_supported(int type, int K) {
+    if (type != kTypeQ8_0 && type != kTypeQ4_K && type != kTypeQ6_K) return false;
+    const int U = type == kTypeQ8_0 ? K / kQK8_0 : (K / kQKK) * 4;
+    int G = 64, KS = 1;
+    if (!pick_fused_shape(U, G, KS)) return false;
+    const FusedLds L(1, K, 0, false, 8, 64 / G, 2, false);
+    return L.total() <= 64 * 1024;
+}
+
+// One token of f32 activations xf (with 16-element sums xs for the K-quants)
+// against one matrix: the logits product (src/native.c:445-462).  Rows per
+// slot R = 1 or 2 (the activation slice takes the registers of larger R).
+hipError_t launch_gemv_fused_f32(int type, const uint8_t *w, int n_out, const float *bias, float *out,
+                                 size_t row_bytes, int K, const float *xf, const float *xs, hipStream_t st) {
+    if (!gemv_fused_f32_supported(type, K)) return hipErrorInvalidValue;
+    FusedArgs a{};
+    a.nmat = 1;
+    a.w[0] = w;
+    a.n_out[0] = n_out;
+    a.bias[0] = bias;
+    a.out[0] = out;
+    a.row_bytes = row_bytes;
+    a.K = K;
+    a.m = 1;
+    a.xf = xf;
+    a.xs = xs;
+    a.nblk = type == kTypeQ8_0 ? K / kQK8_0 : K / kQKK;
+    a.U = type == kTypeQ8_0 ? a.nblk : a.nblk * 4;
+    if (!pick_fused_shape(a.U, a.G, a.KS)) return hipErrorInvalidValue;
+    static const int r_env = env_int("EXQ_FUSED_F32_R", 2);
+    // one row per lane group spills the Q6_K decode's registers; Q6_K keeps two
+    const int r1 = r_env == 1 && type != kTypeQ6_K ? 1 : 2;
+    const int rows_per_tile = (64 / a.G) * r1;
+    const int tiles = (n_out + rows_per_tile - 1) / rows_per_tile;
+    const bool balanced = a.KS == 1 && tiles > 2 * device_cus() * 8 && env_int("EXQ_FUSED_DYN", 1) != 0;
+#define EXQ_F32_LAUNCH(F)                                                                              \
+    return balanced ? (r1 == 1 ? launch_fused_fmt<F, 1, 1, 8, false, 2>(a, st) : launch_fused_fmt<F, 1, 2, 8, false, 2>(a, st)) \
+                    : (r1 == 1 ? launch_fused_fmt<F, 1, 1, 8, false, 0>(a, st) : launch_fused_fmt<F, 1, 2, 8, false, 0>(a, st))
+    switch (type) {
+        case kTypeQ8_0: EXQ_F32_LAUNCH(FmtQ80F32);
+        case kTypeQ4_K: EXQ_F32_LAUNCH(FmtQ4KF32);
+        default:
+            return balanced ? launch_fused_fmt<FmtQ6KF32, 1, 2, 8, false, 2>(a, st)
+                            : launch_fused_fmt<FmtQ6KF32, 1, 2, 8, false, 0>(a, st);
+    }
+#undef EXQ_F32_LAUNCH
 }
 
 // nmat matrices of the same type and K, all applied to the same m tokens:

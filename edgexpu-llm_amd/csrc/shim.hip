@@ -33,6 +33,9 @@ hipError_t launch_gemm_f16(const uint8_t *w, size_t row_bytes, int n_out, int K,
 size_t gemm_f16_workspace(int m, int n_out, int K);
 bool gemm_q8_supported(int type, int n_out, int K, int m);
 bool gemv_fused_supported(int type, int K, int m);
+bool gemv_fused_f32_supported(int type, int K);
+hipError_t launch_gemv_fused_f32(int type, const uint8_t *w, int n_out, const float *bias, float *out,
+                                 size_t row_bytes, int K, const float *xf, const float *xs, hipStream_t st);
 hipError_t launch_gemv_fused(int type, int nmat, const uint8_t *const *w, const int *n_out, const float *const *bias,
                              float *const *out, size_t row_bytes, int K, int m, const float *x, const uint8_t *xq,
                              size_t xq_stride, hipStream_t st);
@@ -504,12 +507,25 @@ int edgexpu_hip_logits_dev(float *scores, uint32_t *best_dev, const float *hidde
     // The reference walks the rows in chunks of chunk_rows (its host-memory
     // budget, src/native.c:2262-2274); every row's score is independent of
     // the chunking, so one launch covers all chunks in row order.
-    const hipError_t e = type == kTypeQ8_0
-                             ? launch_gemv_q8((int)type, (const uint8_t *)w, rb, vocab, n_embd, m, a.xq,
-                                              act_bytes(type, n_embd), bias, scores, vocab, st)
-                             : launch_gemv_f32((int)type, (const uint8_t *)w, rb, vocab, n_embd, m, hidden, a.xs, bias,
-                                               scores, vocab, st);
-    if (!hip_ok(e, "logits gemv")) return 0;
+    // K-quant rows: the fused kernel keeps one hidden vector's f32 slice in
+    // registers across all the rows a wave visits, one launch per vector (a
+    // row's score then does not depend on m, as in the reference's per-token
+    // loop); the generic kernel covers the K the fused one does not.
+    if (type != kTypeQ8_0 && gemv_fused_f32_supported((int)type, n_embd)) {
+        for (int t = 0; t < m; ++t) {
+            const hipError_t e = launch_gemv_fused_f32((int)type, (const uint8_t *)w, vocab, bias,
+                                                       scores + (size_t)t * vocab, rb, n_embd,
+                                                       hidden + (size_t)t * n_embd, a.xs + (size_t)t * (n_embd / 16), st);
+            if (!hip_ok(e, "logits gemv")) return 0;
+        }
+    } else {
+        const hipError_t e = type == kTypeQ8_0
+                                 ? launch_gemv_q8((int)type, (const uint8_t *)w, rb, vocab, n_embd, m, a.xq,
+                                                  act_bytes(type, n_embd), bias, scores, vocab, st)
+                                 : launch_gemv_f32((int)type, (const uint8_t *)w, rb, vocab, n_embd, m, hidden, a.xs,
+                                                   bias, scores, vocab, st);
+        if (!hip_ok(e, "logits gemv")) return 0;
+    }
     if (best_dev != nullptr &&
         !hip_ok(launch_argmax_rows(scores, m, vocab, (size_t)vocab, a.keys, best_dev, st), "argmax"))
         return 0;

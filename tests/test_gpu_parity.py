@@ -377,9 +377,9 @@ def test_logits_and_argmax(hipdev, ora, qt, n, vocab, chunk):
 @pytest.mark.parametrize("qt,n,vocab", [(12, 4096, 3001), (14, 2560, 2050), (8, 576, 4000)])
 @pytest.mark.parametrize("m", [2, 3, 4, 8])
 def test_logits_multi_token(hipdev, ora, qt, n, vocab, m):
-    """m hidden vectors in one call: each row equals the one-token call (the
-    f32-activation formats unpack a row once for all tokens in the same
-    operation order, so bit-identical), within the bound of the oracle, and
+    """m hidden vectors in one call: each row equals the one-token call bit
+    for bit (a score does not depend on how many vectors share the call, as
+    in the reference's per-token loop), within the bound of the oracle, and
     the argmax is per row."""
     rng = np.random.default_rng(7 * qt + vocab + m)
     w = synth.np_weights(qt, vocab, n, rng)
