@@ -190,12 +190,38 @@ __device__ void stage_q8_0(const FusedArgs &a, float4 v0, int8_t *lq, float *ld)
     }
 }
 
-__device__ __forceinline__ void locate(const FusedArgs &a, int tile, int rows_per_tile, int &z, int &row0) {
-    z = 0;
+// The matrix a row tile belongs to and the tile's first row.  The
+// kernel-argument arrays are read at constant indices only and selected
+// between, so their words are loaded once, before the tile loop, and stay in
+// scalar registers; a dynamic index would reload them (a chain of dependent
+// scalar loads) between one tile's data and the next tile's loads.
+// Word 3 of a raw buffer descriptor for untyped dword access: DATA_FORMAT 32
+// (bits 18:15 = 4; a zero format would drop every access), all else zero.
+constexpr int kRawBufferWord3 = 0x00020000;
+// A buffer offset beyond every output buffer: the store is dropped.
+constexpr int kDeadOffset = 0x7ffffff0;
+
+struct TileMat {
+    const uint8_t *w;
+    const float *bias;
+    float *out;
+    int n_out;
+    int row0;
+};
+__device__ __forceinline__ TileMat locate(const FusedArgs &a, int tile, int rows_per_tile) {
+    TileMat t{a.w[0], a.bias[0], a.out[0], a.n_out[0], 0};
+    int start = 0;
 #pragma unroll
-    for (int k = 1; k < kFusedMaxMats; ++k)
-        if (k < a.nmat && tile >= a.tile_start[k]) z = k;
-    row0 = (tile - a.tile_start[z]) * rows_per_tile;
+    for (int k = 1; k < kFusedMaxMats; ++k) {
+        const bool in = k < a.nmat && tile >= a.tile_start[k];
+        t.w = in ? a.w[k] : t.w;
+        t.bias = in ? a.bias[k] : t.bias;
+        t.out = in ? a.out[k] : t.out;
+        t.n_out = in ? a.n_out[k] : t.n_out;
+        start = in ? a.tile_start[k] : start;
+    }
+    t.row0 = (tile - start) * rows_per_tile;
+    return t;
 }
 
 // LDS carve-up shared by the kernel and its launcher.
@@ -223,9 +249,9 @@ constexpr int fused_occupancy(int r, int m, int loop) {
            : loop == 2 ? (r <= 1 ? (sizeof(typename Fmt::W) > 48 ? 5 : 7)
                           : r <= 2 ? (sizeof(typename Fmt::W) > 48 ? 4 : 5)
                                    : (sizeof(typename Fmt::W) > 48 ? 3 : 4))
-           : r * m <= 1 ? (sizeof(typename Fmt::W) > 48 ? 6 : 8)
-           : r * m <= 2 ? (sizeof(typename Fmt::W) > 48 ? (m > 1 ? 4 : 5) : 6)
-                        : 4;
+           : r * m <= 1 ? (sizeof(typename Fmt::W) > 48 ? 5 : 7)
+           : r * m <= 2 ? (sizeof(typename Fmt::W) > 48 ? (m > 1 ? 4 : 5) : (m > 1 ? 5 : 6))
+                        : (sizeof(typename Fmt::W) > 48 ? 3 : 4);
 }
 
 // STAGE: quantize a.x into LDS inside the kernel; otherwise read the codes
@@ -282,18 +308,20 @@ gemv_fused_kernel(FusedArgs a) {
     // no bias) and selected when used: a conditional write to the register
     // of a load still in flight would make the compiler wait for every
     // outstanding load first, which serialises the prefetch.
-    auto load_tile = [&](int wt_, int &z_, int &row0_, float &bias_, typename Fmt::W (&w_)[R]) {
-        locate(a, min(wt_ * RG + rg, a.ntiles - 1), rows_per_tile, z_, row0_);
+    auto issue_tile = [&](const TileMat &t_, float &bias_, typename Fmt::W (&w_)[R]) {
         // the bias first: waiting for it then waits for no weight row
-        const float *bp = a.bias[z_];
-        const float *bsrc = bp != nullptr ? bp + min(row0_ + o_slot + S * o_r, a.n_out[z_] - 1)
-                                          : reinterpret_cast<const float *>(a.w[z_]);
+        const float *bsrc = t_.bias != nullptr ? t_.bias + min(t_.row0 + o_slot + S * o_r, t_.n_out - 1)
+                                               : reinterpret_cast<const float *>(t_.w);
         bias_ = *bsrc;
-        const WSrc src{a.w[z_], a.row_bytes};
+        const WSrc src{t_.w, a.row_bytes};
 #pragma unroll
-        for (int r = 0; r < R; ++r) Fmt::load_w(src, min(row0_ + slot + S * r, a.n_out[z_] - 1), u, w_[r]);
+        for (int r = 0; r < R; ++r) Fmt::load_w(src, min(t_.row0 + slot + S * r, t_.n_out - 1), u, w_[r]);
     };
-    auto bias_of = [&](int z_, float raw) { return a.bias[z_] != nullptr ? raw : 0.0f; };
+    auto load_tile = [&](int wt_, TileMat &t_, float &bias_, typename Fmt::W (&w_)[R]) {
+        t_ = locate(a, min(wt_ * RG + rg, a.ntiles - 1), rows_per_tile);
+        issue_tile(t_, bias_, w_);
+    };
+    auto bias_of = [&](const TileMat &t_, float raw) { return t_.bias != nullptr ? raw : 0.0f; };
 
     // 1. the activation's first staging round, then the first tile's
     //    weights: issued in this order, the activation does not wait behind
@@ -305,10 +333,10 @@ gemv_fused_kernel(FusedArgs a) {
         else v0 = stage_q8_0_load<NW * 64>(a, 0);
     }
     int wt = blockIdx.x;
-    int z, row0;
+    TileMat tm;
     float bias;
     typename Fmt::W wa[R];
-    load_tile(wt, z, row0, bias, wa);
+    load_tile(wt, tm, bias, wa);
     __builtin_amdgcn_sched_barrier(0);  // every load issued before the staging arithmetic
 
     // 2. quantize the activation into LDS once per workgroup while the tile
@@ -329,23 +357,28 @@ gemv_fused_kernel(FusedArgs a) {
     }
 
     // dot products of one tile's weights into vals
+    // Every lane computes (u is clamped to a real unit) and the lanes past the
+    // row's units drop their sums by a select: with no branch around it, every
+    // path through the loop waits for the weights it consumes, so the next
+    // tile's loads need not wait for the previous tile's store.
+    const bool unit_live = unit < a.U;
     auto dot = [&](const typename Fmt::W (&w_)[R], float (&vals)[V]) {
 #pragma unroll
         for (int k = 0; k < V; ++k) vals[k] = 0.0f;
-        if (unit < a.U) {
 #pragma unroll
-            for (int t = 0; t < M; ++t) {
-                typename Fmt::Act x;
-                if constexpr (M == 1) x = x1;
-                else if constexpr (STAGE) Fmt::load_act_lds(act, u, t, x);
-                else Fmt::load_act(a, u, t, x);
+        for (int t = 0; t < M; ++t) {
+            typename Fmt::Act x;
+            if constexpr (M == 1) x = x1;
+            else if constexpr (STAGE) Fmt::load_act_lds(act, u, t, x);
+            else Fmt::load_act(a, u, t, x);
 #pragma unroll
-                for (int r = 0; r < R; ++r) Fmt::dot1(w_[r], u, x, vals[r * M + t]);
-            }
+            for (int r = 0; r < R; ++r) Fmt::dot1(w_[r], u, x, vals[r * M + t]);
         }
+#pragma unroll
+        for (int k = 0; k < V; ++k) vals[k] = unit_live ? vals[k] : 0.0f;
     };
     // lane reduction, K-split sum and store of one tile
-    auto finish = [&](float (&vals)[V], int iter, bool have, int cz, int crow0, float cbias) {
+    auto finish = [&](float (&vals)[V], int iter, bool have, const TileMat &ct, float cbias) {
         group_reduce<V>(vals, G, lane);
         float result = vals[0];
         if (KS > 1) {
@@ -359,37 +392,66 @@ gemv_fused_kernel(FusedArgs a) {
             if (o_live)
                 for (int k2 = 0; k2 < KS; ++k2) result += rb[((rg * KS + k2) * S + o_slot) * NV + o_idx];
         }
-        if (have && o_live) {
-            const int row = crow0 + o_slot + S * o_r;
-            if (row < a.n_out[cz]) a.out[cz][(size_t)o_t * a.n_out[cz] + row] = cbias + result;
-        }
+        // One store instruction per tile on every path: a lane without an
+        // output gets an offset past the end of the buffer, whose range check
+        // drops the write.  With no branch around the store, the compiler
+        // counts exactly one store after each tile's loads and waits for the
+        // weights alone, not for the previous tile's store as well.
+        const int row = ct.row0 + o_slot + S * o_r;
+        const bool live = have && o_live && row < ct.n_out;
+        const __amdgpu_buffer_rsrc_t rs =
+            __builtin_amdgcn_make_buffer_rsrc(ct.out, (short)0, a.m * ct.n_out * 4, kRawBufferWord3);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(cbias + result), rs,
+                                              live ? (o_t * ct.n_out + row) * 4 : kDeadOffset, 0, 0);
     };
 
     // 3. grid-stride loop over workgroup tiles (a uniform trip count, so the
-    //    barriers of the KS > 1 reduction line up).
+    //    barriers of the KS > 1 reduction line up).  A trip that has a next
+    //    tile always loads it and the last trip leaves before loading: a
+    //    conditional load would make the weight registers a merge of old and
+    //    new values, which the register allocator resolves with copies that
+    //    wait for the loads just issued.  The tile's bias is resolved before
+    //    its dot, which frees its register for the next tile's bias without
+    //    a copy.  A dropped store (an empty buffer) enters the loop the way
+    //    its end re-enters it, with one store behind the tile's loads, so
+    //    that no path's wait for a tile's last weights includes the store.
+    __builtin_amdgcn_raw_buffer_store_b32(0u, __builtin_amdgcn_make_buffer_rsrc(tm.out, (short)0, 0, kRawBufferWord3),
+                                          0, 0, 0);
+    auto resolve_bias = [&](const TileMat &t_, float raw) {
+        float b = bias_of(t_, raw);
+        asm volatile("" : "+v"(b));  // the select stays here, not at its use
+        __builtin_amdgcn_sched_barrier(0);
+        return b;
+    };
     if constexpr (LOOP == 1) {
         // Two register buffers in turn: the next tile's loads are issued
         // before the current tile is computed, so each wave keeps a tile in
         // flight while it works and the dot products overlap the stream.
         typename Fmt::W wb[R];
         for (int iter = 0;; iter += 2) {
-            int zb, rowb;
+            TileMat tmb;
             float biasb;
-            const int wt1 = wt + (int)gridDim.x;
-            const bool more1 = wt1 < wg_tiles;  // uniform over the workgroup
-            if (more1) load_tile(wt1, zb, rowb, biasb, wb);
             float vals[V];
-            const float ba = bias_of(z, bias);  // older than the prefetch just issued
+            const int wt1 = wt + (int)gridDim.x;
+            const float ba = resolve_bias(tm, bias);
+            if (wt1 >= wg_tiles) {  // uniform over the workgroup
+                dot(wa, vals);
+                finish(vals, iter, wt * RG + rg < a.ntiles, tm, ba);
+                break;
+            }
+            load_tile(wt1, tmb, biasb, wb);
             dot(wa, vals);
-            finish(vals, iter, wt * RG + rg < a.ntiles, z, row0, ba);
-            if (!more1) break;
+            finish(vals, iter, wt * RG + rg < a.ntiles, tm, ba);
             const int wt2 = wt1 + (int)gridDim.x;
-            const bool more2 = wt2 < wg_tiles;
-            if (more2) load_tile(wt2, z, row0, bias, wa);
-            const float bb = bias_of(zb, biasb);
+            const float bb = resolve_bias(tmb, biasb);
+            if (wt2 >= wg_tiles) {
+                dot(wb, vals);
+                finish(vals, iter + 1, wt1 * RG + rg < a.ntiles, tmb, bb);
+                break;
+            }
+            load_tile(wt2, tm, bias, wa);
             dot(wb, vals);
-            finish(vals, iter + 1, wt1 * RG + rg < a.ntiles, zb, rowb, bb);
-            if (!more2) break;
+            finish(vals, iter + 1, wt1 * RG + rg < a.ntiles, tmb, bb);
             wt = wt2;
         }
     } else if constexpr (LOOP == 2) {
@@ -403,24 +465,18 @@ gemv_fused_kernel(FusedArgs a) {
         int cur = (int)blockIdx.x * RG + rg;
         for (int iter = 0;; ++iter) {
             const bool have = cur < T;
+            const float cbias = resolve_bias(tm, bias);
             float vals[V];
             dot(wa, vals);
-            const int cz = z, crow0 = row0;
-            const float cbias = bias_of(z, bias);
+            const TileMat ct = tm;
             const int next = iter == 0 ? W + rg * nwg + (int)blockIdx.x : cur + W;
-            const bool more = next < T;  // uniform over the wave
-            if (more) {
-                // bias first, then the rows (as load_tile)
-                locate(a, next, rows_per_tile, z, row0);
-                const float *bp = a.bias[z];
-                bias = *(bp != nullptr ? bp + min(row0 + o_slot + S * o_r, a.n_out[z] - 1)
-                                       : reinterpret_cast<const float *>(a.w[z]));
-                const WSrc src{a.w[z], a.row_bytes};
-#pragma unroll
-                for (int r = 0; r < R; ++r) Fmt::load_w(src, min(row0 + slot + S * r, a.n_out[z] - 1), u, wa[r]);
+            if (next >= T) {  // uniform over the wave
+                finish(vals, iter, have, ct, cbias);
+                break;
             }
-            finish(vals, iter, have, cz, crow0, cbias);
-            if (!more) break;
+            tm = locate(a, next, rows_per_tile);
+            issue_tile(tm, bias, wa);
+            finish(vals, iter, have, ct, cbias);
             cur = next;
         }
     } else {
@@ -429,17 +485,19 @@ gemv_fused_kernel(FusedArgs a) {
         // and the store overlap them.
         for (int iter = 0;; ++iter) {
             const bool have = wt * RG + rg < a.ntiles;
-            float vals[V];
-            dot(wa, vals);
-            const int cz = z, crow0 = row0;
             // resolved before the next tile's loads go out, so the store
             // below depends on no outstanding load
-            const float cbias = bias_of(z, bias);
+            const float cbias = resolve_bias(tm, bias);
+            float vals[V];
+            dot(wa, vals);
+            const TileMat ct = tm;
             wt += gridDim.x;
-            const bool more = wt < wg_tiles;  // uniform over the workgroup
-            if (more) load_tile(wt, z, row0, bias, wa);
-            finish(vals, iter, have, cz, crow0, cbias);
-            if (!more) break;
+            if (wt >= wg_tiles) {  // uniform over the workgroup
+                finish(vals, iter, have, ct, cbias);
+                break;
+            }
+            load_tile(wt, tm, bias, wa);
+            finish(vals, iter, have, ct, cbias);
         }
     }
 }
@@ -458,14 +516,16 @@ static int device_cus() {
 
 // Tuning overrides: EXQ_FUSED_R (rows per slot at m = 1: 1, 2 or 4),
 // EXQ_FUSED_NW (waves per workgroup: 4 or 8), EXQ_FUSED_GRID (multiple of the
-// resident workgroup count).
+// resident workgroup count), EXQ_FUSED_PER_CU (workgroups per CU at most),
+// EXQ_FUSED_PIPE / EXQ_FUSED_DYN / EXQ_FUSED_BIG (tile schedule).
 static int env_int(const char *name, int dflt) {
     const char *e = getenv(name);
     return e != nullptr ? atoi(e) : dflt;
 }
 
+// per_cu_cap > 0: at most that many workgroups per CU in the grid.
 template <class Fmt, int M, int R, int NW, bool STAGE, int LOOP>
-static hipError_t launch_fused_fmt(FusedArgs a, hipStream_t st) {
+static hipError_t launch_fused_fmt(FusedArgs a, hipStream_t st, int per_cu_cap = 0) {
     const int S = 64 / a.G, RG = NW / a.KS;
     const int rows_per_tile = S * R;
     int t = 0;
@@ -493,7 +553,9 @@ static hipError_t launch_fused_fmt(FusedArgs a, hipStream_t st) {
         cached_lds = L.total();
     }
     static const int grid_scale = env_int("EXQ_FUSED_GRID", 1);  // tuning override: resident multiple
-    const int resident = per_cu * cus * (grid_scale > 0 ? grid_scale : 1);
+    static const int cu_cap_env = env_int("EXQ_FUSED_PER_CU", 0);  // tuning override: workgroups per CU
+    const int cu_cap = cu_cap_env > 0 ? cu_cap_env : per_cu_cap;
+    const int resident = (cu_cap > 0 && cu_cap < per_cu ? cu_cap : per_cu) * cus * (grid_scale > 0 ? grid_scale : 1);
     const int rounds = (wg_tiles + resident - 1) / resident;
     // workgroup-tile schedule: equal tile counts per workgroup; balanced
     // per-wave schedule: every resident slot (equal work per CU)
@@ -507,15 +569,20 @@ template <class Fmt, int NW, bool STAGE>
 static hipError_t launch_fused_m(FusedArgs a, int r1, int loop, hipStream_t st) {
     switch (a.m) {
         case 1:
-            // the balanced per-wave schedule pays only where the launch has
-            // more than two workgroups' worth of wave tiles per CU (measured:
-            // gate+up [28672 x 4096] 15.3 against 15.7 us; o [4096 x 4096]
-            // 5.5 against 5.0 us)
+            // Launches with more than two workgroups' worth of wave tiles per
+            // CU: two register buffers of 2-row tiles, one workgroup per CU
+            // (EXQ_FUSED_BIG=0: the balanced single-buffer schedule).
+            // Measured, gate+up [28672 x 4096] in the decode step: 14.4 us,
+            // against 15.0-15.2 balanced and 15.7 with workgroup tiles; the
+            // smaller launches (o [4096 x 4096]: 4.9 against 5.5 us) and the
+            // row-split ones keep workgroup tiles at the resident grid.
             if (loop == 2 && a.KS == 1) {
                 const int rows_per_tile = (64 / a.G) * r1;
                 int tiles = 0;
                 for (int z = 0; z < a.nmat; ++z) tiles += (a.n_out[z] + rows_per_tile - 1) / rows_per_tile;
                 if (tiles <= 2 * device_cus() * NW) loop = 0;
+                static const int big = env_int("EXQ_FUSED_BIG", 1);
+                if (loop == 2 && big != 0) return launch_fused_fmt<Fmt, 1, 2, NW, STAGE, 1>(a, st, 1);
             }
             if (loop == 2 && a.KS == 1) {
                 if (r1 == 1) return launch_fused_fmt<Fmt, 1, 1, NW, STAGE, 2>(a, st);
