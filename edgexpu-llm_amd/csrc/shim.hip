@@ -47,8 +47,11 @@ constexpr int kFusedMaxTokens = 4;
 constexpr int kGemmMinTokens = 64;
 // Rows up to this many elements quantize the activation inside the GEMV
 // workgroups; longer rows quantize it once in its own launch (the in-kernel
-// staging costs one load latency per 8192 elements per workgroup).
+// staging costs one load latency per 8192 elements per workgroup) ...
 constexpr int kStageMaxK = 4096;
+// ... except one token's Q8_K activation up to this many elements, which
+// the 16-wave workgroups of the row-split GEMV quantize in one round.
+constexpr int kStageMaxKWide = 16384;
 constexpr int kArgmaxParts = 1024;
 
 struct State {
@@ -123,7 +126,7 @@ bool stage_in_kernel(uint32_t type, int K, int m) {
     static const int mode = env_int("EXQ_FUSED", 1);
     static const int generic = env_int("EXQ_GENERIC", 0);
     if (mode == 0 || generic != 0 || !gemv_fused_supported((int)type, K, m)) return false;
-    return mode == 2 || K <= kStageMaxK;
+    return mode == 2 || K <= kStageMaxK || (type != kTypeQ8_0 && m == 1 && K <= kStageMaxKWide);
 }
 
 bool split_gemv(uint32_t type, int K, int m) {
