@@ -85,6 +85,35 @@ __device__ __forceinline__ int sdot2(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, a), __builtin_bit_cast(short2_t, b), c, false);
 }
 
+// All-reduces within each 16-lane DPP row (lanes 16r..16r+15), every lane
+// active: two quad_perm exchanges (partner lane ^1, ^2) leave each quad with
+// its result, then the half-row mirror (lane i <-> 7-i) pairs the two quads
+// of each half-row and the row mirror (i <-> 15-i) the two halves.  Each step
+// is one VALU instruction with a DPP operand, no LDS round trip.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, true);
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
+constexpr int kDppMirror = 0x140;      // row_mirror
+__device__ __forceinline__ float row8_max(float v) {
+    v = fmaxf(v, __uint_as_float(dpp_u32<kDppXor1>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(dpp_u32<kDppXor2>(__float_as_uint(v))));
+    return fmaxf(v, __uint_as_float(dpp_u32<kDppHalfMirror>(__float_as_uint(v))));
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = row8_max(v);
+    return fmaxf(v, __uint_as_float(dpp_u32<kDppMirror>(__float_as_uint(v))));
+}
+__device__ __forceinline__ uint32_t row16_min(uint32_t v) {
+    v = min(v, dpp_u32<kDppXor1>(v));
+    v = min(v, dpp_u32<kDppXor2>(v));
+    v = min(v, dpp_u32<kDppHalfMirror>(v));
+    return min(v, dpp_u32<kDppMirror>(v));
+}
+
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
     return __shfl_xor(v, mask, 64);
 }

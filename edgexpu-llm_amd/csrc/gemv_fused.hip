@@ -57,10 +57,11 @@ struct WSrc {
 // owning one 16-element group (so its int16 sum needs no reduction); NT/16
 // blocks per round, one round in registers at a time (the register budget of
 // the staging decides the kernel's occupancy).  The first-index signed
-// maximum is one 64-bit max over keys
-//   (|x| bits << 32) | (~index << 1) | sign
-// (equal magnitudes -> lowest index wins; zeros and NaN never enter, matching
-// the reference's strict '>' from amax = 0).
+// maximum is the largest |x| of the block, then the smallest
+//   (index << 1) | sign
+// among the elements equal to it (equal magnitudes -> lowest index wins;
+// zeros and NaN never enter, matching the reference's strict '>' from
+// amax = 0).
 template <int NT>
 __device__ __forceinline__ void quantize_q8_k_group(const float (&xs)[16], int blk, int total, int nb, int K,
                                                     int sub, int8_t *lq, float *ld, int16_t *lbs) {
@@ -77,22 +78,19 @@ __device__ __forceinline__ void quantize_q8_k_group(const float (&xs)[16], int b
         first = hit ? (uint32_t)e : first;
         neg = hit ? (xs[e] < 0.0f ? 1u : 0u) : neg;
     }
-    const uint32_t idx = (uint32_t)(16 * sub) + first;
-    unsigned long long key = ((unsigned long long)__float_as_uint(am) << 32) | (((~idx) & 0x7fffffffu) << 1) | neg;
-    key = (valid && am > 0.0f) ? key : 0ull;
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) {
-        const unsigned long long o = __shfl_xor(key, off, 16);
-        key = o > key ? o : key;
-    }
+    // the block's largest |x| over its 16 threads (one DPP row), then, among
+    // the threads holding it, the lowest (element index, sign): the first
+    // element that attains the maximum
+    const float amax = row16_max(am);
+    const uint32_t win = row16_min(am == amax && amax > 0.0f ? ((((uint32_t)(16 * sub) + first) << 1) | neg)
+                                                              : 0xffffffffu);
     if (!valid) return;
     const int tok = blk / nb, b = blk - tok * nb;
     uint32_t words[4] = {0u, 0u, 0u, 0u};
     int sum = 0;
     float d = 0.0f;
-    if (key != 0ull) {
-        const float amax = __uint_as_float((uint32_t)(key >> 32));
-        const float maxv = (key & 1ull) ? -amax : amax;
+    if (amax > 0.0f) {
+        const float maxv = (win & 1u) ? -amax : amax;
         const float iscale = -127.0f / maxv;
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
@@ -168,10 +166,8 @@ __device__ void stage_q8_0(const FusedArgs &a, float4 v0, int8_t *lq, float *ld)
         const int cb = min(blk, total - 1);
         const int tok = cb / nb, b = cb - tok * nb;
         const float4 v = blk0 == 0 ? v0 : stage_q8_0_load<NT>(a, blk0);
-        float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
-        amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
+        // the block's largest |x| over its 8 threads (half a DPP row)
+        const float amax = row8_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         if (blk >= total) continue;  // uniform within each 8-thread group
         const float d = amax / 127.0f;
         const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
