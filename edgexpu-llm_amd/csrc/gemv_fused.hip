@@ -616,16 +616,34 @@ static hipError_t launch_fused_nw(FusedArgs a, bool stage, hipStream_t st) {
     for (int z = 0; z < a.nmat; ++z) rows += a.n_out[z];
     const int r1 = r_env > 0 ? r_env : (a.KS == 1 && rows <= 4096 ? 2 : 4);
     // Rows split over waves (more than 64 units) with the activation staged
-    // in the kernel, one token: 16-wave workgroups, whose 1024 threads
-    // quantize up to 16384 elements in one round (issued before the first
-    // weight tile) and share it over twice the rows of an 8-wave workgroup.
-    // Measured, down [4096 x 14336] Q4_K in the decode step: 11.4 us, against
-    // 12.6 us for a quantize launch followed by 8-wave workgroups.  Q6_K keeps
+    // in the kernel, one token: 16-wave workgroups (one per CU), whose 1024
+    // threads quantize up to 16384 elements in one round (issued before the
+    // first weight tile) and share it over twice the rows of an 8-wave
+    // workgroup.  Rows per slot: the largest R whose workgroup tiles fill the
+    // grid best (a partial last round leaves CUs idle).  Measured in the
+    // decode steps: down [4096 x 14336] Q4_K 11.4 us (R = 4) against 12.6 us
+    // for a quantize launch and 8-wave workgroups; down [2560 x 9728] Q6_K
+    // 12.0 us (R = 1) against 13.7 us with R = 2; [1024 | 2048 x 14336] Q4_K
+    // 6.9 | 8.4 us (R = 1) against 8.5 | 9.7 us (R = 4).  Q6_K has at most
     // two rows per slot: four exceed the 128 registers of such a workgroup.
     if constexpr (Fmt::kUnitsPerBlock == 4) {  // Q8_K activations (Q4_K, Q6_K rows)
         if (stage && a.m == 1 && a.KS > 1) {
-            if constexpr (sizeof(typename Fmt::W) > 48) return launch_fused_fmt<Fmt, 1, 2, 16, true, 0>(a, st);
-            else return launch_fused_fmt<Fmt, 1, 4, 16, true, 0>(a, st);
+            constexpr int kRMax = sizeof(typename Fmt::W) > 48 ? 2 : 4;
+            const int rg = 16 / a.KS, cus = device_cus();
+            auto fill = [&](int r) {
+                int tiles = 0;
+                for (int z = 0; z < a.nmat; ++z) tiles += (a.n_out[z] + r - 1) / r;
+                const int wg_tiles = (tiles + rg - 1) / rg, rounds = (wg_tiles + cus - 1) / cus;
+                return (double)wg_tiles / (double)(rounds * cus);
+            };
+            static const int r_env = env_int("EXQ_FUSED_NW16_R", 0);  // tuning override: rows per slot
+            int r16 = kRMax;
+            if (kRMax == 4 && fill(2) > fill(r16) + 1e-9) r16 = 2;
+            if (fill(1) > fill(r16) + 1e-9) r16 = 1;
+            if (r_env == 1 || r_env == 2 || (r_env == 4 && kRMax == 4)) r16 = r_env;
+            if (r16 == 1) return launch_fused_fmt<Fmt, 1, 1, 16, true, 0>(a, st);
+            if (r16 == 2) return launch_fused_fmt<Fmt, 1, 2, 16, true, 0>(a, st);
+            if constexpr (kRMax == 4) return launch_fused_fmt<Fmt, 1, 4, 16, true, 0>(a, st);
         }
     }
     if (stage)
