@@ -64,6 +64,8 @@ def parse():
     p.add_argument("--prefill-only", action="store_true", help="run only the prefill-GEMM leg (one JSON line)")
     p.add_argument("--launch-sweep", action="store_true",
                    help="time one Q4_K [rows x 4096] m=1 launch over row counts; fit fixed + marginal cost")
+    p.add_argument("--read-ceiling", action="store_true",
+                   help="time a plain streaming read of each decode launch's weight bytes (one JSON line)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="first copy a 256 MiB buffer 4 times (device to device) for counter calibration")
     return p.parse_args()
@@ -161,6 +163,9 @@ def main():
     gen.manual_seed(args.seed)
     if args.launch_sweep:
         print(json.dumps(launch_sweep(L, E, synth, gen, dev)), flush=True)
+        return
+    if args.read_ceiling:
+        print(json.dumps(read_ceiling(E, cfg, args.workload, dev)), flush=True)
         return
     if args.prefill_only:
         # the prefill GEMM leg alone (for counter runs): one JSON line
@@ -436,6 +441,52 @@ def launch_sweep(L, E, synth, gen, dev):
             "launches": {str(r): v for r, v in res.items()}, "empty_kernel_us": round(empty_us, 3),
             "fit": {"fixed_us": round(float(fixed), 3), "marginal_GBps": round(1e-3 / float(per_byte), 1),
                     "rows_fitted": list(big)}}
+
+
+def read_ceiling(E, cfg, workload, dev):
+    """A plain streaming read (lib/libexq_bench_read.so: one 16-byte load per
+    lane, grid-stride, no arithmetic) of each decode launch's weight bytes,
+    timed like the GEMV launches: a HIP graph of launches over distinct
+    buffers (>= 600 MB in rotation), HIP events around it.  The best of three
+    grid sizes per launch."""
+    import torch
+
+    lib = C.CDLL(os.path.join(ROOT, "edgexpu-llm_amd", "lib", "libexq_bench_read.so"))
+    lib.exq_bench_read.argtypes = [C.c_void_p, C.c_longlong, C.c_void_p, C.c_int, C.c_void_p]
+    lib.exq_bench_read.restype = C.c_int
+    h, t, td = cfg["hidden"], cfg["wtype"], cfg["down_type"]
+    launches = {
+        "qkv": (cfg["qdim"] + 2 * cfg["kv"]) * E.row_bytes(t, h),
+        "o": h * E.row_bytes(t, cfg["qdim"]),
+        "gate_up": 2 * cfg["ffn"] * E.row_bytes(t, h),
+        "down": h * E.row_bytes(td, cfg["ffn"]),
+        "logits": cfg["vocab"] * E.row_bytes(cfg["logits_type"], h),
+    }
+    grids = (1024, 2048, 4096)
+    out = torch.empty(max(grids) * 256, dtype=torch.int32, device=dev)
+    res = {}
+    for name, nbytes in launches.items():
+        nbytes -= nbytes % 256
+        n = max(4, -(-int(MIN_ROTATION_BYTES) // nbytes))
+        buf = torch.ones(n * nbytes, dtype=torch.uint8, device=dev)
+        best = None
+        for grid in grids:
+            def launches_fn(sp, grid=grid):
+                for i in range(n):
+                    if lib.exq_bench_read(buf.data_ptr() + i * nbytes, nbytes, out.data_ptr(), grid, sp) != 0:
+                        raise RuntimeError("exq_bench_read failed")
+
+            g = capture(launches_fn)
+            g.replay()
+            us = min(timed(g.replay, 3) for _ in range(2)) * 1e3 / n
+            if best is None or us < best[0]:
+                best = (us, grid)
+            del g
+        res[name] = {"bytes": nbytes, "us": round(best[0], 3), "GBps": round(nbytes / (best[0] * 1e-6) / 1e9, 1),
+                     "grid": best[1]}
+        del buf
+    return {"metric": "plain read of each decode launch's weight bytes, us per launch, 1 GPU",
+            "workload": workload, "launches": res}
 
 
 def dequant_leg(L, E, synth, gen, dev, no_cpu=False):
