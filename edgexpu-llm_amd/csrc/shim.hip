@@ -24,6 +24,8 @@ hipError_t launch_gemv_q8(int type, const uint8_t *w, size_t row_bytes, int n_ou
 hipError_t launch_gemv_f32(int type, const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const float *xf,
                            const float *xs, const float *bias, float *out, int ldo, hipStream_t st);
 hipError_t launch_xsum16(const float *x, int m, int K, float *xs, hipStream_t st);
+hipError_t launch_rmsnorm(const float *x, const float *w, float *out, int m, int n, float eps, hipStream_t st);
+hipError_t launch_elementwise(const float *a, const float *b, float *out, long long n, int kind, hipStream_t st);
 hipError_t launch_argmax_rows(const float *s, int m, int n, size_t lds, unsigned long long *partial, uint32_t *best,
                               hipStream_t st);
 hipError_t launch_gemm_q8(int type, const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const uint8_t *xq,
@@ -582,6 +584,41 @@ int edgexpu_hip_quantize_q8_0_dev(const float *x, int m, int n, uint8_t *dst, vo
 
 int edgexpu_hip_quantize_q8_k_dev(const float *x, int m, int n, uint8_t *dst, void *stream) {
     return quantize_dev(x, m, n, dst, stream, true);
+}
+
+// ------------------------------------------------------ layer elementwise ops
+
+int edgexpu_hip_rmsnorm_dev(float *out, const float *x, const float *weight, int m, int n, float eps, void *stream) {
+    if (!ensure_init()) return 0;
+    if (out == nullptr || x == nullptr || weight == nullptr || m <= 0 || n <= 0) {
+        set_error(-2, "rmsnorm: null buffer or bad size (m=%d n=%d)", m, n);
+        return 0;
+    }
+    return hip_ok(launch_rmsnorm(x, weight, out, m, n, eps, pick_stream(stream)), "rmsnorm") ? 1 : 0;
+}
+
+namespace {
+int elementwise_dev(float *out, const float *a, const float *b, long long n, int kind, void *stream, const char *what) {
+    if (!ensure_init()) return 0;
+    if (out == nullptr || a == nullptr || (kind != 0 && b == nullptr) || n <= 0) {
+        set_error(-2, "%s: null buffer or bad size (n=%lld)", what, n);
+        return 0;
+    }
+    return hip_ok(launch_elementwise(a, b, out, n, kind, pick_stream(stream)), what) ? 1 : 0;
+}
+}  // namespace
+
+int edgexpu_hip_silu_dev(float *out, const float *x, long long n, void *stream) {
+    return elementwise_dev(out, x, nullptr, n, 0, stream, "silu");
+}
+int edgexpu_hip_mul_dev(float *out, const float *a, const float *b, long long n, void *stream) {
+    return elementwise_dev(out, a, b, n, 1, stream, "mul");
+}
+int edgexpu_hip_add_dev(float *out, const float *a, const float *b, long long n, void *stream) {
+    return elementwise_dev(out, a, b, n, 2, stream, "add");
+}
+int edgexpu_hip_silu_mul_dev(float *out, const float *gate, const float *up, long long n, void *stream) {
+    return elementwise_dev(out, gate, up, n, 3, stream, "silu_mul");
 }
 
 // ------------------------------------------------------------ host entries

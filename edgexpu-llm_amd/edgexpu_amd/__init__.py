@@ -91,6 +91,12 @@ class HipLib:
                                  [_vp, _vp, C.c_uint32, _vp, C.c_int, C.c_int])
         self.dot_q8_rows = _sig(L, "edgexpu_hip_dot_q8_rows", C.c_int,
                                 [_vp, _vp, C.c_uint32, _vp, C.c_int, C.c_int])
+        self.rmsnorm_dev = _sig(L, "edgexpu_hip_rmsnorm_dev", C.c_int,
+                                [_vp, _vp, _vp, C.c_int, C.c_int, C.c_float, _vp])
+        self.silu_dev = _sig(L, "edgexpu_hip_silu_dev", C.c_int, [_vp, _vp, C.c_longlong, _vp])
+        self.mul_dev = _sig(L, "edgexpu_hip_mul_dev", C.c_int, [_vp, _vp, _vp, C.c_longlong, _vp])
+        self.add_dev = _sig(L, "edgexpu_hip_add_dev", C.c_int, [_vp, _vp, _vp, C.c_longlong, _vp])
+        self.silu_mul_dev = _sig(L, "edgexpu_hip_silu_mul_dev", C.c_int, [_vp, _vp, _vp, C.c_longlong, _vp])
 
     def last_error(self) -> tuple[int, str]:
         buf = C.create_string_buffer(512)
@@ -216,3 +222,45 @@ def quantize_q8_k(x):
     L = hip()
     L.check(L.q8k_dev(_ptr(x), m, n, _ptr(dst), _stream()), "quantize_q8_k")
     return dst
+
+
+# ------------------------------------------------------ layer elementwise ops
+
+
+def rmsnorm(x, weight, eps: float, out=None):
+    """RMSNorm of each row of a float32 [m, n] device tensor (edgexpu_hip_rmsnorm_dev)."""
+    import torch
+
+    m, n = x.shape
+    if out is None:
+        out = torch.empty_like(x)
+    L = hip()
+    L.check(L.rmsnorm_dev(out.data_ptr(), x.data_ptr(), weight.data_ptr(), m, n, eps, _stream()), "rmsnorm")
+    return out
+
+
+def _ew(fn, what, a, b=None, out=None):
+    import torch
+
+    if out is None:
+        out = torch.empty_like(a)
+    L = hip()
+    args = [out.data_ptr(), a.data_ptr()] + ([] if b is None else [b.data_ptr()]) + [a.numel(), _stream()]
+    L.check(getattr(L, fn)(*args), what)
+    return out
+
+
+def silu(x, out=None):
+    return _ew("silu_dev", "silu", x, out=out)
+
+
+def mul(a, b, out=None):
+    return _ew("mul_dev", "mul", a, b, out=out)
+
+
+def add(a, b, out=None):
+    return _ew("add_dev", "add", a, b, out=out)
+
+
+def silu_mul(gate, up, out=None):
+    return _ew("silu_mul_dev", "silu_mul", gate, up, out=out)

@@ -148,6 +148,31 @@ int edgexpu_hip_dequantize_dev(const void *src, uint32_t type, uint64_t n_elemen
 int edgexpu_hip_quantize_q8_0_dev(const float *x, int m, int n, uint8_t *dst, void *stream);
 int edgexpu_hip_quantize_q8_k_dev(const float *x, int m, int n, uint8_t *dst, void *stream);
 
+/* The elementwise layer ops around the projections, on device-resident
+ * activations (the ops a decode layer applies between its projections,
+ * src/native.c:2529-2580), so that a layer's activations need not leave the
+ * GPU.  Same arithmetic as the reference op for op:
+ *   rmsnorm:  edgexpu_cpu_rmsnorm (include/edgexpu/cpu_kernel.h:19,
+ *             src/cpu_kernel.c:220-242), over m rows of n elements with one
+ *             weight vector of n; double sum of squares (as a tree: the float
+ *             mean can differ from the reference's index-order sum only where
+ *             its rounding falls within the double sum's error);
+ *   silu:     edgexpu_cpu_silu (cpu_kernel.h:20, src/cpu_kernel.c:244-252),
+ *             exp evaluated in double and rounded once (correctly rounded;
+ *             the host libm's expf is not, on ~0.03 % of inputs, which moves
+ *             silu by up to two ulp there);
+ *   mul, add: edgexpu_cpu_mul / edgexpu_cpu_add (src/cpu_kernel.c:200-218),
+ *             exact;
+ *   silu_mul: silu(gate) then * up in one pass, the reference's
+ *             edgexpu_cpu_silu + edgexpu_cpu_mul (src/native.c:2577-2578).
+ * out may equal an input.  Return 1 on success, 0 on bad arguments or a HIP
+ * error (see edgexpu_hip_last_error). */
+int edgexpu_hip_rmsnorm_dev(float *out, const float *x, const float *weight, int m, int n, float eps, void *stream);
+int edgexpu_hip_silu_dev(float *out, const float *x, long long n, void *stream);
+int edgexpu_hip_mul_dev(float *out, const float *a, const float *b, long long n, void *stream);
+int edgexpu_hip_add_dev(float *out, const float *a, const float *b, long long n, void *stream);
+int edgexpu_hip_silu_mul_dev(float *out, const float *gate, const float *up, long long n, void *stream);
+
 /* ---- host-pointer entry points (synchronous: inputs copied in, outputs
  * copied out before return; the PCIe copies are part of the call) ---- */
 

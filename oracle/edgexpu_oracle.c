@@ -710,6 +710,38 @@ uint32_t ora_logits(float *scores, const float *hidden, const uint8_t *w, uint32
 
 /* -------------------------------------------------------- self-test */
 
+/* -------------------------------------------------- layer elementwise ops */
+
+/* src/cpu_kernel.c:220-242. */
+void ora_rmsnorm(float *out, const float *x, const float *w, int n, float eps) {
+    double ss = 0.0;
+    float mean, scale;
+    int i;
+    for (i = 0; i < n; i++) ss += (double)x[i] * (double)x[i];
+    mean = (float)(ss / (double)n);
+    scale = 1.0f / sqrtf(mean + eps);
+    for (i = 0; i < n; i++) out[i] = x[i] * scale;
+    for (i = 0; i < n; i++) out[i] *= w[i];
+}
+
+/* src/cpu_kernel.c:244-252. */
+void ora_silu(float *out, const float *x, int n) {
+    int i;
+    for (i = 0; i < n; i++) out[i] = x[i] / (1.0f + expf(-x[i]));
+}
+
+/* src/cpu_kernel.c:210-218. */
+void ora_mul(float *out, const float *a, const float *b, int n) {
+    int i;
+    for (i = 0; i < n; i++) out[i] = a[i] * b[i];
+}
+
+/* src/cpu_kernel.c:200-208. */
+void ora_add(float *out, const float *a, const float *b, int n) {
+    int i;
+    for (i = 0; i < n; i++) out[i] = a[i] + b[i];
+}
+
 int ora_selftest(char *error, size_t error_size) {
     uint8_t blk[B_Q4_K];
     float x[QKK];

@@ -81,6 +81,18 @@ int ora_linear_quant_batch(float *out, const float *x, const uint8_t *w, uint32_
 uint32_t ora_logits(float *scores, const float *hidden, const uint8_t *w, uint32_t type,
                     const float *bias, int vocab, int n_embd, size_t chunk_rows);
 
+
+/* The elementwise layer ops around the projections (src/cpu_kernel.c:
+ * 200-252), used by the device-resident layer entry points:
+ *   rmsnorm: double sum of x^2 in index order, mean = (float)(ss / n),
+ *            scale = 1.0f / sqrtf(mean + eps), out = x * scale, out *= w;
+ *   silu:    out = x / (1.0f + expf(-x));
+ *   mul/add: out = a * b, out = a + b. */
+void ora_rmsnorm(float *out, const float *x, const float *w, int n, float eps);
+void ora_silu(float *out, const float *x, int n);
+void ora_mul(float *out, const float *a, const float *b, int n);
+void ora_add(float *out, const float *a, const float *b, int n);
+
 /* Self-checks restated from src/gguf_quant.c:934-1061 (Q4_K/Q8_0 parts).
  * Returns 1 when they pass. */
 int ora_selftest(char *error, size_t error_size);

@@ -56,7 +56,50 @@ class _Lib:
         return f
 
 
-class Oracle(_Lib):
+def _ew_setup(obj, rms, silu, mul, add):
+    """Binds the elementwise layer ops (same signatures in both libraries)."""
+    L = obj.fn
+    obj._rms = L(rms, None, [_f32p, _f32p, _f32p, C.c_int, C.c_float])
+    obj._silu = L(silu, None, [_f32p, _f32p, C.c_int])
+    obj._mul = L(mul, None, [_f32p, _f32p, _f32p, C.c_int])
+    obj._add = L(add, None, [_f32p, _f32p, _f32p, C.c_int])
+
+
+class _Elementwise:
+    """rmsnorm / silu / mul / add over float32 vectors (one row at a time)."""
+
+    def rmsnorm(self, x, w, eps):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        out = np.empty_like(x)
+        for t in range(x.shape[0] if x.ndim == 2 else 1):
+            xr = x[t] if x.ndim == 2 else x
+            orow = out[t] if x.ndim == 2 else out
+            self._rms(_p(orow, _f32p), _p(xr, _f32p), _p(w, _f32p), xr.size, eps)
+        return out
+
+    def silu(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty_like(x)
+        self._silu(_p(out, _f32p), _p(x, _f32p), x.size)
+        return out
+
+    def mul(self, a, b):
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        b = np.ascontiguousarray(b, dtype=np.float32)
+        out = np.empty_like(a)
+        self._mul(_p(out, _f32p), _p(a, _f32p), _p(b, _f32p), a.size)
+        return out
+
+    def add(self, a, b):
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        b = np.ascontiguousarray(b, dtype=np.float32)
+        out = np.empty_like(a)
+        self._add(_p(out, _f32p), _p(a, _f32p), _p(b, _f32p), a.size)
+        return out
+
+
+class Oracle(_Lib, _Elementwise):
     """The clean-room restatement (``ora_*`` symbols)."""
 
     def __init__(self, path: str = ORACLE_SO):
@@ -78,6 +121,7 @@ class Oracle(_Lib):
         self._h2f = L("ora_fp16_to_fp32", C.c_float, [C.c_uint16])
         self._f2h = L("ora_fp32_to_fp16", C.c_uint16, [C.c_float])
         self._self = L("ora_selftest", C.c_int, [C.c_char_p, C.c_size_t])
+        _ew_setup(self, "ora_rmsnorm", "ora_silu", "ora_mul", "ora_add")
 
     # -- codecs
     def fp16_to_fp32(self, h: int) -> float:
@@ -158,7 +202,7 @@ class Oracle(_Lib):
         return bool(ok), buf.value.decode()
 
 
-class Reference(_Lib):
+class Reference(_Lib, _Elementwise):
     """The reference's own kernels, compiled from source into oracle/_ref."""
 
     def __init__(self, path: str = REF_SO):
@@ -174,6 +218,7 @@ class Reference(_Lib):
         self._lin = L("edgexpu_cpu_linear_quant_batch", None,
                       [_f32p, _f32p, _u8p, C.c_uint32, _f32p, C.c_int, C.c_int, C.c_int])
         self._self = L("edgexpu_gguf_quant_selftest", C.c_int, [C.c_char_p, C.c_size_t])
+        _ew_setup(self, "edgexpu_cpu_rmsnorm", "edgexpu_cpu_silu", "edgexpu_cpu_mul", "edgexpu_cpu_add")
 
     def dequantize(self, src, qtype, n):
         src = np.ascontiguousarray(src, dtype=np.uint8)

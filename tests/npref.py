@@ -235,3 +235,16 @@ def q4k_q8k_gemm_f64(w: np.ndarray, xq: np.ndarray):
         val += dx[:, b:b + 1] * (d[None, :, b] * isum - dmin[None, :, b] * imin)
         mag += np.abs(dx[:, b:b + 1]) * (np.abs(d[None, :, b]) * (aq @ ws.T) + np.abs(dmin[None, :, b]) * (aq @ wm.T))
     return val, mag
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """src/cpu_kernel.c:220-242 in numpy: the squares summed in float64 in
+    index order (np.add.accumulate is sequential), the mean rounded to
+    float32, scale = 1 / sqrt(mean + eps) in float32 (correctly rounded
+    sqrt and division), then x * scale and * w, each rounded to float32."""
+    x = np.asarray(x, dtype=np.float32)
+    x64 = x.astype(np.float64)
+    ss = np.add.accumulate(x64 * x64)[-1]
+    mean = np.float32(ss / np.float64(x.size))
+    scale = np.float32(1.0) / np.sqrt(np.float32(mean + np.float32(eps)))
+    return (x * scale) * np.asarray(w, dtype=np.float32)

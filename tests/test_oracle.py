@@ -233,3 +233,68 @@ def test_mutations_are_caught(golden):
     x = gq["x"][idx]
     flipped = npref.quantize_q8_k(-x[::-1].copy())[4:260].view(np.int8)[::-1]
     assert not np.array_equal(flipped.view(np.uint8), gq["q8_k"][idx][4:260])
+
+
+# ------------------------------------------------ 4. layer elementwise ops
+
+def _layer_vectors(rng, n):
+    """Random rows plus the edge cases the layer ops meet: zeros, huge and
+    tiny magnitudes, a single nonzero, negative values."""
+    rows = [rng.normal(0, 1, n), rng.normal(0, 300, n), rng.normal(0, 1e-3, n), np.zeros(n)]
+    one = np.zeros(n)
+    one[n // 3] = -7.25
+    rows.append(one)
+    rows.append(np.linspace(-20, 20, n))
+    return np.asarray(rows, dtype=np.float32)
+
+
+@pytest.mark.parametrize("n", [576, 2560, 4096, 14336])
+def test_layer_ops_vs_reference_build(ora, ref, n):
+    """rmsnorm / silu / mul / add of the oracle are bit-identical to the
+    reference's own (src/cpu_kernel.c:200-252) on the same inputs."""
+    rng = np.random.default_rng(n)
+    xs = _layer_vectors(rng, n)
+    w = rng.normal(1, 0.2, n).astype(np.float32)
+    for x in xs:
+        for eps in (1e-5, 1e-6):
+            assert np.array_equal(bits(ora.rmsnorm(x, w, eps)), bits(ref.rmsnorm(x, w, eps)))
+        assert np.array_equal(bits(ora.silu(x)), bits(ref.silu(x)))
+        assert np.array_equal(bits(ora.mul(x, w)), bits(ref.mul(x, w)))
+        assert np.array_equal(bits(ora.add(x, w)), bits(ref.add(x, w)))
+
+
+@pytest.mark.parametrize("n", [576, 4096])
+def test_rmsnorm_closed_form(ora, n):
+    """The numpy restatement (float64 squares in order, float32 mean, correctly
+    rounded sqrt and division) reproduces the oracle bit for bit; a float32
+    accumulation of the squares (a plausible mistake) does not."""
+    rng = np.random.default_rng(7 + n)
+    w = rng.normal(1, 0.2, n).astype(np.float32)
+    differs = 0
+    for x in _layer_vectors(rng, n):
+        want = ora.rmsnorm(x, w, 1e-5)
+        assert np.array_equal(bits(npref.rmsnorm(x, w, 1e-5)), bits(want))
+        ss32 = np.float32(0)
+        for v in x:
+            ss32 = np.float32(ss32 + np.float32(v * v))
+        wrong = (x * (np.float32(1) / np.sqrt(np.float32(np.float32(ss32 / np.float32(n)) + np.float32(1e-5))))) * w
+        differs += int(not np.array_equal(bits(wrong), bits(want)))
+    assert differs > 0
+
+
+def test_silu_special_values(ora):
+    """silu(0) = 0 (the reference's own self-test, src/cpu_kernel.c:884-887);
+    large positive x returns x exactly (expf(-x) underflows to 0); large
+    negative x gives -0; NaN stays NaN; elsewhere within 2 ulp of float64."""
+    x = np.array([0.0, 100.0, 1e30, -200.0, -1e30], dtype=np.float32)
+    y = ora.silu(x)
+    assert y[0] == 0.0 and y[1] == np.float32(100.0) and y[2] == np.float32(1e30)
+    assert y[3] == 0.0 and np.signbit(y[3]) and y[4] == 0.0
+    assert np.isnan(ora.silu(np.array([np.nan], dtype=np.float32)))[0]
+    rng = np.random.default_rng(11)
+    xs = rng.normal(0, 4, 20000).astype(np.float32)
+    got = ora.silu(xs).astype(np.float64)
+    x64 = xs.astype(np.float64)
+    want = x64 / (1.0 + np.exp(-x64))
+    ulp = np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 2 * ulp)
