@@ -114,6 +114,30 @@ __device__ __forceinline__ uint32_t row16_min(uint32_t v) {
     return min(v, dpp_u32<kDppMirror>(v));
 }
 
+// SiLU as src/cpu_kernel.c:244-252 computes it, x / (1.0f + expf(-x)), with
+// the exponential evaluated in double and rounded once to float (correctly
+// rounded; the host libm's expf is not on a small fraction of inputs, where
+// the two silu values differ by up to two ulp).
+__device__ __forceinline__ float silu_f32(float v) {
+    const float e = (float)exp(-(double)v);
+    return v / (1.0f + e);
+}
+
+// RMSNorm scale from the double sum of squares of n elements, as
+// src/cpu_kernel.c:232-235: mean rounded to float, then 1 / sqrtf(mean + eps)
+// (IEEE sqrt and division).
+__device__ __forceinline__ float rms_scale(double ss, int n, float eps) {
+    const float mean = (float)(ss / (double)n);
+    return 1.0f / sqrtf(mean + eps);
+}
+
+// Sum of a double over the 64 lanes of a wave (every lane gets the total).
+__device__ __forceinline__ double wave_sum_f64(double s) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    return s;
+}
+
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
     return __shfl_xor(v, mask, 64);
 }

@@ -45,6 +45,10 @@ struct FusedArgs {
     size_t xq_stride;      //     (Q8_0: 34 B per 32, Q8_K: 292 B per 256), token t at xq + t*xq_stride
     const float *xf;       // or (f32-activation formats): x [m][K] f32
     const float *xs;       //     and its 16-element sums [m][K/16]
+    const float *resid[kFusedMaxMats];  // added to each output after its bias ([m][n_out[z]]; null: none)
+    const float *x2;       // SiLU-mul prologue: the staged activation is silu(x) * x2
+    const float *nw;       // RMSNorm prologue: the staged activation is rmsnorm(x; nw, eps)
+    float eps;
 };
 
 struct WSrc {
@@ -110,34 +114,90 @@ __device__ __forceinline__ void quantize_q8_k_group(const float (&xs)[16], int b
 }
 
 // This thread's 16 elements of the round starting at block blk0 (clamped:
-// every thread issues the same loads).
+// every thread issues the same loads) from src, whose tokens are tok_stride
+// elements apart (the activation: K; the RMSNorm weights: 0).
 template <int NT>
-__device__ __forceinline__ void stage_q8_k_load(const FusedArgs &a, int blk0, float (&xs)[16]) {
+__device__ __forceinline__ void stage_q8_k_load_from(const float *src, size_t tok_stride, const FusedArgs &a,
+                                                     int blk0, float (&xs)[16]) {
     const int tid = threadIdx.x, sub = tid & 15, bl = tid >> 4;
     const int nb = a.K / kQKK, total = a.m * nb;
     const int cb = min(blk0 + bl, total - 1);
     const int tok = cb / nb;
     const float4 *p =
-        reinterpret_cast<const float4 *>(a.x + (size_t)tok * a.K + (size_t)(cb - tok * nb) * kQKK + 16 * sub);
+        reinterpret_cast<const float4 *>(src + (size_t)tok * tok_stride + (size_t)(cb - tok * nb) * kQKK + 16 * sub);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const float4 u = p[k];
         xs[4 * k] = u.x; xs[4 * k + 1] = u.y; xs[4 * k + 2] = u.z; xs[4 * k + 3] = u.w;
     }
 }
+template <int NT>
+__device__ __forceinline__ void stage_q8_k_load(const FusedArgs &a, int blk0, float (&xs)[16]) {
+    stage_q8_k_load_from<NT>(a.x, (size_t)a.K, a, blk0, xs);
+}
+
+// The prologue's second input for this thread's elements, loaded with the
+// activation: x2 (SiLU-mul) or the RMSNorm weights.
+template <int PRO, int NT>
+__device__ __forceinline__ void stage_pro_load16(const FusedArgs &a, int blk0, float (&ys)[16]) {
+    if constexpr (PRO == 2) stage_q8_k_load_from<NT>(a.x2, (size_t)a.K, a, blk0, ys);
+    else if constexpr (PRO == 1) stage_q8_k_load_from<NT>(a.nw, 0, a, blk0, ys);
+}
+
+// The staging prologue on n elements of one thread (src/native.c:2529,
+// 2576-2578): SiLU-mul, act = silu(x) * x2; RMSNorm (one token, every
+// element of the row loaded in this round), act = (x * scale) * w with scale
+// from the double sum of squares over the workgroup (lanes whose loads were
+// clamped past the row's end contribute nothing).
+template <int PRO, int NW, int N>
+__device__ __forceinline__ void stage_pro_apply(const FusedArgs &a, float (&xs)[N], const float (&ys)[N], bool valid) {
+    if constexpr (PRO == 2) {
+#pragma unroll
+        for (int e = 0; e < N; ++e) xs[e] = silu_f32(xs[e]) * ys[e];
+    } else if constexpr (PRO == 1) {
+        __shared__ double red[NW];
+        double s = 0.0;
+#pragma unroll
+        for (int e = 0; e < N; ++e) {
+            const double v = (double)xs[e];
+            s += v * v;
+        }
+        s = wave_sum_f64(valid ? s : 0.0);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+        __syncthreads();
+        double ss = 0.0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) ss += red[w];
+        const float scale = rms_scale(ss, a.K, a.eps);
+#pragma unroll
+        for (int e = 0; e < N; ++e) {
+            const float v = xs[e] * scale;
+            xs[e] = v * ys[e];
+        }
+    }
+}
 
 // Q8_K quantization of x into LDS, 16 threads per 256-block; the first
 // round's elements (xs0) were loaded by the caller before the first weight
 // tile, so they do not queue behind it.
-template <int NT>
-__device__ void stage_q8_k(const FusedArgs &a, const float (&xs0)[16], int8_t *lq, float *ld, int16_t *lbs) {
+template <int NT, int PRO = 0>
+__device__ void stage_q8_k(const FusedArgs &a, const float (&xs0)[16], const float (&ys0)[16], int8_t *lq,
+                           float *ld, int16_t *lbs) {
     constexpr int BPR = NT / 16;  // blocks per round
     const int tid = threadIdx.x, sub = tid & 15, bl = tid >> 4;
     const int nb = a.K / kQKK, total = a.m * nb;
-    quantize_q8_k_group<NT>(xs0, bl, total, nb, a.K, sub, lq, ld, lbs);
-    for (int blk0 = BPR; blk0 < total; blk0 += BPR) {
+    {
         float xs[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) xs[e] = xs0[e];
+        stage_pro_apply<PRO, NT / 64>(a, xs, ys0, bl < total);
+        quantize_q8_k_group<NT>(xs, bl, total, nb, a.K, sub, lq, ld, lbs);
+    }
+    for (int blk0 = BPR; blk0 < total; blk0 += BPR) {  // RMSNorm prologue: never (one round)
+        float xs[16], ys[16];
         stage_q8_k_load<NT>(a, blk0, xs);
+        stage_pro_load16<PRO, NT>(a, blk0, ys);
+        if constexpr (PRO == 2) stage_pro_apply<PRO, NT / 64>(a, xs, ys, true);
         quantize_q8_k_group<NT>(xs, blk0 + bl, total, nb, a.K, sub, lq, ld, lbs);
     }
 }
@@ -146,26 +206,45 @@ __device__ void stage_q8_k(const FusedArgs &a, const float (&xs0)[16], int8_t *l
 // 8 threads per 32-element block, NT/8 blocks per round; same arithmetic as
 // quantize_q8_0_kernel.
 template <int NT>
-__device__ __forceinline__ float4 stage_q8_0_load(const FusedArgs &a, int blk0) {
+__device__ __forceinline__ float4 stage_q8_0_load_from(const float *src, size_t tok_stride, const FusedArgs &a,
+                                                      int blk0) {
     const int tid = threadIdx.x, part = tid & 7, bl = tid >> 3;
     const int nb = a.K / kQK8_0, total = a.m * nb;
     const int cb = min(blk0 + bl, total - 1);  // clamped: every thread issues the same loads
     const int tok = cb / nb, b = cb - tok * nb;
-    return *reinterpret_cast<const float4 *>(a.x + (size_t)tok * a.K + (size_t)b * kQK8_0 + part * 4);
+    return *reinterpret_cast<const float4 *>(src + (size_t)tok * tok_stride + (size_t)b * kQK8_0 + part * 4);
+}
+template <int NT>
+__device__ __forceinline__ float4 stage_q8_0_load(const FusedArgs &a, int blk0) {
+    return stage_q8_0_load_from<NT>(a.x, (size_t)a.K, a, blk0);
+}
+template <int PRO, int NT>
+__device__ __forceinline__ float4 stage_pro_load4(const FusedArgs &a, int blk0) {
+    if constexpr (PRO == 2) return stage_q8_0_load_from<NT>(a.x2, (size_t)a.K, a, blk0);
+    else if constexpr (PRO == 1) return stage_q8_0_load_from<NT>(a.nw, 0, a, blk0);
+    else return make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
-// v0: this thread's elements of the first round, loaded by the caller before
-// the first weight tile.
-template <int NT>
-__device__ void stage_q8_0(const FusedArgs &a, float4 v0, int8_t *lq, float *ld) {
+// v0 / y0: this thread's elements of the first round (activation and the
+// prologue's second input), loaded by the caller before the first weight
+// tile.
+template <int NT, int PRO = 0>
+__device__ void stage_q8_0(const FusedArgs &a, float4 v0, float4 y0, int8_t *lq, float *ld) {
     constexpr int BPR = NT / 8;  // blocks per round
     const int tid = threadIdx.x, part = tid & 7, bl = tid >> 3;
     const int nb = a.K / kQK8_0, total = a.m * nb;
-    for (int blk0 = 0; blk0 < total; blk0 += BPR) {
+    for (int blk0 = 0; blk0 < total; blk0 += BPR) {  // RMSNorm prologue: one round
         const int blk = blk0 + bl;
         const int cb = min(blk, total - 1);
         const int tok = cb / nb, b = cb - tok * nb;
-        const float4 v = blk0 == 0 ? v0 : stage_q8_0_load<NT>(a, blk0);
+        float4 v = blk0 == 0 ? v0 : stage_q8_0_load<NT>(a, blk0);
+        if constexpr (PRO != 0) {
+            const float4 y = blk0 == 0 ? y0 : stage_pro_load4<PRO, NT>(a, blk0);
+            float xv[4] = {v.x, v.y, v.z, v.w};
+            const float yv[4] = {y.x, y.y, y.z, y.w};
+            stage_pro_apply<PRO, NT / 64>(a, xv, yv, blk < total);
+            v = make_float4(xv[0], xv[1], xv[2], xv[3]);
+        }
         // the block's largest |x| over its 8 threads (half a DPP row)
         const float amax = row8_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         if (blk >= total) continue;  // uniform within each 8-thread group
@@ -197,21 +276,28 @@ constexpr int kRawBufferWord3 = 0x00020000;
 // A buffer offset beyond every output buffer: the store is dropped.
 constexpr int kDeadOffset = 0x7ffffff0;
 
+// A tile output's bias and residual words (zero where there is none).
+struct Epi {
+    float b, r;
+};
+
 struct TileMat {
     const uint8_t *w;
     const float *bias;
+    const float *resid;
     float *out;
     int n_out;
     int row0;
 };
 __device__ __forceinline__ TileMat locate(const FusedArgs &a, int tile, int rows_per_tile) {
-    TileMat t{a.w[0], a.bias[0], a.out[0], a.n_out[0], 0};
+    TileMat t{a.w[0], a.bias[0], a.resid[0], a.out[0], a.n_out[0], 0};
     int start = 0;
 #pragma unroll
     for (int k = 1; k < kFusedMaxMats; ++k) {
         const bool in = k < a.nmat && tile >= a.tile_start[k];
         t.w = in ? a.w[k] : t.w;
         t.bias = in ? a.bias[k] : t.bias;
+        t.resid = in ? a.resid[k] : t.resid;
         t.out = in ? a.out[k] : t.out;
         t.n_out = in ? a.n_out[k] : t.n_out;
         start = in ? a.tile_start[k] : start;
@@ -238,9 +324,9 @@ struct FusedLds {
 // spilling (checked with -Rpass-analysis=kernel-resource-usage).
 template <class Fmt>
 constexpr int fused_occupancy(int r, int m, int loop) {
-    // f32-activation formats: the activation slice (up to 66 floats) stays
+    // f32-activation formats: the activation slice (32 to 68 floats) stays
     // in registers
-    if (sizeof(typename Fmt::Act) > 128) return r <= 1 ? 4 : 3;
+    if (sizeof(typename Fmt::Act) >= 128) return r <= 1 ? 4 : 3;
     return loop == 1 ? (r <= 1 ? (sizeof(typename Fmt::W) > 48 ? 4 : 5) : r <= 2 ? (sizeof(typename Fmt::W) > 48 ? 3 : 4) : 2)
            : loop == 2 ? (r <= 1 ? (sizeof(typename Fmt::W) > 48 ? 5 : 7)
                           : r <= 2 ? (sizeof(typename Fmt::W) > 48 ? 4 : 5)
@@ -252,9 +338,22 @@ constexpr int fused_occupancy(int r, int m, int loop) {
 
 // STAGE: quantize a.x into LDS inside the kernel; otherwise read the codes
 // of a.xq (quantized by an earlier launch) straight from global memory.
-template <class Fmt, int M, int R, int NW, bool STAGE, int LOOP>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(fused_occupancy<Fmt>(R, M, LOOP)))) void
-gemv_fused_kernel(FusedArgs a) {
+// A staging prologue holds its second input (16 more registers) and its
+// arithmetic beside the first tile: one wave per SIMD fewer where the plain
+// kernel runs at more than 5 (4 for the Q6_K rows), so that nothing spills.
+template <class Fmt>
+constexpr int fused_occupancy_pro(int r, int m, int loop, int pro) {
+    const int occ = fused_occupancy<Fmt>(r, m, loop);
+    const int cap = sizeof(typename Fmt::W) > 48 ? 4 : 5;
+    return (pro & 3) != 0 && occ > cap ? cap : occ;
+}
+
+// PRO bits 0-1: staging prologue (0 none, 1 RMSNorm, 2 SiLU-mul; STAGE
+// kernels); bit 2: residual epilogue (outputs += resid).  Without bit 2 the
+// kernel loads no residual word and holds no register for it.
+template <class Fmt, int M, int R, int NW, bool STAGE, int LOOP, int PRO = 0>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(fused_occupancy_pro<Fmt>(R, M, LOOP, PRO))))
+void gemv_fused_kernel(FusedArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     // wave-uniform values go through readfirstlane so that the tile, matrix
     // and pointer selection below is scalar (kernel-argument arrays are read
@@ -298,39 +397,53 @@ gemv_fused_kernel(FusedArgs a) {
     const int o_r = o_idx / M, o_t = o_idx - (o_idx / M) * M;
 
     // Loads of one tile: weights (unconditional: clamped tile, row and unit,
-    // so every path issues the same loads) and the bias of this lane's output.
+    // so every path issues the same loads), the bias and the residual of
+    // this lane's output.
     const int wg_tiles = (a.ntiles + RG - 1) / RG;
-    // The bias word is loaded unconditionally (from the weights when there is
-    // no bias) and selected when used: a conditional write to the register
-    // of a load still in flight would make the compiler wait for every
-    // outstanding load first, which serialises the prefetch.
-    auto issue_tile = [&](const TileMat &t_, float &bias_, typename Fmt::W (&w_)[R]) {
-        // the bias first: waiting for it then waits for no weight row
-        const float *bsrc = t_.bias != nullptr ? t_.bias + min(t_.row0 + o_slot + S * o_r, t_.n_out - 1)
-                                               : reinterpret_cast<const float *>(t_.w);
-        bias_ = *bsrc;
+    constexpr bool kRes = (PRO & 4) != 0;
+    // The bias (and residual) words are loaded unconditionally and selected
+    // when used: a conditional write to the register of a load still in
+    // flight would make the compiler wait for every outstanding load first,
+    // which serialises the prefetch.  Where there is none the load reads the
+    // first word of the lane's first weight row, a line its workgroup's
+    // weight loads fetch anyway (one shared address for every lane of the
+    // grid would queue them all on one L2 channel).
+    auto issue_tile = [&](const TileMat &t_, Epi &e_, typename Fmt::W (&w_)[R]) {
+        // bias and residual first: waiting for them then waits for no weight row
+        const int orow = min(t_.row0 + o_slot + S * o_r, t_.n_out - 1);
+        const float *wf = reinterpret_cast<const float *>(t_.w + (size_t)min(t_.row0 + slot, t_.n_out - 1) * a.row_bytes);
+        e_.b = *(t_.bias != nullptr ? t_.bias + orow : wf);
+        if constexpr (kRes) e_.r = *(t_.resid != nullptr ? t_.resid + (size_t)o_t * t_.n_out + orow : wf);
+        else e_.r = 0.0f;
         const WSrc src{t_.w, a.row_bytes};
 #pragma unroll
         for (int r = 0; r < R; ++r) Fmt::load_w(src, min(t_.row0 + slot + S * r, t_.n_out - 1), u, w_[r]);
     };
-    auto load_tile = [&](int wt_, TileMat &t_, float &bias_, typename Fmt::W (&w_)[R]) {
+    auto load_tile = [&](int wt_, TileMat &t_, Epi &e_, typename Fmt::W (&w_)[R]) {
         t_ = locate(a, min(wt_ * RG + rg, a.ntiles - 1), rows_per_tile);
-        issue_tile(t_, bias_, w_);
+        issue_tile(t_, e_, w_);
     };
-    auto bias_of = [&](const TileMat &t_, float raw) { return t_.bias != nullptr ? raw : 0.0f; };
+    auto bias_of = [&](const TileMat &t_, Epi raw) {
+        return Epi{t_.bias != nullptr ? raw.b : 0.0f, kRes && t_.resid != nullptr ? raw.r : 0.0f};
+    };
 
     // 1. the activation's first staging round, then the first tile's
     //    weights: issued in this order, the activation does not wait behind
     //    the tile (loads of one wave return in order)
-    float xs0[16];
-    float4 v0;
+    float xs0[16], ys0[16];
+    float4 v0, y0;
     if constexpr (STAGE) {
-        if constexpr (kQ8K) stage_q8_k_load<NW * 64>(a, 0, xs0);
-        else v0 = stage_q8_0_load<NW * 64>(a, 0);
+        if constexpr (kQ8K) {
+            stage_q8_k_load<NW * 64>(a, 0, xs0);
+            stage_pro_load16<PRO & 3, NW * 64>(a, 0, ys0);
+        } else {
+            v0 = stage_q8_0_load<NW * 64>(a, 0);
+            y0 = stage_pro_load4<PRO & 3, NW * 64>(a, 0);
+        }
     }
     int wt = blockIdx.x;
     TileMat tm;
-    float bias;
+    Epi bias;
     typename Fmt::W wa[R];
     load_tile(wt, tm, bias, wa);
     __builtin_amdgcn_sched_barrier(0);  // every load issued before the staging arithmetic
@@ -340,8 +453,8 @@ gemv_fused_kernel(FusedArgs a) {
     //    lane in registers instead repeats it in every wave and measured
     //    slower)
     if constexpr (STAGE) {
-        if constexpr (kQ8K) stage_q8_k<NW * 64>(a, xs0, lq, ld, lbs);
-        else stage_q8_0<NW * 64>(a, v0, lq, ld);
+        if constexpr (kQ8K) stage_q8_k<NW * 64, PRO & 3>(a, xs0, ys0, lq, ld, lbs);
+        else stage_q8_0<NW * 64, PRO & 3>(a, v0, y0, lq, ld);
         __syncthreads();
     }
     const ActLds act{lq, ld, lbs, a.K, a.nblk};
@@ -374,7 +487,7 @@ gemv_fused_kernel(FusedArgs a) {
         for (int k = 0; k < V; ++k) vals[k] = unit_live ? vals[k] : 0.0f;
     };
     // lane reduction, K-split sum and store of one tile
-    auto finish = [&](float (&vals)[V], int iter, bool have, const TileMat &ct, float cbias) {
+    auto finish = [&](float (&vals)[V], int iter, bool have, const TileMat &ct, Epi ce) {
         group_reduce<V>(vals, G, lane);
         float result = vals[0];
         if (KS > 1) {
@@ -397,7 +510,10 @@ gemv_fused_kernel(FusedArgs a) {
         const bool live = have && o_live && row < ct.n_out;
         const __amdgpu_buffer_rsrc_t rs =
             __builtin_amdgcn_make_buffer_rsrc(ct.out, (short)0, a.m * ct.n_out * 4, kRawBufferWord3);
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(cbias + result), rs,
+        // out = residual + (bias + dot): the reference's projection, then its
+        // residual add (src/native.c:2571-2580)
+        const float v = ce.b + result;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(kRes && ct.resid != nullptr ? ce.r + v : v), rs,
                                               live ? (o_t * ct.n_out + row) * 4 : kDeadOffset, 0, 0);
     };
 
@@ -413,11 +529,12 @@ gemv_fused_kernel(FusedArgs a) {
     //    that no path's wait for a tile's last weights includes the store.
     __builtin_amdgcn_raw_buffer_store_b32(0u, __builtin_amdgcn_make_buffer_rsrc(tm.out, (short)0, 0, kRawBufferWord3),
                                           0, 0, 0);
-    auto resolve_bias = [&](const TileMat &t_, float raw) {
-        float b = bias_of(t_, raw);
-        asm volatile("" : "+v"(b));  // the select stays here, not at its use
+    auto resolve_bias = [&](const TileMat &t_, Epi raw) {
+        Epi e = bias_of(t_, raw);
+        asm volatile("" : "+v"(e.b));  // the selects stay here, not at their use
+        if constexpr (kRes) asm volatile("" : "+v"(e.r));
         __builtin_amdgcn_sched_barrier(0);
-        return b;
+        return e;
     };
     if constexpr (LOOP == 1) {
         // Two register buffers in turn: the next tile's loads are issued
@@ -426,10 +543,10 @@ gemv_fused_kernel(FusedArgs a) {
         typename Fmt::W wb[R];
         for (int iter = 0;; iter += 2) {
             TileMat tmb;
-            float biasb;
+            Epi biasb;
             float vals[V];
             const int wt1 = wt + (int)gridDim.x;
-            const float ba = resolve_bias(tm, bias);
+            const Epi ba = resolve_bias(tm, bias);
             if (wt1 >= wg_tiles) {  // uniform over the workgroup
                 dot(wa, vals);
                 finish(vals, iter, wt * RG + rg < a.ntiles, tm, ba);
@@ -439,7 +556,7 @@ gemv_fused_kernel(FusedArgs a) {
             dot(wa, vals);
             finish(vals, iter, wt * RG + rg < a.ntiles, tm, ba);
             const int wt2 = wt1 + (int)gridDim.x;
-            const float bb = resolve_bias(tmb, biasb);
+            const Epi bb = resolve_bias(tmb, biasb);
             if (wt2 >= wg_tiles) {
                 dot(wb, vals);
                 finish(vals, iter + 1, wt1 * RG + rg < a.ntiles, tmb, bb);
@@ -461,7 +578,7 @@ gemv_fused_kernel(FusedArgs a) {
         int cur = (int)blockIdx.x * RG + rg;
         for (int iter = 0;; ++iter) {
             const bool have = cur < T;
-            const float cbias = resolve_bias(tm, bias);
+            const Epi cbias = resolve_bias(tm, bias);
             float vals[V];
             dot(wa, vals);
             const TileMat ct = tm;
@@ -483,7 +600,7 @@ gemv_fused_kernel(FusedArgs a) {
             const bool have = wt * RG + rg < a.ntiles;
             // resolved before the next tile's loads go out, so the store
             // below depends on no outstanding load
-            const float cbias = resolve_bias(tm, bias);
+            const Epi cbias = resolve_bias(tm, bias);
             float vals[V];
             dot(wa, vals);
             const TileMat ct = tm;
@@ -520,7 +637,7 @@ static int env_int(const char *name, int dflt) {
 }
 
 // per_cu_cap > 0: at most that many workgroups per CU in the grid.
-template <class Fmt, int M, int R, int NW, bool STAGE, int LOOP>
+template <class Fmt, int M, int R, int NW, bool STAGE, int LOOP, int PRO = 0>
 static hipError_t launch_fused_fmt(FusedArgs a, hipStream_t st, int per_cu_cap = 0) {
     const int S = 64 / a.G, RG = NW / a.KS;
     const int rows_per_tile = S * R;
@@ -541,7 +658,7 @@ static hipError_t launch_fused_fmt(FusedArgs a, hipStream_t st, int per_cu_cap =
     static int per_cu = 1;
     if (L.total() != cached_lds) {
         int v = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_fused_kernel<Fmt, M, R, NW, STAGE, LOOP>, NW * 64,
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_fused_kernel<Fmt, M, R, NW, STAGE, LOOP, PRO>, NW * 64,
                                                          L.total()) != hipSuccess ||
             v < 1)
             v = 1;
@@ -556,7 +673,7 @@ static hipError_t launch_fused_fmt(FusedArgs a, hipStream_t st, int per_cu_cap =
     // workgroup-tile schedule: equal tile counts per workgroup; balanced
     // per-wave schedule: every resident slot (equal work per CU)
     const int grid = LOOP == 2 ? (wg_tiles < resident ? wg_tiles : resident) : (wg_tiles + rounds - 1) / rounds;
-    hipLaunchKernelGGL((gemv_fused_kernel<Fmt, M, R, NW, STAGE, LOOP>), dim3(grid), dim3(NW * 64), L.total(), st, a);
+    hipLaunchKernelGGL((gemv_fused_kernel<Fmt, M, R, NW, STAGE, LOOP, PRO>), dim3(grid), dim3(NW * 64), L.total(), st, a);
     return hipGetLastError();
 }
 
@@ -600,6 +717,52 @@ static hipError_t launch_fused_m(FusedArgs a, int r1, int loop, hipStream_t st) 
     }
 }
 
+// Rows per slot of the 16-wave row-split launch: the largest R whose
+// workgroup tiles fill the grid best (Q6_K at most 2); r_env overrides.
+template <class Fmt>
+static int pick_r16(const FusedArgs &a, int r_env) {
+    constexpr int kRMax = sizeof(typename Fmt::W) > 48 ? 2 : 4;
+    const int rg = 16 / a.KS, cus = device_cus();
+    auto fill = [&](int r) {
+        int tiles = 0;
+        for (int z = 0; z < a.nmat; ++z) tiles += (a.n_out[z] + r - 1) / r;
+        const int wg_tiles = (tiles + rg - 1) / rg, rounds = (wg_tiles + cus - 1) / cus;
+        return (double)wg_tiles / (double)(rounds * cus);
+    };
+    int r16 = kRMax;
+    if (kRMax == 4 && fill(2) > fill(r16) + 1e-9) r16 = 2;
+    if (fill(1) > fill(r16) + 1e-9) r16 = 1;
+    if (r_env == 1 || r_env == 2 || (r_env == 4 && kRMax == 4)) r16 = r_env;
+    return r16;
+}
+
+// One token with a staging prologue (PRO 1: RMSNorm, 2: SiLU-mul): the
+// default one-token schedules of launch_fused_nw, instantiated with it.
+template <class Fmt, int PRO>
+static hipError_t launch_fused_pro(FusedArgs a, hipStream_t st) {
+    if (a.m != 1 || a.KS > 4) return hipErrorInvalidValue;
+    if (a.KS > 1) {
+        if constexpr (Fmt::kUnitsPerBlock == 4) {
+            const int r16 = pick_r16<Fmt>(a, 0);
+            if (r16 == 1) return launch_fused_fmt<Fmt, 1, 1, 16, true, 0, PRO>(a, st);
+            if (r16 == 2) return launch_fused_fmt<Fmt, 1, 2, 16, true, 0, PRO>(a, st);
+            if constexpr (sizeof(typename Fmt::W) <= 48) return launch_fused_fmt<Fmt, 1, 4, 16, true, 0, PRO>(a, st);
+            return hipErrorInvalidValue;
+        } else {
+            return launch_fused_fmt<Fmt, 1, 4, 8, true, 0, PRO>(a, st);
+        }
+    }
+    int rows = 0;
+    for (int z = 0; z < a.nmat; ++z) rows += a.n_out[z];
+    const int r1 = rows <= 4096 ? 2 : 4;
+    const int rows_per_tile = (64 / a.G) * r1;
+    int tiles = 0;
+    for (int z = 0; z < a.nmat; ++z) tiles += (a.n_out[z] + rows_per_tile - 1) / rows_per_tile;
+    if (tiles > 2 * device_cus() * 8) return launch_fused_fmt<Fmt, 1, 2, 8, true, 1, PRO>(a, st, 1);
+    return r1 == 2 ? launch_fused_fmt<Fmt, 1, 2, 8, true, 0, PRO>(a, st)
+                   : launch_fused_fmt<Fmt, 1, 4, 8, true, 0, PRO>(a, st);
+}
+
 // Tile shape: 8 waves per workgroup; R = 4 rows per slot at m = 1 unless
 // the launch is short and unsplit (<= 4096 rows), where R = 2 keeps more
 // workgroups in flight.  (Measured on [1024..28672 x 4096] and
@@ -628,22 +791,11 @@ static hipError_t launch_fused_nw(FusedArgs a, bool stage, hipStream_t st) {
     // two rows per slot: four exceed the 128 registers of such a workgroup.
     if constexpr (Fmt::kUnitsPerBlock == 4) {  // Q8_K activations (Q4_K, Q6_K rows)
         if (stage && a.m == 1 && a.KS > 1) {
-            constexpr int kRMax = sizeof(typename Fmt::W) > 48 ? 2 : 4;
-            const int rg = 16 / a.KS, cus = device_cus();
-            auto fill = [&](int r) {
-                int tiles = 0;
-                for (int z = 0; z < a.nmat; ++z) tiles += (a.n_out[z] + r - 1) / r;
-                const int wg_tiles = (tiles + rg - 1) / rg, rounds = (wg_tiles + cus - 1) / cus;
-                return (double)wg_tiles / (double)(rounds * cus);
-            };
             static const int r_env = env_int("EXQ_FUSED_NW16_R", 0);  // tuning override: rows per slot
-            int r16 = kRMax;
-            if (kRMax == 4 && fill(2) > fill(r16) + 1e-9) r16 = 2;
-            if (fill(1) > fill(r16) + 1e-9) r16 = 1;
-            if (r_env == 1 || r_env == 2 || (r_env == 4 && kRMax == 4)) r16 = r_env;
+            const int r16 = pick_r16<Fmt>(a, r_env);
             if (r16 == 1) return launch_fused_fmt<Fmt, 1, 1, 16, true, 0>(a, st);
             if (r16 == 2) return launch_fused_fmt<Fmt, 1, 2, 16, true, 0>(a, st);
-            if constexpr (kRMax == 4) return launch_fused_fmt<Fmt, 1, 4, 16, true, 0>(a, st);
+            if constexpr (sizeof(typename Fmt::W) <= 48) return launch_fused_fmt<Fmt, 1, 4, 16, true, 0>(a, st);
         }
     }
     if (stage)
@@ -741,9 +893,34 @@ hipError_t launch_gemv_fused_f32(int type, const uint8_t *w, int n_out, const fl
 // nmat matrices of the same type and K, all applied to the same m tokens:
 // f32 x quantized inside the kernel (x != null), or codes already quantized
 // in the reference block layout (xq, token stride xq_stride).
-hipError_t launch_gemv_fused(int type, int nmat, const uint8_t *const *w, const int *n_out,
-                             const float *const *bias, float *const *out, size_t row_bytes, int K, int m,
-                             const float *x, const uint8_t *xq, size_t xq_stride, hipStream_t st) {
+namespace {
+// pro: prologue (0, 1, 2) | 4 for a residual epilogue.  The instantiated
+// one-token combinations are the layer's: RMSNorm (q/k/v, gate/up),
+// residual (o), SiLU-mul with or without residual (down).
+template <class Fmt>
+hipError_t dispatch_fused(const FusedArgs &a, bool stage, int pro, hipStream_t st) {
+    switch (pro) {
+        case 0: return launch_fused_nw<Fmt>(a, stage, st);
+        case 1: return launch_fused_pro<Fmt, 1>(a, st);
+        case 2: return launch_fused_pro<Fmt, 2>(a, st);
+        case 4: return launch_fused_pro<Fmt, 4>(a, st);
+        case 6: return launch_fused_pro<Fmt, 6>(a, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+}  // namespace
+
+// nmat matrices of the same type and K, all applied to the same m tokens:
+// f32 x quantized inside the kernel (x != null), or codes already quantized
+// in the reference block layout (xq, token stride xq_stride).  With a
+// prologue (pro 1: x is RMSNorm-ed with nw and eps; pro 2: x is silu(x) * x2)
+// or a residual (resid non-null: added to each output after its bias) x is
+// staged and m must be 1 (gemv_fused_pro_supported); RMSNorm with a residual
+// is not a layer's combination and is not instantiated.
+hipError_t launch_gemv_fused_layer(int type, int nmat, const uint8_t *const *w, const int *n_out,
+                                   const float *const *bias, const float *const *resid, float *const *out,
+                                   size_t row_bytes, int K, int m, const float *x, const float *x2, const float *nw,
+                                   float eps, int pro, const uint8_t *xq, size_t xq_stride, hipStream_t st) {
     if (nmat < 1 || nmat > kFusedMaxMats) return hipErrorInvalidValue;
     FusedArgs a{};
     a.nmat = nmat;
@@ -751,6 +928,7 @@ hipError_t launch_gemv_fused(int type, int nmat, const uint8_t *const *w, const 
         a.w[z] = w[z];
         a.n_out[z] = n_out[z];
         a.bias[z] = bias != nullptr ? bias[z] : nullptr;
+        a.resid[z] = resid != nullptr ? resid[z] : nullptr;
         a.out[z] = out[z];
     }
     a.row_bytes = row_bytes;
@@ -759,14 +937,44 @@ hipError_t launch_gemv_fused(int type, int nmat, const uint8_t *const *w, const 
     a.x = x;
     a.xq = xq;
     a.xq_stride = xq_stride;
+    a.x2 = x2;
+    a.nw = nw;
+    a.eps = eps;
     if ((x == nullptr) == (xq == nullptr)) return hipErrorInvalidValue;
+    bool any_resid = false;
+    for (int z = 0; z < nmat; ++z) any_resid = any_resid || a.resid[z] != nullptr;
+    const int code = pro | (any_resid ? 4 : 0);
+    if (code != 0 && (x == nullptr || m != 1 || code == 5 || (pro == 1 && nw == nullptr) ||
+                      (pro == 2 && x2 == nullptr)))
+        return hipErrorInvalidValue;
     a.nblk = type == kTypeQ8_0 ? K / kQK8_0 : K / kQKK;
     a.U = type == kTypeQ8_0 ? a.nblk : a.nblk * 4;
     if (!pick_fused_shape(a.U, a.G, a.KS)) return hipErrorInvalidValue;
     switch (type) {
-        case kTypeQ8_0: return launch_fused_nw<FmtQ80>(a, x != nullptr, st);
-        case kTypeQ4_K: return launch_fused_nw<FmtQ4K>(a, x != nullptr, st);
-        case kTypeQ6_K: return launch_fused_nw<FmtQ6K>(a, x != nullptr, st);
+        case kTypeQ8_0: return dispatch_fused<FmtQ80>(a, x != nullptr, code, st);
+        case kTypeQ4_K: return dispatch_fused<FmtQ4K>(a, x != nullptr, code, st);
+        case kTypeQ6_K: return dispatch_fused<FmtQ6K>(a, x != nullptr, code, st);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_gemv_fused(int type, int nmat, const uint8_t *const *w, const int *n_out,
+                             const float *const *bias, float *const *out, size_t row_bytes, int K, int m,
+                             const float *x, const uint8_t *xq, size_t xq_stride, hipStream_t st) {
+    return launch_gemv_fused_layer(type, nmat, w, n_out, bias, nullptr, out, row_bytes, K, m, x, nullptr, nullptr,
+                                   0.0f, 0, xq, xq_stride, st);
+}
+
+// True when the fused kernel runs (type, K) for one token with staging
+// prologue pro (1 RMSNorm, 2 SiLU-mul): the RMSNorm needs the whole row in
+// one staging round (8-wave workgroups: 8192 elements for the K-quants, 2048
+// for Q8_0; the 16-wave row-split ones: 16384).
+bool gemv_fused_pro_supported(int type, int K, int pro) {
+    if (!gemv_fused_supported(type, K, 1)) return false;
+    const int U = type == kTypeQ8_0 ? K / kQK8_0 : (K / kQKK) * 4;
+    int G = 64, KS = 1;
+    if (!pick_fused_shape(U, G, KS)) return false;
+    if (pro != 1) return true;
+    if (type == kTypeQ8_0) return K <= 8 * 64 * 4;
+    return K <= (KS > 1 ? 16 * 64 * 16 : 8 * 64 * 16);
 }

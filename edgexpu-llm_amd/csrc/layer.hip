@@ -39,22 +39,15 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
         const double v = (double)xr[i];
         s += v * v;  // a float square is exact in double
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    s = wave_sum_f64(s);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
     __syncthreads();
     const double ss = (part[0] + part[1]) + (part[2] + part[3]);
-    const float mean = (float)(ss / (double)n);
-    const float scale = 1.0f / sqrtf(mean + eps);
+    const float scale = rms_scale(ss, n, eps);
     for (int i = threadIdx.x; i < n; i += 256) {
         const float v = xr[i] * scale;
         orow[i] = v * w[i];
     }
-}
-
-__device__ __forceinline__ float silu1(float v) {
-    const float e = (float)exp(-(double)v);
-    return v / (1.0f + e);
 }
 
 // kind 0: silu(a); 1: a * b; 2: a + b; 3: silu(a) * b.
@@ -64,10 +57,10 @@ __global__ __launch_bounds__(256) void elementwise_kernel(const float *__restric
     if (i >= n) return;
     const float va = a[i];
     float r;
-    if (kind == 0) r = silu1(va);
+    if (kind == 0) r = silu_f32(va);
     else if (kind == 1) r = va * b[i];
     else if (kind == 2) r = va + b[i];
-    else r = silu1(va) * b[i];
+    else r = silu_f32(va) * b[i];
     out[i] = r;
 }
 

@@ -36,6 +36,11 @@ size_t gemm_f16_workspace(int m, int n_out, int K);
 bool gemm_q8_supported(int type, int n_out, int K, int m);
 bool gemv_fused_supported(int type, int K, int m);
 bool gemv_fused_f32_supported(int type, int K);
+bool gemv_fused_pro_supported(int type, int K, int pro);
+hipError_t launch_gemv_fused_layer(int type, int nmat, const uint8_t *const *w, const int *n_out,
+                                   const float *const *bias, const float *const *resid, float *const *out,
+                                   size_t row_bytes, int K, int m, const float *x, const float *x2, const float *nw,
+                                   float eps, int pro, const uint8_t *xq, size_t xq_stride, hipStream_t st);
 hipError_t launch_gemv_fused_f32(int type, const uint8_t *w, int n_out, const float *bias, float *out,
                                  size_t row_bytes, int K, const float *xf, const float *xs, hipStream_t st);
 hipError_t launch_gemv_fused(int type, int nmat, const uint8_t *const *w, const int *n_out, const float *const *bias,
@@ -65,6 +70,8 @@ struct State {
     void *dbuf = nullptr;  // device staging for host-pointer calls
     void *f16ws = nullptr;  // fp16 prefill GEMM workspace
     size_t f16ws_cap = 0;
+    void *lws = nullptr;    // layer entry: prologue activation and pre-residual outputs
+    size_t lws_cap = 0;
     int prefill_mode = 0;   // EDGEXPU_HIP_PREFILL_EXACT_INT8 / _F16
     size_t dbuf_cap = 0;
     int err = 0;
@@ -168,6 +175,22 @@ void *devbuf(size_t bytes) {
 
 // Workspace of the fp16 prefill GEMM (fp16 activations, split-K partials),
 // grown on demand.
+// The layer entry's own workspace (separate from workspace(), which the
+// projection paths it calls may grow).
+void *layer_ws(size_t bytes) {
+    if (bytes <= g.lws_cap) return g.lws;
+    if (g.lws != nullptr) {
+        if (!hip_ok(hipDeviceSynchronize(), "layer workspace sync")) return nullptr;
+        (void)hipFree(g.lws);
+        g.lws = nullptr;
+        g.lws_cap = 0;
+    }
+    size_t cap = align_up(bytes, (size_t)1 << 20);
+    if (!hip_ok(hipMalloc(&g.lws, cap), "hipMalloc layer workspace")) return nullptr;
+    g.lws_cap = cap;
+    return g.lws;
+}
+
 void *f16ws(size_t bytes) {
     if (bytes <= g.f16ws_cap) return g.f16ws;
     if (g.f16ws != nullptr) {
@@ -315,6 +338,7 @@ void edgexpu_hip_shutdown(void) {
     if (g.ws) (void)hipFree(g.ws);
     if (g.dbuf) (void)hipFree(g.dbuf);
     if (g.f16ws) (void)hipFree(g.f16ws);
+    if (g.lws) (void)hipFree(g.lws);
     (void)hipStreamDestroy(g.stream);
     const int err = g.err;
     char msg[sizeof(g.msg)];
@@ -468,6 +492,80 @@ int edgexpu_hip_linear_quant_group_dev(int nmat, float *const *out, const float 
         return 0;
     }
     return run_linear_group(type, nmat, w, n_out, bias, out, x, m, n_in, pick_stream(stream)) ? 1 : 0;
+}
+
+int edgexpu_hip_layer_linear_dev(int nmat, float *const *out, const float *x, const float *x2,
+                                 const float *norm_weight, float eps, const void *const *w, uint32_t type,
+                                 const float *const *bias, const float *const *residual, const int *n_out, int m,
+                                 int n_in, void *stream) {
+    if (!ensure_init()) return 0;
+    if (nmat < 1 || nmat > 4 || out == nullptr || w == nullptr || n_out == nullptr) {
+        set_error(-2, "layer_linear: nmat must be 1..4 with out, w and n_out arrays");
+        return 0;
+    }
+    if (x2 != nullptr && norm_weight != nullptr) {
+        set_error(-2, "layer_linear: give norm_weight (RMSNorm) or x2 (SiLU-mul), not both");
+        return 0;
+    }
+    for (int z = 0; z < nmat; ++z) {
+        if (!check_linear_args(out[z], x, w[z], type, m, n_out[z], n_in, "layer_linear")) return 0;
+    }
+    if (!aligned16(x) || (x2 != nullptr && !aligned16(x2)) || (norm_weight != nullptr && !aligned16(norm_weight))) {
+        set_error(-2, "layer_linear: x, x2 and norm_weight must be 16-byte aligned");
+        return 0;
+    }
+    const int pro = norm_weight != nullptr ? 1 : (x2 != nullptr ? 2 : 0);
+    hipStream_t st = pick_stream(stream);
+    const size_t rb = edgexpu_hip_row_bytes(type, n_in);
+    bool any_resid = false;
+    size_t res_floats = 0;
+    for (int z = 0; z < nmat; ++z)
+        if (residual != nullptr && residual[z] != nullptr) {
+            any_resid = true;
+            res_floats += align_up((size_t)m * n_out[z], 64);
+        }
+    // one launch: the prologue in the GEMV's staging, the residual in its
+    // store (one token; without either, any token count the kernel covers)
+    const bool plain = pro == 0 && !any_resid;
+    const bool one_token = m == 1 && !(pro == 1 && any_resid) && gemv_fused_pro_supported((int)type, n_in, pro);
+    if (stage_in_kernel(type, n_in, m) && (plain || one_token))
+        return hip_ok(launch_gemv_fused_layer((int)type, nmat, (const uint8_t *const *)w, n_out, bias, residual, out,
+                                              rb, n_in, m, x, x2, norm_weight, eps, pro, nullptr, 0, st),
+                      "layer_linear fused")
+                   ? 1
+                   : 0;
+    // otherwise the same arithmetic in steps: prologue kernel, projection,
+    // residual add (the projection writes to the workspace first, so out may
+    // be the residual)
+    const size_t act_floats = pro != 0 ? align_up((size_t)m * n_in, 64) : 0;
+    float *base = (float *)layer_ws((act_floats + res_floats) * sizeof(float) + 256);
+    if (base == nullptr) return 0;
+    const float *act = x;
+    if (pro == 1) {
+        if (!hip_ok(launch_rmsnorm(x, norm_weight, base, m, n_in, eps, st), "layer_linear rmsnorm")) return 0;
+        act = base;
+    } else if (pro == 2) {
+        if (!hip_ok(launch_elementwise(x, x2, base, (long long)m * n_in, 3, st), "layer_linear silu_mul")) return 0;
+        act = base;
+    }
+    float *outs[4];
+    float *tmp = base + act_floats;
+    for (int z = 0; z < nmat; ++z) {
+        if (residual != nullptr && residual[z] != nullptr) {
+            outs[z] = tmp;
+            tmp += align_up((size_t)m * n_out[z], 64);
+        } else {
+            outs[z] = out[z];
+        }
+    }
+    if (!run_linear_group(type, nmat, w, n_out, bias, outs, act, m, n_in, st)) return 0;
+    if (any_resid)
+        for (int z = 0; z < nmat; ++z)
+            if (residual[z] != nullptr &&
+                !hip_ok(launch_elementwise(residual[z], outs[z], out[z], (long long)m * n_out[z], 2, st),
+                        "layer_linear residual"))
+                return 0;
+    return 1;
 }
 
 int edgexpu_hip_gemv_q8_dev(float *out, const uint8_t *xq, const void *w, uint32_t type, const float *bias, int m,

@@ -97,6 +97,9 @@ class HipLib:
         self.mul_dev = _sig(L, "edgexpu_hip_mul_dev", C.c_int, [_vp, _vp, _vp, C.c_longlong, _vp])
         self.add_dev = _sig(L, "edgexpu_hip_add_dev", C.c_int, [_vp, _vp, _vp, C.c_longlong, _vp])
         self.silu_mul_dev = _sig(L, "edgexpu_hip_silu_mul_dev", C.c_int, [_vp, _vp, _vp, C.c_longlong, _vp])
+        self.layer_linear_dev = _sig(L, "edgexpu_hip_layer_linear_dev", C.c_int,
+                                     [C.c_int, _vp, _vp, _vp, _vp, C.c_float, _vp, C.c_uint32, _vp, _vp, _vp,
+                                      C.c_int, C.c_int, _vp])
 
     def last_error(self) -> tuple[int, str]:
         buf = C.create_string_buffer(512)
@@ -264,3 +267,23 @@ def add(a, b, out=None):
 
 def silu_mul(gate, up, out=None):
     return _ew("silu_mul_dev", "silu_mul", gate, up, out=out)
+
+
+def layer_linear(ws, qtype: int, x, n_outs, n_in: int, x2=None, norm_weight=None, eps: float = 1e-5,
+                 biases=None, residuals=None, outs=None):
+    """outs[z] = residuals[z] + (biases[z] + W[z] . q8(act)), act = rmsnorm(x)
+    (norm_weight), silu(x) * x2 (x2) or x (edgexpu_hip_layer_linear_dev)."""
+    import torch
+
+    m = x.shape[0]
+    k = len(ws)
+    if outs is None:
+        outs = [torch.empty((m, n), dtype=torch.float32, device=x.device) for n in n_outs]
+    arr = C.c_void_p * 4
+    b = None if biases is None else arr(*[_ptr(t) for t in biases])
+    r = None if residuals is None else arr(*[_ptr(t) for t in residuals])
+    L = hip()
+    L.check(L.layer_linear_dev(k, arr(*[o.data_ptr() for o in outs]), x.data_ptr(), _ptr(x2), _ptr(norm_weight),
+                               eps, arr(*[t.data_ptr() for t in ws]), qtype, b, r, (C.c_int * 4)(*n_outs), m, n_in,
+                               _stream()), "layer_linear")
+    return outs

@@ -173,6 +173,30 @@ int edgexpu_hip_mul_dev(float *out, const float *a, const float *b, long long n,
 int edgexpu_hip_add_dev(float *out, const float *a, const float *b, long long n, void *stream);
 int edgexpu_hip_silu_mul_dev(float *out, const float *gate, const float *up, long long n, void *stream);
 
+/* A decode layer's projection with the ops around it, on device-resident
+ * activations (src/native.c:2529-2580: rmsnorm -> q/k/v, o -> add,
+ * rmsnorm -> gate/up, silu * up -> down -> add):
+ *   act    = rmsnorm(x; norm_weight, eps)  when norm_weight != NULL
+ *          = silu(x) * x2                  when x2 != NULL (not both)
+ *          = x                             otherwise
+ *   out[z] = residual[z] + (bias[z] + W[z] . q8(act))
+ * for nmat <= 4 matrices of one type and n_in that share the input (q/k/v,
+ * gate/up), with residual (or any residual[z]) and bias optional, as
+ * edgexpu_cpu_rmsnorm / edgexpu_cpu_silu + edgexpu_cpu_mul, then
+ * edgexpu_cpu_linear_quant_batch (include/edgexpu/cpu_kernel.h:60-80), then
+ * edgexpu_cpu_add compute it: the same result as those entry points of this
+ * library in sequence (the layer ops above, edgexpu_hip_linear_quant_group_dev).
+ * One token with the prologue, or no prologue, runs as one launch (the
+ * prologue in the GEMV's activation staging, the residual in its store);
+ * other shapes run the same steps as separate launches.  out[z] may be
+ * residual[z] (an in-place residual update); out must not overlap x or x2.
+ * x, x2, norm_weight 16-byte aligned.  Returns 1 on success, 0 on bad
+ * arguments or a HIP error. */
+int edgexpu_hip_layer_linear_dev(int nmat, float *const *out, const float *x, const float *x2,
+                                 const float *norm_weight, float eps, const void *const *w, uint32_t type,
+                                 const float *const *bias, const float *const *residual, const int *n_out, int m,
+                                 int n_in, void *stream);
+
 /* ---- host-pointer entry points (synchronous: inputs copied in, outputs
  * copied out before return; the PCIe copies are part of the call) ---- */
 

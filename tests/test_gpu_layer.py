@@ -119,3 +119,129 @@ def test_silu_mul_matches_silu_then_mul(hipdev, ora, n):
     assert np.array_equal(bits(fused), bits(two))
     want = ora.mul(ora.silu(g), u)
     assert np.all(_ulp_diff(fused, want) <= 3.0)
+
+
+# ------------------------------------------------------------ layer_linear
+
+from edgexpu_amd import synth  # noqa: E402
+
+TOL = 1e-5
+
+
+def _cond(ora, qt, w, x, n_out, n_in):
+    """Per-output conditioning scale sum |w x| (float64) of the f32 product."""
+    deq = ora.dequantize(w.reshape(-1), qt, n_out * n_in).reshape(n_out, n_in).astype(np.float64)
+    return np.abs(x.astype(np.float64)) @ np.abs(deq).T
+
+
+def _separate(ws, qt, x, n_outs, n_in, x2=None, nw=None, eps=1e-5, biases=None, residuals=None):
+    """The same layer step as separate device calls: layer op, grouped
+    projection, residual add."""
+    act = x
+    if nw is not None:
+        act = E.rmsnorm(x, nw, eps)
+    elif x2 is not None:
+        act = E.silu_mul(x, x2)
+    outs = E.linear_quant_group(ws, qt, act, n_outs, n_in, biases=biases)
+    if residuals is not None:
+        outs = [o if r is None else E.add(r, o) for o, r in zip(outs, residuals)]
+    return outs
+
+
+@pytest.mark.parametrize("qt,n_in,n_outs", [(12, 4096, (4096, 1024, 1024)), (12, 4096, (14336, 14336)),
+                                            (8, 576, (576, 192, 192)), (14, 2560, (1000,)),
+                                            (12, 14336, (4096,)), (12, 8192, (515, 33))])
+def test_layer_linear_rmsnorm(hipdev, ora, qt, n_in, n_outs):
+    """act = rmsnorm(x) in the GEMV's staging (one token): equal to the
+    separate device rmsnorm + projection bit for bit, and within the bound of
+    the oracle's rmsnorm + linear_quant_batch."""
+    rng = np.random.default_rng(qt + n_in + len(n_outs))
+    wts = [synth.np_weights(qt, n, n_in, rng) for n in n_outs]
+    x = (rng.normal(0, 1, (1, n_in)) * 3).astype(np.float32)
+    nw = rng.normal(1, 0.2, n_in).astype(np.float32)
+    biases = [rng.normal(0, 0.5, n).astype(np.float32) for n in n_outs]
+    ws = [dev(w) for w in wts]
+    got = E.layer_linear(ws, qt, dev(x), n_outs, n_in, norm_weight=dev(nw), eps=1e-5,
+                         biases=[dev(b) for b in biases])
+    sep = _separate(ws, qt, dev(x), n_outs, n_in, nw=dev(nw), biases=[dev(b) for b in biases])
+    act = ora.rmsnorm(x, nw, 1e-5)
+    for z, n in enumerate(n_outs):
+        g = got[z].cpu().numpy()
+        assert np.array_equal(bits(g), bits(sep[z].cpu().numpy())), f"matrix {z}"
+        want = ora.linear_quant_batch(act, wts[z], qt, biases[z], 1, n, n_in)
+        S = _cond(ora, qt, wts[z], act, n, n_in) + np.abs(biases[z])[None, :]
+        assert np.all(np.abs(g - want) <= TOL * S), f"matrix {z}"
+
+
+@pytest.mark.parametrize("qt,n_in,n_out", [(12, 14336, 4096), (14, 9728, 2560), (8, 1536, 576), (12, 4096, 300)])
+def test_layer_linear_silu_mul_residual(hipdev, ora, qt, n_in, n_out):
+    """down: act = silu(gate) * up in the staging, out = residual + proj in
+    the store, written over the residual (in place)."""
+    rng = np.random.default_rng(qt * 7 + n_in)
+    w = synth.np_weights(qt, n_out, n_in, rng)
+    g = rng.normal(0, 2, (1, n_in)).astype(np.float32)
+    u = rng.normal(0, 2, (1, n_in)).astype(np.float32)
+    res = rng.normal(0, 4, (1, n_out)).astype(np.float32)
+    wd = dev(w)
+    sep = _separate([wd], qt, dev(g), (n_out,), n_in, x2=dev(u), residuals=[dev(res)])[0].cpu().numpy()
+    rt = dev(res)
+    E.layer_linear([wd], qt, dev(g), (n_out,), n_in, x2=dev(u), residuals=[rt], outs=[rt])
+    got = rt.cpu().numpy()
+    assert np.array_equal(bits(got), bits(sep))
+    act = ora.mul(ora.silu(g), u)
+    want = ora.add(res, ora.linear_quant_batch(act, w, qt, None, 1, n_out, n_in))
+    S = _cond(ora, qt, w, act, n_out, n_in) + np.abs(res)
+    # the device silu is within two ulp of the reference's (test above): a
+    # rare Q8 code one step apart moves an output by at most ~1e-5 of S
+    assert np.all(np.abs(got - want) <= 2 * TOL * S)
+
+
+def test_layer_linear_residual_only(hipdev, ora):
+    """o: out = residual + (bias + W x), no prologue; grouped with a matrix
+    that has no residual."""
+    qt, n_in, n_outs = 12, 4096, (4096, 1024)
+    rng = np.random.default_rng(99)
+    wts = [synth.np_weights(qt, n, n_in, rng) for n in n_outs]
+    x = rng.normal(0, 1, (1, n_in)).astype(np.float32)
+    res = rng.normal(0, 4, (1, n_outs[0])).astype(np.float32)
+    bias = [rng.normal(0, 0.5, n).astype(np.float32) for n in n_outs]
+    ws = [dev(w) for w in wts]
+    got = E.layer_linear(ws, qt, dev(x), n_outs, n_in, biases=[dev(b) for b in bias], residuals=[dev(res), None])
+    sep = _separate(ws, qt, dev(x), n_outs, n_in, biases=[dev(b) for b in bias], residuals=[dev(res), None])
+    for z in range(2):
+        assert np.array_equal(bits(got[z].cpu().numpy()), bits(sep[z].cpu().numpy()))
+
+
+@pytest.mark.parametrize("m", [2, 3, 70])
+def test_layer_linear_steps_beyond_one_token(hipdev, ora, m):
+    """More than one token: the separate-launch path (rmsnorm kernel,
+    projection, add), equal to the separate device calls bit for bit."""
+    qt, n_in, n_out = 12, 4096, 515
+    rng = np.random.default_rng(m)
+    w = synth.np_weights(qt, n_out, n_in, rng)
+    x = rng.normal(0, 1, (m, n_in)).astype(np.float32)
+    nw = rng.normal(1, 0.2, n_in).astype(np.float32)
+    res = rng.normal(0, 4, (m, n_out)).astype(np.float32)
+    wd = dev(w)
+    got = E.layer_linear([wd], qt, dev(x), (n_out,), n_in, norm_weight=dev(nw), residuals=[dev(res)])[0]
+    sep = _separate([wd], qt, dev(x), (n_out,), n_in, nw=dev(nw), residuals=[dev(res)])[0]
+    assert np.array_equal(bits(got.cpu().numpy()), bits(sep.cpu().numpy()))
+    act = ora.rmsnorm(x, nw, 1e-5)
+    want = ora.add(res, ora.linear_quant_batch(act, w, qt, None, m, n_out, n_in))
+    S = _cond(ora, qt, w, act, n_out, n_in) + np.abs(res)
+    assert np.all(np.abs(got.cpu().numpy() - want) <= TOL * S)
+
+
+def test_layer_linear_rejects_both_prologues(hipdev):
+    L = E.hip()
+    w = torch.zeros(2304 * 8, dtype=torch.uint8, device="cuda:0")
+    x = torch.zeros((1, 4096), device="cuda:0")
+    out = torch.empty((1, 8), device="cuda:0")
+    import ctypes as C
+    arr = C.c_void_p * 4
+    ok = L.layer_linear_dev(1, arr(out.data_ptr()), x.data_ptr(), x.data_ptr(), x.data_ptr(), 1e-5,
+                            arr(w.data_ptr()), 12, None, None, (C.c_int * 4)(8), 1, 4096, None)
+    assert ok == 0
+    code, msg = L.last_error()
+    L.clear_error()
+    assert "not both" in msg
