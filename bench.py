@@ -64,6 +64,8 @@ def parse():
     p.add_argument("--prefill-only", action="store_true", help="run only the prefill-GEMM leg (one JSON line)")
     p.add_argument("--launch-sweep", action="store_true",
                    help="time one Q4_K [rows x 4096] m=1 launch over row counts; fit fixed + marginal cost")
+    p.add_argument("--layer-step", action="store_true",
+                   help="time the decode step with the layer ops on device: fused layer entry vs separate launches")
     p.add_argument("--read-ceiling", action="store_true",
                    help="time a plain streaming read of each decode launch's weight bytes (one JSON line)")
     p.add_argument("--calibrate-copy", action="store_true",
@@ -163,6 +165,10 @@ def main():
     gen.manual_seed(args.seed)
     if args.launch_sweep:
         print(json.dumps(launch_sweep(L, E, synth, gen, dev)), flush=True)
+        return
+    if args.layer_step:
+        print(json.dumps(layer_step(L, E, synth, gen, dev, cfg, args.workload, m, args.steps, args.warmup)),
+              flush=True)
         return
     if args.read_ceiling:
         print(json.dumps(read_ceiling(E, cfg, args.workload, dev)), flush=True)
@@ -441,6 +447,121 @@ def launch_sweep(L, E, synth, gen, dev):
             "launches": {str(r): v for r, v in res.items()}, "empty_kernel_us": round(empty_us, 3),
             "fit": {"fixed_us": round(float(fixed), 3), "marginal_GBps": round(1e-3 / float(per_byte), 1),
                     "rows_fitted": list(big)}}
+
+
+def layer_step(L, E, synth, gen, dev, cfg, workload, m, steps, warmup):
+    """The decode step's matrix path with the ops between the projections on
+    device (src/native.c:2529-2580; attention itself is not on this path, so
+    o reads q):  rmsnorm -> q/k/v, o + residual, rmsnorm -> gate/up,
+    silu(gate) * up -> down + residual, then the logits.  Timed two ways,
+    HIP graphs of whole steps, HIP events: through
+    edgexpu_hip_layer_linear_dev (the layer ops inside the projection
+    launches: 4 launches per layer) and as separate launches (rmsnorm, the
+    grouped projection, add, silu_mul: 9 per layer)."""
+    import torch
+
+    projs = projections(cfg)
+    pinfo = {name: (t, n_out, n_in) for name, t, n_out, n_in, _ in projs}
+    one_copy = sum(cfg["layers"] * n_out * E.row_bytes(t, n_in) for _, t, n_out, n_in, _ in projs)
+    copies = max(1, -(-int(MIN_ROTATION_BYTES) // one_copy))
+    h = cfg["hidden"]
+    model = []
+    for _ in range(copies):
+        model.append([{name: synth.torch_weights_bulk(t, n_out, n_in, gen, dev) for name, t, n_out, n_in, _ in projs}
+                      for _ in range(cfg["layers"])])
+    wout = synth.torch_weights_bulk(cfg["logits_type"], cfg["vocab"], h, gen, dev)
+    norms = [(1 + 0.1 * torch.randn(h, generator=gen, device=dev), 1 + 0.1 * torch.randn(h, generator=gen, device=dev))
+             for _ in range(cfg["layers"])]
+    hidden = torch.randn((m, h), generator=gen, device=dev)
+    buf = {name: torch.empty((m, n_out), device=dev) for name, _, n_out, _, _ in projs}
+    normed = torch.empty((m, h), device=dev)
+    tmp = torch.empty((m, h), device=dev)
+    act = torch.empty((m, cfg["ffn"]), device=dev)
+    scores = torch.empty((m, cfg["vocab"]), device=dev)
+    best = torch.empty(m, dtype=torch.int32, device=dev)
+    arr = C.c_void_p * 4
+    eps = 1e-5
+
+    def ptrs(ts):
+        return arr(*[t.data_ptr() for t in ts])
+
+    def nouts(names):
+        return (C.c_int * 4)(*[pinfo[n][1] for n in names])
+
+    def lin(sp, names, x, outs, lw, x2=None, nw=None, resid=None):
+        t, _, n_in = pinfo[names[0]]
+        ok = L.layer_linear_dev(len(names), ptrs(outs), x.data_ptr(), None if x2 is None else x2.data_ptr(),
+                                None if nw is None else nw.data_ptr(), eps, ptrs([lw[n] for n in names]), t, None,
+                                None if resid is None else arr(*[resid.data_ptr()]), nouts(names), m, n_in, sp)
+        L.check(ok, "layer_linear")
+
+    def group(sp, names, x, outs, lw):
+        t, _, n_in = pinfo[names[0]]
+        L.check(L.linear_group_dev(len(names), ptrs(outs), x.data_ptr(), ptrs([lw[n] for n in names]), t, None,
+                                   nouts(names), m, n_in, sp), "linear group")
+
+    def logits(sp):
+        L.check(L.logits_dev(scores.data_ptr(), best.data_ptr(), hidden.data_ptr(), wout.data_ptr(),
+                             cfg["logits_type"], None, m, cfg["vocab"], h, cfg["logits_chunk"], sp), "logits")
+
+    def fused(sp):
+        for layers in model:
+            for lw, (an, fn) in zip(layers, norms):
+                lin(sp, ["q", "k", "v"], hidden, [buf["q"], buf["k"], buf["v"]], lw, nw=an)
+                lin(sp, ["o"], buf["q"], [hidden], lw, resid=hidden)
+                lin(sp, ["gate", "up"], hidden, [buf["gate"], buf["up"]], lw, nw=fn)
+                lin(sp, ["down"], buf["gate"], [hidden], lw, x2=buf["up"], resid=hidden)
+            logits(sp)
+
+    def separate(sp):
+        for layers in model:
+            for lw, (an, fn) in zip(layers, norms):
+                L.check(L.rmsnorm_dev(normed.data_ptr(), hidden.data_ptr(), an.data_ptr(), m, h, eps, sp), "rmsnorm")
+                group(sp, ["q", "k", "v"], normed, [buf["q"], buf["k"], buf["v"]], lw)
+                group(sp, ["o"], buf["q"], [tmp], lw)
+                L.check(L.add_dev(hidden.data_ptr(), hidden.data_ptr(), tmp.data_ptr(), m * h, sp), "add")
+                L.check(L.rmsnorm_dev(normed.data_ptr(), hidden.data_ptr(), fn.data_ptr(), m, h, eps, sp), "rmsnorm")
+                group(sp, ["gate", "up"], normed, [buf["gate"], buf["up"]], lw)
+                L.check(L.silu_mul_dev(act.data_ptr(), buf["gate"].data_ptr(), buf["up"].data_ptr(),
+                                       m * cfg["ffn"], sp), "silu_mul")
+                group(sp, ["down"], act, [tmp], lw)
+                L.check(L.add_dev(hidden.data_ptr(), hidden.data_ptr(), tmp.data_ptr(), m * h, sp), "add")
+            logits(sp)
+
+    res = {}
+    for name, fn in (("fused", fused), ("separate", separate)):
+        g = capture(fn)
+        for _ in range(max(1, warmup)):
+            g.replay()
+        res[name] = round(timed(g.replay, steps) / copies, 4)
+        del g
+    # each fused launch kind alone over the layers (us per launch)
+    layers0 = model[0]
+    kinds = {
+        "qkv_rmsnorm": lambda sp, lw, an, fn: lin(sp, ["q", "k", "v"], hidden, [buf["q"], buf["k"], buf["v"]], lw,
+                                                  nw=an),
+        "o_residual": lambda sp, lw, an, fn: lin(sp, ["o"], buf["q"], [hidden], lw, resid=hidden),
+        "gate_up_rmsnorm": lambda sp, lw, an, fn: lin(sp, ["gate", "up"], hidden, [buf["gate"], buf["up"]], lw,
+                                                      nw=fn),
+        "down_silu_mul_residual": lambda sp, lw, an, fn: lin(sp, ["down"], buf["gate"], [hidden], lw, x2=buf["up"],
+                                                             resid=hidden),
+    }
+    per = {}
+    for kname, kfn in kinds.items():
+        def body(sp, kfn=kfn):
+            for _ in range(4):
+                for lw, (an, fn) in zip(layers0, norms):
+                    kfn(sp, lw, an, fn)
+        g = capture(body)
+        g.replay()
+        per[kname] = round(timed(g.replay, 3) * 1e3 / (4 * len(layers0)), 3)
+        del g
+    weight_bytes = sum(cfg["layers"] * n_out * E.row_bytes(t, n_in) for _, t, n_out, n_in, _ in projs) \
+        + cfg["vocab"] * E.row_bytes(cfg["logits_type"], h)
+    return {"metric": "decode step with the layer ops on device, ms per step, 1 GPU", "workload": workload,
+            "batch": m, "layers": cfg["layers"], "ms_per_step": res, "fused_us_per_launch": per,
+            "launches_per_layer": {"fused": 4, "separate": 9},
+            "weight_GBps": {k: round(weight_bytes / (v * 1e-3) / 1e9, 1) for k, v in res.items()}}
 
 
 def read_ceiling(E, cfg, workload, dev):
