@@ -455,9 +455,9 @@ def layer_step(L, E, synth, gen, dev, cfg, workload, m, steps, warmup):
     o reads q):  rmsnorm -> q/k/v, o + residual, rmsnorm -> gate/up,
     silu(gate) * up -> down + residual, then the logits.  Timed two ways,
     HIP graphs of whole steps, HIP events: through
-    edgexpu_hip_layer_linear_dev (the layer ops inside the projection
-    launches: 4 launches per layer) and as separate launches (rmsnorm, the
-    grouped projection, add, silu_mul: 9 per layer)."""
+    edgexpu_hip_layer_linear_dev and edgexpu_hip_gate_up_silu_dev (the layer
+    ops inside the projection launches: 4 launches per layer) and as separate
+    launches (rmsnorm, the grouped projection, add, silu_mul: 9 per layer)."""
     import torch
 
     projs = projections(cfg)
@@ -504,13 +504,18 @@ def layer_step(L, E, synth, gen, dev, cfg, workload, m, steps, warmup):
         L.check(L.logits_dev(scores.data_ptr(), best.data_ptr(), hidden.data_ptr(), wout.data_ptr(),
                              cfg["logits_type"], None, m, cfg["vocab"], h, cfg["logits_chunk"], sp), "logits")
 
+    def gate_up_silu(sp, lw, fn):
+        t, _, n_in = pinfo["gate"]
+        L.check(L.gate_up_silu_dev(act.data_ptr(), hidden.data_ptr(), fn.data_ptr(), eps, lw["gate"].data_ptr(),
+                                   lw["up"].data_ptr(), t, None, None, m, cfg["ffn"], n_in, sp), "gate_up_silu")
+
     def fused(sp):
         for layers in model:
             for lw, (an, fn) in zip(layers, norms):
                 lin(sp, ["q", "k", "v"], hidden, [buf["q"], buf["k"], buf["v"]], lw, nw=an)
                 lin(sp, ["o"], buf["q"], [hidden], lw, resid=hidden)
-                lin(sp, ["gate", "up"], hidden, [buf["gate"], buf["up"]], lw, nw=fn)
-                lin(sp, ["down"], buf["gate"], [hidden], lw, x2=buf["up"], resid=hidden)
+                gate_up_silu(sp, lw, fn)
+                lin(sp, ["down"], act, [hidden], lw, resid=hidden)
             logits(sp)
 
     def separate(sp):
@@ -543,6 +548,8 @@ def layer_step(L, E, synth, gen, dev, cfg, workload, m, steps, warmup):
         "o_residual": lambda sp, lw, an, fn: lin(sp, ["o"], buf["q"], [hidden], lw, resid=hidden),
         "gate_up_rmsnorm": lambda sp, lw, an, fn: lin(sp, ["gate", "up"], hidden, [buf["gate"], buf["up"]], lw,
                                                       nw=fn),
+        "gate_up_rmsnorm_silu_mul": lambda sp, lw, an, fn: gate_up_silu(sp, lw, fn),
+        "down_residual": lambda sp, lw, an, fn: lin(sp, ["down"], act, [hidden], lw, resid=hidden),
         "down_silu_mul_residual": lambda sp, lw, an, fn: lin(sp, ["down"], buf["gate"], [hidden], lw, x2=buf["up"],
                                                              resid=hidden),
     }

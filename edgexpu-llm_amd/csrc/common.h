@@ -115,11 +115,12 @@ __device__ __forceinline__ uint32_t row16_min(uint32_t v) {
 }
 
 // SiLU as src/cpu_kernel.c:244-252 computes it, x / (1.0f + expf(-x)), with
-// the exponential evaluated in double and rounded once to float (correctly
-// rounded; the host libm's expf is not on a small fraction of inputs, where
-// the two silu values differ by up to two ulp).
+// the device expf (within about one ulp; the host libm's is within 0.502),
+// so the two silu values can differ by a few ulp.  (A double-precision exp
+// rounded once is correctly rounded but costs registers the fused GEMV
+// epilogue does not have.)
 __device__ __forceinline__ float silu_f32(float v) {
-    const float e = (float)exp(-(double)v);
+    const float e = expf(-v);
     return v / (1.0f + e);
 }
 

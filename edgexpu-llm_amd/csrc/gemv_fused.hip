@@ -365,7 +365,12 @@ void gemv_fused_kernel(FusedArgs a) {
     const int slot = lane / G, gl = lane & (G - 1);
     const int unit = gl + G * ks;
     const int u = min(unit, a.U - 1);
-    const int rows_per_tile = S * R;
+    // PRO bit 3: gate/up pairs (matrix 0 = gate, a.w[1] / a.bias[1] = up):
+    // slot rows r = 2j and 2j+1 are row j of gate and of up, and the tile's
+    // store writes silu(gate) * up (src/native.c:2576-2578) from the gate lane
+    constexpr bool kPair = (PRO & 8) != 0;
+    static_assert(!kPair || (M == 1 && R % 2 == 0), "pairs need one token and an even row count");
+    const int rows_per_tile = S * (kPair ? R / 2 : R);
     constexpr int NV = R * M;
     constexpr int V = NV <= 1 ? 1 : NV <= 2 ? 2 : NV <= 4 ? 4 : NV <= 8 ? 8 : 16;
     static_assert(NV <= 16, "too many partials per lane");
@@ -410,21 +415,25 @@ void gemv_fused_kernel(FusedArgs a) {
     // grid would queue them all on one L2 channel).
     auto issue_tile = [&](const TileMat &t_, Epi &e_, typename Fmt::W (&w_)[R]) {
         // bias and residual first: waiting for them then waits for no weight row
-        const int orow = min(t_.row0 + o_slot + S * o_r, t_.n_out - 1);
+        const int orow = min(t_.row0 + o_slot + S * (kPair ? o_r >> 1 : o_r), t_.n_out - 1);
         const float *wf = reinterpret_cast<const float *>(t_.w + (size_t)min(t_.row0 + slot, t_.n_out - 1) * a.row_bytes);
-        e_.b = *(t_.bias != nullptr ? t_.bias + orow : wf);
+        const float *bsel = kPair && (o_r & 1) ? a.bias[1] : t_.bias;
+        e_.b = *(bsel != nullptr ? bsel + orow : wf);
         if constexpr (kRes) e_.r = *(t_.resid != nullptr ? t_.resid + (size_t)o_t * t_.n_out + orow : wf);
         else e_.r = 0.0f;
-        const WSrc src{t_.w, a.row_bytes};
 #pragma unroll
-        for (int r = 0; r < R; ++r) Fmt::load_w(src, min(t_.row0 + slot + S * r, t_.n_out - 1), u, w_[r]);
+        for (int r = 0; r < R; ++r) {
+            const WSrc src{kPair && (r & 1) ? a.w[1] : t_.w, a.row_bytes};
+            Fmt::load_w(src, min(t_.row0 + slot + S * (kPair ? r >> 1 : r), t_.n_out - 1), u, w_[r]);
+        }
     };
     auto load_tile = [&](int wt_, TileMat &t_, Epi &e_, typename Fmt::W (&w_)[R]) {
         t_ = locate(a, min(wt_ * RG + rg, a.ntiles - 1), rows_per_tile);
         issue_tile(t_, e_, w_);
     };
     auto bias_of = [&](const TileMat &t_, Epi raw) {
-        return Epi{t_.bias != nullptr ? raw.b : 0.0f, kRes && t_.resid != nullptr ? raw.r : 0.0f};
+        const float *bsel = kPair && (o_r & 1) ? a.bias[1] : t_.bias;
+        return Epi{bsel != nullptr ? raw.b : 0.0f, kRes && t_.resid != nullptr ? raw.r : 0.0f};
     };
 
     // 1. the activation's first staging round, then the first tile's
@@ -506,14 +515,22 @@ void gemv_fused_kernel(FusedArgs a) {
         // drops the write.  With no branch around the store, the compiler
         // counts exactly one store after each tile's loads and waits for the
         // weights alone, not for the previous tile's store as well.
-        const int row = ct.row0 + o_slot + S * o_r;
-        const bool live = have && o_live && row < ct.n_out;
+        const int row = ct.row0 + o_slot + S * (kPair ? o_r >> 1 : o_r);
+        const bool live = have && o_live && row < ct.n_out && (!kPair || (o_r & 1) == 0);
         const __amdgpu_buffer_rsrc_t rs =
             __builtin_amdgcn_make_buffer_rsrc(ct.out, (short)0, a.m * ct.n_out * 4, kRawBufferWord3);
         // out = residual + (bias + dot): the reference's projection, then its
         // residual add (src/native.c:2571-2580)
         const float v = ce.b + result;
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(kRes && ct.resid != nullptr ? ce.r + v : v), rs,
+        float o = kRes && ct.resid != nullptr ? ce.r + v : v;
+        if constexpr (kPair) {
+            // the up value of the same row sits on the lane whose value index
+            // differs in bit 0: lane bit G/V after the lane reduction, the next
+            // lane after the K-split sum
+            const float up = shfl_xor_f(v, KS > 1 ? 1 : G / V);
+            o = silu_f32(v) * up;
+        }
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(o), rs,
                                               live ? (o_t * ct.n_out + row) * 4 : kDeadOffset, 0, 0);
     };
 
@@ -640,7 +657,7 @@ static int env_int(const char *name, int dflt) {
 template <class Fmt, int M, int R, int NW, bool STAGE, int LOOP, int PRO = 0>
 static hipError_t launch_fused_fmt(FusedArgs a, hipStream_t st, int per_cu_cap = 0) {
     const int S = 64 / a.G, RG = NW / a.KS;
-    const int rows_per_tile = S * R;
+    const int rows_per_tile = S * ((PRO & 8) != 0 ? R / 2 : R);
     int t = 0;
     for (int z = 0; z < a.nmat; ++z) {
         a.tile_start[z] = t;
@@ -736,15 +753,29 @@ static int pick_r16(const FusedArgs &a, int r_env) {
     return r16;
 }
 
-// One token with a staging prologue (PRO 1: RMSNorm, 2: SiLU-mul): the
-// default one-token schedules of launch_fused_nw, instantiated with it.
+// One token with a staging prologue (PRO 1: RMSNorm, 2: SiLU-mul), a
+// residual (bit 2) or gate/up pairs (bit 3): the default one-token schedules
+// of launch_fused_nw, instantiated with them (pairs take an even row count
+// per slot).
 template <class Fmt, int PRO>
 static hipError_t launch_fused_pro(FusedArgs a, hipStream_t st) {
+    constexpr bool kPair = (PRO & 8) != 0;
     if (a.m != 1 || a.KS > 4) return hipErrorInvalidValue;
     if (a.KS > 1) {
         if constexpr (Fmt::kUnitsPerBlock == 4) {
-            const int r16 = pick_r16<Fmt>(a, 0);
-            if (r16 == 1) return launch_fused_fmt<Fmt, 1, 1, 16, true, 0, PRO>(a, st);
+            int r16 = pick_r16<Fmt>(a, 0);
+            if constexpr (kPair) {
+                // pairs per slot 1 or 2: the count whose workgroup tiles fill the grid best
+                const int rg = 16 / a.KS, cus = device_cus();
+                auto fill = [&](int pairs) {
+                    const int tiles = (a.n_out[0] + pairs - 1) / pairs;
+                    const int wg_tiles = (tiles + rg - 1) / rg, rounds = (wg_tiles + cus - 1) / cus;
+                    return (double)wg_tiles / (double)(rounds * cus);
+                };
+                r16 = sizeof(typename Fmt::W) <= 48 && fill(2) >= fill(1) ? 4 : 2;
+            } else {
+                if (r16 == 1) return launch_fused_fmt<Fmt, 1, 1, 16, true, 0, PRO>(a, st);
+            }
             if (r16 == 2) return launch_fused_fmt<Fmt, 1, 2, 16, true, 0, PRO>(a, st);
             if constexpr (sizeof(typename Fmt::W) <= 48) return launch_fused_fmt<Fmt, 1, 4, 16, true, 0, PRO>(a, st);
             return hipErrorInvalidValue;
@@ -753,11 +784,11 @@ static hipError_t launch_fused_pro(FusedArgs a, hipStream_t st) {
         }
     }
     int rows = 0;
-    for (int z = 0; z < a.nmat; ++z) rows += a.n_out[z];
+    for (int z = 0; z < a.nmat; ++z) rows += a.n_out[z] * (kPair ? 2 : 1);
     const int r1 = rows <= 4096 ? 2 : 4;
     const int rows_per_tile = (64 / a.G) * r1;
     int tiles = 0;
-    for (int z = 0; z < a.nmat; ++z) tiles += (a.n_out[z] + rows_per_tile - 1) / rows_per_tile;
+    for (int z = 0; z < a.nmat; ++z) tiles += (a.n_out[z] * (kPair ? 2 : 1) + rows_per_tile - 1) / rows_per_tile;
     if (tiles > 2 * device_cus() * 8) return launch_fused_fmt<Fmt, 1, 2, 8, true, 1, PRO>(a, st, 1);
     return r1 == 2 ? launch_fused_fmt<Fmt, 1, 2, 8, true, 0, PRO>(a, st)
                    : launch_fused_fmt<Fmt, 1, 4, 8, true, 0, PRO>(a, st);
@@ -894,9 +925,10 @@ hipError_t launch_gemv_fused_f32(int type, const uint8_t *w, int n_out, const fl
 // f32 x quantized inside the kernel (x != null), or codes already quantized
 // in the reference block layout (xq, token stride xq_stride).
 namespace {
-// pro: prologue (0, 1, 2) | 4 for a residual epilogue.  The instantiated
-// one-token combinations are the layer's: RMSNorm (q/k/v, gate/up),
-// residual (o), SiLU-mul with or without residual (down).
+// pro: prologue (0, 1, 2) | 4 for a residual epilogue | 8 for gate/up
+// pairs.  The instantiated one-token combinations are the layer's: RMSNorm
+// (q/k/v, gate/up), residual (o), SiLU-mul with or without residual (down),
+// gate/up pairs with or without RMSNorm.
 template <class Fmt>
 hipError_t dispatch_fused(const FusedArgs &a, bool stage, int pro, hipStream_t st) {
     switch (pro) {
@@ -905,6 +937,8 @@ hipError_t dispatch_fused(const FusedArgs &a, bool stage, int pro, hipStream_t s
         case 2: return launch_fused_pro<Fmt, 2>(a, st);
         case 4: return launch_fused_pro<Fmt, 4>(a, st);
         case 6: return launch_fused_pro<Fmt, 6>(a, st);
+        case 8: return launch_fused_pro<Fmt, 8>(a, st);
+        case 9: return launch_fused_pro<Fmt, 9>(a, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -922,8 +956,14 @@ hipError_t launch_gemv_fused_layer(int type, int nmat, const uint8_t *const *w, 
                                    size_t row_bytes, int K, int m, const float *x, const float *x2, const float *nw,
                                    float eps, int pro, const uint8_t *xq, size_t xq_stride, hipStream_t st) {
     if (nmat < 1 || nmat > kFusedMaxMats) return hipErrorInvalidValue;
+    const bool pair = (pro & 8) != 0;
+    pro &= 3;
+    // pairs: w[0] / bias[0] gate, w[1] / bias[1] up, out[0] the product,
+    // n_out[0] their common row count; the tiles run over gate's rows
+    if (pair && (nmat != 2 || n_out[1] != n_out[0] || (resid != nullptr && (resid[0] || resid[1]))))
+        return hipErrorInvalidValue;
     FusedArgs a{};
-    a.nmat = nmat;
+    a.nmat = pair ? 1 : nmat;
     for (int z = 0; z < nmat; ++z) {
         a.w[z] = w[z];
         a.n_out[z] = n_out[z];
@@ -943,8 +983,8 @@ hipError_t launch_gemv_fused_layer(int type, int nmat, const uint8_t *const *w, 
     if ((x == nullptr) == (xq == nullptr)) return hipErrorInvalidValue;
     bool any_resid = false;
     for (int z = 0; z < nmat; ++z) any_resid = any_resid || a.resid[z] != nullptr;
-    const int code = pro | (any_resid ? 4 : 0);
-    if (code != 0 && (x == nullptr || m != 1 || code == 5 || (pro == 1 && nw == nullptr) ||
+    const int code = pro | (any_resid ? 4 : 0) | (pair ? 8 : 0);
+    if (code != 0 && (x == nullptr || m != 1 || code == 5 || (pair && pro == 2) || (pro == 1 && nw == nullptr) ||
                       (pro == 2 && x2 == nullptr)))
         return hipErrorInvalidValue;
     a.nblk = type == kTypeQ8_0 ? K / kQK8_0 : K / kQKK;

@@ -568,6 +568,49 @@ int edgexpu_hip_layer_linear_dev(int nmat, float *const *out, const float *x, co
     return 1;
 }
 
+int edgexpu_hip_gate_up_silu_dev(float *act, const float *x, const float *norm_weight, float eps, const void *w_gate,
+                                 const void *w_up, uint32_t type, const float *b_gate, const float *b_up, int m,
+                                 int n_ff, int n_in, void *stream) {
+    if (!ensure_init()) return 0;
+    if (!check_linear_args(act, x, w_gate, type, m, n_ff, n_in, "gate_up_silu") ||
+        !check_linear_args(act, x, w_up, type, m, n_ff, n_in, "gate_up_silu"))
+        return 0;
+    if (!aligned16(x) || (norm_weight != nullptr && !aligned16(norm_weight))) {
+        set_error(-2, "gate_up_silu: x and norm_weight must be 16-byte aligned");
+        return 0;
+    }
+    hipStream_t st = pick_stream(stream);
+    const int pro = norm_weight != nullptr ? 1 : 0;
+    const size_t rb = edgexpu_hip_row_bytes(type, n_in);
+    const void *wg[2] = {w_gate, w_up};
+    const float *bg[2] = {b_gate, b_up};
+    const int nn[2] = {n_ff, n_ff};
+    // one launch: gate row j and up row j in the same wave, silu(gate) * up
+    // from the store
+    if (m == 1 && stage_in_kernel(type, n_in, 1) && gemv_fused_pro_supported((int)type, n_in, pro)) {
+        float *outs[2] = {act, act};
+        return hip_ok(launch_gemv_fused_layer((int)type, 2, (const uint8_t *const *)wg, nn, bg, nullptr, outs, rb,
+                                              n_in, 1, x, nullptr, norm_weight, eps, pro | 8, nullptr, 0, st),
+                      "gate_up_silu fused")
+                   ? 1
+                   : 0;
+    }
+    // otherwise: the RMSNorm, gate and up into one sizing of the layer
+    // workspace (nothing below grows it), then silu * up
+    const size_t nf = align_up((size_t)m * n_ff, 64), ni = pro != 0 ? align_up((size_t)m * n_in, 64) : 0;
+    float *base = (float *)layer_ws((2 * nf + ni) * sizeof(float) + 256);
+    if (base == nullptr) return 0;
+    const float *a_in = x;
+    if (pro != 0) {
+        if (!hip_ok(launch_rmsnorm(x, norm_weight, base + 2 * nf, m, n_in, eps, st), "gate_up_silu rmsnorm")) return 0;
+        a_in = base + 2 * nf;
+    }
+    float *outs[2] = {base, base + nf};
+    if (!run_linear_group(type, 2, wg, nn, bg, outs, a_in, m, n_in, st)) return 0;
+    return hip_ok(launch_elementwise(outs[0], outs[1], act, (long long)m * n_ff, 3, st), "gate_up_silu silu_mul") ? 1
+                                                                                                                   : 0;
+}
+
 int edgexpu_hip_gemv_q8_dev(float *out, const uint8_t *xq, const void *w, uint32_t type, const float *bias, int m,
                             int n_out, int n_in, void *stream) {
     if (!ensure_init()) return 0;

@@ -97,6 +97,9 @@ class HipLib:
         self.mul_dev = _sig(L, "edgexpu_hip_mul_dev", C.c_int, [_vp, _vp, _vp, C.c_longlong, _vp])
         self.add_dev = _sig(L, "edgexpu_hip_add_dev", C.c_int, [_vp, _vp, _vp, C.c_longlong, _vp])
         self.silu_mul_dev = _sig(L, "edgexpu_hip_silu_mul_dev", C.c_int, [_vp, _vp, _vp, C.c_longlong, _vp])
+        self.gate_up_silu_dev = _sig(L, "edgexpu_hip_gate_up_silu_dev", C.c_int,
+                                     [_vp, _vp, _vp, C.c_float, _vp, _vp, C.c_uint32, _vp, _vp, C.c_int, C.c_int,
+                                      C.c_int, _vp])
         self.layer_linear_dev = _sig(L, "edgexpu_hip_layer_linear_dev", C.c_int,
                                      [C.c_int, _vp, _vp, _vp, _vp, C.c_float, _vp, C.c_uint32, _vp, _vp, _vp,
                                       C.c_int, C.c_int, _vp])
@@ -287,3 +290,18 @@ def layer_linear(ws, qtype: int, x, n_outs, n_in: int, x2=None, norm_weight=None
                                eps, arr(*[t.data_ptr() for t in ws]), qtype, b, r, (C.c_int * 4)(*n_outs), m, n_in,
                                _stream()), "layer_linear")
     return outs
+
+
+def gate_up_silu(w_gate, w_up, qtype: int, x, n_ff: int, n_in: int, norm_weight=None, eps: float = 1e-5,
+                 b_gate=None, b_up=None, out=None):
+    """act = silu(gate(a)) * up(a), a = rmsnorm(x) or x (edgexpu_hip_gate_up_silu_dev)."""
+    import torch
+
+    m = x.shape[0]
+    if out is None:
+        out = torch.empty((m, n_ff), dtype=torch.float32, device=x.device)
+    L = hip()
+    L.check(L.gate_up_silu_dev(out.data_ptr(), x.data_ptr(), _ptr(norm_weight), eps, w_gate.data_ptr(),
+                               w_up.data_ptr(), qtype, _ptr(b_gate), _ptr(b_up), m, n_ff, n_in, _stream()),
+            "gate_up_silu")
+    return out

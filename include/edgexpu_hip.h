@@ -158,9 +158,8 @@ int edgexpu_hip_quantize_q8_k_dev(const float *x, int m, int n, uint8_t *dst, vo
  *             mean can differ from the reference's index-order sum only where
  *             its rounding falls within the double sum's error);
  *   silu:     edgexpu_cpu_silu (cpu_kernel.h:20, src/cpu_kernel.c:244-252),
- *             exp evaluated in double and rounded once (correctly rounded;
- *             the host libm's expf is not, on ~0.03 % of inputs, which moves
- *             silu by up to two ulp there);
+ *             with the device expf (about one ulp; the host libm's 0.502):
+ *             within four ulp of the reference's silu;
  *   mul, add: edgexpu_cpu_mul / edgexpu_cpu_add (src/cpu_kernel.c:200-218),
  *             exact;
  *   silu_mul: silu(gate) then * up in one pass, the reference's
@@ -196,6 +195,20 @@ int edgexpu_hip_layer_linear_dev(int nmat, float *const *out, const float *x, co
                                  const float *norm_weight, float eps, const void *const *w, uint32_t type,
                                  const float *const *bias, const float *const *residual, const int *n_out, int m,
                                  int n_in, void *stream);
+
+/* A decode layer's gate and up projections with the SwiGLU product
+ * (src/native.c:2575-2578):
+ *   a   = rmsnorm(x; norm_weight, eps)  (norm_weight != NULL) or x
+ *   act = silu(b_gate + W_gate . q8(a)) * (b_up + W_up . q8(a))   [m][n_ff]
+ * as edgexpu_hip_layer_linear_dev over gate and up followed by
+ * edgexpu_hip_silu_mul_dev compute it (bit for bit).  At one token it is one
+ * launch: row j of gate and row j of up are reduced in the same wave and the
+ * store writes their product, so SiLU runs once per element and the down
+ * projection takes act with no prologue.  Biases optional; act must not
+ * overlap x.  Returns 1 on success, 0 on bad arguments or a HIP error. */
+int edgexpu_hip_gate_up_silu_dev(float *act, const float *x, const float *norm_weight, float eps, const void *w_gate,
+                                 const void *w_up, uint32_t type, const float *b_gate, const float *b_up, int m,
+                                 int n_ff, int n_in, void *stream);
 
 /* ---- host-pointer entry points (synchronous: inputs copied in, outputs
  * copied out before return; the PCIe copies are part of the call) ---- */
