@@ -18,9 +18,11 @@ KERNELS_SO = os.path.join(LIB_DIR, "libedgexpu_kernels.so")
 
 F32, F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 2, 6, 8, 12, 13, 14
 # (elements per block, bytes per block); Q8_K is the activation format
-BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+BLOCK = {F32: (1, 4), F16: (1, 2), Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34),
+         Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
 Q8_K_BLOCK = (256, 292)
-TYPE_NAMES = {Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k"}
+TYPE_NAMES = {F32: "f32", F16: "f16", Q4_0: "q4_0", Q5_0: "q5_0", Q8_0: "q8_0", Q4_K: "q4_k",
+              Q5_K: "q5_k", Q6_K: "q6_k"}
 
 
 class HipError(RuntimeError):

@@ -6,6 +6,9 @@ Distributions (the workloads' definitions):
         [0, 63]); 128 qs bytes uniform (4-bit codes 0..15)
   Q6_K  d = fp16(|N(0, 0.01)|) (sigma chosen here; not given by the workload);
         ql/qh bytes uniform; 16 int8 sub-scales uniform in [-128, 127]
+  Q4_0, Q5_0  d = fp16(|N(0, 0.02)| / 16); qs (and Q5_0's qh) bytes uniform
+  Q5_K  as Q4_K, with the 32 qh bytes uniform
+  F16   N(0, 0.02) rounded to fp16
   activations f32 N(0, 1)
 
 ``np_*`` functions build host arrays with numpy's PCG64 (tests); ``torch_*``
@@ -17,7 +20,7 @@ from __future__ import annotations
 
 import numpy as np
 
-Q8_0, Q4_K, Q6_K = 8, 12, 14
+F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 1, 2, 6, 8, 12, 13, 14
 
 
 def _f16_bytes(a: np.ndarray) -> np.ndarray:
@@ -36,6 +39,19 @@ def np_weights(qtype: int, rows: int, n: int, rng: np.random.Generator) -> np.nd
         dd = _f16_bytes(np.abs(rng.normal(0.0, 0.01, (rows, nb, 2)))).reshape(rows, nb, 4)
         rest = rng.integers(0, 256, (rows, nb, 140), dtype=np.int16).astype(np.uint8)
         return np.concatenate([dd, rest], axis=2).reshape(rows, nb * 144)
+    if qtype == Q5_K:
+        nb = n // 256
+        dd = _f16_bytes(np.abs(rng.normal(0.0, 0.01, (rows, nb, 2)))).reshape(rows, nb, 4)
+        rest = rng.integers(0, 256, (rows, nb, 172), dtype=np.int16).astype(np.uint8)
+        return np.concatenate([dd, rest], axis=2).reshape(rows, nb * 176)
+    if qtype in (Q4_0, Q5_0):
+        nb = n // 32
+        nq = 16 if qtype == Q4_0 else 20
+        d = _f16_bytes(np.abs(rng.normal(0.0, 0.02, (rows, nb))) / 16.0).reshape(rows, nb, 2)
+        q = rng.integers(0, 256, (rows, nb, nq), dtype=np.int16).astype(np.uint8)
+        return np.concatenate([d, q], axis=2).reshape(rows, nb * (2 + nq))
+    if qtype == F16:
+        return _f16_bytes(rng.normal(0.0, 0.02, (rows, n))).reshape(rows, 2 * n)
     if qtype == Q6_K:
         nb = n // 256
         qlh = rng.integers(0, 256, (rows, nb, 192), dtype=np.int16).astype(np.uint8)
@@ -66,6 +82,19 @@ def torch_weights(qtype: int, rows: int, n: int, generator, device="cuda"):
         dd = f16b(torch.randn((rows, nb, 2), generator=generator, device=device).abs_() * 0.01)
         rest = torch.randint(0, 256, (rows, nb, 140), generator=generator, device=device, dtype=torch.uint8)
         return torch.cat([dd.view(rows, nb, 4), rest], dim=2).reshape(rows, nb * 144)
+    if qtype == Q5_K:
+        nb = n // 256
+        dd = _f16_bytes(np.abs(rng.normal(0.0, 0.01, (rows, nb, 2)))).reshape(rows, nb, 4)
+        rest = rng.integers(0, 256, (rows, nb, 172), dtype=np.int16).astype(np.uint8)
+        return np.concatenate([dd, rest], axis=2).reshape(rows, nb * 176)
+    if qtype in (Q4_0, Q5_0):
+        nb = n // 32
+        nq = 16 if qtype == Q4_0 else 20
+        d = _f16_bytes(np.abs(rng.normal(0.0, 0.02, (rows, nb))) / 16.0).reshape(rows, nb, 2)
+        q = rng.integers(0, 256, (rows, nb, nq), dtype=np.int16).astype(np.uint8)
+        return np.concatenate([d, q], axis=2).reshape(rows, nb * (2 + nq))
+    if qtype == F16:
+        return _f16_bytes(rng.normal(0.0, 0.02, (rows, n))).reshape(rows, 2 * n)
     if qtype == Q6_K:
         nb = n // 256
         qlh = torch.randint(0, 256, (rows, nb, 192), generator=generator, device=device, dtype=torch.uint8)

@@ -17,7 +17,10 @@
 #define QK32 32
 #define QKK 256
 #define B_Q8_0 34
+#define B_Q4_0 18
+#define B_Q5_0 22
 #define B_Q4_K 144
+#define B_Q5_K 176
 #define B_Q6_K 210
 #define B_Q8_K 292
 #define LOGIT_CHUNK_BYTES ((size_t)48u * 1024u * 1024u) /* include/edgexpu/scheduler.h:34 */
@@ -158,6 +161,36 @@ static int q4_code(const uint8_t *sb, int e) {
     return ((e % 64) < 32) ? (qs[l] & 0x0f) : (qs[l] >> 4);
 }
 
+/* Q4_0 element e (0..31) of an 18-byte block: nibble code 0..15, value
+ * code - 8 (src/gguf_quant.c:193-210: low nibbles are elements 0..15). */
+static int q4_0_code(const uint8_t *blk, int e) {
+    return e < 16 ? (blk[2 + e] & 0x0f) : (blk[2 + e - 16] >> 4);
+}
+
+/* Q5_0 element e (0..31) of a 22-byte block: 5-bit code, value code - 16;
+ * the fifth bit of element e is bit e of the 32-bit qh word
+ * (src/gguf_quant.c:157-180). */
+static int q5_0_code(const uint8_t *blk, int e) {
+    uint32_t qh;
+    int nib;
+    memcpy(&qh, blk + 2, 4);
+    nib = e < 16 ? (blk[6 + e] & 0x0f) : (blk[6 + e - 16] >> 4);
+    return nib | (int)(((qh >> e) & 1u) << 4);
+}
+
+/* Q5_K element e (0..255) of a 176-byte super-block: 5-bit code.  Chunk
+ * j = e/64 reads qs[32j + l] (low nibble for the first 32 elements, high for
+ * the next 32) and bit 2j (resp. 2j+1) of qh[l], l = e%32
+ * (src/gguf_quant.c:305-353). */
+static int q5_k_code(const uint8_t *sb, int e) {
+    int j = e / 64;
+    int hi = (e % 64) >= 32;
+    int l = e % 32;
+    int q = sb[48 + 32 * j + l];
+    int nib = hi ? (q >> 4) : (q & 0x0f);
+    return nib + (((sb[16 + l] >> (2 * j + hi)) & 1) << 4);
+}
+
 /* ------------------------------------------------------------- dequant */
 
 int ora_dequantize(const uint8_t *src, uint32_t type, uint64_t n, float *dst) {
@@ -177,6 +210,49 @@ int ora_dequantize(const uint8_t *src, uint32_t type, uint64_t n, float *dst) {
                 int j;
                 for (j = 0; j < QK32; j++) {
                     dst[b * QK32 + j] = d * (float)(int8_t)blk[2 + j];
+                }
+            }
+            return 1;
+        case ORA_F16: /* src/gguf_quant.c:183-191 */
+            for (b = 0; b < n; b++) {
+                dst[b] = ld_f16(src + 2 * b);
+            }
+            return 1;
+        case ORA_Q4_0: /* src/gguf_quant.c:193-210: y = ((float)c - 8) * d */
+            for (b = 0; b < n / QK32; b++) {
+                const uint8_t *blk = src + b * B_Q4_0;
+                float d = ld_f16(blk);
+                int e;
+                for (e = 0; e < QK32; e++) {
+                    dst[b * QK32 + (uint64_t)e] = ((float)q4_0_code(blk, e) - 8.0f) * d;
+                }
+            }
+            return 1;
+        case ORA_Q5_0: /* src/gguf_quant.c:157-180: y = (float)(c - 16) * d */
+            for (b = 0; b < n / QK32; b++) {
+                const uint8_t *blk = src + b * B_Q5_0;
+                float d = ld_f16(blk);
+                int e;
+                for (e = 0; e < QK32; e++) {
+                    dst[b * QK32 + (uint64_t)e] = (float)(q5_0_code(blk, e) - 16) * d;
+                }
+            }
+            return 1;
+        case ORA_Q5_K: /* src/gguf_quant.c:305-353: y = (d*sc)*c - (dmin*m) */
+            for (b = 0; b < n / QKK; b++) {
+                const uint8_t *sb = src + b * B_Q5_K;
+                float d = ld_f16(sb);
+                float dmin = ld_f16(sb + 2);
+                int e;
+                for (e = 0; e < QKK; e++) {
+                    int sc;
+                    int mn;
+                    float ds;
+                    float ms;
+                    k4_scale_min(sb + 4, e / 32, &sc, &mn);
+                    ds = d * (float)sc;
+                    ms = dmin * (float)mn;
+                    dst[b * QKK + (uint64_t)e] = ds * (float)q5_k_code(sb, e) - ms;
                 }
             }
             return 1;
@@ -372,6 +448,67 @@ void ora_q6_k_block_lanes(const uint8_t *wsb, const uint8_t *xsb, int32_t lanes[
     }
 }
 
+/* Q4_0 / Q5_0 x Q8_0: the same eight 4-element lanes as Q8_0, on the signed
+ * values c - 8 (src/gguf_dot_q8.c:552-568) and c - 16 (:482-502). */
+void ora_q4_0_block_lanes(const uint8_t *wblk, const uint8_t *xblk, int32_t lanes[8]) {
+    int u;
+    for (u = 0; u < 8; u++) {
+        int32_t s = 0;
+        int e;
+        for (e = 4 * u; e < 4 * u + 4; e++) {
+            s += (q4_0_code(wblk, e) - 8) * (int32_t)(int8_t)xblk[2 + e];
+        }
+        lanes[u] = s;
+    }
+}
+
+void ora_q5_0_block_lanes(const uint8_t *wblk, const uint8_t *xblk, int32_t lanes[8]) {
+    int u;
+    for (u = 0; u < 8; u++) {
+        int32_t s = 0;
+        int e;
+        for (e = 4 * u; e < 4 * u + 4; e++) {
+            s += (q5_0_code(wblk, e) - 16) * (int32_t)(int8_t)xblk[2 + e];
+        }
+        lanes[u] = s;
+    }
+}
+
+/* Q5_K x Q8_K (src/gguf_dot_q8.c:772-838, AVX2): lane u sums sc[sub] times the
+ * 4-element products 4u..4u+3 of each 32-element sub-block, as Q4_K; the
+ * min term is one integer, sum_k m[k] * (bsum[2k] + bsum[2k+1]). */
+void ora_q5_k_block_lanes(const uint8_t *wsb, const uint8_t *xsb, int32_t lanes[8], int32_t *mins) {
+    const int8_t *q8 = (const int8_t *)(xsb + 4);
+    int16_t bs[16];
+    int sc[8];
+    int mn[8];
+    int u;
+    int k;
+    int32_t total = 0;
+    memcpy(bs, xsb + 4 + QKK, sizeof(bs));
+    for (k = 0; k < 8; k++) {
+        k4_scale_min(wsb + 4, k, &sc[k], &mn[k]);
+    }
+    for (u = 0; u < 8; u++) {
+        int32_t s = 0;
+        int sub;
+        for (sub = 0; sub < 8; sub++) {
+            int32_t p = 0;
+            int e;
+            for (e = 4 * u; e < 4 * u + 4; e++) {
+                int idx = 32 * sub + e;
+                p += q5_k_code(wsb, idx) * (int32_t)q8[idx];
+            }
+            s += sc[sub] * p;
+        }
+        lanes[u] = s;
+    }
+    for (k = 0; k < 8; k++) {
+        total += mn[k] * ((int32_t)bs[2 * k] + bs[2 * k + 1]);
+    }
+    *mins = total;
+}
+
 /* hsum_float_8, src/gguf_dot_q8.c:129-135 */
 static float hsum8_dotq8(const float v[8]) {
     float r0 = v[4] + v[0];
@@ -456,11 +593,70 @@ static float dot_q6_k_q8_k(const uint8_t *w, const uint8_t *xq, int n) {
     return hsum8_dotq8(acc);
 }
 
+/* Q4_0 / Q5_0 x Q8_0 (src/gguf_dot_q8.c:552-568, 482-502; AVX2): per block
+ * d = fp16(w.d) * fp16(x.d), eight lane FMAs, hsum_float_8 at the end. */
+static float dot_q4_0_q5_0_q8_0(uint32_t type, const uint8_t *w, const uint8_t *xq, int n) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    size_t bb = type == ORA_Q4_0 ? B_Q4_0 : B_Q5_0;
+    int b;
+    for (b = 0; b < n / QK32; b++) {
+        const uint8_t *wb = w + (size_t)b * bb;
+        const uint8_t *xb = xq + (size_t)b * B_Q8_0;
+        float d = ld_f16(wb) * ld_f16(xb);
+        int32_t l[8];
+        int u;
+        if (type == ORA_Q4_0) {
+            ora_q4_0_block_lanes(wb, xb, l);
+        } else {
+            ora_q5_0_block_lanes(wb, xb, l);
+        }
+        for (u = 0; u < 8; u++) {
+            acc[u] = fmaf(d, (float)l[u], acc[u]);
+        }
+    }
+    return hsum8_dotq8(acc);
+}
+
 float ora_dot_q8(uint32_t type, const uint8_t *wrow, const uint8_t *xq, int n) {
     if (wrow == NULL || xq == NULL || n <= 0 || n % QK32 != 0) {
         return 0.0f;
     }
-    return type == ORA_Q8_0 ? dot_q8_0_q8_0(wrow, xq, n) : 0.0f;
+    switch (type) {
+        case ORA_Q8_0: return dot_q8_0_q8_0(wrow, xq, n);
+        case ORA_Q4_0:
+        case ORA_Q5_0: return dot_q4_0_q5_0_q8_0(type, wrow, xq, n);
+        default: return 0.0f;
+    }
+}
+
+/* Q5_K x Q8_K (src/gguf_dot_q8.c:772-838): lanes FMA'd with d = dx * w.d;
+ * the min term accumulates in one float, summs += (-dx * w.dmin) * total,
+ * multiply and add rounded separately; result hsum_float_8 + summs. */
+static float dot_q5_k_q8_k(const uint8_t *w, const uint8_t *xq, int n) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float summs = 0.0f;
+    int b;
+    for (b = 0; b < n / QKK; b++) {
+        const uint8_t *sb = w + (size_t)b * B_Q5_K;
+        const uint8_t *yb = xq + (size_t)b * B_Q8_K;
+        float dx;
+        float d;
+        float dmin;
+        float prod;
+        int32_t l[8];
+        int32_t total;
+        int u;
+        memcpy(&dx, yb, 4);
+        d = dx * ld_f16(sb);
+        dmin = -dx * ld_f16(sb + 2);
+        ora_q5_k_block_lanes(sb, yb, l, &total);
+        prod = dmin * (float)total;
+        summs = summs + prod;
+        for (u = 0; u < 8; u++) {
+            acc[u] = fmaf(d, (float)l[u], acc[u]);
+        }
+    }
+    return hsum8_dotq8(acc) + summs;
 }
 
 float ora_dot_q8k(uint32_t type, const uint8_t *wrow, const uint8_t *xq, int n) {
@@ -472,6 +668,9 @@ float ora_dot_q8k(uint32_t type, const uint8_t *wrow, const uint8_t *xq, int n) 
     }
     if (type == ORA_Q6_K) {
         return dot_q6_k_q8_k(wrow, xq, n);
+    }
+    if (type == ORA_Q5_K) {
+        return dot_q5_k_q8_k(wrow, xq, n);
     }
     return 0.0f;
 }
@@ -567,11 +766,114 @@ static float dot_q8_0_f32(const uint8_t *w, const float *x, int n) {
     return acc;
 }
 
+/* dot_f16, src/gguf_quant.c:796-808: double products, serial double sum. */
+static float dot_f16_f32(const uint8_t *w, const float *x, int n) {
+    double acc = 0.0;
+    int i;
+    for (i = 0; i < n; i++) {
+        acc += (double)ld_f16(w + 2 * (size_t)i) * (double)x[i];
+    }
+    return (float)acc;
+}
+
+/* dot_f32_row, src/gguf_quant.c:506-536: eight FMA lanes over the first
+ * n - n%8 elements, hsum256, then the tail in double. */
+static float dot_f32_f32(const float *w, const float *x, int n) {
+    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    double acc = 0.0;
+    int i = 0;
+    for (; i + 8 <= n; i += 8) {
+        int l;
+        for (l = 0; l < 8; l++) {
+            v[l] = fmaf(w[i + l], x[i + l], v[l]);
+        }
+    }
+    acc += (double)hsum8_quant(v);
+    for (; i < n; i++) {
+        acc += (double)w[i] * (double)x[i];
+    }
+    return (float)acc;
+}
+
+/* dot_q4_0, src/gguf_quant.c:810-835: serial, acc += (d*(c-8))*x per
+ * element, low-nibble element before its high-nibble partner. */
+static float dot_q4_0_f32(const uint8_t *w, const float *x, int n) {
+    float acc = 0.0f;
+    int b;
+    for (b = 0; b < n / QK32; b++) {
+        const uint8_t *blk = w + (size_t)b * B_Q4_0;
+        const float *xx = x + (size_t)b * QK32;
+        float d = ld_f16(blk);
+        int j;
+        for (j = 0; j < 16; j++) {
+            acc += d * ((float)q4_0_code(blk, j) - 8.0f) * xx[j];
+            acc += d * ((float)q4_0_code(blk, j + 16) - 8.0f) * xx[j + 16];
+        }
+    }
+    return acc;
+}
+
+/* dot_q5_0, src/gguf_quant.c:672-702: acc += d * (c0*x0 + c1*x1) per pair. */
+static float dot_q5_0_f32(const uint8_t *w, const float *x, int n) {
+    float acc = 0.0f;
+    int b;
+    for (b = 0; b < n / QK32; b++) {
+        const uint8_t *blk = w + (size_t)b * B_Q5_0;
+        const float *xx = x + (size_t)b * QK32;
+        float d = ld_f16(blk);
+        int j;
+        for (j = 0; j < 16; j++) {
+            float v0 = (float)(q5_0_code(blk, j) - 16);
+            float v1 = (float)(q5_0_code(blk, j + 16) - 16);
+            acc += d * (v0 * xx[j] + v1 * xx[j + 16]);
+        }
+    }
+    return acc;
+}
+
+/* dot_q5_k, src/gguf_quant.c:837-892: serial, acc += (d1*c - m1) * x, the
+ * low-nibble element of each pair before the high-nibble one. */
+static float dot_q5_k_f32(const uint8_t *w, const float *x, int n) {
+    float acc = 0.0f;
+    int b;
+    for (b = 0; b < n / QKK; b++) {
+        const uint8_t *sb = w + (size_t)b * B_Q5_K;
+        const float *xx = x + (size_t)b * QKK;
+        float d = ld_f16(sb);
+        float dmin = ld_f16(sb + 2);
+        int j;
+        for (j = 0; j < 4; j++) {
+            int sc;
+            int mn;
+            float d1, m1, d2, m2;
+            int l;
+            k4_scale_min(sb + 4, 2 * j, &sc, &mn);
+            d1 = d * (float)sc;
+            m1 = dmin * (float)mn;
+            k4_scale_min(sb + 4, 2 * j + 1, &sc, &mn);
+            d2 = d * (float)sc;
+            m2 = dmin * (float)mn;
+            for (l = 0; l < 32; l++) {
+                float q0 = (float)q5_k_code(sb, 64 * j + l);
+                float q1 = (float)q5_k_code(sb, 64 * j + 32 + l);
+                acc += (d1 * q0 - m1) * xx[64 * j + l];
+                acc += (d2 * q1 - m2) * xx[64 * j + 32 + l];
+            }
+        }
+    }
+    return acc;
+}
+
 float ora_dot_f32(uint32_t type, const uint8_t *wrow, const float *x, int n) {
     if (wrow == NULL || x == NULL || n <= 0) {
         return 0.0f;
     }
     switch (type) {
+        case ORA_F32: return dot_f32_f32((const float *)wrow, x, n);
+        case ORA_F16: return dot_f16_f32(wrow, x, n);
+        case ORA_Q4_0: return (n % QK32) ? 0.0f : dot_q4_0_f32(wrow, x, n);
+        case ORA_Q5_0: return (n % QK32) ? 0.0f : dot_q5_0_f32(wrow, x, n);
+        case ORA_Q5_K: return (n % QKK) ? 0.0f : dot_q5_k_f32(wrow, x, n);
         case ORA_Q8_0: return (n % QK32) ? 0.0f : dot_q8_0_f32(wrow, x, n);
         case ORA_Q4_K: return (n % QKK) ? 0.0f : dot_q4_k_f32(wrow, x, n);
         case ORA_Q6_K: return (n % QKK) ? 0.0f : dot_q6_k_f32(wrow, x, n);
@@ -598,39 +900,73 @@ static uint8_t *scratch_ensure(size_t nbytes) {
     return g_scratch;
 }
 
+/* edgexpu_cpu_linear, src/cpu_kernel.c:462-523 (F32 weights, one token):
+ * acc = (double)bias, eight FMA lanes, hsum256 added in double, the tail in
+ * double, one final rounding. */
+static void linear_f32_one(float *out, const float *x, const float *w, const float *bias, int n_out, int n_in) {
+    int o;
+    for (o = 0; o < n_out; o++) {
+        const float *row = w + (size_t)o * (size_t)n_in;
+        double acc = bias != NULL ? (double)bias[o] : 0.0;
+        float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        int i = 0;
+        for (; i + 8 <= n_in; i += 8) {
+            int l;
+            for (l = 0; l < 8; l++) {
+                v[l] = fmaf(x[i + l], row[i + l], v[l]);
+            }
+        }
+        acc += (double)hsum8_quant(v);
+        for (; i < n_in; i++) {
+            acc += (double)x[i] * (double)row[i];
+        }
+        out[o] = (float)acc;
+    }
+}
+
+/* src/cpu_kernel.c:545-644: F32 at one token -> edgexpu_cpu_linear; the
+ * Q8_0 family (Q4_0, Q5_0, Q8_0) with n_in % 32 == 0 -> Q8_0 activations;
+ * the K-quants with n_in % 256 == 0 -> Q8_K activations; anything else ->
+ * the f32-activation row dot.  out = bias + dot. */
 int ora_linear_quant_batch(float *out, const float *x, const uint8_t *w, uint32_t type,
                            const float *bias, int m, int n_out, int n_in) {
     size_t rb;
-    size_t qb;
-    uint8_t *xq;
+    size_t qb = 0;
+    uint8_t *xq = NULL;
     int o;
     int t;
-    int k_quant;
+    int path; /* 0: Q8_0 activations, 1: Q8_K activations, 2: f32 */
     if (out == NULL || x == NULL || w == NULL || m <= 0 || n_out <= 0 || n_in <= 0) {
         return 0;
+    }
+    if (m == 1 && type == ORA_F32) {
+        linear_f32_one(out, x, (const float *)w, bias, n_out, n_in);
+        return 1;
     }
     rb = ora_row_bytes(type, n_in);
     if (rb == 0) {
         return 0;
     }
-    if (type == ORA_Q8_0) {
-        k_quant = 0;
+    if ((type == ORA_Q8_0 || type == ORA_Q4_0 || type == ORA_Q5_0) && n_in % QK32 == 0) {
+        path = 0;
         qb = ora_q8_0_nbytes(n_in);
-    } else if ((type == ORA_Q4_K || type == ORA_Q6_K) && n_in % QKK == 0) {
-        k_quant = 1;
+    } else if ((type == ORA_Q4_K || type == ORA_Q5_K || type == ORA_Q6_K) && n_in % QKK == 0) {
+        path = 1;
         qb = ora_q8_k_nbytes(n_in);
     } else {
-        return 0;
+        path = 2;
     }
-    xq = scratch_ensure((size_t)m * qb);
-    if (xq == NULL) {
-        return 0;
-    }
-    for (t = 0; t < m; t++) { /* quantize every token once, serially */
-        if (k_quant) {
-            ora_quantize_q8_k(x + (size_t)t * n_in, n_in, xq + (size_t)t * qb);
-        } else {
-            ora_quantize_q8_0(x + (size_t)t * n_in, n_in, xq + (size_t)t * qb);
+    if (path != 2) {
+        xq = scratch_ensure((size_t)m * qb);
+        if (xq == NULL) {
+            return 0;
+        }
+        for (t = 0; t < m; t++) { /* quantize every token once, serially */
+            if (path == 1) {
+                ora_quantize_q8_k(x + (size_t)t * n_in, n_in, xq + (size_t)t * qb);
+            } else {
+                ora_quantize_q8_0(x + (size_t)t * n_in, n_in, xq + (size_t)t * qb);
+            }
         }
     }
 #pragma omp parallel for schedule(static)
@@ -639,8 +975,14 @@ int ora_linear_quant_batch(float *out, const float *x, const uint8_t *w, uint32_
         float b = bias != NULL ? bias[o] : 0.0f;
         int tok;
         for (tok = 0; tok < m; tok++) {
-            const uint8_t *xt = xq + (size_t)tok * qb;
-            float dot = k_quant ? ora_dot_q8k(type, wr, xt, n_in) : ora_dot_q8(type, wr, xt, n_in);
+            float dot;
+            if (path == 0) {
+                dot = ora_dot_q8(type, wr, xq + (size_t)tok * qb, n_in);
+            } else if (path == 1) {
+                dot = ora_dot_q8k(type, wr, xq + (size_t)tok * qb, n_in);
+            } else {
+                dot = ora_dot_f32(type, wr, x + (size_t)tok * n_in, n_in);
+            }
             out[(size_t)tok * n_out + o] = b + dot;
         }
     }
@@ -657,7 +999,7 @@ uint32_t ora_logits(float *scores, const float *hidden, const uint8_t *w, uint32
     if (rb == 0 || vocab <= 0 || hidden == NULL || w == NULL) {
         return 0;
     }
-    if (type == ORA_Q8_0) { /* src/native.c:2317-2319: only Q8_0-family quantizes */
+    if (type == ORA_Q8_0 || type == ORA_Q4_0 || type == ORA_Q5_0) { /* src/native.c:2317-2319 */
         xq = (uint8_t *)malloc(ora_q8_0_nbytes(n_embd));
         if (xq == NULL || !ora_quantize_q8_0(hidden, n_embd, xq)) {
             free(xq);
@@ -779,6 +1121,65 @@ int ora_selftest(char *error, size_t error_size) {
         fused = ora_dot_q8(ORA_Q8_0, w, xq, QK32);
         if (fabsf(fused - 32.0f) > 0.5f) {
             snprintf(error, error_size, "q8_0 integer dot %.6f", fused);
+            return 0;
+        }
+        /* Q5_0 block of zero codes (value -16 each) against the same x */
+        memset(w, 0, B_Q5_0);
+        memcpy(w, &one, 2);
+        fused = ora_dot_q8(ORA_Q5_0, w, xq, QK32);
+        if (fabsf(fused + 512.0f) > 1.0f) {
+            snprintf(error, error_size, "q5_0 integer dot %.6f", fused);
+            return 0;
+        }
+    }
+    { /* Q4_0: low nibble 9 of element 0 -> value 1; x[0] = 3 */
+        uint8_t q40[B_Q4_0];
+        float x0[QK32];
+        float y0[QK32];
+        memset(q40, 0, sizeof(q40));
+        memset(x0, 0, sizeof(x0));
+        memcpy(q40, &one, 2);
+        q40[2] = 0x09;
+        x0[0] = 3.0f;
+        ora_dequantize(q40, ORA_Q4_0, QK32, y0);
+        expanded = 0.0f;
+        for (i = 0; i < QK32; i++) {
+            expanded += y0[i] * x0[i];
+        }
+        fused = ora_dot_f32(ORA_Q4_0, q40, x0, QK32);
+        if (fabsf(fused - expanded) > 1e-4f || fabsf(fused - 3.0f) > 1e-3f) {
+            snprintf(error, error_size, "q4_0 fused dot %.6f expanded %.6f", fused, expanded);
+            return 0;
+        }
+    }
+    { /* F16 row {1, 2} . {2, 3} = 8 */
+        uint8_t h[4];
+        float xh[2] = {2.0f, 3.0f};
+        uint16_t two = 0x4000;
+        memcpy(h, &one, 2);
+        memcpy(h + 2, &two, 2);
+        fused = ora_dot_f32(ORA_F16, h, xh, 2);
+        if (fabsf(fused - 8.0f) > 1e-3f) {
+            snprintf(error, error_size, "f16 dot %.6f", fused);
+            return 0;
+        }
+    }
+    { /* Q5_K: sc0 = 1, code 2 at element 0, x[0] = 3 -> 6 */
+        uint8_t q5[B_Q5_K];
+        memset(q5, 0, sizeof(q5));
+        memset(x, 0, sizeof(x));
+        memcpy(q5, &one, 2);
+        q5[4] = 1;
+        q5[48] = 0x02;
+        x[0] = 3.0f;
+        ora_dequantize(q5, ORA_Q5_K, QKK, y);
+        expanded = 0.0f;
+        for (i = 0; i < QKK; i++) {
+            expanded += y[i] * x[i];
+        }
+        fused = ora_dot_f32(ORA_Q5_K, q5, x, QKK);
+        if (fabsf(fused - expanded) > 1e-4f || fabsf(fused - 6.0f) > 1e-3f) {
+            snprintf(error, error_size, "q5_k fused dot %.6f expanded %.6f", fused, expanded);
             return 0;
         }
     }

@@ -2,7 +2,8 @@
  * edgexpu_oracle.h -- TEST INFRASTRUCTURE ONLY.
  *
  * A clean-room CPU restatement of tangjie133/edgexpu-llm's quantized-weight
- * matrix path (GGUF Q8_0 / Q4_K / Q6_K), used as the parity checker for the
+ * matrix path (GGUF Q8_0 / Q4_K / Q6_K, and the dispatcher's other formats
+ * Q4_0 / Q5_0 / Q5_K / F16 / F32), used as the parity checker for the
  * HIP kernels and as the "port" CPU baseline.  Nothing in the product links,
  * loads or calls this code; only tests/, the smoke entry and the bench's CPU
  * baseline leg do.
@@ -41,7 +42,8 @@ size_t ora_row_bytes(uint32_t type, int n);
 size_t ora_q8_0_nbytes(int n);
 size_t ora_q8_k_nbytes(int n);
 
-/* Bulk dequantization: src/gguf_quant.c:139-155, 212-302, 355-411.
+/* Bulk dequantization: src/gguf_quant.c:139-353 (F16, Q4_0, Q5_0, Q8_0, Q4_K,
+ * Q5_K, Q6_K), dispatched as in 355-411.
  * Returns 1 on success, 0 for a bad argument or unsupported type. */
 int ora_dequantize(const uint8_t *src, uint32_t type, uint64_t n, float *dst);
 
@@ -57,25 +59,31 @@ int ora_quantize_q8_k(const float *x, int n, uint8_t *dst);
 void ora_q8_0_block_lanes(const uint8_t *wblk, const uint8_t *xblk, int32_t lanes[8]);
 void ora_q4_k_block_lanes(const uint8_t *wsb, const uint8_t *xsb, int32_t lanes[8], int32_t mins[4]);
 void ora_q6_k_block_lanes(const uint8_t *wsb, const uint8_t *xsb, int32_t lanes[8]);
+/*   q4_0 / q5_0: lanes[u] = sum_{e=4u..4u+3} (c[e]-8 | c[e]-16) * x[e]   (gguf_dot_q8.c:552-568, 482-502)
+ *   q5_k: lanes[u] as q4_k with 5-bit codes; *mins = sum_k m[k]*(bs[2k]+bs[2k+1]) (gguf_dot_q8.c:772-838) */
+void ora_q4_0_block_lanes(const uint8_t *wblk, const uint8_t *xblk, int32_t lanes[8]);
+void ora_q5_0_block_lanes(const uint8_t *wblk, const uint8_t *xblk, int32_t lanes[8]);
+void ora_q5_k_block_lanes(const uint8_t *wsb, const uint8_t *xsb, int32_t lanes[8], int32_t *mins);
 
-/* Row dots against quantized activations: src/gguf_dot_q8.c:436-480, 603-666,
- * 897-963, dispatched as in 1004-1044. */
+/* Row dots against quantized activations: src/gguf_dot_q8.c:436-1002 (AVX2
+ * variants), dispatched as in 1004-1044. */
 float ora_dot_q8(uint32_t type, const uint8_t *wrow, const uint8_t *xq, int n);
 float ora_dot_q8k(uint32_t type, const uint8_t *wrow, const uint8_t *xq, int n);
 
-/* Row dots against f32 activations: src/gguf_quant.c:539-604, 606-670,
- * 704-794, dispatched as in 894-918. */
+/* Row dots against f32 activations: src/gguf_quant.c:506-892, dispatched as
+ * in 894-918 (F32, F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K). */
 float ora_dot_f32(uint32_t type, const uint8_t *wrow, const float *x, int n);
 
-/* The matvec / prefill driver: src/cpu_kernel.c:545-656 (OpenMP row loop,
- * activations quantized once per token).  Returns 0 on bad arguments or an
+/* The matvec / prefill driver: src/cpu_kernel.c:462-656 (OpenMP row loop,
+ * activations quantized once per token; F32 at one token through the
+ * edgexpu_cpu_linear arithmetic; F16 and other rows through the f32 dot).  Returns 0 on bad arguments or an
  * unsupported type, 1 otherwise. */
 int ora_linear_quant_batch(float *out, const float *x, const uint8_t *w, uint32_t type,
                            const float *bias, int m, int n_out, int n_in);
 
 /* Logits product of src/native.c:2292-2401: scores[i] = dot(W[i], h) (+ bias[i]),
- * with the Q8_0 activation path for Q8_0 weights and the f32 path for the
- * K-quants; rows processed in chunks of chunk_rows (0 = the 48 MiB budget of
+ * with the Q8_0 activation path for the Q8_0 family (Q4_0, Q5_0, Q8_0) and the
+ * f32 path for the others; rows processed in chunks of chunk_rows (0 = the 48 MiB budget of
  * include/edgexpu/scheduler.h:34).  Returns the greedy argmax (lowest index
  * on ties).  scores may be NULL. */
 uint32_t ora_logits(float *scores, const float *hidden, const uint8_t *w, uint32_t type,
@@ -93,7 +101,8 @@ void ora_silu(float *out, const float *x, int n);
 void ora_mul(float *out, const float *a, const float *b, int n);
 void ora_add(float *out, const float *a, const float *b, int n);
 
-/* Self-checks restated from src/gguf_quant.c:934-1061 (Q4_K/Q8_0 parts).
+/* Self-checks restated from src/gguf_quant.c:934-1061 (Q4_K, Q4_0, F16, Q5_K,
+ * Q8_0 and Q5_0 parts).
  * Returns 1 when they pass. */
 int ora_selftest(char *error, size_t error_size);
 

@@ -24,7 +24,8 @@ ORACLE_SO = os.path.join(HERE, "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libedgexpu_ref.so")
 
 F32, F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 2, 6, 8, 12, 13, 14
-BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+BLOCK = {F32: (1, 4), F16: (1, 2), Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34),
+         Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
 
 _u8p = C.POINTER(C.c_uint8)
 _f32p = C.POINTER(C.c_float)
@@ -118,6 +119,9 @@ class Oracle(_Lib, _Elementwise):
         self._l80 = L("ora_q8_0_block_lanes", None, [_u8p, _u8p, _i32p])
         self._l4k = L("ora_q4_k_block_lanes", None, [_u8p, _u8p, _i32p, _i32p])
         self._l6k = L("ora_q6_k_block_lanes", None, [_u8p, _u8p, _i32p])
+        self._l40 = L("ora_q4_0_block_lanes", None, [_u8p, _u8p, _i32p])
+        self._l50 = L("ora_q5_0_block_lanes", None, [_u8p, _u8p, _i32p])
+        self._l5k = L("ora_q5_k_block_lanes", None, [_u8p, _u8p, _i32p, _i32p])
         self._h2f = L("ora_fp16_to_fp32", C.c_float, [C.c_uint16])
         self._f2h = L("ora_fp32_to_fp16", C.c_uint16, [C.c_float])
         self._self = L("ora_selftest", C.c_int, [C.c_char_p, C.c_size_t])
@@ -163,6 +167,12 @@ class Oracle(_Lib, _Elementwise):
             self._l4k(_p(wblk, _u8p), _p(xblk, _u8p), _p(lanes, _i32p), _p(mins, _i32p))
         elif qtype == Q6_K:
             self._l6k(_p(wblk, _u8p), _p(xblk, _u8p), _p(lanes, _i32p))
+        elif qtype == Q4_0:
+            self._l40(_p(wblk, _u8p), _p(xblk, _u8p), _p(lanes, _i32p))
+        elif qtype == Q5_0:
+            self._l50(_p(wblk, _u8p), _p(xblk, _u8p), _p(lanes, _i32p))
+        elif qtype == Q5_K:
+            self._l5k(_p(wblk, _u8p), _p(xblk, _u8p), _p(lanes, _i32p), _p(mins, _i32p))
         else:
             raise ValueError(qtype)
         return lanes, mins

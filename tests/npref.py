@@ -58,6 +58,35 @@ def q6_k_parts(sb: np.ndarray):
     return d, sc, codes.reshape(-1, 256)
 
 
+def q4_0_parts(blocks: np.ndarray):
+    """[nb, 18] -> d [nb]; signed values c - 8 [nb, 32] (low nibbles first)."""
+    b = blocks.reshape(-1, 18)
+    qs = b[:, 2:].astype(np.int64)
+    return f16(b[:, 0:2]), np.concatenate([qs & 15, qs >> 4], axis=1) - 8
+
+
+def q5_0_parts(blocks: np.ndarray):
+    """[nb, 22] -> d [nb]; signed values c - 16 [nb, 32]; bit e of qh is the
+    fifth bit of element e."""
+    b = blocks.reshape(-1, 22)
+    qh = b[:, 2:6].copy().view(np.uint32).astype(np.int64)       # [nb, 1]
+    qs = b[:, 6:].astype(np.int64)
+    nib = np.concatenate([qs & 15, qs >> 4], axis=1)
+    hb = (qh >> np.arange(32)[None, :]) & 1
+    return f16(b[:, 0:2]), (nib | (hb << 4)) - 16
+
+
+def q5_k_parts(sb: np.ndarray):
+    """[nb, 176] -> d, dmin; sc, m [nb, 8]; codes [nb, 256] (0..31).  Chunk j
+    takes bit 2j (first 32 elements) and 2j+1 (next 32) of qh[l]."""
+    s = sb.reshape(-1, 176)
+    as_q4 = np.concatenate([s[:, 0:16], s[:, 48:176]], axis=1)   # same header + qs layout as Q4_K
+    d, dmin, sc, m, codes = q4_k_parts(as_q4)
+    qh = s[:, 16:48].astype(np.int64)                              # [nb, l]
+    hb = np.stack([(qh >> (2 * j + h)) & 1 for j in range(4) for h in range(2)], axis=1)   # [nb, 8, l]
+    return d, dmin, sc, m, codes + 16 * hb.reshape(-1, 256)
+
+
 # ------------------------------------------------------------ dequant
 
 
@@ -77,6 +106,21 @@ def dequant(qtype: int, src: np.ndarray) -> np.ndarray:
         ds = (d[:, None] * sc.astype(f32)).astype(f32)        # [nb, 16]
         sub = np.repeat(np.arange(16), 16)
         return (ds[:, sub] * (codes - 32).astype(f32)).astype(f32).reshape(-1)
+    if qtype == 2:   # ((float)c - 8) * d
+        d, v = q4_0_parts(src)
+        return (v.astype(f32) * d[:, None]).astype(f32).reshape(-1)
+    if qtype == 6:   # (float)(c - 16) * d
+        d, v = q5_0_parts(src)
+        return (v.astype(f32) * d[:, None]).astype(f32).reshape(-1)
+    if qtype == 13:  # (d*sc) * c - (dmin*m)
+        d, dmin, sc, m, codes = q5_k_parts(src)
+        ds = (d[:, None] * sc.astype(f32)).astype(f32)
+        ms = (dmin[:, None] * m.astype(f32)).astype(f32)
+        sub = np.repeat(np.arange(8), 32)
+        prod = (ds[:, sub] * codes.astype(f32)).astype(f32)
+        return (prod - ms[:, sub]).astype(f32).reshape(-1)
+    if qtype == 1:
+        return np.ascontiguousarray(src).view(np.float16).astype(f32).reshape(-1)
     raise ValueError(qtype)
 
 
@@ -158,6 +202,28 @@ def q6_k_lanes(wsb, xsb):
     return np.array(lanes)
 
 
+def q4_0_lanes(wblk, xblk):
+    _, v = q4_0_parts(wblk)
+    _, qx = q8_0_parts(xblk)
+    return (v[0] * qx[0]).reshape(8, 4).sum(axis=1)
+
+
+def q5_0_lanes(wblk, xblk):
+    _, v = q5_0_parts(wblk)
+    _, qx = q8_0_parts(xblk)
+    return (v[0] * qx[0]).reshape(8, 4).sum(axis=1)
+
+
+def q5_k_lanes(wsb, xsb):
+    """(lanes[8], min total) of one Q5_K super-block against Q8_K."""
+    _, _, sc, m, codes = q5_k_parts(wsb)
+    q8 = xsb[4:260].view(np.int8).astype(np.int64)
+    bs = xsb[260:292].view(np.int16).astype(np.int64)
+    e = np.arange(256)
+    lanes = np.array([np.sum((sc[0][e // 32] * codes[0] * q8)[((e % 32) // 4) == u]) for u in range(8)])
+    return lanes, int((m[0] * bs.reshape(8, 2).sum(axis=1)).sum())
+
+
 # ------------------------------------------------------------ f64 results + scale
 
 
@@ -168,8 +234,8 @@ def q8_dot_f64(qtype: int, wrow: np.ndarray, xq: np.ndarray):
     sum_k |dx*dw*sc*q_k*q8_k| (+ sum_k |dx*dmin*m*q8_k| for Q4_K): any fp32
     summation order of the row, the reference's AVX2 lanes included, stays
     within a few ulp of S."""
-    if qtype == 8:
-        dw, qw = q8_0_parts(wrow)
+    if qtype in (2, 6, 8):
+        dw, qw = {2: q4_0_parts, 6: q5_0_parts, 8: q8_0_parts}[qtype](wrow)
         dx, qx = q8_0_parts(xq)
         isum = (qw * qx).sum(axis=1)
         scale = dw.astype(np.float64) * dx.astype(np.float64)
@@ -178,8 +244,8 @@ def q8_dot_f64(qtype: int, wrow: np.ndarray, xq: np.ndarray):
     dx = xb[:, 0:4].copy().view(np.float32)[:, 0].astype(np.float64)
     q8 = xb[:, 4:260].view(np.int8).astype(np.int64)
     bs = xb[:, 260:292].copy().view(np.int16).astype(np.int64)
-    if qtype == 12:
-        d, dmin, sc, m, codes = q4_k_parts(wrow)
+    if qtype in (12, 13):
+        d, dmin, sc, m, codes = (q4_k_parts if qtype == 12 else q5_k_parts)(wrow)
         sub = np.repeat(np.arange(8), 32)
         isum = (sc[:, sub] * codes * q8).sum(axis=1)
         imin = (m * bs.reshape(-1, 8, 2).sum(axis=2)).sum(axis=1)
