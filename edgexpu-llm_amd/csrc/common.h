@@ -5,7 +5,10 @@
 // Block byte maps (little-endian), as laid out by the reference
 // (src/gguf_quant.c:17-26,138-302; src/gguf_dot_q8.c:18-26,98-110):
 //   Q8_0  34 B / 32 elem : fp16 d | int8 q[32]
+//   Q4_0  18 B / 32 elem : fp16 d | qs[16] (element j low nibble, j+16 high; value c-8)
+//   Q5_0  22 B / 32 elem : fp16 d | u32 qh (bit e = fifth bit of element e) | qs[16] (value c-16)
 //   Q4_K 144 B / 256 elem: fp16 d | fp16 dmin | scales[12] (6-bit sc/m) | qs[128]
+//   Q5_K 176 B / 256 elem: fp16 d | fp16 dmin | scales[12] | qh[32] | qs[128] (chunk j: bits 2j, 2j+1 of qh[l])
 //   Q6_K 210 B / 256 elem: ql[128] | qh[64] | int8 sc[16] | fp16 d
 //   Q8_K 292 B / 256 elem: f32 d | int8 q[256] | int16 bsums[16]
 #pragma once
@@ -16,16 +19,28 @@
 namespace exq {
 
 constexpr int kTypeF32 = 0;
+constexpr int kTypeF16 = 1;
+constexpr int kTypeQ4_0 = 2;
+constexpr int kTypeQ5_0 = 6;
 constexpr int kTypeQ8_0 = 8;
 constexpr int kTypeQ4_K = 12;
+constexpr int kTypeQ5_K = 13;
 constexpr int kTypeQ6_K = 14;
 
 constexpr int kQK8_0 = 32;
 constexpr int kQKK = 256;
 constexpr int kBytesQ8_0 = 34;
+constexpr int kBytesQ4_0 = 18;
+constexpr int kBytesQ5_0 = 22;
 constexpr int kBytesQ4_K = 144;
+constexpr int kBytesQ5_K = 176;
 constexpr int kBytesQ6_K = 210;
 constexpr int kBytesQ8_K = 292;
+
+// Activation families of the reference's dispatcher (src/gguf_dot_q8.c:414-434):
+// Q4_0 / Q5_0 / Q8_0 rows take Q8_0 activations, the K-quants Q8_K.
+__host__ __device__ constexpr bool q8_0_family(int t) { return t == kTypeQ8_0 || t == kTypeQ4_0 || t == kTypeQ5_0; }
+__host__ __device__ constexpr bool k_family(int t) { return t == kTypeQ4_K || t == kTypeQ5_K || t == kTypeQ6_K; }
 
 // Loads that tolerate the 2-byte alignment of Q8_0 / Q6_K blocks: gfx950
 // global memory runs in unaligned-access mode, so these become plain

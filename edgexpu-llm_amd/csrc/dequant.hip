@@ -8,6 +8,10 @@
 //   Q8_0  y = d * q                                  (src/gguf_quant.c:152)
 //   Q4_K  y = (d*sc) * q - (dmin*m)                  (src/gguf_quant.c:251-260)
 //   Q6_K  y = (d*sc) * (q-32)                        (src/gguf_quant.c:291-294)
+//   Q4_0  y = ((float)c - 8) * d                     (src/gguf_quant.c:205-206)
+//   Q5_0  y = (float)(c - 16) * d                    (src/gguf_quant.c:176-177)
+//   Q5_K  y = (d*sc) * c - (dmin*m)                  (src/gguf_quant.c:339-343)
+//   F16   y = (float)h                               (src/gguf_quant.c:183-191)
 #include "common.h"
 
 namespace exq {
@@ -108,6 +112,112 @@ __global__ __launch_bounds__(256) void dequant_q6_k_kernel(const uint8_t *__rest
     store8(dst + b * kQKK + 8 * p, y);
 }
 
+// 4 threads per 18-byte Q4_0 block; thread p covers elements 8p..8p+7: the
+// low (p < 2) or high nibbles of qs[8(p&1) .. 8(p&1)+7].
+__global__ __launch_bounds__(256) void dequant_q4_0_kernel(const uint8_t *__restrict__ src,
+                                                           long long n_threads, float *__restrict__ dst) {
+    const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_threads) return;
+    const long long b = t >> 2;
+    const int p = (int)(t & 3);
+    const uint8_t *blk = src + b * kBytesQ4_0;
+    const float d = f16_bits_to_f32(ldg_unaligned<uint16_t>(blk));
+    const uint2 q = ldg8(blk + 2 + 8 * (p & 1));
+    const int shift = (p >> 1) * 4;
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t w = e < 4 ? q.x : q.y;
+        const int c = (int)((w >> (8 * (e & 3) + shift)) & 0x0fu);
+        y[e] = ((float)c - 8.0f) * d;
+    }
+    store8(dst + b * kQK8_0 + 8 * p, y);
+}
+
+// 4 threads per 22-byte Q5_0 block, elements as Q4_0; the fifth bit of
+// element e is bit e of the block's qh word.
+__global__ __launch_bounds__(256) void dequant_q5_0_kernel(const uint8_t *__restrict__ src,
+                                                           long long n_threads, float *__restrict__ dst) {
+    const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_threads) return;
+    const long long b = t >> 2;
+    const int p = (int)(t & 3);
+    const uint8_t *blk = src + b * kBytesQ5_0;
+    const float d = f16_bits_to_f32(ldg_unaligned<uint16_t>(blk));
+    const uint32_t qh = ldg_unaligned<uint32_t>(blk + 2) >> (8 * p);
+    const uint2 q = ldg8(blk + 6 + 8 * (p & 1));
+    const int shift = (p >> 1) * 4;
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t w = e < 4 ? q.x : q.y;
+        const int c = (int)((w >> (8 * (e & 3) + shift)) & 0x0fu) | (int)(((qh >> e) & 1u) << 4);
+        y[e] = (float)(c - 16) * d;
+    }
+    store8(dst + b * kQK8_0 + 8 * p, y);
+}
+
+// 32 threads per 176-byte Q5_K super-block; thread p covers elements
+// 8p..8p+7 of sub-block s = p/4 (64-chunk j = s/2, nibble half s&1), whose
+// fifth bits are bit s of qh[8(p&3) .. 8(p&3)+7].
+__global__ __launch_bounds__(256) void dequant_q5_k_kernel(const uint8_t *__restrict__ src,
+                                                           long long n_threads, float *__restrict__ dst) {
+    const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_threads) return;
+    const long long b = t >> 5;
+    const int p = (int)(t & 31);
+    const uint8_t *sb = src + b * kBytesQ5_K;
+    const uint4 h = ldg16(sb);  // d, dmin, scales[12]
+    const float d = f16_bits_to_f32(h.x & 0xffffu);
+    const float dmin = f16_bits_to_f32(h.x >> 16);
+    const int s = p >> 2;
+    const uint32_t sw[3] = {h.y, h.z, h.w};
+    auto byte_at = [&](int i) -> int { return (int)((sw[i >> 2] >> (8 * (i & 3))) & 0xffu); };
+    int sc, mn;
+    if (s < 4) {
+        sc = byte_at(s) & 63;
+        mn = byte_at(s + 4) & 63;
+    } else {
+        sc = (byte_at(s + 4) & 0x0f) | ((byte_at(s - 4) >> 6) << 4);
+        mn = (byte_at(s + 4) >> 4) | ((byte_at(s) >> 6) << 4);
+    }
+    const float ds = d * (float)sc;
+    const float ms = dmin * (float)mn;
+    const int j = s >> 1;
+    const int shift = (s & 1) * 4;
+    const uint2 q = ldg8(sb + 48 + 32 * j + 8 * (p & 3));
+    const uint2 qh = ldg8(sb + 16 + 8 * (p & 3));
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t w = e < 4 ? q.x : q.y;
+        const uint32_t wh = e < 4 ? qh.x : qh.y;
+        const int c = (int)((w >> (8 * (e & 3) + shift)) & 0x0fu) + (int)(((wh >> (8 * (e & 3) + s)) & 1u) << 4);
+        const float prod = ds * (float)c;
+        y[e] = prod - ms;
+    }
+    store8(dst + b * kQKK + 8 * p, y);
+}
+
+// F16: one thread per 8 elements (the last thread of an n not divisible by
+// 8 converts the remainder one by one).
+__global__ __launch_bounds__(256) void dequant_f16_kernel(const uint8_t *__restrict__ src, long long n,
+                                                          float *__restrict__ dst) {
+    const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long e0 = 8 * t;
+    if (e0 >= n) return;
+    if (e0 + 8 <= n) {
+        const uint4 v = ldg16(src + 2 * e0);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = f16_bits_to_f32((w[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+        store8(dst + e0, y);
+    } else {
+        for (long long e = e0; e < n; ++e) dst[e] = f16_bits_to_f32(ldg_unaligned<uint16_t>(src + 2 * e));
+    }
+}
+
 }  // namespace exq
 
 using namespace exq;
@@ -129,6 +239,22 @@ hipError_t launch_dequantize(const uint8_t *src, int type, unsigned long long n,
             threads = (long long)(n / kQKK) * 32;
             hipLaunchKernelGGL(dequant_q6_k_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, src,
                                threads, dst);
+            break;
+        case kTypeQ4_0:
+        case kTypeQ5_0:
+            threads = (long long)(n / kQK8_0) * 4;
+            hipLaunchKernelGGL(type == kTypeQ4_0 ? dequant_q4_0_kernel : dequant_q5_0_kernel,
+                               dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, src, threads, dst);
+            break;
+        case kTypeQ5_K:
+            threads = (long long)(n / kQKK) * 32;
+            hipLaunchKernelGGL(dequant_q5_k_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, src,
+                               threads, dst);
+            break;
+        case kTypeF16:
+            threads = (long long)((n + 7) / 8);
+            hipLaunchKernelGGL(dequant_f16_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, src,
+                               (long long)n, dst);
             break;
         default:
             return hipErrorInvalidValue;

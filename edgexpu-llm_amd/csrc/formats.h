@@ -7,6 +7,10 @@
 //   Q4_K x Q8_K  -- dot_q4_k_q8_k  src/gguf_dot_q8.c:603-762
 //   Q6_K x Q8_K  -- dot_q6_k_q8_k  src/gguf_dot_q8.c:897-1002
 //   Q4_K/Q6_K/Q8_0 x f32 -- dot_q4_k / dot_q6_k / dot_q8_0, src/gguf_quant.c:539-794
+//   Q4_0 / Q5_0 x Q8_0 -- dot_q4_0_q8_0 / dot_q5_0_q8_0, src/gguf_dot_q8.c:482-601
+//   Q5_K x Q8_K  -- dot_q5_k_q8_k  src/gguf_dot_q8.c:764-895
+//   Q4_0/Q5_0/Q5_K/F16 x f32 -- dot_q4_0 / dot_q5_0 / dot_q5_k / dot_f16,
+//                   src/gguf_quant.c:672-702, 796-892
 //
 // Integer block sums are exact (sdot4 on the int8 codes); their fp32
 // combination differs from the reference only in summation order.
@@ -271,6 +275,172 @@ struct FmtQ80 {
     }
 };
 
+// ------------------------------------------------------- Q4_0 / Q5_0 / Q5_K
+
+// Q8_0 activation slice plus its code sum: the 4- and 5-bit formats store
+// unsigned codes c with value c - 8 (Q4_0) or c - 16 (Q5_0), so a block's
+// integer sum is sum(c * q8) - off * sum(q8), both with sdot4 on codes that
+// fit a signed byte.
+struct ActQ80S {
+    uint32_t q[8];
+    float dx;
+    int sx;  // sum of the 32 int8 codes
+};
+
+template <class A>
+__device__ static void load_act_q80s(const A &a, int unit, int tk, ActQ80S &x) {
+    FmtQ80::Act t;
+    FmtQ80::load_act(a, unit, tk, t);
+    int sx = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        x.q[k] = t.q[k];
+        sx = sdot4(0x01010101u, t.q[k], sx);
+    }
+    x.dx = t.dx;
+    x.sx = sx;
+}
+
+__device__ static void load_act_lds_q80s(const ActLds &s, int unit, int tk, ActQ80S &x) {
+    FmtQ80::Act t;
+    FmtQ80::load_act_lds(s, unit, tk, t);
+    int sx = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        x.q[k] = t.q[k];
+        sx = sdot4(0x01010101u, t.q[k], sx);
+    }
+    x.dx = t.dx;
+    x.sx = sx;
+}
+
+// Q4_0 rows against Q8_0 activations.  Unit = one 18-byte block: dword k of
+// qs holds elements 4k..4k+3 (low nibbles) and 16+4k..16+4k+3 (high).
+struct FmtQ40 {
+    static constexpr int kUnitsPerBlock = 1;
+    using Act = ActQ80S;
+    template <class A>
+    __device__ static void load_act(const A &a, int unit, int tk, Act &x) { load_act_q80s(a, unit, tk, x); }
+    __device__ static void load_act_lds(const ActLds &s, int unit, int tk, Act &x) { load_act_lds_q80s(s, unit, tk, x); }
+    struct W {
+        uint4 q;
+        uint32_t d;
+    };
+    template <class A>
+    __device__ static void load_w(const A &a, int row, int unit, W &w) {
+        const uint8_t *blk = a.w + (size_t)row * a.row_bytes + (size_t)unit * kBytesQ4_0;
+        w.d = ldg_unaligned<uint16_t>(blk);
+        w.q = ldg16(blk + 2);
+    }
+    __device__ static void dot1(const W &w, int, const Act &xa, float &acc) {
+        const float d = f16_bits_to_f32(w.d);
+        const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+        int s = -8 * xa.sx;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            s = sdot4(q[k] & 0x0f0f0f0fu, xa.q[k], s);
+            s = sdot4((q[k] >> 4) & 0x0f0f0f0fu, xa.q[4 + k], s);
+        }
+        acc = fmaf(d * xa.dx, (float)s, acc);
+    }
+};
+
+// Four bits t (0..15) to bit 4 of four bytes: the multiplier's shifted copies
+// of t do not overlap, so the product is their OR.
+__device__ __forceinline__ uint32_t spread4_bit4(uint32_t t) { return (t * 0x02040810u) & 0x10101010u; }
+
+// Q5_0 rows against Q8_0 activations.  Unit = one 22-byte block; the fifth
+// bit of element e is bit e of qh.
+struct FmtQ50 {
+    static constexpr int kUnitsPerBlock = 1;
+    using Act = ActQ80S;
+    template <class A>
+    __device__ static void load_act(const A &a, int unit, int tk, Act &x) { load_act_q80s(a, unit, tk, x); }
+    __device__ static void load_act_lds(const ActLds &s, int unit, int tk, Act &x) { load_act_lds_q80s(s, unit, tk, x); }
+    struct W {
+        uint4 q;
+        uint32_t qh;
+        uint32_t d;
+    };
+    template <class A>
+    __device__ static void load_w(const A &a, int row, int unit, W &w) {
+        const uint8_t *blk = a.w + (size_t)row * a.row_bytes + (size_t)unit * kBytesQ5_0;
+        w.d = ldg_unaligned<uint16_t>(blk);
+        w.qh = ldg_unaligned<uint32_t>(blk + 2);
+        w.q = ldg16(blk + 6);
+    }
+    __device__ static void dot1(const W &w, int, const Act &xa, float &acc) {
+        const float d = f16_bits_to_f32(w.d);
+        const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+        int s = -16 * xa.sx;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t lo = (q[k] & 0x0f0f0f0fu) | spread4_bit4((w.qh >> (4 * k)) & 0xfu);
+            const uint32_t hi = ((q[k] >> 4) & 0x0f0f0f0fu) | spread4_bit4((w.qh >> (16 + 4 * k)) & 0xfu);
+            s = sdot4(lo, xa.q[k], s);
+            s = sdot4(hi, xa.q[4 + k], s);
+        }
+        acc = fmaf(d * xa.dx, (float)s, acc);
+    }
+};
+
+// Q5_K rows against Q8_K activations.  Unit = (super-block i, 64-chunk j) as
+// Q4_K; the 32 qh bytes hold the fifth bits of chunk j at bits 2j (first 32
+// elements) and 2j+1 (next 32).
+struct FmtQ5K {
+    static constexpr int kUnitsPerBlock = 4;
+    using Act = FmtQ4K::Act;
+    template <class A>
+    __device__ static void load_act(const A &a, int unit, int tk, Act &x) { FmtQ4K::load_act(a, unit, tk, x); }
+    __device__ static void load_act_lds(const ActLds &s, int unit, int tk, Act &x) {
+        FmtQ4K::load_act_lds(s, unit, tk, x);
+    }
+    struct W {
+        uint4 h, q0, q1, h0, h1;
+    };
+    template <class A>
+    __device__ static void load_w(const A &a, int row, int unit, W &w) {
+        const int i = unit >> 2, j = unit & 3;
+        const uint8_t *sb = a.w + (size_t)row * a.row_bytes + (size_t)i * kBytesQ5_K;
+        w.h = ldg16(sb);
+        w.h0 = ldg16(sb + 16);
+        w.h1 = ldg16(sb + 32);
+        w.q0 = ldg16(sb + 48 + 32 * j);
+        w.q1 = ldg16(sb + 64 + 32 * j);
+    }
+    __device__ static void dot1(const W &w, int unit, const Act &xa, float &acc) {
+        const int j = unit & 3;
+        const float d = f16_bits_to_f32(w.h.x & 0xffffu);
+        const float dmin = f16_bits_to_f32(w.h.x >> 16);
+        // six-bit scale/min pairs of sub-blocks 2j, 2j+1, as Q4_K
+        const int sh = 16 * (j & 1);
+        uint32_t scp, mp;
+        if (j < 2) {
+            scp = (w.h.y >> sh) & 0x3f3fu;
+            mp = (w.h.z >> sh) & 0x3f3fu;
+        } else {
+            scp = ((w.h.w >> sh) & 0x0f0fu) | (((w.h.y >> sh) >> 2) & 0x3030u);
+            mp = (((w.h.w >> sh) >> 4) & 0x0f0fu) | (((w.h.z >> sh) >> 2) & 0x3030u);
+        }
+        const int sc0 = (int)(scp & 0xffu), sc1 = (int)(scp >> 8);
+        const uint32_t mpair = (mp & 0xffu) | ((mp & 0xff00u) << 8);
+        const uint32_t qw[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+        const uint32_t hw[8] = {w.h0.x, w.h0.y, w.h0.z, w.h0.w, w.h1.x, w.h1.y, w.h1.z, w.h1.w};
+        int dlo = 0, dhi = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t lo = (qw[k] & 0x0f0f0f0fu) | (((hw[k] >> (2 * j)) & 0x01010101u) << 4);
+            const uint32_t hi = ((qw[k] >> 4) & 0x0f0f0f0fu) | (((hw[k] >> (2 * j + 1)) & 0x01010101u) << 4);
+            dlo = sdot4(lo, xa.q[k], dlo);
+            dhi = sdot4(hi, xa.q[8 + k], dhi);
+        }
+        const int isum = sc0 * dlo + sc1 * dhi;
+        const int imin = sdot2(mpair, xa.spair, 0);
+        acc = fmaf(xa.dx * d, (float)isum, acc);
+        acc = fmaf(-(xa.dx * dmin), (float)imin, acc);
+    }
+};
+
 // ------------------------------------------------------------ f32 activations
 
 // Q4_K weights against f32 activations (logits path, dot_q4_k).
@@ -441,6 +611,149 @@ struct FmtQ80F32 {
             }
             acc = fmaf(d, s, acc);
         }
+    }
+};
+
+// 32-float activation slice of one 32-element unit (the f32 paths below).
+struct ActF32x32 {
+    float x[32];
+};
+
+template <class A>
+__device__ static void load_act_f32x32(const A &a, int unit, int tk, ActF32x32 &x) {
+    const float4 *p = reinterpret_cast<const float4 *>(a.xf + (size_t)tk * a.K + 32 * unit);
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+        const float4 t = p[v];
+        x.x[4 * v] = t.x; x.x[4 * v + 1] = t.y; x.x[4 * v + 2] = t.z; x.x[4 * v + 3] = t.w;
+    }
+}
+
+// Q4_0 / Q5_0 rows against f32 activations (dot_q4_0, dot_q5_0).  Unit = one block.
+struct FmtQ40F32 {
+    static constexpr int kUnitsPerBlock = 1;
+    using Act = ActF32x32;
+    template <class A>
+    __device__ static void load_act(const A &a, int unit, int tk, Act &x) { load_act_f32x32(a, unit, tk, x); }
+    using W = FmtQ40::W;
+    template <class A>
+    __device__ static void load_w(const A &a, int row, int unit, W &w) { FmtQ40::load_w(a, row, unit, w); }
+    __device__ static void dot1(const W &w, int, const Act &xa, float &acc) {
+        const float d = f16_bits_to_f32(w.d);
+        const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+        float s = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t c = (q[k] >> (8 * e)) & 0xffu;
+                s = fmaf((float)(int)(c & 0x0fu) - 8.0f, xa.x[4 * k + e], s);
+                s = fmaf((float)(int)(c >> 4) - 8.0f, xa.x[16 + 4 * k + e], s);
+            }
+        }
+        acc = fmaf(d, s, acc);
+    }
+};
+
+struct FmtQ50F32 {
+    static constexpr int kUnitsPerBlock = 1;
+    using Act = ActF32x32;
+    template <class A>
+    __device__ static void load_act(const A &a, int unit, int tk, Act &x) { load_act_f32x32(a, unit, tk, x); }
+    using W = FmtQ50::W;
+    template <class A>
+    __device__ static void load_w(const A &a, int row, int unit, W &w) { FmtQ50::load_w(a, row, unit, w); }
+    __device__ static void dot1(const W &w, int, const Act &xa, float &acc) {
+        const float d = f16_bits_to_f32(w.d);
+        const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+        float s = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int l = 4 * k + e;
+                const uint32_t c = (q[k] >> (8 * e)) & 0xffu;
+                const int c0 = (int)(c & 0x0fu) | (int)(((w.qh >> l) & 1u) << 4);
+                const int c1 = (int)(c >> 4) | (int)(((w.qh >> (l + 16)) & 1u) << 4);
+                s = fmaf((float)(c0 - 16), xa.x[l], s);
+                s = fmaf((float)(c1 - 16), xa.x[16 + l], s);
+            }
+        }
+        acc = fmaf(d, s, acc);
+    }
+};
+
+// F16 rows against f32 activations (dot_f16).  Unit = 32 elements (64 bytes).
+struct FmtF16F32 {
+    static constexpr int kUnitsPerBlock = 1;
+    using Act = ActF32x32;
+    template <class A>
+    __device__ static void load_act(const A &a, int unit, int tk, Act &x) { load_act_f32x32(a, unit, tk, x); }
+    struct W {
+        uint4 v[4];
+    };
+    template <class A>
+    __device__ static void load_w(const A &a, int row, int unit, W &w) {
+        const uint8_t *p = a.w + (size_t)row * a.row_bytes + (size_t)unit * 64;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w.v[k] = ldg16(p + 16 * k);
+    }
+    __device__ static void dot1(const W &w, int, const Act &xa, float &acc) {
+        float s = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t u[4] = {w.v[k].x, w.v[k].y, w.v[k].z, w.v[k].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                s = fmaf(f16_bits_to_f32(u[e] & 0xffffu), xa.x[8 * k + 2 * e], s);
+                s = fmaf(f16_bits_to_f32(u[e] >> 16), xa.x[8 * k + 2 * e + 1], s);
+            }
+        }
+        acc += s;
+    }
+};
+
+// Q5_K rows against f32 activations (dot_q5_k).  Unit = (super-block i,
+// 64-chunk j) with the 64-float slice and its two 32-element sums, as Q4_K.
+struct FmtQ5KF32 {
+    static constexpr int kUnitsPerBlock = 4;
+    using Act = FmtQ4KF32::Act;
+    template <class A>
+    __device__ static void load_act(const A &a, int unit, int tk, Act &x) { FmtQ4KF32::load_act(a, unit, tk, x); }
+    using W = FmtQ5K::W;
+    template <class A>
+    __device__ static void load_w(const A &a, int row, int unit, W &w) { FmtQ5K::load_w(a, row, unit, w); }
+    __device__ static void dot1(const W &w, int unit, const Act &xa, float &acc) {
+        const int j = unit & 3;
+        const float d = f16_bits_to_f32(w.h.x & 0xffffu);
+        const float dmin = f16_bits_to_f32(w.h.x >> 16);
+        const int sh = 16 * (j & 1);
+        uint32_t scp, mp;
+        if (j < 2) {
+            scp = (w.h.y >> sh) & 0x3f3fu;
+            mp = (w.h.z >> sh) & 0x3f3fu;
+        } else {
+            scp = ((w.h.w >> sh) & 0x0f0fu) | (((w.h.y >> sh) >> 2) & 0x3030u);
+            mp = (((w.h.w >> sh) >> 4) & 0x0f0fu) | (((w.h.z >> sh) >> 2) & 0x3030u);
+        }
+        const float d1 = d * (float)(scp & 0xffu), d2 = d * (float)(scp >> 8);
+        const float m1 = dmin * (float)(mp & 0xffu), m2 = dmin * (float)(mp >> 8);
+        const uint32_t qw[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+        const uint32_t hw[8] = {w.h0.x, w.h0.y, w.h0.z, w.h0.w, w.h1.x, w.h1.y, w.h1.z, w.h1.w};
+        float qlo = 0.0f, qhi = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t lo = (qw[k] & 0x0f0f0f0fu) | (((hw[k] >> (2 * j)) & 0x01010101u) << 4);
+            const uint32_t hi = ((qw[k] >> 4) & 0x0f0f0f0fu) | (((hw[k] >> (2 * j + 1)) & 0x01010101u) << 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                qlo = fmaf((float)((lo >> (8 * e)) & 0xffu), xa.x[4 * k + e], qlo);
+                qhi = fmaf((float)((hi >> (8 * e)) & 0xffu), xa.x[32 + 4 * k + e], qhi);
+            }
+        }
+        float r = d1 * qlo - m1 * xa.sx0;
+        r += d2 * qhi - m2 * xa.sx1;
+        acc += r;
     }
 };
 

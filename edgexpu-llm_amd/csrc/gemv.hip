@@ -6,6 +6,9 @@
 //   Q6_K x Q8_K  -- dot_q6_k_q8_k  src/gguf_dot_q8.c:897-1002
 //   Q4_K/Q6_K/Q8_0 x f32 -- dot_q4_k / dot_q6_k / dot_q8_0, src/gguf_quant.c:539-794
 //     (the logits product of src/native.c:445-514 for K-quant output weights)
+//   Q4_0 / Q5_0 x Q8_0, Q5_K x Q8_K, and Q4_0 / Q5_0 / Q5_K / F16 x f32: the
+//     dispatcher's other formats (src/gguf_dot_q8.c:482-601, 764-895;
+//     src/gguf_quant.c:672-702, 796-892)
 //
 // Work decomposition.  A row's K range is cut into U "units" (64 elements of
 // one super-block for the K-quants, one 32-element block for Q8_0).  A
@@ -166,14 +169,18 @@ hipError_t launch_gemv_q8(int type, const uint8_t *w, size_t row_bytes, int n_ou
     a.ldo = ldo;
     switch (type) {
         case kTypeQ8_0: a.nblk = K / kQK8_0; return launch_m<FmtQ80>(a, st);
+        case kTypeQ4_0: a.nblk = K / kQK8_0; return launch_m<FmtQ40>(a, st);
+        case kTypeQ5_0: a.nblk = K / kQK8_0; return launch_m<FmtQ50>(a, st);
         case kTypeQ4_K: a.nblk = K / kQKK; return launch_m<FmtQ4K>(a, st);
+        case kTypeQ5_K: a.nblk = K / kQKK; return launch_m<FmtQ5K>(a, st);
         case kTypeQ6_K: a.nblk = K / kQKK; return launch_m<FmtQ6K>(a, st);
         default: return hipErrorInvalidValue;
     }
 }
 
-// f32-activation GEMV over m <= 8 rows of x (logits path).  xs holds the
-// 16-element sums of x ([m][K/16]); unused for Q8_0.
+// f32-activation GEMV over m <= 8 rows of x (logits path, F16 rows, the
+// per-row f32 dots).  xs holds the 16-element sums of x ([m][K/16]); read
+// only by the K-quant formats.  F16 rows need K % 32 == 0.
 hipError_t launch_gemv_f32(int type, const uint8_t *w, size_t row_bytes, int n_out, int K, int m,
                            const float *xf, const float *xs, const float *bias, float *out, int ldo,
                            hipStream_t st) {
@@ -190,7 +197,11 @@ hipError_t launch_gemv_f32(int type, const uint8_t *w, size_t row_bytes, int n_o
     a.ldo = ldo;
     switch (type) {
         case kTypeQ8_0: a.nblk = K / kQK8_0; return launch_m<FmtQ80F32>(a, st);
+        case kTypeQ4_0: a.nblk = K / kQK8_0; return launch_m<FmtQ40F32>(a, st);
+        case kTypeQ5_0: a.nblk = K / kQK8_0; return launch_m<FmtQ50F32>(a, st);
+        case kTypeF16: a.nblk = K / 32; return launch_m<FmtF16F32>(a, st);
         case kTypeQ4_K: a.nblk = K / kQKK; return launch_m<FmtQ4KF32>(a, st);
+        case kTypeQ5_K: a.nblk = K / kQKK; return launch_m<FmtQ5KF32>(a, st);
         case kTypeQ6_K: a.nblk = K / kQKK; return launch_m<FmtQ6KF32>(a, st);
         default: return hipErrorInvalidValue;
     }

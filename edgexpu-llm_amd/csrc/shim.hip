@@ -105,18 +105,36 @@ bool ensure_init() {
 // orders with the caller's other default-stream work.
 hipStream_t pick_stream(void *s) { return (hipStream_t)s; }
 
-bool gpu_type(uint32_t t) { return t == kTypeQ8_0 || t == kTypeQ4_K || t == kTypeQ6_K; }
+// Every type of the reference's dispatcher but F32 (src/gguf_quant.c:69-108):
+// the Q8_0 family and the K-quants through their integer dots, F16 through
+// the f32-activation dot.
+bool gpu_type(uint32_t t) { return q8_0_family((int)t) || k_family((int)t) || t == (uint32_t)kTypeF16; }
 
-size_t block_elems(uint32_t t) { return t == kTypeQ8_0 ? (size_t)kQK8_0 : (size_t)kQKK; }
-
-size_t block_bytes(uint32_t t) {
-    return t == kTypeQ8_0 ? (size_t)kBytesQ8_0 : (t == kTypeQ4_K ? (size_t)kBytesQ4_K : (size_t)kBytesQ6_K);
+size_t block_elems(uint32_t t) {
+    return q8_0_family((int)t) ? (size_t)kQK8_0 : (k_family((int)t) ? (size_t)kQKK : (size_t)1);
 }
 
-// Bytes of one token's quantized activation: Q8_0 blocks for Q8_0 weights,
-// Q8_K blocks for the K-quants (src/cpu_kernel.c:577-631).
+size_t block_bytes(uint32_t t) {
+    switch (t) {
+        case kTypeQ8_0: return kBytesQ8_0;
+        case kTypeQ4_0: return kBytesQ4_0;
+        case kTypeQ5_0: return kBytesQ5_0;
+        case kTypeQ4_K: return kBytesQ4_K;
+        case kTypeQ5_K: return kBytesQ5_K;
+        case kTypeQ6_K: return kBytesQ6_K;
+        case kTypeF16: return 2;
+        default: return 0;
+    }
+}
+
+// Elements of K one GEMV lane unit spans: a block, or 32 F16 values (the
+// F16 products need n_in % 32 == 0; dequant takes any count).
+size_t unit_elems(uint32_t t) { return t == (uint32_t)kTypeF16 ? (size_t)32 : block_elems(t); }
+
+// Bytes of one token's quantized activation: Q8_0 blocks for the Q8_0
+// family, Q8_K blocks for the K-quants (src/cpu_kernel.c:577-631).
 size_t act_bytes(uint32_t t, int K) {
-    return t == kTypeQ8_0 ? (size_t)(K / kQK8_0) * kBytesQ8_0 : (size_t)(K / kQKK) * kBytesQ8_K;
+    return q8_0_family((int)t) ? (size_t)(K / kQK8_0) * kBytesQ8_0 : (size_t)(K / kQKK) * kBytesQ8_K;
 }
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
@@ -135,7 +153,7 @@ bool stage_in_kernel(uint32_t type, int K, int m) {
     static const int mode = env_int("EXQ_FUSED", 1);
     static const int generic = env_int("EXQ_GENERIC", 0);
     if (mode == 0 || generic != 0 || !gemv_fused_supported((int)type, K, m)) return false;
-    return mode == 2 || K <= kStageMaxK || (type != kTypeQ8_0 && m == 1 && K <= kStageMaxKWide);
+    return mode == 2 || K <= kStageMaxK || (k_family((int)type) && m == 1 && K <= kStageMaxKWide);
 }
 
 bool split_gemv(uint32_t type, int K, int m) {
@@ -231,12 +249,41 @@ bool check_linear_args(const void *out, const void *x, const void *w, uint32_t t
         return false;
     }
     if (!gpu_type(type)) {
-        set_error(-3, "%s: GGUF type %u is not supported on the GPU (Q8_0/Q4_K/Q6_K only)", who, type);
+        set_error(-3, "%s: GGUF type %u is not supported on the GPU (F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)", who,
+                  type);
         return false;
     }
-    if ((size_t)n_in % block_elems(type) != 0) {
-        set_error(-2, "%s: n_in=%d is not a multiple of the type-%u block (%zu)", who, n_in, type, block_elems(type));
+    if ((size_t)n_in % unit_elems(type) != 0) {
+        set_error(-2, "%s: n_in=%d is not a multiple of %zu for type %u", who, n_in, unit_elems(type), type);
         return false;
+    }
+    return true;
+}
+
+// f32-activation products (F16 rows in the batch driver; every type in the
+// per-row f32 dot and the K-quant logits): at most kGemvMaxTokens tokens per
+// launch of the generic kernel, or the fused kernel one token at a time for
+// the K-quant formats it covers.  xs: the tokens' 16-element sums of x
+// (K-quants only).
+bool run_f32_product(uint32_t type, const void *w, int n_out, int n_in, int m, const float *x, const float *xs,
+                     const float *bias, float *out, int ldo, hipStream_t st) {
+    const size_t rb = edgexpu_hip_row_bytes(type, n_in);
+    if (k_family((int)type) && ldo == n_out && gemv_fused_f32_supported((int)type, n_in)) {
+        for (int t = 0; t < m; ++t) {
+            if (!hip_ok(launch_gemv_fused_f32((int)type, (const uint8_t *)w, n_out, bias, out + (size_t)t * ldo, rb,
+                                              n_in, x + (size_t)t * n_in, xs + (size_t)t * (n_in / 16), st),
+                        "gemv_f32 fused"))
+                return false;
+        }
+        return true;
+    }
+    for (int t0 = 0; t0 < m; t0 += kGemvMaxTokens) {
+        const int mt = m - t0 < kGemvMaxTokens ? m - t0 : kGemvMaxTokens;
+        if (!hip_ok(launch_gemv_f32((int)type, (const uint8_t *)w, rb, n_out, n_in, mt, x + (size_t)t0 * n_in,
+                                    xs != nullptr ? xs + (size_t)t0 * (n_in / 16) : nullptr, bias,
+                                    out + (size_t)t0 * ldo, ldo, st),
+                    "gemv_f32"))
+            return false;
     }
     return true;
 }
@@ -277,6 +324,15 @@ bool run_q8_product(uint32_t type, const void *w, int n_out, int n_in, int m, co
 bool run_linear_group(uint32_t type, int nmat, const void *const *w, const int *n_out, const float *const *bias,
                       float *const *out, const float *x, int m, int n_in, hipStream_t st) {
     const size_t rb = edgexpu_hip_row_bytes(type, n_in);
+    if (type == (uint32_t)kTypeF16) {
+        // src/cpu_kernel.c:632-641: rows with neither activation quantizer
+        // take the f32-activation row dot, out = bias + dot per token
+        for (int z = 0; z < nmat; ++z)
+            if (!run_f32_product(type, w[z], n_out[z], n_in, m, x, nullptr, bias != nullptr ? bias[z] : nullptr,
+                                 out[z], n_out[z], st))
+                return false;
+        return true;
+    }
     if (stage_in_kernel(type, n_in, m)) {
         return hip_ok(launch_gemv_fused((int)type, nmat, (const uint8_t *const *)w, n_out, bias, out, rb, n_in, m, x,
                                         nullptr, 0, st),
@@ -284,8 +340,8 @@ bool run_linear_group(uint32_t type, int nmat, const void *const *w, const int *
     }
     ActWs a;
     if (!act_ws(type, m, n_in, a)) return false;
-    const hipError_t e = type == kTypeQ8_0 ? launch_quantize_q8_0(x, m, n_in, n_in, a.xq, st)
-                                           : launch_quantize_q8_k(x, m, n_in, n_in, a.xq, st);
+    const hipError_t e = q8_0_family((int)type) ? launch_quantize_q8_0(x, m, n_in, n_in, a.xq, st)
+                                                : launch_quantize_q8_k(x, m, n_in, n_in, a.xq, st);
     if (!hip_ok(e, "quantize activations")) return false;
     if (split_gemv(type, n_in, m) && m < kGemmMinTokens) {
         return hip_ok(launch_gemv_fused((int)type, nmat, (const uint8_t *const *)w, n_out, bias, out, rb, n_in, m,
@@ -615,9 +671,14 @@ int edgexpu_hip_gemv_q8_dev(float *out, const uint8_t *xq, const void *w, uint32
                             int n_out, int n_in, void *stream) {
     if (!ensure_init()) return 0;
     if (!check_linear_args(out, xq, w, type, m, n_out, n_in, "gemv_q8")) return 0;
+    if (type == (uint32_t)kTypeF16) {
+        set_error(-3, "gemv_q8: F16 rows have no quantized-activation dot (src/gguf_dot_q8.c:414-434)");
+        return 0;
+    }
     // the block scale heads every Q8_K (f32) / Q8_0 (f16) block
-    if (((uintptr_t)xq & (type == kTypeQ8_0 ? 1u : 3u)) != 0) {
-        set_error(-2, "gemv_q8: xq must be %d-byte aligned", type == kTypeQ8_0 ? 2 : 4);
+    const bool q80 = q8_0_family((int)type);
+    if (((uintptr_t)xq & (q80 ? 1u : 3u)) != 0) {
+        set_error(-2, "gemv_q8: xq must be %d-byte aligned", q80 ? 2 : 4);
         return 0;
     }
     return run_q8_product(type, w, n_out, n_in, m, xq, bias, out, n_out, pick_stream(stream)) ? 1 : 0;
@@ -643,34 +704,25 @@ int edgexpu_hip_logits_dev(float *scores, uint32_t *best_dev, const float *hidde
     const size_t rb = edgexpu_hip_row_bytes(type, n_embd);
     ActWs a;
     if (!act_ws(type, m, n_embd, a)) return 0;
-    if (type == kTypeQ8_0) {
-        // src/native.c:2317-2319: Q8_0 output weights use the Q8_0-activation dot
-        if (!hip_ok(launch_quantize_q8_0(hidden, m, n_embd, n_embd, a.xq, st), "quantize_q8_0")) return 0;
-    } else {
-        // K-quant output weights use the f32-activation dots (src/native.c:445-462)
-        if (!hip_ok(launch_xsum16(hidden, m, n_embd, a.xs, st), "xsum16")) return 0;
-    }
     // The reference walks the rows in chunks of chunk_rows (its host-memory
     // budget, src/native.c:2262-2274); every row's score is independent of
     // the chunking, so one launch covers all chunks in row order.
-    // K-quant rows: the fused kernel keeps one hidden vector's f32 slice in
-    // registers across all the rows a wave visits, one launch per vector (a
-    // row's score then does not depend on m, as in the reference's per-token
-    // loop); the generic kernel covers the K the fused one does not.
-    if (type != kTypeQ8_0 && gemv_fused_f32_supported((int)type, n_embd)) {
-        for (int t = 0; t < m; ++t) {
-            const hipError_t e = launch_gemv_fused_f32((int)type, (const uint8_t *)w, vocab, bias,
-                                                       scores + (size_t)t * vocab, rb, n_embd,
-                                                       hidden + (size_t)t * n_embd, a.xs + (size_t)t * (n_embd / 16), st);
-            if (!hip_ok(e, "logits gemv")) return 0;
-        }
+    if (q8_0_family((int)type)) {
+        // src/native.c:2317-2319: the Q8_0 family scores rows against the
+        // Q8_0-quantized hidden vector
+        if (!hip_ok(launch_quantize_q8_0(hidden, m, n_embd, n_embd, a.xq, st), "quantize_q8_0")) return 0;
+        if (!hip_ok(launch_gemv_q8((int)type, (const uint8_t *)w, rb, vocab, n_embd, m, a.xq,
+                                   act_bytes(type, n_embd), bias, scores, vocab, st),
+                    "logits gemv"))
+            return 0;
     } else {
-        const hipError_t e = type == kTypeQ8_0
-                                 ? launch_gemv_q8((int)type, (const uint8_t *)w, rb, vocab, n_embd, m, a.xq,
-                                                  act_bytes(type, n_embd), bias, scores, vocab, st)
-                                 : launch_gemv_f32((int)type, (const uint8_t *)w, rb, vocab, n_embd, m, hidden, a.xs,
-                                                   bias, scores, vocab, st);
-        if (!hip_ok(e, "logits gemv")) return 0;
+        // the other formats use the f32-activation dots (src/native.c:445-462);
+        // K-quant rows one hidden vector per fused launch (a row's score then
+        // does not depend on m, as in the reference's per-token loop)
+        if (k_family((int)type) && !hip_ok(launch_xsum16(hidden, m, n_embd, a.xs, st), "xsum16")) return 0;
+        if (!run_f32_product(type, w, vocab, n_embd, m, hidden, k_family((int)type) ? a.xs : nullptr, bias, scores,
+                             vocab, st))
+            return 0;
     }
     if (best_dev != nullptr &&
         !hip_ok(launch_argmax_rows(scores, m, vocab, (size_t)vocab, a.keys, best_dev, st), "argmax"))
@@ -685,7 +737,8 @@ int edgexpu_hip_dequantize_dev(const void *src, uint32_t type, uint64_t n_elemen
         return 0;
     }
     if (!gpu_type(type)) {
-        set_error(-3, "dequantize: GGUF type %u is not supported on the GPU (Q8_0/Q4_K/Q6_K only)", type);
+        set_error(-3, "dequantize: GGUF type %u is not supported on the GPU (F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)",
+                  type);
         return 0;
     }
     if (n_elements % block_elems(type) != 0) {
@@ -874,7 +927,16 @@ int edgexpu_hip_dot_f32_rows(float *out, const uint8_t *w, uint32_t type, const 
     float *dout = (float *)(d + wo + xo);
     if (!hip_ok(hipMemcpyAsync(d, w, rb * (size_t)rows, hipMemcpyHostToDevice, g.stream), "H2D w")) return 0;
     if (!hip_ok(hipMemcpyAsync(dx, x, (size_t)n * sizeof(float), hipMemcpyHostToDevice, g.stream), "H2D x")) return 0;
-    if (!edgexpu_hip_logits_dev(dout, nullptr, dx, d, type, nullptr, 1, rows, n, 0, g.stream)) return 0;
+    // the f32-activation dot for every type (edgexpu_gguf_dot_quant never
+    // quantizes x, src/gguf_quant.c:894-918)
+    float *xs = nullptr;
+    if (k_family((int)type)) {
+        ActWs a;
+        if (!act_ws(type, 1, n, a)) return 0;
+        xs = a.xs;
+        if (!hip_ok(launch_xsum16(dx, 1, n, xs, g.stream), "xsum16")) return 0;
+    }
+    if (!run_f32_product(type, d, rows, n, 1, dx, xs, nullptr, dout, rows, g.stream)) return 0;
     if (!hip_ok(hipMemcpyAsync(out, dout, (size_t)rows * sizeof(float), hipMemcpyDeviceToHost, g.stream), "D2H"))
         return 0;
     return hip_ok(hipStreamSynchronize(g.stream), "sync") ? 1 : 0;

@@ -166,7 +166,7 @@ int edgexpu_gguf_dequantize(const uint8_t *src, uint32_t type, uint64_t n_elemen
         return 0;
     }
     if (!edgexpu_hip_supports_type(type)) {
-        snprintf(msg, sizeof(msg), "GGUF type %u is not on the GPU path (Q8_0/Q4_K/Q6_K only)", type);
+        snprintf(msg, sizeof(msg), "GGUF type %u is not on the GPU path (F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)", type);
         set_msg(error, error_size, msg);
         return 0;
     }
@@ -212,7 +212,9 @@ float edgexpu_gguf_dot_quant_q8(uint32_t type, const uint8_t *wrow, const uint8_
     if (wrow == NULL || x_q8 == NULL || n <= 0 || n % 32 != 0) {
         return 0.0f;
     }
-    if (type != EDGEXPU_GGUF_TYPE_Q8_0 || !edgexpu_hip_dot_q8_rows(&out, wrow, type, x_q8, 1, n)) {
+    /* the Q8_0-activation family of src/gguf_dot_q8.c:1004-1023 */
+    if ((type != EDGEXPU_GGUF_TYPE_Q8_0 && type != EDGEXPU_GGUF_TYPE_Q4_0 && type != EDGEXPU_GGUF_TYPE_Q5_0) ||
+        !edgexpu_hip_dot_q8_rows(&out, wrow, type, x_q8, 1, n)) {
         return 0.0f;
     }
     return out;
@@ -223,7 +225,8 @@ float edgexpu_gguf_dot_quant_q8k(uint32_t type, const uint8_t *wrow, const uint8
     if (wrow == NULL || x_q8k == NULL || n <= 0 || n % 256 != 0) {
         return 0.0f;
     }
-    if ((type != EDGEXPU_GGUF_TYPE_Q4_K && type != EDGEXPU_GGUF_TYPE_Q6_K) ||
+    /* the Q8_K-activation family of src/gguf_dot_q8.c:1025-1044 */
+    if ((type != EDGEXPU_GGUF_TYPE_Q4_K && type != EDGEXPU_GGUF_TYPE_Q5_K && type != EDGEXPU_GGUF_TYPE_Q6_K) ||
         !edgexpu_hip_dot_q8_rows(&out, wrow, type, x_q8k, 1, n)) {
         return 0.0f;
     }

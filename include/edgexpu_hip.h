@@ -1,6 +1,7 @@
 /*
  * edgexpu_hip.h -- C-ABI of libedgexpu_hip.so, the MI355X (gfx950) kernel set
- * for the GGUF Q8_0 / Q4_K / Q6_K quantized-weight matrix path.
+ * for the GGUF quantized-weight matrix path (Q8_0 / Q4_K / Q6_K, and the
+ * dispatcher's other formats Q4_0 / Q5_0 / Q5_K / F16).
  *
  * Plain C types only (no HIP or torch types): device pointers are `void *` /
  * typed pointers into device memory, streams are `void *` holding a
@@ -47,8 +48,10 @@ void edgexpu_hip_shutdown(void);
  * message into buf.  The error stays set until edgexpu_hip_clear_error(). */
 int edgexpu_hip_last_error(char *buf, size_t size);
 void edgexpu_hip_clear_error(void);
-/* 1 when `type` runs on the GPU (edgexpu_gguf_can_dot_q8/_q8k dispatch,
- * src/gguf_dot_q8.c:414-434, restricted to Q8_0/Q4_K/Q6_K). */
+/* 1 when `type` runs on the GPU: every type of the reference's dispatcher but
+ * F32 (src/gguf_quant.c:69-108; src/gguf_dot_q8.c:414-434): Q4_0, Q5_0, Q8_0
+ * with Q8_0 activations, Q4_K, Q5_K, Q6_K with Q8_K activations, F16 with
+ * f32 activations (its products need n_in % 32 == 0). */
 int edgexpu_hip_supports_type(uint32_t type);
 /* Prefill (m >= 64 tokens, Q4_K) arithmetic.  No reference counterpart: the
  * reference has one CPU path.

@@ -66,9 +66,12 @@ def test_layout_helpers_match_oracle(ora):
 
 def test_hip_host_helpers_without_gpu():
     L = E.HipLib()
-    assert [t for t in range(16) if L.supports_type(t)] == [8, 12, 14]
+    # every type of the reference's dispatcher but F32 (src/gguf_quant.c:69-108)
+    assert [t for t in range(16) if L.supports_type(t)] == [1, 2, 6, 8, 12, 13, 14]
     assert L.row_bytes(12, 4096) == 2304 and L.row_bytes(14, 9728) == 7980 and L.row_bytes(8, 576) == 612
-    assert L.row_bytes(12, 100) == 0 and L.row_bytes(2, 64) == 0
+    assert L.row_bytes(2, 576) == 324 and L.row_bytes(6, 1536) == 1056 and L.row_bytes(13, 2560) == 1760
+    assert L.row_bytes(1, 576) == 1152 and L.row_bytes(1, 7) == 14
+    assert L.row_bytes(12, 100) == 0 and L.row_bytes(2, 48) == 0 and L.row_bytes(0, 64) == 0
 
 
 def test_layer_kind_projection_tables():

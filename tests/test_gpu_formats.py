@@ -1,0 +1,320 @@
+"""GPU parity of the dispatcher's other formats (Q4_0, Q5_0, Q5_K, F16), of
+the f32-activation row dots of every format, and of the reference-named
+drop-in library (libedgexpu_kernels.so) called with host buffers.
+
+Bars as for the main formats: dequant bit-exact against the oracle (which is
+bit-exact against the reference build and its fixtures); integer block sums
+exact (unit-scale end-to-end check); fp32 outputs within TOL of the row's
+conditioning scale S (sum of |block terms| for the quantized-activation dots,
+sum |w_k x_k| for the f32-activation ones).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+import npref
+import oracle as O
+import edgexpu_amd as E
+from edgexpu_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+DEV = "cuda:0"
+F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 1, 2, 6, 8, 12, 13, 14
+TN = {1: "f16", 2: "q4_0", 6: "q5_0", 8: "q8_0", 12: "q4_k", 13: "q5_k", 14: "q6_k"}
+Q80_FAMILY = (Q4_0, Q5_0, Q8_0)
+MORE = [F16, Q4_0, Q5_0, Q5_K]
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def scales(qt, w, x):
+    """S[t, i]: block-term scale (quantized activations) or sum |w x| (F16)."""
+    m = x.shape[0]
+    S = np.zeros((m, w.shape[0]))
+    for t in range(m):
+        if qt == F16:
+            for i in range(w.shape[0]):
+                S[t, i] = npref.f32_dot_f64(qt, w[i], x[t])[1]
+            continue
+        xq = npref.quantize_q8_0(x[t]) if qt in Q80_FAMILY else npref.quantize_q8_k(x[t])
+        for i in range(w.shape[0]):
+            S[t, i] = npref.q8_dot_f64(qt, w[i], xq)[1]
+    return S
+
+
+def assert_tol(got, want, S, what=""):
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    bad = err > TOL * S + 1e-30
+    assert not bad.any(), f"{what}: {bad.sum()} outside tolerance, worst ratio {(err / np.maximum(S, 1e-30)).max():.3e}"
+
+
+# ------------------------------------------------------------------ dequant
+
+
+@pytest.mark.parametrize("qt", MORE)
+def test_dequant_golden_bit_exact(hipdev, golden, qt):
+    g = golden(f"dequant_{TN[qt]}")
+    out = E.dequantize(dev(g["src"]), qt, g["out"].size)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out.cpu().numpy()), bits(g["out"]))
+
+
+@pytest.mark.parametrize("qt,nblocks", [(Q4_0, 300001), (Q5_0, 200003), (Q5_K, 40001), (F16, 1)])
+def test_dequant_random_bit_exact(hipdev, ora, qt, nblocks):
+    rng = np.random.default_rng(910 + qt)
+    n = nblocks * {Q4_0: 32, Q5_0: 32, Q5_K: 256, F16: 1}[qt]
+    if qt == F16:
+        n = 1234567  # not a multiple of 8: the last thread converts the tail
+        src = synth.np_weights(F16, 1, n, rng).reshape(-1)
+    else:
+        src = synth.np_weights(qt, 1, n, rng).reshape(-1)
+    out = E.dequantize(dev(src), qt, n)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out.cpu().numpy()), bits(ora.dequantize(src, qt, n)))
+
+
+def test_dequant_f16_every_code(hipdev, ora):
+    """All 65536 half codes: bit-exact, NaN codes give NaN (payload bits of a
+    NaN are not part of the comparison)."""
+    src = np.arange(65536, dtype=np.uint16).view(np.uint8)
+    got = E.dequantize(dev(src), F16, 65536).cpu().numpy()
+    want = ora.dequantize(src, F16, 65536)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(bits(got[~nan]), bits(want[~nan]))
+
+
+# ------------------------------------------------------------------ linear
+
+
+LINEAR = ["linear_q4_0_576", "linear_q5_0_1536", "linear_q5_k_2560", "linear_q5_k_4096", "linear_f16_576"]
+
+
+@pytest.mark.parametrize("name", LINEAR)
+def test_linear_golden(hipdev, golden, name):
+    g = golden(name)
+    qt, w, x, bias = int(g["type"]), g["w"], g["x"], g["bias"]
+    n_out, (m, n_in) = w.shape[0], x.shape
+    S = scales(qt, w, x)
+    y = E.linear_quant_batch(dev(w), qt, dev(x), n_out, n_in).cpu().numpy()
+    assert_tol(y, g["out"], S, name)
+    yb = E.linear_quant_batch(dev(w), qt, dev(x), n_out, n_in, bias=dev(bias)).cpu().numpy()
+    assert_tol(yb, g["out_bias"], S + np.abs(bias)[None, :], name + "+bias")
+
+
+@pytest.mark.parametrize("qt,n_in,n_out", [(Q4_0, 576, 577), (Q4_0, 4096, 301), (Q4_0, 32, 65), (Q5_0, 1536, 300),
+                                           (Q5_0, 64, 129), (Q5_K, 2560, 515), (Q5_K, 4096, 1001),
+                                           (Q5_K, 14336, 130), (Q5_K, 256, 70), (F16, 576, 300), (F16, 4096, 129),
+                                           (F16, 32, 17)])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8, 11])
+def test_linear_random_vs_oracle(hipdev, ora, qt, n_in, n_out, m):
+    rng = np.random.default_rng(qt * 1000 + n_in + n_out + m)
+    w = synth.np_weights(qt, n_out, n_in, rng)
+    x = synth.np_activations(m, n_in, rng)
+    bias = rng.normal(0, 0.5, n_out).astype(np.float32)
+    want = ora.linear_quant_batch(x, w, qt, bias, m, n_out, n_in)
+    got = E.linear_quant_batch(dev(w), qt, dev(x), n_out, n_in, bias=dev(bias)).cpu().numpy()
+    S = scales(qt, w, x) if n_out * m <= 3000 else np.abs(want) * 0 + np.abs(want).max() * 10
+    assert_tol(got, want, S + np.abs(bias)[None, :], f"{TN[qt]} {n_out}x{n_in} m={m}")
+
+
+@pytest.mark.parametrize("qt", [Q4_0, Q5_0, Q5_K])
+def test_integer_sums_exact_end_to_end(hipdev, qt):
+    """Unit scales and integer activations make every fp32 step exact, so the
+    output equals the int64 closed form exactly."""
+    rng = np.random.default_rng(70 + qt)
+    n_in, n_out = (1536, 64) if qt in Q80_FAMILY else (2048, 64)
+    w = synth.np_weights(qt, n_out, n_in, rng)
+    one = np.array([1.0], np.float16).view(np.uint8)
+    x = rng.integers(-127, 128, (1, n_in)).astype(np.float32)
+    if qt in Q80_FAMILY:
+        w.reshape(n_out, -1, 18 if qt == Q4_0 else 22)[:, :, 0:2] = one
+        x.reshape(-1, 32)[:, 0] = 127.0  # amax 127 -> d = 1: q = x
+    else:
+        wb = w.reshape(n_out, -1, 176)
+        wb[:, :, 0:2] = one
+        wb[:, :, 2:4] = one
+        x.reshape(-1, 256)[:, 0] = -127.0  # first max -127 -> iscale = 1: q = x, d = 1
+    got = E.linear_quant_batch(dev(w), qt, dev(x), n_out, n_in).cpu().numpy()[0]
+    xq = npref.quantize_q8_0(x[0]) if qt in Q80_FAMILY else npref.quantize_q8_k(x[0])
+    want = np.array([npref.q8_dot_f64(qt, w[i], xq)[0] for i in range(n_out)])
+    assert np.all(np.abs(want) < 2**24)
+    assert np.array_equal(got.astype(np.float64), want)
+
+
+@pytest.mark.parametrize("qt,n_in,n_outs", [(Q5_K, 2560, (4096, 1024, 1024)), (Q4_0, 576, (576, 192, 192)),
+                                            (F16, 576, (1536, 1536))])
+@pytest.mark.parametrize("m", [1, 3])
+def test_linear_group_matches_single(hipdev, qt, n_in, n_outs, m):
+    rng = np.random.default_rng(qt + n_in + m)
+    ws = [dev(synth.np_weights(qt, n, n_in, rng)) for n in n_outs]
+    x = dev(synth.np_activations(m, n_in, rng))
+    bs = [dev(rng.normal(0, 0.5, n).astype(np.float32)) for n in n_outs]
+    outs = E.linear_quant_group(ws, qt, x, list(n_outs), n_in, biases=bs)
+    for z, n in enumerate(n_outs):
+        one = E.linear_quant_batch(ws[z], qt, x, n, n_in, bias=bs[z])
+        assert np.array_equal(bits(outs[z].cpu().numpy()), bits(one.cpu().numpy())), f"matrix {z}"
+
+
+# ------------------------------------------------------------------ f32 row dots and logits
+
+
+DOTF32 = ["dotf32_q4_k_4096", "dotf32_q4_k_2560", "dotf32_q6_k_2560", "dotf32_q8_0_576", "dotf32_q4_0_576",
+          "dotf32_q5_0_1536", "dotf32_q5_k_2560", "dotf32_f16_576"]
+
+
+def _dot_f32_rows(w, qt, h):
+    """edgexpu_hip_dot_f32_rows: host buffers in and out."""
+    rows, n = w.shape[0], h.size
+    out = np.zeros(rows, np.float32)
+    w = np.ascontiguousarray(w)
+    h = np.ascontiguousarray(h, dtype=np.float32)
+    lib = E.hip()
+    lib.check(lib.dot_f32_rows(out.ctypes.data, w.ctypes.data, qt, h.ctypes.data, rows, n), "dot_f32_rows")
+    return out
+
+
+@pytest.mark.parametrize("name", DOTF32)
+def test_f32_row_dots_golden(hipdev, golden, name):
+    """The per-row f32-activation dot (edgexpu_gguf_dot_quant) of every format,
+    Q8_0 included: x is never quantized (src/gguf_quant.c:894-918)."""
+    g = golden(name)
+    qt, w, h = int(g["type"]), g["w"], g["h"]
+    got = _dot_f32_rows(w, qt, h)
+    S = np.array([npref.f32_dot_f64(qt, w[i], h)[1] for i in range(w.shape[0])])
+    assert_tol(got, g["scores"], S, name)
+
+
+@pytest.mark.parametrize("qt,n,vocab", [(Q4_0, 576, 20001), (Q5_0, 1536, 3000), (Q5_K, 2560, 15001),
+                                        (F16, 576, 5000)])
+def test_logits_and_argmax(hipdev, ora, qt, n, vocab):
+    """Logits of the other formats: the Q8_0 family against the Q8_0-quantized
+    hidden vector, Q5_K and F16 against f32 (src/native.c:2317-2319, 445-514)."""
+    rng = np.random.default_rng(qt + vocab)
+    w = synth.np_weights(qt, vocab, n, rng)
+    h = rng.normal(0, 1, n).astype(np.float32)
+    bias = rng.normal(0, 0.01, vocab).astype(np.float32)
+    want, want_best = ora.logits(h, w, qt, bias, vocab, n, 0)
+    scores, best = E.logits(dev(w), qt, dev(h[None, :]), vocab, n, bias=dev(bias))
+    got = scores.cpu().numpy()[0]
+    sample = rng.choice(vocab, 200, replace=False)
+    S = scales(qt, w[sample], h[None, :])[0] + np.abs(bias[sample])
+    assert_tol(got[sample], want[sample], S, f"{TN[qt]} sampled rows")
+    assert np.abs(got - want).max() <= TOL * S.max() * 4
+    b = int(best.cpu().numpy()[0])
+    assert b == int(np.argmax(got))
+    top2 = np.sort(want)[-2:]
+    if top2[1] - top2[0] > 8 * TOL * S.max():
+        assert b == want_best
+
+
+# ------------------------------------------------------------------ reference-named drop-ins
+
+
+_f32p = C.POINTER(C.c_float)
+_u8p = C.POINTER(C.c_uint8)
+
+
+@pytest.fixture(scope="module")
+def kern(hipdev):
+    k = C.CDLL(E.KERNELS_SO)
+    k.edgexpu_cpu_linear_quant_batch.restype = None
+    k.edgexpu_cpu_linear_quant_batch.argtypes = [_f32p, _f32p, _u8p, C.c_uint32, _f32p, C.c_int, C.c_int, C.c_int]
+    k.edgexpu_gguf_dequantize.restype = C.c_int
+    k.edgexpu_gguf_dequantize.argtypes = [_u8p, C.c_uint32, C.c_uint64, _f32p, C.c_char_p, C.c_size_t]
+    k.edgexpu_gguf_dot_quant.restype = C.c_float
+    k.edgexpu_gguf_dot_quant.argtypes = [C.c_uint32, _u8p, _f32p, C.c_int]
+    k.edgexpu_gguf_dot_quant_q8.restype = C.c_float
+    k.edgexpu_gguf_dot_quant_q8.argtypes = [C.c_uint32, _u8p, _u8p, C.c_int]
+    k.edgexpu_gguf_dot_quant_q8k.restype = C.c_float
+    k.edgexpu_gguf_dot_quant_q8k.argtypes = [C.c_uint32, _u8p, _u8p, C.c_int]
+    k.edgexpu_gguf_quantize_q8_0.restype = C.c_int
+    k.edgexpu_gguf_quantize_q8_0.argtypes = [_f32p, C.c_int, _u8p]
+    k.edgexpu_gguf_quantize_q8_k.restype = C.c_int
+    k.edgexpu_gguf_quantize_q8_k.argtypes = [_f32p, C.c_int, _u8p]
+    return k
+
+
+def _p(a, t):
+    return None if a is None else a.ctypes.data_as(t)
+
+
+@pytest.mark.parametrize("qt,n_in,n_out,m", [(Q8_0, 576, 70, 2), (Q4_K, 4096, 33, 1), (Q6_K, 2560, 40, 3),
+                                             (Q4_0, 576, 65, 2), (Q5_0, 1536, 30, 1), (Q5_K, 2560, 41, 4),
+                                             (F16, 576, 37, 3)])
+def test_dropin_linear_quant_batch(kern, ora, qt, n_in, n_out, m):
+    """edgexpu_cpu_linear_quant_batch (src/cpu_kernel.c:545-644) through the
+    drop-in set: host pointers, the weight uploaded inside the call."""
+    rng = np.random.default_rng(5000 + qt + n_in + m)
+    w = np.ascontiguousarray(synth.np_weights(qt, n_out, n_in, rng))
+    x = np.ascontiguousarray(synth.np_activations(m, n_in, rng))
+    bias = rng.normal(0, 0.5, n_out).astype(np.float32)
+    out = np.full((m, n_out), np.nan, np.float32)
+    kern.edgexpu_cpu_linear_quant_batch(_p(out, _f32p), _p(x, _f32p), _p(w, _u8p), qt, _p(bias, _f32p), m, n_out,
+                                        n_in)
+    want = ora.linear_quant_batch(x, w, qt, bias, m, n_out, n_in)
+    assert_tol(out, want, scales(qt, w, x) + np.abs(bias)[None, :], f"drop-in {TN[qt]}")
+
+
+@pytest.mark.parametrize("qt", [Q8_0, Q4_K, Q6_K] + MORE)
+def test_dropin_dequant_and_row_dots(kern, ora, qt):
+    """edgexpu_gguf_dequantize bit-exact; edgexpu_gguf_dot_quant (f32 x) and
+    edgexpu_gguf_dot_quant_q8 / _q8k (quantized x) within the bound, each on
+    one row as the reference's per-row API."""
+    rng = np.random.default_rng(6000 + qt)
+    n = 2560 if qt in (Q4_K, Q5_K, Q6_K) else 576
+    w = np.ascontiguousarray(synth.np_weights(qt, 1, n, rng)[0])
+    x = np.ascontiguousarray(synth.np_activations(1, n, rng)[0])
+    y = np.zeros(n, np.float32)
+    err = C.create_string_buffer(256)
+    assert kern.edgexpu_gguf_dequantize(_p(w, _u8p), qt, n, _p(y, _f32p), err, 256) == 1, err.value
+    assert np.array_equal(bits(y), bits(ora.dequantize(w, qt, n)))
+    got = kern.edgexpu_gguf_dot_quant(qt, _p(w, _u8p), _p(x, _f32p), n)
+    want = ora.dot_f32(qt, w, x, n)
+    fv, fs = npref.f32_dot_f64(qt, w, x)
+    assert abs(got - want) <= TOL * fs, (got, want)
+    if qt == F16:
+        xq = np.zeros(ora_q8_bytes(n), np.uint8)
+        assert kern.edgexpu_gguf_dot_quant_q8(qt, _p(w, _u8p), _p(xq, _u8p), n) == 0.0  # no Q8 dot for F16
+        return
+    if qt in Q80_FAMILY:
+        xq = np.zeros(n // 32 * 34, np.uint8)
+        assert kern.edgexpu_gguf_quantize_q8_0(_p(x, _f32p), n, _p(xq, _u8p)) == 1
+        assert np.array_equal(xq, ora.quantize_q8_0(x))
+        got = kern.edgexpu_gguf_dot_quant_q8(qt, _p(w, _u8p), _p(xq, _u8p), n)
+        assert kern.edgexpu_gguf_dot_quant_q8k(qt, _p(w, _u8p), _p(xq, _u8p), n) == 0.0  # wrong family
+        want = ora.dot_q8(qt, w, xq, n)
+    else:
+        xq = np.zeros(n // 256 * 292, np.uint8)
+        assert kern.edgexpu_gguf_quantize_q8_k(_p(x, _f32p), n, _p(xq, _u8p)) == 1
+        assert np.array_equal(xq, ora.quantize_q8_k(x))
+        got = kern.edgexpu_gguf_dot_quant_q8k(qt, _p(w, _u8p), _p(xq, _u8p), n)
+        want = ora.dot_q8k(qt, w, xq, n)
+    S = npref.q8_dot_f64(qt, w, xq)[1]
+    assert abs(got - want) <= TOL * S, (got, want)
+
+
+def ora_q8_bytes(n):
+    return n // 32 * 34
+
+
+def test_unsupported_shapes_are_refused(hipdev):
+    """F32 rows stay on the host's own kernels; F16 products need n_in % 32 == 0."""
+    lib = E.hip()
+    assert lib.supports_type(0) == 0
+    for t in (1, 2, 6, 8, 12, 13, 14):
+        assert lib.supports_type(t) == 1
+    w = dev(np.zeros((4, 2 * 40), np.uint8))
+    x = dev(np.zeros((1, 40), np.float32))
+    with pytest.raises(E.HipError):
+        E.linear_quant_batch(w, F16, x, 4, 40)

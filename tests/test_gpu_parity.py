@@ -431,9 +431,17 @@ def test_bad_arguments_are_rejected(hipdev):
     code, msg = L.last_error()
     assert code != 0 and "multiple" in msg
     L.clear_error()
-    assert L.linear_dev(out.data_ptr(), x.data_ptr(), w.data_ptr(), 2, None, 1, 4, 96, None) == 0  # Q4_0
+    assert L.linear_dev(out.data_ptr(), x.data_ptr(), w.data_ptr(), 0, None, 1, 4, 96, None) == 0  # F32
     code, msg = L.last_error()
     assert "not supported" in msg
+    L.clear_error()
+    assert L.linear_dev(out.data_ptr(), x.data_ptr(), w.data_ptr(), 5, None, 1, 4, 96, None) == 0  # no such type
+    code, msg = L.last_error()
+    assert "not supported" in msg
+    L.clear_error()
+    assert L.gemv_q8_dev(out.data_ptr(), x.data_ptr(), w.data_ptr(), 1, None, 1, 4, 96, None) == 0  # F16: f32 x only
+    code, msg = L.last_error()
+    assert code != 0 and "F16" in msg
     L.clear_error()
     sc = torch.zeros((1, 4), device=DEV)
     assert L.logits_dev(sc.data_ptr(), None, x.data_ptr(), w.data_ptr(), 12, None, 1, 4, 256, -1, None) == 0
