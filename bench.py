@@ -68,6 +68,8 @@ def parse():
                    help="time the decode step with the layer ops on device: fused layer entry vs separate launches")
     p.add_argument("--read-ceiling", action="store_true",
                    help="time a plain streaming read of each decode launch's weight bytes (one JSON line)")
+    p.add_argument("--formats", action="store_true",
+                   help="decode GEMV [14336 x 4096] m=1 and 1 GiB dequant for every GPU format (one JSON line)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="first copy a 256 MiB buffer 4 times (device to device) for counter calibration")
     return p.parse_args()
@@ -172,6 +174,9 @@ def main():
         return
     if args.read_ceiling:
         print(json.dumps(read_ceiling(E, cfg, args.workload, dev)), flush=True)
+        return
+    if args.formats:
+        print(json.dumps(formats_leg(L, E, synth, gen, dev, no_cpu=args.no_cpu)), flush=True)
         return
     if args.prefill_only:
         # the prefill GEMM leg alone (for counter runs): one JSON line
@@ -617,7 +622,46 @@ def read_ceiling(E, cfg, workload, dev):
             "workload": workload, "launches": res}
 
 
-def dequant_leg(L, E, synth, gen, dev, no_cpu=False):
+def formats_leg(L, E, synth, gen, dev, no_cpu=False):
+    """One decode GEMV launch (m = 1, [14336 x 4096], f32 x quantized inside
+    the launch where the format takes quantized activations) per GPU format,
+    through the grouped entry point, in a HIP graph over distinct matrices
+    (>= 600 MB in rotation); GB/s = (weights + x + y bytes) / launch time.
+    Then 1 GiB bulk dequant of the formats beyond Q8_0 / Q4_K / Q6_K."""
+    import torch
+
+    K, N = 4096, 14336
+    x = torch.randn((1, K), generator=gen, device=dev)
+    y = torch.empty((1, N), device=dev)
+    arr = C.c_void_p * 4
+    nouts = (C.c_int * 4)(N)
+    gemv = {}
+    for qt in (8, 2, 6, 12, 13, 14, 1):
+        rb = E.row_bytes(qt, K)
+        nmat = max(2, -(-int(MIN_ROTATION_BYTES) // (N * rb)))
+        ws = [synth.torch_weights_bulk(qt, N, K, gen, dev) for _ in range(nmat)]
+
+        def launches(sp, ws=ws, qt=qt):
+            for _ in range(2):
+                for w in ws:
+                    if not L.linear_group_dev(1, arr(y.data_ptr()), x.data_ptr(), arr(w.data_ptr()), qt, None, nouts,
+                                              1, K, sp):
+                        L.check(0, "linear group")
+
+        g = capture(launches)
+        g.replay()
+        us = timed(g.replay, 5) * 1e3 / (2 * nmat)
+        byts = N * rb + K * 4 + N * 4
+        gemv[E_name(qt)] = {"us": round(us, 3), "bytes": byts, "GBps": round(byts / (us * 1e-6) / 1e9, 1),
+                            "frac": round(byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "matrices": nmat}
+        del ws, g
+        torch.cuda.empty_cache()
+    deq = dequant_leg(L, E, synth, gen, dev, no_cpu=no_cpu, types=((2, "q4_0"), (6, "q5_0"), (13, "q5_k"), (1, "f16")))
+    return {"metric": "decode GEMV and bulk dequant per GGUF format, 1 GPU", "gemv_shape": [N, K], "m": 1,
+            "gemv": gemv, "dequant_1GiB": deq}
+
+
+def dequant_leg(L, E, synth, gen, dev, no_cpu=False, types=((8, "q8_0"), (12, "q4_k"), (14, "q6_k"))):
     """Bulk dequantization of 1 GiB of blocks per format to f32 (the block
     contents are a 16 MiB seeded tile repeated); GB/s = (src + dst bytes) / s.
     Beside it, unless no_cpu, the reference's own dequant on one host core."""
@@ -632,9 +676,9 @@ def dequant_leg(L, E, synth, gen, dev, no_cpu=False):
         ref, kind = O.load_reference(), "reference"
         if ref is None:
             ref, kind = O.load_oracle(), "port"
-    for qt, name in ((8, "q8_0"), (12, "q4_k"), (14, "q6_k")):
-        bb = E.row_bytes(qt, 32 if qt == 8 else 256)
-        be = 32 if qt == 8 else 256
+    for qt, name in types:
+        be = {1: 32, 2: 32, 6: 32, 8: 32}.get(qt, 256)
+        bb = E.row_bytes(qt, be)
         nblk = (1 << 30) // bb
         tile_rows = tile_bytes // (bb * 64)
         tile = synth.torch_weights_bulk(qt, tile_rows, 64 * be, gen, dev).reshape(-1)
@@ -704,7 +748,7 @@ def cpu_baseline(args, cfg, layers, xin, projs, m):
 
 
 def E_name(t):
-    return {8: "q8_0", 12: "q4_k", 14: "q6_k"}[t]
+    return {1: "f16", 2: "q4_0", 6: "q5_0", 8: "q8_0", 12: "q4_k", 13: "q5_k", 14: "q6_k"}[t]
 
 
 if __name__ == "__main__":

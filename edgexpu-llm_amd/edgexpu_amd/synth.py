@@ -84,17 +84,17 @@ def torch_weights(qtype: int, rows: int, n: int, generator, device="cuda"):
         return torch.cat([dd.view(rows, nb, 4), rest], dim=2).reshape(rows, nb * 144)
     if qtype == Q5_K:
         nb = n // 256
-        dd = _f16_bytes(np.abs(rng.normal(0.0, 0.01, (rows, nb, 2)))).reshape(rows, nb, 4)
-        rest = rng.integers(0, 256, (rows, nb, 172), dtype=np.int16).astype(np.uint8)
-        return np.concatenate([dd, rest], axis=2).reshape(rows, nb * 176)
+        dd = f16b(torch.randn((rows, nb, 2), generator=generator, device=device).abs_() * 0.01)
+        rest = torch.randint(0, 256, (rows, nb, 172), generator=generator, device=device, dtype=torch.uint8)
+        return torch.cat([dd.view(rows, nb, 4), rest], dim=2).reshape(rows, nb * 176)
     if qtype in (Q4_0, Q5_0):
         nb = n // 32
         nq = 16 if qtype == Q4_0 else 20
-        d = _f16_bytes(np.abs(rng.normal(0.0, 0.02, (rows, nb))) / 16.0).reshape(rows, nb, 2)
-        q = rng.integers(0, 256, (rows, nb, nq), dtype=np.int16).astype(np.uint8)
-        return np.concatenate([d, q], axis=2).reshape(rows, nb * (2 + nq))
+        d = f16b(torch.randn((rows, nb, 1), generator=generator, device=device).abs_() * (0.02 / 16.0))
+        q = torch.randint(0, 256, (rows, nb, nq), generator=generator, device=device, dtype=torch.uint8)
+        return torch.cat([d.view(rows, nb, 2), q], dim=2).reshape(rows, nb * (2 + nq))
     if qtype == F16:
-        return _f16_bytes(rng.normal(0.0, 0.02, (rows, n))).reshape(rows, 2 * n)
+        return f16b(torch.randn((rows, n), generator=generator, device=device) * 0.02).reshape(rows, 2 * n)
     if qtype == Q6_K:
         nb = n // 256
         qlh = torch.randint(0, 256, (rows, nb, 192), generator=generator, device=device, dtype=torch.uint8)
