@@ -469,11 +469,19 @@ void gemv_fused_kernel(FusedArgs a) {
         __syncthreads();
     }
     const ActLds act{lq, ld, lbs, a.K, a.nblk};
-    // one token: the activation slice stays in registers for every tile
+    // the tokens' activation slices stay in registers for every tile
     typename Fmt::Act x1;
     if (M == 1) {
         if constexpr (STAGE) Fmt::load_act_lds(act, u, 0, x1);
         else Fmt::load_act(a, u, 0, x1);
+    }
+    typename Fmt::Act xr[M > 1 ? M : 1];
+    if constexpr (M > 1) {
+#pragma unroll
+        for (int t = 0; t < M; ++t) {
+            if constexpr (STAGE) Fmt::load_act_lds(act, u, t, xr[t]);
+            else Fmt::load_act(a, u, t, xr[t]);
+        }
     }
 
     // dot products of one tile's weights into vals
@@ -489,8 +497,7 @@ void gemv_fused_kernel(FusedArgs a) {
         for (int t = 0; t < M; ++t) {
             typename Fmt::Act x;
             if constexpr (M == 1) x = x1;
-            else if constexpr (STAGE) Fmt::load_act_lds(act, u, t, x);
-            else Fmt::load_act(a, u, t, x);
+            else x = xr[t];
 #pragma unroll
             for (int r = 0; r < R; ++r) Fmt::dot1(w_[r], u, x, vals[r * M + t]);
         }
