@@ -329,6 +329,9 @@ constexpr int fused_occupancy(int r, int m, int loop) {
     // f32-activation formats: the activation slice (32 to 68 floats) stays
     // in registers
     if (sizeof(typename Fmt::Act) >= 128) return r <= 1 ? 4 : 3;
+    // two register buffers at 2-4 tokens: one 8-wave workgroup per CU, two
+    // waves per SIMD
+    if (loop == 1 && m > 1) return 2;
     return loop == 1 ? (r <= 1 ? (sizeof(typename Fmt::W) > 48 ? 4 : 5) : r <= 2 ? (sizeof(typename Fmt::W) > 48 ? 3 : 4) : 2)
            : loop == 2 ? (r <= 1 ? (sizeof(typename Fmt::W) > 48 ? 5 : 7)
                           : r <= 2 ? (sizeof(typename Fmt::W) > 48 ? 4 : 5)
@@ -736,9 +739,31 @@ static hipError_t launch_fused_m(FusedArgs a, int r1, int loop, hipStream_t st) 
             if (r1 == 1) return launch_fused_fmt<Fmt, 1, 1, NW, STAGE, 0>(a, st);
             if (r1 == 4) return launch_fused_fmt<Fmt, 1, 4, NW, STAGE, 0>(a, st);
             return launch_fused_fmt<Fmt, 1, 2, NW, STAGE, 0>(a, st);
-        case 2: return launch_fused_fmt<Fmt, 2, 1, NW, STAGE, 0>(a, st);
-        case 3: return launch_fused_fmt<Fmt, 3, 1, NW, STAGE, 0>(a, st);
-        case 4: return launch_fused_fmt<Fmt, 4, 1, NW, STAGE, 0>(a, st);
+        case 2:
+        case 3:
+        case 4: {
+            // 2-4 tokens (measured on the Llama-3-8B and hybrid ~4B decode
+            // steps): mid-size unsplit launches (4096 < 1-row tiles <= 12288,
+            // e.g. q+k+v [6144 x 4096]: 11.8 -> 10.1 us at m = 4) take two
+            // register buffers at one workgroup per CU; otherwise workgroup
+            // tiles, two rows per slot at m = 2 (gate+up [28672 x 4096]:
+            // 17.5 -> 16.4 us) and one at m = 3, 4 (the registers hold every
+            // token's activation slice).
+            if constexpr (NW == 8 && STAGE) {
+                int tiles = 0;
+                for (int z = 0; z < a.nmat; ++z) tiles += (a.n_out[z] + (64 / a.G) - 1) / (64 / a.G);
+                const int per_gen = device_cus() * NW;
+                if (a.KS == 1 && tiles > 2 * per_gen && tiles <= 6 * per_gen) {
+                    if (a.m == 2) return launch_fused_fmt<Fmt, 2, 1, NW, STAGE, 1>(a, st, 1);
+                    if (a.m == 3) return launch_fused_fmt<Fmt, 3, 1, NW, STAGE, 1>(a, st, 1);
+                    return launch_fused_fmt<Fmt, 4, 1, NW, STAGE, 1>(a, st, 1);
+                }
+                if (a.m == 2) return launch_fused_fmt<Fmt, 2, 2, NW, STAGE, 0>(a, st);
+            }
+            if (a.m == 2) return launch_fused_fmt<Fmt, 2, 1, NW, STAGE, 0>(a, st);
+            if (a.m == 3) return launch_fused_fmt<Fmt, 3, 1, NW, STAGE, 0>(a, st);
+            return launch_fused_fmt<Fmt, 4, 1, NW, STAGE, 0>(a, st);
+        }
         default: return hipErrorInvalidValue;
     }
 }
