@@ -12,6 +12,13 @@ hipError_t launch_gemv_fused_more(int type, const FusedArgs &a, bool stage, hipS
 
 using namespace exq;
 
+// Rows split over three waves (12-wave workgroups) are instantiated for one
+// staged token of Q4_K / Q6_K rows (EXQ_FUSED_KS3=0: never).
+static bool fused_with3(int type, int m, bool staged) {
+    static const int ks3 = env_int("EXQ_FUSED_KS3", 1);
+    return ks3 != 0 && m == 1 && staged && (type == kTypeQ4_K || type == kTypeQ6_K);
+}
+
 // True when the fused kernel covers (type, K, m): every unit in one pass and
 // the quantized activation fits the LDS budget.
 bool gemv_fused_supported(int type, int K, int m) {
@@ -143,7 +150,9 @@ hipError_t launch_gemv_fused_layer(int type, int nmat, const uint8_t *const *w, 
         return hipErrorInvalidValue;
     a.nblk = q8_0_family(type) ? K / kQK8_0 : K / kQKK;
     a.U = q8_0_family(type) ? a.nblk : a.nblk * 4;
-    if (!pick_fused_shape(a.U, a.G, a.KS)) return hipErrorInvalidValue;
+    // three waves per row: one-token K-quant launches (Q4_K, Q6_K)
+    const bool with3 = fused_with3(type, m, x != nullptr);
+    if (!pick_fused_shape(a.U, a.G, a.KS, with3)) return hipErrorInvalidValue;
     switch (type) {
         case kTypeQ8_0: return dispatch_fused<FmtQ80>(a, x != nullptr, code, st);
         case kTypeQ4_K: return dispatch_fused<FmtQ4K>(a, x != nullptr, code, st);
@@ -172,8 +181,8 @@ bool gemv_fused_pro_supported(int type, int K, int pro) {
     if (!gemv_fused_supported(type, K, 1)) return false;
     const int U = type == kTypeQ8_0 ? K / kQK8_0 : (K / kQKK) * 4;
     int G = 64, KS = 1;
-    if (!pick_fused_shape(U, G, KS)) return false;
+    if (!pick_fused_shape(U, G, KS, fused_with3(type, 1, true))) return false;
     if (pro != 1) return true;
     if (type == kTypeQ8_0) return K <= 8 * 64 * 4;
-    return K <= (KS > 1 ? 16 * 64 * 16 : 8 * 64 * 16);
+    return K <= (KS == 3 ? 12 : KS > 1 ? 16 : 8) * 64 * 16;
 }

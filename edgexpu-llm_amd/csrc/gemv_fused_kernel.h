@@ -787,6 +787,30 @@ static int pick_r16(const FusedArgs &a, int r_env) {
     return r16;
 }
 
+// One token of a K-quant row split over three waves (12-wave workgroups,
+// four row groups): rows per slot by grid fill as pick_r16.
+template <class Fmt, int PRO = 0>
+static hipError_t launch_fused_ks3(FusedArgs a, hipStream_t st) {
+    constexpr bool kPair = (PRO & 8) != 0;
+    constexpr int kRMax = sizeof(typename Fmt::W) > 48 ? 2 : 4;
+    const int cus = device_cus();
+    auto fill = [&](int r) {
+        int tiles = 0;
+        for (int z = 0; z < a.nmat; ++z) tiles += (a.n_out[z] * (kPair ? 2 : 1) + r - 1) / r;
+        const int wg_tiles = (tiles + 3) / 4, rounds = (wg_tiles + cus - 1) / cus;
+        return (double)wg_tiles / (double)(rounds * cus);
+    };
+    int r = kRMax;
+    if (kRMax == 4 && fill(2) > fill(r) + 1e-9) r = 2;
+    if (!kPair && fill(1) > fill(r) + 1e-9) r = 1;
+    if constexpr (!kPair) {
+        if (r == 1) return launch_fused_fmt<Fmt, 1, 1, 12, true, 0, PRO>(a, st);
+    }
+    if (r == 2) return launch_fused_fmt<Fmt, 1, 2, 12, true, 0, PRO>(a, st);
+    if constexpr (kRMax == 4) return launch_fused_fmt<Fmt, 1, 4, 12, true, 0, PRO>(a, st);
+    return hipErrorInvalidValue;
+}
+
 // One token with a staging prologue (PRO 1: RMSNorm, 2: SiLU-mul), a
 // residual (bit 2) or gate/up pairs (bit 3): the default one-token schedules
 // of launch_fused_nw, instantiated with them (pairs take an even row count
@@ -797,6 +821,7 @@ static hipError_t launch_fused_pro(FusedArgs a, hipStream_t st) {
     if (a.m != 1 || a.KS > 4) return hipErrorInvalidValue;
     if (a.KS > 1) {
         if constexpr (Fmt::kUnitsPerBlock == 4) {
+            if (a.KS == 3) return launch_fused_ks3<Fmt, PRO>(a, st);
             int r16 = pick_r16<Fmt>(a, 0);
             if constexpr (kPair) {
                 // pairs per slot 1 or 2: the count whose workgroup tiles fill the grid best
@@ -855,6 +880,7 @@ static hipError_t launch_fused_nw(FusedArgs a, bool stage, hipStream_t st) {
     // 6.9 | 8.4 us (R = 1) against 8.5 | 9.7 us (R = 4).  Q6_K has at most
     // two rows per slot: four exceed the 128 registers of such a workgroup.
     if constexpr (Fmt::kUnitsPerBlock == 4) {  // Q8_K activations (Q4_K, Q6_K rows)
+        if (stage && a.m == 1 && a.KS == 3) return launch_fused_ks3<Fmt>(a, st);
         if (stage && a.m == 1 && a.KS > 1) {
             static const int r_env = env_int("EXQ_FUSED_NW16_R", 0);  // tuning override: rows per slot
             const int r16 = pick_r16<Fmt>(a, r_env);
@@ -870,11 +896,15 @@ static hipError_t launch_fused_nw(FusedArgs a, bool stage, hipStream_t st) {
 
 // Lanes per slot G and waves per row KS for U units so that every unit is
 // covered in one pass (G * KS >= U) with the best lane use; KS <= 4 so that
-// both workgroup sizes can hold a row group.
-static bool pick_fused_shape(int U, int &G, int &KS) {
+// both workgroup sizes can hold a row group.  with3: KS = 3 too, for rows of
+// more than 128 units (12-wave workgroups; one token of a K-quant row):
+// measured on the Q6_K down [2560 x 9728] (152 units), 12.1 -> 10.0 us; the
+// 40-unit rows of K = 2560 ran slower as 3 x 16 lanes than as 64.
+static bool pick_fused_shape(int U, int &G, int &KS, bool with3 = false) {
     double best = -1.0;
     bool found = false;
-    for (int ks = 1; ks <= 4; ks *= 2) {
+    for (int ks = 1; ks <= 4; ++ks) {
+        if (ks == 3 && (!with3 || U <= 128)) continue;  // only where four waves were the choice
         for (int g = 64; g >= 16; g >>= 1) {
             if (g * ks < U) continue;
             const double util = (double)U / (double)(g * ks);

@@ -141,7 +141,8 @@ def _separate(ws, qt, x, n_outs, n_in, x2=None, nw=None, eps=1e-5, biases=None, 
 
 @pytest.mark.parametrize("qt,n_in,n_outs", [(12, 4096, (4096, 1024, 1024)), (12, 4096, (14336, 14336)),
                                             (8, 576, (576, 192, 192)), (14, 2560, (1000,)),
-                                            (12, 14336, (4096,)), (12, 8192, (515, 33))])
+                                            (12, 14336, (4096,)), (12, 8192, (515, 33)),
+                                            (12, 12288, (700, 33)), (14, 9728, (300,))])
 def test_layer_linear_rmsnorm(hipdev, ora, qt, n_in, n_outs):
     """act = rmsnorm(x) in the GEMV's staging (one token): equal to the
     separate device rmsnorm + projection bit for bit, and within the bound of
@@ -164,7 +165,8 @@ def test_layer_linear_rmsnorm(hipdev, ora, qt, n_in, n_outs):
         assert np.all(np.abs(g - want) <= TOL * S), f"matrix {z}"
 
 
-@pytest.mark.parametrize("qt,n_in,n_out", [(12, 14336, 4096), (14, 9728, 2560), (8, 1536, 576), (12, 4096, 300)])
+@pytest.mark.parametrize("qt,n_in,n_out", [(12, 14336, 4096), (14, 9728, 2560), (8, 1536, 576), (12, 4096, 300),
+                                           (12, 9728, 1000)])
 def test_layer_linear_silu_mul_residual(hipdev, ora, qt, n_in, n_out):
     """down: act = silu(gate) * up in the staging, out = residual + proj in
     the store, written over the residual (in place)."""
@@ -239,7 +241,7 @@ def test_layer_linear_rejects_both_prologues(hipdev):
 
 
 @pytest.mark.parametrize("qt,n_in,n_ff", [(12, 4096, 14336), (14, 2560, 1000), (8, 576, 1536), (12, 14336, 4096),
-                                          (12, 8192, 515), (12, 4096, 300)])
+                                          (12, 8192, 515), (12, 4096, 300), (12, 9728, 700), (14, 12288, 301)])
 @pytest.mark.parametrize("norm", [True, False])
 def test_gate_up_silu(hipdev, ora, qt, n_in, n_ff, norm):
     """act = silu(gate) * up from one launch (gate row j and up row j in the

@@ -151,7 +151,8 @@ def test_linear_golden(hipdev, ora, golden, name):
 @pytest.mark.parametrize("qt,n_in,n_out", [(8, 576, 577), (8, 1536, 300), (12, 4096, 1001), (12, 2560, 515),
                                            (12, 14336, 130), (14, 2560, 260), (14, 9728, 129), (12, 256, 70),
                                            (14, 256, 33), (8, 32, 65), (12, 16384, 67), (14, 16384, 35),
-                                           (12, 4352, 21), (14, 8192, 513)])
+                                           (12, 4352, 21), (14, 8192, 513), (12, 12288, 77), (12, 9728, 300),
+                                           (14, 8448, 65)])
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 11])
 def test_linear_random_vs_oracle(hipdev, ora, qt, n_in, n_out, m):
     rng = np.random.default_rng(qt * 1000 + n_in + n_out + m)
