@@ -23,10 +23,7 @@ __device__ __forceinline__ void store8(float *dst, const float (&y)[8]) {
 }
 
 // 4 threads per 34-byte block.
-__global__ __launch_bounds__(256) void dequant_q8_0_kernel(const uint8_t *__restrict__ src,
-                                                           long long n_threads, float *__restrict__ dst) {
-    const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= n_threads) return;
+__device__ __forceinline__ void dq_q8_0(const uint8_t *__restrict__ src, long long t, float *__restrict__ dst) {
     const long long b = t >> 2;
     const int p = (int)(t & 3);
     const uint8_t *blk = src + b * kBytesQ8_0;
@@ -42,12 +39,16 @@ __global__ __launch_bounds__(256) void dequant_q8_0_kernel(const uint8_t *__rest
     store8(dst + b * kQK8_0 + 8 * p, y);
 }
 
-// 32 threads per 144-byte super-block; thread p covers elements 8p..8p+7,
-// which lie in sub-block s = p/4 (64-chunk j = s/2, nibble half s&1).
-__global__ __launch_bounds__(256) void dequant_q4_k_kernel(const uint8_t *__restrict__ src,
+__global__ __launch_bounds__(256) void dequant_q8_0_kernel(const uint8_t *__restrict__ src,
                                                            long long n_threads, float *__restrict__ dst) {
     const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= n_threads) return;
+    dq_q8_0(src, t, dst);
+}
+
+// 32 threads per 144-byte super-block; thread p covers elements 8p..8p+7,
+// which lie in sub-block s = p/4 (64-chunk j = s/2, nibble half s&1).
+__device__ __forceinline__ void dq_q4_k(const uint8_t *__restrict__ src, long long t, float *__restrict__ dst) {
     const long long b = t >> 5;
     const int p = (int)(t & 31);
     const uint8_t *sb = src + b * kBytesQ4_K;
@@ -82,12 +83,16 @@ __global__ __launch_bounds__(256) void dequant_q4_k_kernel(const uint8_t *__rest
     store8(dst + b * kQKK + 8 * p, y);
 }
 
-// 32 threads per 210-byte super-block; thread p covers elements 8p..8p+7:
-// half h = p/16, quarter k = (p%16)/4, position l0 = 8*(p%4).
-__global__ __launch_bounds__(256) void dequant_q6_k_kernel(const uint8_t *__restrict__ src,
+__global__ __launch_bounds__(256) void dequant_q4_k_kernel(const uint8_t *__restrict__ src,
                                                            long long n_threads, float *__restrict__ dst) {
     const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= n_threads) return;
+    dq_q4_k(src, t, dst);
+}
+
+// 32 threads per 210-byte super-block; thread p covers elements 8p..8p+7:
+// half h = p/16, quarter k = (p%16)/4, position l0 = 8*(p%4).
+__device__ __forceinline__ void dq_q6_k(const uint8_t *__restrict__ src, long long t, float *__restrict__ dst) {
     const long long b = t >> 5;
     const int p = (int)(t & 31);
     const uint8_t *sb = src + b * kBytesQ6_K;
@@ -112,12 +117,16 @@ __global__ __launch_bounds__(256) void dequant_q6_k_kernel(const uint8_t *__rest
     store8(dst + b * kQKK + 8 * p, y);
 }
 
-// 4 threads per 18-byte Q4_0 block; thread p covers elements 8p..8p+7: the
-// low (p < 2) or high nibbles of qs[8(p&1) .. 8(p&1)+7].
-__global__ __launch_bounds__(256) void dequant_q4_0_kernel(const uint8_t *__restrict__ src,
+__global__ __launch_bounds__(256) void dequant_q6_k_kernel(const uint8_t *__restrict__ src,
                                                            long long n_threads, float *__restrict__ dst) {
     const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= n_threads) return;
+    dq_q6_k(src, t, dst);
+}
+
+// 4 threads per 18-byte Q4_0 block; thread p covers elements 8p..8p+7: the
+// low (p < 2) or high nibbles of qs[8(p&1) .. 8(p&1)+7].
+__device__ __forceinline__ void dq_q4_0(const uint8_t *__restrict__ src, long long t, float *__restrict__ dst) {
     const long long b = t >> 2;
     const int p = (int)(t & 3);
     const uint8_t *blk = src + b * kBytesQ4_0;
@@ -134,12 +143,16 @@ __global__ __launch_bounds__(256) void dequant_q4_0_kernel(const uint8_t *__rest
     store8(dst + b * kQK8_0 + 8 * p, y);
 }
 
-// 4 threads per 22-byte Q5_0 block, elements as Q4_0; the fifth bit of
-// element e is bit e of the block's qh word.
-__global__ __launch_bounds__(256) void dequant_q5_0_kernel(const uint8_t *__restrict__ src,
+__global__ __launch_bounds__(256) void dequant_q4_0_kernel(const uint8_t *__restrict__ src,
                                                            long long n_threads, float *__restrict__ dst) {
     const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= n_threads) return;
+    dq_q4_0(src, t, dst);
+}
+
+// 4 threads per 22-byte Q5_0 block, elements as Q4_0; the fifth bit of
+// element e is bit e of the block's qh word.
+__device__ __forceinline__ void dq_q5_0(const uint8_t *__restrict__ src, long long t, float *__restrict__ dst) {
     const long long b = t >> 2;
     const int p = (int)(t & 3);
     const uint8_t *blk = src + b * kBytesQ5_0;
@@ -157,13 +170,17 @@ __global__ __launch_bounds__(256) void dequant_q5_0_kernel(const uint8_t *__rest
     store8(dst + b * kQK8_0 + 8 * p, y);
 }
 
-// 32 threads per 176-byte Q5_K super-block; thread p covers elements
-// 8p..8p+7 of sub-block s = p/4 (64-chunk j = s/2, nibble half s&1), whose
-// fifth bits are bit s of qh[8(p&3) .. 8(p&3)+7].
-__global__ __launch_bounds__(256) void dequant_q5_k_kernel(const uint8_t *__restrict__ src,
+__global__ __launch_bounds__(256) void dequant_q5_0_kernel(const uint8_t *__restrict__ src,
                                                            long long n_threads, float *__restrict__ dst) {
     const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= n_threads) return;
+    dq_q5_0(src, t, dst);
+}
+
+// 32 threads per 176-byte Q5_K super-block; thread p covers elements
+// 8p..8p+7 of sub-block s = p/4 (64-chunk j = s/2, nibble half s&1), whose
+// fifth bits are bit s of qh[8(p&3) .. 8(p&3)+7].
+__device__ __forceinline__ void dq_q5_k(const uint8_t *__restrict__ src, long long t, float *__restrict__ dst) {
     const long long b = t >> 5;
     const int p = (int)(t & 31);
     const uint8_t *sb = src + b * kBytesQ5_K;
@@ -199,11 +216,17 @@ __global__ __launch_bounds__(256) void dequant_q5_k_kernel(const uint8_t *__rest
     store8(dst + b * kQKK + 8 * p, y);
 }
 
+__global__ __launch_bounds__(256) void dequant_q5_k_kernel(const uint8_t *__restrict__ src,
+                                                           long long n_threads, float *__restrict__ dst) {
+    const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_threads) return;
+    dq_q5_k(src, t, dst);
+}
+
 // F16: one thread per 8 elements (the last thread of an n not divisible by
 // 8 converts the remainder one by one).
-__global__ __launch_bounds__(256) void dequant_f16_kernel(const uint8_t *__restrict__ src, long long n,
-                                                          float *__restrict__ dst) {
-    const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void dq_f16(const uint8_t *__restrict__ src, long long t, long long n,
+                                       float *__restrict__ dst) {
     const long long e0 = 8 * t;
     if (e0 >= n) return;
     if (e0 + 8 <= n) {
@@ -218,9 +241,75 @@ __global__ __launch_bounds__(256) void dequant_f16_kernel(const uint8_t *__restr
     }
 }
 
+__global__ __launch_bounds__(256) void dequant_f16_kernel(const uint8_t *__restrict__ src, long long n,
+                                                          float *__restrict__ dst) {
+    dq_f16(src, (long long)blockIdx.x * blockDim.x + threadIdx.x, n, dst);
+}
+
+// Rows of a GGUF matrix gathered by index (the embedding lookup of
+// src/native.c:428-443 through edgexpu_gguf_dequantize_row,
+// src/gguf_quant.c:428-466): token y's row ids[y] dequantized into
+// out[y][0..n_embd) with the bulk kernels' per-thread arithmetic
+// (threads_per_row threads of 8 outputs each).  An index outside
+// [0, n_rows) gives a row of zeros and sets *bad (when given) to 1.
+template <int TYPE>
+__global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t *__restrict__ table, size_t row_bytes,
+                                                           long long n_rows, const int32_t *__restrict__ ids,
+                                                           int n_embd, long long threads_per_row,
+                                                           float *__restrict__ out, int *bad) {
+    const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= threads_per_row) return;
+    const int id = ids[blockIdx.y];
+    float *dst = out + (size_t)blockIdx.y * n_embd;
+    if (id < 0 || (long long)id >= n_rows) {
+        for (long long e = 8 * t; e < 8 * t + 8 && e < n_embd; ++e) dst[e] = 0.0f;
+        if (t == 0 && bad != nullptr) *bad = 1;
+        return;
+    }
+    const uint8_t *src = table + (size_t)id * row_bytes;
+    if constexpr (TYPE == kTypeQ8_0) dq_q8_0(src, t, dst);
+    else if constexpr (TYPE == kTypeQ4_0) dq_q4_0(src, t, dst);
+    else if constexpr (TYPE == kTypeQ5_0) dq_q5_0(src, t, dst);
+    else if constexpr (TYPE == kTypeQ4_K) dq_q4_k(src, t, dst);
+    else if constexpr (TYPE == kTypeQ5_K) dq_q5_k(src, t, dst);
+    else if constexpr (TYPE == kTypeQ6_K) dq_q6_k(src, t, dst);
+    else dq_f16(src, t, n_embd, dst);
+}
+
 }  // namespace exq
 
 using namespace exq;
+
+// n_ids rows ids[0..n_ids) of a [n_rows x n_embd] matrix of `type` into
+// out[n_ids][n_embd] (16-byte aligned; n_embd a multiple of the block, of
+// 32 for F16).
+hipError_t launch_dequantize_rows(const uint8_t *table, int type, long long n_rows, int n_embd, const int32_t *ids,
+                                  int n_ids, float *out, int *bad, hipStream_t st) {
+    const bool q80 = q8_0_family(type);
+    const int be = q80 ? kQK8_0 : (k_family(type) ? kQKK : 1);
+    const int bb = type == kTypeQ8_0 ? kBytesQ8_0 : type == kTypeQ4_0 ? kBytesQ4_0 : type == kTypeQ5_0 ? kBytesQ5_0
+                 : type == kTypeQ4_K ? kBytesQ4_K : type == kTypeQ5_K ? kBytesQ5_K : type == kTypeQ6_K ? kBytesQ6_K : 2;
+    const size_t row_bytes = (size_t)(n_embd / be) * bb;
+    // threads per row: 4 per 32-element block, 32 per super-block, n/8 for F16
+    const long long tpr = q80 ? (long long)(n_embd / kQK8_0) * 4 : k_family(type) ? (long long)(n_embd / kQKK) * 32
+                                                                               : (long long)((n_embd + 7) / 8);
+    const dim3 grid((unsigned)((tpr + 255) / 256), (unsigned)n_ids);
+#define EXQ_ROWS(T)                                                                                                 \
+    hipLaunchKernelGGL(dequant_rows_kernel<T>, grid, dim3(256), 0, st, table, row_bytes, n_rows, ids, n_embd, tpr, \
+                       out, bad)
+    switch (type) {
+        case kTypeQ8_0: EXQ_ROWS(kTypeQ8_0); break;
+        case kTypeQ4_0: EXQ_ROWS(kTypeQ4_0); break;
+        case kTypeQ5_0: EXQ_ROWS(kTypeQ5_0); break;
+        case kTypeQ4_K: EXQ_ROWS(kTypeQ4_K); break;
+        case kTypeQ5_K: EXQ_ROWS(kTypeQ5_K); break;
+        case kTypeQ6_K: EXQ_ROWS(kTypeQ6_K); break;
+        case kTypeF16: EXQ_ROWS(kTypeF16); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef EXQ_ROWS
+    return hipGetLastError();
+}
 
 hipError_t launch_dequantize(const uint8_t *src, int type, unsigned long long n, float *dst, hipStream_t st) {
     long long threads;

@@ -900,7 +900,7 @@ static hipError_t launch_fused_nw(FusedArgs a, bool stage, hipStream_t st) {
 // more than 128 units (12-wave workgroups; one token of a K-quant row):
 // measured on the Q6_K down [2560 x 9728] (152 units), 12.1 -> 10.0 us; the
 // 40-unit rows of K = 2560 ran slower as 3 x 16 lanes than as 64.
-static bool pick_fused_shape(int U, int &G, int &KS, bool with3 = false) {
+static inline bool pick_fused_shape(int U, int &G, int &KS, bool with3 = false) {
     double best = -1.0;
     bool found = false;
     for (int ks = 1; ks <= 4; ++ks) {

@@ -19,6 +19,8 @@ using namespace exq;
 hipError_t launch_quantize_q8_0(const float *x, int m, int K, int ldx, uint8_t *packed, hipStream_t st);
 hipError_t launch_quantize_q8_k(const float *x, int m, int K, int ldx, uint8_t *packed, hipStream_t st);
 hipError_t launch_dequantize(const uint8_t *src, int type, unsigned long long n, float *dst, hipStream_t st);
+hipError_t launch_dequantize_rows(const uint8_t *table, int type, long long n_rows, int n_embd, const int32_t *ids,
+                                  int n_ids, float *out, int *bad, hipStream_t st);
 hipError_t launch_gemv_q8(int type, const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const uint8_t *xq,
                           size_t xq_stride, const float *bias, float *out, int ldo, hipStream_t st);
 hipError_t launch_gemv_f32(int type, const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const float *xf,
@@ -752,6 +754,32 @@ int edgexpu_hip_dequantize_dev(const void *src, uint32_t type, uint64_t n_elemen
     }
     return hip_ok(launch_dequantize((const uint8_t *)src, (int)type, n_elements, dst, pick_stream(stream)),
                   "dequantize")
+               ? 1
+               : 0;
+}
+
+int edgexpu_hip_embed_rows_dev(float *out, const void *table, uint32_t type, long long n_rows, int n_embd,
+                               const int32_t *ids, int n_ids, int *bad, void *stream) {
+    if (!ensure_init()) return 0;
+    if (out == nullptr || table == nullptr || ids == nullptr || n_rows <= 0 || n_embd <= 0 || n_ids <= 0 ||
+        n_ids > 65535) {
+        set_error(-2, "embed_rows: null buffer or bad size (n_rows=%lld n_embd=%d n_ids=%d, at most 65535 ids)",
+                  n_rows, n_embd, n_ids);
+        return 0;
+    }
+    if (!gpu_type(type)) {
+        set_error(-3, "embed_rows: GGUF type %u is not supported on the GPU (F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)",
+                  type);
+        return 0;
+    }
+    if ((size_t)n_embd % unit_elems(type) != 0 || !aligned16(out)) {
+        set_error(-2, "embed_rows: n_embd=%d must be a multiple of %zu for type %u and out 16-byte aligned", n_embd,
+                  unit_elems(type), type);
+        return 0;
+    }
+    return hip_ok(launch_dequantize_rows((const uint8_t *)table, (int)type, n_rows, n_embd, ids, n_ids, out, bad,
+                                         pick_stream(stream)),
+                  "embed_rows")
                ? 1
                : 0;
 }

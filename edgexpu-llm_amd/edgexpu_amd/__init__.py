@@ -80,6 +80,8 @@ class HipLib:
         self.logits_dev = _sig(L, "edgexpu_hip_logits_dev", C.c_int,
                                [_vp, _vp, _vp, _vp, C.c_uint32, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp])
         self.dequant_dev = _sig(L, "edgexpu_hip_dequantize_dev", C.c_int, [_vp, C.c_uint32, C.c_uint64, _vp, _vp])
+        self.embed_rows_dev = _sig(L, "edgexpu_hip_embed_rows_dev", C.c_int,
+                                   [_vp, _vp, C.c_uint32, C.c_longlong, C.c_int, _vp, C.c_int, _vp, _vp])
         self.q80_dev = _sig(L, "edgexpu_hip_quantize_q8_0_dev", C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp])
         self.q8k_dev = _sig(L, "edgexpu_hip_quantize_q8_k_dev", C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp])
         self.linear_host_w = _sig(L, "edgexpu_hip_linear_quant_batch", C.c_int, [_vp, _vp, _vp, C.c_int])
@@ -210,6 +212,21 @@ def dequantize(src, qtype: int, n: int, dst=None):
     L = hip()
     L.check(L.dequant_dev(_ptr(src), qtype, n, _ptr(dst), _stream()), "dequantize")
     return dst
+
+
+def embed_rows(table, qtype: int, n_rows: int, n_embd: int, ids, bad=None, out=None):
+    """out[len(ids), n_embd] = rows ids of the GGUF matrix `table` dequantized
+    (edgexpu_hip_embed_rows_dev); ids is an int32 device tensor, bad an optional
+    int32 device tensor of one element set to 1 for an index out of range."""
+    import torch
+
+    n = ids.numel()
+    if out is None:
+        out = torch.empty((n, n_embd), dtype=torch.float32, device=ids.device)
+    L = hip()
+    L.check(L.embed_rows_dev(_ptr(out), _ptr(table), qtype, n_rows, n_embd, _ptr(ids), n, _ptr(bad), _stream()),
+            "embed_rows")
+    return out
 
 
 def quantize_q8_0(x):

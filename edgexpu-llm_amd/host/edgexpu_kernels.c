@@ -150,6 +150,34 @@ const edgexpu_hip_weight *edgexpu_kernels_lookup_weight(const uint8_t *blocks) {
     return e != NULL ? e->w : NULL;
 }
 
+uint64_t edgexpu_gguf_tensor_elements(const edgexpu_gguf_tensor *tensor) {
+    uint64_t n = 1;
+    uint32_t i;
+    if (tensor == NULL) {
+        return 0;
+    }
+    for (i = 0; i < tensor->n_dims && i < 4; i++) {
+        n *= tensor->dims[i];
+    }
+    return n;
+}
+
+size_t edgexpu_gguf_tensor_nbytes(const edgexpu_gguf_tensor *tensor) {
+    uint64_t n;
+    size_t bs;
+    size_t bb;
+    if (tensor == NULL) {
+        return 0;
+    }
+    n = edgexpu_gguf_tensor_elements(tensor);
+    bs = edgexpu_gguf_type_block_size(tensor->type);
+    bb = edgexpu_gguf_type_block_bytes(tensor->type);
+    if (bs == 0 || bb == 0 || n % bs != 0) {
+        return 0;
+    }
+    return (size_t)(n / bs) * bb;
+}
+
 /* ------------------------------------------------------------ dequant */
 
 int edgexpu_gguf_dequantize(const uint8_t *src, uint32_t type, uint64_t n_elements, float *dst, char *error,
@@ -176,6 +204,47 @@ int edgexpu_gguf_dequantize(const uint8_t *src, uint32_t type, uint64_t n_elemen
         return 0;
     }
     return 1;
+}
+
+int edgexpu_gguf_dequantize_q8_0_rows(const uint8_t *src, uint64_t row, int n_embd, float *dst) {
+    size_t rb;
+    if (src == NULL || dst == NULL || n_embd <= 0 || n_embd % 32 != 0) {
+        return 0; /* src/gguf_quant.c:420-422 */
+    }
+    rb = (size_t)(n_embd / 32) * 34;
+    return edgexpu_gguf_dequantize(src + row * rb, EDGEXPU_GGUF_TYPE_Q8_0, (uint64_t)n_embd, dst, NULL, 0);
+}
+
+int edgexpu_gguf_dequantize_row(const uint8_t *src, const edgexpu_gguf_tensor *tensor, uint64_t row, int n_embd,
+                                float *dst, char *error, size_t error_size) {
+    uint64_t n;
+    uint64_t rows;
+    size_t nbytes;
+    /* the checks and messages of src/gguf_quant.c:442-463 */
+    if (src == NULL || tensor == NULL || dst == NULL || n_embd <= 0) {
+        set_msg(error, error_size, "dequantize_row 参数为空");
+        return 0;
+    }
+    n = edgexpu_gguf_tensor_elements(tensor);
+    if (n == 0 || n % (uint64_t)n_embd != 0) {
+        set_msg(error, error_size, "tensor 行宽与 embedding_length 不匹配");
+        return 0;
+    }
+    rows = n / (uint64_t)n_embd;
+    if (row >= rows) {
+        set_msg(error, error_size, "tensor 行越界");
+        return 0;
+    }
+    if (tensor->type == EDGEXPU_GGUF_TYPE_Q8_0) {
+        return edgexpu_gguf_dequantize_q8_0_rows(src, row, n_embd, dst);
+    }
+    nbytes = edgexpu_gguf_tensor_nbytes(tensor);
+    if (nbytes == 0 || nbytes % rows != 0) {
+        set_msg(error, error_size, "tensor 字节数无法按行切分");
+        return 0;
+    }
+    return edgexpu_gguf_dequantize(src + row * (nbytes / rows), tensor->type, (uint64_t)n_embd, dst, error,
+                                   error_size);
 }
 
 /* ------------------------------------------------------------ quantizers */
@@ -205,6 +274,15 @@ float edgexpu_gguf_dot_quant(uint32_t type, const uint8_t *row, const float *x, 
         return 0.0f;
     }
     return out;
+}
+
+float edgexpu_gguf_q8_0_dot_row(const uint8_t *src, uint64_t row, int n_embd, const float *x) {
+    if (src == NULL || x == NULL || n_embd <= 0 || n_embd % 32 != 0) {
+        return 0.0f; /* src/gguf_quant.c:927-929 */
+    }
+    return edgexpu_gguf_dot_quant(EDGEXPU_GGUF_TYPE_Q8_0, src + row * edgexpu_gguf_row_bytes(EDGEXPU_GGUF_TYPE_Q8_0,
+                                                                                             n_embd),
+                                  x, n_embd);
 }
 
 float edgexpu_gguf_dot_quant_q8(uint32_t type, const uint8_t *wrow, const uint8_t *x_q8, int n) {
@@ -310,4 +388,114 @@ static const edgexpu_kernel_set g_hip_set = {
 
 const edgexpu_kernel_set *edgexpu_kernels_hip(void) {
     return &g_hip_set;
+}
+
+/* ------------------------------------------------------------ self-test */
+
+/* The known-answer checks of src/gguf_quant.c:934-1061, each built here and
+ * run through this kernel set (so on the GPU). */
+int edgexpu_gguf_quant_selftest(char *error, size_t error_size) {
+    const uint16_t one = 0x3c00; /* fp16 1.0 */
+    const uint16_t two = 0x4000; /* fp16 2.0 */
+    char msg[160];
+    float fused;
+    int i;
+    { /* Q4_K: d = 1, sc0 = 1, code 2 at element 0; x[0] = 3 -> 6 */
+        uint8_t blk[144];
+        float x[256];
+        memset(blk, 0, sizeof(blk));
+        memset(x, 0, sizeof(x));
+        memcpy(blk, &one, 2);
+        blk[4] = 1;
+        blk[16] = 0x02;
+        x[0] = 3.0f;
+        fused = edgexpu_gguf_dot_quant(EDGEXPU_GGUF_TYPE_Q4_K, blk, x, 256);
+        if (!(fused > 6.0f - 1e-3f && fused < 6.0f + 1e-3f)) {
+            snprintf(msg, sizeof(msg), "q4_k fused dot selftest failed fused=%.6f", fused);
+            set_msg(error, error_size, msg);
+            return 0;
+        }
+    }
+    { /* Q4_0: low nibble 9 (value 1) at element 0; x[0] = 3 -> 3 */
+        uint8_t blk[18];
+        float x[32];
+        memset(blk, 0, sizeof(blk));
+        memset(x, 0, sizeof(x));
+        memcpy(blk, &one, 2);
+        for (i = 0; i < 16; i++) {
+            blk[2 + i] = 0x88; /* value 0 */
+        }
+        blk[2] = 0x89;
+        x[0] = 3.0f;
+        fused = edgexpu_gguf_dot_quant(EDGEXPU_GGUF_TYPE_Q4_0, blk, x, 32);
+        if (!(fused > 3.0f - 1e-3f && fused < 3.0f + 1e-3f)) {
+            snprintf(msg, sizeof(msg), "q4_0 fused dot selftest failed fused=%.6f", fused);
+            set_msg(error, error_size, msg);
+            return 0;
+        }
+    }
+    { /* F16: {1, 2} . {2, 3} = 8 */
+        uint8_t h[64];
+        float x[32];
+        memset(h, 0, sizeof(h));
+        memset(x, 0, sizeof(x));
+        memcpy(h, &one, 2);
+        memcpy(h + 2, &two, 2);
+        x[0] = 2.0f;
+        x[1] = 3.0f;
+        fused = edgexpu_gguf_dot_quant(EDGEXPU_GGUF_TYPE_F16, h, x, 32);
+        if (!(fused > 8.0f - 1e-3f && fused < 8.0f + 1e-3f)) {
+            snprintf(msg, sizeof(msg), "f16 fused dot selftest failed fused=%.6f", fused);
+            set_msg(error, error_size, msg);
+            return 0;
+        }
+    }
+    { /* Q5_K: d = 1, sc0 = 1, code 2 at element 0; x[0] = 3 -> 6 */
+        uint8_t blk[176];
+        float x[256];
+        memset(blk, 0, sizeof(blk));
+        memset(x, 0, sizeof(x));
+        memcpy(blk, &one, 2);
+        blk[4] = 1;
+        blk[48] = 0x02;
+        x[0] = 3.0f;
+        fused = edgexpu_gguf_dot_quant(EDGEXPU_GGUF_TYPE_Q5_K, blk, x, 256);
+        if (!(fused > 6.0f - 1e-3f && fused < 6.0f + 1e-3f)) {
+            snprintf(msg, sizeof(msg), "q5_k fused dot selftest failed fused=%.6f", fused);
+            set_msg(error, error_size, msg);
+            return 0;
+        }
+    }
+    { /* Q8_0 x Q8_0: all-ones codes, d = 1, x = 1 -> 32; Q5_0 zero codes -> -512 */
+        uint8_t w[34];
+        uint8_t xq[34];
+        float x[32];
+        for (i = 0; i < 32; i++) {
+            x[i] = 1.0f;
+        }
+        memset(w, 0, sizeof(w));
+        memcpy(w, &one, 2);
+        for (i = 0; i < 32; i++) {
+            w[2 + i] = 1;
+        }
+        if (!edgexpu_gguf_quantize_q8_0(x, 32, xq)) {
+            set_msg(error, error_size, "q8_0 quantize selftest failed");
+            return 0;
+        }
+        fused = edgexpu_gguf_dot_quant_q8(EDGEXPU_GGUF_TYPE_Q8_0, w, xq, 32);
+        if (!(fused > 32.0f - 0.5f && fused < 32.0f + 0.5f)) {
+            snprintf(msg, sizeof(msg), "q8_0 integer dot selftest failed fused=%.6f", fused);
+            set_msg(error, error_size, msg);
+            return 0;
+        }
+        memset(w, 0, 22);
+        memcpy(w, &one, 2);
+        fused = edgexpu_gguf_dot_quant_q8(EDGEXPU_GGUF_TYPE_Q5_0, w, xq, 32);
+        if (!(fused > -512.0f - 1.0f && fused < -512.0f + 1.0f)) {
+            snprintf(msg, sizeof(msg), "q5_0 integer dot selftest failed fused=%.6f", fused);
+            set_msg(error, error_size, msg);
+            return 0;
+        }
+    }
+    return 1;
 }

@@ -144,6 +144,18 @@ int edgexpu_hip_logits_dev(float *scores, uint32_t *best_dev, const float *hidde
  * n_elements must be a multiple of the block size; dst 16-byte aligned. */
 int edgexpu_hip_dequantize_dev(const void *src, uint32_t type, uint64_t n_elements, float *dst, void *stream);
 
+/* Embedding lookup on device: rows ids[0..n_ids) of the [n_rows x n_embd]
+ * matrix `table` (device-resident GGUF rows of `type`) dequantized into
+ * out[n_ids][n_embd] (16-byte aligned), each bit-identical to
+ * edgexpu_gguf_dequantize_row on that row (src/gguf_quant.c:428-466, called
+ * per token by src/native.c:428-443).  ids is a device array (for example
+ * the greedy argmax of the previous step); an id outside [0, n_rows) gives a
+ * row of zeros and, when `bad` (device int) is non-null, stores 1 into it
+ * (the reference reports "row out of range").  n_embd a multiple of the
+ * type's block (32 for F16); 1 <= n_ids <= 65535. */
+int edgexpu_hip_embed_rows_dev(float *out, const void *table, uint32_t type, long long n_rows, int n_embd,
+                               const int32_t *ids, int n_ids, int *bad, void *stream);
+
 /* Activation quantizers writing the reference's block bytes
  * (edgexpu_gguf_quantize_q8_0 / _q8_k, include/edgexpu/gguf_quant.h:80-87,
  * src/gguf_dot_q8.c:269-412): m rows of n f32 -> m*(n/32)*34 or

@@ -7,9 +7,14 @@
  * include/edgexpu/gguf_quant.h links against this library instead of
  * src/cpu_kernel.c + src/gguf_quant.c + src/gguf_dot_q8.c.  Every compute
  * entry runs on the GPU through libedgexpu_hip.so; nothing here computes on
- * the CPU.  GGUF types the GPU does not run (F32, F16, Q4_0, Q5_0, Q5_K) are
- * refused (void entries leave `out` untouched, others return 0 / 0.0f) with a
- * sticky error naming the type, so the host routes them to its CPU kernels.
+ * the CPU.  Every type of the reference's dispatcher runs on the GPU except
+ * F32 rows (and F16 products with n % 32 != 0), which are refused (void
+ * entries leave `out` untouched, others return 0 / 0.0f) with a sticky error
+ * naming the type, so the host routes them to its CPU kernels.
+ *
+ * The row entry points take the reference's edgexpu_gguf_tensor
+ * (include/edgexpu/gguf.h:21-27).  Hosts that include that header include it
+ * before this one; otherwise the same layout is declared here.
  */
 #ifndef EDGEXPU_KERNELS_H
 #define EDGEXPU_KERNELS_H
@@ -44,12 +49,51 @@ size_t edgexpu_gguf_q8_k_nbytes(int n);               /* gguf_quant.h:85, src/gg
 int edgexpu_gguf_can_dot_q8(uint32_t type);           /* gguf_quant.h:82, src/gguf_dot_q8.c:414-423 */
 int edgexpu_gguf_can_dot_q8k(uint32_t type);          /* gguf_quant.h:87, src/gguf_dot_q8.c:425-434 */
 
+#ifndef EDGEXPU_GGUF_H
+/* include/edgexpu/gguf.h:19-27: one entry of the GGUF tensor table, same
+ * field order and types (name, n_dims, type, dims, data offset). */
+#define EDGEXPU_GGUF_TENSOR_NAME 96
+typedef struct edgexpu_gguf_tensor {
+    char name[EDGEXPU_GGUF_TENSOR_NAME];
+    uint32_t n_dims;
+    uint32_t type;
+    uint64_t dims[4];
+    uint64_t offset;
+} edgexpu_gguf_tensor;
+#endif
+
+/* include/edgexpu/gguf_quant.h:28-29 (src/gguf_quant.c:110-136): element
+ * count (product of dims) and block bytes of a tensor; 0 for NULL, unknown
+ * types or counts that are not whole blocks. */
+uint64_t edgexpu_gguf_tensor_elements(const edgexpu_gguf_tensor *tensor);
+size_t edgexpu_gguf_tensor_nbytes(const edgexpu_gguf_tensor *tensor);
+
 /* ---- GPU entry points with the reference signatures ---- */
 
 /* include/edgexpu/gguf_quant.h:32-39 (src/gguf_quant.c:355-411): returns 1 on
  * success, 0 with a message in `error` otherwise. */
 int edgexpu_gguf_dequantize(const uint8_t *src, uint32_t type, uint64_t n_elements, float *dst, char *error,
                             size_t error_size);
+
+/* include/edgexpu/gguf_quant.h:42-57 (src/gguf_quant.c:413-466): one row of
+ * an [rows x n_embd] matrix (the embedding lookup of src/native.c:428-443),
+ * bit-identical to the reference.  _q8_0_rows: Q8_0 rows, returns 0 for bad
+ * arguments; _row: any type, with the reference's checks and messages (row
+ * width, row range, byte split).  Device-resident tables use
+ * edgexpu_hip_embed_rows_dev, which gathers many rows in one launch. */
+int edgexpu_gguf_dequantize_q8_0_rows(const uint8_t *src, uint64_t row, int n_embd, float *dst);
+int edgexpu_gguf_dequantize_row(const uint8_t *src, const edgexpu_gguf_tensor *tensor, uint64_t row, int n_embd,
+                                float *dst, char *error, size_t error_size);
+
+/* include/edgexpu/gguf_quant.h:58-63 (src/gguf_quant.c:920-932): the f32 dot
+ * of row `row` of a Q8_0 matrix with x; 0.0f for bad arguments. */
+float edgexpu_gguf_q8_0_dot_row(const uint8_t *src, uint64_t row, int n_embd, const float *x);
+
+/* include/edgexpu/gguf_quant.h:103 (src/gguf_quant.c:934-1061): the
+ * reference's known-answer checks (Q4_K, Q4_0, F16, Q5_K f32 dots; Q8_0 and
+ * Q5_0 integer dots) run through this kernel set on the GPU; 1 when all pass,
+ * else 0 with the failing check in `error`. */
+int edgexpu_gguf_quant_selftest(char *error, size_t error_size);
 
 /* include/edgexpu/gguf_quant.h:81,86 (src/gguf_dot_q8.c:269-412): reference
  * block bytes, bit-identical to the reference's x86 build. */

@@ -5,6 +5,7 @@ import ctypes as C
 import os
 import re
 
+import numpy as np
 import pytest
 
 import edgexpu_amd as E
@@ -100,3 +101,51 @@ def test_kernel_set_table():
     assert ks.name == b"hip.gfx950"
     assert C.cast(k.edgexpu_cpu_linear_quant_batch, C.c_void_p).value == ks.linear_quant_batch
     assert all(getattr(ks, f) for f, _ in KS._fields_[1:])
+
+
+class _Tensor(C.Structure):
+    """include/edgexpu/gguf.h:21-27 layout."""
+    _fields_ = [("name", C.c_char * 96), ("n_dims", C.c_uint32), ("type", C.c_uint32),
+                ("dims", C.c_uint64 * 4), ("offset", C.c_uint64)]
+
+
+def _tensor(qtype, dims):
+    t = _Tensor()
+    t.n_dims = len(dims)
+    t.type = qtype
+    for i, d in enumerate(dims):
+        t.dims[i] = d
+    return t
+
+
+def test_tensor_sizes_and_row_checks_without_gpu():
+    """edgexpu_gguf_tensor_elements / _nbytes (src/gguf_quant.c:110-136) and the
+    argument checks of edgexpu_gguf_dequantize_row (:442-463), which fail
+    before any GPU work with the reference's messages."""
+    k = C.CDLL(E.KERNELS_SO)
+    k.edgexpu_gguf_tensor_elements.restype = C.c_uint64
+    k.edgexpu_gguf_tensor_nbytes.restype = C.c_size_t
+    for qtype, dims, nbytes in ((12, (4096, 32000), 32000 * 2304), (8, (576, 49152), 49152 * 612),
+                                (1, (7, 3), 42), (13, (2560, 10), 17600), (12, (100, 3), 0), (5, (64,), 0)):
+        t = _tensor(qtype, dims)
+        assert k.edgexpu_gguf_tensor_elements(C.byref(t)) == int(np.prod(dims))
+        assert k.edgexpu_gguf_tensor_nbytes(C.byref(t)) == nbytes
+    assert k.edgexpu_gguf_tensor_nbytes(None) == 0 and k.edgexpu_gguf_tensor_elements(None) == 0
+    k.edgexpu_gguf_dequantize_row.restype = C.c_int
+    k.edgexpu_gguf_dequantize_row.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_int, C.c_void_p, C.c_char_p,
+                                               C.c_size_t]
+    src = (C.c_uint8 * 64)()
+    dst = (C.c_float * 256)()
+    err = C.create_string_buffer(256)
+    t = _tensor(12, (256, 4))
+    assert k.edgexpu_gguf_dequantize_row(src, C.byref(t), 4, 256, dst, err, 256) == 0
+    assert err.value.decode() == "tensor 行越界"
+    assert k.edgexpu_gguf_dequantize_row(src, C.byref(t), 0, 300, dst, err, 256) == 0
+    assert err.value.decode() == "tensor 行宽与 embedding_length 不匹配"
+    assert k.edgexpu_gguf_dequantize_row(None, C.byref(t), 0, 256, dst, err, 256) == 0
+    assert err.value.decode() == "dequantize_row 参数为空"
+    k.edgexpu_gguf_dequantize_q8_0_rows.argtypes = [C.c_void_p, C.c_uint64, C.c_int, C.c_void_p]
+    assert k.edgexpu_gguf_dequantize_q8_0_rows(src, 0, 48, dst) == 0      # not whole blocks
+    k.edgexpu_gguf_q8_0_dot_row.restype = C.c_float
+    k.edgexpu_gguf_q8_0_dot_row.argtypes = [C.c_void_p, C.c_uint64, C.c_int, C.c_void_p]
+    assert k.edgexpu_gguf_q8_0_dot_row(src, 0, 33, dst) == 0.0

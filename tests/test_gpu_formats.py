@@ -318,3 +318,83 @@ def test_unsupported_shapes_are_refused(hipdev):
     x = dev(np.zeros((1, 40), np.float32))
     with pytest.raises(E.HipError):
         E.linear_quant_batch(w, F16, x, 4, 40)
+
+
+# ------------------------------------------------------------------ embedding rows
+
+
+@pytest.mark.parametrize("qt,n_embd", [(Q8_0, 576), (Q4_0, 2048), (Q5_0, 96), (Q4_K, 4096), (Q5_K, 2560),
+                                       (Q6_K, 2560), (F16, 160)])
+def test_embed_rows_bit_exact(hipdev, ora, qt, n_embd):
+    """Rows gathered by device ids (duplicates, first and last row) equal the
+    oracle's dequant of those rows bit for bit; an id out of range gives a
+    zero row and sets the flag."""
+    rng = np.random.default_rng(300 + qt + n_embd)
+    n_rows = 517
+    table = synth.np_weights(qt, n_rows, n_embd, rng)
+    ids = np.array([0, n_rows - 1, 5, 5, 300, 17, 516, 2] * 3, np.int32)
+    bad = torch.zeros(1, dtype=torch.int32, device=DEV)
+    got = E.embed_rows(dev(table), qt, n_rows, n_embd, dev(ids), bad=bad).cpu().numpy()
+    for i, r in enumerate(ids):
+        want = ora.dequantize(np.ascontiguousarray(table[r]), qt, n_embd)
+        assert np.array_equal(bits(got[i]), bits(want)), f"row {r}"
+    assert int(bad.cpu()[0]) == 0
+    ids2 = np.array([3, n_rows, -1, 4], np.int32)
+    got2 = E.embed_rows(dev(table), qt, n_rows, n_embd, dev(ids2), bad=bad).cpu().numpy()
+    assert int(bad.cpu()[0]) == 1
+    assert not got2[1].any() and not got2[2].any()
+    assert np.array_equal(bits(got2[0]), bits(ora.dequantize(np.ascontiguousarray(table[3]), qt, n_embd)))
+
+
+def test_embed_rows_rejects_bad_shapes(hipdev):
+    t = dev(np.zeros((4, 2 * 40), np.uint8))
+    ids = dev(np.zeros(2, np.int32))
+    with pytest.raises(E.HipError):
+        E.embed_rows(t, F16, 4, 40, ids)      # F16 rows need n_embd % 32 == 0
+    with pytest.raises(E.HipError):
+        E.embed_rows(t, 0, 4, 32, ids)       # F32 tables stay on the host
+
+
+@pytest.mark.parametrize("qt,n_embd", [(Q8_0, 576), (Q4_K, 2560), (Q6_K, 256), (Q5_0, 64), (F16, 96)])
+def test_dropin_row_entry_points(kern, ora, qt, n_embd):
+    """edgexpu_gguf_dequantize_row / _q8_0_rows and edgexpu_gguf_q8_0_dot_row
+    (src/gguf_quant.c:413-466, 920-932) with host buffers."""
+    rng = np.random.default_rng(800 + qt)
+    n_rows = 9
+    table = np.ascontiguousarray(synth.np_weights(qt, n_rows, n_embd, rng))
+    kern.edgexpu_gguf_dequantize_row.restype = C.c_int
+    kern.edgexpu_gguf_dequantize_row.argtypes = [_u8p, C.c_void_p, C.c_uint64, C.c_int, _f32p, C.c_char_p,
+                                                  C.c_size_t]
+
+    class T(C.Structure):
+        _fields_ = [("name", C.c_char * 96), ("n_dims", C.c_uint32), ("type", C.c_uint32),
+                    ("dims", C.c_uint64 * 4), ("offset", C.c_uint64)]
+
+    t = T()
+    t.n_dims, t.type = 2, qt
+    t.dims[0], t.dims[1] = n_embd, n_rows
+    err = C.create_string_buffer(256)
+    for r in (0, 4, n_rows - 1):
+        y = np.zeros(n_embd, np.float32)
+        assert kern.edgexpu_gguf_dequantize_row(_p(table, _u8p), C.byref(t), r, n_embd, _p(y, _f32p), err, 256) == 1
+        assert np.array_equal(bits(y), bits(ora.dequantize(np.ascontiguousarray(table[r]), qt, n_embd))), r
+    if qt == Q8_0:
+        kern.edgexpu_gguf_dequantize_q8_0_rows.restype = C.c_int
+        kern.edgexpu_gguf_dequantize_q8_0_rows.argtypes = [_u8p, C.c_uint64, C.c_int, _f32p]
+        y = np.zeros(n_embd, np.float32)
+        assert kern.edgexpu_gguf_dequantize_q8_0_rows(_p(table, _u8p), 7, n_embd, _p(y, _f32p)) == 1
+        assert np.array_equal(bits(y), bits(ora.dequantize(np.ascontiguousarray(table[7]), qt, n_embd)))
+        kern.edgexpu_gguf_q8_0_dot_row.restype = C.c_float
+        kern.edgexpu_gguf_q8_0_dot_row.argtypes = [_u8p, C.c_uint64, C.c_int, _f32p]
+        x = np.ascontiguousarray(synth.np_activations(1, n_embd, rng)[0])
+        got = kern.edgexpu_gguf_q8_0_dot_row(_p(table, _u8p), 3, n_embd, _p(x, _f32p))
+        want = ora.dot_f32(qt, np.ascontiguousarray(table[3]), x, n_embd)
+        assert abs(got - want) <= TOL * npref.f32_dot_f64(qt, table[3], x)[1]
+
+
+def test_dropin_selftest(kern):
+    """edgexpu_gguf_quant_selftest: the reference's known answers through the GPU."""
+    kern.edgexpu_gguf_quant_selftest.restype = C.c_int
+    kern.edgexpu_gguf_quant_selftest.argtypes = [C.c_char_p, C.c_size_t]
+    err = C.create_string_buffer(256)
+    assert kern.edgexpu_gguf_quant_selftest(err, 256) == 1, err.value
