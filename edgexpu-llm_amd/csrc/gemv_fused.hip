@@ -72,6 +72,15 @@ hipError_t launch_gemv_fused_f32(int type, const uint8_t *w, int n_out, const fl
 #define EXQ_F32_LAUNCH(F)                                                                              \
     return balanced ? (r1 == 1 ? launch_fused_fmt<F, 1, 1, 8, false, 2>(a, st) : launch_fused_fmt<F, 1, 2, 8, false, 2>(a, st)) \
                     : (r1 == 1 ? launch_fused_fmt<F, 1, 1, 8, false, 0>(a, st) : launch_fused_fmt<F, 1, 2, 8, false, 0>(a, st))
+    // K-quant rows of 33-48 units (K = 2112..3072): 16-lane slots over three
+    // waves use 83 % of the lanes where one 64-lane slot uses 62.5 %
+    static const int f32_ks3 = env_int("EXQ_FUSED_F32_KS3", 1);
+    if (f32_ks3 != 0 && type != kTypeQ8_0 && a.U > 32 && a.U <= 48) {
+        a.G = 16;
+        a.KS = 3;
+        return type == kTypeQ4_K ? launch_fused_fmt<FmtQ4KF32, 1, 2, 12, false, 0>(a, st)
+                                 : launch_fused_fmt<FmtQ6KF32, 1, 2, 12, false, 0>(a, st);
+    }
     switch (type) {
         case kTypeQ8_0: EXQ_F32_LAUNCH(FmtQ80F32);
         case kTypeQ4_K: EXQ_F32_LAUNCH(FmtQ4KF32);
