@@ -263,10 +263,11 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ s
     }
 }
 
-// Pass 2: one wavefront per row t reduces its nparts partials to best[t].
+// Pass 2: one wavefront per row t reduces its nparts partials (at
+// partial + t*stride) to best[t].
 __global__ __launch_bounds__(64) void argmax_finish_kernel(const unsigned long long *__restrict__ partial,
-                                                           int nparts, uint32_t *__restrict__ best) {
-    const unsigned long long *p = partial + (size_t)blockIdx.x * kArgmaxParts;
+                                                           int nparts, int stride, uint32_t *__restrict__ best) {
+    const unsigned long long *p = partial + (size_t)blockIdx.x * stride;
     unsigned long long b = 0ull;
     for (int i = threadIdx.x; i < nparts; i += 64) b = p[i] > b ? p[i] : b;
     for (int off = 32; off > 0; off >>= 1) {
@@ -286,6 +287,14 @@ hipError_t launch_argmax_rows(const float *s, int m, int n, size_t lds, unsigned
         hipLaunchKernelGGL(argmax_kernel, dim3(grid), dim3(256), 0, st, s + (size_t)t * lds, n,
                            partial + (size_t)t * kArgmaxParts);
     }
-    hipLaunchKernelGGL(argmax_finish_kernel, dim3(m), dim3(64), 0, st, partial, grid, best);
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(m), dim3(64), 0, st, partial, grid, kArgmaxParts, best);
+    return hipGetLastError();
+}
+
+// best[t] from the nparts keys of row t at partial + t*stride (keys written
+// by the logits launch's argmax epilogue).
+hipError_t launch_argmax_finish(const unsigned long long *partial, int m, int nparts, int stride, uint32_t *best,
+                                hipStream_t st) {
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(m), dim3(64), 0, st, partial, nparts, stride, best);
     return hipGetLastError();
 }

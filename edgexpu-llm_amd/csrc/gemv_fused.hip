@@ -46,9 +46,67 @@ bool gemv_fused_f32_supported(int type, int K) {
 // One token of f32 activations xf (with 16-element sums xs for the K-quants)
 // against one matrix: the logits product (src/native.c:445-462).  Rows per
 // slot R = 1 or 2 (the activation slice takes the registers of larger R).
+namespace {
+// The f32 logits launch with the argmax epilogue: the same shapes and
+// schedules as launch_gemv_fused_f32, one key per workgroup of the grid.
+template <class F, int R, int NW, int LOOP>
+hipError_t launch_argmax_fmt(FusedArgs a, hipStream_t st, int *nparts) {
+    const hipError_t e = launch_fused_fmt<F, 1, R, NW, false, LOOP, 16>(a, st);
+    *nparts = fused_last_grid();
+    return e;
+}
+}  // namespace
+
+hipError_t launch_gemv_fused_f32_argmax(int type, const uint8_t *w, int n_out, const float *bias, float *out,
+                                        size_t row_bytes, int K, const float *xf, const float *xs, hipStream_t st,
+                                        unsigned long long *amax, int *nparts) {
+    FusedArgs a{};
+    a.amax_cap = kFusedArgmaxParts;
+    a.nmat = 1;
+    a.w[0] = w;
+    a.n_out[0] = n_out;
+    a.bias[0] = bias;
+    a.out[0] = out;
+    a.row_bytes = row_bytes;
+    a.K = K;
+    a.m = 1;
+    a.xf = xf;
+    a.xs = xs;
+    a.amax = amax;
+    a.nblk = type == kTypeQ8_0 ? K / kQK8_0 : K / kQKK;
+    a.U = type == kTypeQ8_0 ? a.nblk : a.nblk * 4;
+    if (!pick_fused_shape(a.U, a.G, a.KS)) return hipErrorInvalidValue;
+    static const int f32_ks3 = env_int("EXQ_FUSED_F32_KS3", 1);
+    if (f32_ks3 != 0 && type != kTypeQ8_0 && a.U > 32 && a.U <= 48) {
+        a.G = 16;
+        a.KS = 3;
+        return type == kTypeQ4_K ? launch_argmax_fmt<FmtQ4KF32, 2, 12, 0>(a, st, nparts)
+                                 : launch_argmax_fmt<FmtQ6KF32, 2, 12, 0>(a, st, nparts);
+    }
+    const int rows_per_tile = (64 / a.G) * 2;
+    const int tiles = (n_out + rows_per_tile - 1) / rows_per_tile;
+    const bool balanced = a.KS == 1 && tiles > 2 * device_cus() * 8 && env_int("EXQ_FUSED_DYN", 1) != 0;
+    switch (type) {
+        case kTypeQ8_0:
+            return balanced ? launch_argmax_fmt<FmtQ80F32, 2, 8, 2>(a, st, nparts)
+                            : launch_argmax_fmt<FmtQ80F32, 2, 8, 0>(a, st, nparts);
+        case kTypeQ4_K:
+            return balanced ? launch_argmax_fmt<FmtQ4KF32, 2, 8, 2>(a, st, nparts)
+                            : launch_argmax_fmt<FmtQ4KF32, 2, 8, 0>(a, st, nparts);
+        default:
+            return balanced ? launch_argmax_fmt<FmtQ6KF32, 2, 8, 2>(a, st, nparts)
+                            : launch_argmax_fmt<FmtQ6KF32, 2, 8, 0>(a, st, nparts);
+    }
+}
+
+// With amax non-null (at least kFusedArgmaxParts keys) the launch also
+// writes one greedy-argmax key per workgroup there and *nparts the count.
 hipError_t launch_gemv_fused_f32(int type, const uint8_t *w, int n_out, const float *bias, float *out,
-                                 size_t row_bytes, int K, const float *xf, const float *xs, hipStream_t st) {
+                                 size_t row_bytes, int K, const float *xf, const float *xs, hipStream_t st,
+                                 unsigned long long *amax, int *nparts) {
     if (!gemv_fused_f32_supported(type, K)) return hipErrorInvalidValue;
+    if (amax != nullptr) return launch_gemv_fused_f32_argmax(type, w, n_out, bias, out, row_bytes, K, xf, xs, st, amax,
+                                                             nparts);
     FusedArgs a{};
     a.nmat = 1;
     a.w[0] = w;

@@ -27,6 +27,9 @@ namespace exq {
 
 constexpr int kFusedMaxMats = 4;
 
+// Greedy-argmax keys one f32 logits launch writes at most (one per workgroup).
+constexpr int kFusedArgmaxParts = 4096;
+
 struct FusedArgs {
     int nmat;
     const uint8_t *w[kFusedMaxMats];
@@ -51,7 +54,19 @@ struct FusedArgs {
     const float *x2;       // SiLU-mul prologue: the staged activation is silu(x) * x2
     const float *nw;       // RMSNorm prologue: the staged activation is rmsnorm(x; nw, eps)
     float eps;
+    unsigned long long *amax;  // argmax epilogue: one key per workgroup, at blockIdx.x
+    int amax_cap;              //     keys amax holds (the grid is clamped to it)
 };
+
+// Greedy-argmax key of a score (src/native.c:2355-2396): order-preserving
+// score bits above ~index, so the largest key is the largest score at the
+// lowest index; NaN and -inf give 0 and never win.
+__device__ __forceinline__ unsigned long long score_key(float s, unsigned idx) {
+    if (!(s > -INFINITY)) return 0ull;
+    uint32_t u = __float_as_uint(s);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (unsigned long long)(~idx);
+}
 
 struct WSrc {
     const uint8_t *w;
@@ -355,7 +370,10 @@ constexpr int fused_occupancy_pro(int r, int m, int loop, int pro) {
 
 // PRO bits 0-1: staging prologue (0 none, 1 RMSNorm, 2 SiLU-mul; STAGE
 // kernels); bit 2: residual epilogue (outputs += resid).  Without bit 2 the
-// kernel loads no residual word and holds no register for it.
+// kernel loads no residual word and holds no register for it.  Bit 4:
+// greedy-argmax epilogue (one matrix, one token): every stored score also
+// enters its lane's running best key, and each workgroup writes its best to
+// a.amax at the end.
 template <class Fmt, int M, int R, int NW, bool STAGE, int LOOP, int PRO = 0>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(fused_occupancy_pro<Fmt>(R, M, LOOP, PRO))))
 void gemv_fused_kernel(FusedArgs a) {
@@ -405,6 +423,12 @@ void gemv_fused_kernel(FusedArgs a) {
         o_live = ks == 0 && lane < S * NV;
     }
     const int o_r = o_idx / M, o_t = o_idx - (o_idx / M) * M;
+    constexpr bool kArgmax = (PRO & 16) != 0;
+    static_assert(!kArgmax || (M == 1 && (LOOP == 0 || LOOP == 2)), "the argmax epilogue: one token, grid-stride schedules");
+    // argmax epilogue: each lane's running best key lives in LDS, not in
+    // registers (the logits kernels have none to spare)
+    __shared__ unsigned long long lbest[kArgmax ? NW * 64 : 1];
+    if constexpr (kArgmax) lbest[threadIdx.x] = 0ull;
 
     // Loads of one tile: weights (unconditional: clamped tile, row and unit,
     // so every path issues the same loads), the bias and the residual of
@@ -544,6 +568,11 @@ void gemv_fused_kernel(FusedArgs a) {
         }
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(o), rs,
                                               live ? (o_t * ct.n_out + row) * 4 : kDeadOffset, 0, 0);
+        if constexpr (kArgmax) {
+            const unsigned long long k = live ? score_key(o, (unsigned)row) : 0ull;
+            const unsigned long long b = lbest[threadIdx.x];
+            lbest[threadIdx.x] = k > b ? k : b;
+        }
     };
 
     // 3. grid-stride loop over workgroup tiles (a uniform trip count, so the
@@ -642,6 +671,23 @@ void gemv_fused_kernel(FusedArgs a) {
             finish(vals, iter, have, ct, cbias);
         }
     }
+    if constexpr (kArgmax) {
+        // the workgroup's best key: each wave over its 64 lanes, then the
+        // first wave over the NW wave results; one key per workgroup
+        unsigned long long best_key = lbest[threadIdx.x];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const unsigned long long o = __shfl_xor(best_key, off, 64);
+            best_key = o > best_key ? o : best_key;
+        }
+        __syncthreads();  // every lane has read its own lbest entry
+        if (lane == 0) lbest[wave] = best_key;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int k = 1; k < NW; ++k) best_key = lbest[k] > best_key ? lbest[k] : best_key;
+            a.amax[blockIdx.x] = best_key;
+        }
+    }
 }
 
 // Compute units of the current device (256 if the query fails).
@@ -663,6 +709,12 @@ static int device_cus() {
 static int env_int(const char *name, int dflt) {
     const char *e = getenv(name);
     return e != nullptr ? atoi(e) : dflt;
+}
+
+// Grid of the most recent launch_fused_fmt (the argmax epilogue's key count).
+static int &fused_last_grid() {
+    static int g = 0;
+    return g;
 }
 
 // per_cu_cap > 0: at most that many workgroups per CU in the grid.
@@ -701,7 +753,13 @@ static hipError_t launch_fused_fmt(FusedArgs a, hipStream_t st, int per_cu_cap =
     const int rounds = (wg_tiles + resident - 1) / resident;
     // workgroup-tile schedule: equal tile counts per workgroup; balanced
     // per-wave schedule: every resident slot (equal work per CU)
-    const int grid = LOOP == 2 ? (wg_tiles < resident ? wg_tiles : resident) : (wg_tiles + rounds - 1) / rounds;
+    int grid = LOOP == 2 ? (wg_tiles < resident ? wg_tiles : resident) : (wg_tiles + rounds - 1) / rounds;
+    // argmax epilogue: one key per workgroup must fit a.amax (both schedules
+    // that carry it stride over the tiles by the grid, so any grid is complete)
+    if constexpr ((PRO & 16) != 0) {
+        if (grid > a.amax_cap) grid = a.amax_cap;
+    }
+    fused_last_grid() = grid;
     hipLaunchKernelGGL((gemv_fused_kernel<Fmt, M, R, NW, STAGE, LOOP, PRO>), dim3(grid), dim3(NW * 64), L.total(), st, a);
     return hipGetLastError();
 }

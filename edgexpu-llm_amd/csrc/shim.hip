@@ -44,7 +44,10 @@ hipError_t launch_gemv_fused_layer(int type, int nmat, const uint8_t *const *w, 
                                    size_t row_bytes, int K, int m, const float *x, const float *x2, const float *nw,
                                    float eps, int pro, const uint8_t *xq, size_t xq_stride, hipStream_t st);
 hipError_t launch_gemv_fused_f32(int type, const uint8_t *w, int n_out, const float *bias, float *out,
-                                 size_t row_bytes, int K, const float *xf, const float *xs, hipStream_t st);
+                                 size_t row_bytes, int K, const float *xf, const float *xs, hipStream_t st,
+                                 unsigned long long *amax = nullptr, int *nparts = nullptr);
+hipError_t launch_argmax_finish(const unsigned long long *partial, int m, int nparts, int stride, uint32_t *best,
+                                hipStream_t st);
 hipError_t launch_gemv_fused(int type, int nmat, const uint8_t *const *w, const int *n_out, const float *const *bias,
                              float *const *out, size_t row_bytes, int K, int m, const float *x, const uint8_t *xq,
                              size_t xq_stride, hipStream_t st);
@@ -61,7 +64,7 @@ constexpr int kStageMaxK = 4096;
 // ... except one token's Q8_K activation up to this many elements, which
 // the 16-wave workgroups of the row-split GEMV quantize in one round.
 constexpr int kStageMaxKWide = 16384;
-constexpr int kArgmaxParts = 1024;
+constexpr int kArgmaxParts = 4096;  // per token: the two-pass argmax's 1024, or one key per wave of a logits launch
 
 struct State {
     bool ready = false;
@@ -229,7 +232,7 @@ void *f16ws(size_t bytes) {
 struct ActWs {
     uint8_t *xq;               // m * act_bytes   quantized activations
     float *xs;                 // m * K/16        16-element sums of f32 x (f32 logits path)
-    unsigned long long *keys;  // m * 1024        argmax partials
+    unsigned long long *keys;  // m * 4096        argmax partials
 };
 
 bool act_ws(uint32_t type, int m, int K, ActWs &a) {
@@ -720,8 +723,23 @@ int edgexpu_hip_logits_dev(float *scores, uint32_t *best_dev, const float *hidde
     } else {
         // the other formats use the f32-activation dots (src/native.c:445-462);
         // K-quant rows one hidden vector per fused launch (a row's score then
-        // does not depend on m, as in the reference's per-token loop)
+        // does not depend on m, as in the reference's per-token loop), whose
+        // store also keeps each wave's greedy-argmax key: one small launch
+        // then reduces those keys instead of re-reading the scores
         if (k_family((int)type) && !hip_ok(launch_xsum16(hidden, m, n_embd, a.xs, st), "xsum16")) return 0;
+        static const int fused_argmax = env_int("EXQ_LOGITS_ARGMAX", 1);  // 0: two-pass argmax over the scores
+        if (fused_argmax != 0 && best_dev != nullptr && k_family((int)type) &&
+            gemv_fused_f32_supported((int)type, n_embd)) {
+            int nparts = 0;
+            for (int t = 0; t < m; ++t) {
+                const hipError_t e = launch_gemv_fused_f32(
+                    (int)type, (const uint8_t *)w, vocab, bias, scores + (size_t)t * vocab, rb, n_embd,
+                    hidden + (size_t)t * n_embd, a.xs + (size_t)t * (n_embd / 16), st, a.keys + (size_t)t * kArgmaxParts,
+                    &nparts);
+                if (!hip_ok(e, "logits gemv + argmax")) return 0;
+            }
+            return hip_ok(launch_argmax_finish(a.keys, m, nparts, kArgmaxParts, best_dev, st), "argmax") ? 1 : 0;
+        }
         if (!run_f32_product(type, w, vocab, n_embd, m, hidden, k_family((int)type) ? a.xs : nullptr, bias, scores,
                              vocab, st))
             return 0;

@@ -396,6 +396,29 @@ def test_logits_multi_token(hipdev, ora, qt, n, vocab, m):
     assert np.array_equal(best.cpu().numpy(), np.argmax(got, axis=1))
 
 
+@pytest.mark.parametrize("qt,n,vocab", [(12, 4096, 20000), (14, 2560, 15001), (12, 2560, 3001)])
+def test_logits_fused_argmax(hipdev, qt, n, vocab):
+    """K-quant logits with the argmax in the GEMV's store: the scores equal the
+    scores-only launch bit for bit, the index is the lowest one of the largest
+    score (two rows made equal and largest), and a NaN score never wins."""
+    rng = np.random.default_rng(qt * 31 + vocab)
+    w = synth.np_weights(qt, vocab, n, rng)
+    w[vocab - 7] = w[13]                       # identical rows: equal scores
+    h = rng.normal(0, 1, n).astype(np.float32)
+    bias = np.zeros(vocab, np.float32)
+    bias[[13, vocab - 7]] = 1e4                # ... and the largest
+    s1, best = E.logits(dev(w), qt, dev(h[None, :]), vocab, n, bias=dev(bias))
+    s0, _ = E.logits(dev(w), qt, dev(h[None, :]), vocab, n, bias=dev(bias), want_best=False)
+    got = s1.cpu().numpy()[0]
+    assert np.array_equal(bits(got), bits(s0.cpu().numpy()[0]))
+    assert got[13] == got[vocab - 7]
+    assert int(best.cpu().numpy()[0]) == 13
+    bias[5] = np.nan                           # NaN never wins
+    bias[vocab - 1] = 2e4
+    s2, best2 = E.logits(dev(w), qt, dev(h[None, :]), vocab, n, bias=dev(bias))
+    assert np.isnan(s2.cpu().numpy()[0][5]) and int(best2.cpu().numpy()[0]) == vocab - 1
+
+
 def test_argmax_rules(hipdev):
     # A Q8_0 matrix whose rows are all zero except rows 10 and 4000: equal best
     # scores, so the lowest index must win (src/native.c:2380).
