@@ -147,8 +147,8 @@ def timed(run, n):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the path shards by rows; "
-              "see DESIGN.md for the multi-GPU design)", file=sys.stderr)
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (across GPUs the path would "
+              "split each matrix by rows, with the activation broadcast and the outputs gathered)", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

@@ -1,6 +1,6 @@
 """GPU parity of the HIP kernels against the oracle, through the C-ABI.
 
-Bars (BASELINE numerics contract):
+Bars (the numerics contract of the path):
   * dequant and activation quantizers: bit-exact;
   * integer block sums: exact (checked end to end with inputs whose fp32
     combination is exact, so any integer error shows as a wrong output);
