@@ -1050,6 +1050,138 @@ uint32_t ora_logits(float *scores, const float *hidden, const uint8_t *w, uint32
     return best;
 }
 
+/* ----------------------------------------------------------- sampling */
+
+/* edgexpu_cpu_softmax, src/cpu_kernel.c:328-353: first-wins max by '>',
+ * e = expf(x - max) in float, double sum in index order, p = (float)(e / sum). */
+void ora_softmax(float *io, int n) {
+    float mx;
+    double sum = 0.0;
+    int i;
+    if (io == NULL || n <= 0) {
+        return;
+    }
+    mx = io[0];
+    for (i = 1; i < n; i++) {
+        if (io[i] > mx) {
+            mx = io[i];
+        }
+    }
+    for (i = 0; i < n; i++) {
+        io[i] = expf(io[i] - mx);
+        sum += (double)io[i];
+    }
+    if (sum <= 0.0) {
+        return;
+    }
+    for (i = 0; i < n; i++) {
+        io[i] = (float)((double)io[i] / sum);
+    }
+}
+
+/* xorshift64 step of src/cpu_kernel.c:781-786 (a zero state is seeded first). */
+uint64_t ora_rng_step(uint64_t *rng) {
+    if (*rng == 0) {
+        *rng = 0x00ED6E50ULL;
+    }
+    *rng ^= *rng << 13;
+    *rng ^= *rng >> 7;
+    *rng ^= *rng << 17;
+    return *rng;
+}
+
+typedef struct {
+    float p;
+    uint32_t id;
+} ora_item;
+
+/* probability descending, then id ascending (src/cpu_kernel.c:744-760) */
+static int ora_item_cmp(const void *a, const void *b) {
+    const ora_item *x = (const ora_item *)a;
+    const ora_item *y = (const ora_item *)b;
+    if (y->p > x->p) {
+        return 1;
+    }
+    if (y->p < x->p) {
+        return -1;
+    }
+    return x->id < y->id ? -1 : (x->id > y->id ? 1 : 0);
+}
+
+/* edgexpu_cpu_sample_softmax, src/cpu_kernel.c:762-849: softmax in place,
+ * one xorshift step, u = (rng & 0xFFFFFFF) / 2^28; with 0 < top_p < 1 the
+ * items sorted by (p desc, id asc) are kept until their double sum reaches
+ * top_p, pick = u * (sum of the kept) and the first kept item whose running
+ * sum reaches pick is drawn; otherwise the same walk over all items in index
+ * order.  Returns 1, or 0 for bad arguments. */
+int ora_sample_softmax(float *logits, int n, float top_p, uint64_t *rng, uint32_t *out) {
+    double sum = 0.0;
+    double cursor = 0.0;
+    double pick;
+    int i;
+    if (logits == NULL || rng == NULL || out == NULL || n <= 0) {
+        return 0;
+    }
+    ora_softmax(logits, n);
+    ora_rng_step(rng);
+    if (top_p > 0.0f && top_p < 1.0f) {
+        int kept = n;
+        ora_item *items = (ora_item *)malloc((size_t)n * sizeof(ora_item));
+        if (items == NULL) {
+            return 0;
+        }
+        for (i = 0; i < n; i++) {
+            items[i].p = logits[i];
+            items[i].id = (uint32_t)i;
+        }
+        qsort(items, (size_t)n, sizeof(ora_item), ora_item_cmp);
+        for (i = 0; i < n; i++) {
+            sum += (double)items[i].p;
+            if (sum >= (double)top_p) {
+                kept = i + 1;
+                break;
+            }
+        }
+        sum = 0.0;
+        for (i = 0; i < kept; i++) {
+            sum += (double)items[i].p;
+        }
+        if (sum <= 0.0) {
+            *out = items[0].id;
+            free(items);
+            return 1;
+        }
+        pick = ((double)(*rng & 0xFFFFFFFu) / (double)0x10000000u) * sum;
+        *out = items[kept - 1].id;
+        for (i = 0; i < kept; i++) {
+            cursor += (double)items[i].p;
+            if (cursor >= pick) {
+                *out = items[i].id;
+                break;
+            }
+        }
+        free(items);
+        return 1;
+    }
+    for (i = 0; i < n; i++) {
+        sum += (double)logits[i];
+    }
+    if (sum <= 0.0) {
+        *out = 0;
+        return 1;
+    }
+    pick = ((double)(*rng & 0xFFFFFFFu) / (double)0x10000000u) * sum;
+    *out = (uint32_t)(n - 1);
+    for (i = 0; i < n; i++) {
+        cursor += (double)logits[i];
+        if (cursor >= pick) {
+            *out = (uint32_t)i;
+            break;
+        }
+    }
+    return 1;
+}
+
 /* -------------------------------------------------------- self-test */
 
 /* -------------------------------------------------- layer elementwise ops */

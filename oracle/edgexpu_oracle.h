@@ -101,6 +101,12 @@ void ora_silu(float *out, const float *x, int n);
 void ora_mul(float *out, const float *a, const float *b, int n);
 void ora_add(float *out, const float *a, const float *b, int n);
 
+/* Temperature sampling of src/native.c:2326-2350: softmax in place
+ * (src/cpu_kernel.c:328-353), the xorshift64 step (:781-786) and the
+ * full-distribution or top-p draw (:762-849). */
+void ora_softmax(float *io, int n);
+uint64_t ora_rng_step(uint64_t *rng);
+int ora_sample_softmax(float *logits, int n, float top_p, uint64_t *rng, uint32_t *out);
 /* Self-checks restated from src/gguf_quant.c:934-1061 (Q4_K, Q4_0, F16, Q5_K,
  * Q8_0 and Q5_0 parts).
  * Returns 1 when they pass. */

@@ -66,6 +66,27 @@ def _ew_setup(obj, rms, silu, mul, add):
     obj._add = L(add, None, [_f32p, _f32p, _f32p, C.c_int])
 
 
+def _sample_setup(obj, softmax, sample):
+    obj._softmax = obj.fn(softmax, None, [_f32p, C.c_int])
+    obj._sample = obj.fn(sample, C.c_int, [_f32p, C.c_int, C.c_float, C.POINTER(C.c_uint64), C.POINTER(C.c_uint32)])
+
+    def softmax_(x):
+        io = np.array(x, dtype=np.float32, copy=True)
+        obj._softmax(_p(io, _f32p), io.size)
+        return io
+
+    def sample_softmax(logits, top_p, rng):
+        """(token, probabilities, new rng state)."""
+        io = np.array(logits, dtype=np.float32, copy=True)
+        st = C.c_uint64(rng)
+        out = C.c_uint32(0)
+        assert obj._sample(_p(io, _f32p), io.size, C.c_float(top_p), C.byref(st), C.byref(out)) == 1
+        return int(out.value), io, int(st.value)
+
+    obj.softmax = softmax_
+    obj.sample_softmax = sample_softmax
+
+
 class _Elementwise:
     """rmsnorm / silu / mul / add over float32 vectors (one row at a time)."""
 
@@ -126,6 +147,7 @@ class Oracle(_Lib, _Elementwise):
         self._f2h = L("ora_fp32_to_fp16", C.c_uint16, [C.c_float])
         self._self = L("ora_selftest", C.c_int, [C.c_char_p, C.c_size_t])
         _ew_setup(self, "ora_rmsnorm", "ora_silu", "ora_mul", "ora_add")
+        _sample_setup(self, "ora_softmax", "ora_sample_softmax")
 
     # -- codecs
     def fp16_to_fp32(self, h: int) -> float:
@@ -229,6 +251,7 @@ class Reference(_Lib, _Elementwise):
                       [_f32p, _f32p, _u8p, C.c_uint32, _f32p, C.c_int, C.c_int, C.c_int])
         self._self = L("edgexpu_gguf_quant_selftest", C.c_int, [C.c_char_p, C.c_size_t])
         _ew_setup(self, "edgexpu_cpu_rmsnorm", "edgexpu_cpu_silu", "edgexpu_cpu_mul", "edgexpu_cpu_add")
+        _sample_setup(self, "edgexpu_cpu_softmax", "edgexpu_cpu_sample_softmax")
 
     def dequantize(self, src, qtype, n):
         src = np.ascontiguousarray(src, dtype=np.uint8)

@@ -314,3 +314,37 @@ def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
     mean = np.float32(ss / np.float64(x.size))
     scale = np.float32(1.0) / np.sqrt(np.float32(mean + np.float32(eps)))
     return (x * scale) * np.asarray(w, dtype=np.float32)
+
+
+# ------------------------------------------------------------ sampling
+
+
+def draw(p, top_p, rng_after):
+    """The draw written from its definition with numpy: the uniform u =
+    (state & 0xFFFFFFF) / 2^28; with 0 < top_p < 1 the (p desc, id asc) order
+    and its smallest prefix whose running double sum reaches top_p, else the
+    index order; then the first position whose running sum reaches u * (sum
+    of that prefix)."""
+    u = float(rng_after & 0xFFFFFFF) / float(1 << 28)
+    ids = np.arange(p.size)
+    if 0.0 < np.float32(top_p) < 1.0:
+        order = np.lexsort((ids, -p.astype(np.float64)))
+        c = np.cumsum(p[order].astype(np.float64))
+        hit = np.nonzero(c >= np.float64(np.float32(top_p)))[0]
+        kept = int(hit[0]) + 1 if hit.size else p.size
+        order = order[:kept]
+    else:
+        order = ids
+    c = np.cumsum(p[order].astype(np.float64))
+    if not c[-1] > 0.0:
+        return int(order[0])
+    hit = np.nonzero(c >= u * c[-1])[0]
+    return int(order[hit[0]]) if hit.size else int(order[-1])
+
+
+def xorshift(s):
+    s = s or 0x00ED6E50
+    s ^= (s << 13) & 0xFFFFFFFFFFFFFFFF
+    s ^= s >> 7
+    s ^= (s << 17) & 0xFFFFFFFFFFFFFFFF
+    return s

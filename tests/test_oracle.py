@@ -405,3 +405,48 @@ def test_silu_special_values(ora):
     want = x64 / (1.0 + np.exp(-x64))
     ulp = np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
     assert np.all(np.abs(got - want) <= 2 * ulp)
+
+
+# ------------------------------------------------------------ sampling
+
+
+@pytest.mark.parametrize("n", [1, 2, 7, 1000, 32000])
+@pytest.mark.parametrize("top_p", [1.0, 0.95, 0.5, 0.0, 1e-6])
+def test_sampler_vs_reference_build(ora, ref, n, top_p):
+    rng = np.random.default_rng(n * 7 + int(top_p * 100))
+    for seed in (0, 1, 0x123456789ABCDEF):
+        logits = (rng.standard_normal(n) * rng.choice([0.5, 3.0, 12.0])).astype(np.float32)
+        t_o, p_o, s_o = ora.sample_softmax(logits, top_p, seed)
+        t_r, p_r, s_r = ref.sample_softmax(logits, top_p, seed)
+        assert (t_o, s_o) == (t_r, s_r)
+        assert np.array_equal(bits(p_o), bits(p_r))
+        assert np.array_equal(bits(ora.softmax(logits)), bits(p_r))
+
+
+@pytest.mark.parametrize("n", [1, 3, 100, 5000])
+@pytest.mark.parametrize("top_p", [1.0, 0.9, 0.3])
+def test_sampler_draw_from_definition(ora, n, top_p):
+    """The oracle's draw and generator step against numpy's cumsum / lexsort
+    statement of the same definition, over many generator states."""
+    rng = np.random.default_rng(n + int(top_p * 10))
+    logits = (rng.standard_normal(n) * 4.0).astype(np.float32)
+    # ties: equal probabilities must fall back to the lower id first
+    logits[: n // 3] = logits[0]
+    seed = 0
+    for _ in range(40):
+        tok, p, seed_next = ora.sample_softmax(logits, top_p, seed)
+        assert seed_next == npref.xorshift(seed)
+        assert tok == npref.draw(p, top_p, seed_next)
+        assert abs(float(np.sum(p, dtype=np.float64)) - 1.0) < 1e-5
+        seed = seed_next
+
+
+def test_sampler_reference_known_answers(ora):
+    """src/cpu_kernel.c:951-968: {0, 20, 0, 0} with state 1 draws 1, with
+    top_p 1.0 and then 0.9; and softmax of {0, 0} is {0.5, 0.5}
+    (src/cpu_kernel.c:876-882)."""
+    tok, _, s = ora.sample_softmax(np.array([0, 20, 0, 0], np.float32), 1.0, 1)
+    assert tok == 1
+    tok, _, _ = ora.sample_softmax(np.array([0, 20, 0, 0], np.float32), 0.9, s)
+    assert tok == 1
+    assert np.array_equal(ora.softmax(np.zeros(2, np.float32)), np.float32([0.5, 0.5]))
