@@ -46,6 +46,8 @@ hipError_t launch_gemv_fused_layer(int type, int nmat, const uint8_t *const *w, 
 hipError_t launch_gemv_fused_f32(int type, const uint8_t *w, int n_out, const float *bias, float *out,
                                  size_t row_bytes, int K, const float *xf, const float *xs, hipStream_t st,
                                  unsigned long long *amax = nullptr, int *nparts = nullptr);
+hipError_t launch_sample_softmax(float *x, int n, float top_p, double u, uint32_t *out, void *ws, hipStream_t st);
+size_t sample_workspace_bytes(int n);
 hipError_t launch_argmax_finish(const unsigned long long *partial, int m, int nparts, int stride, uint32_t *best,
                                 hipStream_t st);
 hipError_t launch_gemv_fused(int type, int nmat, const uint8_t *const *w, const int *n_out, const float *const *bias,
@@ -71,6 +73,8 @@ struct State {
     int device = 0;
     hipStream_t stream = nullptr;
     void *ws = nullptr;  // device workspace (quantized activations, sums, argmax partials)
+    void *sws = nullptr;  // sampling workspace (segment sums, sort keys)
+    size_t sws_cap = 0;
     size_t ws_cap = 0;
     void *dbuf = nullptr;  // device staging for host-pointer calls
     void *f16ws = nullptr;  // fp16 prefill GEMM workspace
@@ -212,6 +216,20 @@ void *layer_ws(size_t bytes) {
     if (!hip_ok(hipMalloc(&g.lws, cap), "hipMalloc layer workspace")) return nullptr;
     g.lws_cap = cap;
     return g.lws;
+}
+
+void *sample_ws(size_t bytes) {
+    if (bytes <= g.sws_cap) return g.sws;
+    if (g.sws != nullptr) {
+        if (!hip_ok(hipDeviceSynchronize(), "sample workspace sync")) return nullptr;
+        (void)hipFree(g.sws);
+        g.sws = nullptr;
+        g.sws_cap = 0;
+    }
+    size_t cap = align_up(bytes, (size_t)1 << 20);
+    if (!hip_ok(hipMalloc(&g.sws, cap), "hipMalloc sample workspace")) return nullptr;
+    g.sws_cap = cap;
+    return g.sws;
 }
 
 void *f16ws(size_t bytes) {
@@ -399,6 +417,7 @@ void edgexpu_hip_shutdown(void) {
     if (g.ws) (void)hipFree(g.ws);
     if (g.dbuf) (void)hipFree(g.dbuf);
     if (g.f16ws) (void)hipFree(g.f16ws);
+    if (g.sws) (void)hipFree(g.sws);
     if (g.lws) (void)hipFree(g.lws);
     (void)hipStreamDestroy(g.stream);
     const int err = g.err;
@@ -802,6 +821,39 @@ int edgexpu_hip_embed_rows_dev(float *out, const void *table, uint32_t type, lon
                : 0;
 }
 
+// The reference's generator step (src/cpu_kernel.c:781-786) and its uniform
+// (src/cpu_kernel.c:820,834): (state & 0xFFFFFFF) / 2^28.
+static double sample_uniform(uint64_t *rng) {
+    if (*rng == 0) *rng = 0x00ED6E50ULL;
+    *rng ^= *rng << 13;
+    *rng ^= *rng >> 7;
+    *rng ^= *rng << 17;
+    return (double)(*rng & 0xFFFFFFFu) / (double)0x10000000u;
+}
+
+int edgexpu_hip_sample_softmax_dev(float *logits, int n, float top_p, uint64_t *rng, uint32_t *out, void *stream) {
+    if (!ensure_init()) return 0;
+    if (logits == nullptr || rng == nullptr || out == nullptr || n <= 0 || n > (1 << 24)) {
+        set_error(-2, "sample_softmax: null argument or n=%d outside 1..2^24", n);
+        return 0;
+    }
+    void *ws = sample_ws(sample_workspace_bytes(n));
+    if (ws == nullptr) return 0;
+    const double u = sample_uniform(rng);
+    return hip_ok(launch_sample_softmax(logits, n, top_p, u, out, ws, pick_stream(stream)), "sample_softmax") ? 1 : 0;
+}
+
+int edgexpu_hip_softmax_dev(float *io, int n, void *stream) {
+    if (!ensure_init()) return 0;
+    if (io == nullptr || n <= 0 || n > (1 << 24)) {
+        set_error(-2, "softmax: null argument or n=%d outside 1..2^24", n);
+        return 0;
+    }
+    void *ws = sample_ws(sample_workspace_bytes(n));
+    if (ws == nullptr) return 0;
+    return hip_ok(launch_sample_softmax(io, n, 1.0f, 0.0, nullptr, ws, pick_stream(stream)), "softmax") ? 1 : 0;
+}
+
 static int quantize_dev(const float *x, int m, int n, uint8_t *dst, void *stream, bool k_quant) {
     if (!ensure_init()) return 0;
     const int qk = k_quant ? kQKK : kQK8_0;
@@ -955,6 +1007,40 @@ static int quantize_host(const float *x, int n, uint8_t *dst, bool k_quant) {
     if (!hip_ok(hipMemcpyAsync(d, x, (size_t)n * sizeof(float), hipMemcpyHostToDevice, g.stream), "H2D x")) return 0;
     if (!quantize_dev((const float *)d, 1, n, d + xo, g.stream, k_quant)) return 0;
     if (!hip_ok(hipMemcpyAsync(dst, d + xo, qb, hipMemcpyDeviceToHost, g.stream), "D2H q")) return 0;
+    return hip_ok(hipStreamSynchronize(g.stream), "sync") ? 1 : 0;
+}
+
+int edgexpu_hip_sample_softmax(float *logits, int n, float top_p, uint64_t *rng, uint32_t *out) {
+    if (!ensure_init()) return 0;
+    if (logits == nullptr || rng == nullptr || out == nullptr || n <= 0 || n > (1 << 24)) {
+        set_error(-2, "sample_softmax: null argument or n=%d outside 1..2^24", n);
+        return 0;
+    }
+    const size_t xb = align_up((size_t)n * sizeof(float), 256);
+    uint8_t *d = (uint8_t *)devbuf(xb + 256);
+    if (d == nullptr) return 0;
+    uint32_t *dout = (uint32_t *)(d + xb);
+    if (!hip_ok(hipMemcpyAsync(d, logits, (size_t)n * sizeof(float), hipMemcpyHostToDevice, g.stream), "H2D logits"))
+        return 0;
+    if (!edgexpu_hip_sample_softmax_dev((float *)d, n, top_p, rng, dout, g.stream)) return 0;
+    if (!hip_ok(hipMemcpyAsync(logits, d, (size_t)n * sizeof(float), hipMemcpyDeviceToHost, g.stream), "D2H p") ||
+        !hip_ok(hipMemcpyAsync(out, dout, sizeof(uint32_t), hipMemcpyDeviceToHost, g.stream), "D2H token"))
+        return 0;
+    return hip_ok(hipStreamSynchronize(g.stream), "sync") ? 1 : 0;
+}
+
+int edgexpu_hip_softmax(float *io, int n) {
+    if (!ensure_init()) return 0;
+    if (io == nullptr || n <= 0 || n > (1 << 24)) {
+        set_error(-2, "softmax: null argument or n=%d outside 1..2^24", n);
+        return 0;
+    }
+    float *d = (float *)devbuf(align_up((size_t)n * sizeof(float), 256));
+    if (d == nullptr) return 0;
+    if (!hip_ok(hipMemcpyAsync(d, io, (size_t)n * sizeof(float), hipMemcpyHostToDevice, g.stream), "H2D x") ||
+        !edgexpu_hip_softmax_dev(d, n, g.stream) ||
+        !hip_ok(hipMemcpyAsync(io, d, (size_t)n * sizeof(float), hipMemcpyDeviceToHost, g.stream), "D2H p"))
+        return 0;
     return hip_ok(hipStreamSynchronize(g.stream), "sync") ? 1 : 0;
 }
 

@@ -82,6 +82,12 @@ class HipLib:
         self.dequant_dev = _sig(L, "edgexpu_hip_dequantize_dev", C.c_int, [_vp, C.c_uint32, C.c_uint64, _vp, _vp])
         self.embed_rows_dev = _sig(L, "edgexpu_hip_embed_rows_dev", C.c_int,
                                    [_vp, _vp, C.c_uint32, C.c_longlong, C.c_int, _vp, C.c_int, _vp, _vp])
+        self.sample_dev = _sig(L, "edgexpu_hip_sample_softmax_dev", C.c_int,
+                               [_vp, C.c_int, C.c_float, C.POINTER(C.c_uint64), _vp, _vp])
+        self.softmax_dev = _sig(L, "edgexpu_hip_softmax_dev", C.c_int, [_vp, C.c_int, _vp])
+        self.sample_host = _sig(L, "edgexpu_hip_sample_softmax", C.c_int,
+                                [_vp, C.c_int, C.c_float, C.POINTER(C.c_uint64), C.POINTER(C.c_uint32)])
+        self.softmax_host = _sig(L, "edgexpu_hip_softmax", C.c_int, [_vp, C.c_int])
         self.q80_dev = _sig(L, "edgexpu_hip_quantize_q8_0_dev", C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp])
         self.q8k_dev = _sig(L, "edgexpu_hip_quantize_q8_k_dev", C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp])
         self.linear_host_w = _sig(L, "edgexpu_hip_linear_quant_batch", C.c_int, [_vp, _vp, _vp, C.c_int])
@@ -227,6 +233,31 @@ def embed_rows(table, qtype: int, n_rows: int, n_embd: int, ids, bad=None, out=N
     L.check(L.embed_rows_dev(_ptr(out), _ptr(table), qtype, n_rows, n_embd, _ptr(ids), n, _ptr(bad), _stream()),
             "embed_rows")
     return out
+
+
+def sample_softmax(logits, top_p: float, rng: int, out=None):
+    """Softmax of the f32 device tensor `logits` in place, then one draw
+    (edgexpu_hip_sample_softmax_dev; the reference's edgexpu_cpu_sample_softmax,
+    src/cpu_kernel.c:762-849).  Returns (token tensor [1] int32 on the device,
+    the advanced rng state)."""
+    import ctypes as C
+
+    import torch
+
+    if out is None:
+        out = torch.empty(1, dtype=torch.int32, device=logits.device)
+    state = C.c_uint64(rng)
+    L = hip()
+    L.check(L.sample_dev(_ptr(logits), logits.numel(), top_p, C.byref(state), _ptr(out), _stream()), "sample_softmax")
+    return out, state.value
+
+
+def softmax(io):
+    """Softmax of the f32 device tensor `io` in place (edgexpu_hip_softmax_dev;
+    the reference's edgexpu_cpu_softmax, src/cpu_kernel.c:328-353)."""
+    L = hip()
+    L.check(L.softmax_dev(_ptr(io), io.numel(), _stream()), "softmax")
+    return io
 
 
 def quantize_q8_0(x):

@@ -311,6 +311,22 @@ float edgexpu_gguf_dot_quant_q8k(uint32_t type, const uint8_t *wrow, const uint8
     return out;
 }
 
+/* ---------------------------------------------------------- sampling */
+
+void edgexpu_cpu_softmax(float *io, int n) {
+    if (io == NULL || n <= 0) {
+        return; /* src/cpu_kernel.c:333-335 */
+    }
+    (void)edgexpu_hip_softmax(io, n);
+}
+
+int edgexpu_cpu_sample_softmax(float *logits, int n, float top_p, uint64_t *rng, uint32_t *out) {
+    if (logits == NULL || rng == NULL || out == NULL || n <= 0) {
+        return 0; /* src/cpu_kernel.c:776-778 */
+    }
+    return edgexpu_hip_sample_softmax(logits, n, top_p, rng, out);
+}
+
 /* ------------------------------------------------------------ linear */
 
 void edgexpu_cpu_linear_quant_batch(float *out, const float *x, const uint8_t *weight, uint32_t type,

@@ -156,6 +156,23 @@ int edgexpu_hip_dequantize_dev(const void *src, uint32_t type, uint64_t n_elemen
 int edgexpu_hip_embed_rows_dev(float *out, const void *table, uint32_t type, long long n_rows, int n_embd,
                                const int32_t *ids, int n_ids, int *bad, void *stream);
 
+/* Sampling on device (edgexpu_cpu_sample_softmax,
+ * include/edgexpu/cpu_kernel.h:86-94, src/cpu_kernel.c:762-849, the
+ * temperature path of src/native.c:2326-2350): softmax of logits[0..n) in
+ * place (edgexpu_cpu_softmax, cpu_kernel.h:24, src/cpu_kernel.c:328-353),
+ * then one draw into *out (a device uint32): from the whole distribution in
+ * index order, or with 0 < top_p < 1 from the smallest prefix, in (p desc,
+ * id asc) order, whose sum reaches top_p.  *rng is a host word advanced by the
+ * reference's xorshift step (a zero state is seeded with 0x00ED6E50); the
+ * uniform is (state & 0xFFFFFFF) / 2^28 as in the reference.  Probabilities
+ * agree with the reference within a few float ulp (device expf; sums in
+ * double in a fixed segment order); the token differs only where the pick
+ * falls within that distance of a running sum.  logits 16-byte aligned,
+ * 1 <= n <= 2^24. */
+int edgexpu_hip_sample_softmax_dev(float *logits, int n, float top_p, uint64_t *rng, uint32_t *out, void *stream);
+/* Softmax of io[0..n) in place on device (edgexpu_cpu_softmax). */
+int edgexpu_hip_softmax_dev(float *io, int n, void *stream);
+
 /* Activation quantizers writing the reference's block bytes
  * (edgexpu_gguf_quantize_q8_0 / _q8_k, include/edgexpu/gguf_quant.h:80-87,
  * src/gguf_dot_q8.c:269-412): m rows of n f32 -> m*(n/32)*34 or
@@ -241,6 +258,11 @@ int edgexpu_hip_linear_quant_batch_host(float *out, const float *x, const uint8_
  * host [vocab] (may be NULL), *best receives the greedy argmax. */
 int edgexpu_hip_logits(float *scores, uint32_t *best, const float *hidden, const edgexpu_hip_weight *w,
                        int chunk_rows);
+
+/* Host-buffer sampling and softmax: logits / io host f32 (overwritten with
+ * the probabilities), *out a host word. */
+int edgexpu_hip_sample_softmax(float *logits, int n, float top_p, uint64_t *rng, uint32_t *out);
+int edgexpu_hip_softmax(float *io, int n);
 
 /* Host-buffer dequantization: src host bytes, dst host f32. */
 int edgexpu_hip_dequantize(const uint8_t *src, uint32_t type, uint64_t n_elements, float *dst);

@@ -118,6 +118,14 @@ void edgexpu_cpu_linear_quant(float *out, const float *x, const uint8_t *weight,
 void edgexpu_cpu_linear_quant_batch(float *out, const float *x, const uint8_t *weight, uint32_t type,
                                     const float *bias, int m, int n_out, int n_in);
 
+/* include/edgexpu/cpu_kernel.h:24 (src/cpu_kernel.c:328-353): softmax in
+ * place; and include/edgexpu/cpu_kernel.h:86-94 (src/cpu_kernel.c:762-849):
+ * softmax in place, then one draw (top_p in (0,1): nucleus) with the
+ * reference's xorshift state *rng.  Returns 0 on bad arguments, 1 otherwise.
+ * Computed on the GPU. */
+void edgexpu_cpu_softmax(float *io, int n);
+int edgexpu_cpu_sample_softmax(float *logits, int n, float top_p, uint64_t *rng, uint32_t *out);
+
 /* ---- device residency for host-pointer callers (no reference counterpart:
  * replaces the per-token staging copies of src/native.c:350-380) ---- */
 
