@@ -70,6 +70,8 @@ def parse():
                    help="time a plain streaming read of each decode launch's weight bytes (one JSON line)")
     p.add_argument("--formats", action="store_true",
                    help="decode GEMV [14336 x 4096] m=1 and 1 GiB dequant for every GPU format (one JSON line)")
+    p.add_argument("--sample", action="store_true",
+                   help="softmax + temperature / top-p draw over a 128256-entry vocabulary on device (one JSON line)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="first copy a 256 MiB buffer 4 times (device to device) for counter calibration")
     return p.parse_args()
@@ -177,6 +179,9 @@ def main():
         return
     if args.formats:
         print(json.dumps(formats_leg(L, E, synth, gen, dev, no_cpu=args.no_cpu)), flush=True)
+        return
+    if args.sample:
+        print(json.dumps(sample_leg(L, gen, dev, no_cpu=args.no_cpu)), flush=True)
         return
     if args.prefill_only:
         # the prefill GEMM leg alone (for counter runs): one JSON line
@@ -659,6 +664,48 @@ def formats_leg(L, E, synth, gen, dev, no_cpu=False):
     deq = dequant_leg(L, E, synth, gen, dev, no_cpu=no_cpu, types=((2, "q4_0"), (6, "q5_0"), (13, "q5_k"), (1, "f16")))
     return {"metric": "decode GEMV and bulk dequant per GGUF format, 1 GPU", "gemv_shape": [N, K], "m": 1,
             "gemv": gemv, "dequant_1GiB": deq}
+
+
+def sample_leg(L, gen, dev, no_cpu=False, vocab=128256, reps=50):
+    """Softmax of a [vocab] f32 score vector in place and one draw
+    (edgexpu_hip_sample_softmax_dev), eager launches on one stream (the
+    generator's uniform is a kernel argument, so a draw is not replayed from
+    a graph); top_p 1.0 (index-order draw) and 0.9 (bitonic sort of the
+    vocabulary).  Later calls run on the previous call's probabilities: the
+    same launches and bytes.  Beside it, unless no_cpu, the reference's
+    edgexpu_cpu_sample_softmax on one host core over the same scores."""
+    import torch
+
+    base = torch.randn(vocab, generator=gen, device=dev) * 3.0
+    x = torch.empty_like(base)
+    out = torch.empty(1, dtype=torch.int32, device=dev)
+    st = C.c_uint64(1)
+    sp = torch.cuda.current_stream().cuda_stream
+    res = {}
+    for top_p in (1.0, 0.9):
+        x.copy_(base)
+
+        def run(top_p=top_p):
+            if not L.sample_dev(x.data_ptr(), vocab, top_p, C.byref(st), out.data_ptr(), sp):
+                L.check(0, "sample_softmax")
+
+        run()
+        us = timed(run, reps) * 1e3
+        res[f"top_p_{top_p}"] = {"us": round(us, 2)}
+    if not no_cpu:
+        import oracle as O
+
+        ref, kind = O.load_reference(), "reference"
+        if ref is None:
+            ref, kind = O.load_oracle(), "port"
+        scores = base.cpu().numpy()
+        for top_p in (1.0, 0.9):
+            t0 = time.perf_counter()
+            for _ in range(5):
+                ref.sample_softmax(scores, top_p, 1)
+            res[f"top_p_{top_p}"]["cpu_us"] = round((time.perf_counter() - t0) / 5 * 1e6, 1)
+        res["cpu_kind"] = kind
+    return {"metric": "softmax + draw per decode step, 1 GPU", "vocab": vocab, "unit": "us", "sample": res}
 
 
 def dequant_leg(L, E, synth, gen, dev, no_cpu=False, types=((8, "q8_0"), (12, "q4_k"), (14, "q6_k"))):

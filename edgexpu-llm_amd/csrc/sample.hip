@@ -20,6 +20,7 @@
 // sort last).
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <cmath>
 #include <cstdint>
 
@@ -67,15 +68,21 @@ __global__ __launch_bounds__(kSampleThreads) void seg_max_kernel(const float *__
 __global__ __launch_bounds__(kSampleThreads) void seg_exp_kernel(float *__restrict__ x, int n, int S, int B,
                                                                  const float *__restrict__ pmax,
                                                                  double *__restrict__ psum) {
-    __shared__ float mx_s;
+    __shared__ float mred[4];
     __shared__ double red[4];
-    if (threadIdx.x == 0) {
-        float m = pmax[0];
-        for (int k = 1; k < B; ++k) m = pmax[k] > m ? pmax[k] : m;
-        mx_s = m;
+    // max over segments 1..B-1 (none of them NaN), then segment 0's value
+    // first, as the reference's scan from x[0]: a NaN there stays
+    float m = -INFINITY;
+    for (int k = 1 + threadIdx.x; k < B; k += kSampleThreads) m = pmax[k] > m ? pmax[k] : m;
+    for (int off = 32; off > 0; off >>= 1) {
+        const float o = __shfl_xor(m, off, 64);
+        m = o > m ? o : m;
     }
+    if ((threadIdx.x & 63) == 0) mred[threadIdx.x >> 6] = m;
     __syncthreads();
-    const float mx = mx_s;
+    float mx = pmax[0];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) mx = mred[k] > mx ? mred[k] : mx;
     const int b = blockIdx.x, lo = b * S, hi = min(n, lo + S);
     double s = 0.0;
     for (int i = lo + threadIdx.x; i < hi; i += kSampleThreads) {
@@ -93,15 +100,10 @@ __global__ __launch_bounds__(kSampleThreads) void seg_exp_kernel(float *__restri
 __global__ __launch_bounds__(kSampleThreads) void seg_norm_kernel(float *__restrict__ x, int n, int S, int B,
                                                                   const double *__restrict__ esum,
                                                                   double *__restrict__ psum) {
-    __shared__ double tot_s;
     __shared__ double red[4];
-    if (threadIdx.x == 0) {
-        double t = 0.0;
-        for (int k = 0; k < B; ++k) t += esum[k];
-        tot_s = t;
-    }
-    __syncthreads();
-    const double tot = tot_s;
+    double t = 0.0;
+    for (int k = threadIdx.x; k < B; k += kSampleThreads) t += esum[k];
+    const double tot = block_sum_f64(t, red);
     const int b = blockIdx.x, lo = b * S, hi = min(n, lo + S);
     double s = 0.0;
     for (int i = lo + threadIdx.x; i < hi; i += kSampleThreads) {
@@ -116,36 +118,109 @@ __global__ __launch_bounds__(kSampleThreads) void seg_norm_kernel(float *__restr
     if (threadIdx.x == 0) psum[b] = s;
 }
 
+constexpr int kDrawThreads = 1024;
+
+// Inclusive prefix sums of v over the block (a fixed order: each wave's
+// shuffle scan, then the 16 wave totals scanned by wave 0); *total is the
+// block's sum, the same addition as the last prefix.
+__device__ double block_scan_f64(double v, double *wtot, double *total) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const double o = __shfl_up(v, off, 64);
+        if (lane >= off) v += o;
+    }
+    if (lane == 63) wtot[w] = v;
+    __syncthreads();
+    if (w == 0) {
+        double t = lane < kDrawThreads / 64 ? wtot[lane] : 0.0;
+#pragma unroll
+        for (int off = 1; off < kDrawThreads / 64; off <<= 1) {
+            const double o = __shfl_up(t, off, 64);
+            if (lane >= off) t += o;
+        }
+        if (lane < kDrawThreads / 64) wtot[lane] = t;
+    }
+    __syncthreads();
+    if (w > 0) v += wtot[w - 1];
+    *total = wtot[kDrawThreads / 64 - 1];
+    __syncthreads();
+    return v;
+}
+
+// The smallest idx over the threads whose flag is set (INT_MAX: none).
+__device__ int block_first(bool flag, int idx, int *slot) {
+    if (threadIdx.x == 0) *slot = INT_MAX;
+    __syncthreads();
+    if (flag) atomicMin(slot, idx);
+    __syncthreads();
+    const int r = *slot;
+    __syncthreads();
+    return r;
+}
+
+// The value of thread `src`'s v on every thread.
+__device__ double block_bcast(double v, int src, double *sh) {
+    if (threadIdx.x == src) *sh = v;
+    __syncthreads();
+    const double r = *sh;
+    __syncthreads();
+    return r;
+}
+
+struct Sh {
+    double wtot[kDrawThreads / 64];
+    double b;
+    int slot;
+};
+
+// The first position i in [start, lim) whose running sum carry + v[start..i]
+// reaches target (-1: none), in chunks of kDrawThreads entries; *run is the
+// running sum at i (at lim - 1 when none).
+template <class V>
+__device__ int block_walk(V val, int start, int lim, double target, double carry, double *run, Sh &sh) {
+    for (int c = start; c < lim; c += kDrawThreads) {
+        const int i = c + threadIdx.x;
+        const double v = i < lim ? val(i) : 0.0;
+        double tot;
+        const double pre = carry + block_scan_f64(v, sh.wtot, &tot);
+        const int hit = block_first(i < lim && pre >= target, i, &sh.slot);
+        if (hit != INT_MAX) {
+            *run = block_bcast(pre, hit - c, &sh.b);
+            return hit;
+        }
+        carry += tot;
+    }
+    *run = carry;
+    return -1;
+}
+
 // One draw over entries in index order: pick = u * total, the first index
 // whose running sum reaches pick (n - 1 if rounding leaves none; 0 when the
-// total is not positive).  One thread; the running sum is the segments'
-// sums in order, then the crossing segment's entries one by one.
-__global__ void draw_kernel(const float *__restrict__ p, int n, int S, int B, const double *__restrict__ psum,
-                            double u, uint32_t *__restrict__ out) {
-    if (threadIdx.x != 0) return;
-    double tot = 0.0;
-    for (int k = 0; k < B; ++k) tot += psum[k];
+// total is not positive).  The running sums: the segments' sums scanned,
+// then the crossing segment's entries scanned on from there.  B <= 1024.
+__global__ __launch_bounds__(kDrawThreads) void draw_kernel(const float *__restrict__ p, int n, int S, int B,
+                                                            const double *__restrict__ psum, double u,
+                                                            uint32_t *__restrict__ out) {
+    __shared__ Sh sh;
+    const int t = threadIdx.x;
+    const double v = t < B ? psum[t] : 0.0;
+    double tot;
+    const double pre = block_scan_f64(v, sh.wtot, &tot);
     if (tot <= 0.0) {
-        *out = 0u;
+        if (t == 0) *out = 0u;
         return;
     }
     const double pick = u * tot;
-    double cur = 0.0;
-    for (int k = 0; k < B; ++k) {
-        if (cur + psum[k] >= pick) {
-            const int lo = k * S, hi = min(n, lo + S);
-            for (int i = lo; i < hi; ++i) {
-                cur += (double)p[i];
-                if (cur >= pick) {
-                    *out = (uint32_t)i;
-                    return;
-                }
-            }
-        } else {
-            cur += psum[k];
-        }
+    const int k = block_first(t < B && pre >= pick, t, &sh.slot);
+    if (k == INT_MAX) {
+        if (t == 0) *out = (uint32_t)(n - 1);
+        return;
     }
-    *out = (uint32_t)(n - 1);
+    const double carry = k > 0 ? block_bcast(pre, k - 1, &sh.b) : 0.0;
+    double run;
+    const int i = block_walk([&](int j) { return (double)p[j]; }, k * S, n, pick, carry, &run, sh);
+    if (t == 0) *out = (uint32_t)(i >= 0 ? i : n - 1);
 }
 
 // keys[i] = ~bits(p_i) << 32 | i for i < n, all ones for the padding.
@@ -171,36 +246,40 @@ __global__ __launch_bounds__(kSampleThreads) void bitonic_kernel(unsigned long l
     }
 }
 
-// Steps of the network inside one workgroup's 2 * kSampleThreads keys (every
-// j < 2 * kSampleThreads, so partners stay in the tile): stage k = k_lo from
-// step j0 down to 1, then the whole stages k_lo*2 .. k_hi.
-__global__ __launch_bounds__(kSampleThreads) void bitonic_tile_kernel(unsigned long long *__restrict__ keys, int j0,
-                                                                      int k_lo, int k_hi) {
-    __shared__ unsigned long long t[2 * kSampleThreads];
-    const int base = blockIdx.x * 2 * kSampleThreads;
-    t[threadIdx.x] = keys[base + threadIdx.x];
-    t[threadIdx.x + kSampleThreads] = keys[base + threadIdx.x + kSampleThreads];
+// Steps of the network inside one workgroup's kTileKeys keys (every
+// j < kTileKeys, so partners stay in the tile): stage k = k_lo from step j0
+// down to 1, then the whole stages k_lo*2 .. k_hi.
+constexpr int kTileThreads = 1024;
+constexpr int kTileKeys = 8192;  // 64 KiB of LDS
+constexpr int kTilePer = kTileKeys / kTileThreads;
+
+__global__ __launch_bounds__(kTileThreads) void bitonic_tile_kernel(unsigned long long *__restrict__ keys, int j0,
+                                                                    int k_lo, int k_hi) {
+    __shared__ unsigned long long t[kTileKeys];
+    const int base = blockIdx.x * kTileKeys;
+#pragma unroll
+    for (int h = 0; h < kTilePer; ++h) t[threadIdx.x + h * kTileThreads] = keys[base + threadIdx.x + h * kTileThreads];
     __syncthreads();
     for (int k = k_lo; k <= k_hi; k <<= 1) {
         for (int j = k == k_lo ? j0 : k >> 1; j > 0; j >>= 1) {
+            // the kTileKeys / 2 pairs (li, li ^ j) with li's bit j clear
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int li = threadIdx.x + h * kSampleThreads;
-                const int ll = li ^ j;
-                if (ll > li) {
-                    const unsigned long long a = t[li], b = t[ll];
-                    const bool up = ((base + li) & k) == 0;
-                    if ((a > b) == up) {
-                        t[li] = b;
-                        t[ll] = a;
-                    }
+            for (int h = 0; h < kTilePer / 2; ++h) {
+                const int q = threadIdx.x + h * kTileThreads;
+                const int li = ((q & ~(j - 1)) << 1) | (q & (j - 1));
+                const int ll = li | j;
+                const unsigned long long a = t[li], b = t[ll];
+                const bool up = ((base + li) & k) == 0;
+                if ((a > b) == up) {
+                    t[li] = b;
+                    t[ll] = a;
                 }
             }
             __syncthreads();
         }
     }
-    keys[base + threadIdx.x] = t[threadIdx.x];
-    keys[base + threadIdx.x + kSampleThreads] = t[threadIdx.x + kSampleThreads];
+#pragma unroll
+    for (int h = 0; h < kTilePer; ++h) keys[base + threadIdx.x + h * kTileThreads] = t[threadIdx.x + h * kTileThreads];
 }
 
 __device__ __forceinline__ float key_p(unsigned long long k) { return __uint_as_float(~(uint32_t)(k >> 32)); }
@@ -219,66 +298,42 @@ __global__ __launch_bounds__(kSampleThreads) void seg_sorted_sum_kernel(const un
 // Top-p draw over the sorted keys: kept = 1 + the first position whose
 // running sum reaches top_p (n when none does); pick = u * (running sum at
 // kept); the first kept position whose running sum reaches pick
-// (src/cpu_kernel.c:788-832).  One thread.
-__global__ void draw_topp_kernel(const unsigned long long *__restrict__ keys, int n, int S, int B,
-                                 const double *__restrict__ psum, double top_p, double u, uint32_t *__restrict__ out) {
-    if (threadIdx.x != 0) return;
-    // running sum up to and including position i, walking segment by segment
+// (src/cpu_kernel.c:788-832).  Running sums as in draw_kernel.
+__global__ __launch_bounds__(kDrawThreads) void draw_topp_kernel(const unsigned long long *__restrict__ keys, int n,
+                                                                 int S, int B, const double *__restrict__ psum,
+                                                                 double top_p, double u,
+                                                                 uint32_t *__restrict__ out) {
+    __shared__ Sh sh;
+    const int t = threadIdx.x;
+    auto val = [&](int j) { return (double)key_p(keys[j]); };
+    const double v = t < B ? psum[t] : 0.0;
+    double tot;
+    const double pre = block_scan_f64(v, sh.wtot, &tot);
     int kept = n;
-    double at_kept = 0.0;
-    {
-        double cur = 0.0;
-        bool found = false;
-        for (int k = 0; k < B && !found; ++k) {
-            const int lo = k * S, hi = min(n, lo + S);
-            if (cur + psum[k] >= top_p) {
-                for (int i = lo; i < hi; ++i) {
-                    cur += (double)key_p(keys[i]);
-                    if (cur >= top_p) {
-                        kept = i + 1;
-                        found = true;
-                        break;
-                    }
-                }
-            } else {
-                cur += psum[k];
-            }
-        }
-        at_kept = cur;
-        if (!found) {
-            // no prefix reached top_p: every entry is kept, the sum is the total
-            double t = 0.0;
-            for (int k = 0; k < B; ++k) t += psum[k];
-            at_kept = t;
+    double at_kept = tot;
+    const int k = block_first(t < B && pre >= top_p, t, &sh.slot);
+    if (k != INT_MAX) {
+        const double carry = k > 0 ? block_bcast(pre, k - 1, &sh.b) : 0.0;
+        double run;
+        const int i = block_walk(val, k * S, n, top_p, carry, &run, sh);
+        if (i >= 0) {
+            kept = i + 1;
+            at_kept = run;
         }
     }
     if (at_kept <= 0.0) {
-        *out = (uint32_t)(keys[0] & 0xffffffffull);
+        if (t == 0) *out = (uint32_t)(keys[0] & 0xffffffffull);
         return;
     }
     const double pick = u * at_kept;
-    uint32_t res = (uint32_t)(keys[kept - 1] & 0xffffffffull);
-    double cur = 0.0;
-    for (int k = 0; k < B; ++k) {
-        const int lo = k * S, hi = min(kept, lo + S);
-        if (lo >= kept) break;
-        const bool whole = lo + S <= kept;
-        if (whole && cur + psum[k] < pick) {
-            cur += psum[k];
-            continue;
-        }
-        bool hit = false;
-        for (int i = lo; i < hi; ++i) {
-            cur += (double)key_p(keys[i]);
-            if (cur >= pick) {
-                res = (uint32_t)(keys[i] & 0xffffffffull);
-                hit = true;
-                break;
-            }
-        }
-        if (hit) break;
-    }
-    *out = res;
+    // segments wholly below kept by their sums, then entries up to kept
+    const int kfull = kept / S;
+    const int k2 = block_first(t < kfull && pre >= pick, t, &sh.slot);
+    const int start_seg = k2 != INT_MAX ? k2 : kfull;
+    const double carry = start_seg > 0 ? block_bcast(pre, start_seg - 1, &sh.b) : 0.0;
+    double run;
+    const int i = block_walk(val, start_seg * S, kept, pick, carry, &run, sh);
+    if (t == 0) *out = (uint32_t)(keys[i >= 0 ? i : kept - 1] & 0xffffffffull);
 }
 
 }  // namespace exq
@@ -289,7 +344,7 @@ using namespace exq;
 size_t sample_workspace_bytes(int n) {
     int N2 = 1;
     while (N2 < n) N2 <<= 1;
-    if (N2 < 2 * kSampleThreads) N2 = 2 * kSampleThreads;
+    if (N2 < kTileKeys) N2 = kTileKeys;
     const size_t B = 1024;
     return B * sizeof(float) + 2 * B * sizeof(double) + (size_t)N2 * sizeof(unsigned long long) + 256;
 }
@@ -326,25 +381,25 @@ hipError_t launch_sample_softmax(float *x, int n, float top_p, double u, uint32_
     hipLaunchKernelGGL(seg_exp_kernel, dim3(B), dim3(kSampleThreads), 0, st, x, n, S, B, pmax, esum);
     hipLaunchKernelGGL(seg_norm_kernel, dim3(B), dim3(kSampleThreads), 0, st, x, n, S, B, esum, psum);
     if (!(top_p > 0.0f && top_p < 1.0f)) {
-        hipLaunchKernelGGL(draw_kernel, dim3(1), dim3(64), 0, st, x, n, S, B, psum, u, out);
+        hipLaunchKernelGGL(draw_kernel, dim3(1), dim3(kDrawThreads), 0, st, x, n, S, B, psum, u, out);
         return hipGetLastError();
     }
     int N2 = 1;
     while (N2 < n) N2 <<= 1;
-    if (N2 < 2 * kSampleThreads) N2 = 2 * kSampleThreads;
+    if (N2 < kTileKeys) N2 = kTileKeys;
     const unsigned grid = (unsigned)((N2 + kSampleThreads - 1) / kSampleThreads);
     hipLaunchKernelGGL(keys_kernel, dim3(grid), dim3(kSampleThreads), 0, st, x, n, N2, keys);
-    const unsigned tiles = (unsigned)(N2 / (2 * kSampleThreads));
-    // stages 2 .. 2 * kSampleThreads sort each tile on its own: one launch
-    hipLaunchKernelGGL(bitonic_tile_kernel, dim3(tiles), dim3(kSampleThreads), 0, st, keys, 1, 2,
-                       2 * kSampleThreads);
-    for (int k = 4 * kSampleThreads; k <= N2; k <<= 1) {
+    const unsigned tiles = (unsigned)(N2 / kTileKeys);
+    // stages 2 .. kTileKeys sort each tile on its own: one launch
+    hipLaunchKernelGGL(bitonic_tile_kernel, dim3(tiles), dim3(kTileThreads), 0, st, keys, 1, 2, kTileKeys);
+    for (int k = 2 * kTileKeys; k <= N2; k <<= 1) {
         int j = k >> 1;
-        for (; j >= 2 * kSampleThreads; j >>= 1)
+        for (; j >= kTileKeys; j >>= 1)
             hipLaunchKernelGGL(bitonic_kernel, dim3(grid), dim3(kSampleThreads), 0, st, keys, N2, j, k);
-        hipLaunchKernelGGL(bitonic_tile_kernel, dim3(tiles), dim3(kSampleThreads), 0, st, keys, j, k, k);
+        hipLaunchKernelGGL(bitonic_tile_kernel, dim3(tiles), dim3(kTileThreads), 0, st, keys, j, k, k);
     }
     hipLaunchKernelGGL(seg_sorted_sum_kernel, dim3(B), dim3(kSampleThreads), 0, st, keys, n, S, psum);
-    hipLaunchKernelGGL(draw_topp_kernel, dim3(1), dim3(64), 0, st, keys, n, S, B, psum, (double)top_p, u, out);
+    hipLaunchKernelGGL(draw_topp_kernel, dim3(1), dim3(kDrawThreads), 0, st, keys, n, S, B, psum, (double)top_p, u,
+                       out);
     return hipGetLastError();
 }
