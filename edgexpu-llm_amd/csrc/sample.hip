@@ -249,20 +249,24 @@ __global__ __launch_bounds__(kSampleThreads) void bitonic_kernel(unsigned long l
 // Steps of the network inside one workgroup's kTileKeys keys (every
 // j < kTileKeys, so partners stay in the tile): stage k = k_lo from step j0
 // down to 1, then the whole stages k_lo*2 .. k_hi.
+// TK keys per workgroup: 2048 for the first stages (more workgroups), 8192
+// (64 KiB of LDS) for the later ones.
 constexpr int kTileThreads = 1024;
-constexpr int kTileKeys = 8192;  // 64 KiB of LDS
-constexpr int kTilePer = kTileKeys / kTileThreads;
+constexpr int kTileKeys = 8192;
+constexpr int kTileKeysSmall = 2048;
 
+template <int TK>
 __global__ __launch_bounds__(kTileThreads) void bitonic_tile_kernel(unsigned long long *__restrict__ keys, int j0,
                                                                     int k_lo, int k_hi) {
-    __shared__ unsigned long long t[kTileKeys];
-    const int base = blockIdx.x * kTileKeys;
+    constexpr int kTilePer = TK / kTileThreads;
+    __shared__ unsigned long long t[TK];
+    const int base = blockIdx.x * TK;
 #pragma unroll
     for (int h = 0; h < kTilePer; ++h) t[threadIdx.x + h * kTileThreads] = keys[base + threadIdx.x + h * kTileThreads];
     __syncthreads();
     for (int k = k_lo; k <= k_hi; k <<= 1) {
         for (int j = k == k_lo ? j0 : k >> 1; j > 0; j >>= 1) {
-            // the kTileKeys / 2 pairs (li, li ^ j) with li's bit j clear
+            // the TK / 2 pairs (li, li ^ j) with li's bit j clear
 #pragma unroll
             for (int h = 0; h < kTilePer / 2; ++h) {
                 const int q = threadIdx.x + h * kTileThreads;
@@ -390,13 +394,17 @@ hipError_t launch_sample_softmax(float *x, int n, float top_p, double u, uint32_
     const unsigned grid = (unsigned)((N2 + kSampleThreads - 1) / kSampleThreads);
     hipLaunchKernelGGL(keys_kernel, dim3(grid), dim3(kSampleThreads), 0, st, x, n, N2, keys);
     const unsigned tiles = (unsigned)(N2 / kTileKeys);
-    // stages 2 .. kTileKeys sort each tile on its own: one launch
-    hipLaunchKernelGGL(bitonic_tile_kernel, dim3(tiles), dim3(kTileThreads), 0, st, keys, 1, 2, kTileKeys);
+    // stages 2 .. kTileKeys sort each tile on its own: 2048-key tiles, then
+    // their merges inside 8192-key tiles
+    hipLaunchKernelGGL(bitonic_tile_kernel<kTileKeysSmall>, dim3((unsigned)(N2 / kTileKeysSmall)),
+                       dim3(kTileThreads), 0, st, keys, 1, 2, kTileKeysSmall);
+    hipLaunchKernelGGL(bitonic_tile_kernel<kTileKeys>, dim3(tiles), dim3(kTileThreads), 0, st, keys,
+                       kTileKeysSmall, 2 * kTileKeysSmall, kTileKeys);
     for (int k = 2 * kTileKeys; k <= N2; k <<= 1) {
         int j = k >> 1;
         for (; j >= kTileKeys; j >>= 1)
             hipLaunchKernelGGL(bitonic_kernel, dim3(grid), dim3(kSampleThreads), 0, st, keys, N2, j, k);
-        hipLaunchKernelGGL(bitonic_tile_kernel, dim3(tiles), dim3(kTileThreads), 0, st, keys, j, k, k);
+        hipLaunchKernelGGL(bitonic_tile_kernel<kTileKeys>, dim3(tiles), dim3(kTileThreads), 0, st, keys, j, k, k);
     }
     hipLaunchKernelGGL(seg_sorted_sum_kernel, dim3(B), dim3(kSampleThreads), 0, st, keys, n, S, psum);
     hipLaunchKernelGGL(draw_topp_kernel, dim3(1), dim3(kDrawThreads), 0, st, keys, n, S, B, psum, (double)top_p, u,
