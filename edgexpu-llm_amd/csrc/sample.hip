@@ -340,9 +340,24 @@ __global__ __launch_bounds__(kDrawThreads) void draw_topp_kernel(const unsigned 
     if (t == 0) *out = (uint32_t)(keys[i >= 0 ? i : kept - 1] & 0xffffffffull);
 }
 
+// io[i] = io[i] / d (the temperature scaling of src/native.c:2339; float
+// division, correctly rounded).
+__global__ __launch_bounds__(kSampleThreads) void div_scalar_kernel(float *__restrict__ io, long long n, float d) {
+    const long long stride = (long long)gridDim.x * kSampleThreads;
+    for (long long i = (long long)blockIdx.x * kSampleThreads + threadIdx.x; i < n; i += stride) io[i] = io[i] / d;
+}
+
 }  // namespace exq
 
 using namespace exq;
+
+hipError_t launch_div_scalar(float *io, long long n, float d, hipStream_t st) {
+    if (n <= 0) return hipErrorInvalidValue;
+    long long blocks = (n + kSampleThreads - 1) / kSampleThreads;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(div_scalar_kernel, dim3((unsigned)blocks), dim3(kSampleThreads), 0, st, io, n, d);
+    return hipGetLastError();
+}
 
 // Bytes of workspace launch_sample_softmax needs for n entries.
 size_t sample_workspace_bytes(int n) {

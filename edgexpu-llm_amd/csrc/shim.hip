@@ -48,6 +48,7 @@ hipError_t launch_gemv_fused_f32(int type, const uint8_t *w, int n_out, const fl
                                  unsigned long long *amax = nullptr, int *nparts = nullptr);
 hipError_t launch_sample_softmax(float *x, int n, float top_p, double u, uint32_t *out, void *ws, hipStream_t st);
 size_t sample_workspace_bytes(int n);
+hipError_t launch_div_scalar(float *io, long long n, float d, hipStream_t st);
 hipError_t launch_argmax_finish(const unsigned long long *partial, int m, int nparts, int stride, uint32_t *best,
                                 hipStream_t st);
 hipError_t launch_gemv_fused(int type, int nmat, const uint8_t *const *w, const int *n_out, const float *const *bias,
@@ -841,6 +842,15 @@ int edgexpu_hip_sample_softmax_dev(float *logits, int n, float top_p, uint64_t *
     if (ws == nullptr) return 0;
     const double u = sample_uniform(rng);
     return hip_ok(launch_sample_softmax(logits, n, top_p, u, out, ws, pick_stream(stream)), "sample_softmax") ? 1 : 0;
+}
+
+int edgexpu_hip_div_scalar_dev(float *io, long long n, float d, void *stream) {
+    if (!ensure_init()) return 0;
+    if (io == nullptr || n <= 0) {
+        set_error(-2, "div_scalar: null buffer or n=%lld", n);
+        return 0;
+    }
+    return hip_ok(launch_div_scalar(io, n, d, pick_stream(stream)), "div_scalar") ? 1 : 0;
 }
 
 int edgexpu_hip_softmax_dev(float *io, int n, void *stream) {

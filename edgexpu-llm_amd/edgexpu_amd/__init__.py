@@ -85,6 +85,7 @@ class HipLib:
         self.sample_dev = _sig(L, "edgexpu_hip_sample_softmax_dev", C.c_int,
                                [_vp, C.c_int, C.c_float, C.POINTER(C.c_uint64), _vp, _vp])
         self.softmax_dev = _sig(L, "edgexpu_hip_softmax_dev", C.c_int, [_vp, C.c_int, _vp])
+        self.div_scalar_dev = _sig(L, "edgexpu_hip_div_scalar_dev", C.c_int, [_vp, C.c_longlong, C.c_float, _vp])
         self.sample_host = _sig(L, "edgexpu_hip_sample_softmax", C.c_int,
                                 [_vp, C.c_int, C.c_float, C.POINTER(C.c_uint64), C.POINTER(C.c_uint32)])
         self.softmax_host = _sig(L, "edgexpu_hip_softmax", C.c_int, [_vp, C.c_int])
@@ -250,6 +251,14 @@ def sample_softmax(logits, top_p: float, rng: int, out=None):
     L = hip()
     L.check(L.sample_dev(_ptr(logits), logits.numel(), top_p, C.byref(state), _ptr(out), _stream()), "sample_softmax")
     return out, state.value
+
+
+def div_scalar(io, d: float):
+    """io /= d in place on the device (edgexpu_hip_div_scalar_dev: the
+    temperature scaling of src/native.c:2339)."""
+    L = hip()
+    L.check(L.div_scalar_dev(_ptr(io), io.numel(), d, _stream()), "div_scalar")
+    return io
 
 
 def softmax(io):

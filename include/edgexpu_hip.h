@@ -170,6 +170,9 @@ int edgexpu_hip_embed_rows_dev(float *out, const void *table, uint32_t type, lon
  * falls within that distance of a running sum.  logits 16-byte aligned,
  * 1 <= n <= 2^24. */
 int edgexpu_hip_sample_softmax_dev(float *logits, int n, float top_p, uint64_t *rng, uint32_t *out, void *stream);
+/* io[i] = io[i] / d on device, float division: the temperature scaling of
+ * the scores before sampling (src/native.c:2339). */
+int edgexpu_hip_div_scalar_dev(float *io, long long n, float d, void *stream);
 /* Softmax of io[0..n) in place on device (edgexpu_cpu_softmax). */
 int edgexpu_hip_softmax_dev(float *io, int n, void *stream);
 

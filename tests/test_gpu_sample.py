@@ -144,3 +144,15 @@ def test_dropin_sample_bad_arguments(kern):
     kern.edgexpu_cpu_softmax(None, 4)
     kern.edgexpu_cpu_softmax(io.ctypes.data_as(_f32p), 0)
     assert np.array_equal(io, np.zeros(4, np.float32))
+
+
+@pytest.mark.parametrize("n", [1, 1000, 128256, 3000001])
+@pytest.mark.parametrize("temp", [0.7, 1.3, 3.0])
+def test_temperature_division_bit_exact(hipdev, n, temp):
+    """logits[i] = score / temperature (src/native.c:2339): float division,
+    bit-identical to numpy's."""
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * 10.0).astype(np.float32)
+    d = torch.from_numpy(x).to("cuda:0")
+    E.div_scalar(d, temp)
+    assert np.array_equal(bits(d.cpu().numpy()), bits(x / np.float32(temp)))
