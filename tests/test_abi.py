@@ -37,7 +37,10 @@ def test_reference_entry_points_present():
                  "edgexpu_gguf_quantize_q8_0", "edgexpu_gguf_quantize_q8_k", "edgexpu_gguf_dot_quant",
                  "edgexpu_gguf_dot_quant_q8", "edgexpu_gguf_dot_quant_q8k", "edgexpu_gguf_row_bytes",
                  "edgexpu_gguf_type_block_size", "edgexpu_gguf_type_block_bytes", "edgexpu_gguf_q8_0_nbytes",
-                 "edgexpu_gguf_q8_k_nbytes", "edgexpu_gguf_can_dot_q8", "edgexpu_gguf_can_dot_q8k"]
+                 "edgexpu_gguf_q8_k_nbytes", "edgexpu_gguf_can_dot_q8", "edgexpu_gguf_can_dot_q8k",
+                 "edgexpu_gguf_dequantize_row", "edgexpu_gguf_dequantize_q8_0_rows", "edgexpu_gguf_q8_0_dot_row",
+                 "edgexpu_gguf_tensor_elements", "edgexpu_gguf_tensor_nbytes", "edgexpu_gguf_quant_selftest",
+                 "edgexpu_cpu_softmax", "edgexpu_cpu_sample_softmax"]
     lib = C.CDLL(E.KERNELS_SO)
     assert all(hasattr(lib, n) for n in ref_names)
 
@@ -149,3 +152,27 @@ def test_tensor_sizes_and_row_checks_without_gpu():
     k.edgexpu_gguf_q8_0_dot_row.restype = C.c_float
     k.edgexpu_gguf_q8_0_dot_row.argtypes = [C.c_void_p, C.c_uint64, C.c_int, C.c_void_p]
     assert k.edgexpu_gguf_q8_0_dot_row(src, 0, 33, dst) == 0.0
+
+
+def test_sampling_argument_checks_without_gpu():
+    """edgexpu_cpu_sample_softmax / edgexpu_cpu_softmax refuse bad arguments
+    before any device call, as src/cpu_kernel.c:333-335 and 776-778: 0 and
+    nothing written."""
+    lib = C.CDLL(E.KERNELS_SO)
+    f32p = C.POINTER(C.c_float)
+    lib.edgexpu_cpu_sample_softmax.restype = C.c_int
+    lib.edgexpu_cpu_sample_softmax.argtypes = [f32p, C.c_int, C.c_float, C.POINTER(C.c_uint64),
+                                               C.POINTER(C.c_uint32)]
+    lib.edgexpu_cpu_softmax.restype = None
+    lib.edgexpu_cpu_softmax.argtypes = [f32p, C.c_int]
+    io = np.ones(4, np.float32)
+    st, out = C.c_uint64(5), C.c_uint32(9)
+    p = io.ctypes.data_as(f32p)
+    assert lib.edgexpu_cpu_sample_softmax(p, 0, 1.0, C.byref(st), C.byref(out)) == 0
+    assert lib.edgexpu_cpu_sample_softmax(p, -3, 0.5, C.byref(st), C.byref(out)) == 0
+    assert lib.edgexpu_cpu_sample_softmax(None, 4, 1.0, C.byref(st), C.byref(out)) == 0
+    assert lib.edgexpu_cpu_sample_softmax(p, 4, 1.0, None, C.byref(out)) == 0
+    assert lib.edgexpu_cpu_sample_softmax(p, 4, 1.0, C.byref(st), None) == 0
+    lib.edgexpu_cpu_softmax(None, 4)
+    lib.edgexpu_cpu_softmax(p, 0)
+    assert st.value == 5 and out.value == 9 and np.array_equal(io, np.ones(4, np.float32))
