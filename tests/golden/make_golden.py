@@ -146,6 +146,24 @@ def main() -> int:
         scores = np.array([ref.dot_f32(qt, w[i], h, n) for i in range(rows)], np.float32)
         save(f"dotf32_{TNAME[qt]}_{n}", type=np.array(qt), w=w, h=h, scores=scores)
 
+    # 6. softmax and sampling (src/cpu_kernel.c:328-353,762-849): per (n, seed)
+    # one score vector and its probabilities; per top_p the token and state
+    srng = np.random.default_rng(SEED + 6)
+    sizes, seeds, tops = [1, 4, 7, 300, 2000], [0, 1, 0xDEADBEEF], [1.0, 0.9, 0.5, 0.0]
+    logits, probs, toks, states = [], [], [], []
+    for n in sizes:
+        for seed in seeds:
+            x = (srng.standard_normal(n) * srng.choice([1.0, 4.0, 12.0])).astype(np.float32)
+            logits.append(x)
+            probs.append(ref.softmax(x))
+            for top_p in tops:
+                t, _, st = ref.sample_softmax(x, top_p, seed)
+                toks.append(t)
+                states.append(st)
+    save("sample", sizes=np.array(sizes, np.int32), seeds=np.array(seeds, np.uint64),
+         top_p=np.array(tops, np.float32), logits=np.concatenate(logits), probs=np.concatenate(probs),
+         tokens=np.array(toks, np.uint32), states=np.array(states, np.uint64))
+
     with open(os.path.join(HERE, "MANIFEST.json"), "w") as f:
         json.dump({"seed": SEED, "generator": "tests/golden/make_golden.py",
                    "reference_build": "oracle/Makefile target ref", "fixtures": manifest}, f, indent=1,

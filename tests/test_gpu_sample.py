@@ -156,3 +156,22 @@ def test_temperature_division_bit_exact(hipdev, n, temp):
     d = torch.from_numpy(x).to("cuda:0")
     E.div_scalar(d, temp)
     assert np.array_equal(bits(d.cpu().numpy()), bits(x / np.float32(temp)))
+
+
+def test_sample_vs_golden(hipdev, golden):
+    """The reference build's fixtures: state equal, probabilities within 4
+    ulp, token = the definition's draw over the device probabilities, and
+    the reference's token in all but a pick that lands within a few ulp of a
+    running sum (at most 3 of the 60 cases)."""
+    from test_oracle import _sample_cases
+
+    g = golden("sample")
+    same = total = 0
+    for n, seed, top_p, x, p, tok, st in _sample_cases(g):
+        t_d, p_d, s_d = dev_sample(x, top_p, seed)
+        assert s_d == st
+        assert_ulp(p_d, p)
+        assert t_d == npref.draw(p_d, top_p, s_d), (n, seed, top_p)
+        same += t_d == tok
+        total += 1
+    assert total == 60 and same >= total - 3

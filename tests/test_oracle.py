@@ -450,3 +450,23 @@ def test_sampler_reference_known_answers(ora):
     tok, _, _ = ora.sample_softmax(np.array([0, 20, 0, 0], np.float32), 0.9, s)
     assert tok == 1
     assert np.array_equal(ora.softmax(np.zeros(2, np.float32)), np.float32([0.5, 0.5]))
+
+
+def _sample_cases(g):
+    off, i = 0, 0
+    for n in g["sizes"]:
+        for seed in g["seeds"]:
+            x, p = g["logits"][off:off + n], g["probs"][off:off + n]
+            for top_p in g["top_p"]:
+                yield int(n), int(seed), float(top_p), x, p, int(g["tokens"][i]), int(g["states"][i])
+                i += 1
+            off += n
+
+
+def test_oracle_sampler_matches_golden(ora, golden):
+    """Tokens, states and probability bits written by the reference build."""
+    g = golden("sample")
+    for n, seed, top_p, x, p, tok, st in _sample_cases(g):
+        t_o, p_o, s_o = ora.sample_softmax(x, top_p, seed)
+        assert (t_o, s_o) == (tok, st), (n, seed, top_p)
+        assert np.array_equal(bits(p_o), bits(p)) and np.array_equal(bits(ora.softmax(x)), bits(p))
