@@ -14,6 +14,7 @@
 // the drop-in quantize entry points return byte-identical buffers and the
 // GEMV kernels read the same bytes the reference's integer dots consume.
 #include "common.h"
+#include "q8k.h"
 
 namespace exq {
 
@@ -62,53 +63,20 @@ __global__ __launch_bounds__(256) void quantize_q8_k_kernel(
     const int tok = (int)(blk / nb);
     const int b = (int)(blk % nb);
     const float4 v = *reinterpret_cast<const float4 *>(x + (size_t)tok * ldx + (size_t)b * kQKK + lane * 4);
-    const float xs[4] = {v.x, v.y, v.z, v.w};
-    // First-index signed maximum of |x|: one 64-bit max over keys
-    // (|x| bits << 32) | (~index << 1) | sign -- equal magnitudes -> lowest
-    // index wins; zeros and NaN never enter (the reference's strict '>' from
-    // amax = 0).
-    unsigned long long key = 0ull;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float av = fabsf(xs[e]);
-        const uint32_t idx = (uint32_t)(lane * 4 + e);
-        unsigned long long k = ((unsigned long long)__float_as_uint(av) << 32) | (((~idx) & 0x7fffffffu) << 1) |
-                               (xs[e] < 0.0f ? 1u : 0u);
-        k = av > 0.0f ? k : 0ull;
-        key = k > key ? k : key;
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const unsigned long long o = __shfl_xor(key, off, 64);
-        key = o > key ? o : key;
-    }
-    const float amax = __uint_as_float((uint32_t)(key >> 32));
-    const float maxv = (key & 1ull) ? -amax : amax;
+    const Q8KLane r = q8k_quantize_lane(v, lane);
     uint8_t *blkp = packed + ((size_t)tok * nb + b) * kBytesQ8_K;  // 4-byte aligned
-    if (key == 0ull) {
+    if (r.zero) {
         reinterpret_cast<uint32_t *>(blkp + 4)[lane] = 0u;
         if (lane < 8) reinterpret_cast<uint32_t *>(blkp + 260)[lane] = 0u;
         if (lane == 0) *reinterpret_cast<uint32_t *>(blkp) = 0u;
         return;
     }
-    const float iscale = -127.0f / maxv;
-    uint32_t word = 0;
-    int sum = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float p = iscale * xs[e];
-        // lrintf: a NaN or infinite product gives LONG_MIN, whose low 32 bits are 0.
-        int q = fabsf(p) < 2147483648.0f ? (int)rintf(p) : 0;
-        q = q > 127 ? 127 : (q < -127 ? -127 : q);
-        sum += q;
-        word |= (uint32_t)(q & 0xff) << (8 * e);
-    }
+    int sum = r.sum4;
     sum += __shfl_xor(sum, 1, 64);
     sum += __shfl_xor(sum, 2, 64);
-    const float d = 1.0f / iscale;
-    reinterpret_cast<uint32_t *>(blkp + 4)[lane] = word;
+    reinterpret_cast<uint32_t *>(blkp + 4)[lane] = r.word;
     if ((lane & 3) == 0) reinterpret_cast<int16_t *>(blkp + 260)[lane >> 2] = (int16_t)sum;
-    if (lane == 0) *reinterpret_cast<float *>(blkp) = d;
+    if (lane == 0) *reinterpret_cast<float *>(blkp) = r.d;
 }
 
 }  // namespace exq

@@ -30,8 +30,11 @@ hipError_t launch_rmsnorm(const float *x, const float *w, float *out, int m, int
 hipError_t launch_elementwise(const float *a, const float *b, float *out, long long n, int kind, hipStream_t st);
 hipError_t launch_argmax_rows(const float *s, int m, int n, size_t lds, unsigned long long *partial, uint32_t *best,
                               hipStream_t st);
-hipError_t launch_gemm_q8(int type, const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const uint8_t *xq,
-                          size_t xq_stride, const float *bias, float *out, int ldo, hipStream_t st);
+size_t gemm_q4k_pack_bytes(int m, int K);
+hipError_t launch_q8k_pack_f32(const float *x, int m, int K, int ldx, uint8_t *pack, hipStream_t st);
+hipError_t launch_q8k_pack_q8k(const uint8_t *xq, size_t xq_stride, int m, int K, uint8_t *pack, hipStream_t st);
+hipError_t launch_gemm_q4k(const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const uint8_t *pack,
+                           const float *bias, float *out, int ldo, hipStream_t st);
 hipError_t launch_gemm_f16(const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const uint8_t *xq,
                            size_t xq_stride, void *ws, const float *bias, float *out, int ldo, hipStream_t st);
 size_t gemm_f16_workspace(int m, int n_out, int K);
@@ -83,6 +86,8 @@ struct State {
     void *lws = nullptr;    // layer entry: prologue activation and pre-residual outputs
     size_t lws_cap = 0;
     int prefill_mode = 0;   // EDGEXPU_HIP_PREFILL_EXACT_INT8 / _F16
+    void *gws = nullptr;    // exact prefill GEMM: activation pack
+    size_t gws_cap = 0;
     size_t dbuf_cap = 0;
     int err = 0;
     char msg[512] = {0};
@@ -247,6 +252,46 @@ void *f16ws(size_t bytes) {
     return g.f16ws;
 }
 
+// Workspace of the exact prefill GEMM (the activation pack), grown on demand.
+void *gemm_ws(size_t bytes) {
+    if (bytes <= g.gws_cap) return g.gws;
+    if (g.gws != nullptr) {
+        if (!hip_ok(hipDeviceSynchronize(), "gemm workspace sync")) return nullptr;
+        (void)hipFree(g.gws);
+        g.gws = nullptr;
+        g.gws_cap = 0;
+    }
+    size_t cap = align_up(bytes, (size_t)1 << 20);
+    if (!hip_ok(hipMalloc(&g.gws, cap), "hipMalloc gemm workspace")) return nullptr;
+    g.gws_cap = cap;
+    return g.gws;
+}
+
+// Exact Q4_K prefill GEMM of nmat matrices over one input: f32 activations
+// (x != nullptr) or Q8_K blocks already in memory (xq).  The activations are
+// packed once into the GEMM's operand layout, then one launch per matrix.
+bool run_gemm_q4k(int nmat, const void *const *w, const int *n_out, int n_in, int m, const float *x,
+                  const uint8_t *xq, size_t xq_stride, const float *const *bias, float *const *out, const int *ldo,
+                  hipStream_t st) {
+    uint8_t *pack = (uint8_t *)gemm_ws(gemm_q4k_pack_bytes(m, n_in));
+    if (pack == nullptr) return false;
+    const hipError_t e = x != nullptr ? launch_q8k_pack_f32(x, m, n_in, n_in, pack, st)
+                                      : launch_q8k_pack_q8k(xq, xq_stride, m, n_in, pack, st);
+    if (!hip_ok(e, "pack activations")) return false;
+    const size_t rb = edgexpu_hip_row_bytes(kTypeQ4_K, n_in);
+    for (int z = 0; z < nmat; ++z)
+        if (!hip_ok(launch_gemm_q4k((const uint8_t *)w[z], rb, n_out[z], n_in, m, pack,
+                                    bias != nullptr ? bias[z] : nullptr, out[z], ldo[z], st),
+                    "gemm_q4k"))
+            return false;
+    return true;
+}
+
+bool use_exact_gemm(uint32_t type, int n_out, int n_in, int m) {
+    return m >= kGemmMinTokens && g.prefill_mode == EDGEXPU_HIP_PREFILL_EXACT_INT8 &&
+           gemm_q8_supported((int)type, n_out, n_in, m);
+}
+
 // Workspace carve-up for m tokens of K elements.
 struct ActWs {
     uint8_t *xq;               // m * act_bytes   quantized activations
@@ -324,8 +369,7 @@ bool run_q8_product(uint32_t type, const void *w, int n_out, int n_in, int m, co
             return hip_ok(launch_gemm_f16((const uint8_t *)w, rb, n_out, n_in, m, xq, ab, ws, bias, out, ldo, st),
                           "gemm_f16");
         }
-        return hip_ok(launch_gemm_q8((int)type, (const uint8_t *)w, rb, n_out, n_in, m, xq, ab, bias, out, ldo, st),
-                      "gemm_q8");
+        return run_gemm_q4k(1, &w, &n_out, n_in, m, nullptr, xq, ab, &bias, &out, &ldo, st);
     }
     if (ldo == n_out && split_gemv(type, n_in, m)) {
         const uint8_t *wp = (const uint8_t *)w;
@@ -362,6 +406,8 @@ bool run_linear_group(uint32_t type, int nmat, const void *const *w, const int *
                                         nullptr, 0, st),
                       "gemv_fused");
     }
+    if (use_exact_gemm(type, n_out[0], n_in, m))  // the GEMM quantizes x into its own operand layout
+        return run_gemm_q4k(nmat, w, n_out, n_in, m, x, nullptr, 0, bias, out, n_out, st);
     ActWs a;
     if (!act_ws(type, m, n_in, a)) return false;
     const hipError_t e = q8_0_family((int)type) ? launch_quantize_q8_0(x, m, n_in, n_in, a.xq, st)
@@ -420,6 +466,7 @@ void edgexpu_hip_shutdown(void) {
     if (g.f16ws) (void)hipFree(g.f16ws);
     if (g.sws) (void)hipFree(g.sws);
     if (g.lws) (void)hipFree(g.lws);
+    if (g.gws) (void)hipFree(g.gws);
     (void)hipStreamDestroy(g.stream);
     const int err = g.err;
     char msg[sizeof(g.msg)];

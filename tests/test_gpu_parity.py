@@ -220,10 +220,13 @@ def _q8k_rows(ora, x):
 
 
 @pytest.mark.parametrize("n_in,n_out,m", [(4096, 300, 64), (2560, 515, 100), (256, 70, 129), (14336, 130, 64),
-                                          (4096, 257, 200), (1024, 128, 128)])
+                                          (4096, 257, 200), (1024, 128, 128), (1280, 200, 64), (2048, 16385, 70)])
 def test_prefill_gemm_vs_oracle(hipdev, ora, n_in, n_out, m):
-    """m >= 64 Q4_K products run on the int8 matrix cores; every output within
-    the fp32 bound of the reference (oracle) on its conditioning scale."""
+    """m >= 64 Q4_K products run on the matrix cores with exact block integers;
+    every output within the fp32 bound of the reference (oracle) on its
+    conditioning scale.  Shapes cover ragged token and row counts, one
+    super-block, the K range split in two (odd super-block count 5 included)
+    and unsplit (129 row blocks)."""
     rng = np.random.default_rng(900 + n_in + n_out + m)
     w = synth.np_weights(12, n_out, n_in, rng)
     x = synth.np_activations(m, n_in, rng)
@@ -334,6 +337,72 @@ def test_prefill_equals_decode_rows(hipdev, ora):
     for t in (0, 37, 95):
         one = E.linear_quant_batch(dev(w), 12, dev(x[t:t + 1]), n_out, n_in).cpu().numpy()[0]
         assert_tol(big[t], one, 2 * S[t], f"token {t}")
+
+
+def _q4k_headers(w, d, dmin):
+    hb = np.frombuffer(np.array([d, dmin], dtype=np.float16).tobytes(), dtype=np.uint8)
+    wb = w.reshape(w.shape[0], -1, 144)
+    wb[:, :, 0:4] = hb
+    return w
+
+
+@pytest.mark.parametrize("n_in,n_out,m", [(2048, 256, 64), (2048, 4224, 512)])
+def test_prefill_gemm_integers_exact(hipdev, n_in, n_out, m):
+    """Unit scales (d = dmin = 1) and integer activations that are their own
+    Q8_K codes (each block's first element -127: d = 1): every fp32 step of the
+    GEMM is then exact, so the output equals the int64 closed form exactly --
+    the block integers are exact through the matrix cores, with the K range
+    split in two (2 tiles) and unsplit (132 tiles)."""
+    rng = np.random.default_rng(5150 + n_out)
+    w = _q4k_headers(synth.np_weights(12, n_out, n_in, rng), 1.0, 1.0)
+    x = rng.integers(-127, 128, (m, n_in)).astype(np.float32)
+    x.reshape(m, -1, 256)[:, :, 0] = -127.0
+    got = E.linear_quant_batch(dev(w), 12, dev(x), n_out, n_in).cpu().numpy()
+    xq = np.stack([npref.quantize_q8_k(x[t]) for t in range(m)])
+    want, _ = npref.q4k_q8k_gemm_f64(w, xq)
+    assert np.abs(want).max() < 2**24
+    assert np.array_equal(got.astype(np.float64), want)
+
+
+def test_prefill_gemm_two_chains(hipdev, ora):
+    """Tokens whose Q8_K codes are all +-127 (sum |q8| = 32512 per super-block,
+    beyond the 17753 one exact chain allows) run every super-block as two
+    chains; rows with every scale and min 63 and every code 15 push sumi to
+    30.7 M.  Mixed with ordinary tokens in other workgroups' token blocks.
+    Outputs within the bound of the float64 restatement and of the oracle."""
+    rng = np.random.default_rng(6161)
+    n_in, n_out, m = 2048, 300, 200
+    w = synth.np_weights(12, n_out, n_in, rng)
+    for o in (0, 1, 150, n_out - 1):
+        wb = w[o].reshape(-1, 144)
+        wb[:, 4:144] = 0xFF
+    x = synth.np_activations(m, n_in, rng)
+    x[:128] = np.where(rng.random((128, n_in)) < 0.5, -1.0, 1.0).astype(np.float32)
+    x[:128] *= rng.uniform(0.5, 2.0, (128, 1)).astype(np.float32)
+    got = E.linear_quant_batch(dev(w), 12, dev(x), n_out, n_in).cpu().numpy()
+    xq = _q8k_rows(ora, x)
+    exact, S = npref.q4k_q8k_gemm_f64(w, xq)
+    assert_tol(got, exact.astype(np.float32), S, "two chains vs float64")
+    want = ora.linear_quant_batch(x[:4], w, 12, None, 4, n_out, n_in)
+    assert_tol(got[:4], want, S[:4], "two chains vs oracle")
+
+
+def test_prefill_gemm_q8k_input_and_repeat(hipdev, ora):
+    """The GEMM over Q8_K block bytes already in memory (edgexpu_hip_gemv_q8_dev)
+    equals the GEMM over the f32 activations bit for bit (same codes, same
+    operand pack), and a second call gives the same bits (the split-K flags
+    the first call used are back at zero)."""
+    rng = np.random.default_rng(7272)
+    n_in, n_out, m = 4096, 300, 100
+    w = synth.np_weights(12, n_out, n_in, rng)
+    x = synth.np_activations(m, n_in, rng)
+    bias = rng.normal(0, 0.5, n_out).astype(np.float32)
+    a = E.linear_quant_batch(dev(w), 12, dev(x), n_out, n_in, bias=dev(bias)).cpu().numpy()
+    b = E.linear_quant_batch(dev(w), 12, dev(x), n_out, n_in, bias=dev(bias)).cpu().numpy()
+    xq = _q8k_rows(ora, x)
+    c = E.gemv_q8(dev(w), 12, dev(xq), m, n_out, n_in, bias=dev(bias)).cpu().numpy()
+    assert np.array_equal(bits(a), bits(b))
+    assert np.array_equal(bits(a), bits(c))
 
 
 # ------------------------------------------------------------------ logits
