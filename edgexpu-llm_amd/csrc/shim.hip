@@ -299,15 +299,28 @@ struct ActWs {
     unsigned long long *keys;  // m * 4096        argmax partials
 };
 
-bool act_ws(uint32_t type, int m, int K, ActWs &a) {
-    const size_t qb = align_up((size_t)m * act_bytes(type, K), 256);
-    const size_t sb = align_up((size_t)m * (K / 16) * sizeof(float), 256);
-    const size_t kb = align_up((size_t)m * kArgmaxParts * sizeof(unsigned long long), 256);
-    uint8_t *base = (uint8_t *)workspace(qb + sb + kb);
-    if (base == nullptr) return false;
+// Byte sizes of the three parts, each a multiple of 256.
+void act_ws_sizes(uint32_t type, int m, int K, size_t &qb, size_t &sb, size_t &kb) {
+    qb = align_up((size_t)m * act_bytes(type, K), 256);
+    sb = align_up((size_t)m * (K / 16) * sizeof(float), 256);
+    kb = align_up((size_t)m * kArgmaxParts * sizeof(unsigned long long), 256);
+}
+
+// The three parts carved out of base (256-byte aligned).
+void act_ws_carve(uint32_t type, int m, int K, uint8_t *base, ActWs &a) {
+    size_t qb, sb, kb;
+    act_ws_sizes(type, m, K, qb, sb, kb);
     a.xq = base;
     a.xs = (float *)(base + qb);
     a.keys = (unsigned long long *)(base + qb + sb);
+}
+
+bool act_ws(uint32_t type, int m, int K, ActWs &a) {
+    size_t qb, sb, kb;
+    act_ws_sizes(type, m, K, qb, sb, kb);
+    uint8_t *base = (uint8_t *)workspace(qb + sb + kb);
+    if (base == nullptr) return false;
+    act_ws_carve(type, m, K, base, a);
     return true;
 }
 
@@ -756,65 +769,84 @@ int edgexpu_hip_gemv_q8_dev(float *out, const uint8_t *xq, const void *w, uint32
     return run_q8_product(type, w, n_out, n_in, m, xq, bias, out, n_out, pick_stream(stream)) ? 1 : 0;
 }
 
-int edgexpu_hip_logits_dev(float *scores, uint32_t *best_dev, const float *hidden, const void *w, uint32_t type,
-                           const float *bias, int m, int vocab, int n_embd, int chunk_rows, void *stream) {
-    if (!ensure_init()) return 0;
-    if (!check_linear_args(scores, hidden, w, type, m, vocab, n_embd, "logits")) return 0;
+}  // extern "C"
+
+namespace {
+
+bool check_logits_args(float *scores, const float *hidden, const void *w, uint32_t type, int m, int vocab,
+                       int n_embd, int chunk_rows, const char *who) {
+    if (!check_linear_args(scores, hidden, w, type, m, vocab, n_embd, who)) return false;
     if (m > kGemvMaxTokens) {
-        set_error(-2, "logits: at most %d hidden vectors per call (m=%d)", kGemvMaxTokens, m);
-        return 0;
+        set_error(-2, "%s: at most %d hidden vectors per call (m=%d)", who, kGemvMaxTokens, m);
+        return false;
     }
     if (!aligned16(hidden)) {
-        set_error(-2, "logits: hidden must be 16-byte aligned");
-        return 0;
+        set_error(-2, "%s: hidden must be 16-byte aligned", who);
+        return false;
     }
     if (chunk_rows < 0) {
-        set_error(-2, "logits: chunk_rows must be >= 0 (got %d)", chunk_rows);
-        return 0;
+        set_error(-2, "%s: chunk_rows must be >= 0 (got %d)", who, chunk_rows);
+        return false;
     }
-    hipStream_t st = pick_stream(stream);
+    return true;
+}
+
+// The logits product and greedy argmax over scratch `a` (quantized hidden
+// vectors, 16-element sums, argmax partial keys), every part of which the
+// kernels write before they read it.
+bool logits_run(float *scores, uint32_t *best_dev, const float *hidden, const void *w, uint32_t type,
+                const float *bias, int m, int vocab, int n_embd, hipStream_t st, const ActWs &a) {
     const size_t rb = edgexpu_hip_row_bytes(type, n_embd);
-    ActWs a;
-    if (!act_ws(type, m, n_embd, a)) return 0;
     // The reference walks the rows in chunks of chunk_rows (its host-memory
     // budget, src/native.c:2262-2274); every row's score is independent of
     // the chunking, so one launch covers all chunks in row order.
     if (q8_0_family((int)type)) {
         // src/native.c:2317-2319: the Q8_0 family scores rows against the
         // Q8_0-quantized hidden vector
-        if (!hip_ok(launch_quantize_q8_0(hidden, m, n_embd, n_embd, a.xq, st), "quantize_q8_0")) return 0;
+        if (!hip_ok(launch_quantize_q8_0(hidden, m, n_embd, n_embd, a.xq, st), "quantize_q8_0")) return false;
         if (!hip_ok(launch_gemv_q8((int)type, (const uint8_t *)w, rb, vocab, n_embd, m, a.xq,
                                    act_bytes(type, n_embd), bias, scores, vocab, st),
                     "logits gemv"))
-            return 0;
+            return false;
     } else {
         // the other formats use the f32-activation dots (src/native.c:445-462);
         // K-quant rows one hidden vector per fused launch (a row's score then
         // does not depend on m, as in the reference's per-token loop), whose
         // store also keeps each wave's greedy-argmax key: one small launch
         // then reduces those keys instead of re-reading the scores
-        if (k_family((int)type) && !hip_ok(launch_xsum16(hidden, m, n_embd, a.xs, st), "xsum16")) return 0;
-        static const int fused_argmax = env_int("EXQ_LOGITS_ARGMAX", 1);  // 0: two-pass argmax over the scores
-        if (fused_argmax != 0 && best_dev != nullptr && k_family((int)type) &&
-            gemv_fused_f32_supported((int)type, n_embd)) {
+        if (k_family((int)type) && !hip_ok(launch_xsum16(hidden, m, n_embd, a.xs, st), "xsum16")) return false;
+        if (best_dev != nullptr && k_family((int)type) && gemv_fused_f32_supported((int)type, n_embd)) {
             int nparts = 0;
             for (int t = 0; t < m; ++t) {
                 const hipError_t e = launch_gemv_fused_f32(
                     (int)type, (const uint8_t *)w, vocab, bias, scores + (size_t)t * vocab, rb, n_embd,
                     hidden + (size_t)t * n_embd, a.xs + (size_t)t * (n_embd / 16), st, a.keys + (size_t)t * kArgmaxParts,
                     &nparts);
-                if (!hip_ok(e, "logits gemv + argmax")) return 0;
+                if (!hip_ok(e, "logits gemv + argmax")) return false;
             }
-            return hip_ok(launch_argmax_finish(a.keys, m, nparts, kArgmaxParts, best_dev, st), "argmax") ? 1 : 0;
+            return hip_ok(launch_argmax_finish(a.keys, m, nparts, kArgmaxParts, best_dev, st), "argmax");
         }
         if (!run_f32_product(type, w, vocab, n_embd, m, hidden, k_family((int)type) ? a.xs : nullptr, bias, scores,
                              vocab, st))
-            return 0;
+            return false;
     }
     if (best_dev != nullptr &&
         !hip_ok(launch_argmax_rows(scores, m, vocab, (size_t)vocab, a.keys, best_dev, st), "argmax"))
-        return 0;
-    return 1;
+        return false;
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int edgexpu_hip_logits_dev(float *scores, uint32_t *best_dev, const float *hidden, const void *w, uint32_t type,
+                           const float *bias, int m, int vocab, int n_embd, int chunk_rows, void *stream) {
+    if (!ensure_init()) return 0;
+    if (!check_logits_args(scores, hidden, w, type, m, vocab, n_embd, chunk_rows, "logits")) return 0;
+    ActWs a;
+    if (!act_ws(type, m, n_embd, a)) return 0;
+    return logits_run(scores, best_dev, hidden, w, type, bias, m, vocab, n_embd, pick_stream(stream), a) ? 1 : 0;
 }
 
 int edgexpu_hip_dequantize_dev(const void *src, uint32_t type, uint64_t n_elements, float *dst, void *stream) {
