@@ -95,6 +95,22 @@ struct State {
 
 State g;
 
+// Fixed device scratch of edgexpu_hip_logits_noalloc_dev: the quantized
+// hidden vectors, their 16-element sums and the argmax partial keys of up to
+// kGemvMaxTokens vectors of kScratchMaxEmbd elements (each GPU the library
+// runs on holds its own copy until the process ends).  Host code never hands
+// `scratch` itself to a kernel: its device address comes from
+// hipGetSymbolAddress, once per device at init, into g_scratch_ptr.
+constexpr int kScratchMaxEmbd = 16384;
+constexpr size_t kScratchBytes =
+    ((size_t)kGemvMaxTokens * (kScratchMaxEmbd / kQKK) * kBytesQ8_K + 255) / 256 * 256 +  // Q8_K (> Q8_0) codes
+    (size_t)kGemvMaxTokens * (kScratchMaxEmbd / 16) * sizeof(float) +                    // 16-element sums
+    (size_t)kGemvMaxTokens * kArgmaxParts * sizeof(unsigned long long);                  // argmax keys
+static_assert(kScratchBytes <= 512 * 1024, "a modest fixed scratch");
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+void *g_scratch_ptr[kMaxDevices];
+
 void set_error(int code, const char *fmt, ...) {
     if (g.err != 0) return;  // sticky: keep the first error
     g.err = code != 0 ? code : -1;
@@ -465,6 +481,11 @@ int edgexpu_hip_init(int device) {
         return 0;
     }
     if (!hip_ok(hipSetDevice(device), "hipSetDevice")) return 0;
+    if (device < kMaxDevices && g_scratch_ptr[device] == nullptr) {
+        void *p = nullptr;
+        if (!hip_ok(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "scratch address")) return 0;
+        g_scratch_ptr[device] = p;
+    }
     if (!hip_ok(hipStreamCreate(&g.stream), "hipStreamCreate")) return 0;
     g.device = device;
     g.ready = true;
@@ -846,6 +867,27 @@ int edgexpu_hip_logits_dev(float *scores, uint32_t *best_dev, const float *hidde
     if (!check_logits_args(scores, hidden, w, type, m, vocab, n_embd, chunk_rows, "logits")) return 0;
     ActWs a;
     if (!act_ws(type, m, n_embd, a)) return 0;
+    return logits_run(scores, best_dev, hidden, w, type, bias, m, vocab, n_embd, pick_stream(stream), a) ? 1 : 0;
+}
+
+int edgexpu_hip_logits_noalloc_dev(float *scores, uint32_t *best_dev, const float *hidden, const void *w,
+                                   uint32_t type, const float *bias, int m, int vocab, int n_embd, int chunk_rows,
+                                   void *stream) {
+    // no allocation of any kind here: the library must be set up already
+    if (!g.ready || g.device >= kMaxDevices || g_scratch_ptr[g.device] == nullptr) {
+        set_error(-4, "logits_noalloc: call edgexpu_hip_init first (this entry point allocates nothing)");
+        return 0;
+    }
+    if (!check_logits_args(scores, hidden, w, type, m, vocab, n_embd, chunk_rows, "logits_noalloc")) return 0;
+    size_t qb, sb, kb;
+    act_ws_sizes(type, m, n_embd, qb, sb, kb);
+    if (n_embd > kScratchMaxEmbd || qb + sb + kb > kScratchBytes) {
+        set_error(-2, "logits_noalloc: m=%d x n_embd=%d exceeds the fixed scratch (n_embd <= %d, m <= %d)", m,
+                  n_embd, kScratchMaxEmbd, kGemvMaxTokens);
+        return 0;
+    }
+    ActWs a;
+    act_ws_carve(type, m, n_embd, (uint8_t *)g_scratch_ptr[g.device], a);
     return logits_run(scores, best_dev, hidden, w, type, bias, m, vocab, n_embd, pick_stream(stream), a) ? 1 : 0;
 }
 

@@ -79,6 +79,8 @@ class HipLib:
                                 [_vp, _vp, _vp, C.c_uint32, _vp, C.c_int, C.c_int, C.c_int, _vp])
         self.logits_dev = _sig(L, "edgexpu_hip_logits_dev", C.c_int,
                                [_vp, _vp, _vp, _vp, C.c_uint32, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp])
+        self.logits_noalloc_dev = _sig(L, "edgexpu_hip_logits_noalloc_dev", C.c_int,
+                                       [_vp, _vp, _vp, _vp, C.c_uint32, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp])
         self.dequant_dev = _sig(L, "edgexpu_hip_dequantize_dev", C.c_int, [_vp, C.c_uint32, C.c_uint64, _vp, _vp])
         self.embed_rows_dev = _sig(L, "edgexpu_hip_embed_rows_dev", C.c_int,
                                    [_vp, _vp, C.c_uint32, C.c_longlong, C.c_int, _vp, C.c_int, _vp, _vp])

@@ -139,6 +139,21 @@ int edgexpu_hip_gemv_q8_dev(float *out, const uint8_t *xq, const void *w, uint32
 int edgexpu_hip_logits_dev(float *scores, uint32_t *best_dev, const float *hidden, const void *w, uint32_t type,
                            const float *bias, int m, int vocab, int n_embd, int chunk_rows, void *stream);
 
+/* edgexpu_hip_logits_dev with no allocation of any kind, for callers that
+ * cannot allocate device memory: code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc.  No counterpart in the reference.
+ * Same arguments, checks and results (bit for bit) as edgexpu_hip_logits_dev.
+ * Its scratch (quantized hidden vectors, 16-element sums, argmax partial
+ * keys) is one fixed device array of about 430 KiB per GPU, held until the
+ * process ends: m <= 8 and n_embd <= 16384, larger calls are refused.
+ * edgexpu_hip_init must have run on the device first.  Every call on a GPU
+ * shares that GPU's array, which keeps the last call's contents (every part
+ * is written before it is read, nothing needs clearing): calls that overlap
+ * on one GPU (several streams or threads) race. */
+int edgexpu_hip_logits_noalloc_dev(float *scores, uint32_t *best_dev, const float *hidden, const void *w,
+                                   uint32_t type, const float *bias, int m, int vocab, int n_embd, int chunk_rows,
+                                   void *stream);
+
 /* Bulk dequantization (edgexpu_gguf_dequantize, include/edgexpu/gguf_quant.h:32-39,
  * src/gguf_quant.c:355-411), bit-identical to the reference's x86 build.
  * n_elements must be a multiple of the block size; dst 16-byte aligned. */

@@ -1,0 +1,72 @@
+"""The no-allocation logits entry (edgexpu_hip_logits_noalloc_dev) against the
+allocating one (edgexpu_hip_logits_dev) through the C-ABI: the same kernels
+over a fixed device array instead of the library workspace, so scores and
+greedy argmax agree bit for bit, on two calls in a row (the second with fewer
+vectors, a shorter vocabulary and a shorter hidden vector) and for every
+weight family (Q4_K / Q6_K fused argmax, Q8_0 two-pass argmax).  Sizes past the
+fixed array are refused with a message, before any launch."""
+import numpy as np
+import pytest
+import torch
+
+import edgexpu_amd as E
+from edgexpu_amd import synth
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _both(L, w, qt, h, vocab, n, bias):
+    m = h.shape[0]
+    out = []
+    for fn in (L.logits_dev, L.logits_noalloc_dev):
+        scores = torch.full((m, vocab), float("nan"), device=DEV)
+        best = torch.full((m,), -1, dtype=torch.int32, device=DEV)
+        ok = fn(scores.data_ptr(), best.data_ptr(), h.data_ptr(), w.data_ptr(), qt,
+                None if bias is None else bias.data_ptr(), m, vocab, n, 0,
+                torch.cuda.current_stream().cuda_stream)
+        L.check(ok, "logits")
+        torch.cuda.synchronize()
+        out.append((scores.cpu().numpy(), best.cpu().numpy()))
+    return out
+
+
+@pytest.mark.parametrize("qt,calls", [
+    (12, [(4096, 20000, 3), (2560, 3001, 1)]),
+    (14, [(2560, 15001, 2), (2560, 2050, 1)]),
+    (8, [(576, 49152, 4), (576, 4000, 2)]),
+])
+def test_logits_noalloc_equals_logits(hipdev, qt, calls):
+    L = hipdev
+    L.check(L.init(0), "init")
+    rng = np.random.default_rng(99 + qt)
+    for n, vocab, m in calls:
+        w = _dev(synth.np_weights(qt, vocab, n, rng))
+        h = _dev(rng.normal(0, 1, (m, n)).astype(np.float32))
+        bias = _dev(rng.normal(0, 0.01, vocab).astype(np.float32))
+        (s0, b0), (s1, b1) = _both(L, w, qt, h, vocab, n, bias)
+        assert np.isfinite(s0).all()
+        assert np.array_equal(s0.view(np.uint32), s1.view(np.uint32)), f"scores n={n} vocab={vocab} m={m}"
+        assert np.array_equal(b0, b1), f"argmax n={n} vocab={vocab} m={m}"
+        assert np.array_equal(b1, np.argmax(s1, axis=1))
+
+
+def test_logits_noalloc_refuses_oversize(hipdev):
+    L = hipdev
+    L.check(L.init(0), "init")
+    x = torch.zeros((9, 16640), device=DEV)
+    w = torch.zeros(1 << 20, dtype=torch.uint8, device=DEV)
+    sc = torch.zeros((9, 4), device=DEV)
+    s = torch.cuda.current_stream().cuda_stream
+    assert L.logits_noalloc_dev(sc.data_ptr(), None, x.data_ptr(), w.data_ptr(), 12, None, 1, 4, 16640, 0, s) == 0
+    code, msg = L.last_error()
+    assert code != 0 and "fixed scratch" in msg
+    L.clear_error()
+    assert L.logits_noalloc_dev(sc.data_ptr(), None, x.data_ptr(), w.data_ptr(), 12, None, 9, 4, 256, 0, s) == 0
+    code, msg = L.last_error()
+    assert code != 0 and "at most 8" in msg
+    L.clear_error()
