@@ -15,8 +15,22 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 namespace exq {
+
+// Launch-shape tuning knobs (EXQ_* names).  The library fixes every knob at
+// its default at compile time; only a build with -DEXQ_TUNING_ENV (a
+// launch-shape sweep, never the shipped library) reads the environment
+// variable of the same name, once per process.
+#ifdef EXQ_TUNING_ENV
+inline int tuning_knob(const char *name, int dflt) {
+    const char *e = getenv(name);
+    return e != nullptr ? atoi(e) : dflt;
+}
+#else
+constexpr int tuning_knob(const char *, int dflt) { return dflt; }
+#endif
 
 constexpr int kTypeF32 = 0;
 constexpr int kTypeF16 = 1;

@@ -12,6 +12,7 @@
 //   Q5_0  y = (float)(c - 16) * d                    (src/gguf_quant.c:176-177)
 //   Q5_K  y = (d*sc) * c - (dmin*m)                  (src/gguf_quant.c:339-343)
 //   F16   y = (float)h                               (src/gguf_quant.c:183-191)
+//   F32   y = x, a copy                              (src/gguf_quant.c:376-378)
 #include "common.h"
 
 namespace exq {
@@ -246,6 +247,27 @@ __global__ __launch_bounds__(256) void dequant_f16_kernel(const uint8_t *__restr
     dq_f16(src, (long long)blockIdx.x * blockDim.x + threadIdx.x, n, dst);
 }
 
+// F32: one thread per 8 elements, a copy (the last thread of an n not
+// divisible by 8 copies the remainder one by one).
+__device__ __forceinline__ void dq_f32(const uint8_t *__restrict__ src, long long t, long long n,
+                                       float *__restrict__ dst) {
+    const long long e0 = 8 * t;
+    if (e0 >= n) return;
+    if (e0 + 8 <= n) {
+        const uint4 a = ldg16(src + 4 * e0), b = ldg16(src + 4 * e0 + 16);
+        const float y[8] = {__uint_as_float(a.x), __uint_as_float(a.y), __uint_as_float(a.z), __uint_as_float(a.w),
+                            __uint_as_float(b.x), __uint_as_float(b.y), __uint_as_float(b.z), __uint_as_float(b.w)};
+        store8(dst + e0, y);
+    } else {
+        for (long long e = e0; e < n; ++e) dst[e] = __uint_as_float(ldg4(src + 4 * e));
+    }
+}
+
+__global__ __launch_bounds__(256) void dequant_f32_kernel(const uint8_t *__restrict__ src, long long n,
+                                                          float *__restrict__ dst) {
+    dq_f32(src, (long long)blockIdx.x * blockDim.x + threadIdx.x, n, dst);
+}
+
 // Rows of a GGUF matrix gathered by index (the embedding lookup of
 // src/native.c:428-443 through edgexpu_gguf_dequantize_row,
 // src/gguf_quant.c:428-466): token y's row ids[y] dequantized into
@@ -273,7 +295,8 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t *__rest
     else if constexpr (TYPE == kTypeQ4_K) dq_q4_k(src, t, dst);
     else if constexpr (TYPE == kTypeQ5_K) dq_q5_k(src, t, dst);
     else if constexpr (TYPE == kTypeQ6_K) dq_q6_k(src, t, dst);
-    else dq_f16(src, t, n_embd, dst);
+    else if constexpr (TYPE == kTypeF16) dq_f16(src, t, n_embd, dst);
+    else dq_f32(src, t, n_embd, dst);
 }
 
 }  // namespace exq
@@ -282,15 +305,16 @@ using namespace exq;
 
 // n_ids rows ids[0..n_ids) of a [n_rows x n_embd] matrix of `type` into
 // out[n_ids][n_embd] (16-byte aligned; n_embd a multiple of the block, of
-// 32 for F16).
+// 4 for F16 and F32).
 hipError_t launch_dequantize_rows(const uint8_t *table, int type, long long n_rows, int n_embd, const int32_t *ids,
                                   int n_ids, float *out, int *bad, hipStream_t st) {
     const bool q80 = q8_0_family(type);
     const int be = q80 ? kQK8_0 : (k_family(type) ? kQKK : 1);
     const int bb = type == kTypeQ8_0 ? kBytesQ8_0 : type == kTypeQ4_0 ? kBytesQ4_0 : type == kTypeQ5_0 ? kBytesQ5_0
-                 : type == kTypeQ4_K ? kBytesQ4_K : type == kTypeQ5_K ? kBytesQ5_K : type == kTypeQ6_K ? kBytesQ6_K : 2;
+                 : type == kTypeQ4_K ? kBytesQ4_K : type == kTypeQ5_K ? kBytesQ5_K : type == kTypeQ6_K ? kBytesQ6_K
+                 : type == kTypeF16 ? 2 : 4;
     const size_t row_bytes = (size_t)(n_embd / be) * bb;
-    // threads per row: 4 per 32-element block, 32 per super-block, n/8 for F16
+    // threads per row: 4 per 32-element block, 32 per super-block, n/8 for F16 and F32
     const long long tpr = q80 ? (long long)(n_embd / kQK8_0) * 4 : k_family(type) ? (long long)(n_embd / kQKK) * 32
                                                                                : (long long)((n_embd + 7) / 8);
     const dim3 grid((unsigned)((tpr + 255) / 256), (unsigned)n_ids);
@@ -305,6 +329,7 @@ hipError_t launch_dequantize_rows(const uint8_t *table, int type, long long n_ro
         case kTypeQ5_K: EXQ_ROWS(kTypeQ5_K); break;
         case kTypeQ6_K: EXQ_ROWS(kTypeQ6_K); break;
         case kTypeF16: EXQ_ROWS(kTypeF16); break;
+        case kTypeF32: EXQ_ROWS(kTypeF32); break;
         default: return hipErrorInvalidValue;
     }
 #undef EXQ_ROWS
@@ -341,9 +366,10 @@ hipError_t launch_dequantize(const uint8_t *src, int type, unsigned long long n,
                                threads, dst);
             break;
         case kTypeF16:
+        case kTypeF32:
             threads = (long long)((n + 7) / 8);
-            hipLaunchKernelGGL(dequant_f16_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, src,
-                               (long long)n, dst);
+            hipLaunchKernelGGL(type == kTypeF16 ? dequant_f16_kernel : dequant_f32_kernel,
+                               dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, src, (long long)n, dst);
             break;
         default:
             return hipErrorInvalidValue;

@@ -390,7 +390,6 @@ void f16_split(int m, int n_out, int K, int &split, int &per) {
     const int tiles = ((n_out + kF16TileO - 1) / kF16TileO) * ((m + kF16TileT - 1) / kF16TileT);
     const int total = K / kF16KStep;  // a multiple of 4
     int s = kF16TargetGroups / tiles;
-    if (const char *e = getenv("EXQ_F16_SPLIT")) s = atoi(e);
     s = s < 1 ? 1 : (s > kF16MaxSplit ? kF16MaxSplit : s);
     if (s > total / 2) s = total / 2;
     per = (total + s - 1) / s;

@@ -129,7 +129,7 @@ static hipError_t launch_fmt(GemvArgs a, hipStream_t st) {
 
 template <class Fmt>
 static hipError_t launch_m(GemvArgs a, hipStream_t st) {
-    static const int r1 = getenv("EXQ_GEMV_R") ? atoi(getenv("EXQ_GEMV_R")) : 4;  // tuning override
+    static const int r1 = tuning_knob("EXQ_GEMV_R", 4);  // rows per slot at one token
     switch (a.m) {
         case 1:
             if (r1 == 1) return launch_fmt<Fmt, 1, 1>(a, st);
@@ -234,7 +234,9 @@ hipError_t launch_xsum16(const float *x, int m, int K, float *xs, hipStream_t st
 // index 0 when nothing beats -inf.  Key = (order-preserving score bits, ~index).
 __device__ __forceinline__ unsigned long long argmax_key(float s, unsigned idx) {
     if (!(s > -INFINITY)) return 0ull;  // NaN and -inf never win
-    uint32_t u = __float_as_uint(s);
+    // -0.0 and +0.0 compare equal in the reference's `score > best`, so they
+    // share one key (the lower index then wins)
+    uint32_t u = s == 0.0f ? 0u : __float_as_uint(s);
     u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return ((unsigned long long)u << 32) | (unsigned long long)(~idx);
 }

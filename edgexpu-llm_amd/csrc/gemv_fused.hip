@@ -13,9 +13,9 @@ hipError_t launch_gemv_fused_more(int type, const FusedArgs &a, bool stage, hipS
 using namespace exq;
 
 // Rows split over three waves (12-wave workgroups) are instantiated for one
-// staged token of Q4_K / Q6_K rows (EXQ_FUSED_KS3=0: never).
+// staged token of Q4_K / Q6_K rows (knob EXQ_FUSED_KS3=0: never).
 static bool fused_with3(int type, int m, bool staged) {
-    static const int ks3 = env_int("EXQ_FUSED_KS3", 1);
+    static const int ks3 = tuning_knob("EXQ_FUSED_KS3", 1);
     return ks3 != 0 && m == 1 && staged && (type == kTypeQ4_K || type == kTypeQ6_K);
 }
 
@@ -76,7 +76,7 @@ hipError_t launch_gemv_fused_f32_argmax(int type, const uint8_t *w, int n_out, c
     a.nblk = type == kTypeQ8_0 ? K / kQK8_0 : K / kQKK;
     a.U = type == kTypeQ8_0 ? a.nblk : a.nblk * 4;
     if (!pick_fused_shape(a.U, a.G, a.KS)) return hipErrorInvalidValue;
-    static const int f32_ks3 = env_int("EXQ_FUSED_F32_KS3", 1);
+    static const int f32_ks3 = tuning_knob("EXQ_FUSED_F32_KS3", 1);
     if (f32_ks3 != 0 && type != kTypeQ8_0 && a.U > 32 && a.U <= 48) {
         a.G = 16;
         a.KS = 3;
@@ -85,7 +85,7 @@ hipError_t launch_gemv_fused_f32_argmax(int type, const uint8_t *w, int n_out, c
     }
     const int rows_per_tile = (64 / a.G) * 2;
     const int tiles = (n_out + rows_per_tile - 1) / rows_per_tile;
-    const bool balanced = a.KS == 1 && tiles > 2 * device_cus() * 8 && env_int("EXQ_FUSED_DYN", 1) != 0;
+    const bool balanced = a.KS == 1 && tiles > 2 * device_cus() * 8 && tuning_knob("EXQ_FUSED_DYN", 1) != 0;
     switch (type) {
         case kTypeQ8_0:
             return balanced ? launch_argmax_fmt<FmtQ80F32, 2, 8, 2>(a, st, nparts)
@@ -121,18 +121,18 @@ hipError_t launch_gemv_fused_f32(int type, const uint8_t *w, int n_out, const fl
     a.nblk = type == kTypeQ8_0 ? K / kQK8_0 : K / kQKK;
     a.U = type == kTypeQ8_0 ? a.nblk : a.nblk * 4;
     if (!pick_fused_shape(a.U, a.G, a.KS)) return hipErrorInvalidValue;
-    static const int r_env = env_int("EXQ_FUSED_F32_R", 2);
+    static const int r_env = tuning_knob("EXQ_FUSED_F32_R", 2);
     // one row per lane group spills the Q6_K decode's registers; Q6_K keeps two
     const int r1 = r_env == 1 && type != kTypeQ6_K ? 1 : 2;
     const int rows_per_tile = (64 / a.G) * r1;
     const int tiles = (n_out + rows_per_tile - 1) / rows_per_tile;
-    const bool balanced = a.KS == 1 && tiles > 2 * device_cus() * 8 && env_int("EXQ_FUSED_DYN", 1) != 0;
+    const bool balanced = a.KS == 1 && tiles > 2 * device_cus() * 8 && tuning_knob("EXQ_FUSED_DYN", 1) != 0;
 #define EXQ_F32_LAUNCH(F)                                                                              \
     return balanced ? (r1 == 1 ? launch_fused_fmt<F, 1, 1, 8, false, 2>(a, st) : launch_fused_fmt<F, 1, 2, 8, false, 2>(a, st)) \
                     : (r1 == 1 ? launch_fused_fmt<F, 1, 1, 8, false, 0>(a, st) : launch_fused_fmt<F, 1, 2, 8, false, 0>(a, st))
     // K-quant rows of 33-48 units (K = 2112..3072): 16-lane slots over three
     // waves use 83 % of the lanes where one 64-lane slot uses 62.5 %
-    static const int f32_ks3 = env_int("EXQ_FUSED_F32_KS3", 1);
+    static const int f32_ks3 = tuning_knob("EXQ_FUSED_F32_KS3", 1);
     if (f32_ks3 != 0 && type != kTypeQ8_0 && a.U > 32 && a.U <= 48) {
         a.G = 16;
         a.KS = 3;

@@ -63,7 +63,9 @@ struct FusedArgs {
 // lowest index; NaN and -inf give 0 and never win.
 __device__ __forceinline__ unsigned long long score_key(float s, unsigned idx) {
     if (!(s > -INFINITY)) return 0ull;
-    uint32_t u = __float_as_uint(s);
+    // -0.0 and +0.0 compare equal in the reference's `score > best`, so they
+    // share one key (the lower index then wins)
+    uint32_t u = s == 0.0f ? 0u : __float_as_uint(s);
     u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return ((unsigned long long)u << 32) | (unsigned long long)(~idx);
 }
@@ -702,14 +704,10 @@ static int device_cus() {
     return cus;
 }
 
-// Tuning overrides: EXQ_FUSED_R (rows per slot at m = 1: 1, 2 or 4),
-// EXQ_FUSED_NW (waves per workgroup: 4 or 8), EXQ_FUSED_GRID (multiple of the
-// resident workgroup count), EXQ_FUSED_PER_CU (workgroups per CU at most),
+// Tuning knobs (tuning_knob): EXQ_FUSED_R (rows per slot at m = 1: 1, 2 or
+// 4), EXQ_FUSED_NW (waves per workgroup: 4 or 8), EXQ_FUSED_GRID (multiple of
+// the resident workgroup count), EXQ_FUSED_PER_CU (workgroups per CU at most),
 // EXQ_FUSED_PIPE / EXQ_FUSED_DYN / EXQ_FUSED_BIG (tile schedule).
-static int env_int(const char *name, int dflt) {
-    const char *e = getenv(name);
-    return e != nullptr ? atoi(e) : dflt;
-}
 
 // Grid of the most recent launch_fused_fmt (the argmax epilogue's key count).
 static int &fused_last_grid() {
@@ -746,8 +744,8 @@ static hipError_t launch_fused_fmt(FusedArgs a, hipStream_t st, int per_cu_cap =
         per_cu = v;
         cached_lds = L.total();
     }
-    static const int grid_scale = env_int("EXQ_FUSED_GRID", 1);  // tuning override: resident multiple
-    static const int cu_cap_env = env_int("EXQ_FUSED_PER_CU", 0);  // tuning override: workgroups per CU
+    static const int grid_scale = tuning_knob("EXQ_FUSED_GRID", 1);  // resident multiple
+    static const int cu_cap_env = tuning_knob("EXQ_FUSED_PER_CU", 0);  // workgroups per CU
     const int cu_cap = cu_cap_env > 0 ? cu_cap_env : per_cu_cap;
     const int resident = (cu_cap > 0 && cu_cap < per_cu ? cu_cap : per_cu) * cus * (grid_scale > 0 ? grid_scale : 1);
     const int rounds = (wg_tiles + resident - 1) / resident;
@@ -781,7 +779,7 @@ static hipError_t launch_fused_m(FusedArgs a, int r1, int loop, hipStream_t st) 
                 int tiles = 0;
                 for (int z = 0; z < a.nmat; ++z) tiles += (a.n_out[z] + rows_per_tile - 1) / rows_per_tile;
                 if (tiles <= 2 * device_cus() * NW) loop = 0;
-                static const int big = env_int("EXQ_FUSED_BIG", 1);
+                static const int big = tuning_knob("EXQ_FUSED_BIG", 1);
                 if (loop == 2 && big != 0) return launch_fused_fmt<Fmt, 1, 2, NW, STAGE, 1>(a, st, 1);
             }
             if (loop == 2 && a.KS == 1) {
@@ -914,14 +912,14 @@ static hipError_t launch_fused_pro(FusedArgs a, hipStream_t st) {
 // Tile shape: 8 waves per workgroup; R = 4 rows per slot at m = 1 unless
 // the launch is short and unsplit (<= 4096 rows), where R = 2 keeps more
 // workgroups in flight.  (Measured on [1024..28672 x 4096] and
-// [4096 x 14336] Q4_K.)  EXQ_FUSED_R / EXQ_FUSED_NW override.
+// [4096 x 14336] Q4_K.)  Knobs EXQ_FUSED_R / EXQ_FUSED_NW.
 template <class Fmt>
 static hipError_t launch_fused_nw(FusedArgs a, bool stage, hipStream_t st) {
-    static const int r_env = env_int("EXQ_FUSED_R", 0);
-    static const int nw = env_int("EXQ_FUSED_NW", 8);
+    static const int r_env = tuning_knob("EXQ_FUSED_R", 0);
+    static const int nw = tuning_knob("EXQ_FUSED_NW", 8);
     // 2: balanced per-wave schedule (m = 1, rows not split over waves); 1:
     // two register buffers; 0: workgroup tiles, grid-stride
-    static const int loop = env_int("EXQ_FUSED_PIPE", 0) != 0 ? 1 : (env_int("EXQ_FUSED_DYN", 1) != 0 ? 2 : 0);
+    static const int loop = tuning_knob("EXQ_FUSED_PIPE", 0) != 0 ? 1 : (tuning_knob("EXQ_FUSED_DYN", 1) != 0 ? 2 : 0);
     if (a.KS > 4) return hipErrorInvalidValue;
     int rows = 0;
     for (int z = 0; z < a.nmat; ++z) rows += a.n_out[z];
@@ -940,7 +938,7 @@ static hipError_t launch_fused_nw(FusedArgs a, bool stage, hipStream_t st) {
     if constexpr (Fmt::kUnitsPerBlock == 4) {  // Q8_K activations (Q4_K, Q6_K rows)
         if (stage && a.m == 1 && a.KS == 3) return launch_fused_ks3<Fmt>(a, st);
         if (stage && a.m == 1 && a.KS > 1) {
-            static const int r_env = env_int("EXQ_FUSED_NW16_R", 0);  // tuning override: rows per slot
+            static const int r_env = tuning_knob("EXQ_FUSED_NW16_R", 0);  // rows per slot
             const int r16 = pick_r16<Fmt>(a, r_env);
             if (r16 == 1) return launch_fused_fmt<Fmt, 1, 1, 16, true, 0>(a, st);
             if (r16 == 2) return launch_fused_fmt<Fmt, 1, 2, 16, true, 0>(a, st);

@@ -25,6 +25,8 @@ hipError_t launch_gemv_q8(int type, const uint8_t *w, size_t row_bytes, int n_ou
                           size_t xq_stride, const float *bias, float *out, int ldo, hipStream_t st);
 hipError_t launch_gemv_f32(int type, const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const float *xf,
                            const float *xs, const float *bias, float *out, int ldo, hipStream_t st);
+hipError_t launch_gemv_plain(int type, const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const float *x,
+                             int ldx, const float *bias, bool bias_f64, float *out, int ldo, hipStream_t st);
 hipError_t launch_xsum16(const float *x, int m, int K, float *xs, hipStream_t st);
 hipError_t launch_rmsnorm(const float *x, const float *w, float *out, int m, int n, float eps, hipStream_t st);
 hipError_t launch_elementwise(const float *a, const float *b, float *out, long long n, int kind, hipStream_t st);
@@ -136,10 +138,11 @@ bool ensure_init() {
 // orders with the caller's other default-stream work.
 hipStream_t pick_stream(void *s) { return (hipStream_t)s; }
 
-// Every type of the reference's dispatcher but F32 (src/gguf_quant.c:69-108):
-// the Q8_0 family and the K-quants through their integer dots, F16 through
-// the f32-activation dot.
-bool gpu_type(uint32_t t) { return q8_0_family((int)t) || k_family((int)t) || t == (uint32_t)kTypeF16; }
+// Every type of the reference's dispatcher (src/gguf_quant.c:69-108): the
+// Q8_0 family and the K-quants through their integer dots, F16 and F32
+// through the f32-activation dot.
+bool plain_type(uint32_t t) { return t == (uint32_t)kTypeF16 || t == (uint32_t)kTypeF32; }
+bool gpu_type(uint32_t t) { return q8_0_family((int)t) || k_family((int)t) || plain_type(t); }
 
 size_t block_elems(uint32_t t) {
     return q8_0_family((int)t) ? (size_t)kQK8_0 : (k_family((int)t) ? (size_t)kQKK : (size_t)1);
@@ -154,13 +157,18 @@ size_t block_bytes(uint32_t t) {
         case kTypeQ5_K: return kBytesQ5_K;
         case kTypeQ6_K: return kBytesQ6_K;
         case kTypeF16: return 2;
+        case kTypeF32: return 4;
         default: return 0;
     }
 }
 
-// Elements of K one GEMV lane unit spans: a block, or 32 F16 values (the
-// F16 products need n_in % 32 == 0; dequant takes any count).
-size_t unit_elems(uint32_t t) { return t == (uint32_t)kTypeF16 ? (size_t)32 : block_elems(t); }
+// The granule of n_in the products take: a block (F16 and F32 rows of any
+// length: the tiled F16 kernel for multiples of 32, the plain kernel else).
+size_t unit_elems(uint32_t t) { return block_elems(t); }
+
+// The granule of n_embd a row gather takes: a block, or 4 plain values (the
+// gathered rows are written with 16-byte stores).
+size_t embed_unit(uint32_t t) { return plain_type(t) ? (size_t)4 : block_elems(t); }
 
 // Bytes of one token's quantized activation: Q8_0 blocks for the Q8_0
 // family, Q8_K blocks for the K-quants (src/cpu_kernel.c:577-631).
@@ -172,23 +180,18 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-// Tuning overrides: EXQ_FUSED=0 never quantizes inside the GEMV, 2 always
-// does (where the kernel covers the shape), 1 (default) by row length;
+// Tuning knobs: EXQ_FUSED=0 never quantizes inside the GEMV, 2 always does
+// (where the kernel covers the shape), 1 (default) by row length;
 // EXQ_GENERIC=1 sends every quantized-activation GEMV to the generic kernel.
-int env_int(const char *name, int dflt) {
-    const char *e = getenv(name);
-    return e != nullptr ? atoi(e) : dflt;
-}
-
 bool stage_in_kernel(uint32_t type, int K, int m) {
-    static const int mode = env_int("EXQ_FUSED", 1);
-    static const int generic = env_int("EXQ_GENERIC", 0);
+    static const int mode = tuning_knob("EXQ_FUSED", 1);
+    static const int generic = tuning_knob("EXQ_GENERIC", 0);
     if (mode == 0 || generic != 0 || !gemv_fused_supported((int)type, K, m)) return false;
     return mode == 2 || K <= kStageMaxK || (k_family((int)type) && m == 1 && K <= kStageMaxKWide);
 }
 
 bool split_gemv(uint32_t type, int K, int m) {
-    static const int generic = env_int("EXQ_GENERIC", 0);
+    static const int generic = tuning_knob("EXQ_GENERIC", 0);
     return generic == 0 && m <= kFusedMaxTokens && gemv_fused_supported((int)type, K, m);
 }
 
@@ -347,8 +350,7 @@ bool check_linear_args(const void *out, const void *x, const void *w, uint32_t t
         return false;
     }
     if (!gpu_type(type)) {
-        set_error(-3, "%s: GGUF type %u is not supported on the GPU (F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)", who,
-                  type);
+        set_error(-3, "%s: GGUF type %u is not supported (F32, F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)", who, type);
         return false;
     }
     if ((size_t)n_in % unit_elems(type) != 0) {
@@ -358,14 +360,26 @@ bool check_linear_args(const void *out, const void *x, const void *w, uint32_t t
     return true;
 }
 
-// f32-activation products (F16 rows in the batch driver; every type in the
-// per-row f32 dot and the K-quant logits): at most kGemvMaxTokens tokens per
-// launch of the generic kernel, or the fused kernel one token at a time for
-// the K-quant formats it covers.  xs: the tokens' 16-element sums of x
-// (K-quants only).
+// f32-activation products (F16 and F32 rows in the batch driver; every type
+// in the per-row f32 dot and the logits of the non-Q8_0 formats): at most
+// kGemvMaxTokens tokens per launch of the generic kernels, or the fused
+// kernel one token at a time for the K-quant formats it covers.  xs: the
+// tokens' 16-element sums of x (K-quants only).  bias_f64: F32 rows add the
+// bias in double before the final rounding (the one-token linear of
+// src/cpu_kernel.c:566-569, 462-523).
 bool run_f32_product(uint32_t type, const void *w, int n_out, int n_in, int m, const float *x, const float *xs,
-                     const float *bias, float *out, int ldo, hipStream_t st) {
+                     const float *bias, float *out, int ldo, hipStream_t st, bool bias_f64 = false) {
     const size_t rb = edgexpu_hip_row_bytes(type, n_in);
+    if (type == (uint32_t)kTypeF32 || (type == (uint32_t)kTypeF16 && n_in % 32 != 0)) {
+        for (int t0 = 0; t0 < m; t0 += kGemvMaxTokens) {
+            const int mt = m - t0 < kGemvMaxTokens ? m - t0 : kGemvMaxTokens;
+            if (!hip_ok(launch_gemv_plain((int)type, (const uint8_t *)w, rb, n_out, n_in, mt, x + (size_t)t0 * n_in,
+                                          n_in, bias, bias_f64, out + (size_t)t0 * ldo, ldo, st),
+                        "gemv_plain"))
+                return false;
+        }
+        return true;
+    }
     if (k_family((int)type) && ldo == n_out && gemv_fused_f32_supported((int)type, n_in)) {
         for (int t = 0; t < m; ++t) {
             if (!hip_ok(launch_gemv_fused_f32((int)type, (const uint8_t *)w, n_out, bias, out + (size_t)t * ldo, rb,
@@ -421,12 +435,15 @@ bool run_q8_product(uint32_t type, const void *w, int n_out, int n_in, int m, co
 bool run_linear_group(uint32_t type, int nmat, const void *const *w, const int *n_out, const float *const *bias,
                       float *const *out, const float *x, int m, int n_in, hipStream_t st) {
     const size_t rb = edgexpu_hip_row_bytes(type, n_in);
-    if (type == (uint32_t)kTypeF16) {
+    if (plain_type(type)) {
         // src/cpu_kernel.c:632-641: rows with neither activation quantizer
-        // take the f32-activation row dot, out = bias + dot per token
+        // take the f32-activation row dot, out = bias + dot per token; F32
+        // at one token is edgexpu_cpu_linear (src/cpu_kernel.c:566-569),
+        // whose sum starts at the bias in double
+        const bool f64 = type == (uint32_t)kTypeF32 && m == 1;
         for (int z = 0; z < nmat; ++z)
             if (!run_f32_product(type, w[z], n_out[z], n_in, m, x, nullptr, bias != nullptr ? bias[z] : nullptr,
-                                 out[z], n_out[z], st))
+                                 out[z], n_out[z], st, f64))
                 return false;
         return true;
     }
@@ -777,8 +794,8 @@ int edgexpu_hip_gemv_q8_dev(float *out, const uint8_t *xq, const void *w, uint32
                             int n_out, int n_in, void *stream) {
     if (!ensure_init()) return 0;
     if (!check_linear_args(out, xq, w, type, m, n_out, n_in, "gemv_q8")) return 0;
-    if (type == (uint32_t)kTypeF16) {
-        set_error(-3, "gemv_q8: F16 rows have no quantized-activation dot (src/gguf_dot_q8.c:414-434)");
+    if (plain_type(type)) {
+        set_error(-3, "gemv_q8: F16 and F32 rows have no quantized-activation dot (src/gguf_dot_q8.c:414-434)");
         return 0;
     }
     // the block scale heads every Q8_K (f32) / Q8_0 (f16) block
@@ -898,8 +915,7 @@ int edgexpu_hip_dequantize_dev(const void *src, uint32_t type, uint64_t n_elemen
         return 0;
     }
     if (!gpu_type(type)) {
-        set_error(-3, "dequantize: GGUF type %u is not supported on the GPU (F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)",
-                  type);
+        set_error(-3, "dequantize: GGUF type %u is not supported (F32, F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)", type);
         return 0;
     }
     if (n_elements % block_elems(type) != 0) {
@@ -927,13 +943,12 @@ int edgexpu_hip_embed_rows_dev(float *out, const void *table, uint32_t type, lon
         return 0;
     }
     if (!gpu_type(type)) {
-        set_error(-3, "embed_rows: GGUF type %u is not supported on the GPU (F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)",
-                  type);
+        set_error(-3, "embed_rows: GGUF type %u is not supported (F32, F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)", type);
         return 0;
     }
-    if ((size_t)n_embd % unit_elems(type) != 0 || !aligned16(out)) {
+    if ((size_t)n_embd % embed_unit(type) != 0 || !aligned16(out)) {
         set_error(-2, "embed_rows: n_embd=%d must be a multiple of %zu for type %u and out 16-byte aligned", n_embd,
-                  unit_elems(type), type);
+                  embed_unit(type), type);
         return 0;
     }
     return hip_ok(launch_dequantize_rows((const uint8_t *)table, (int)type, n_rows, n_embd, ids, n_ids, out, bad,

@@ -9,6 +9,7 @@ Distributions (the workloads' definitions):
   Q4_0, Q5_0  d = fp16(|N(0, 0.02)| / 16); qs (and Q5_0's qh) bytes uniform
   Q5_K  as Q4_K, with the 32 qh bytes uniform
   F16   N(0, 0.02) rounded to fp16
+  F32   N(0, 0.02)
   activations f32 N(0, 1)
 
 ``np_*`` functions build host arrays with numpy's PCG64 (tests); ``torch_*``
@@ -20,7 +21,7 @@ from __future__ import annotations
 
 import numpy as np
 
-F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 1, 2, 6, 8, 12, 13, 14
+F32, F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 2, 6, 8, 12, 13, 14
 
 
 def _f16_bytes(a: np.ndarray) -> np.ndarray:
@@ -52,6 +53,8 @@ def np_weights(qtype: int, rows: int, n: int, rng: np.random.Generator) -> np.nd
         return np.concatenate([d, q], axis=2).reshape(rows, nb * (2 + nq))
     if qtype == F16:
         return _f16_bytes(rng.normal(0.0, 0.02, (rows, n))).reshape(rows, 2 * n)
+    if qtype == F32:
+        return np.ascontiguousarray(rng.normal(0.0, 0.02, (rows, n)).astype(np.float32)).view(np.uint8)
     if qtype == Q6_K:
         nb = n // 256
         qlh = rng.integers(0, 256, (rows, nb, 192), dtype=np.int16).astype(np.uint8)
@@ -95,6 +98,8 @@ def torch_weights(qtype: int, rows: int, n: int, generator, device="cuda"):
         return torch.cat([d.view(rows, nb, 2), q], dim=2).reshape(rows, nb * (2 + nq))
     if qtype == F16:
         return f16b(torch.randn((rows, n), generator=generator, device=device) * 0.02).reshape(rows, 2 * n)
+    if qtype == F32:
+        return (torch.randn((rows, n), generator=generator, device=device) * 0.02).view(torch.uint8)
     if qtype == Q6_K:
         nb = n // 256
         qlh = torch.randint(0, 256, (rows, nb, 192), generator=generator, device=device, dtype=torch.uint8)

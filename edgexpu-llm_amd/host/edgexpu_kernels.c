@@ -194,7 +194,7 @@ int edgexpu_gguf_dequantize(const uint8_t *src, uint32_t type, uint64_t n_elemen
         return 0;
     }
     if (!edgexpu_hip_supports_type(type)) {
-        snprintf(msg, sizeof(msg), "GGUF type %u is not on the GPU path (F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)", type);
+        snprintf(msg, sizeof(msg), "GGUF type %u is not supported (F32, F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)", type);
         set_msg(error, error_size, msg);
         return 0;
     }
@@ -338,11 +338,8 @@ void edgexpu_cpu_linear_quant_batch(float *out, const float *x, const uint8_t *w
     if (edgexpu_gguf_row_bytes(type, n_in) == 0) {
         return; /* src/cpu_kernel.c:571-574 */
     }
-    if (!edgexpu_hip_supports_type(type)) {
-        /* refuse explicitly: the caller keeps its CPU kernel for this type */
-        edgexpu_hip_linear_quant_batch_host(out, x, weight, type, bias, m, n_out, n_in);
-        return;
-    }
+    /* every type with a row layout runs on the GPU, F32 included (its
+     * one-token sum starts at the bias in double, src/cpu_kernel.c:566-569) */
     e = reg_find(weight);
     if (e != NULL && e->type == type && e->n_out == n_out && e->n_in == n_in && e->bias == bias) {
         edgexpu_hip_linear_quant_batch(out, x, e->w, m);

@@ -1,7 +1,7 @@
 /*
  * edgexpu_hip.h -- C-ABI of libedgexpu_hip.so, the MI355X (gfx950) kernel set
  * for the GGUF quantized-weight matrix path (Q8_0 / Q4_K / Q6_K, and the
- * dispatcher's other formats Q4_0 / Q5_0 / Q5_K / F16).
+ * dispatcher's other formats Q4_0 / Q5_0 / Q5_K / F16 / F32).
  *
  * Plain C types only (no HIP or torch types): device pointers are `void *` /
  * typed pointers into device memory, streams are `void *` holding a
@@ -18,9 +18,10 @@
  *  - Single caller: like the reference path (process-global activation
  *    scratch, src/cpu_kernel.c:525-543) the library keeps one device, one
  *    stream and one workspace per process and is not reentrant.
- *  - Type ids are GGUF's (include/edgexpu/gguf_quant.h:17-24).  Only Q8_0 (8),
- *    Q4_K (12) and Q6_K (14) run on the GPU; any other type is reported as
- *    unsupported so the caller can route it to its CPU kernels.
+ *  - Type ids are GGUF's (include/edgexpu/gguf_quant.h:17-24).  Every type
+ *    of the reference's dispatcher runs on the GPU: F32 (0), F16 (1),
+ *    Q4_0 (2), Q5_0 (6), Q8_0 (8), Q4_K (12), Q5_K (13), Q6_K (14); any other
+ *    id is rejected as unsupported.
  */
 #ifndef EDGEXPU_HIP_H
 #define EDGEXPU_HIP_H
@@ -48,10 +49,10 @@ void edgexpu_hip_shutdown(void);
  * message into buf.  The error stays set until edgexpu_hip_clear_error(). */
 int edgexpu_hip_last_error(char *buf, size_t size);
 void edgexpu_hip_clear_error(void);
-/* 1 when `type` runs on the GPU: every type of the reference's dispatcher but
- * F32 (src/gguf_quant.c:69-108; src/gguf_dot_q8.c:414-434): Q4_0, Q5_0, Q8_0
- * with Q8_0 activations, Q4_K, Q5_K, Q6_K with Q8_K activations, F16 with
- * f32 activations (its products need n_in % 32 == 0). */
+/* 1 when `type` runs on the GPU: every type of the reference's dispatcher
+ * (src/gguf_quant.c:69-108; src/gguf_dot_q8.c:414-434): Q4_0, Q5_0, Q8_0
+ * with Q8_0 activations, Q4_K, Q5_K, Q6_K with Q8_K activations, F16 and F32
+ * with f32 activations (any n_in). */
 int edgexpu_hip_supports_type(uint32_t type);
 /* Prefill (m >= 64 tokens, Q4_K) arithmetic.  No reference counterpart: the
  * reference has one CPU path.
@@ -102,8 +103,10 @@ int edgexpu_hip_weight_n_in(const edgexpu_hip_weight *w);
 /* out[t*n_out + o] = bias[o] + dot(W[o], q8(x[t]))  for t < m.
  * Replaces edgexpu_cpu_linear_quant_batch (include/edgexpu/cpu_kernel.h:71-80,
  * src/cpu_kernel.c:545-644): activations are quantized once per token
- * (Q8_0 for Q8_0 weights, Q8_K for Q4_K/Q6_K) and every row is dotted with
- * the integer block kernels.  x is [m][n_in] f32, out [m][n_out] f32, both
+ * (Q8_0 for the Q8_0 family, Q8_K for the K-quants) and every row is dotted
+ * with the integer block kernels; F16 and F32 rows take the f32-activation
+ * dot (F32 at m == 1 adds the bias in double, as edgexpu_cpu_linear,
+ * src/cpu_kernel.c:462-523).  x is [m][n_in] f32, out [m][n_out] f32, x
  * 16-byte aligned; bias may be NULL. */
 int edgexpu_hip_linear_quant_batch_dev(float *out, const float *x, const void *w, uint32_t type,
                                        const float *bias, int m, int n_out, int n_in, void *stream);
@@ -167,7 +170,8 @@ int edgexpu_hip_dequantize_dev(const void *src, uint32_t type, uint64_t n_elemen
  * the greedy argmax of the previous step); an id outside [0, n_rows) gives a
  * row of zeros and, when `bad` (device int) is non-null, stores 1 into it
  * (the reference reports "row out of range").  n_embd a multiple of the
- * type's block (32 for F16); 1 <= n_ids <= 65535. */
+ * type's block (of 4 for F16 and F32, whose rows are written with 16-byte
+ * stores); 1 <= n_ids <= 65535. */
 int edgexpu_hip_embed_rows_dev(float *out, const void *table, uint32_t type, long long n_rows, int n_embd,
                                const int32_t *ids, int n_ids, int *bad, void *stream);
 

@@ -7,10 +7,13 @@
  * include/edgexpu/gguf_quant.h links against this library instead of
  * src/cpu_kernel.c + src/gguf_quant.c + src/gguf_dot_q8.c.  Every compute
  * entry runs on the GPU through libedgexpu_hip.so; nothing here computes on
- * the CPU.  Every type of the reference's dispatcher runs on the GPU except
- * F32 rows (and F16 products with n % 32 != 0), which are refused (void
- * entries leave `out` untouched, others return 0 / 0.0f) with a sticky error
- * naming the type, so the host routes them to its CPU kernels.
+ * the CPU.  Every type of the reference's dispatcher runs on the GPU: F32,
+ * F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K and Q6_K, rows of any length the type's
+ * block allows.  What the reference silently ignores (NULL buffers,
+ * non-positive sizes, unknown types, lengths that are not whole blocks) is
+ * ignored here too: void entries leave `out` untouched, the others return
+ * 0 / 0.0f, and a sticky error readable with edgexpu_hip_last_error() names
+ * the cause.
  *
  * The row entry points take the reference's edgexpu_gguf_tensor
  * (include/edgexpu/gguf.h:21-27).  Hosts that include that header include it
@@ -101,9 +104,15 @@ int edgexpu_gguf_quantize_q8_0(const float *x, int n, uint8_t *dst);
 int edgexpu_gguf_quantize_q8_k(const float *x, int n, uint8_t *dst);
 
 /* include/edgexpu/gguf_quant.h:72-77,90-102 (src/gguf_quant.c:894-918,
- * src/gguf_dot_q8.c:1004-1044): one row per call, on the GPU.  Correct, but a
- * device round trip per row; batch rows with edgexpu_hip_dot_*_rows or the
- * linear entry points instead. */
+ * src/gguf_dot_q8.c:1004-1044): one row per call, on the GPU.  Correct, but
+ * each call is a device round trip: two host-to-device copies, one launch,
+ * one device-to-host copy and a stream synchronisation: 32-41 us per call
+ * measured on MI355X for Q8_0 [576], Q6_K [2560], F32 and Q4_K [4096] rows,
+ * whatever the row length (a 4096-element Q4_K row is about 1 us of one CPU
+ * core's work).  A loop over the rows of a matrix (the
+ * reference's logit_score, src/native.c:500-514) belongs on
+ * edgexpu_hip_logits / edgexpu_hip_dot_*_rows or the linear entry points,
+ * which take all rows in one call. */
 float edgexpu_gguf_dot_quant(uint32_t type, const uint8_t *row, const float *x, int n);
 float edgexpu_gguf_dot_quant_q8(uint32_t type, const uint8_t *wrow, const uint8_t *x_q8, int n);
 float edgexpu_gguf_dot_quant_q8k(uint32_t type, const uint8_t *wrow, const uint8_t *x_q8k, int n);
@@ -122,7 +131,11 @@ void edgexpu_cpu_linear_quant_batch(float *out, const float *x, const uint8_t *w
  * place; and include/edgexpu/cpu_kernel.h:86-94 (src/cpu_kernel.c:762-849):
  * softmax in place, then one draw (top_p in (0,1): nucleus) with the
  * reference's xorshift state *rng.  Returns 0 on bad arguments, 1 otherwise.
- * Computed on the GPU. */
+ * Computed on the GPU, for n <= 2^24 (16 777 216, a vocabulary 100 times the
+ * largest in use): a larger n, or a failing GPU call, leaves io / logits as
+ * given (edgexpu_cpu_softmax cannot return a status; the sticky error of
+ * edgexpu_hip_last_error() names the cause) and edgexpu_cpu_sample_softmax
+ * returns 0, where the reference would normalise. */
 void edgexpu_cpu_softmax(float *io, int n);
 int edgexpu_cpu_sample_softmax(float *logits, int n, float top_p, uint64_t *rng, uint32_t *out);
 

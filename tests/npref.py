@@ -121,6 +121,8 @@ def dequant(qtype: int, src: np.ndarray) -> np.ndarray:
         return (prod - ms[:, sub]).astype(f32).reshape(-1)
     if qtype == 1:
         return np.ascontiguousarray(src).view(np.float16).astype(f32).reshape(-1)
+    if qtype == 0:
+        return np.ascontiguousarray(src).view(f32).reshape(-1)
     raise ValueError(qtype)
 
 
@@ -336,7 +338,7 @@ def draw(p, top_p, rng_after):
     else:
         order = ids
     c = np.cumsum(p[order].astype(np.float64))
-    if not c[-1] > 0.0:
+    if c[-1] <= 0.0:  # a NaN sum falls through: no position reaches it, the last is drawn
         return int(order[0])
     hit = np.nonzero(c >= u * c[-1])[0]
     return int(order[hit[0]]) if hit.size else int(order[-1])

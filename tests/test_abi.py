@@ -70,12 +70,13 @@ def test_layout_helpers_match_oracle(ora):
 
 def test_hip_host_helpers_without_gpu():
     L = E.HipLib()
-    # every type of the reference's dispatcher but F32 (src/gguf_quant.c:69-108)
-    assert [t for t in range(16) if L.supports_type(t)] == [1, 2, 6, 8, 12, 13, 14]
+    # every type of the reference's dispatcher (src/gguf_quant.c:69-108)
+    assert [t for t in range(16) if L.supports_type(t)] == [0, 1, 2, 6, 8, 12, 13, 14]
     assert L.row_bytes(12, 4096) == 2304 and L.row_bytes(14, 9728) == 7980 and L.row_bytes(8, 576) == 612
     assert L.row_bytes(2, 576) == 324 and L.row_bytes(6, 1536) == 1056 and L.row_bytes(13, 2560) == 1760
     assert L.row_bytes(1, 576) == 1152 and L.row_bytes(1, 7) == 14
-    assert L.row_bytes(12, 100) == 0 and L.row_bytes(2, 48) == 0 and L.row_bytes(0, 64) == 0
+    assert L.row_bytes(0, 64) == 256 and L.row_bytes(0, 7) == 28
+    assert L.row_bytes(12, 100) == 0 and L.row_bytes(2, 48) == 0 and L.row_bytes(5, 64) == 0
 
 
 def test_layer_kind_projection_tables():
@@ -176,3 +177,20 @@ def test_sampling_argument_checks_without_gpu():
     lib.edgexpu_cpu_softmax(None, 4)
     lib.edgexpu_cpu_softmax(p, 0)
     assert st.value == 5 and out.value == 9 and np.array_equal(io, np.ones(4, np.float32))
+
+
+def test_registry_refusals_without_gpu():
+    """edgexpu_kernels_register_weight refuses a NULL weight before any device
+    work; lookup and unregister of a pointer never registered find nothing."""
+    k = C.CDLL(E.KERNELS_SO)
+    k.edgexpu_kernels_register_weight.restype = C.c_int
+    k.edgexpu_kernels_register_weight.argtypes = [C.c_void_p, C.c_uint32, C.c_int, C.c_int, C.c_void_p]
+    k.edgexpu_kernels_unregister_weight.restype = C.c_int
+    k.edgexpu_kernels_unregister_weight.argtypes = [C.c_void_p]
+    k.edgexpu_kernels_lookup_weight.restype = C.c_void_p
+    k.edgexpu_kernels_lookup_weight.argtypes = [C.c_void_p]
+    assert k.edgexpu_kernels_register_weight(None, 12, 4, 256, None) == 0
+    buf = C.create_string_buffer(16)
+    assert k.edgexpu_kernels_lookup_weight(C.addressof(buf)) is None
+    assert k.edgexpu_kernels_unregister_weight(C.addressof(buf)) == 0
+    assert k.edgexpu_kernels_unregister_weight(None) == 0

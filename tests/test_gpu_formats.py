@@ -1,4 +1,4 @@
-"""GPU parity of the dispatcher's other formats (Q4_0, Q5_0, Q5_K, F16), of
+"""GPU parity of the dispatcher's other formats (Q4_0, Q5_0, Q5_K, F16, F32), of
 the f32-activation row dots of every format, and of the reference-named
 drop-in library (libedgexpu_kernels.so) called with host buffers.
 
@@ -6,7 +6,7 @@ Bars as for the main formats: dequant bit-exact against the oracle (which is
 bit-exact against the reference build and its fixtures); integer block sums
 exact (unit-scale end-to-end check); fp32 outputs within TOL of the row's
 conditioning scale S (sum of |block terms| for the quantized-activation dots,
-sum |w_k x_k| for the f32-activation ones).
+sum |w_k x_k| for the f32-activation ones: F16 and F32 rows).
 """
 import ctypes as C
 
@@ -23,8 +23,8 @@ pytestmark = pytest.mark.gpu
 
 TOL = 1e-5
 DEV = "cuda:0"
-F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 1, 2, 6, 8, 12, 13, 14
-TN = {1: "f16", 2: "q4_0", 6: "q5_0", 8: "q8_0", 12: "q4_k", 13: "q5_k", 14: "q6_k"}
+F32, F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 2, 6, 8, 12, 13, 14
+TN = {0: "f32", 1: "f16", 2: "q4_0", 6: "q5_0", 8: "q8_0", 12: "q4_k", 13: "q5_k", 14: "q6_k"}
 Q80_FAMILY = (Q4_0, Q5_0, Q8_0)
 MORE = [F16, Q4_0, Q5_0, Q5_K]
 
@@ -38,11 +38,11 @@ def dev(a):
 
 
 def scales(qt, w, x):
-    """S[t, i]: block-term scale (quantized activations) or sum |w x| (F16)."""
+    """S[t, i]: block-term scale (quantized activations) or sum |w x| (F16, F32)."""
     m = x.shape[0]
     S = np.zeros((m, w.shape[0]))
     for t in range(m):
-        if qt == F16:
+        if qt in (F16, F32):
             for i in range(w.shape[0]):
                 S[t, i] = npref.f32_dot_f64(qt, w[i], x[t])[1]
             continue
@@ -115,7 +115,8 @@ def test_linear_golden(hipdev, golden, name):
 @pytest.mark.parametrize("qt,n_in,n_out", [(Q4_0, 576, 577), (Q4_0, 4096, 301), (Q4_0, 32, 65), (Q5_0, 1536, 300),
                                            (Q5_0, 64, 129), (Q5_K, 2560, 515), (Q5_K, 4096, 1001),
                                            (Q5_K, 14336, 130), (Q5_K, 256, 70), (F16, 576, 300), (F16, 4096, 129),
-                                           (F16, 32, 17)])
+                                           (F16, 32, 17), (F16, 40, 65), (F16, 1001, 64), (F32, 1000, 300),
+                                           (F32, 4096, 129), (F32, 7, 33), (F32, 4099, 70)])
 @pytest.mark.parametrize("m", [1, 2, 3, 5, 8, 11])
 def test_linear_random_vs_oracle(hipdev, ora, qt, n_in, n_out, m):
     rng = np.random.default_rng(qt * 1000 + n_in + n_out + m)
@@ -196,10 +197,11 @@ def test_f32_row_dots_golden(hipdev, golden, name):
 
 
 @pytest.mark.parametrize("qt,n,vocab", [(Q4_0, 576, 20001), (Q5_0, 1536, 3000), (Q5_K, 2560, 15001),
-                                        (F16, 576, 5000)])
+                                        (F16, 576, 5000), (F32, 2560, 9001), (F32, 1000, 300)])
 def test_logits_and_argmax(hipdev, ora, qt, n, vocab):
     """Logits of the other formats: the Q8_0 family against the Q8_0-quantized
-    hidden vector, Q5_K and F16 against f32 (src/native.c:2317-2319, 445-514)."""
+    hidden vector, Q5_K, F16 and F32 against f32 (src/native.c:2317-2319,
+    445-514)."""
     rng = np.random.default_rng(qt + vocab)
     w = synth.np_weights(qt, vocab, n, rng)
     h = rng.normal(0, 1, n).astype(np.float32)
@@ -207,7 +209,7 @@ def test_logits_and_argmax(hipdev, ora, qt, n, vocab):
     want, want_best = ora.logits(h, w, qt, bias, vocab, n, 0)
     scores, best = E.logits(dev(w), qt, dev(h[None, :]), vocab, n, bias=dev(bias))
     got = scores.cpu().numpy()[0]
-    sample = rng.choice(vocab, 200, replace=False)
+    sample = rng.choice(vocab, min(vocab, 200), replace=False)
     S = scales(qt, w[sample], h[None, :])[0] + np.abs(bias[sample])
     assert_tol(got[sample], want[sample], S, f"{TN[qt]} sampled rows")
     assert np.abs(got - want).max() <= TOL * S.max() * 4
@@ -251,10 +253,13 @@ def _p(a, t):
 
 @pytest.mark.parametrize("qt,n_in,n_out,m", [(Q8_0, 576, 70, 2), (Q4_K, 4096, 33, 1), (Q6_K, 2560, 40, 3),
                                              (Q4_0, 576, 65, 2), (Q5_0, 1536, 30, 1), (Q5_K, 2560, 41, 4),
-                                             (F16, 576, 37, 3)])
+                                             (F16, 576, 37, 3), (F16, 100, 9, 2), (F32, 1000, 37, 1),
+                                             (F32, 4096, 20, 3), (F32, 7, 9, 1), (F32, 2560, 33, 9)])
 def test_dropin_linear_quant_batch(kern, ora, qt, n_in, n_out, m):
     """edgexpu_cpu_linear_quant_batch (src/cpu_kernel.c:545-644) through the
-    drop-in set: host pointers, the weight uploaded inside the call."""
+    drop-in set: host pointers, the weight uploaded inside the call.  F32 at
+    one token is edgexpu_cpu_linear (bias added in double), at several tokens
+    bias + the f32 row dot; both are written, never left untouched."""
     rng = np.random.default_rng(5000 + qt + n_in + m)
     w = np.ascontiguousarray(synth.np_weights(qt, n_out, n_in, rng))
     x = np.ascontiguousarray(synth.np_activations(m, n_in, rng))
@@ -266,7 +271,7 @@ def test_dropin_linear_quant_batch(kern, ora, qt, n_in, n_out, m):
     assert_tol(out, want, scales(qt, w, x) + np.abs(bias)[None, :], f"drop-in {TN[qt]}")
 
 
-@pytest.mark.parametrize("qt", [Q8_0, Q4_K, Q6_K] + MORE)
+@pytest.mark.parametrize("qt", [Q8_0, Q4_K, Q6_K, F32] + MORE)
 def test_dropin_dequant_and_row_dots(kern, ora, qt):
     """edgexpu_gguf_dequantize bit-exact; edgexpu_gguf_dot_quant (f32 x) and
     edgexpu_gguf_dot_quant_q8 / _q8k (quantized x) within the bound, each on
@@ -283,9 +288,9 @@ def test_dropin_dequant_and_row_dots(kern, ora, qt):
     want = ora.dot_f32(qt, w, x, n)
     fv, fs = npref.f32_dot_f64(qt, w, x)
     assert abs(got - want) <= TOL * fs, (got, want)
-    if qt == F16:
+    if qt in (F16, F32):
         xq = np.zeros(ora_q8_bytes(n), np.uint8)
-        assert kern.edgexpu_gguf_dot_quant_q8(qt, _p(w, _u8p), _p(xq, _u8p), n) == 0.0  # no Q8 dot for F16
+        assert kern.edgexpu_gguf_dot_quant_q8(qt, _p(w, _u8p), _p(xq, _u8p), n) == 0.0  # no Q8 dot for F16/F32
         return
     if qt in Q80_FAMILY:
         xq = np.zeros(n // 32 * 34, np.uint8)
@@ -309,22 +314,27 @@ def ora_q8_bytes(n):
 
 
 def test_unsupported_shapes_are_refused(hipdev):
-    """F32 rows stay on the host's own kernels; F16 products need n_in % 32 == 0."""
+    """Every type of the reference's dispatcher runs on the GPU (F32 and F16
+    rows of any length); unknown ids and lengths that are not whole blocks
+    are refused before any launch."""
     lib = E.hip()
-    assert lib.supports_type(0) == 0
-    for t in (1, 2, 6, 8, 12, 13, 14):
+    for t in (0, 1, 2, 6, 8, 12, 13, 14):
         assert lib.supports_type(t) == 1
+    for t in (3, 4, 5, 7, 9, 10, 11, 15, 16, 30):
+        assert lib.supports_type(t) == 0
     w = dev(np.zeros((4, 2 * 40), np.uint8))
     x = dev(np.zeros((1, 40), np.float32))
     with pytest.raises(E.HipError):
-        E.linear_quant_batch(w, F16, x, 4, 40)
+        E.linear_quant_batch(w, Q4_K, x, 4, 40)     # not whole super-blocks
+    with pytest.raises(E.HipError):
+        E.linear_quant_batch(w, Q8_0, x, 4, 40)     # not whole blocks
 
 
 # ------------------------------------------------------------------ embedding rows
 
 
 @pytest.mark.parametrize("qt,n_embd", [(Q8_0, 576), (Q4_0, 2048), (Q5_0, 96), (Q4_K, 4096), (Q5_K, 2560),
-                                       (Q6_K, 2560), (F16, 160)])
+                                       (Q6_K, 2560), (F16, 160), (F16, 44), (F32, 100), (F32, 2048)])
 def test_embed_rows_bit_exact(hipdev, ora, qt, n_embd):
     """Rows gathered by device ids (duplicates, first and last row) equal the
     oracle's dequant of those rows bit for bit; an id out of range gives a
@@ -350,9 +360,11 @@ def test_embed_rows_rejects_bad_shapes(hipdev):
     t = dev(np.zeros((4, 2 * 40), np.uint8))
     ids = dev(np.zeros(2, np.int32))
     with pytest.raises(E.HipError):
-        E.embed_rows(t, F16, 4, 40, ids)      # F16 rows need n_embd % 32 == 0
+        E.embed_rows(t, F16, 4, 42, ids)      # F16 rows need n_embd % 4 == 0
     with pytest.raises(E.HipError):
-        E.embed_rows(t, 0, 4, 32, ids)       # F32 tables stay on the host
+        E.embed_rows(t, F32, 4, 18, ids)      # F32 rows too
+    with pytest.raises(E.HipError):
+        E.embed_rows(t, Q4_K, 4, 40, ids)     # not whole super-blocks
 
 
 @pytest.mark.parametrize("qt,n_embd", [(Q8_0, 576), (Q4_K, 2560), (Q6_K, 256), (Q5_0, 64), (F16, 96)])
