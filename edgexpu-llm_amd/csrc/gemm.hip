@@ -40,18 +40,30 @@
 // instructions per 8 weights, and each A operand is one conflict-free
 // ds_read_b128 (the pack is already in lane order).
 //
-// Tiling: a workgroup of 8 waves (two per SIMD) computes 128 tokens x 128
-// rows; wave w owns rows 32 (w % 4) .. + 31 for tokens 64 (w / 4) .. + 63 (2
-// tiles of 32 x 32), and the two chains advance together, each weight
-// operand feeding both.  The activation pack of a super-block (69 KiB for the
-// 128 tokens) goes global -> LDS with buffer_load ... lds (no registers, no
-// address arithmetic) into one of two stages while the other is computed;
-// the weight bytes go straight to registers, one super-block ahead.  The two
-// stages are distinct LDS objects and the loop names them statically, so the
-// compiler sees that a super-block's reads never touch the stage in flight
-// (otherwise it waits for every outstanding load before the first read).
-// Two waves per SIMD double the LDS read rate a single wave sustains and
-// let one wave's VALU work run beside the other's MFMAs.
+// Budget that shapes the tiling (measured on MI355X): a 32x32x16 fp16 MFMA
+// occupies its SIMD for 32 cycles and hides only ~4 independent VALU
+// instructions; every VALU instruction beyond that adds its own 4 cycles.
+// LDS serves ~155 B per clock per CU.  So every dequantized weight operand
+// (9 VALU) must feed several MFMAs, and every 1 KB activation operand read
+// from LDS at least one:
+//   * a workgroup of 8 waves (two per SIMD) computes 256 rows x 128 tokens;
+//     wave w owns rows 32 w .. + 31 for all 128 tokens (4 tiles of 32 x 32),
+//     so each weight operand feeds 4 MFMAs and the combination costs
+//     48 VALU per tile and super-block: ~5.7 VALU per MFMA in all;
+//   * the activation pack of a half super-block (128 tokens x 128 K, 32 KiB)
+//     goes global -> LDS with buffer_load ... lds into a ring of 4 slots,
+//     requested two half super-blocks ahead (plus a 5 KiB block of bsums, d
+//     and sum |q8| per super-block, in a ring of 2); the weight bytes go
+//     straight to registers, one super-block ahead.  One barrier per half
+//     super-block, each wave waiting only for the loads of the slot it is
+//     about to read.  The slots are distinct LDS objects named statically
+//     (the loop is unrolled over the ring), so the compiler sees that reads
+//     never touch a slot in flight.
+// Shapes whose tiles cannot fill the chip split K over up to 4 workgroups
+// per tile; each writes its partial tile, and the last to arrive (counted
+// with a device-scope atomic) adds the partials in split order and the bias,
+// so the result does not depend on which workgroup finishes last, and
+// resets the counter for the next launch.
 //
 // MFMA operand layout (v_mfma_f32_32x32x16_f16): lane l supplies row l % 32
 // of A (a token) and column l % 32 of B (a weight row), K slots
@@ -69,61 +81,41 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void;
 
-// Raw buffer resource over [base, base + bytes): loads past the end read 0.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
-}
-
-// Activation pack: per (super-block, tile of 32 tokens) one block of
-constexpr int kPkA = 16 * 64 * 16;                      // fp16 codes [K-step][MFMA lane][8]
-constexpr int kPkMn = 64 * 16;                          // fp16 bsums [MFMA lane][8]
-constexpr int kPkDx = 32 * 4;                           // f32 d per token
-constexpr int kPkSq = 32 * 4;                           // int32 sum |q8| per token
-constexpr int kPkTile = kPkA + kPkMn + kPkDx + kPkSq;  // 17664 bytes
-constexpr int kGmTiles = 4;                             // token tiles per workgroup (128 tokens)
-constexpr int kWvTiles = 2;                             // token tiles per wave (64 tokens)
-constexpr int kGmRows = 128;                            // rows per workgroup (4 row quarters of 32)
-constexpr int kGmThreads = 512;                         // 8 waves: 4 row quarters x 2 token halves
-constexpr int kGmStage = kGmTiles * kPkTile;            // 70656 bytes = 69 KiB
-constexpr int kGmChunks = kGmStage / 1024;              // 1 KiB DMA chunks per stage
-constexpr int kGmLds = 2 * kGmStage;                    // 141312 bytes
-static_assert(kGmStage % 1024 == 0, "whole 1 KiB DMA chunks");
-static_assert(kGmLds <= 160 * 1024, "two activation stages in the gfx950 LDS");
+constexpr int kTiles = 4;                 // MFMA token tiles of 32 per workgroup
+constexpr int kTokB = 32 * kTiles;        // 128 tokens per workgroup
+constexpr int kWaves = 8;                 // two per SIMD
+constexpr int kRowsB = 32 * kWaves;       // 256 weight rows per workgroup
+constexpr int kThreads = 64 * kWaves;
+// Activation pack, one block per (super-block, 128-token block):
+//   codes  [half 2][K-step 8][tile 4][MFMA lane 64][8 fp16]   64 KiB
+//   mn     [tile 4][MFMA lane 64][8 fp16]  bsums for the min term
+//   dx     [128] f32, sq [128] int32 (sum |q8| of the super-block)
+constexpr int kPkHalf = 8 * kTiles * 1024;        // 32768
+constexpr int kPkCodes = 2 * kPkHalf;
+constexpr int kPkMn = kTiles * 1024;
+constexpr int kPkDx = kTokB * 4;
+constexpr int kPkSq = kTokB * 4;
+constexpr int kPkExtra = kPkMn + kPkDx + kPkSq;   // 5120
+constexpr int kPkBlk = kPkCodes + kPkExtra;       // 70656
+constexpr int kHalfChunks = kPkHalf / 1024;       // 1 KiB DMA chunks per half
+constexpr int kExtraChunks = kPkExtra / 1024;
+static_assert(kHalfChunks == 4 * kWaves, "four code chunks per wave and half super-block");
+static_assert(kExtraChunks <= kWaves && kPkExtra % 1024 == 0, "one extras chunk per wave at most");
 // largest sum |q8| of a token for which one chain of 256 products is exact:
 // 17753 * 945 < 2^24
 constexpr int kExactSqMax = 16777215 / 945;
+constexpr int kMaxSplit = 4;
+constexpr int kGemmCounters = 1024;               // arrival counters in the workspace
 
 // --------------------------------------------------------------- packing
 
-// Writes one token's super-block into the pack from the codes a lane owns
-// (elements 4l .. 4l+3), its 16-element sum (lanes 4i), d and sum |q8|.
 __device__ __forceinline__ uint32_t h2_bits(int lo, int hi) {
     const _Float16 l = (_Float16)(float)lo, h = (_Float16)(float)hi;
     return (uint32_t)__builtin_bit_cast(uint16_t, l) | ((uint32_t)__builtin_bit_cast(uint16_t, h) << 16);
 }
 
-__device__ __forceinline__ void pack_store(uint8_t *tile, int tl, int lane, const int q[4], int bsum, float d,
-                                           int sq) {
-    const int j = lane >> 4;                  // 64-element chunk = 32-byte qs group
-    const int nib = (lane >> 3) & 1;          // elements 32..63 of the chunk: high nibbles
-    const int s = 8 * (j & 1) + (lane & 7);   // K-step
-    const int L = tl + 32 * (j >> 1);         // MFMA lane
-    uint8_t *dst = tile + s * 1024 + L * 16;
-    *reinterpret_cast<uint32_t *>(dst + 4 * nib) = h2_bits(q[0], q[2]);
-    *reinterpret_cast<uint32_t *>(dst + 8 + 4 * nib) = h2_bits(q[1], q[3]);
-    if ((lane & 3) == 0) {
-        const int i = lane >> 2;  // bsum index
-        const _Float16 b = (_Float16)(float)bsum;
-        *reinterpret_cast<uint16_t *>(tile + kPkA + (tl + 32 * (i >> 3)) * 16 + (i & 7) * 2) =
-            __builtin_bit_cast(uint16_t, b);
-    }
-    if (lane == 0) {
-        *reinterpret_cast<float *>(tile + kPkA + kPkMn + 4 * tl) = d;
-        *reinterpret_cast<int *>(tile + kPkA + kPkMn + kPkDx + 4 * tl) = sq;
-    }
-}
+__device__ __forceinline__ int sbyte(uint32_t w, int b) { return (int)(int8_t)((w >> (8 * b)) & 0xffu); }
 
 __device__ __forceinline__ int wave_sum(int v) {
 #pragma unroll
@@ -131,115 +123,193 @@ __device__ __forceinline__ int wave_sum(int v) {
     return v;
 }
 
-// One wavefront per (token, super-block) of the padded token range: the
-// Q8_K quantization (bit-identical to quantize_q8_k_kernel) written in pack
-// order; tokens past m get zero codes and d = 0.
-__global__ __launch_bounds__(256) void q8k_pack_f32_kernel(const float *__restrict__ x, int m, int K, int ldx,
-                                                           int mp, uint8_t *__restrict__ pack) {
-    const int nb = K / kQKK;
-    const int lane = threadIdx.x & 63;
-    const long long g = ((long long)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    if (g >= (long long)mp * nb) return;  // wavefront-uniform
-    const int t = (int)(g % mp), sb = (int)(g / mp);
-    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (t < m) v = *reinterpret_cast<const float4 *>(x + (size_t)t * ldx + (size_t)sb * kQKK + lane * 4);
-    const Q8KLane r = q8k_quantize_lane(v, lane);
-    int bsum = r.sum4;
-    bsum += __shfl_xor(bsum, 1, 64);
-    bsum += __shfl_xor(bsum, 2, 64);
-    const int sq = wave_sum(abs(r.q[0]) + abs(r.q[1]) + abs(r.q[2]) + abs(r.q[3]));
-    uint8_t *tile = pack + ((size_t)sb * (mp / 32) + (t >> 5)) * kPkTile;
-    pack_store(tile, t & 31, lane, r.q, bsum, r.d, sq);
-}
+constexpr int kPackTokensPerWave = 1;
+constexpr int kPackWaves = 4;  // consecutive tokens of one super-block per workgroup
 
-// The same pack from Q8_K block bytes already in memory (token t at
-// xq + t * xq_stride): the block's own d, codes and 16-element sums.
-__global__ __launch_bounds__(256) void q8k_pack_q8k_kernel(const uint8_t *__restrict__ xq, size_t xq_stride, int m,
-                                                           int K, int mp, uint8_t *__restrict__ pack) {
+// The pack kernel: one wavefront per (super-block, token), 4 wavefronts (4
+// consecutive tokens, whose 16-byte vectors share 64-byte segments) per
+// workgroup, everything in registers.  Per token the wave quantizes the
+// block (Q8_K, bit-identical to quantize_q8_k_kernel) or reads its Q8_K
+// bytes; lane l then holds elements 4l .. 4l+3.  The 16-byte code vector of
+// (half hf, K-step s, lane half h) holds elements 64 j + 4 s .. + 3 (low
+// nibble positions, lane 16 j + s) and 64 j + 32 + 4 s .. + 3 (high, lane
+// 16 j + 8 + s) with j = 2 h + hf, so lane 16 j + s writes it after one
+// exchange with lane 16 j + s + 8.  Tokens past m get zero codes and d = 0.
+template <bool F32IN>
+__global__ __launch_bounds__(256) void q8k_pack_kernel(const float *__restrict__ x, int ldx,
+                                                       const uint8_t *__restrict__ xq, size_t xq_stride, int m,
+                                                       int K, int ntb, uint8_t *__restrict__ pack) {
     const int nb = K / kQKK;
-    const int lane = threadIdx.x & 63;
-    const long long g = ((long long)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    if (g >= (long long)mp * nb) return;
-    const int t = (int)(g % mp), sb = (int)(g / mp);
-    int q[4] = {0, 0, 0, 0};
-    int bsum = 0;
-    float d = 0.0f;
-    if (t < m) {
-        const uint8_t *blk = xq + (size_t)t * xq_stride + (size_t)sb * kBytesQ8_K;
-        const uint32_t w = ldg4(blk + 4 + 4 * lane);
+    const int sb = (int)blockIdx.x % nb, tg = (int)blockIdx.x / nb;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tbase = (tg * kPackWaves + wave) * kPackTokensPerWave;
+    // all the wave's loads first
+    float4 xv[kPackTokensPerWave];
+    uint32_t qw[kPackTokensPerWave], dw[kPackTokensPerWave], bw[kPackTokensPerWave];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) q[e] = (int)(int8_t)((w >> (8 * e)) & 0xffu);
-        d = __uint_as_float(ldg4(blk));
-        const int i = lane >> 2;  // this lane group's 16-element sum (int16 at 260 + 2i)
-        if ((lane & 3) == 0) bsum = (int)(int16_t)((ldg4(blk + 260 + 4 * (i >> 1)) >> (16 * (i & 1))) & 0xffffu);
+    for (int i = 0; i < kPackTokensPerWave; ++i) {
+        const int t = tbase + i;
+        if (F32IN) {
+            xv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (t < m) xv[i] = *reinterpret_cast<const float4 *>(x + (size_t)t * ldx + (size_t)sb * kQKK + lane * 4);
+        } else {
+            qw[i] = dw[i] = bw[i] = 0u;
+            if (t < m) {
+                const uint8_t *blk = xq + (size_t)t * xq_stride + (size_t)sb * kBytesQ8_K;
+                qw[i] = ldg4(blk + 4 + 4 * lane);
+                dw[i] = ldg4(blk);
+                bw[i] = ldg4(blk + 260 + 4 * (lane >> 3));  // bsums 2k, 2k+1 of k = lane >> 2
+            }
+        }
     }
-    const int sq = wave_sum(abs(q[0]) + abs(q[1]) + abs(q[2]) + abs(q[3]));
-    uint8_t *tile = pack + ((size_t)sb * (mp / 32) + (t >> 5)) * kPkTile;
-    pack_store(tile, t & 31, lane, q, bsum, d, sq);
+    const int j = lane >> 4, s8 = lane & 7;
+    const int h = j >> 1, hf = j & 1;
+#pragma unroll
+    for (int i = 0; i < kPackTokensPerWave; ++i) {
+        const int t = tbase + i;
+        const int tb = t / kTokB, tt = (t % kTokB) / 32, tl = t % 32;
+        uint8_t *blk = pack + ((size_t)sb * ntb + tb) * kPkBlk;
+        int q[4];
+        int bsum;
+        float d;
+        uint32_t word;
+        if (F32IN) {
+            const Q8KLane r = q8k_quantize_lane(xv[i], lane);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q[e] = r.q[e];
+            word = r.word;
+            d = r.d;
+            bsum = r.sum4;
+            bsum += __shfl_xor(bsum, 1, 64);
+            bsum += __shfl_xor(bsum, 2, 64);
+        } else {
+            word = qw[i];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q[e] = sbyte(word, e);
+            d = __uint_as_float(dw[i]);
+            bsum = (int)(int16_t)((bw[i] >> (16 * ((lane >> 2) & 1))) & 0xffffu);
+        }
+        const int sq = wave_sum(abs(q[0]) + abs(q[1]) + abs(q[2]) + abs(q[3]));
+        const uint32_t hiw = (uint32_t)__shfl_xor((int)word, 8, 64);
+        if ((lane & 8) == 0) {
+            v4u o;
+            o[0] = h2_bits(sbyte(word, 0), sbyte(word, 2));
+            o[1] = h2_bits(sbyte(hiw, 0), sbyte(hiw, 2));
+            o[2] = h2_bits(sbyte(word, 1), sbyte(word, 3));
+            o[3] = h2_bits(sbyte(hiw, 1), sbyte(hiw, 3));
+            *reinterpret_cast<v4u *>(blk + hf * kPkHalf + (s8 * kTiles + tt) * 1024 + (tl + 32 * h) * 16) = o;
+        }
+        // min-term vector of lane half hh = lane (lanes 0, 1): bsums 8 hh .. 8 hh + 7,
+        // held by lanes 32 hh + 4 k
+        int bv[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) bv[k] = __shfl(bsum, 32 * (lane & 1) + 4 * k, 64);
+        if (lane < 2) {
+            v4u o;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o[k] = h2_bits(bv[2 * k], bv[2 * k + 1]);
+            *reinterpret_cast<v4u *>(blk + kPkCodes + tt * 1024 + (tl + 32 * lane) * 16) = o;
+        }
+        if (lane == 0) {
+            *reinterpret_cast<float *>(blk + kPkCodes + kPkMn + 4 * (32 * tt + tl)) = d;
+            *reinterpret_cast<int *>(blk + kPkCodes + kPkMn + kPkDx + 4 * (32 * tt + tl)) = sq;
+        }
+    }
 }
 
 // ------------------------------------------------------------------ GEMM
+//
+// Wave tiles: wave w owns row group g = w % 4 (64 rows: 2 halves of 32) and
+// token half th = w / 4 (64 tokens: 2 MFMA tiles).  Per K-step it builds 2
+// weight operands (9 VALU each), reads 2 activation operands (1 KiB each)
+// and issues 4 MFMAs, so LDS serves 0.5 KiB per MFMA -- reading one
+// activation operand per MFMA (32 rows x 128 tokens per wave) saturates the
+// LDS at ~42 % of the matrix-core peak.
+//
+// Every global load of the main loop is an LDS DMA (buffer_load ... lds)
+// written as inline assembly, and every wait for one is an explicit
+// s_waitcnt: the compiler then has no loads of its own in the loop and no
+// reason to drain the DMA queue before LDS reads it cannot tell apart from
+// the slots in flight.  The weights come from HBM (first touch) and are
+// requested two steps ahead; the codes are L2 hits (every row block reads
+// them) and one step ahead is enough.  LDS (135 KiB of the 160):
+//   codes    2 slots x 32 KiB  half super-block of activation codes, one step ahead
+//   extras   2 slots x 5 KiB   bsums / d / sum |q8| of a super-block (+1 KiB dummy target)
+//   weights  3 slots x 20 KiB  per row group 5 KiB: qs pieces of both row
+//                              halves and the 64 headers; two steps ahead
+constexpr int kCodeSlots = 2;
+constexpr int kWSlots = 3;
+constexpr int kWGrp = 5 * 1024;
+constexpr int kWSlot = 4 * kWGrp;
+constexpr int kLdsCodes = 0;
+constexpr int kLdsEx = kLdsCodes + kCodeSlots * kPkHalf;
+constexpr int kLdsExDummy = kLdsEx + 2 * kPkExtra;
+constexpr int kLdsW = kLdsExDummy + 1024;
+constexpr int kLdsLast = kLdsW + kWSlots * kWSlot;
+constexpr int kLdsBytes = kLdsLast + 16;
+static_assert(kLdsBytes <= 160 * 1024, "the LDS rings fit the gfx950 LDS");
 
 struct GmArgs {
     const uint8_t *w;     // [n_out][row_bytes] Q4_K
     size_t row_bytes;
-    const uint8_t *pack;  // [nblk][mtp][kPkTile]
+    const uint8_t *pack;  // [nblk][ntb][kPkBlk]
     uint32_t pack_bytes;  // < 4 GiB (checked at launch)
-    int mtp;              // token tiles in the pack (a multiple of kGmTiles)
+    int ntb;              // 128-token blocks in the pack
     const float *bias;    // [n_out] or null
     float *out;           // [m][ldo]
     int ldo, m, n_out, nblk;
-    int nrb;              // row blocks of kGmRows
-    int ntiles;           // nrb * token blocks
+    int nrb;              // row blocks of kRowsB
+    int ntiles;           // nrb * ntb
+    int nsplit;           // workgroups per tile along K (1 .. kMaxSplit)
+    float *part;          // [nsplit][ntiles][16][kThreads] float4 partial tiles (nsplit > 1)
+    unsigned *cnt;        // [ntiles] arrival counters, zero between launches
 };
 
-// This lane's bytes of one super-block: the 16-byte header and its half
-// (64 bytes) of the nibbles.
-struct WRaw {
-    v4u hd;
-    v4u q[4];
-};
-
-// This lane's bytes of one super-block, global -> registers (rows past n_out
-// lie past the resource and read as zeros): header at 0, nibbles at
-// 16 + 64 h .. + 63 of the row's block.
-__device__ __forceinline__ void load_w(__amdgpu_buffer_rsrc_t rows, uint32_t voff, int h, int sb, WRaw &r) {
-    const uint32_t so = (uint32_t)sb * kBytesQ4_K;
-    r.hd = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rows, voff, so, 0));
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        r.q[i] = __builtin_bit_cast(
-            v4u, __builtin_amdgcn_raw_buffer_load_b128(rows, voff + 16 + 64 * h + 16 * i, so, 0));
+// Buffer descriptor words (gfx9): base, base_hi | stride 0, num_records,
+// dword format.  Loads whose per-lane offset is at or past num_records read 0.
+__device__ __forceinline__ v4u rsrc_words(const void *base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    return v4u{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, bytes, 0x00020000u};
 }
 
-// Constants of one super-block for this lane's row and sub-blocks 4h .. 4h+3:
-// the packed-FMA multipliers / addends for the low- and high-nibble weights
-// of sub-block pairs (4h, 4h+1) and (4h+2, 4h+3), the min operand, d, -dmin.
+// One LDS DMA: each lane's 16 bytes at base + soff + voff land at LDS byte
+// address lds + 16 * lane.
+__device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, const v4u &rs, uint32_t soff) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "buffer_load_dwordx4 %1, %2, %3 offen lds"
+        :
+        : "s"(lds), "v"(voff), "s"(rs), "s"(soff)
+        : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N): at most N of this wave's DMAs still in flight.
+template <int N>
+__device__ __forceinline__ void wait_dma() {
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// Constants of one super-block for one row and sub-blocks 4h .. 4h+3
+// (get_scale_min_k4, src/gguf_quant.c:212-220, for four sub-blocks at once):
+// the four 6-bit scales, the min operand, d and -dmin.
 struct WConst {
-    h2 mlo[2], alo[2], mhi[2], ahi[2];
+    uint32_t sc4;
     v8h bmn;
     float dd, ndm;
 };
 
 __device__ __forceinline__ WConst w_const(const v4u hd, int h) {
-    // get_scale_min_k4 (src/gguf_quant.c:212-220) for four sub-blocks at once
     const uint32_t w0 = hd[1], w1 = hd[2], w2 = hd[3];
     const uint32_t sel = 0u - (uint32_t)h;  // all ones for sub-blocks 4..7
-    const uint32_t sc4 = ((w0 & 0x3f3f3f3fu) & ~sel) | (((w2 & 0x0f0f0f0fu) | ((w0 >> 2) & 0x30303030u)) & sel);
     const uint32_t m4 = ((w1 & 0x3f3f3f3fu) & ~sel) | ((((w2 >> 4) & 0x0f0f0f0fu) | ((w1 >> 2) & 0x30303030u)) & sel);
     WConst c;
+    c.sc4 = ((w0 & 0x3f3f3f3fu) & ~sel) | (((w2 & 0x0f0f0f0fu) | ((w0 >> 2) & 0x30303030u)) & sel);
     c.dd = f16_bits_to_f32(hd[0] & 0xffffu);
     c.ndm = -f16_bits_to_f32(hd[0] >> 16);
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        const float lo = (float)((sc4 >> (16 * p)) & 0xffu), hi = (float)((sc4 >> (16 * p + 8)) & 0xffu);
-        const _Float16 ml = (_Float16)lo, al = (_Float16)(-1024.0f * lo);
-        const _Float16 mh = (_Float16)(0.0625f * hi), ah = (_Float16)(-64.0f * hi);
-        c.mlo[p] = h2{ml, ml};
-        c.alo[p] = h2{al, al};
-        c.mhi[p] = h2{mh, mh};
-        c.ahi[p] = h2{ah, ah};
-    }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const _Float16 mv = (_Float16)(float)((m4 >> (8 * k)) & 0xffu);
@@ -249,24 +319,34 @@ __device__ __forceinline__ WConst w_const(const v4u hd, int h) {
     return c;
 }
 
-// Weight operand of K-step s (qs dword s of this lane's 64 bytes; s is a
-// constant once the K-step loops are unrolled).
+// The packed-FMA multipliers / addends of half p of the super-block: the
+// low- and high-nibble weights of sub-blocks 4h + 2p and 4h + 2p + 1.
+struct HalfConst {
+    h2 mlo, alo, mhi, ahi;
+};
+
+__device__ __forceinline__ HalfConst half_const(uint32_t sc4, int p) {
+    const float lo = (float)((sc4 >> (16 * p)) & 0xffu), hi = (float)((sc4 >> (16 * p + 8)) & 0xffu);
+    const _Float16 ml = (_Float16)lo, al = (_Float16)(-1024.0f * lo);
+    const _Float16 mh = (_Float16)(0.0625f * hi), ah = (_Float16)(-64.0f * hi);
+    return HalfConst{h2{ml, ml}, h2{al, al}, h2{mh, mh}, h2{ah, ah}};
+}
+
 struct NibMasks {
     uint32_t lo, hi, bias;  // 0x000F000F, 0x00F000F0, 0x64006400, held in VGPRs
 };
 
-__device__ __forceinline__ v8h w_operand(const WRaw &r, const WConst &c, const NibMasks &k, int s) {
-    const int p = s >> 3;
-    const uint32_t u = r.q[s >> 2][s & 3];
+// Weight operand of one K-step from its 4 qs bytes u (the lane's qs dword).
+__device__ __forceinline__ v8h w_operand(uint32_t u, const HalfConst &c, const NibMasks &k) {
     const uint32_t u8 = u >> 8;
     const h2 y0 = __builtin_bit_cast(h2, (u & k.lo) | k.bias);
     const h2 y1 = __builtin_bit_cast(h2, (u & k.hi) | k.bias);
     const h2 y2 = __builtin_bit_cast(h2, (u8 & k.lo) | k.bias);
     const h2 y3 = __builtin_bit_cast(h2, (u8 & k.hi) | k.bias);
-    const h2 b0 = __builtin_elementwise_fma(y0, c.mlo[p], c.alo[p]);
-    const h2 b1 = __builtin_elementwise_fma(y1, c.mhi[p], c.ahi[p]);
-    const h2 b2 = __builtin_elementwise_fma(y2, c.mlo[p], c.alo[p]);
-    const h2 b3 = __builtin_elementwise_fma(y3, c.mhi[p], c.ahi[p]);
+    const h2 b0 = __builtin_elementwise_fma(y0, c.mlo, c.alo);
+    const h2 b1 = __builtin_elementwise_fma(y1, c.mhi, c.ahi);
+    const h2 b2 = __builtin_elementwise_fma(y2, c.mlo, c.alo);
+    const h2 b3 = __builtin_elementwise_fma(y3, c.mhi, c.ahi);
     return v8h{b0.x, b0.y, b1.x, b1.y, b2.x, b2.y, b3.x, b3.y};
 }
 
@@ -275,66 +355,89 @@ __device__ __forceinline__ v16f mfma(v8h a, v8h b, v16f c) {
 }
 
 __device__ __forceinline__ v8h lds_v8h(const uint8_t *p) { return *reinterpret_cast<const v8h *>(p); }
+__device__ __forceinline__ v4u lds_v4u(const uint8_t *p) { return *reinterpret_cast<const v4u *>(p); }
 
-// K-steps S0 .. S1-1 of one super-block for the wave's 2 token tiles: two
-// independent accumulator chains advance together, so each K-step issues 2
-// MFMAs behind one weight operand (built just in time) and the next K-step's
-// activation operands are read while they run.
-template <int S0, int S1>
-__device__ __forceinline__ void sb_chains(const uint8_t *stage, int lane, const WRaw &r, const WConst &c,
-                                          const NibMasks &k, v16f (&C)[kWvTiles]) {
-    v8h a[kWvTiles];
+// C[g][tt]: the wave's 2 row halves x 2 token tiles.
+typedef v16f Tiles[2][2];
+
+// The 8 K-steps of half p: codes slot `cur` (this wave's two token tiles at
+// `cur + tt * 1024`, stride 4 KiB per K-step), this row group's weight slot
+// `wq` (qs pieces of row half g at wq + 2 KiB g).  Four accumulator chains
+// advance together; each K-step reads 2 activation operands and issues 4
+// MFMAs on 2 weight operands.  The weight operands of the next K-step (18
+// VALU) are built while this K-step's MFMAs run, interleaved with them
+// (an MFMA hides only a few VALU instructions issued behind it, and a block
+// of VALU with no MFMA in flight leaves the matrix core idle).  FIRST: the
+// chains start at zero.
+template <int P, bool FIRST>
+__device__ __forceinline__ void half_chains(const uint8_t *cur, const uint8_t *wq, int lane, const WConst (&wc)[2],
+                                            const NibMasks &k, Tiles &C) {
+    const HalfConst c0 = half_const(wc[0].sc4, P), c1 = half_const(wc[1].sc4, P);
+    const v4u q00 = lds_v4u(wq + lane * 16), q01 = lds_v4u(wq + 1024 + lane * 16);
+    const v4u q10 = lds_v4u(wq + 2048 + lane * 16), q11 = lds_v4u(wq + 3072 + lane * 16);
+    v8h a[2];
 #pragma unroll
-    for (int tt = 0; tt < kWvTiles; ++tt) {
-        C[tt] = v16f{};
-        a[tt] = lds_v8h(stage + tt * kPkTile + S0 * 1024 + lane * 16);
-    }
+    for (int tt = 0; tt < 2; ++tt) a[tt] = lds_v8h(cur + tt * 1024 + lane * 16);
+    v8h b0 = w_operand(q00[0], c0, k), b1 = w_operand(q10[0], c1, k);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int s = S0; s < S1; ++s) {
-        const v8h b = w_operand(r, c, k, s);
-        v8h an[kWvTiles];
-        if (s + 1 < S1) {
-#pragma unroll
-            for (int tt = 0; tt < kWvTiles; ++tt) an[tt] = lds_v8h(stage + tt * kPkTile + (s + 1) * 1024 + lane * 16);
+    for (int s = 0; s < 8; ++s) {
+        v8h nb0 = b0, nb1 = b1;
+        if (s + 1 < 8) {
+            nb0 = w_operand(s + 1 < 4 ? q00[s + 1] : q01[s - 3], c0, k);
+            nb1 = w_operand(s + 1 < 4 ? q10[s + 1] : q11[s - 3], c1, k);
         }
 #pragma unroll
-        for (int tt = 0; tt < kWvTiles; ++tt) C[tt] = mfma(a[tt], b, C[tt]);
-        if (s + 1 < S1) {
-#pragma unroll
-            for (int tt = 0; tt < kWvTiles; ++tt) a[tt] = an[tt];
+        for (int tt = 0; tt < 2; ++tt) {
+            C[0][tt] = mfma(a[tt], b0, (FIRST && s == 0) ? v16f{} : C[0][tt]);
+            C[1][tt] = mfma(a[tt], b1, (FIRST && s == 0) ? v16f{} : C[1][tt]);
+            if (s + 1 < 8) a[tt] = lds_v8h(cur + (s + 1) * 4096 + tt * 1024 + lane * 16);
         }
-        // one K-step per scheduling region: the next step's operand reads
-        // stay one step ahead instead of being hoisted (and held) further
+        // MFMA, VALU x5, MFMA, DS read, VALU x4, MFMA, VALU x5, MFMA, DS read, VALU x4
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+        }
         __builtin_amdgcn_sched_barrier(0);
+        b0 = nb0;
+        b1 = nb1;
     }
 }
 
-// acc += dx * (C * d - mn * dmin) for the wave's tiles (MN = false: acc += dx * C * d);
-// the next tile's min-term MFMA is issued before this tile's VALU work.
+// acc += dx * (C * d - mn * dmin) for the wave's tiles (MN = false:
+// acc += dx * C * d).  `ex` is the extras slot, `tq` the wave's first token
+// tile in the workgroup (0 or 2).
 template <bool MN>
-__device__ __forceinline__ void sb_combine(const uint8_t *stage, int lane, const WConst &c, const v16f (&C)[kWvTiles],
-                                           v16f (&acc)[kWvTiles]) {
+__device__ __forceinline__ void combine(const uint8_t *ex, int tq, int lane, const WConst (&wc)[2], const Tiles &C,
+                                        Tiles &acc) {
     const int h = lane >> 5;
-    v16f mn{};
-    if (MN) mn = mfma(lds_v8h(stage + kPkA + lane * 16), c.bmn, v16f{});
 #pragma unroll
-    for (int tt = 0; tt < kWvTiles; ++tt) {
-        const uint8_t *tile = stage + tt * kPkTile;
-        v16f mn_next{};
-        if (MN && tt + 1 < kWvTiles) mn_next = mfma(lds_v8h(tile + kPkTile + kPkA + lane * 16), c.bmn, v16f{});
+    for (int tt = 0; tt < 2; ++tt) {
+        v16f mn[2] = {v16f{}, v16f{}};
+        if (MN) {
+            const v8h bs = lds_v8h(ex + (tq + tt) * 1024 + lane * 16);
+            mn[0] = mfma(bs, wc[0].bmn, v16f{});
+            mn[1] = mfma(bs, wc[1].bmn, v16f{});
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float4 dx = *reinterpret_cast<const float4 *>(tile + kPkA + kPkMn + 4 * (8 * i + 4 * h));
+            const float4 dx = *reinterpret_cast<const float4 *>(ex + kPkMn + 4 * (32 * (tq + tt) + 8 * i + 4 * h));
             const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = 4 * i + e;
-                float v = C[tt][r] * c.dd;
-                if (MN) v = __builtin_fmaf(mn[r], c.ndm, v);
-                acc[tt][r] = __builtin_fmaf(v, dxs[e], acc[tt][r]);
+            for (int g = 0; g < 2; ++g) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = 4 * i + e;
+                    float v = C[g][tt][r] * wc[g].dd;
+                    if (MN) v = __builtin_fmaf(mn[g][r], wc[g].ndm, v);
+                    acc[g][tt][r] = __builtin_fmaf(v, dxs[e], acc[g][tt][r]);
+                }
             }
         }
-        if (MN) mn = mn_next;
         __builtin_amdgcn_sched_barrier(0);
     }
 }
@@ -350,120 +453,224 @@ __device__ __forceinline__ int wave_max_dpp(int v) {
     return __builtin_amdgcn_readlane(v, 63);
 }
 
-// The workgroup's activation pack of one super-block (at byte soff of the
-// pack), global -> LDS.
-__device__ __forceinline__ void stage_pack(__amdgpu_buffer_rsrc_t pack, uint32_t soff, uint8_t *dst, int wave,
-                                           int lane) {
-    static_assert(kGmChunks == 8 * 8 + 5, "8 chunks per wave and one more for waves 0..4");
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int ch = 8 * i + wave;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(pack, (lds_void *)(dst + ch * 1024), 16, lane * 16,
-                                                 soff + ch * 1024, 0, 0);
-    }
-    if (wave < 5)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(pack, (lds_void *)(dst + (64 + wave) * 1024), 16, lane * 16,
-                                                 soff + (64 + wave) * 1024, 0, 0);
-}
-
-
 // Per-wave state of the main loop.
 struct GmLoop {
-    __amdgpu_buffer_rsrc_t pack, rows;
-    uint32_t pk0, pk_sb, woff;
+    v4u pack, rows;           // descriptors: the activation pack, this row group's 64 rows
+    uint32_t pk0, pk_sb;      // pack offset of this token block, bytes per super-block
+    uint32_t voff_q, voff_h;  // per lane: qs half of row 32 th + lane % 32 (+ 64 h), header of row lane
+    uint32_t smem;            // LDS address of the workgroup's buffer
     NibMasks km;
-    int lane, wave, h, th;
+    int lane, wave, grp, th, sb0, sblast;
 };
 
-// One super-block from stage `cur` while the next one (if `more`) is
-// requested into `nxt` and the next weights into wn.  cur and nxt are
-// distinct LDS objects, so the compiler sees that the requests in flight do
-// not touch what this super-block reads and needs no wait for them.
-__device__ __forceinline__ void sb_step(const GmLoop &L, int sb, bool more, const uint8_t *cur, uint8_t *nxt,
-                                        const WRaw &wr, WRaw &wn, v16f (&acc)[kWvTiles]) {
-    if (more) {
-        stage_pack(L.pack, L.pk0 + (uint32_t)(sb + 1) * L.pk_sb, nxt, L.wave, L.lane);
-        load_w(L.rows, L.woff, L.h, sb + 1, wn);
+// Step s (half hf = s & 1 of super-block sb0 + s / 2) requests, in this
+// order: the codes of step s + 1 (4 DMAs, a quarter of the half super-block),
+// on odd steps the extras of the next super-block (1 DMA; waves 5..7 repeat
+// chunk 4 into the dummy target), then the weights of step s + 2 (3 DMAs:
+// qs pieces 0 and 1 of row half th of the wave's row group, the group's 64
+// headers -- both token-half waves request them, the same bytes; rows past
+// n_out read zeros).  Requests past the end of the K range re-request its
+// last super-block into slots nobody reads again, so every step issues its
+// weights last: a wait for vmcnt(3) at the start of step s + 1 leaves
+// exactly the weights of step s + 2 in flight.
+constexpr int kWLoads = 3;
+
+__device__ __forceinline__ void step_requests(const GmLoop &L, int s) {
+    const uint32_t lv = (uint32_t)L.lane * 16;
+    const int s1 = s + 1;
+    const int sbc = min(L.sb0 + (s1 >> 1), L.sblast);
+    const uint32_t cdst = L.smem + kLdsCodes + (uint32_t)(s1 % kCodeSlots) * kPkHalf;
+    const uint32_t cso = L.pk0 + (uint32_t)sbc * L.pk_sb + (uint32_t)(s1 & 1) * kPkHalf;
+#pragma unroll
+    for (int i = 0; i < kHalfChunks / kWaves; ++i) {
+        const uint32_t ch = (uint32_t)(kWaves * i + L.wave);
+        dma16(cdst + ch * 1024, lv, L.pack, cso + ch * 1024);
     }
-    const uint8_t *mine = cur + (kWvTiles * L.th) * kPkTile;  // this wave's two token tiles
-    const WConst c = w_const(wr.hd, L.h);
-    // the exactness bound of one chain over the wave's 64 tokens
-    const int sq = *reinterpret_cast<const int *>(mine + (L.lane >> 5) * kPkTile + kPkA + kPkMn + kPkDx +
-                                                   4 * (L.lane & 31));
-    const int sqmax = wave_max_dpp(sq);
-    v16f C[kWvTiles];
-    if (sqmax <= kExactSqMax) {
-        sb_chains<0, 16>(mine, L.lane, wr, c, L.km, C);
-        sb_combine<true>(mine, L.lane, c, C, acc);
-    } else {
-        sb_chains<0, 8>(mine, L.lane, wr, c, L.km, C);
-        sb_combine<true>(mine, L.lane, c, C, acc);
-        sb_chains<8, 16>(mine, L.lane, wr, c, L.km, C);
-        sb_combine<false>(mine, L.lane, c, C, acc);
+    if (s & 1) {  // extras of super-block sb0 + (s + 1) / 2
+        const int je = s1 >> 1;
+        const int sbe = min(L.sb0 + je, L.sblast);
+        const int ch = min(L.wave, kExtraChunks - 1);
+        const uint32_t edst = L.wave < kExtraChunks
+                                  ? L.smem + kLdsEx + (uint32_t)(je & 1) * kPkExtra + (uint32_t)ch * 1024
+                                  : L.smem + kLdsExDummy;
+        dma16(edst, lv, L.pack, L.pk0 + (uint32_t)sbe * L.pk_sb + kPkCodes + (uint32_t)ch * 1024);
     }
-    __builtin_amdgcn_s_waitcnt(0);  // the next stage and weights have landed
-    __syncthreads();                // and every wave is done with this stage
+    const int s2 = s + 2;
+    const int sbw = min(L.sb0 + (s2 >> 1), L.sblast);
+    const uint32_t wdst = L.smem + kLdsW + (uint32_t)(s2 % kWSlots) * kWSlot + (uint32_t)L.grp * kWGrp;
+    const uint32_t wso = (uint32_t)sbw * kBytesQ4_K + 16 + 32 * (uint32_t)(s2 & 1);
+    dma16(wdst + 2048 * L.th, L.voff_q, L.rows, wso);
+    dma16(wdst + 2048 * L.th + 1024, L.voff_q, L.rows, wso + 16);
+    dma16(wdst + 4096, L.voff_h, L.rows, (uint32_t)sbw * kBytesQ4_K);
 }
 
-__global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_q4k_kernel(GmArgs a) {
-    // two activation stages: kGmLds bytes of LDS
-    __shared__ __align__(16) uint8_t stage0[kGmStage];
-    __shared__ __align__(16) uint8_t stage1[kGmStage];
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_q4k_kernel(GmArgs a) {
+    __shared__ __align__(16) uint8_t smem[kLdsBytes];
+    int *s_last = reinterpret_cast<int *>(smem + kLdsLast);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int rq = wave & 3, th = wave >> 2;  // row quarter, token half
     const int h = lane >> 5;
+    const int grp = wave & 3, th = wave >> 2;
 
     // workgroups sharing a row block are a multiple of nrb apart; with nrb a
     // multiple of 8 they land on one XCD and share its L2 copy of the weights
-    const int rb = (int)blockIdx.x % a.nrb, tb = (int)blockIdx.x / a.nrb;
-    const int sb0 = 0, sb1 = a.nblk;
+    const int tile = (int)blockIdx.x % a.ntiles, z = (int)blockIdx.x / a.ntiles;
+    const int rb = tile % a.nrb, tb = tile / a.nrb;
+    const int sb0 = (int)((long long)a.nblk * z / a.nsplit);
+    const int sb1 = (int)((long long)a.nblk * (z + 1) / a.nsplit);
+    const int nsb = sb1 - sb0;
 
-    const int row0 = rb * kGmRows + 32 * rq;
-    const int row = min(row0 + (lane & 31), a.n_out - 1);
+    const int rowg = rb * kRowsB + 64 * grp;  // first row of the row group
     GmLoop L;
     L.lane = lane;
     L.wave = wave;
-    L.h = h;
+    L.grp = grp;
     L.th = th;
-    L.pk_sb = (uint32_t)a.mtp * kPkTile;
-    L.pk0 = (uint32_t)(kGmTiles * tb) * kPkTile;
-    L.pack = buffer_rsrc(a.pack, a.pack_bytes);
-    const int live_rows = min(32, a.n_out - row0);  // rows past n_out lie past the resource (zeros)
-    L.rows = buffer_rsrc(a.w + (size_t)min(row0, a.n_out - 1) * a.row_bytes,
-                         live_rows > 0 ? (uint32_t)live_rows * (uint32_t)a.row_bytes : 0u);
-    L.woff = (uint32_t)(lane & 31) * (uint32_t)a.row_bytes;
+    L.sb0 = sb0;
+    L.sblast = sb1 - 1;
+    L.pk_sb = (uint32_t)a.ntb * kPkBlk;
+    L.pk0 = (uint32_t)tb * kPkBlk;
+    L.pack = rsrc_words(a.pack, a.pack_bytes);
+    const int live_rows = min(64, a.n_out - rowg);  // rows past n_out lie past the descriptor (zeros)
+    L.rows = rsrc_words(a.w + (size_t)min(rowg, a.n_out - 1) * a.row_bytes,
+                        live_rows > 0 ? (uint32_t)live_rows * (uint32_t)a.row_bytes : 0u);
+    L.voff_h = (uint32_t)lane * (uint32_t)a.row_bytes;
+    L.voff_q = (uint32_t)(32 * th + (lane & 31)) * (uint32_t)a.row_bytes + 64u * (uint32_t)h;
+    L.smem = lds_addr(smem);
     L.km = NibMasks{0x000F000Fu, 0x00F000F0u, 0x64006400u};
     asm volatile("" : "+v"(L.km.lo), "+v"(L.km.hi), "+v"(L.km.bias));
 
-    v16f acc[kWvTiles];
+    Tiles acc, C;
 #pragma unroll
-    for (int tt = 0; tt < kWvTiles; ++tt) acc[tt] = v16f{};
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) acc[g][tt] = v16f{};
 
-    WRaw w0, w1;
-    stage_pack(L.pack, L.pk0 + (uint32_t)sb0 * L.pk_sb, stage0, wave, lane);
-    load_w(L.rows, L.woff, h, sb0, w0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    // the first super-block: codes of step 0, its extras, weights of steps 0
+    // and 1 (then each step's requests continue the pattern)
+    {
+        const uint32_t lv = (uint32_t)lane * 16;
+        const uint32_t cso = L.pk0 + (uint32_t)sb0 * L.pk_sb;
+#pragma unroll
+        for (int i = 0; i < kHalfChunks / kWaves; ++i) {
+            const uint32_t c = (uint32_t)(kWaves * i + wave);
+            dma16(L.smem + kLdsCodes + c * 1024, lv, L.pack, cso + c * 1024);
+        }
+        const int ch = min(wave, kExtraChunks - 1);
+        dma16(wave < kExtraChunks ? L.smem + kLdsEx + (uint32_t)ch * 1024 : L.smem + kLdsExDummy, lv, L.pack,
+              cso + kPkCodes + (uint32_t)ch * 1024);
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const uint32_t wdst = L.smem + kLdsW + (uint32_t)hf * kWSlot + (uint32_t)grp * kWGrp;
+            const uint32_t wso = (uint32_t)sb0 * kBytesQ4_K;
+            dma16(wdst + 2048 * th, L.voff_q, L.rows, wso + 16 + 32 * hf);
+            dma16(wdst + 2048 * th + 1024, L.voff_q, L.rows, wso + 32 + 32 * hf);
+            dma16(wdst + 4096, L.voff_h, L.rows, wso);
+        }
+    }
 
-    // two super-blocks per trip: each step names its stages and weight
-    // registers statically
-    for (int sb = sb0; sb < sb1; sb += 2) {
-        sb_step(L, sb, sb + 1 < sb1, stage0, stage1, w0, w1, acc);
-        if (sb + 1 >= sb1) break;
-        sb_step(L, sb + 1, sb + 2 < sb1, stage1, stage0, w1, w0, acc);
+    const int tq = 2 * th;  // the wave's first token tile
+    for (int j = 0; j < nsb; ++j) {
+        const int s = 2 * j;
+        const uint8_t *ex = smem + kLdsEx + (j & 1) * kPkExtra;
+        // even step: half 0 of super-block sb0 + j
+        wait_dma<kWLoads>();
+        __syncthreads();
+        step_requests(L, s);
+        const uint8_t *wq0 = smem + kLdsW + (s % kWSlots) * kWSlot + grp * kWGrp;
+        WConst wc[2];
+#pragma unroll
+        for (int g = 0; g < 2; ++g) wc[g] = w_const(lds_v4u(wq0 + 4096 + (32 * g + (lane & 31)) * 16), h);
+        const int sq0 = *reinterpret_cast<const int *>(ex + kPkMn + kPkDx + 4 * lane);
+        const int sq1 = *reinterpret_cast<const int *>(ex + kPkMn + kPkDx + 4 * (lane + 64));
+        // the exactness bound of one chain over the workgroup's 128 tokens
+        const bool split = wave_max_dpp(max(sq0, sq1)) > kExactSqMax;
+        const uint8_t *cur0 = smem + kLdsCodes + tq * 1024;  // even steps use code slot 0
+        half_chains<0, true>(cur0, wq0, lane, wc, L.km, C);
+        if (split) combine<false>(ex, tq, lane, wc, C, acc);
+        // odd step: half 1
+        wait_dma<kWLoads>();
+        __syncthreads();
+        step_requests(L, s + 1);
+        const uint8_t *wq1 = smem + kLdsW + ((s + 1) % kWSlots) * kWSlot + grp * kWGrp;
+        const uint8_t *cur1 = smem + kLdsCodes + kPkHalf + tq * 1024;
+        if (split)
+            half_chains<1, true>(cur1, wq1, lane, wc, L.km, C);
+        else
+            half_chains<1, false>(cur1, wq1, lane, wc, L.km, C);
+        combine<true>(ex, tq, lane, wc, C, acc);
+    }
+    wait_dma<0>();  // the requests past the end have landed before the LDS is released
+
+    if (a.nsplit > 1) {
+        // partial tile out; the last of the tile's workgroups adds them up in
+        // split order.  Release: every thread's stores are complete (vmcnt 0)
+        // before the barrier, one thread writes them back to the device level
+        // and counts the arrival; the last arriver invalidates its caches
+        // (acquire) before any thread reads the others' partials.
+        float4 *part = reinterpret_cast<float4 *>(a.part);
+        const size_t base = ((size_t)z * a.ntiles + tile) * 16;
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    part[(base + (2 * g + tt) * 4 + i) * kThreads + tid] =
+                        make_float4(acc[g][tt][4 * i], acc[g][tt][4 * i + 1], acc[g][tt][4 * i + 2],
+                                    acc[g][tt][4 * i + 3]);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) {
+            const unsigned old =
+                __hip_atomic_fetch_add(&a.cnt[tile], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            const int last = old == (unsigned)(a.nsplit - 1);
+            if (last) {
+                __hip_atomic_store(&a.cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            }
+            *s_last = last;
+        }
+        __syncthreads();
+        if (!*s_last) return;
+        Tiles sum;
+        for (int zz = 0; zz < a.nsplit; ++zz) {
+            const size_t bz = ((size_t)zz * a.ntiles + tile) * 16;
+#pragma unroll
+            for (int g = 0; g < 2; ++g)
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float4 p = zz == z ? make_float4(acc[g][tt][4 * i], acc[g][tt][4 * i + 1],
+                                                               acc[g][tt][4 * i + 2], acc[g][tt][4 * i + 3])
+                                                 : part[(bz + (2 * g + tt) * 4 + i) * kThreads + tid];
+                        const float pv[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            sum[g][tt][4 * i + e] = zz == 0 ? pv[e] : sum[g][tt][4 * i + e] + pv[e];
+                    }
+        }
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) acc[g][tt] = sum[g][tt];
     }
 
     // bias after the whole dot (the reference's b + dot), then the store
-    const int o = row0 + (lane & 31);
-    const float b = a.bias != nullptr ? a.bias[row] : 0.0f;
-    if (o >= a.n_out) return;
+    const int t0 = kTokB * tb + 64 * th;
 #pragma unroll
-    for (int tt = 0; tt < kWvTiles; ++tt) {
+    for (int g = 0; g < 2; ++g) {
+        const int o = rowg + 32 * g + (lane & 31);
+        if (o >= a.n_out) continue;
+        const float b = a.bias != nullptr ? a.bias[o] : 0.0f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int t = kGmTiles * 32 * tb + 64 * th + 32 * tt + 8 * (r >> 2) + 4 * h + (r & 3);
-            if (t < a.m) a.out[(size_t)t * a.ldo + o] = b + acc[tt][r];
+        for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int t = t0 + 32 * tt + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (t < a.m) a.out[(size_t)t * a.ldo + o] = b + acc[g][tt][r];
+            }
         }
     }
 }
@@ -476,34 +683,51 @@ bool gemm_q8_supported(int type, int n_out, int K, int m) {
     return type == kTypeQ4_K && K % kQKK == 0 && n_out > 0 && m >= 1;
 }
 
-// Token tiles of the activation pack for m tokens (whole workgroup blocks).
-static int pack_tiles(int m) { return (m + 32 * kGmTiles - 1) / (32 * kGmTiles) * kGmTiles; }
+// 128-token blocks of the activation pack for m tokens.
+static int pack_tblocks(int m) { return (m + kTokB - 1) / kTokB; }
 
-size_t gemm_q4k_pack_bytes(int m, int K) { return (size_t)(K / kQKK) * pack_tiles(m) * kPkTile; }
+size_t gemm_q4k_pack_bytes(int m, int K) { return (size_t)(K / kQKK) * pack_tblocks(m) * kPkBlk; }
 
-static int gemm_tiles(int m, int n_out) {
-    return ((n_out + kGmRows - 1) / kGmRows) * (pack_tiles(m) / kGmTiles);
+// K split: enough workgroups to cover the chip's 256 CUs where the tiles
+// alone cannot, at least two super-blocks per workgroup.
+static int gemm_split(int ntiles, int nblk) {
+    int s = 256 / ntiles;
+    if (s > kMaxSplit) s = kMaxSplit;
+    if (s > nblk / 2) s = nblk / 2;
+    if (ntiles > kGemmCounters) s = 1;
+    return s < 1 ? 1 : s;
 }
 
+static int gemm_tiles(int m, int n_out) { return ((n_out + kRowsB - 1) / kRowsB) * pack_tblocks(m); }
+
+// Partial tiles of the K split (bytes), and the counters' size.
+size_t gemm_q4k_part_bytes(int m, int n_out, int K) {
+    const int nt = gemm_tiles(m, n_out);
+    const int s = gemm_split(nt, K / kQKK);
+    return s > 1 ? (size_t)s * nt * kTokB * kRowsB * sizeof(float) : 0;
+}
+size_t gemm_q4k_counter_bytes() { return kGemmCounters * sizeof(unsigned); }
+
 hipError_t launch_q8k_pack_f32(const float *x, int m, int K, int ldx, uint8_t *pack, hipStream_t st) {
-    const int mp = pack_tiles(m) * 32;
-    const long long threads = (long long)mp * (K / kQKK) * 64;
-    hipLaunchKernelGGL(q8k_pack_f32_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, x, m, K, ldx,
-                       mp, pack);
+    const int ntb = pack_tblocks(m);
+    const unsigned grid = (unsigned)((K / kQKK) * ntb * (kTokB / (kPackWaves * kPackTokensPerWave)));
+    hipLaunchKernelGGL(q8k_pack_kernel<true>, dim3(grid), dim3(256), 0, st, x, ldx, nullptr, (size_t)0, m, K, ntb,
+                       pack);
     return hipGetLastError();
 }
 
 hipError_t launch_q8k_pack_q8k(const uint8_t *xq, size_t xq_stride, int m, int K, uint8_t *pack, hipStream_t st) {
-    const int mp = pack_tiles(m) * 32;
-    const long long threads = (long long)mp * (K / kQKK) * 64;
-    hipLaunchKernelGGL(q8k_pack_q8k_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, xq, xq_stride,
-                       m, K, mp, pack);
+    const int ntb = pack_tblocks(m);
+    const unsigned grid = (unsigned)((K / kQKK) * ntb * (kTokB / (kPackWaves * kPackTokensPerWave)));
+    hipLaunchKernelGGL(q8k_pack_kernel<false>, dim3(grid), dim3(256), 0, st, nullptr, 0, xq, xq_stride, m, K, ntb,
+                       pack);
     return hipGetLastError();
 }
 
-// out = bias + W x over a packed activation (launch_q8k_pack_*).
+// out = bias + W x over a packed activation (launch_q8k_pack_*); part holds
+// gemm_q4k_part_bytes and cnt gemm_q4k_counter_bytes, zero-filled once.
 hipError_t launch_gemm_q4k(const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const uint8_t *pack,
-                           const float *bias, float *out, int ldo, hipStream_t st) {
+                           float *part, unsigned *cnt, const float *bias, float *out, int ldo, hipStream_t st) {
     if (!gemm_q8_supported(kTypeQ4_K, n_out, K, m)) return hipErrorInvalidValue;
     if (((uintptr_t)w & 15u) != 0 || (row_bytes & 15u) != 0 || ((uintptr_t)pack & 15u) != 0)
         return hipErrorInvalidValue;
@@ -511,9 +735,9 @@ hipError_t launch_gemm_q4k(const uint8_t *w, size_t row_bytes, int n_out, int K,
     a.w = w;
     a.row_bytes = row_bytes;
     a.pack = pack;
-    a.mtp = pack_tiles(m);
+    a.ntb = pack_tblocks(m);
     const size_t pb = gemm_q4k_pack_bytes(m, K);
-    if (pb >= ((size_t)1 << 32) || (size_t)kGmRows * row_bytes >= ((size_t)1 << 31)) return hipErrorInvalidValue;
+    if (pb >= ((size_t)1 << 32) || (size_t)32 * row_bytes >= ((size_t)1 << 31)) return hipErrorInvalidValue;
     a.pack_bytes = (uint32_t)pb;
     a.bias = bias;
     a.out = out;
@@ -521,8 +745,12 @@ hipError_t launch_gemm_q4k(const uint8_t *w, size_t row_bytes, int n_out, int K,
     a.m = m;
     a.n_out = n_out;
     a.nblk = K / kQKK;
-    a.nrb = (n_out + kGmRows - 1) / kGmRows;
+    a.nrb = (n_out + kRowsB - 1) / kRowsB;
     a.ntiles = gemm_tiles(m, n_out);
-    hipLaunchKernelGGL(gemm_q4k_kernel, dim3((unsigned)a.ntiles), dim3(kGmThreads), 0, st, a);
+    a.nsplit = gemm_split(a.ntiles, a.nblk);
+    a.part = part;
+    a.cnt = cnt;
+    if (a.nsplit > 1 && (part == nullptr || cnt == nullptr)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gemm_q4k_kernel, dim3((unsigned)(a.ntiles * a.nsplit)), dim3(kThreads), 0, st, a);
     return hipGetLastError();
 }

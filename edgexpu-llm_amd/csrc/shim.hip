@@ -33,10 +33,12 @@ hipError_t launch_elementwise(const float *a, const float *b, float *out, long l
 hipError_t launch_argmax_rows(const float *s, int m, int n, size_t lds, unsigned long long *partial, uint32_t *best,
                               hipStream_t st);
 size_t gemm_q4k_pack_bytes(int m, int K);
+size_t gemm_q4k_part_bytes(int m, int n_out, int K);
+size_t gemm_q4k_counter_bytes();
 hipError_t launch_q8k_pack_f32(const float *x, int m, int K, int ldx, uint8_t *pack, hipStream_t st);
 hipError_t launch_q8k_pack_q8k(const uint8_t *xq, size_t xq_stride, int m, int K, uint8_t *pack, hipStream_t st);
 hipError_t launch_gemm_q4k(const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const uint8_t *pack,
-                           const float *bias, float *out, int ldo, hipStream_t st);
+                           float *part, unsigned *cnt, const float *bias, float *out, int ldo, hipStream_t st);
 hipError_t launch_gemm_f16(const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const uint8_t *xq,
                            size_t xq_stride, void *ws, const float *bias, float *out, int ldo, hipStream_t st);
 size_t gemm_f16_workspace(int m, int n_out, int K);
@@ -282,6 +284,10 @@ void *gemm_ws(size_t bytes) {
     }
     size_t cap = align_up(bytes, (size_t)1 << 20);
     if (!hip_ok(hipMalloc(&g.gws, cap), "hipMalloc gemm workspace")) return nullptr;
+    // the K-split arrival counters at its start are zero between launches
+    // (each tile's last workgroup resets its own); cleared here once, outside
+    // any stream work a caller may capture
+    if (!hip_ok(hipMemset(g.gws, 0, gemm_q4k_counter_bytes()), "clear gemm counters")) return nullptr;
     g.gws_cap = cap;
     return g.gws;
 }
@@ -292,14 +298,25 @@ void *gemm_ws(size_t bytes) {
 bool run_gemm_q4k(int nmat, const void *const *w, const int *n_out, int n_in, int m, const float *x,
                   const uint8_t *xq, size_t xq_stride, const float *const *bias, float *const *out, const int *ldo,
                   hipStream_t st) {
-    uint8_t *pack = (uint8_t *)gemm_ws(gemm_q4k_pack_bytes(m, n_in));
-    if (pack == nullptr) return false;
+    // workspace: arrival counters | activation pack | K-split partial tiles
+    size_t part_bytes = 0;
+    for (int z = 0; z < nmat; ++z) {
+        const size_t pb = gemm_q4k_part_bytes(m, n_out[z], n_in);
+        part_bytes = pb > part_bytes ? pb : part_bytes;
+    }
+    const size_t cnt_bytes = gemm_q4k_counter_bytes();
+    const size_t pack_bytes = align_up(gemm_q4k_pack_bytes(m, n_in), (size_t)256);
+    uint8_t *ws = (uint8_t *)gemm_ws(cnt_bytes + pack_bytes + part_bytes);
+    if (ws == nullptr) return false;
+    unsigned *cnt = (unsigned *)ws;
+    uint8_t *pack = ws + cnt_bytes;
+    float *part = part_bytes != 0 ? (float *)(pack + pack_bytes) : nullptr;
     const hipError_t e = x != nullptr ? launch_q8k_pack_f32(x, m, n_in, n_in, pack, st)
                                       : launch_q8k_pack_q8k(xq, xq_stride, m, n_in, pack, st);
     if (!hip_ok(e, "pack activations")) return false;
     const size_t rb = edgexpu_hip_row_bytes(kTypeQ4_K, n_in);
     for (int z = 0; z < nmat; ++z)
-        if (!hip_ok(launch_gemm_q4k((const uint8_t *)w[z], rb, n_out[z], n_in, m, pack,
+        if (!hip_ok(launch_gemm_q4k((const uint8_t *)w[z], rb, n_out[z], n_in, m, pack, part, cnt,
                                     bias != nullptr ? bias[z] : nullptr, out[z], ldo[z], st),
                     "gemm_q4k"))
             return false;
