@@ -305,6 +305,73 @@ def q4k_q8k_gemm_f64(w: np.ndarray, xq: np.ndarray):
     return val, mag
 
 
+def q8_rows_f64(qtype: int, w: np.ndarray, xq: np.ndarray, chunk: int = 2048):
+    """q8_dot_f64 for every row of w against one token's quantized activation
+    xq, vectorized over rows (chunks of `chunk` rows): (value [n_out],
+    S [n_out]) with the same exact integers and conditioning scale."""
+    n_out = w.shape[0]
+    val = np.zeros(n_out)
+    mag = np.zeros(n_out)
+    if qtype in (2, 6, 8):
+        bb = {2: 18, 6: 22, 8: 34}[qtype]
+        parts = {2: q4_0_parts, 6: q5_0_parts, 8: q8_0_parts}[qtype]
+        nb = w.shape[1] // bb
+        dx, qx = q8_0_parts(xq)
+        for r0 in range(0, n_out, chunk):
+            r1 = min(n_out, r0 + chunk)
+            dw, qw = parts(w[r0:r1].reshape(-1, bb))
+            prod = qw.reshape(r1 - r0, nb, 32) * qx[None]
+            scale = dw.astype(np.float64).reshape(r1 - r0, nb) * dx.astype(np.float64)[None]
+            val[r0:r1] = (scale * prod.sum(axis=2)).sum(axis=1)
+            mag[r0:r1] = (np.abs(scale) * np.abs(prod).sum(axis=2)).sum(axis=1)
+        return val, mag
+    xb = xq.reshape(-1, 292)
+    nb = xb.shape[0]
+    dx = xb[:, 0:4].copy().view(np.float32)[:, 0].astype(np.float64)
+    q8 = xb[:, 4:260].view(np.int8).astype(np.int64)
+    bs = xb[:, 260:292].copy().view(np.int16).astype(np.int64)
+    for r0 in range(0, n_out, chunk):
+        r1 = min(n_out, r0 + chunk)
+        n = r1 - r0
+        if qtype in (12, 13):
+            bb = 144 if qtype == 12 else 176
+            d, dmin, sc, m, codes = (q4_k_parts if qtype == 12 else q5_k_parts)(w[r0:r1].reshape(-1, bb))
+            sub = np.repeat(np.arange(8), 32)
+            t = (sc[:, sub] * codes).reshape(n, nb, 256) * q8[None]
+            isum = t.sum(axis=2)
+            mm = m.reshape(n, nb, 8)
+            imin = (mm * bs.reshape(nb, 8, 2).sum(axis=2)[None]).sum(axis=2)
+            dd = d.astype(np.float64).reshape(n, nb) * dx[None]
+            dm = dmin.astype(np.float64).reshape(n, nb) * dx[None]
+            val[r0:r1] = (dd * isum - dm * imin).sum(axis=1)
+            tm = np.abs(mm[:, :, sub] * q8[None]).sum(axis=2)
+            mag[r0:r1] = (np.abs(dd) * np.abs(t).sum(axis=2) + np.abs(dm) * tm).sum(axis=1)
+        elif qtype == 14:
+            d, sc, codes = q6_k_parts(w[r0:r1].reshape(-1, 210))
+            sub = np.repeat(np.arange(16), 16)
+            t = (sc[:, sub] * (codes - 32)).reshape(n, nb, 256) * q8[None]
+            dd = d.astype(np.float64).reshape(n, nb) * dx[None]
+            val[r0:r1] = (dd * t.sum(axis=2)).sum(axis=1)
+            mag[r0:r1] = (np.abs(dd) * np.abs(t).sum(axis=2)).sum(axis=1)
+        else:
+            raise ValueError(qtype)
+    return val, mag
+
+
+def f32_rows_f64(qtype: int, w: np.ndarray, x: np.ndarray, chunk: int = 4096):
+    """f32_dot_f64 for every row of w (chunks of `chunk` rows): (value, S)."""
+    n_out, n = w.shape[0], x.size
+    xv = x.astype(np.float64)
+    val = np.zeros(n_out)
+    mag = np.zeros(n_out)
+    for r0 in range(0, n_out, chunk):
+        r1 = min(n_out, r0 + chunk)
+        wd = dequant(qtype, w[r0:r1]).reshape(r1 - r0, n).astype(np.float64)
+        val[r0:r1] = wd @ xv
+        mag[r0:r1] = np.abs(wd) @ np.abs(xv)
+    return val, mag
+
+
 def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
     """src/cpu_kernel.c:220-242 in numpy: the squares summed in float64 in
     index order (np.add.accumulate is sequential), the mean rounded to

@@ -194,3 +194,32 @@ def test_registry_refusals_without_gpu():
     assert k.edgexpu_kernels_lookup_weight(C.addressof(buf)) is None
     assert k.edgexpu_kernels_unregister_weight(C.addressof(buf)) == 0
     assert k.edgexpu_kernels_unregister_weight(None) == 0
+
+
+REF_INCLUDE = "/root/reference/include"
+
+
+@pytest.mark.skipif(not os.path.isdir(REF_INCLUDE), reason="the reference's headers are absent")
+def test_drop_in_header_compiles_with_reference_headers(tmp_path):
+    """A C translation unit that includes the reference's own gguf_quant.h and
+    cpu_kernel.h together with include/edgexpu_kernels.h compiles under
+    -Wall -Wextra -Werror (every function both declare has the same
+    signature), and links against libedgexpu_kernels.so with every
+    reference-named entry point resolved there."""
+    import subprocess
+
+    names = ["edgexpu_cpu_linear_quant", "edgexpu_cpu_linear_quant_batch", "edgexpu_cpu_softmax",
+             "edgexpu_cpu_sample_softmax"] + [n for n in declared("edgexpu_kernels.h") if n.startswith("edgexpu_gguf_")]
+    src = tmp_path / "dropin.c"
+    src.write_text(
+        "#include \"edgexpu/gguf_quant.h\"\n#include \"edgexpu/cpu_kernel.h\"\n#include \"edgexpu_kernels.h\"\n"
+        "#include <stdio.h>\n"
+        "int main(void) {\n    void (*volatile fns[])(void) = {\n"
+        + "".join(f"        (void (*)(void)){n},\n" for n in names)
+        + "    };\n    printf(\"%p\\n\", (void *)fns[0]);\n    return 0;\n}\n")
+    obj, exe = tmp_path / "dropin.o", tmp_path / "dropin"
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Wextra", "-Werror", "-Wno-cast-function-type", "-I", REF_INCLUDE,
+                    "-I", os.path.join(ROOT, "include"), "-c", str(src), "-o", str(obj)], check=True)
+    libdir = os.path.dirname(E.KERNELS_SO)
+    subprocess.run(["gcc", str(obj), "-o", str(exe), "-L", libdir, "-ledgexpu_kernels",
+                    "-Wl,--allow-shlib-undefined", "-Wl,--no-undefined"], check=True)

@@ -168,17 +168,18 @@ def test_linear_random_vs_oracle(hipdev, ora, qt, n_in, n_out, m):
 
 @pytest.mark.parametrize("qt,n_in,n_out", [(12, 4096, 14336), (12, 14336, 4096), (8, 576, 49152), (14, 9728, 2560)])
 def test_linear_full_shape(hipdev, ora, qt, n_in, n_out):
-    """Workload shapes at full size; tolerance against the largest block-term scale."""
+    """Workload shapes at full size: every row within 1e-5 of its own
+    conditioning scale, against the oracle and against the float64
+    restatement (exact block integers)."""
     rng = np.random.default_rng(5 + qt + n_in)
     w = synth.np_weights(qt, n_out, n_in, rng)
     x = synth.np_activations(1, n_in, rng)
     want = ora.linear_quant_batch(x, w, qt, None, 1, n_out, n_in)
     got = E.linear_quant_batch(dev(w), qt, dev(x), n_out, n_in).cpu().numpy()
-    sample = rng.choice(n_out, 64, replace=False)
-    S = q8_scales(ora, qt, w[sample], x)[0]
-    assert_tol(got[0, sample], want[0, sample], S, "sampled rows")
-    # every row: relative to the row-sampled conditioning level
-    assert np.abs(got - want).max() <= TOL * S.max()
+    xq = ora.quantize_q8_0(x[0]) if qt == 8 else ora.quantize_q8_k(x[0])
+    exact, S = npref.q8_rows_f64(qt, w, xq)
+    assert_tol(want[0], exact.astype(np.float32), S, "oracle vs float64")
+    assert_tol(got[0], want[0], S, f"{TN[qt]} {n_out}x{n_in} every row")
 
 
 @pytest.mark.parametrize("qt", [8, 12, 14])
@@ -280,6 +281,25 @@ def test_prefill_gemm_f16_vs_oracle(hipdev, ora, n_in, n_out, m):
     err = np.abs(got.astype(np.float64) - want) / (S + np.abs(bias)[None, :])
     assert err.max() <= F16_TOL, f"worst {err.max():.3e}"
     assert np.median(err) < 1e-4
+
+
+def test_prefill_gemm_f16_full_shape(hipdev, ora):
+    """EDGEXPU_HIP_PREFILL_F16 at the [14336 x 4096] prefill shape, m = 512:
+    a row sample within 1e-3 of its conditioning scale (float64 restatement)."""
+    L = hipdev
+    n_in, n_out, m = 4096, 14336, 512
+    rng = np.random.default_rng(8811)
+    w = synth.np_weights(12, n_out, n_in, rng)
+    x = synth.np_activations(m, n_in, rng)
+    assert L.set_prefill_mode(1) == 1
+    try:
+        got = E.linear_quant_batch(dev(w), 12, dev(x), n_out, n_in).cpu().numpy()
+    finally:
+        assert L.set_prefill_mode(0) == 1
+    rows = np.sort(rng.choice(n_out, 256, replace=False))
+    exact, S = npref.q4k_q8k_gemm_f64(w[rows], _q8k_rows(ora, x))
+    err = np.abs(got[:, rows].astype(np.float64) - exact) / S
+    assert err.max() <= F16_TOL, f"worst {err.max():.3e}"
 
 
 @pytest.mark.parametrize("n_in,n_out,m", [(4096, 300, 200), (2560, 130, 64), (2048, 140, 300), (2048, 11008, 300)])
@@ -440,6 +460,29 @@ def test_logits_and_argmax(hipdev, ora, qt, n, vocab, chunk):
     assert b == int(np.argmax(got))           # GPU argmax is exact over GPU scores
     top2 = np.sort(want)[-2:]
     if top2[1] - top2[0] > 2 * TOL * scale:  # unambiguous winner: must agree with the oracle
+        assert b == want_best
+
+
+@pytest.mark.parametrize("qt,n,vocab,chunk", [(12, 4096, 128256, 8192), (14, 2560, 151936, 0)])
+def test_logits_full_vocabulary(hipdev, ora, qt, n, vocab, chunk):
+    """The full output matrices the decode step times: [128256 x 4096] Q4_K in
+    8192-row chunks and [151936 x 2560] Q6_K, f32 hidden vector.  Every score
+    within 1e-5 of its row's conditioning scale sum |w x| (float64
+    restatement), against the oracle; the greedy index is the lowest one of
+    the largest device score, and the oracle's when its winner is clear."""
+    rng = np.random.default_rng(31 + qt + vocab)
+    w = synth.np_weights(qt, vocab, n, rng)
+    h = rng.normal(0, 1, n).astype(np.float32)
+    want, want_best = ora.logits(h, w, qt, None, vocab, n, chunk)
+    scores, best = E.logits(dev(w), qt, dev(h[None, :]), vocab, n, chunk_rows=chunk)
+    got = scores.cpu().numpy()[0]
+    exact, S = npref.f32_rows_f64(qt, w, h)
+    assert_tol(want, exact.astype(np.float32), S, "oracle vs float64")
+    assert_tol(got, want, S, f"logits {TN[qt]} [{vocab} x {n}]")
+    b = int(best.cpu().numpy()[0])
+    assert b == int(np.argmax(got))
+    top2 = np.sort(want)[-2:]
+    if top2[1] - top2[0] > 2 * TOL * S[np.argsort(want)[-2:]].max():
         assert b == want_best
 
 
