@@ -273,14 +273,18 @@ __device__ __forceinline__ v4u rsrc_words(const void *base, uint32_t bytes) {
 }
 
 // One LDS DMA: each lane's 16 bytes at base + soff + voff land at LDS byte
-// address lds + 16 * lane.
+// address lds + 16 * lane.  M0 (which holds the LDS address) is a register
+// the compiler reserves, so the block restores it before returning.
 __device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, const v4u &rs, uint32_t soff) {
+    uint32_t saved;
     asm volatile(
-        "s_mov_b32 m0, %0\n\t"
-        "buffer_load_dwordx4 %1, %2, %3 offen lds"
-        :
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
         : "s"(lds), "v"(voff), "s"(rs), "s"(soff)
-        : "memory", "m0");
+        : "memory");
 }
 
 // s_waitcnt vmcnt(N): at most N of this wave's DMAs still in flight.

@@ -623,6 +623,34 @@ edgexpu_hip_weight *edgexpu_hip_weight_upload(const uint8_t *blocks, uint32_t ty
     return w;
 }
 
+void *edgexpu_hip_upload_bytes(const void *host, size_t n) {
+    if (!ensure_init()) return nullptr;
+    if (host == nullptr || n == 0) {
+        set_error(-2, "edgexpu_hip_upload_bytes: bad arguments (host=%p n=%zu)", host, n);
+        return nullptr;
+    }
+    void *dev = nullptr;
+    if (!hip_ok(hipMalloc(&dev, align_up(n, 256)), "hipMalloc upload")) return nullptr;
+    if (!hip_ok(hipMemcpy(dev, host, n, hipMemcpyHostToDevice), "upload bytes")) {
+        (void)hipFree(dev);
+        return nullptr;
+    }
+    return dev;
+}
+
+int edgexpu_hip_download_bytes(void *host, const void *dev, size_t n) {
+    if (!ensure_init()) return 0;
+    if (host == nullptr || dev == nullptr) {
+        set_error(-2, "edgexpu_hip_download_bytes: bad arguments");
+        return 0;
+    }
+    return hip_ok(hipMemcpy(host, dev, n, hipMemcpyDeviceToHost), "download bytes") ? 1 : 0;
+}
+
+void edgexpu_hip_free_bytes(void *dev) {
+    if (dev != nullptr) (void)hipFree(dev);
+}
+
 edgexpu_hip_weight *edgexpu_hip_weight_wrap(const void *dev_blocks, uint32_t type, int n_out, int n_in,
                                             const float *dev_bias) {
     if (dev_blocks == nullptr || n_out <= 0 || edgexpu_hip_row_bytes(type, n_in) == 0) {

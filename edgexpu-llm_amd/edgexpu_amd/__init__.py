@@ -71,6 +71,9 @@ class HipLib:
         self.weight_upload = _sig(L, "edgexpu_hip_weight_upload", _vp, [_vp, C.c_uint32, C.c_int, C.c_int, _vp])
         self.weight_wrap = _sig(L, "edgexpu_hip_weight_wrap", _vp, [_vp, C.c_uint32, C.c_int, C.c_int, _vp])
         self.weight_free = _sig(L, "edgexpu_hip_weight_free", None, [_vp])
+        self.upload_bytes = _sig(L, "edgexpu_hip_upload_bytes", _vp, [_vp, C.c_size_t])
+        self.download_bytes = _sig(L, "edgexpu_hip_download_bytes", C.c_int, [_vp, _vp, C.c_size_t])
+        self.free_bytes = _sig(L, "edgexpu_hip_free_bytes", None, [_vp])
         self.linear_dev = _sig(L, "edgexpu_hip_linear_quant_batch_dev", C.c_int,
                                [_vp, _vp, _vp, C.c_uint32, _vp, C.c_int, C.c_int, C.c_int, _vp])
         self.linear_group_dev = _sig(L, "edgexpu_hip_linear_quant_group_dev", C.c_int,
@@ -366,3 +369,83 @@ def gate_up_silu(w_gate, w_up, qtype: int, x, n_ff: int, n_in: int, norm_weight=
                                w_up.data_ptr(), qtype, _ptr(b_gate), _ptr(b_up), m, n_ff, n_in, _stream()),
             "gate_up_silu")
     return out
+
+
+# ---------------------------------------------------------------- GGUF upload
+
+
+class GgufTensor(C.Structure):
+    """edgexpu_gguf_up_tensor (include/edgexpu_gguf_upload.h)."""
+    _fields_ = [("name", C.c_char * 96), ("n_dims", C.c_uint32), ("type", C.c_uint32),
+                ("dims", C.c_uint64 * 4), ("offset", C.c_uint64), ("nbytes", C.c_uint64)]
+
+
+class GgufTable(C.Structure):
+    """edgexpu_gguf_up_table."""
+    _fields_ = [("version", C.c_uint32), ("alignment", C.c_uint32), ("tensor_count", C.c_uint64),
+                ("kv_count", C.c_uint64), ("data_offset", C.c_uint64), ("file_size", C.c_uint64),
+                ("n_tensors", C.c_uint32), ("tensors", C.POINTER(GgufTensor))]
+
+
+class Gguf:
+    """Bindings of include/edgexpu_gguf_upload.h (libedgexpu_kernels.so)."""
+
+    def __init__(self, path: str = KERNELS_SO):
+        if not os.path.exists(path):
+            raise HipError(f"{path} is missing: build it with `make -C edgexpu-llm_amd`")
+        L = C.CDLL(path)
+        self._read = _sig(L, "edgexpu_gguf_up_read_table", C.c_int,
+                          [C.c_char_p, C.POINTER(GgufTable), C.c_char_p, C.c_size_t])
+        self._free_table = _sig(L, "edgexpu_gguf_up_table_free", None, [C.POINTER(GgufTable)])
+        self._upload = _sig(L, "edgexpu_gguf_device_upload", _vp, [C.c_char_p, C.c_char_p, C.c_size_t])
+        self._dtable = _sig(L, "edgexpu_gguf_device_table", C.POINTER(GgufTable), [_vp])
+        self._dtensor = _sig(L, "edgexpu_gguf_device_tensor", _vp, [_vp, C.c_char_p])
+        self._dweight = _sig(L, "edgexpu_gguf_device_weight", _vp,
+                             [_vp, C.c_char_p, C.c_int, C.c_int, C.c_char_p, C.c_size_t])
+        self._dfree = _sig(L, "edgexpu_gguf_device_free", None, [_vp])
+
+    @staticmethod
+    def _table_dict(t: GgufTable) -> dict:
+        tensors = []
+        for i in range(t.n_tensors):
+            e = t.tensors[i]
+            tensors.append({"name": e.name.decode(errors="replace"), "n_dims": e.n_dims, "type": e.type,
+                            "dims": list(e.dims)[:e.n_dims], "offset": e.offset, "nbytes": e.nbytes})
+        return {"version": t.version, "alignment": t.alignment, "tensor_count": t.tensor_count,
+                "kv_count": t.kv_count, "data_offset": t.data_offset, "file_size": t.file_size,
+                "tensors": tensors}
+
+    def read_table(self, path: str) -> dict:
+        """The tensor table of a GGUF v3 file; raises ValueError with the library's message."""
+        t = GgufTable()
+        err = C.create_string_buffer(256)
+        if not self._read(path.encode(), C.byref(t), err, 256):
+            raise ValueError(err.value.decode(errors="replace"))
+        try:
+            return self._table_dict(t)
+        finally:
+            self._free_table(C.byref(t))
+
+    def upload(self, path: str) -> int:
+        """The file's data section on the GPU (an opaque model handle)."""
+        err = C.create_string_buffer(256)
+        h = self._upload(path.encode(), err, 256)
+        if not h:
+            raise ValueError(err.value.decode(errors="replace"))
+        return h
+
+    def device_table(self, h: int) -> dict:
+        return self._table_dict(self._dtable(h).contents)
+
+    def device_tensor(self, h: int, name: str) -> int | None:
+        return self._dtensor(h, name.encode())
+
+    def device_weight(self, h: int, name: str, n_out: int, n_in: int) -> int:
+        err = C.create_string_buffer(256)
+        w = self._dweight(h, name.encode(), n_out, n_in, err, 256)
+        if not w:
+            raise ValueError(err.value.decode(errors="replace"))
+        return w
+
+    def free(self, h: int):
+        self._dfree(h)

@@ -92,6 +92,13 @@ edgexpu_hip_weight *edgexpu_hip_weight_upload(const uint8_t *blocks, uint32_t ty
 edgexpu_hip_weight *edgexpu_hip_weight_wrap(const void *dev_blocks, uint32_t type, int n_out, int n_in,
                                             const float *dev_bias);
 void edgexpu_hip_weight_free(edgexpu_hip_weight *w);
+/* One device allocation holding a copy of n bytes of host memory (pageable
+ * memory or a mapped file; copied synchronously), for the model upload of
+ * edgexpu_gguf_upload.h.  NULL on error.  Free with edgexpu_hip_free_bytes. */
+void *edgexpu_hip_upload_bytes(const void *host, size_t n);
+/* Copies n bytes of device memory to host memory (synchronous). */
+int edgexpu_hip_download_bytes(void *host, const void *dev, size_t n);
+void edgexpu_hip_free_bytes(void *dev);
 const void *edgexpu_hip_weight_data(const edgexpu_hip_weight *w);
 uint32_t edgexpu_hip_weight_type(const edgexpu_hip_weight *w);
 int edgexpu_hip_weight_n_out(const edgexpu_hip_weight *w);
