@@ -221,9 +221,10 @@ def _q8k_rows(ora, x):
 
 
 @pytest.mark.parametrize("n_in,n_out,m", [(4096, 300, 64), (2560, 515, 100), (256, 70, 129), (14336, 130, 64),
-                                          (4096, 257, 200), (1024, 128, 128), (1280, 200, 64), (2048, 16385, 70)])
+                                          (4096, 257, 200), (1024, 128, 128), (1280, 200, 64), (2048, 16385, 70),
+                                          (4096, 300, 16), (2560, 515, 23), (14336, 260, 40), (1280, 1100, 63)])
 def test_prefill_gemm_vs_oracle(hipdev, ora, n_in, n_out, m):
-    """m >= 64 Q4_K products run on the matrix cores with exact block integers;
+    """m >= 16 Q4_K products run on the matrix cores with exact block integers;
     every output within the fp32 bound of the reference (oracle) on its
     conditioning scale.  Shapes cover ragged token and row counts, one
     super-block, the K range split in two (odd super-block count 5 included)
