@@ -73,55 +73,18 @@
 #include <stdint.h>
 
 #include "common.h"
+#include "gemm_common.h"
 #include "q8k.h"
 
 namespace exq {
 
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef float v16f __attribute__((ext_vector_type(16)));
-typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-
-constexpr int kTiles = 4;                 // MFMA token tiles of 32 per workgroup
-constexpr int kTokB = 32 * kTiles;        // 128 tokens per workgroup
-constexpr int kWaves = 8;                 // two per SIMD
-constexpr int kRowsB = 32 * kWaves;       // 256 weight rows per workgroup
-constexpr int kThreads = 64 * kWaves;
-// Activation pack, one block per (super-block, 128-token block):
-//   codes  [half 2][K-step 8][tile 4][MFMA lane 64][8 fp16]   64 KiB
-//   mn     [tile 4][MFMA lane 64][8 fp16]  bsums for the min term
-//   dx     [128] f32, sq [128] int32 (sum |q8| of the super-block)
-constexpr int kPkHalf = 8 * kTiles * 1024;        // 32768
-constexpr int kPkCodes = 2 * kPkHalf;
-constexpr int kPkMn = kTiles * 1024;
-constexpr int kPkDx = kTokB * 4;
-constexpr int kPkSq = kTokB * 4;
-constexpr int kPkExtra = kPkMn + kPkDx + kPkSq;   // 5120
-constexpr int kPkBlk = kPkCodes + kPkExtra;       // 70656
-constexpr int kHalfChunks = kPkHalf / 1024;       // 1 KiB DMA chunks per half
-constexpr int kExtraChunks = kPkExtra / 1024;
-static_assert(kHalfChunks == 4 * kWaves, "four code chunks per wave and half super-block");
-static_assert(kExtraChunks <= kWaves && kPkExtra % 1024 == 0, "one extras chunk per wave at most");
+constexpr int kRowsB = 32 * kWaves;  // 256 weight rows per workgroup
 // largest sum |q8| of a token for which one chain of 256 products is exact:
 // 17753 * 945 < 2^24
 constexpr int kExactSqMax = 16777215 / 945;
 constexpr int kMaxSplit = 4;
-constexpr int kGemmCounters = 1024;               // arrival counters in the workspace
 
 // --------------------------------------------------------------- packing
-
-__device__ __forceinline__ uint32_t h2_bits(int lo, int hi) {
-    const _Float16 l = (_Float16)(float)lo, h = (_Float16)(float)hi;
-    return (uint32_t)__builtin_bit_cast(uint16_t, l) | ((uint32_t)__builtin_bit_cast(uint16_t, h) << 16);
-}
-
-__device__ __forceinline__ int sbyte(uint32_t w, int b) { return (int)(int8_t)((w >> (8 * b)) & 0xffu); }
-
-__device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
 
 constexpr int kPackTokensPerWave = 1;
 constexpr int kPackWaves = 4;  // consecutive tokens of one super-block per workgroup
@@ -265,38 +228,6 @@ struct GmArgs {
     unsigned *cnt;        // [ntiles] arrival counters, zero between launches
 };
 
-// Buffer descriptor words (gfx9): base, base_hi | stride 0, num_records,
-// dword format.  Loads whose per-lane offset is at or past num_records read 0.
-__device__ __forceinline__ v4u rsrc_words(const void *base, uint32_t bytes) {
-    const uint64_t a = (uint64_t)(uintptr_t)base;
-    return v4u{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, bytes, 0x00020000u};
-}
-
-// One LDS DMA: each lane's 16 bytes at base + soff + voff land at LDS byte
-// address lds + 16 * lane.  M0 (which holds the LDS address) is a register
-// the compiler reserves, so the block restores it before returning.
-__device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, const v4u &rs, uint32_t soff) {
-    uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
-        "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "s"(lds), "v"(voff), "s"(rs), "s"(soff)
-        : "memory");
-}
-
-// s_waitcnt vmcnt(N): at most N of this wave's DMAs still in flight.
-template <int N>
-__device__ __forceinline__ void wait_dma() {
-    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
-
 // Constants of one super-block for one row and sub-blocks 4h .. 4h+3
 // (get_scale_min_k4, src/gguf_quant.c:212-220, for four sub-blocks at once):
 // the four 6-bit scales, the min operand, d and -dmin.
@@ -353,13 +284,6 @@ __device__ __forceinline__ v8h w_operand(uint32_t u, const HalfConst &c, const N
     const h2 b3 = __builtin_elementwise_fma(y3, c.mhi, c.ahi);
     return v8h{b0.x, b0.y, b1.x, b1.y, b2.x, b2.y, b3.x, b3.y};
 }
-
-__device__ __forceinline__ v16f mfma(v8h a, v8h b, v16f c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ v8h lds_v8h(const uint8_t *p) { return *reinterpret_cast<const v8h *>(p); }
-__device__ __forceinline__ v4u lds_v4u(const uint8_t *p) { return *reinterpret_cast<const v4u *>(p); }
 
 // C[g][tt]: the wave's 2 row halves x 2 token tiles.
 typedef v16f Tiles[2][2];
@@ -444,17 +368,6 @@ __device__ __forceinline__ void combine(const uint8_t *ex, int tq, int lane, con
         }
         __builtin_amdgcn_sched_barrier(0);
     }
-}
-
-// Wavefront maximum through DPP row shifts and broadcasts (no LDS round trips).
-__device__ __forceinline__ int wave_max_dpp(int v) {
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x111, 0xf, 0xf, false));  // row_shr:1
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x112, 0xf, 0xf, false));  // row_shr:2
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x114, 0xf, 0xf, false));  // row_shr:4
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x118, 0xf, 0xf, false));  // row_shr:8
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xa, 0xf, false));  // row_bcast:15
-    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x143, 0xc, 0xf, false));  // row_bcast:31
-    return __builtin_amdgcn_readlane(v, 63);
 }
 
 // Per-wave state of the main loop.
@@ -607,58 +520,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     wait_dma<0>();  // the requests past the end have landed before the LDS is released
 
     if (a.nsplit > 1) {
-        // partial tile out; the last of the tile's workgroups adds them up in
-        // split order.  Release: every thread's stores are complete (vmcnt 0)
-        // before the barrier, one thread writes them back to the device level
-        // and counts the arrival; the last arriver invalidates its caches
-        // (acquire) before any thread reads the others' partials.
-        float4 *part = reinterpret_cast<float4 *>(a.part);
-        const size_t base = ((size_t)z * a.ntiles + tile) * 16;
-#pragma unroll
-        for (int g = 0; g < 2; ++g)
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    part[(base + (2 * g + tt) * 4 + i) * kThreads + tid] =
-                        make_float4(acc[g][tt][4 * i], acc[g][tt][4 * i + 1], acc[g][tt][4 * i + 2],
-                                    acc[g][tt][4 * i + 3]);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (tid == 0) {
-            const unsigned old =
-                __hip_atomic_fetch_add(&a.cnt[tile], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-            const int last = old == (unsigned)(a.nsplit - 1);
-            if (last) {
-                __hip_atomic_store(&a.cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            }
-            *s_last = last;
-        }
-        __syncthreads();
-        if (!*s_last) return;
-        Tiles sum;
-        for (int zz = 0; zz < a.nsplit; ++zz) {
-            const size_t bz = ((size_t)zz * a.ntiles + tile) * 16;
-#pragma unroll
-            for (int g = 0; g < 2; ++g)
-#pragma unroll
-                for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float4 p = zz == z ? make_float4(acc[g][tt][4 * i], acc[g][tt][4 * i + 1],
-                                                               acc[g][tt][4 * i + 2], acc[g][tt][4 * i + 3])
-                                                 : part[(bz + (2 * g + tt) * 4 + i) * kThreads + tid];
-                        const float pv[4] = {p.x, p.y, p.z, p.w};
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            sum[g][tt][4 * i + e] = zz == 0 ? pv[e] : sum[g][tt][4 * i + e] + pv[e];
-                    }
-        }
-#pragma unroll
-        for (int g = 0; g < 2; ++g)
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) acc[g][tt] = sum[g][tt];
+        // the wave's four tiles in the order (row half, token tile)
+        v16f(&flat)[4] = reinterpret_cast<v16f(&)[4]>(acc);
+        if (!split_reduce<4>(flat, a.part, a.cnt, a.nsplit, a.ntiles, tile, z, s_last)) return;
     }
 
     // bias after the whole dot (the reference's b + dot), then the store
@@ -687,20 +551,9 @@ bool gemm_q8_supported(int type, int n_out, int K, int m) {
     return type == kTypeQ4_K && K % kQKK == 0 && n_out > 0 && m >= 1;
 }
 
-// 128-token blocks of the activation pack for m tokens.
-static int pack_tblocks(int m) { return (m + kTokB - 1) / kTokB; }
-
 size_t gemm_q4k_pack_bytes(int m, int K) { return (size_t)(K / kQKK) * pack_tblocks(m) * kPkBlk; }
 
-// K split: enough workgroups to cover the chip's 256 CUs where the tiles
-// alone cannot, at least two super-blocks per workgroup.
-static int gemm_split(int ntiles, int nblk) {
-    int s = 256 / ntiles;
-    if (s > kMaxSplit) s = kMaxSplit;
-    if (s > nblk / 2) s = nblk / 2;
-    if (ntiles > kGemmCounters) s = 1;
-    return s < 1 ? 1 : s;
-}
+static int gemm_split(int ntiles, int nblk) { return gemm_split_for(ntiles, nblk, kMaxSplit); }
 
 static int gemm_tiles(int m, int n_out) { return ((n_out + kRowsB - 1) / kRowsB) * pack_tblocks(m); }
 

@@ -15,7 +15,7 @@
 
 using namespace exq;
 
-// kernels (quantize.hip, dequant.hip, gemv.hip, gemm.hip)
+// kernels (quantize.hip, dequant.hip, gemv.hip, gemm.hip, gemm_kq.hip)
 hipError_t launch_quantize_q8_0(const float *x, int m, int K, int ldx, uint8_t *packed, hipStream_t st);
 hipError_t launch_quantize_q8_k(const float *x, int m, int K, int ldx, uint8_t *packed, hipStream_t st);
 hipError_t launch_dequantize(const uint8_t *src, int type, unsigned long long n, float *dst, hipStream_t st);
@@ -43,6 +43,13 @@ hipError_t launch_gemm_f16(const uint8_t *w, size_t row_bytes, int n_out, int K,
                            size_t xq_stride, void *ws, const float *bias, float *out, int ldo, hipStream_t st);
 size_t gemm_f16_workspace(int m, int n_out, int K);
 bool gemm_q8_supported(int type, int n_out, int K, int m);
+bool gemm_kq_supported(int type, int n_out, int K, int m);
+size_t gemm_kq_repack_bytes(int n_out, int K);
+size_t gemm_kq_part_bytes(int m, int n_out, int K);
+hipError_t launch_kq_repack(int type, const uint8_t *w, size_t row_bytes, int n_out, int K, uint8_t *rw,
+                            hipStream_t st);
+hipError_t launch_gemm_kq(int type, const uint8_t *rw, int n_out, int K, int m, const uint8_t *pack, float *part,
+                          unsigned *cnt, const float *bias, float *out, int ldo, hipStream_t st);
 bool gemv_fused_supported(int type, int K, int m);
 bool gemv_fused_f32_supported(int type, int K);
 bool gemv_fused_pro_supported(int type, int K, int pro);
@@ -296,40 +303,62 @@ void *gemm_ws(size_t bytes) {
     return g.gws;
 }
 
-// Exact Q4_K prefill GEMM of nmat matrices over one input: f32 activations
+// Formats with an exact matrix-core prefill GEMM: Q4_K straight from its
+// blocks (gemm.hip), Q5_K and Q6_K over a per-call repack (gemm_kq.hip).
+bool exact_gemm_type(uint32_t type, int n_out, int n_in, int m) {
+    return gemm_q8_supported((int)type, n_out, n_in, m) || gemm_kq_supported((int)type, n_out, n_in, m);
+}
+
+// Exact prefill GEMM of nmat matrices over one input: f32 activations
 // (x != nullptr) or Q8_K blocks already in memory (xq).  The activations are
-// packed once into the GEMM's operand layout, then one launch per matrix.
-bool run_gemm_q4k(int nmat, const void *const *w, const int *n_out, int n_in, int m, const float *x,
-                  const uint8_t *xq, size_t xq_stride, const float *const *bias, float *const *out, const int *ldo,
-                  hipStream_t st) {
-    // workspace: arrival counters | activation pack | K-split partial tiles
-    size_t part_bytes = 0;
+// packed once into the GEMM's operand layout, then one launch per matrix
+// (Q5_K / Q6_K: a repack of the matrix into the workspace, then the GEMM;
+// the launches are stream-ordered, so one repack buffer serves every matrix).
+bool run_gemm_exact(uint32_t type, int nmat, const void *const *w, const int *n_out, int n_in, int m, const float *x,
+                    const uint8_t *xq, size_t xq_stride, const float *const *bias, float *const *out, const int *ldo,
+                    hipStream_t st) {
+    const bool kq = type != (uint32_t)kTypeQ4_K;
+    // workspace: arrival counters | activation pack | K-split partial tiles | repacked weights
+    size_t part_bytes = 0, rw_bytes = 0;
     for (int z = 0; z < nmat; ++z) {
-        const size_t pb = gemm_q4k_part_bytes(m, n_out[z], n_in);
+        const size_t pb = kq ? gemm_kq_part_bytes(m, n_out[z], n_in) : gemm_q4k_part_bytes(m, n_out[z], n_in);
         part_bytes = pb > part_bytes ? pb : part_bytes;
+        const size_t rb = kq ? gemm_kq_repack_bytes(n_out[z], n_in) : 0;
+        rw_bytes = rb > rw_bytes ? rb : rw_bytes;
     }
     const size_t cnt_bytes = gemm_q4k_counter_bytes();
     const size_t pack_bytes = align_up(gemm_q4k_pack_bytes(m, n_in), (size_t)256);
-    uint8_t *ws = (uint8_t *)gemm_ws(cnt_bytes + pack_bytes + part_bytes);
+    part_bytes = align_up(part_bytes, (size_t)256);
+    uint8_t *ws = (uint8_t *)gemm_ws(cnt_bytes + pack_bytes + part_bytes + rw_bytes);
     if (ws == nullptr) return false;
     unsigned *cnt = (unsigned *)ws;
     uint8_t *pack = ws + cnt_bytes;
     float *part = part_bytes != 0 ? (float *)(pack + pack_bytes) : nullptr;
+    uint8_t *rw = pack + pack_bytes + part_bytes;
     const hipError_t e = x != nullptr ? launch_q8k_pack_f32(x, m, n_in, n_in, pack, st)
                                       : launch_q8k_pack_q8k(xq, xq_stride, m, n_in, pack, st);
     if (!hip_ok(e, "pack activations")) return false;
-    const size_t rb = edgexpu_hip_row_bytes(kTypeQ4_K, n_in);
-    for (int z = 0; z < nmat; ++z)
-        if (!hip_ok(launch_gemm_q4k((const uint8_t *)w[z], rb, n_out[z], n_in, m, pack, part, cnt,
-                                    bias != nullptr ? bias[z] : nullptr, out[z], ldo[z], st),
-                    "gemm_q4k"))
+    const size_t rb = edgexpu_hip_row_bytes(type, n_in);
+    for (int z = 0; z < nmat; ++z) {
+        const float *bz = bias != nullptr ? bias[z] : nullptr;
+        if (!kq) {
+            if (!hip_ok(launch_gemm_q4k((const uint8_t *)w[z], rb, n_out[z], n_in, m, pack, part, cnt, bz, out[z],
+                                        ldo[z], st),
+                        "gemm_q4k"))
+                return false;
+            continue;
+        }
+        if (!hip_ok(launch_kq_repack((int)type, (const uint8_t *)w[z], rb, n_out[z], n_in, rw, st), "kq repack") ||
+            !hip_ok(launch_gemm_kq((int)type, rw, n_out[z], n_in, m, pack, part, cnt, bz, out[z], ldo[z], st),
+                    "gemm_kq"))
             return false;
+    }
     return true;
 }
 
 bool use_exact_gemm(uint32_t type, int n_out, int n_in, int m) {
     return m >= kGemmMinTokens && g.prefill_mode == EDGEXPU_HIP_PREFILL_EXACT_INT8 &&
-           gemm_q8_supported((int)type, n_out, n_in, m);
+           exact_gemm_type(type, n_out, n_in, m);
 }
 
 // Workspace carve-up for m tokens of K elements.
@@ -426,14 +455,14 @@ bool run_q8_product(uint32_t type, const void *w, int n_out, int n_in, int m, co
                     float *out, int ldo, hipStream_t st) {
     const size_t rb = edgexpu_hip_row_bytes(type, n_in);
     const size_t ab = act_bytes(type, n_in);
-    if (m >= kGemmMinTokens && gemm_q8_supported((int)type, n_out, n_in, m)) {
-        if (g.prefill_mode == EDGEXPU_HIP_PREFILL_F16) {
+    if (m >= kGemmMinTokens && exact_gemm_type(type, n_out, n_in, m)) {
+        if (g.prefill_mode == EDGEXPU_HIP_PREFILL_F16 && gemm_q8_supported((int)type, n_out, n_in, m)) {
             void *ws = f16ws(gemm_f16_workspace(m, n_out, n_in));
             if (ws == nullptr) return false;
             return hip_ok(launch_gemm_f16((const uint8_t *)w, rb, n_out, n_in, m, xq, ab, ws, bias, out, ldo, st),
                           "gemm_f16");
         }
-        return run_gemm_q4k(1, &w, &n_out, n_in, m, nullptr, xq, ab, &bias, &out, &ldo, st);
+        return run_gemm_exact(type, 1, &w, &n_out, n_in, m, nullptr, xq, ab, &bias, &out, &ldo, st);
     }
     if (ldo == n_out && split_gemv(type, n_in, m)) {
         const uint8_t *wp = (const uint8_t *)w;
@@ -474,7 +503,7 @@ bool run_linear_group(uint32_t type, int nmat, const void *const *w, const int *
                       "gemv_fused");
     }
     if (use_exact_gemm(type, n_out[0], n_in, m))  // the GEMM quantizes x into its own operand layout
-        return run_gemm_q4k(nmat, w, n_out, n_in, m, x, nullptr, 0, bias, out, n_out, st);
+        return run_gemm_exact(type, nmat, w, n_out, n_in, m, x, nullptr, 0, bias, out, n_out, st);
     ActWs a;
     if (!act_ws(type, m, n_in, a)) return false;
     const hipError_t e = q8_0_family((int)type) ? launch_quantize_q8_0(x, m, n_in, n_in, a.xq, st)

@@ -272,37 +272,54 @@ def f32_dot_f64(qtype: int, wrow: np.ndarray, x: np.ndarray):
     return p.sum(), np.abs(p).sum()
 
 
-def q4k_q8k_gemm_f64(w: np.ndarray, xq: np.ndarray):
-    """Many-token Q4_K x Q8_K product in float64 with exact integer block sums.
+def kq_q8k_gemm_f64(qtype: int, w: np.ndarray, xq: np.ndarray):
+    """Many-token K-quant (Q4_K 12, Q5_K 13, Q6_K 14) x Q8_K product in
+    float64 with exact integer block sums.
 
-    w: [n_out, row_bytes] Q4_K rows; xq: [m, nb*292] Q8_K rows.  Returns
+    w: [n_out, row_bytes] rows; xq: [m, nb*292] Q8_K rows.  Returns
     (value [m, n_out], S [m, n_out]) with S the element-level conditioning
     scale of q8_dot_f64, computed with matrix products (every partial sum is
     an integer below 2**53, so float64 products are exact)."""
     n_out = w.shape[0]
     m = xq.shape[0]
-    nb = w.shape[1] // 144
-    d, dmin, sc, mn, codes = q4_k_parts(w.reshape(-1, 144))
+    bb = {12: 144, 13: 176, 14: 210}[qtype]
+    nb = w.shape[1] // bb
+    if qtype == 14:
+        d, sc, codes = q6_k_parts(w.reshape(-1, bb))
+        dmin = np.zeros_like(d)
+        mn = np.zeros((d.shape[0], 8), np.int64)
+        sub = np.repeat(np.arange(16), 16)
+        sc = sc.reshape(n_out, nb, 16)
+        codes = codes.astype(np.int64) - 32
+    else:
+        d, dmin, sc, mn, codes = (q4_k_parts if qtype == 12 else q5_k_parts)(w.reshape(-1, bb))
+        sub = np.repeat(np.arange(8), 32)
+        sc = sc.reshape(n_out, nb, 8)
     d = d.astype(np.float64).reshape(n_out, nb)
     dmin = dmin.astype(np.float64).reshape(n_out, nb)
-    sc = sc.reshape(n_out, nb, 8)
     mn = mn.reshape(n_out, nb, 8)
     codes = codes.reshape(n_out, nb, 256)
     xb = xq.reshape(m, nb, 292)
     dx = xb[:, :, 0:4].copy().view(np.float32)[:, :, 0].astype(np.float64)
     q8 = xb[:, :, 4:260].copy().view(np.int8).astype(np.float64)
-    sub = np.repeat(np.arange(8), 32)
+    msub = np.repeat(np.arange(8), 32)
     val = np.zeros((m, n_out))
     mag = np.zeros((m, n_out))
     for b in range(nb):
         ws = (sc[:, b, sub] * codes[:, b, :]).astype(np.float64)     # [n_out, 256]
-        wm = mn[:, b, sub].astype(np.float64)                          # [n_out, 256]
+        wm = mn[:, b, msub].astype(np.float64)                         # [n_out, 256]
         isum = q8[:, b, :] @ ws.T                                      # [m, n_out]
         imin = q8[:, b, :] @ wm.T
         aq = np.abs(q8[:, b, :])
         val += dx[:, b:b + 1] * (d[None, :, b] * isum - dmin[None, :, b] * imin)
-        mag += np.abs(dx[:, b:b + 1]) * (np.abs(d[None, :, b]) * (aq @ ws.T) + np.abs(dmin[None, :, b]) * (aq @ wm.T))
+        mag += np.abs(dx[:, b:b + 1]) * (np.abs(d[None, :, b]) * (aq @ np.abs(ws).T) +
+                                         np.abs(dmin[None, :, b]) * (aq @ wm.T))
     return val, mag
+
+
+def q4k_q8k_gemm_f64(w: np.ndarray, xq: np.ndarray):
+    """kq_q8k_gemm_f64 for Q4_K rows."""
+    return kq_q8k_gemm_f64(12, w, xq)
 
 
 def q8_rows_f64(qtype: int, w: np.ndarray, xq: np.ndarray, chunk: int = 2048):

@@ -21,7 +21,7 @@ pytestmark = pytest.mark.gpu
 
 TOL = 1e-5
 DEV = "cuda:0"
-TN = {8: "q8_0", 12: "q4_k", 14: "q6_k"}
+TN = E.TYPE_NAMES
 
 
 def bits(a):
@@ -256,6 +256,88 @@ def test_prefill_gemm_full_shape(hipdev, ora, n_in, n_out):
     assert_tol(got[:, rows], exact.astype(np.float32), S, f"gemm {n_out}x{n_in} m=512 (sampled rows)")
     tok = rng.choice(m, 4, replace=False)
     want = ora.linear_quant_batch(x[tok], w[rows], 12, None, 4, rows.size, n_in)
+    assert_tol(got[tok][:, rows], want, S[tok], "vs oracle")
+
+
+@pytest.mark.parametrize("qt", [13, 14])
+@pytest.mark.parametrize("n_in,n_out,m", [(2560, 300, 16), (4096, 257, 64), (256, 70, 129), (9728, 130, 100),
+                                          (1280, 515, 200), (2048, 384, 512), (1024, 16385, 33), (512, 129, 47)])
+def test_prefill_gemm_kq_vs_oracle(hipdev, ora, qt, n_in, n_out, m):
+    """m >= 16 Q5_K / Q6_K products run on the matrix cores over a per-call
+    repack, two exact chains per K-step (scale split 16 s1 + s0); every
+    output within the fp32 bound of the oracle on its conditioning scale.
+    Shapes cover one super-block, ragged tokens and rows, the K split (odd
+    super-block counts), 129 row blocks and a full 512-token block."""
+    rng = np.random.default_rng(4100 + 7 * qt + n_in + n_out + m)
+    w = synth.np_weights(qt, n_out, n_in, rng)
+    x = synth.np_activations(m, n_in, rng)
+    bias = rng.normal(0, 0.5, n_out).astype(np.float32)
+    want = ora.linear_quant_batch(x, w, qt, bias, m, n_out, n_in)
+    got = E.linear_quant_batch(dev(w), qt, dev(x), n_out, n_in, bias=dev(bias)).cpu().numpy()
+    exact, S = npref.kq_q8k_gemm_f64(qt, w, _q8k_rows(ora, x))
+    assert_tol(want - bias[None, :], exact.astype(np.float32), S, "oracle vs float64")
+    assert_tol(got, want, S + np.abs(bias)[None, :], f"{TN[qt]} gemm {n_out}x{n_in} m={m}")
+
+
+@pytest.mark.parametrize("qt", [13, 14])
+def test_prefill_gemm_kq_from_q8k(hipdev, ora, qt):
+    """The same GEMM fed with Q8_K blocks already in memory (the activation
+    pack built from the blocks, not from f32 rows): identical to the f32 entry."""
+    n_in, n_out, m = 2304, 200, 40
+    rng = np.random.default_rng(4400 + qt)
+    w = synth.np_weights(qt, n_out, n_in, rng)
+    x = synth.np_activations(m, n_in, rng)
+    xq = _q8k_rows(ora, x)
+    got = E.gemv_q8(dev(w), qt, dev(xq), m, n_out, n_in).cpu().numpy()
+    ref = E.linear_quant_batch(dev(w), qt, dev(x), n_out, n_in).cpu().numpy()
+    assert np.array_equal(got, ref)
+    exact, S = npref.kq_q8k_gemm_f64(qt, w, xq)
+    assert_tol(got, exact.astype(np.float32), S, f"{TN[qt]} from Q8_K")
+
+
+@pytest.mark.parametrize("qt", [13, 14])
+def test_prefill_gemm_kq_integers_exact(hipdev, qt):
+    """Unit d, zero dmin and integer activations with a first element of
+    -127 (so the Q8_K codes equal x and dx = 1): every super-block integer,
+    including the largest scale / quant combinations, must come out exactly."""
+    n_in, n_out, m = 512, 96, 32
+    rng = np.random.default_rng(4500 + qt)
+    w = synth.np_weights(qt, n_out, n_in, rng)
+    one = np.array([1.0], np.float16).view(np.uint8)
+    if qt == 14:
+        wb = w.reshape(n_out, -1, 210)
+        wb[:, :, 208:210] = one
+        sc = wb[:, :, 192:208].view(np.int8)
+        sc[:, :, 0] = -128  # s1 = -8, s0 = 0
+        sc[:, :, 1] = 127   # s1 = 7, s0 = 15
+    else:
+        wb = w.reshape(n_out, -1, 176)
+        wb[:, :, 0:2] = one
+        wb[:, :, 2:4] = 0
+        wb[:, :, 4:8] = 63  # scales 0..3 at their maximum
+    x = rng.integers(-127, 128, (m, n_in)).astype(np.float32)
+    x.reshape(m, -1, 256)[:, :, 0] = -127.0
+    got = E.linear_quant_batch(dev(w), qt, dev(x), n_out, n_in).cpu().numpy()
+    xq = np.stack([npref.quantize_q8_k(x[t]) for t in range(m)])
+    want, _ = npref.kq_q8k_gemm_f64(qt, w, xq)
+    assert np.all(np.abs(want) < 2**24)
+    assert np.array_equal(got.astype(np.float64), want)
+
+
+def test_prefill_gemm_q6k_full_shape(hipdev, ora):
+    """Q6_K at the [2560 x 9728] down-projection shape, m = 512: a row sample
+    against the float64 restatement, a token sample also against the oracle."""
+    n_in, n_out, m = 9728, 2560, 512
+    rng = np.random.default_rng(4600)
+    w = synth.np_weights(14, n_out, n_in, rng)
+    x = synth.np_activations(m, n_in, rng)
+    got = E.linear_quant_batch(dev(w), 14, dev(x), n_out, n_in).cpu().numpy()
+    xq = _q8k_rows(ora, x)
+    rows = np.sort(rng.choice(n_out, 192, replace=False))
+    exact, S = npref.kq_q8k_gemm_f64(14, w[rows], xq)
+    assert_tol(got[:, rows], exact.astype(np.float32), S, "q6_k gemm 2560x9728 m=512 (sampled rows)")
+    tok = rng.choice(m, 4, replace=False)
+    want = ora.linear_quant_batch(x[tok], w[rows], 14, None, 4, rows.size, n_in)
     assert_tol(got[tok][:, rows], want, S[tok], "vs oracle")
 
 

@@ -470,3 +470,22 @@ def test_oracle_sampler_matches_golden(ora, golden):
         t_o, p_o, s_o = ora.sample_softmax(x, top_p, seed)
         assert (t_o, s_o) == (tok, st), (n, seed, top_p)
         assert np.array_equal(bits(p_o), bits(p)) and np.array_equal(bits(ora.softmax(x)), bits(p))
+
+
+@pytest.mark.parametrize("qt", [12, 13, 14])
+def test_gemm_f64_restatement_vs_rows_and_oracle(ora, qt):
+    """The many-token float64 restatement the prefill GEMM tests use equals the
+    per-row restatement token by token (same exact integers, same S), and
+    agrees with the oracle's batch product within the fp32 bound."""
+    rng = np.random.default_rng(7300 + qt)
+    n_in, n_out, m = 768, 40, 5
+    w = synth.np_weights(qt, n_out, n_in, rng)
+    x = synth.np_activations(m, n_in, rng)
+    xq = np.stack([ora.quantize_q8_k(x[t]) for t in range(m)])
+    val, S = npref.kq_q8k_gemm_f64(qt, w, xq)
+    for t in range(m):
+        v1, s1 = npref.q8_rows_f64(qt, w, xq[t])
+        assert np.allclose(val[t], v1, rtol=1e-12, atol=1e-9 * s1.max())
+        assert np.allclose(S[t], s1, rtol=1e-12)
+    want = ora.linear_quant_batch(x, w, qt, None, m, n_out, n_in)
+    assert np.all(np.abs(want - val) <= 1e-5 * S)
