@@ -197,7 +197,7 @@ __global__ __launch_bounds__(256) void q8k_pack_kernel(const float *__restrict__
 // requested two steps ahead; the codes are L2 hits (every row block reads
 // them) and one step ahead is enough.  LDS (135 KiB of the 160):
 //   codes    2 slots x 32 KiB  half super-block of activation codes, one step ahead
-//   extras   2 slots x 5 KiB   bsums / d / sum |q8| of a super-block (+1 KiB dummy target)
+//   extras   2 slots x 5 KiB   bsums / d / sum |q8| of a super-block
 //   weights  3 slots x 20 KiB  per row group 5 KiB: qs pieces of both row
 //                              halves and the 64 headers; two steps ahead
 constexpr int kCodeSlots = 2;
@@ -206,8 +206,7 @@ constexpr int kWGrp = 5 * 1024;
 constexpr int kWSlot = 4 * kWGrp;
 constexpr int kLdsCodes = 0;
 constexpr int kLdsEx = kLdsCodes + kCodeSlots * kPkHalf;
-constexpr int kLdsExDummy = kLdsEx + 2 * kPkExtra;
-constexpr int kLdsW = kLdsExDummy + 1024;
+constexpr int kLdsW = kLdsEx + 2 * kPkExtra;
 constexpr int kLdsLast = kLdsW + kWSlots * kWSlot;
 constexpr int kLdsBytes = kLdsLast + 16;
 static_assert(kLdsBytes <= 160 * 1024, "the LDS rings fit the gfx950 LDS");
@@ -297,15 +296,15 @@ typedef v16f Tiles[2][2];
 // (an MFMA hides only a few VALU instructions issued behind it, and a block
 // of VALU with no MFMA in flight leaves the matrix core idle).  FIRST: the
 // chains start at zero.
-template <int P, bool FIRST>
+template <int P, bool FIRST, int NT>
 __device__ __forceinline__ void half_chains(const uint8_t *cur, const uint8_t *wq, int lane, const WConst (&wc)[2],
                                             const NibMasks &k, Tiles &C) {
     const HalfConst c0 = half_const(wc[0].sc4, P), c1 = half_const(wc[1].sc4, P);
     const v4u q00 = lds_v4u(wq + lane * 16), q01 = lds_v4u(wq + 1024 + lane * 16);
     const v4u q10 = lds_v4u(wq + 2048 + lane * 16), q11 = lds_v4u(wq + 3072 + lane * 16);
-    v8h a[2];
+    v8h a[NT];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) a[tt] = lds_v8h(cur + tt * 1024 + lane * 16);
+    for (int tt = 0; tt < NT; ++tt) a[tt] = lds_v8h(cur + tt * 1024 + lane * 16);
     v8h b0 = w_operand(q00[0], c0, k), b1 = w_operand(q10[0], c1, k);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -316,19 +315,28 @@ __device__ __forceinline__ void half_chains(const uint8_t *cur, const uint8_t *w
             nb1 = w_operand(s + 1 < 4 ? q10[s + 1] : q11[s - 3], c1, k);
         }
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
+        for (int tt = 0; tt < NT; ++tt) {
             C[0][tt] = mfma(a[tt], b0, (FIRST && s == 0) ? v16f{} : C[0][tt]);
             C[1][tt] = mfma(a[tt], b1, (FIRST && s == 0) ? v16f{} : C[1][tt]);
             if (s + 1 < 8) a[tt] = lds_v8h(cur + (s + 1) * 4096 + tt * 1024 + lane * 16);
         }
-        // MFMA, VALU x5, MFMA, DS read, VALU x4, MFMA, VALU x5, MFMA, DS read, VALU x4
+        if (NT == 2) {
+            // MFMA, VALU x5, MFMA, DS read, VALU x4, MFMA, VALU x5, MFMA, DS read, VALU x4
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+            for (int i = 0; i < 2; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+            }
+        } else {
+            // MFMA, VALU x9, DS read, MFMA, VALU x9
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 9, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 9, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
         b0 = nb0;
@@ -339,12 +347,12 @@ __device__ __forceinline__ void half_chains(const uint8_t *cur, const uint8_t *w
 // acc += dx * (C * d - mn * dmin) for the wave's tiles (MN = false:
 // acc += dx * C * d).  `ex` is the extras slot, `tq` the wave's first token
 // tile in the workgroup (0 or 2).
-template <bool MN>
+template <bool MN, int NT>
 __device__ __forceinline__ void combine(const uint8_t *ex, int tq, int lane, const WConst (&wc)[2], const Tiles &C,
                                         Tiles &acc) {
     const int h = lane >> 5;
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
+    for (int tt = 0; tt < NT; ++tt) {
         v16f mn[2] = {v16f{}, v16f{}};
         if (MN) {
             const v8h bs = lds_v8h(ex + (tq + tt) * 1024 + lane * 16);
@@ -378,18 +386,22 @@ struct GmLoop {
     uint32_t smem;            // LDS address of the workgroup's buffer
     NibMasks km;
     int lane, wave, grp, th, sb0, sblast;
+    bool codes_on;            // the wave's code chunks (token tile wave % 4) hold a token below m
+    bool ex_on;               // the wave's extras chunk: bsums of a live tile, or dx / sum |q8|
 };
 
 // Step s (half hf = s & 1 of super-block sb0 + s / 2) requests, in this
 // order: the codes of step s + 1 (4 DMAs, a quarter of the half super-block),
-// on odd steps the extras of the next super-block (1 DMA; waves 5..7 repeat
-// chunk 4 into the dummy target), then the weights of step s + 2 (3 DMAs:
+// on odd steps the extras of the next super-block (1 DMA, waves 0..4), then
+// the weights of step s + 2 (3 DMAs:
 // qs pieces 0 and 1 of row half th of the wave's row group, the group's 64
 // headers -- both token-half waves request them, the same bytes; rows past
 // n_out read zeros).  Requests past the end of the K range re-request its
 // last super-block into slots nobody reads again, so every step issues its
 // weights last: a wait for vmcnt(3) at the start of step s + 1 leaves
-// exactly the weights of step s + 2 in flight.
+// exactly the weights of step s + 2 in flight, however many code and extras
+// chunks a wave skips (those of token tiles past the last token, which no
+// wave reads).
 constexpr int kWLoads = 3;
 
 __device__ __forceinline__ void step_requests(const GmLoop &L, int s) {
@@ -398,19 +410,19 @@ __device__ __forceinline__ void step_requests(const GmLoop &L, int s) {
     const int sbc = min(L.sb0 + (s1 >> 1), L.sblast);
     const uint32_t cdst = L.smem + kLdsCodes + (uint32_t)(s1 % kCodeSlots) * kPkHalf;
     const uint32_t cso = L.pk0 + (uint32_t)sbc * L.pk_sb + (uint32_t)(s1 & 1) * kPkHalf;
+    if (L.codes_on) {
 #pragma unroll
-    for (int i = 0; i < kHalfChunks / kWaves; ++i) {
-        const uint32_t ch = (uint32_t)(kWaves * i + L.wave);
-        dma16(cdst + ch * 1024, lv, L.pack, cso + ch * 1024);
+        for (int i = 0; i < kHalfChunks / kWaves; ++i) {
+            const uint32_t ch = (uint32_t)(kWaves * i + L.wave);
+            dma16(cdst + ch * 1024, lv, L.pack, cso + ch * 1024);
+        }
     }
-    if (s & 1) {  // extras of super-block sb0 + (s + 1) / 2
+    if ((s & 1) && L.ex_on) {  // extras of super-block sb0 + (s + 1) / 2
         const int je = s1 >> 1;
         const int sbe = min(L.sb0 + je, L.sblast);
-        const int ch = min(L.wave, kExtraChunks - 1);
-        const uint32_t edst = L.wave < kExtraChunks
-                                  ? L.smem + kLdsEx + (uint32_t)(je & 1) * kPkExtra + (uint32_t)ch * 1024
-                                  : L.smem + kLdsExDummy;
-        dma16(edst, lv, L.pack, L.pk0 + (uint32_t)sbe * L.pk_sb + kPkCodes + (uint32_t)ch * 1024);
+        const uint32_t ch = (uint32_t)L.wave;
+        dma16(L.smem + kLdsEx + (uint32_t)(je & 1) * kPkExtra + ch * 1024, lv, L.pack,
+              L.pk0 + (uint32_t)sbe * L.pk_sb + kPkCodes + ch * 1024);
     }
     const int s2 = s + 2;
     const int sbw = min(L.sb0 + (s2 >> 1), L.sblast);
@@ -419,6 +431,49 @@ __device__ __forceinline__ void step_requests(const GmLoop &L, int s) {
     dma16(wdst + 2048 * L.th, L.voff_q, L.rows, wso);
     dma16(wdst + 2048 * L.th + 1024, L.voff_q, L.rows, wso + 16);
     dma16(wdst + 4096, L.voff_h, L.rows, (uint32_t)sbw * kBytesQ4_K);
+}
+
+// The main loop over the workgroup's super-blocks for a wave with NT live
+// token tiles (NT = 0: the wave only moves data for the others).
+template <int NT>
+__device__ __forceinline__ void q4k_loop(const GmLoop &L, uint8_t *smem, int nsb, int tq, Tiles &C, Tiles &acc) {
+    const int lane = L.lane, grp = L.grp, h = lane >> 5;
+    for (int j = 0; j < nsb; ++j) {
+        const int s = 2 * j;
+        const uint8_t *ex = smem + kLdsEx + (j & 1) * kPkExtra;
+        // even step: half 0 of super-block sb0 + j
+        wait_dma<kWLoads>();
+        __syncthreads();
+        step_requests(L, s);
+        if constexpr (NT > 0) {
+            const uint8_t *wq0 = smem + kLdsW + (s % kWSlots) * kWSlot + grp * kWGrp;
+            WConst wc[2];
+#pragma unroll
+            for (int g = 0; g < 2; ++g) wc[g] = w_const(lds_v4u(wq0 + 4096 + (32 * g + (lane & 31)) * 16), h);
+            const int sq0 = *reinterpret_cast<const int *>(ex + kPkMn + kPkDx + 4 * lane);
+            const int sq1 = *reinterpret_cast<const int *>(ex + kPkMn + kPkDx + 4 * (lane + 64));
+            // the exactness bound of one chain over the workgroup's 128 tokens
+            const bool split = wave_max_dpp(max(sq0, sq1)) > kExactSqMax;
+            const uint8_t *cur0 = smem + kLdsCodes + tq * 1024;  // even steps use code slot 0
+            half_chains<0, true, NT>(cur0, wq0, lane, wc, L.km, C);
+            if (split) combine<false, NT>(ex, tq, lane, wc, C, acc);
+            // odd step: half 1
+            wait_dma<kWLoads>();
+            __syncthreads();
+            step_requests(L, s + 1);
+            const uint8_t *wq1 = smem + kLdsW + ((s + 1) % kWSlots) * kWSlot + grp * kWGrp;
+            const uint8_t *cur1 = smem + kLdsCodes + kPkHalf + tq * 1024;
+            if (split)
+                half_chains<1, true, NT>(cur1, wq1, lane, wc, L.km, C);
+            else
+                half_chains<1, false, NT>(cur1, wq1, lane, wc, L.km, C);
+            combine<true, NT>(ex, tq, lane, wc, C, acc);
+        } else {
+            wait_dma<kWLoads>();
+            __syncthreads();
+            step_requests(L, s + 1);
+        }
+    }
 }
 
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_q4k_kernel(GmArgs a) {
@@ -454,6 +509,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     L.voff_h = (uint32_t)lane * (uint32_t)a.row_bytes;
     L.voff_q = (uint32_t)(32 * th + (lane & 31)) * (uint32_t)a.row_bytes + 64u * (uint32_t)h;
     L.smem = lds_addr(smem);
+    const int live_wg = min(kTiles, max(0, (a.m - kTokB * tb + 31) / 32));  // token tiles holding a token
+    L.codes_on = (wave & 3) < live_wg;
+    L.ex_on = wave < kTiles ? wave < live_wg : wave == kTiles;  // chunk 4: dx and sum |q8|
     L.km = NibMasks{0x000F000Fu, 0x00F000F0u, 0x64006400u};
     asm volatile("" : "+v"(L.km.lo), "+v"(L.km.hi), "+v"(L.km.bias));
 
@@ -468,14 +526,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     {
         const uint32_t lv = (uint32_t)lane * 16;
         const uint32_t cso = L.pk0 + (uint32_t)sb0 * L.pk_sb;
+        if (L.codes_on) {
 #pragma unroll
-        for (int i = 0; i < kHalfChunks / kWaves; ++i) {
-            const uint32_t c = (uint32_t)(kWaves * i + wave);
-            dma16(L.smem + kLdsCodes + c * 1024, lv, L.pack, cso + c * 1024);
+            for (int i = 0; i < kHalfChunks / kWaves; ++i) {
+                const uint32_t c = (uint32_t)(kWaves * i + wave);
+                dma16(L.smem + kLdsCodes + c * 1024, lv, L.pack, cso + c * 1024);
+            }
         }
-        const int ch = min(wave, kExtraChunks - 1);
-        dma16(wave < kExtraChunks ? L.smem + kLdsEx + (uint32_t)ch * 1024 : L.smem + kLdsExDummy, lv, L.pack,
-              cso + kPkCodes + (uint32_t)ch * 1024);
+        if (L.ex_on)
+            dma16(L.smem + kLdsEx + (uint32_t)wave * 1024, lv, L.pack, cso + kPkCodes + (uint32_t)wave * 1024);
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
             const uint32_t wdst = L.smem + kLdsW + (uint32_t)hf * kWSlot + (uint32_t)grp * kWGrp;
@@ -487,36 +546,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
 
     const int tq = 2 * th;  // the wave's first token tile
-    for (int j = 0; j < nsb; ++j) {
-        const int s = 2 * j;
-        const uint8_t *ex = smem + kLdsEx + (j & 1) * kPkExtra;
-        // even step: half 0 of super-block sb0 + j
-        wait_dma<kWLoads>();
-        __syncthreads();
-        step_requests(L, s);
-        const uint8_t *wq0 = smem + kLdsW + (s % kWSlots) * kWSlot + grp * kWGrp;
-        WConst wc[2];
-#pragma unroll
-        for (int g = 0; g < 2; ++g) wc[g] = w_const(lds_v4u(wq0 + 4096 + (32 * g + (lane & 31)) * 16), h);
-        const int sq0 = *reinterpret_cast<const int *>(ex + kPkMn + kPkDx + 4 * lane);
-        const int sq1 = *reinterpret_cast<const int *>(ex + kPkMn + kPkDx + 4 * (lane + 64));
-        // the exactness bound of one chain over the workgroup's 128 tokens
-        const bool split = wave_max_dpp(max(sq0, sq1)) > kExactSqMax;
-        const uint8_t *cur0 = smem + kLdsCodes + tq * 1024;  // even steps use code slot 0
-        half_chains<0, true>(cur0, wq0, lane, wc, L.km, C);
-        if (split) combine<false>(ex, tq, lane, wc, C, acc);
-        // odd step: half 1
-        wait_dma<kWLoads>();
-        __syncthreads();
-        step_requests(L, s + 1);
-        const uint8_t *wq1 = smem + kLdsW + ((s + 1) % kWSlots) * kWSlot + grp * kWGrp;
-        const uint8_t *cur1 = smem + kLdsCodes + kPkHalf + tq * 1024;
-        if (split)
-            half_chains<1, true>(cur1, wq1, lane, wc, L.km, C);
-        else
-            half_chains<1, false>(cur1, wq1, lane, wc, L.km, C);
-        combine<true>(ex, tq, lane, wc, C, acc);
-    }
+    const int live = min(2, max(0, live_wg - tq));  // of its two tiles, those holding a token
+    // one instance of the loop per live-tile count, so that neither carries
+    // the other's registers
+    if (live == 2)
+        q4k_loop<2>(L, smem, nsb, tq, C, acc);
+    else if (live == 1)
+        q4k_loop<1>(L, smem, nsb, tq, C, acc);
+    else
+        q4k_loop<0>(L, smem, nsb, tq, C, acc);
     wait_dma<0>();  // the requests past the end have landed before the LDS is released
 
     if (a.nsplit > 1) {

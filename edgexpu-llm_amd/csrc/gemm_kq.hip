@@ -38,7 +38,7 @@
 // chains = 4 accumulator tiles).  The main loop is the Q4_K GEMM's: LDS DMA
 // only (inline assembly, explicit waits), codes one step ahead in 2 slots,
 // extras (bsums / dx) per super-block in 2 slots, weights two steps ahead in
-// 3 slots; one barrier per step.  LDS: 64 + 11 + 72 KiB.
+// 3 slots; one barrier per step.  LDS: 64 + 10 + 72 KiB.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -56,36 +56,40 @@ constexpr int kKqWSlot = 4 * kKqGrpBytes;
 constexpr int kKqWSlots = 3;
 constexpr int kKqLdsCodes = 0;
 constexpr int kKqLdsEx = kKqLdsCodes + 2 * kPkHalf;
-constexpr int kKqLdsExDummy = kKqLdsEx + 2 * kPkExtra;
-constexpr int kKqLdsW = kKqLdsExDummy + 1024;
+constexpr int kKqLdsW = kKqLdsEx + 2 * kPkExtra;
 constexpr int kKqLdsLast = kKqLdsW + kKqWSlots * kKqWSlot;
 constexpr int kKqLdsBytes = kKqLdsLast + 16;
 static_assert(kKqLdsBytes <= 160 * 1024, "the LDS rings fit the gfx950 LDS");
 
 // ----------------------------------------------------------------- repack
 
-// Element of the super-block behind slot k of K-step s, lane half h, half hf
-// (the activation pack's K order).
-__device__ __forceinline__ int kq_element(int hf, int h, int s, int k) {
-    const int j = 2 * h + hf;
-    const int b = 4 * s + ((k & 4) ? 1 : 0) + ((k & 1) ? 2 : 0);
-    return 64 * j + b + ((k & 2) ? 32 : 0);
+// The slot order of one K-step, [lo b0, lo b2, hi b0, hi b2] and
+// [lo b1, lo b3, hi b1, hi b3], from the four biased codes of the lo group
+// (elements 64 j + 4 s + b) and of the hi group (64 j + 32 + 4 s + b).
+__device__ __forceinline__ uint2 slot_order(uint32_t lo4, uint32_t hi4) {
+    return make_uint2(__builtin_amdgcn_perm(hi4, lo4, 0x06040200u), __builtin_amdgcn_perm(hi4, lo4, 0x07050301u));
 }
 
-// Q6_K (src/gguf_dot_q8.c:971-983): q of element e, in -32..31.
-__device__ __forceinline__ int q6k_value(const uint8_t *blk, int e) {
-    const int n = e >> 7, l = e & 127, qq = l >> 5, i = l & 31;
-    const int ql = blk[64 * n + 32 * (qq & 1) + i];
-    const int qh = blk[128 + 32 * n + i];
-    return (((ql >> (4 * (qq >> 1))) & 15) | (((qh >> (2 * qq)) & 3) << 4)) - 32;
+// Q6_K codes (src/gguf_dot_q8.c:971-983, q = ql nibble | qh 2 bits << 4,
+// minus 32) of K-step s in half hf, lane half h, biased by +128: element
+// 64 j + 4 s + b + 32 hi (j = 2 h + hf) is ql byte 64 h + 32 hi + 4 s + b,
+// nibble hf, and bits 4 hf + 2 hi of qh byte 32 h + 4 s + b; four bytes at
+// once per 32-bit word.
+__device__ __forceinline__ uint2 q6k_step(uint32_t ql_lo, uint32_t ql_hi, uint32_t qh, int hf) {
+    const int sh = 4 * hf;
+    const uint32_t lo = ((ql_lo >> sh) & 0x0F0F0F0Fu) | (((qh >> sh) & 0x03030303u) << 4);
+    const uint32_t hi = ((ql_hi >> sh) & 0x0F0F0F0Fu) | (((qh >> (sh + 2)) & 0x03030303u) << 4);
+    return slot_order(lo + 0x60606060u, hi + 0x60606060u);  // q6 - 32 + 128
 }
 
-// Q5_K (dequant_q5_k, src/gguf_quant.c:305-345): q of element e, in 0..31.
-__device__ __forceinline__ int q5k_value(const uint8_t *blk, int e) {
-    const int jj = e >> 6, hi = (e >> 5) & 1, i = e & 31;
-    const int qs = blk[48 + 32 * jj + i];
-    const int qh = blk[16 + i];
-    return ((qs >> (4 * hi)) & 15) + 16 * ((qh >> (2 * jj + hi)) & 1);
+// Q5_K codes (dequant_q5_k, src/gguf_quant.c:305-345, q = qs nibble + 16 *
+// qh bit) of K-step s in half hf, lane half h, biased by +128: element
+// 64 j + 4 s + b + 32 hi is nibble hi of qs byte 32 j + 4 s + b and bit
+// 2 j + hi of qh byte 4 s + b.
+__device__ __forceinline__ uint2 q5k_step(uint32_t qs, uint32_t qh, int j) {
+    const uint32_t lo = (qs & 0x0F0F0F0Fu) | (((qh >> (2 * j)) & 0x01010101u) << 4);
+    const uint32_t hi = ((qs >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * j + 1)) & 0x01010101u) << 4);
+    return slot_order(lo + 0x80808080u, hi + 0x80808080u);
 }
 
 // get_scale_min_k4 (src/gguf_quant.c:212-220).
@@ -106,76 +110,72 @@ __device__ __forceinline__ uint32_t f16_pair(float lo, float hi) {
 
 constexpr int kRepackRecs = 16;  // (row, super-block) records per workgroup
 
-// One workgroup of 256 threads per 16 consecutive records (row-major, so
-// their source bytes are contiguous): the blocks are staged in LDS with
-// 2-byte loads (every block is 2-byte aligned), then thread t of a record writes q chunk t (16 B:
-// half t / 8, lane half (t / 4) % 2, K-steps 2 (t % 4), +1) and threads 0..3
-// the c and x chunks of (half t / 2, lane half t % 2).
+// 16 threads per record (rows are contiguous runs of blocks, so record r is
+// the block at w + r * block bytes): thread t writes q chunk t (16 B: half
+// t / 8, lane half (t / 4) % 2, K-steps 2 (t % 4) and + 1) from three 8-byte
+// loads of its block, and threads 0..3 the c and x chunks of (half t / 2,
+// lane half t % 2).  Q6_K blocks are 2-byte aligned; gfx950 global memory
+// runs in unaligned-access mode, so the loads stay plain dwordx2 loads.
 template <int TYPE>
-__global__ __launch_bounds__(256) void kq_repack_kernel(const uint8_t *__restrict__ w, size_t row_bytes, int nb,
-                                                        long long nrec, uint8_t *__restrict__ rw) {
+__global__ __launch_bounds__(256) void kq_repack_kernel(const uint8_t *__restrict__ w, long long nrec,
+                                                        uint8_t *__restrict__ rw) {
     constexpr int kB = TYPE == kTypeQ6_K ? kBytesQ6_K : kBytesQ5_K;
-    __shared__ uint32_t sblk[kRepackRecs * kB / 4 + 4];
-    const long long r0 = (long long)blockIdx.x * kRepackRecs;
-    const int nr = (int)min((long long)kRepackRecs, nrec - r0);
-    // records r0 .. r0 + nr - 1 may span rows: stage each block on its own
-    const uint8_t *sb8 = reinterpret_cast<const uint8_t *>(sblk);
-    for (int i = threadIdx.x; i < nr * (kB / 2); i += 256) {
-        const int rec = i / (kB / 2), off = 2 * (i % (kB / 2));
-        const long long r = r0 + rec;
-        const uint8_t *src = w + (size_t)(r / nb) * row_bytes + (size_t)(r % nb) * kB + off;
-        reinterpret_cast<uint16_t *>(sblk)[rec * (kB / 2) + off / 2] = *reinterpret_cast<const uint16_t *>(src);
-    }
-    __syncthreads();
-    const int rec = threadIdx.x >> 4, t = threadIdx.x & 15;
-    if (rec >= nr) return;
-    const long long r = r0 + rec;
-    const uint8_t *blk = sb8 + rec * kB;
-    uint8_t *dst = rw + (size_t)(r / nb) * ((size_t)nb * kKqRec) + (size_t)(r % nb) * kKqRec;
+    const long long r = (long long)blockIdx.x * kRepackRecs + (threadIdx.x >> 4);
+    if (r >= nrec) return;
+    const int t = threadIdx.x & 15;
+    const uint8_t *blk = w + (size_t)r * kB;
+    uint8_t *dst = rw + (size_t)r * kKqRec;
     {
-        const int hf = t >> 3, h = (t >> 2) & 1, s0 = 2 * (t & 3);
-        uint32_t o[4];
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            uint32_t word = 0;
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const int s = s0 + (d >> 1), k = 4 * (d & 1) + b;
-                const int e = kq_element(hf, h, s, k);
-                const int q = TYPE == kTypeQ6_K ? q6k_value(blk, e) : q5k_value(blk, e);
-                word |= (uint32_t)(q + 128) << (8 * b);
-            }
-            o[d] = word;
+        const int hf = t >> 3, h = (t >> 2) & 1, p = t & 3;
+        uint2 a, b;
+        if (TYPE == kTypeQ6_K) {
+            const uint2 lo = ldg8(blk + 64 * h + 8 * p), hi = ldg8(blk + 64 * h + 32 + 8 * p);
+            const uint2 qh = ldg8(blk + 128 + 32 * h + 8 * p);
+            a = q6k_step(lo.x, hi.x, qh.x, hf);
+            b = q6k_step(lo.y, hi.y, qh.y, hf);
+        } else {
+            const int j = 2 * h + hf;
+            const uint2 qs = ldg8(blk + 48 + 32 * j + 8 * p), qh = ldg8(blk + 16 + 8 * p);
+            a = q5k_step(qs.x, qh.x, j);
+            b = q5k_step(qs.y, qh.y, j);
         }
-        *reinterpret_cast<uint4 *>(dst + hf * kKqHalfRec + 64 * h + 16 * (t & 3)) = make_uint4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<uint4 *>(dst + hf * kKqHalfRec + 64 * h + 16 * p) = make_uint4(a.x, a.y, b.x, b.y);
     }
     if (t < 4) {
         const int hf = t >> 1, h = t & 1, j = 2 * h + hf;
         uint32_t c[4], x[4];
         int mv[4] = {0, 0, 0, 0};
-        float d = 0.0f, dmin = 0.0f;
+        float d, dmin = 0.0f;
         if (TYPE == kTypeQ6_K) {
-            const int8_t *sc = reinterpret_cast<const int8_t *>(blk + 192);
+            const uint32_t s4 = ldg4(blk + 192 + 4 * j);  // int8 scales of 16-element sub-blocks 4j .. 4j + 3
 #pragma unroll
             for (int kc = 0; kc < 4; ++kc) {
-                const int v = sc[4 * j + kc];  // 16-element sub-blocks 4j .. 4j + 3
+                const int v = (int)(int8_t)(s4 >> (8 * kc));
                 c[kc] = f16_pair((float)(v & 15), (float)(v >> 4));
             }
-            d = f16_bits_to_f32((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
+            d = f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(blk + 208));
         } else {
+            const uint32_t hd = ldg4(blk);
+            uint8_t q[12];
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                const uint32_t v = ldg4(blk + 4 + 4 * i);
+#pragma unroll
+                for (int b = 0; b < 4; ++b) q[4 * i + b] = (uint8_t)(v >> (8 * b));
+            }
 #pragma unroll
             for (int kc = 0; kc < 4; ++kc) {
                 int v, m;
-                k4_scale_min(blk + 4, 2 * j + (kc >> 1), v, m);  // lo: sub-block 2j, hi: 2j + 1
+                k4_scale_min(q, 2 * j + (kc >> 1), v, m);  // lo: sub-block 2j, hi: 2j + 1
                 c[kc] = f16_pair((float)(v & 15), (float)(v >> 4));
             }
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 int v;
-                k4_scale_min(blk + 4, 4 * h + k, v, mv[k]);
+                k4_scale_min(q, 4 * h + k, v, mv[k]);
             }
-            d = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-            dmin = f16_bits_to_f32((uint32_t)blk[2] | ((uint32_t)blk[3] << 8));
+            d = f16_bits_to_f32(hd & 0xffffu);
+            dmin = f16_bits_to_f32(hd >> 16);
         }
         const int mb = 2 * hf;  // half 0 carries m(4h), m(4h+1); half 1 m(4h+2), m(4h+3)
         x[0] = f16_pair((float)mv[mb], (float)mv[mb]);
@@ -209,6 +209,8 @@ struct KqLoop {
     uint32_t voff_q, voff_cx;  // lane's q record (row lane % 32, + 64 h) and c / x (+ 16 h)
     uint32_t smem;
     int lane, wave, grp, th, sb0, sblast;
+    bool codes_on;  // the wave's code chunks (token tile wave % 4) hold a token below m
+    bool ex_on;     // the wave's extras chunk is needed: bsums of a live tile (min term), or dx
 };
 
 constexpr int kKqWLoads = 3;
@@ -217,26 +219,29 @@ constexpr int kKqWLoads = 3;
 // the next super-block (1 DMA), then the weights of step s + 2 (3 DMAs:
 // token-half 0 waves q pieces 0, 1 and c; token-half 1 waves q pieces 2, 3
 // and x).  Past the end of the K range the last super-block is requested
-// again into slots nobody reads, so the weights are always the last 3.
+// again into slots nobody reads, so the weights are always the last 3: a
+// wait for vmcnt(3) covers everything before them however many code and
+// extras chunks a wave skips (those of token tiles past the last token,
+// which no wave reads).
 __device__ __forceinline__ void kq_step_requests(const KqLoop &L, int s) {
     const uint32_t lv = (uint32_t)L.lane * 16;
     const int s1 = s + 1;
     const int sbc = min(L.sb0 + (s1 >> 1), L.sblast);
     const uint32_t cdst = L.smem + kKqLdsCodes + (uint32_t)(s1 & 1) * kPkHalf;
     const uint32_t cso = L.pk0 + (uint32_t)sbc * L.pk_sb + (uint32_t)(s1 & 1) * kPkHalf;
+    if (L.codes_on) {
 #pragma unroll
-    for (int i = 0; i < kHalfChunks / kWaves; ++i) {
-        const uint32_t ch = (uint32_t)(kWaves * i + L.wave);
-        dma16(cdst + ch * 1024, lv, L.pack, cso + ch * 1024);
+        for (int i = 0; i < kHalfChunks / kWaves; ++i) {
+            const uint32_t ch = (uint32_t)(kWaves * i + L.wave);
+            dma16(cdst + ch * 1024, lv, L.pack, cso + ch * 1024);
+        }
     }
-    if (s & 1) {
+    if ((s & 1) && L.ex_on) {
         const int je = s1 >> 1;
         const int sbe = min(L.sb0 + je, L.sblast);
-        const int ch = min(L.wave, kExtraChunks - 1);
-        const uint32_t edst = L.wave < kExtraChunks
-                                  ? L.smem + kKqLdsEx + (uint32_t)(je & 1) * kPkExtra + (uint32_t)ch * 1024
-                                  : L.smem + kKqLdsExDummy;
-        dma16(edst, lv, L.pack, L.pk0 + (uint32_t)sbe * L.pk_sb + kPkCodes + (uint32_t)ch * 1024);
+        const uint32_t ch = (uint32_t)L.wave;
+        dma16(L.smem + kKqLdsEx + (uint32_t)(je & 1) * kPkExtra + ch * 1024, lv, L.pack,
+              L.pk0 + (uint32_t)sbe * L.pk_sb + kPkCodes + ch * 1024);
     }
     const int s2 = s + 2;
     const int sbw = min(L.sb0 + (s2 >> 1), L.sblast);
@@ -289,19 +294,20 @@ __device__ __forceinline__ void kq_operands(uint32_t q0, uint32_t q1, const KqCo
 // C[chain][token tile]
 typedef v16f KqTiles[2][2];
 
-// The 8 K-steps of one half: codes slot `cur` (the wave's token tiles at
-// cur + tt * 1024, 4 KiB per K-step), weight slot `wq` (q pieces at
-// wq + 1024 p, c at wq + 4096).  The operands of the next K-step are built
-// while this K-step's 4 MFMAs run.
-template <bool FIRST>
+// The 8 K-steps of one half for the wave's first NT token tiles: codes
+// slot `cur` (token tiles at cur + tt * 1024, 4 KiB per K-step), weight slot
+// `wq` (q pieces at wq + 1024 p, c at wq + 4096).  The operands of the next
+// K-step are built while this K-step's MFMAs run.  NT < 2 when the wave's
+// second token tile lies entirely past the last token.
+template <bool FIRST, int NT>
 __device__ __forceinline__ void kq_half(const uint8_t *cur, const uint8_t *wq, int lane, uint32_t hi64, KqTiles &C) {
     const KqConst k = kq_const(lds_v4u(wq + 4096 + lane * 16));
     v4u q[4];
 #pragma unroll
     for (int p = 0; p < 4; ++p) q[p] = lds_v4u(wq + 1024 * p + lane * 16);
-    v8h a[2];
+    v8h a[NT];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) a[tt] = lds_v8h(cur + tt * 1024 + lane * 16);
+    for (int tt = 0; tt < NT; ++tt) a[tt] = lds_v8h(cur + tt * 1024 + lane * 16);
     v8h w0, w1;
     kq_operands(q[0][0], q[0][1], k, 0, 2, hi64, w0, w1);
     __builtin_amdgcn_sched_barrier(0);
@@ -314,23 +320,95 @@ __device__ __forceinline__ void kq_half(const uint8_t *cur, const uint8_t *wq, i
                         nw0, nw1);
         }
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
+        for (int tt = 0; tt < NT; ++tt) {
             C[0][tt] = mfma(a[tt], w0, (FIRST && s == 0) ? v16f{} : C[0][tt]);
             C[1][tt] = mfma(a[tt], w1, (FIRST && s == 0) ? v16f{} : C[1][tt]);
             if (s + 1 < 8) a[tt] = lds_v8h(cur + (s + 1) * 4096 + tt * 1024 + lane * 16);
         }
-        // MFMA, VALU x3, MFMA, DS read, VALU x2, MFMA, VALU x3, MFMA, DS read, VALU x2
+        if (NT == 2) {
+            // MFMA, VALU x3, MFMA, DS read, VALU x2, MFMA, VALU x3, MFMA, DS read, VALU x2
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+            for (int i = 0; i < 2; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+            }
+        } else {
+            // MFMA, VALU x6, DS read, MFMA, VALU x6
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
         w0 = nw0;
         w1 = nw1;
+    }
+}
+
+// acc += dx * ((16 C1 + C0) * d - mn * dmin) for the wave's first NT token
+// tiles (extras slot `ex`, the wave's first token tile tq).
+template <bool MIN, int NT>
+__device__ __forceinline__ void kq_combine(const uint8_t *ex, int tq, int lane, float dd, float ndm, v8h bmn,
+                                           const KqTiles &C, v16f (&acc)[2]) {
+    const int h = lane >> 5;
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+        v16f mn = v16f{};
+        if (MIN) mn = mfma(lds_v8h(ex + (tq + tt) * 1024 + lane * 16), bmn, v16f{});
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 dx = *reinterpret_cast<const float4 *>(ex + kPkMn + 4 * (32 * (tq + tt) + 8 * i + 4 * h));
+            const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = 4 * i + e;
+                float v = __builtin_fmaf(C[1][tt][r], 16.0f, C[0][tt][r]) * dd;
+                if (MIN) v = __builtin_fmaf(mn[r], ndm, v);
+                acc[tt][r] = __builtin_fmaf(v, dxs[e], acc[tt][r]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// The main loop over the workgroup's super-blocks for a wave with NT live
+// token tiles (NT = 0: the wave only moves data for the others).
+template <bool MIN, int NT>
+__device__ __forceinline__ void kq_loop(const KqLoop &L, uint8_t *smem, int nsb, int tq, uint32_t hi64, KqTiles &C,
+                                        v16f (&acc)[2]) {
+    const int lane = L.lane, grp = L.grp;
+    for (int j = 0; j < nsb; ++j) {
+        const int s = 2 * j;
+        const uint8_t *ex = smem + kKqLdsEx + (j & 1) * kPkExtra;
+        // even step: half 0; its x chunk holds m(4h), m(4h+1), d and dmin
+        wait_dma<kKqWLoads>();
+        __syncthreads();
+        kq_step_requests(L, s);
+        if constexpr (NT > 0) {
+            const uint8_t *wq0 = smem + kKqLdsW + (s % kKqWSlots) * kKqWSlot + grp * kKqGrpBytes;
+            const v4u x0 = lds_v4u(wq0 + 5120 + lane * 16);
+            kq_half<true, NT>(smem + kKqLdsCodes + tq * 1024, wq0, lane, hi64, C);
+            // odd step: half 1, then the super-block's combination
+            wait_dma<kKqWLoads>();
+            __syncthreads();
+            kq_step_requests(L, s + 1);
+            const uint8_t *wq1 = smem + kKqLdsW + ((s + 1) % kKqWSlots) * kKqWSlot + grp * kKqGrpBytes;
+            v4u x1 = v4u{0u, 0u, 0u, 0u};
+            if (MIN) x1 = lds_v4u(wq1 + 5120 + lane * 16);
+            kq_half<false, NT>(smem + kKqLdsCodes + kPkHalf + tq * 1024, wq1, lane, hi64, C);
+            const float dd = __uint_as_float(x0[2]), ndm = -__uint_as_float(x0[3]);
+            v8h bmn = v8h{};
+            if (MIN) bmn = __builtin_bit_cast(v8h, v4u{x0[0], x0[1], x1[0], x1[1]});
+            kq_combine<MIN, NT>(ex, tq, lane, dd, ndm, bmn, C, acc);
+        } else {
+            wait_dma<kKqWLoads>();
+            __syncthreads();
+            kq_step_requests(L, s + 1);
+        }
     }
 }
 
@@ -366,6 +444,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     L.voff_q = (uint32_t)(lane & 31) * a.rstride + 64u * (uint32_t)h;
     L.voff_cx = (uint32_t)(lane & 31) * a.rstride + 16u * (uint32_t)h;
     L.smem = lds_addr(smem);
+    const int live_wg = min(kTiles, max(0, (a.m - kTokB * tb + 31) / 32));  // token tiles holding a token
+    L.codes_on = (wave & 3) < live_wg;
+    L.ex_on = wave < kTiles ? (MIN && wave < live_wg) : wave == kTiles;  // chunk 4: dx and sum |q8|
     uint32_t hi64 = 0x64646464u;
     asm volatile("" : "+v"(hi64));
 
@@ -377,14 +458,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     {
         const uint32_t lv = (uint32_t)lane * 16;
         const uint32_t cso = L.pk0 + (uint32_t)sb0 * L.pk_sb;
+        if (L.codes_on) {
 #pragma unroll
-        for (int i = 0; i < kHalfChunks / kWaves; ++i) {
-            const uint32_t c = (uint32_t)(kWaves * i + wave);
-            dma16(L.smem + kKqLdsCodes + c * 1024, lv, L.pack, cso + c * 1024);
+            for (int i = 0; i < kHalfChunks / kWaves; ++i) {
+                const uint32_t c = (uint32_t)(kWaves * i + wave);
+                dma16(L.smem + kKqLdsCodes + c * 1024, lv, L.pack, cso + c * 1024);
+            }
         }
-        const int ch = min(wave, kExtraChunks - 1);
-        dma16(wave < kExtraChunks ? L.smem + kKqLdsEx + (uint32_t)ch * 1024 : L.smem + kKqLdsExDummy, lv, L.pack,
-              cso + kPkCodes + (uint32_t)ch * 1024);
+        if (L.ex_on)
+            dma16(L.smem + kKqLdsEx + (uint32_t)wave * 1024, lv, L.pack, cso + kPkCodes + (uint32_t)wave * 1024);
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
             const uint32_t wdst = L.smem + kKqLdsW + (uint32_t)hf * kKqWSlot + (uint32_t)grp * kKqGrpBytes;
@@ -396,46 +478,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
 
     const int tq = 2 * th;
-    for (int j = 0; j < nsb; ++j) {
-        const int s = 2 * j;
-        const uint8_t *ex = smem + kKqLdsEx + (j & 1) * kPkExtra;
-        // even step: half 0; its x chunk holds m(4h), m(4h+1), d and dmin
-        wait_dma<kKqWLoads>();
-        __syncthreads();
-        kq_step_requests(L, s);
-        const uint8_t *wq0 = smem + kKqLdsW + (s % kKqWSlots) * kKqWSlot + grp * kKqGrpBytes;
-        const v4u x0 = lds_v4u(wq0 + 5120 + lane * 16);
-        kq_half<true>(smem + kKqLdsCodes + tq * 1024, wq0, lane, hi64, C);
-        // odd step: half 1, then the super-block's combination
-        wait_dma<kKqWLoads>();
-        __syncthreads();
-        kq_step_requests(L, s + 1);
-        const uint8_t *wq1 = smem + kKqLdsW + ((s + 1) % kKqWSlots) * kKqWSlot + grp * kKqGrpBytes;
-        v4u x1 = v4u{0u, 0u, 0u, 0u};
-        if (MIN) x1 = lds_v4u(wq1 + 5120 + lane * 16);
-        kq_half<false>(smem + kKqLdsCodes + kPkHalf + tq * 1024, wq1, lane, hi64, C);
-        const float dd = __uint_as_float(x0[2]), ndm = -__uint_as_float(x0[3]);
-        v8h bmn = v8h{};
-        if (MIN) bmn = __builtin_bit_cast(v8h, v4u{x0[0], x0[1], x1[0], x1[1]});
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            v16f mn = v16f{};
-            if (MIN) mn = mfma(lds_v8h(ex + (tq + tt) * 1024 + lane * 16), bmn, v16f{});
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float4 dx = *reinterpret_cast<const float4 *>(ex + kPkMn + 4 * (32 * (tq + tt) + 8 * i + 4 * h));
-                const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int r = 4 * i + e;
-                    float v = __builtin_fmaf(C[1][tt][r], 16.0f, C[0][tt][r]) * dd;
-                    if (MIN) v = __builtin_fmaf(mn[r], ndm, v);
-                    acc[tt][r] = __builtin_fmaf(v, dxs[e], acc[tt][r]);
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
+    // token tiles of this wave that hold at least one token below m; one
+    // instance of the loop per count, so that neither carries the other's
+    // registers
+    const int live = min(2, max(0, live_wg - tq));
+    if (live == 2)
+        kq_loop<MIN, 2>(L, smem, nsb, tq, hi64, C, acc);
+    else if (live == 1)
+        kq_loop<MIN, 1>(L, smem, nsb, tq, hi64, C, acc);
+    else
+        kq_loop<MIN, 0>(L, smem, nsb, tq, hi64, C, acc);
     wait_dma<0>();
 
     if (a.nsplit > 1 && !split_reduce<2>(acc, a.part, a.cnt, a.nsplit, a.ntiles, tile, z, s_last)) return;
@@ -474,14 +526,17 @@ size_t gemm_kq_part_bytes(int m, int n_out, int K) {
 
 hipError_t launch_kq_repack(int type, const uint8_t *w, size_t row_bytes, int n_out, int K, uint8_t *rw,
                             hipStream_t st) {
-    if (!gemm_kq_supported(type, n_out, K, 1) || ((uintptr_t)rw & 15u) != 0) return hipErrorInvalidValue;
+    if (!gemm_kq_supported(type, n_out, K, 1) || ((uintptr_t)rw & 15u) != 0 || ((uintptr_t)w & 1u) != 0)
+        return hipErrorInvalidValue;
     const int nb = K / kQKK;
+    // rows are contiguous runs of blocks (GGUF rows carry no padding)
+    if (row_bytes != (size_t)nb * (type == kTypeQ6_K ? kBytesQ6_K : kBytesQ5_K)) return hipErrorInvalidValue;
     const long long nrec = (long long)n_out * nb;
     const unsigned grid = (unsigned)((nrec + kRepackRecs - 1) / kRepackRecs);
     if (type == kTypeQ6_K)
-        hipLaunchKernelGGL(kq_repack_kernel<kTypeQ6_K>, dim3(grid), dim3(256), 0, st, w, row_bytes, nb, nrec, rw);
+        hipLaunchKernelGGL(kq_repack_kernel<kTypeQ6_K>, dim3(grid), dim3(256), 0, st, w, nrec, rw);
     else
-        hipLaunchKernelGGL(kq_repack_kernel<kTypeQ5_K>, dim3(grid), dim3(256), 0, st, w, row_bytes, nb, nrec, rw);
+        hipLaunchKernelGGL(kq_repack_kernel<kTypeQ5_K>, dim3(grid), dim3(256), 0, st, w, nrec, rw);
     return hipGetLastError();
 }
 

@@ -76,8 +76,10 @@ constexpr int kFusedMaxTokens = 4;
 // From 16 tokens the matrix-core GEMM reads each weight row once for all
 // tokens; below that the GEMV reads it once per 8 tokens.  Measured at
 // [14336 x 4096] Q4_K: GEMV 44 / 80 / 151 us at 8 / 16 / 32 tokens, GEMM
-// ~45-50 us from 16 to 128 tokens ([4096 x 4096]: 18 / 31 / 55 against ~40).
-constexpr int kGemmMinTokens = 16;
+// 40 / 41 / 46 us at 16 / 32 / 64 ([4096 x 4096]: GEMV 18 / 31 / 55, GEMM
+// 29 / 31 / 35).  Q5_K pays a weight repack per call: GEMV 31 / 55 us at 16 /
+// 32 tokens against 47 / 48, so it switches at 32.
+int gemm_min_tokens(uint32_t type) { return type == (uint32_t)kTypeQ5_K ? 32 : 16; }
 // Rows up to this many elements quantize the activation inside the GEMV
 // workgroups; longer rows quantize it once in its own launch (the in-kernel
 // staging costs one load latency per 8192 elements per workgroup) ...
@@ -357,7 +359,7 @@ bool run_gemm_exact(uint32_t type, int nmat, const void *const *w, const int *n_
 }
 
 bool use_exact_gemm(uint32_t type, int n_out, int n_in, int m) {
-    return m >= kGemmMinTokens && g.prefill_mode == EDGEXPU_HIP_PREFILL_EXACT_INT8 &&
+    return m >= gemm_min_tokens(type) && g.prefill_mode == EDGEXPU_HIP_PREFILL_EXACT_INT8 &&
            exact_gemm_type(type, n_out, n_in, m);
 }
 
@@ -455,7 +457,7 @@ bool run_q8_product(uint32_t type, const void *w, int n_out, int n_in, int m, co
                     float *out, int ldo, hipStream_t st) {
     const size_t rb = edgexpu_hip_row_bytes(type, n_in);
     const size_t ab = act_bytes(type, n_in);
-    if (m >= kGemmMinTokens && exact_gemm_type(type, n_out, n_in, m)) {
+    if (m >= gemm_min_tokens(type) && exact_gemm_type(type, n_out, n_in, m)) {
         if (g.prefill_mode == EDGEXPU_HIP_PREFILL_F16 && gemm_q8_supported((int)type, n_out, n_in, m)) {
             void *ws = f16ws(gemm_f16_workspace(m, n_out, n_in));
             if (ws == nullptr) return false;
@@ -509,7 +511,7 @@ bool run_linear_group(uint32_t type, int nmat, const void *const *w, const int *
     const hipError_t e = q8_0_family((int)type) ? launch_quantize_q8_0(x, m, n_in, n_in, a.xq, st)
                                                 : launch_quantize_q8_k(x, m, n_in, n_in, a.xq, st);
     if (!hip_ok(e, "quantize activations")) return false;
-    if (split_gemv(type, n_in, m) && m < kGemmMinTokens) {
+    if (split_gemv(type, n_in, m) && m < gemm_min_tokens(type)) {
         return hip_ok(launch_gemv_fused((int)type, nmat, (const uint8_t *const *)w, n_out, bias, out, rb, n_in, m,
                                         nullptr, a.xq, act_bytes(type, n_in), st),
                       "gemv_split");

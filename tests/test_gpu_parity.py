@@ -263,8 +263,9 @@ def test_prefill_gemm_full_shape(hipdev, ora, n_in, n_out):
 @pytest.mark.parametrize("n_in,n_out,m", [(2560, 300, 16), (4096, 257, 64), (256, 70, 129), (9728, 130, 100),
                                           (1280, 515, 200), (2048, 384, 512), (1024, 16385, 33), (512, 129, 47)])
 def test_prefill_gemm_kq_vs_oracle(hipdev, ora, qt, n_in, n_out, m):
-    """m >= 16 Q5_K / Q6_K products run on the matrix cores over a per-call
-    repack, two exact chains per K-step (scale split 16 s1 + s0); every
+    """Q6_K products from 16 tokens and Q5_K from 32 run on the matrix cores
+    over a per-call repack, two exact chains per K-step (scale split
+    16 s1 + s0; Q5_K at 16 tokens takes the GEMV); every
     output within the fp32 bound of the oracle on its conditioning scale.
     Shapes cover one super-block, ragged tokens and rows, the K split (odd
     super-block counts), 129 row blocks and a full 512-token block."""
