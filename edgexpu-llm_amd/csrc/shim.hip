@@ -15,7 +15,7 @@
 
 using namespace exq;
 
-// kernels (quantize.hip, dequant.hip, gemv.hip, gemm.hip, gemm_kq.hip)
+// kernels (quantize.hip, dequant.hip, gemv.hip, gemm.hip, gemm_kq.hip, gemm_g32.hip)
 hipError_t launch_quantize_q8_0(const float *x, int m, int K, int ldx, uint8_t *packed, hipStream_t st);
 hipError_t launch_quantize_q8_k(const float *x, int m, int K, int ldx, uint8_t *packed, hipStream_t st);
 hipError_t launch_dequantize(const uint8_t *src, int type, unsigned long long n, float *dst, hipStream_t st);
@@ -50,6 +50,16 @@ hipError_t launch_kq_repack(int type, const uint8_t *w, size_t row_bytes, int n_
                             hipStream_t st);
 hipError_t launch_gemm_kq(int type, const uint8_t *rw, int n_out, int K, int m, const uint8_t *pack, float *part,
                           unsigned *cnt, const float *bias, float *out, int ldo, hipStream_t st);
+bool gemm_g32_supported(int type, int n_out, int K, int m);
+size_t gemm_g32_repack_bytes(int n_out, int K);
+size_t gemm_g32_pack_bytes(int m, int K);
+size_t gemm_g32_part_bytes(int m, int n_out, int K);
+hipError_t launch_g32_repack(int type, const uint8_t *w, size_t row_bytes, int n_out, int K, uint8_t *rw,
+                             hipStream_t st);
+hipError_t launch_g32_pack(const float *x, const uint8_t *xq, size_t xq_stride, int m, int K, uint8_t *pack,
+                           hipStream_t st);
+hipError_t launch_gemm_g32(int type, const uint8_t *rw, int n_out, int K, int m, const uint8_t *pack, float *part,
+                           unsigned *cnt, const float *bias, float *out, int ldo, hipStream_t st);
 bool gemv_fused_supported(int type, int K, int m);
 bool gemv_fused_f32_supported(int type, int K);
 bool gemv_fused_pro_supported(int type, int K, int pro);
@@ -306,30 +316,38 @@ void *gemm_ws(size_t bytes) {
 }
 
 // Formats with an exact matrix-core prefill GEMM: Q4_K straight from its
-// blocks (gemm.hip), Q5_K and Q6_K over a per-call repack (gemm_kq.hip).
+// blocks (gemm.hip), Q5_K and Q6_K over a per-call repack (gemm_kq.hip), and
+// Q8_0 / Q4_0 / Q5_0 over a per-call repack against Q8_0 activations
+// (gemm_g32.hip).
 bool exact_gemm_type(uint32_t type, int n_out, int n_in, int m) {
-    return gemm_q8_supported((int)type, n_out, n_in, m) || gemm_kq_supported((int)type, n_out, n_in, m);
+    return gemm_q8_supported((int)type, n_out, n_in, m) || gemm_kq_supported((int)type, n_out, n_in, m) ||
+           gemm_g32_supported((int)type, n_out, n_in, m);
 }
 
 // Exact prefill GEMM of nmat matrices over one input: f32 activations
-// (x != nullptr) or Q8_K blocks already in memory (xq).  The activations are
-// packed once into the GEMM's operand layout, then one launch per matrix
-// (Q5_K / Q6_K: a repack of the matrix into the workspace, then the GEMM;
-// the launches are stream-ordered, so one repack buffer serves every matrix).
+// (x != nullptr) or quantized blocks already in memory (xq: Q8_K for the
+// K-quants, Q8_0 for the 32-element formats).  The activations are packed
+// once into the GEMM's operand layout, then one launch per matrix (all but
+// Q4_K: a repack of the matrix into the workspace, then the GEMM; the
+// launches are stream-ordered, so one repack buffer serves every matrix).
 bool run_gemm_exact(uint32_t type, int nmat, const void *const *w, const int *n_out, int n_in, int m, const float *x,
                     const uint8_t *xq, size_t xq_stride, const float *const *bias, float *const *out, const int *ldo,
                     hipStream_t st) {
-    const bool kq = type != (uint32_t)kTypeQ4_K;
+    const bool g32 = q8_0_family((int)type);
+    const bool kq = !g32 && type != (uint32_t)kTypeQ4_K;
     // workspace: arrival counters | activation pack | K-split partial tiles | repacked weights
     size_t part_bytes = 0, rw_bytes = 0;
     for (int z = 0; z < nmat; ++z) {
-        const size_t pb = kq ? gemm_kq_part_bytes(m, n_out[z], n_in) : gemm_q4k_part_bytes(m, n_out[z], n_in);
+        const size_t pb = g32  ? gemm_g32_part_bytes(m, n_out[z], n_in)
+                          : kq ? gemm_kq_part_bytes(m, n_out[z], n_in)
+                               : gemm_q4k_part_bytes(m, n_out[z], n_in);
         part_bytes = pb > part_bytes ? pb : part_bytes;
-        const size_t rb = kq ? gemm_kq_repack_bytes(n_out[z], n_in) : 0;
+        const size_t rb = g32 ? gemm_g32_repack_bytes(n_out[z], n_in) : kq ? gemm_kq_repack_bytes(n_out[z], n_in) : 0;
         rw_bytes = rb > rw_bytes ? rb : rw_bytes;
     }
     const size_t cnt_bytes = gemm_q4k_counter_bytes();
-    const size_t pack_bytes = align_up(gemm_q4k_pack_bytes(m, n_in), (size_t)256);
+    const size_t pack_bytes =
+        align_up(g32 ? gemm_g32_pack_bytes(m, n_in) : gemm_q4k_pack_bytes(m, n_in), (size_t)256);
     part_bytes = align_up(part_bytes, (size_t)256);
     uint8_t *ws = (uint8_t *)gemm_ws(cnt_bytes + pack_bytes + part_bytes + rw_bytes);
     if (ws == nullptr) return false;
@@ -337,23 +355,28 @@ bool run_gemm_exact(uint32_t type, int nmat, const void *const *w, const int *n_
     uint8_t *pack = ws + cnt_bytes;
     float *part = part_bytes != 0 ? (float *)(pack + pack_bytes) : nullptr;
     uint8_t *rw = pack + pack_bytes + part_bytes;
-    const hipError_t e = x != nullptr ? launch_q8k_pack_f32(x, m, n_in, n_in, pack, st)
-                                      : launch_q8k_pack_q8k(xq, xq_stride, m, n_in, pack, st);
+    const hipError_t e = g32            ? launch_g32_pack(x, xq, xq_stride, m, n_in, pack, st)
+                         : x != nullptr ? launch_q8k_pack_f32(x, m, n_in, n_in, pack, st)
+                                        : launch_q8k_pack_q8k(xq, xq_stride, m, n_in, pack, st);
     if (!hip_ok(e, "pack activations")) return false;
     const size_t rb = edgexpu_hip_row_bytes(type, n_in);
     for (int z = 0; z < nmat; ++z) {
         const float *bz = bias != nullptr ? bias[z] : nullptr;
-        if (!kq) {
-            if (!hip_ok(launch_gemm_q4k((const uint8_t *)w[z], rb, n_out[z], n_in, m, pack, part, cnt, bz, out[z],
-                                        ldo[z], st),
-                        "gemm_q4k"))
+        if (g32) {
+            if (!hip_ok(launch_g32_repack((int)type, (const uint8_t *)w[z], rb, n_out[z], n_in, rw, st), "g32 repack") ||
+                !hip_ok(launch_gemm_g32((int)type, rw, n_out[z], n_in, m, pack, part, cnt, bz, out[z], ldo[z], st),
+                        "gemm_g32"))
                 return false;
-            continue;
-        }
-        if (!hip_ok(launch_kq_repack((int)type, (const uint8_t *)w[z], rb, n_out[z], n_in, rw, st), "kq repack") ||
-            !hip_ok(launch_gemm_kq((int)type, rw, n_out[z], n_in, m, pack, part, cnt, bz, out[z], ldo[z], st),
-                    "gemm_kq"))
+        } else if (kq) {
+            if (!hip_ok(launch_kq_repack((int)type, (const uint8_t *)w[z], rb, n_out[z], n_in, rw, st), "kq repack") ||
+                !hip_ok(launch_gemm_kq((int)type, rw, n_out[z], n_in, m, pack, part, cnt, bz, out[z], ldo[z], st),
+                        "gemm_kq"))
+                return false;
+        } else if (!hip_ok(launch_gemm_q4k((const uint8_t *)w[z], rb, n_out[z], n_in, m, pack, part, cnt, bz, out[z],
+                                           ldo[z], st),
+                           "gemm_q4k")) {
             return false;
+        }
     }
     return true;
 }

@@ -317,6 +317,29 @@ def kq_q8k_gemm_f64(qtype: int, w: np.ndarray, xq: np.ndarray):
     return val, mag
 
 
+def g32_q80_gemm_f64(qtype: int, w: np.ndarray, xq: np.ndarray):
+    """Many-token Q8_0 (8) / Q4_0 (2) / Q5_0 (6) x Q8_0 product in float64
+    with exact integer block sums: w [n_out, row_bytes], xq [m, nb*34].
+    Returns (value [m, n_out], S [m, n_out]) like q8_rows_f64."""
+    bb = {2: 18, 6: 22, 8: 34}[qtype]
+    parts = {2: q4_0_parts, 6: q5_0_parts, 8: q8_0_parts}[qtype]
+    n_out, m = w.shape[0], xq.shape[0]
+    nb = w.shape[1] // bb
+    dw, qw = parts(w.reshape(-1, bb))
+    dw = dw.astype(np.float64).reshape(n_out, nb)
+    qw = qw.reshape(n_out, nb, 32).astype(np.float64)
+    dx, qx = q8_0_parts(xq.reshape(-1, 34))
+    dx = dx.astype(np.float64).reshape(m, nb)
+    qx = qx.reshape(m, nb, 32).astype(np.float64)
+    val = np.zeros((m, n_out))
+    mag = np.zeros((m, n_out))
+    for b in range(nb):
+        sc = dx[:, b:b + 1] * dw[None, :, b]
+        val += sc * (qx[:, b, :] @ qw[:, b, :].T)
+        mag += np.abs(sc) * (np.abs(qx[:, b, :]) @ np.abs(qw[:, b, :]).T)
+    return val, mag
+
+
 def q4k_q8k_gemm_f64(w: np.ndarray, xq: np.ndarray):
     """kq_q8k_gemm_f64 for Q4_K rows."""
     return kq_q8k_gemm_f64(12, w, xq)

@@ -342,6 +342,87 @@ def test_prefill_gemm_q6k_full_shape(hipdev, ora):
     assert_tol(got[tok][:, rows], want, S[tok], "vs oracle")
 
 
+def _q80_rows(ora, x):
+    return np.stack([ora.quantize_q8_0(x[t]) for t in range(x.shape[0])])
+
+
+@pytest.mark.parametrize("qt", [8, 2, 6])
+@pytest.mark.parametrize("n_in,n_out,m", [(576, 1536, 16), (1536, 576, 64), (4096, 257, 100), (96, 70, 129),
+                                          (2048, 300, 512), (1024, 16385, 33), (160, 129, 47), (14336, 130, 20)])
+def test_prefill_gemm_g32_vs_oracle(hipdev, ora, qt, n_in, n_out, m):
+    """m >= 16 Q8_0 / Q4_0 / Q5_0 products run on the matrix cores over a
+    per-call repack into 128-element records, one exact chain per block and
+    a per-block combine; every output within the fp32 bound of the oracle on
+    its conditioning scale.  Shapes: the 576 / 1536 hidden sizes, rows that
+    end inside a record (96, 160, 576), the K split, 129 row blocks, a full
+    512-token block."""
+    rng = np.random.default_rng(4700 + 11 * qt + n_in + n_out + m)
+    w = synth.np_weights(qt, n_out, n_in, rng)
+    x = synth.np_activations(m, n_in, rng)
+    bias = rng.normal(0, 0.5, n_out).astype(np.float32)
+    want = ora.linear_quant_batch(x, w, qt, bias, m, n_out, n_in)
+    got = E.linear_quant_batch(dev(w), qt, dev(x), n_out, n_in, bias=dev(bias)).cpu().numpy()
+    exact, S = npref.g32_q80_gemm_f64(qt, w, _q80_rows(ora, x))
+    assert_tol(want - bias[None, :], exact.astype(np.float32), S, "oracle vs float64")
+    assert_tol(got, want, S + np.abs(bias)[None, :], f"{TN[qt]} gemm {n_out}x{n_in} m={m}")
+
+
+@pytest.mark.parametrize("qt", [8, 2, 6])
+def test_prefill_gemm_g32_from_q80(hipdev, ora, qt):
+    """The same GEMM fed with Q8_0 blocks already in memory: identical to the
+    f32 entry (the packer's quantization is the Q8_0 quantizer's)."""
+    n_in, n_out, m = 1248, 200, 40
+    rng = np.random.default_rng(4800 + qt)
+    w = synth.np_weights(qt, n_out, n_in, rng)
+    x = synth.np_activations(m, n_in, rng)
+    xq = _q80_rows(ora, x)
+    got = E.gemv_q8(dev(w), qt, dev(xq), m, n_out, n_in).cpu().numpy()
+    ref = E.linear_quant_batch(dev(w), qt, dev(x), n_out, n_in).cpu().numpy()
+    assert np.array_equal(got, ref)
+    exact, S = npref.g32_q80_gemm_f64(qt, w, xq)
+    assert_tol(got, exact.astype(np.float32), S, f"{TN[qt]} from Q8_0")
+
+
+@pytest.mark.parametrize("qt", [8, 2, 6])
+def test_prefill_gemm_g32_integers_exact(hipdev, qt):
+    """Unit block scales and integer activations with one +-127 per block (so
+    the Q8_0 codes equal x and dx = 1), the largest codes included: every
+    output is an exact integer and must come out exactly."""
+    n_in, n_out, m = 640, 96, 24
+    rng = np.random.default_rng(4900 + qt)
+    w = synth.np_weights(qt, n_out, n_in, rng)
+    bb = {2: 18, 6: 22, 8: 34}[qt]
+    wb = w.reshape(n_out, -1, bb)
+    wb[:, :, 0:2] = np.array([1.0], np.float16).view(np.uint8)
+    if qt == 8:
+        wb[:, :, 2] = 0x80  # q = -128 in the first slot of every block
+    x = rng.integers(-127, 128, (m, n_in)).astype(np.float32)
+    x.reshape(m, -1, 32)[:, :, 5] = 127.0
+    got = E.linear_quant_batch(dev(w), qt, dev(x), n_out, n_in).cpu().numpy()
+    xq = np.stack([npref.quantize_q8_0(x[t]) for t in range(m)])
+    want, _ = npref.g32_q80_gemm_f64(qt, w, xq)
+    assert np.all(np.abs(want) < 2**24)
+    assert np.array_equal(got.astype(np.float64), want)
+
+
+@pytest.mark.parametrize("n_in,n_out", [(576, 1536), (4096, 4096)])
+def test_prefill_gemm_q80_full_shape(hipdev, ora, n_in, n_out):
+    """Q8_0 at m = 512: a row sample against the float64 restatement, a token
+    sample also against the oracle."""
+    m = 512
+    rng = np.random.default_rng(5000 + n_in)
+    w = synth.np_weights(8, n_out, n_in, rng)
+    x = synth.np_activations(m, n_in, rng)
+    got = E.linear_quant_batch(dev(w), 8, dev(x), n_out, n_in).cpu().numpy()
+    xq = _q80_rows(ora, x)
+    rows = np.sort(rng.choice(n_out, 192, replace=False))
+    exact, S = npref.g32_q80_gemm_f64(8, w[rows], xq)
+    assert_tol(got[:, rows], exact.astype(np.float32), S, f"q8_0 gemm {n_out}x{n_in} m=512 (sampled rows)")
+    tok = rng.choice(m, 4, replace=False)
+    want = ora.linear_quant_batch(x[tok], w[rows], 8, None, 4, rows.size, n_in)
+    assert_tol(got[tok][:, rows], want, S[tok], "vs oracle")
+
+
 F16_TOL = 1e-3  # prefill bound for the fp16 matrix-core path (each factor rounded once to fp16)
 
 

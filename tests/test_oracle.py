@@ -489,3 +489,21 @@ def test_gemm_f64_restatement_vs_rows_and_oracle(ora, qt):
         assert np.allclose(S[t], s1, rtol=1e-12)
     want = ora.linear_quant_batch(x, w, qt, None, m, n_out, n_in)
     assert np.all(np.abs(want - val) <= 1e-5 * S)
+
+
+@pytest.mark.parametrize("qt", [2, 6, 8])
+def test_g32_gemm_f64_restatement_vs_rows_and_oracle(ora, qt):
+    """The many-token float64 restatement for the 32-element formats equals
+    the per-row restatement token by token and agrees with the oracle."""
+    rng = np.random.default_rng(7400 + qt)
+    n_in, n_out, m = 352, 40, 5
+    w = synth.np_weights(qt, n_out, n_in, rng)
+    x = synth.np_activations(m, n_in, rng)
+    xq = np.stack([ora.quantize_q8_0(x[t]) for t in range(m)])
+    val, S = npref.g32_q80_gemm_f64(qt, w, xq)
+    for t in range(m):
+        v1, s1 = npref.q8_rows_f64(qt, w, xq[t])
+        assert np.allclose(val[t], v1, rtol=1e-12, atol=1e-9 * s1.max())
+        assert np.allclose(S[t], s1, rtol=1e-12)
+    want = ora.linear_quant_batch(x, w, qt, None, m, n_out, n_in)
+    assert np.all(np.abs(want - val) <= 1e-5 * S)
