@@ -1,4 +1,4 @@
-// Prefill GEMM (m >= 64 tokens) of the quantized-weight path on the matrix
+// Prefill GEMM (m >= 16 tokens) of the quantized-weight path on the matrix
 // cores, every block integer exact:
 //   out[t][o] = bias[o] + sum_sb dx[t][sb] * (d[o][sb] * sumi - dmin[o][sb] * summ)
 // for Q4_K weights against Q8_K activations -- edgexpu_cpu_linear_quant_batch
@@ -45,20 +45,16 @@
 // instructions; every VALU instruction beyond that adds its own 4 cycles.
 // LDS serves ~155 B per clock per CU.  So every dequantized weight operand
 // (9 VALU) must feed several MFMAs, and every 1 KB activation operand read
-// from LDS at least one:
+// from LDS more than one:
 //   * a workgroup of 8 waves (two per SIMD) computes 256 rows x 128 tokens;
-//     wave w owns rows 32 w .. + 31 for all 128 tokens (4 tiles of 32 x 32),
-//     so each weight operand feeds 4 MFMAs and the combination costs
-//     48 VALU per tile and super-block: ~5.7 VALU per MFMA in all;
-//   * the activation pack of a half super-block (128 tokens x 128 K, 32 KiB)
-//     goes global -> LDS with buffer_load ... lds into a ring of 4 slots,
-//     requested two half super-blocks ahead (plus a 5 KiB block of bsums, d
-//     and sum |q8| per super-block, in a ring of 2); the weight bytes go
-//     straight to registers, one super-block ahead.  One barrier per half
-//     super-block, each wave waiting only for the loads of the slot it is
-//     about to read.  The slots are distinct LDS objects named statically
-//     (the loop is unrolled over the ring), so the compiler sees that reads
-//     never touch a slot in flight.
+//     wave w owns 64 rows (row group w % 4) for 64 tokens (token half w / 4):
+//     4 MFMA tiles, each weight operand and each activation operand feeding
+//     2 MFMAs, the combination 48 VALU per tile and super-block;
+//   * every main-loop load is an LDS DMA; the activation pack of a half
+//     super-block (128 tokens x 128 K, 32 KiB) one step ahead, its 5 KiB of
+//     bsums, d and sum |q8| per super-block, the weight bytes two steps
+//     ahead (the GEMM section below has the rings); one barrier per half
+//     super-block.
 // Shapes whose tiles cannot fill the chip split K over up to 4 workgroups
 // per tile; each writes its partial tile, and the last to arrive (counted
 // with a device-scope atomic) adds the partials in split order and the bias,
@@ -87,10 +83,11 @@ constexpr int kMaxSplit = 4;
 // --------------------------------------------------------------- packing
 
 constexpr int kPackTokensPerWave = 1;
-constexpr int kPackWaves = 4;  // consecutive tokens of one super-block per workgroup
+constexpr int kPackWaves = 8;  // consecutive tokens of one super-block per workgroup
+constexpr int kPackThreads = 64 * kPackWaves;
 
-// The pack kernel: one wavefront per (super-block, token), 4 wavefronts (4
-// consecutive tokens, whose 16-byte vectors share 64-byte segments) per
+// The pack kernel: one wavefront per (super-block, token), 8 wavefronts (8
+// consecutive tokens, whose 16-byte vectors fill 128-byte lines) per
 // workgroup, everything in registers.  Per token the wave quantizes the
 // block (Q8_K, bit-identical to quantize_q8_k_kernel) or reads its Q8_K
 // bytes; lane l then holds elements 4l .. 4l+3.  The 16-byte code vector of
@@ -99,7 +96,7 @@ constexpr int kPackWaves = 4;  // consecutive tokens of one super-block per work
 // 16 j + 8 + s) with j = 2 h + hf, so lane 16 j + s writes it after one
 // exchange with lane 16 j + s + 8.  Tokens past m get zero codes and d = 0.
 template <bool F32IN>
-__global__ __launch_bounds__(256) void q8k_pack_kernel(const float *__restrict__ x, int ldx,
+__global__ __launch_bounds__(kPackThreads) void q8k_pack_kernel(const float *__restrict__ x, int ldx,
                                                        const uint8_t *__restrict__ xq, size_t xq_stride, int m,
                                                        int K, int ntb, uint8_t *__restrict__ pack) {
     const int nb = K / kQKK;
@@ -606,16 +603,16 @@ size_t gemm_q4k_counter_bytes() { return kGemmCounters * sizeof(unsigned); }
 hipError_t launch_q8k_pack_f32(const float *x, int m, int K, int ldx, uint8_t *pack, hipStream_t st) {
     const int ntb = pack_tblocks(m);
     const unsigned grid = (unsigned)((K / kQKK) * ntb * (kTokB / (kPackWaves * kPackTokensPerWave)));
-    hipLaunchKernelGGL(q8k_pack_kernel<true>, dim3(grid), dim3(256), 0, st, x, ldx, nullptr, (size_t)0, m, K, ntb,
-                       pack);
+    hipLaunchKernelGGL(q8k_pack_kernel<true>, dim3(grid), dim3(kPackThreads), 0, st, x, ldx, nullptr, (size_t)0, m,
+                       K, ntb, pack);
     return hipGetLastError();
 }
 
 hipError_t launch_q8k_pack_q8k(const uint8_t *xq, size_t xq_stride, int m, int K, uint8_t *pack, hipStream_t st) {
     const int ntb = pack_tblocks(m);
     const unsigned grid = (unsigned)((K / kQKK) * ntb * (kTokB / (kPackWaves * kPackTokensPerWave)));
-    hipLaunchKernelGGL(q8k_pack_kernel<false>, dim3(grid), dim3(256), 0, st, nullptr, 0, xq, xq_stride, m, K, ntb,
-                       pack);
+    hipLaunchKernelGGL(q8k_pack_kernel<false>, dim3(grid), dim3(kPackThreads), 0, st, nullptr, 0, xq, xq_stride, m,
+                       K, ntb, pack);
     return hipGetLastError();
 }
 

@@ -1,4 +1,4 @@
-// Prefill GEMM (m >= 64 tokens) on the fp16 matrix cores: out[t][o] =
+// Prefill GEMM (m >= 16 tokens) on the fp16 matrix cores: out[t][o] =
 // bias[o] + sum_k A[t][k] * W[o][k] with
 //   A[t][k] = fp16(dx[t][sb] * q8[t][k])       the Q8_K activation the
 //                                              reference's integer dots use

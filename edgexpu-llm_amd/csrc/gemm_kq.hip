@@ -92,15 +92,15 @@ __device__ __forceinline__ uint2 q5k_step(uint32_t qs, uint32_t qh, int j) {
     return slot_order(lo + 0x80808080u, hi + 0x80808080u);
 }
 
-// get_scale_min_k4 (src/gguf_quant.c:212-220).
-__device__ __forceinline__ void k4_scale_min(const uint8_t *q, int j, int &sc, int &m) {
-    if (j < 4) {
-        sc = q[j] & 63;
-        m = q[j + 4] & 63;
-    } else {
-        sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
-        m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
-    }
+// get_scale_min_k4 (src/gguf_quant.c:212-220) on the 12 scale bytes held as
+// three words (w0: bytes 0..3, w1: 4..7, w2: 8..11), for a sub-block j that
+// may differ between lanes: shifts and one select, no indexed memory.
+__device__ __forceinline__ void k4_scale_min(uint32_t w0, uint32_t w1, uint32_t w2, int j, int &sc, int &m) {
+    const int sh = 8 * (j & 3);
+    const uint32_t a = w0 >> sh, b = w1 >> sh, c = w2 >> sh;
+    const bool lo = j < 4;
+    sc = (int)(lo ? (a & 63u) : ((c & 0xFu) | (((a >> 6) & 3u) << 4)));
+    m = (int)(lo ? (b & 63u) : (((c >> 4) & 0xFu) | (((b >> 6) & 3u) << 4)));
 }
 
 __device__ __forceinline__ uint32_t f16_pair(float lo, float hi) {
@@ -113,8 +113,8 @@ constexpr int kRepackRecs = 16;  // (row, super-block) records per workgroup
 // 16 threads per record (rows are contiguous runs of blocks, so record r is
 // the block at w + r * block bytes): thread t writes q chunk t (16 B: half
 // t / 8, lane half (t / 4) % 2, K-steps 2 (t % 4) and + 1) from three 8-byte
-// loads of its block, and threads 0..3 the c and x chunks of (half t / 2,
-// lane half t % 2).  Q6_K blocks are 2-byte aligned; gfx950 global memory
+// loads of its block, threads 0..3 the c chunks and 4..7 the x chunks of
+// (half (t / 2) % 2, lane half t % 2).  Q6_K blocks are 2-byte aligned; gfx950 global memory
 // runs in unaligned-access mode, so the loads stay plain dwordx2 loads.
 template <int TYPE>
 __global__ __launch_bounds__(256) void kq_repack_kernel(const uint8_t *__restrict__ w, long long nrec,
@@ -141,49 +141,46 @@ __global__ __launch_bounds__(256) void kq_repack_kernel(const uint8_t *__restric
         }
         *reinterpret_cast<uint4 *>(dst + hf * kKqHalfRec + 64 * h + 16 * p) = make_uint4(a.x, a.y, b.x, b.y);
     }
-    if (t < 4) {
-        const int hf = t >> 1, h = t & 1, j = 2 * h + hf;
-        uint32_t c[4], x[4];
-        int mv[4] = {0, 0, 0, 0};
-        float d, dmin = 0.0f;
+    if (t < 8) {  // threads 0..3: the c chunk, 4..7: the x chunk of (half (t >> 1) & 1, lane half t & 1)
+        const int hf = (t >> 1) & 1, h = t & 1, j = 2 * h + hf;
+        uint32_t o[4];
         if (TYPE == kTypeQ6_K) {
-            const uint32_t s4 = ldg4(blk + 192 + 4 * j);  // int8 scales of 16-element sub-blocks 4j .. 4j + 3
+            if (t < 4) {
+                const uint32_t s4 = ldg4(blk + 192 + 4 * j);  // int8 scales of 16-element sub-blocks 4j .. 4j + 3
 #pragma unroll
-            for (int kc = 0; kc < 4; ++kc) {
-                const int v = (int)(int8_t)(s4 >> (8 * kc));
-                c[kc] = f16_pair((float)(v & 15), (float)(v >> 4));
+                for (int kc = 0; kc < 4; ++kc) {
+                    const int v = (int)(int8_t)(s4 >> (8 * kc));
+                    o[kc] = f16_pair((float)(v & 15), (float)(v >> 4));
+                }
+            } else {
+                const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(blk + 208));
+                o[0] = o[1] = 0u;  // no min term
+                o[2] = hf == 0 ? __float_as_uint(d) : 0u;
+                o[3] = 0u;
             }
-            d = f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(blk + 208));
         } else {
-            const uint32_t hd = ldg4(blk);
-            uint8_t q[12];
+            const uint32_t w0 = ldg4(blk + 4), w1 = ldg4(blk + 8), w2 = ldg4(blk + 12);
+            if (t < 4) {
 #pragma unroll
-            for (int i = 0; i < 3; ++i) {
-                const uint32_t v = ldg4(blk + 4 + 4 * i);
-#pragma unroll
-                for (int b = 0; b < 4; ++b) q[4 * i + b] = (uint8_t)(v >> (8 * b));
+                for (int kc = 0; kc < 4; ++kc) {
+                    int v, m;
+                    k4_scale_min(w0, w1, w2, 2 * j + (kc >> 1), v, m);  // lo: sub-block 2j, hi: 2j + 1
+                    o[kc] = f16_pair((float)(v & 15), (float)(v >> 4));
+                }
+            } else {
+                // half 0 carries m(4h), m(4h+1), d and dmin; half 1 m(4h+2), m(4h+3)
+                int v, m0, m1;
+                k4_scale_min(w0, w1, w2, 4 * h + 2 * hf, v, m0);
+                k4_scale_min(w0, w1, w2, 4 * h + 2 * hf + 1, v, m1);
+                const uint32_t hd = ldg4(blk);
+                o[0] = f16_pair((float)m0, (float)m0);
+                o[1] = f16_pair((float)m1, (float)m1);
+                o[2] = hf == 0 ? __float_as_uint(f16_bits_to_f32(hd & 0xffffu)) : 0u;
+                o[3] = hf == 0 ? __float_as_uint(f16_bits_to_f32(hd >> 16)) : 0u;
             }
-#pragma unroll
-            for (int kc = 0; kc < 4; ++kc) {
-                int v, m;
-                k4_scale_min(q, 2 * j + (kc >> 1), v, m);  // lo: sub-block 2j, hi: 2j + 1
-                c[kc] = f16_pair((float)(v & 15), (float)(v >> 4));
-            }
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                int v;
-                k4_scale_min(q, 4 * h + k, v, mv[k]);
-            }
-            d = f16_bits_to_f32(hd & 0xffffu);
-            dmin = f16_bits_to_f32(hd >> 16);
         }
-        const int mb = 2 * hf;  // half 0 carries m(4h), m(4h+1); half 1 m(4h+2), m(4h+3)
-        x[0] = f16_pair((float)mv[mb], (float)mv[mb]);
-        x[1] = f16_pair((float)mv[mb + 1], (float)mv[mb + 1]);
-        x[2] = hf == 0 ? __float_as_uint(d) : 0u;
-        x[3] = hf == 0 ? __float_as_uint(dmin) : 0u;
-        *reinterpret_cast<uint4 *>(dst + hf * kKqHalfRec + 128 + 16 * h) = make_uint4(c[0], c[1], c[2], c[3]);
-        *reinterpret_cast<uint4 *>(dst + hf * kKqHalfRec + 160 + 16 * h) = make_uint4(x[0], x[1], x[2], x[3]);
+        *reinterpret_cast<uint4 *>(dst + hf * kKqHalfRec + (t < 4 ? 128 : 160) + 16 * h) =
+            make_uint4(o[0], o[1], o[2], o[3]);
     }
 }
 

@@ -54,16 +54,17 @@ void edgexpu_hip_clear_error(void);
  * with Q8_0 activations, Q4_K, Q5_K, Q6_K with Q8_K activations, F16 and F32
  * with f32 activations (any n_in). */
 int edgexpu_hip_supports_type(uint32_t type);
-/* Prefill (m >= 64 tokens, Q4_K) arithmetic.  No reference counterpart: the
- * reference has one CPU path.
- *  EDGEXPU_HIP_PREFILL_EXACT_INT8 (default): int8 matrix cores with every
- *    block integer exact, outputs within the 1e-5 bound of the reference;
- *  EDGEXPU_HIP_PREFILL_F16: fp16 matrix cores on the Q8_K activation and the
- *    dequantized weight (each rounded once to fp16, after exact power-of-two
- *    row prescales that keep any magnitude in fp16 range), fp32 sums: outputs
- *    within the 1e-3 prefill bound, 1.2-1.8x the int8 mode's throughput at
- *    m = 512 on the 8B shapes.
- * Process-wide setting of this library (like its stream); decode (m < 64)
+/* Prefill (m >= 16 tokens; Q5_K from 32) arithmetic.  No reference
+ * counterpart: the reference has one CPU path.
+ *  EDGEXPU_HIP_PREFILL_EXACT_INT8 (default, every quantized format): the
+ *    matrix cores on integer operands with every block integer exact,
+ *    outputs within the 1e-5 bound of the reference;
+ *  EDGEXPU_HIP_PREFILL_F16 (Q4_K; the other formats stay exact): fp16 matrix
+ *    cores on the Q8_K activation and the dequantized weight (each rounded
+ *    once to fp16, after exact power-of-two row prescales that keep any
+ *    magnitude in fp16 range), fp32 sums: outputs within the 1e-3 prefill
+ *    bound.
+ * Process-wide setting of this library (like its stream); decode (m < 16)
  * is unaffected.  Returns 1, or 0 (sticky error) for an unknown mode. */
 #define EDGEXPU_HIP_PREFILL_EXACT_INT8 0
 #define EDGEXPU_HIP_PREFILL_F16 1
