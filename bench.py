@@ -62,6 +62,8 @@ def parse():
     p.add_argument("--seed", type=int, default=20261203)
     p.add_argument("--no-extra", action="store_true", help="skip the prefill-GEMM and bulk-dequant legs")
     p.add_argument("--prefill-only", action="store_true", help="run only the prefill-GEMM leg (one JSON line)")
+    p.add_argument("--dequant-only", action="store_true",
+                   help="run only the bulk-dequant leg with its write ceilings (one JSON line)")
     p.add_argument("--launch-sweep", action="store_true",
                    help="time one Q4_K [rows x 4096] m=1 launch over row counts; fit fixed + marginal cost")
     p.add_argument("--layer-step", action="store_true",
@@ -193,6 +195,18 @@ def main():
         # the prefill GEMM leg alone (for counter runs): one JSON line
         res = prefill_leg(L, E, synth, gen, dev, capture, timed)
         print(json.dumps({"metric": "prefill quant-GEMM TOPS, 1 GPU", "n_gpus": 1, "prefill": res}), flush=True)
+        return
+    if args.dequant_only:
+        # the bulk dequant leg alone (for counter runs), with the calibration
+        # copy first: one JSON line
+        src_buf = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+        dst_buf = torch.empty_like(src_buf)
+        for _ in range(4):
+            dst_buf.copy_(src_buf)
+        torch.cuda.synchronize()
+        del src_buf, dst_buf
+        res = dequant_leg(L, E, synth, gen, dev, no_cpu=args.no_cpu)
+        print(json.dumps({"metric": "bulk dequant GB/s, 1 GPU", "n_gpus": 1, "dequant": res}), flush=True)
         return
 
     if args.calibrate_copy:
@@ -804,10 +818,44 @@ def sample_leg(L, gen, dev, no_cpu=False, vocab=128256, reps=50):
     return {"metric": "softmax + draw per decode step, 1 GPU", "vocab": vocab, "unit": "us", "sample": res}
 
 
+def _write_ceilings(dst, dst_bytes, src, src_bytes, sp):
+    """ms of a plain write of dst_bytes, and of a read of src_bytes feeding a
+    write of dst_bytes (lib/libexq_bench_read.so), best over grid sizes."""
+    import torch
+
+    lib = C.CDLL(os.path.join(ROOT, "edgexpu-llm_amd", "lib", "libexq_bench_read.so"))
+    lib.exq_bench_write.argtypes = [C.c_void_p, C.c_longlong, C.c_int, C.c_void_p]
+    lib.exq_bench_write.restype = C.c_int
+    lib.exq_bench_read_write.argtypes = [C.c_void_p, C.c_longlong, C.c_void_p, C.c_longlong, C.c_int, C.c_void_p]
+    lib.exq_bench_read_write.restype = C.c_int
+    db = dst_bytes // 16 * 16
+
+    def best(fn):
+        res = []
+        for grid in (2048, 4096, 8192, 16384):
+            if fn(grid) != 0:
+                raise RuntimeError("ceiling kernel refused its arguments")
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(3):
+                fn(grid)
+            b.record()
+            torch.cuda.synchronize()
+            res.append(a.elapsed_time(b) / 3)
+        return min(res)
+
+    w = best(lambda g: lib.exq_bench_write(dst.data_ptr(), db, g, sp))
+    rw = best(lambda g: lib.exq_bench_read_write(src.data_ptr(), src_bytes, dst.data_ptr(), db, g, sp))
+    return w, rw
+
+
 def dequant_leg(L, E, synth, gen, dev, no_cpu=False, types=((8, "q8_0"), (12, "q4_k"), (14, "q6_k"))):
     """Bulk dequantization of 1 GiB of blocks per format to f32 (the block
     contents are a 16 MiB seeded tile repeated); GB/s = (src + dst bytes) / s.
-    Beside it, unless no_cpu, the reference's own dequant on one host core."""
+    Beside it the same bytes without the arithmetic (a plain write of the
+    output; a read of the source feeding the write), and, unless no_cpu, the
+    reference's own dequant on one host core."""
     import torch
 
     out = {}
@@ -841,6 +889,12 @@ def dequant_leg(L, E, synth, gen, dev, no_cpu=False, types=((8, "q8_0"), (12, "q
         byts = nblk * bb + n * 4
         out[name] = {"blocks": nblk, "src_bytes": nblk * bb, "dst_bytes": n * 4, "ms": round(ms, 3),
                      "GBps": round(byts / (ms * 1e-3) / 1e9, 1)}
+        # ceilings of the same bytes without the arithmetic (best grid):
+        # writing the output alone, and reading the source while writing it
+        cw, crw = _write_ceilings(dst, n * 4, src, (nblk * bb) // 16 * 16, sp)
+        out[name]["ceiling"] = {"write_only_ms": round(cw, 3), "read_write_ms": round(crw, 3),
+                                "read_write_GBps": round(byts / (crw * 1e-3) / 1e9, 1),
+                                "frac_of_read_write": round(crw / ms, 3)}
         if ref is not None:
             # the reference's dequant is single-threaded (no OpenMP): the same
             # 1 GiB of blocks in host memory, 64 MiB pieces in turn (source and

@@ -47,13 +47,39 @@ __global__ __launch_bounds__(256) void dequant_q8_0_kernel(const uint8_t *__rest
     dq_q8_0(src, t, dst);
 }
 
+// Output stores of the bulk kernels: the f32 output (up to 8x the source)
+// is not read again by the kernel, so it streams past the caches.
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void store8_nt(float *dst, const float (&y)[8]) {
+    v4f *p = reinterpret_cast<v4f *>(dst);
+    __builtin_nontemporal_store(v4f{y[0], y[1], y[2], y[3]}, p);
+    __builtin_nontemporal_store(v4f{y[4], y[5], y[6], y[7]}, p + 1);
+}
+
+// Units per thread of the Q4_K and Q6_K bulk kernels: both units' loads
+// are issued before either's arithmetic.
+constexpr int kDqUnits = 2;
+
 // 32 threads per 144-byte super-block; thread p covers elements 8p..8p+7,
 // which lie in sub-block s = p/4 (64-chunk j = s/2, nibble half s&1).
-__device__ __forceinline__ void dq_q4_k(const uint8_t *__restrict__ src, long long t, float *__restrict__ dst) {
+struct Q4KUnit {
+    uint4 h;  // d, dmin, scales[12]
+    uint2 q;
+};
+
+__device__ __forceinline__ void dq_q4_k_load(const uint8_t *__restrict__ src, long long t, Q4KUnit &u) {
     const long long b = t >> 5;
     const int p = (int)(t & 31);
     const uint8_t *sb = src + b * kBytesQ4_K;
-    const uint4 h = *reinterpret_cast<const uint4 *>(sb);  // d, dmin, scales[12]
+    u.h = *reinterpret_cast<const uint4 *>(sb);
+    u.q = *reinterpret_cast<const uint2 *>(sb + 16 + 32 * (p >> 3) + 8 * (p & 3));
+}
+
+__device__ __forceinline__ void dq_q4_k_finish(const Q4KUnit &u, long long t, float *__restrict__ dst) {
+    const long long b = t >> 5;
+    const int p = (int)(t & 31);
+    const uint4 h = u.h;
     const float d = f16_bits_to_f32(h.x & 0xffffu);
     const float dmin = f16_bits_to_f32(h.x >> 16);
     const int s = p >> 2;
@@ -70,29 +96,39 @@ __device__ __forceinline__ void dq_q4_k(const uint8_t *__restrict__ src, long lo
     }
     const float ds = d * (float)sc;
     const float ms = dmin * (float)mn;
-    const int j = s >> 1;
     const int shift = (s & 1) * 4;
-    const uint2 q = *reinterpret_cast<const uint2 *>(sb + 16 + 32 * j + 8 * (p & 3));
     float y[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        const uint32_t w = e < 4 ? q.x : q.y;
+        const uint32_t w = e < 4 ? u.q.x : u.q.y;
         const int c = (int)((w >> (8 * (e & 3) + shift)) & 0x0fu);
         const float prod = ds * (float)c;
         y[e] = prod - ms;
     }
-    store8(dst + b * kQKK + 8 * p, y);
+    store8_nt(dst + b * kQKK + 8 * p, y);
+}
+
+__device__ __forceinline__ void dq_q4_k(const uint8_t *__restrict__ src, long long t, float *__restrict__ dst) {
+    Q4KUnit u;
+    dq_q4_k_load(src, t, u);
+    dq_q4_k_finish(u, t, dst);
 }
 
 __global__ __launch_bounds__(256) void dequant_q4_k_kernel(const uint8_t *__restrict__ src,
                                                            long long n_threads, float *__restrict__ dst) {
-    const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= n_threads) return;
-    dq_q4_k(src, t, dst);
+    const long long t0 = (long long)blockIdx.x * (256 * kDqUnits) + threadIdx.x;
+    Q4KUnit u[kDqUnits];
+#pragma unroll
+    for (int k = 0; k < kDqUnits; ++k)
+        if (t0 + 256 * k < n_threads) dq_q4_k_load(src, t0 + 256 * k, u[k]);
+#pragma unroll
+    for (int k = 0; k < kDqUnits; ++k)
+        if (t0 + 256 * k < n_threads) dq_q4_k_finish(u[k], t0 + 256 * k, dst);
 }
 
 // 32 threads per 210-byte super-block; thread p covers elements 8p..8p+7:
-// half h = p/16, quarter k = (p%16)/4, position l0 = 8*(p%4).
+// half h = p/16, quarter k = (p%16)/4, position l0 = 8*(p%4).  Used by the
+// row gather; the bulk kernel below gives a thread all four quarters.
 __device__ __forceinline__ void dq_q6_k(const uint8_t *__restrict__ src, long long t, float *__restrict__ dst) {
     const long long b = t >> 5;
     const int p = (int)(t & 31);
@@ -118,11 +154,96 @@ __device__ __forceinline__ void dq_q6_k(const uint8_t *__restrict__ src, long lo
     store8(dst + b * kQKK + 8 * p, y);
 }
 
+// Bulk Q6_K: 16 threads per super-block; thread p writes the 16 contiguous
+// elements 128 h + 32 k + l0 .. + 15 (h = p / 8, quarter k = (p / 2) % 4,
+// l0 = 16 (p % 2)) -- one 16-element sub-block, one scale -- from 16 bytes
+// of ql, 16 of qh (each from aligned words, the block being only 2-byte
+// aligned), the scale byte and d.  Two units per thread, both units' loads
+// before either's arithmetic.
+struct Q6KUnit {
+    uint4 ql, qh;
+    uint32_t s4, dw;  // the scale byte, d's bits
+};
+
+// 16 bytes at p (2-byte aligned) from 4-byte-aligned words: a dwordx4 and
+// one dword at the aligned address below p, joined with v_alignbyte.  A
+// 16-byte load at an address 2 mod 4 runs several times slower than these.
+// The fifth word is only needed when p is not 4-byte aligned; otherwise the
+// fourth is read again, so nothing past p + 15 is touched.
+__device__ __forceinline__ uint4 ldg16_a2(const uint8_t *p) {
+    // the aligned address by subtraction from p (not through an integer), so
+    // the compiler keeps these global loads
+    const uint32_t sh = (uint32_t)((uintptr_t)p & 3);
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(p - sh);
+    const uint32_t w0 = q[0], w1 = q[1], w2 = q[2], w3 = q[3], w4 = q[sh != 0 ? 4 : 3];
+    return make_uint4(__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh),
+                      __builtin_amdgcn_alignbyte(w3, w2, sh), __builtin_amdgcn_alignbyte(w4, w3, sh));
+}
+
+__device__ __forceinline__ void dq_q6_k16_load(const uint8_t *__restrict__ src, long long t, Q6KUnit &u) {
+    const long long b = t >> 4;
+    const int p = (int)(t & 15);
+    const int h = p >> 3, k = (p >> 1) & 3, l0 = 16 * (p & 1);
+    const uint8_t *sb = src + b * kBytesQ6_K;
+    u.ql = ldg16_a2(sb + 64 * h + 32 * (k & 1) + l0);
+    u.qh = ldg16_a2(sb + 128 + 32 * h + l0);
+    u.s4 = sb[192 + p];                                        // sc[8h + 2k + p % 2] = sc[p]
+    u.dw = *reinterpret_cast<const uint16_t *>(sb + 208);      // d (2-byte aligned)
+}
+
+// The unit's 16 outputs (values only; the caller places them).
+__device__ __forceinline__ void dq_q6_k16_values(const Q6KUnit &u, int p, float (&y)[16]) {
+    const int k = (p >> 1) & 3;
+    const float d = f16_bits_to_f32(u.dw);
+    const float ds = d * (float)(int8_t)(u.s4 & 0xffu);
+    const int nshift = (k >> 1) * 4, hshift = 2 * k;
+    const uint32_t ql[4] = {u.ql.x, u.ql.y, u.ql.z, u.ql.w}, qh[4] = {u.qh.x, u.qh.y, u.qh.z, u.qh.w};
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int lo = (int)((ql[e >> 2] >> (8 * (e & 3) + nshift)) & 0x0fu);
+        const int hi = (int)((qh[e >> 2] >> (8 * (e & 3) + hshift)) & 0x03u);
+        y[e] = ds * (float)((lo | (hi << 4)) - 32);
+    }
+}
+
+// A wave's 64 units are 4 super-blocks of contiguous output (4 KiB).  Each
+// lane's 16 values go to LDS, then come back so that each of the four
+// stores writes 1 KiB of consecutive float4 (lane i: float4 64 s + i): whole
+// lines per store instruction, which streaming stores need.
 __global__ __launch_bounds__(256) void dequant_q6_k_kernel(const uint8_t *__restrict__ src,
                                                            long long n_threads, float *__restrict__ dst) {
-    const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= n_threads) return;
-    dq_q6_k(src, t, dst);
+    __shared__ v4f stage[4][4 * 64];  // [wave][float4 of the wave's 4 KiB]
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const long long t0 = (long long)blockIdx.x * (256 * kDqUnits) + threadIdx.x;
+    Q6KUnit u[kDqUnits];
+    // loads clamped to the last unit (in bounds, no branch around them)
+#pragma unroll
+    for (int k = 0; k < kDqUnits; ++k) dq_q6_k16_load(src, min(t0 + 256 * k, n_threads - 1), u[k]);
+#pragma unroll
+    for (int k = 0; k < kDqUnits; ++k) {
+        const long long t = t0 + 256 * k;
+        // the wave's first unit: units are 16 per super-block and a wave's 64
+        // units are whole super-blocks (n_threads is a multiple of 16)
+        const long long wt0 = t - lane;
+        if (wt0 >= n_threads) break;  // wave-uniform
+        float y[16];
+        dq_q6_k16_values(u[k], (int)(t & 15), y);  // lanes past the end: discarded below
+#pragma unroll
+        for (int q = 0; q < 4; ++q) stage[wv][4 * lane + q] = v4f{y[4 * q], y[4 * q + 1], y[4 * q + 2], y[4 * q + 3]};
+        // one wave's LDS operations execute in issue order, so only the
+        // compiler must not move the reads above the writes (a fence would
+        // also wait for the other unit's loads)
+        asm volatile("" ::: "memory");
+        // the wave's output starts at super-block wt0 / 16; float4 64 s + lane of it
+        v4f *out = reinterpret_cast<v4f *>(dst + (wt0 >> 4) * kQKK);
+        const long long live4 = (min(n_threads, wt0 + 64) - wt0) * 4;  // float4s of live units
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int f = 64 * s + lane;
+            if (f < live4) __builtin_nontemporal_store(stage[wv][f], out + f);
+        }
+        asm volatile("" ::: "memory");
+    }
 }
 
 // 4 threads per 18-byte Q4_0 block; thread p covers elements 8p..8p+7: the
@@ -346,13 +467,13 @@ hipError_t launch_dequantize(const uint8_t *src, int type, unsigned long long n,
             break;
         case kTypeQ4_K:
             threads = (long long)(n / kQKK) * 32;
-            hipLaunchKernelGGL(dequant_q4_k_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, src,
-                               threads, dst);
+            hipLaunchKernelGGL(dequant_q4_k_kernel, dim3((unsigned)((threads + 256 * kDqUnits - 1) / (256 * kDqUnits))),
+                               dim3(256), 0, st, src, threads, dst);
             break;
         case kTypeQ6_K:
-            threads = (long long)(n / kQKK) * 32;
-            hipLaunchKernelGGL(dequant_q6_k_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, src,
-                               threads, dst);
+            threads = (long long)(n / kQKK) * 16;
+            hipLaunchKernelGGL(dequant_q6_k_kernel, dim3((unsigned)((threads + 256 * kDqUnits - 1) / (256 * kDqUnits))),
+                               dim3(256), 0, st, src, threads, dst);
             break;
         case kTypeQ4_0:
         case kTypeQ5_0:
