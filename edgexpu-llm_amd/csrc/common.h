@@ -70,6 +70,30 @@ __device__ __forceinline__ uint4 ldg16(const uint8_t *p) { return ldg_unaligned<
 __device__ __forceinline__ uint2 ldg8(const uint8_t *p) { return ldg_unaligned<uint2>(p); }
 __device__ __forceinline__ uint32_t ldg4(const uint8_t *p) { return ldg_unaligned<uint32_t>(p); }
 
+// 16 / 8 bytes at an even address p from 4-byte-aligned loads: the words
+// from p - (p & 3) and the 16-bit word ending the range, joined with
+// v_alignbyte.  Measured on gfx950: wide loads at addresses 2 mod 4 (every
+// other Q8_0 / Q6_K / Q4_0 / Q5_0 block) run several times slower than
+// these.  Only bytes in [p - 2, p + 16) are read, and p - 2 only when p is
+// 2 mod 4, so never before the 4-byte-aligned start of the buffer that holds
+// p.  p must be even.  The aligned address is formed by subtracting from p,
+// not through an integer, so the loads stay global ones.
+__device__ __forceinline__ uint4 ldg16_a2(const uint8_t *p) {
+    const uint32_t sh = (uint32_t)((uintptr_t)p & 3);
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(p - sh);
+    const uint32_t w0 = q[0], w1 = q[1], w2 = q[2], w3 = q[3];
+    const uint32_t t = *reinterpret_cast<const uint16_t *>(p + 14);
+    return make_uint4(__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh),
+                      __builtin_amdgcn_alignbyte(w3, w2, sh), __builtin_amdgcn_alignbyte(t, w3, sh));
+}
+__device__ __forceinline__ uint2 ldg8_a2(const uint8_t *p) {
+    const uint32_t sh = (uint32_t)((uintptr_t)p & 3);
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(p - sh);
+    const uint32_t w0 = q[0], w1 = q[1];
+    const uint32_t t = *reinterpret_cast<const uint16_t *>(p + 6);
+    return make_uint2(__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(t, w1, sh));
+}
+
 // IEEE half -> float; exact for every input including subnormals.
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
     _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)(h & 0xffffu));

@@ -165,21 +165,6 @@ struct Q6KUnit {
     uint32_t s4, dw;  // the scale byte, d's bits
 };
 
-// 16 bytes at p (2-byte aligned) from 4-byte-aligned words: a dwordx4 and
-// one dword at the aligned address below p, joined with v_alignbyte.  A
-// 16-byte load at an address 2 mod 4 runs several times slower than these.
-// The fifth word is only needed when p is not 4-byte aligned; otherwise the
-// fourth is read again, so nothing past p + 15 is touched.
-__device__ __forceinline__ uint4 ldg16_a2(const uint8_t *p) {
-    // the aligned address by subtraction from p (not through an integer), so
-    // the compiler keeps these global loads
-    const uint32_t sh = (uint32_t)((uintptr_t)p & 3);
-    const uint32_t *q = reinterpret_cast<const uint32_t *>(p - sh);
-    const uint32_t w0 = q[0], w1 = q[1], w2 = q[2], w3 = q[3], w4 = q[sh != 0 ? 4 : 3];
-    return make_uint4(__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh),
-                      __builtin_amdgcn_alignbyte(w3, w2, sh), __builtin_amdgcn_alignbyte(w4, w3, sh));
-}
-
 __device__ __forceinline__ void dq_q6_k16_load(const uint8_t *__restrict__ src, long long t, Q6KUnit &u) {
     const long long b = t >> 4;
     const int p = (int)(t & 15);

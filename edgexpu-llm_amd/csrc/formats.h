@@ -189,10 +189,10 @@ struct FmtQ6K {
     __device__ static void load_w(const A &a, int row, int unit, W &w) {
         const int i = unit >> 2, h = (unit >> 1) & 1, p = unit & 1;
         const uint8_t *sb = a.w + (size_t)row * a.row_bytes + (size_t)i * kBytesQ6_K;
-        w.A = ldg16(sb + 64 * h + 16 * p);
-        w.B = ldg16(sb + 64 * h + 32 + 16 * p);
-        w.H = ldg16(sb + 128 + 32 * h + 16 * p);
-        w.sc = ldg8(sb + 192 + 8 * h);
+        w.A = ldg16_a2(sb + 64 * h + 16 * p);  // 210-byte super-blocks: sb is only even
+        w.B = ldg16_a2(sb + 64 * h + 32 + 16 * p);
+        w.H = ldg16_a2(sb + 128 + 32 * h + 16 * p);
+        w.sc = ldg8_a2(sb + 192 + 8 * h);
         w.d = *reinterpret_cast<const uint16_t *>(sb + 208);
     }
     __device__ static void dot1(const W &w, int unit, const Act &xa, float &acc) {
@@ -240,7 +240,7 @@ struct FmtQ80 {
     template <class A>
     __device__ static void load_act(const A &a, int unit, int tk, Act &x) {
         const uint8_t *blk = a.xq + (size_t)tk * a.xq_stride + (size_t)unit * kBytesQ8_0;
-        const uint4 t0 = ldg16(blk + 2), t1 = ldg16(blk + 18);
+        const uint4 t0 = ldg16_a2(blk + 2), t1 = ldg16_a2(blk + 18);  // 34-byte blocks
         x.q[0] = t0.x; x.q[1] = t0.y; x.q[2] = t0.z; x.q[3] = t0.w;
         x.q[4] = t1.x; x.q[5] = t1.y; x.q[6] = t1.z; x.q[7] = t1.w;
         x.dx = f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(blk));
@@ -260,8 +260,8 @@ struct FmtQ80 {
     __device__ static void load_w(const A &a, int row, int unit, W &w) {
         const uint8_t *blk = a.w + (size_t)row * a.row_bytes + (size_t)unit * kBytesQ8_0;
         w.d = *reinterpret_cast<const uint16_t *>(blk);
-        w.q0 = ldg16(blk + 2);
-        w.q1 = ldg16(blk + 18);
+        w.q0 = ldg16_a2(blk + 2);  // 34-byte blocks: blk is only even
+        w.q1 = ldg16_a2(blk + 18);
     }
     __device__ static void dot1(const W &w, int, const Act &xa, float &acc) {
         const float d = f16_bits_to_f32(w.d);
@@ -330,7 +330,7 @@ struct FmtQ40 {
     __device__ static void load_w(const A &a, int row, int unit, W &w) {
         const uint8_t *blk = a.w + (size_t)row * a.row_bytes + (size_t)unit * kBytesQ4_0;
         w.d = ldg_unaligned<uint16_t>(blk);
-        w.q = ldg16(blk + 2);
+        w.q = ldg16_a2(blk + 2);  // 18-byte blocks
     }
     __device__ static void dot1(const W &w, int, const Act &xa, float &acc) {
         const float d = f16_bits_to_f32(w.d);
@@ -365,9 +365,10 @@ struct FmtQ50 {
     template <class A>
     __device__ static void load_w(const A &a, int row, int unit, W &w) {
         const uint8_t *blk = a.w + (size_t)row * a.row_bytes + (size_t)unit * kBytesQ5_0;
-        w.d = ldg_unaligned<uint16_t>(blk);
-        w.qh = ldg_unaligned<uint32_t>(blk + 2);
-        w.q = ldg16(blk + 6);
+        const uint2 h = ldg8_a2(blk);  // 22-byte blocks: d, qh, 2 bytes of qs
+        w.d = h.x & 0xffffu;
+        w.qh = __builtin_amdgcn_alignbyte(h.y, h.x, 2);
+        w.q = ldg16_a2(blk + 6);
     }
     __device__ static void dot1(const W &w, int, const Act &xa, float &acc) {
         const float d = f16_bits_to_f32(w.d);
