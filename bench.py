@@ -68,6 +68,8 @@ def parse():
                    help="time one Q4_K [rows x 4096] m=1 launch over row counts; fit fixed + marginal cost")
     p.add_argument("--layer-step", action="store_true",
                    help="time the decode step with the layer ops on device: fused layer entry vs separate launches")
+    p.add_argument("--sync-costs", action="store_true",
+                   help="time an empty dependent launch against a grid barrier inside one launch (one JSON line)")
     p.add_argument("--read-ceiling", action="store_true",
                    help="time a plain streaming read of each decode launch's weight bytes (one JSON line)")
     p.add_argument("--formats", action="store_true",
@@ -184,6 +186,9 @@ def main():
         return
     if args.read_ceiling:
         print(json.dumps(read_ceiling(E, cfg, args.workload, dev)), flush=True)
+        return
+    if args.sync_costs:
+        print(json.dumps(sync_costs(dev)), flush=True)
         return
     if args.formats:
         print(json.dumps(formats_leg(L, E, synth, gen, dev, no_cpu=args.no_cpu)), flush=True)
@@ -735,6 +740,54 @@ def read_ceiling(E, cfg, workload, dev):
         del buf
     return {"metric": "plain read of each decode launch's weight bytes, us per launch, 1 GPU",
             "workload": workload, "launches": res}
+
+
+def sync_costs(dev):
+    """What a persistent multi-phase decode kernel would pay per phase
+    instead of a dependent launch (lib/libexq_bench_read.so): an empty
+    launch in a HIP graph, against a grid barrier of one workgroup per CU
+    (all 256, or the 32 of XCD 0) with agent-scope release/acquire (every
+    store visible to every later load on any XCD) or with relaxed atomics
+    only (no data visibility).  Barrier cost = (launch of 101 barriers -
+    launch of 1) / 100."""
+    import torch
+
+    lib = C.CDLL(os.path.join(ROOT, "edgexpu-llm_amd", "lib", "libexq_bench_read.so"))
+    lib.exq_bench_empty.argtypes = [C.c_int, C.c_int, C.c_void_p]
+    lib.exq_bench_barrier.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p]
+    lib.exq_bench_barrier_words.restype = C.c_longlong
+    words = torch.zeros(int(lib.exq_bench_barrier_words()) // 4, dtype=torch.int32, device=dev)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    res = {"cus": cus, "empty_launch_us": {}, "barrier_us": {}}
+    for grid, threads in ((1, 64), (cus, 1024)):
+        def empties(sp, grid=grid, threads=threads):
+            for _ in range(200):
+                if lib.exq_bench_empty(grid, threads, sp) != 0:
+                    raise RuntimeError("exq_bench_empty failed")
+
+        g = capture(empties)
+        res["empty_launch_us"][f"{grid}x{threads}"] = round(min(timed(g.replay, 3) for _ in range(2)) * 1e3 / 200, 3)
+        del g
+    for xcd0 in (0, 1):
+        for mode in (0, 1):
+            per = {}
+            for rounds in (1, 101):
+                def barriers(sp, rounds=rounds):
+                    for _ in range(20):
+                        if lib.exq_bench_barrier(words.data_ptr(), cus, 1024, rounds, mode, xcd0, sp) != 0:
+                            raise RuntimeError("exq_bench_barrier failed")
+
+                g = capture(barriers)
+                per[rounds] = min(timed(g.replay, 2) for _ in range(2)) * 1e3 / 20
+                del g
+            key = ("xcd0_32wg" if xcd0 else f"all_{cus}wg") + ("_release_acquire" if mode == 0 else "_relaxed")
+            res["barrier_us"][key] = {"launch_1_barrier": round(per[1], 3),
+                                      "per_barrier": round((per[101] - per[1]) / 100, 3)}
+    torch.cuda.synchronize()
+    err = int(words.view(-1)[64].item())
+    if err != 0:
+        raise RuntimeError("a barrier wait ran out of polls (grid not co-resident)")
+    return {"metric": "dependent launch vs grid barrier, us, 1 GPU", **res}
 
 
 def formats_leg(L, E, synth, gen, dev, no_cpu=False):

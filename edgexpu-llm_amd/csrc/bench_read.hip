@@ -8,7 +8,10 @@
 //  * write and read+write: the bulk dequant's bytes without its arithmetic --
 //    16-byte stores of a constant over the output, and a pass that reads the
 //    source (16 bytes per lane) and writes the output (8 floats per lane per
-//    source word, one 16-byte load per two 16-byte stores, as Q8_0's ratio).
+//    source word, one 16-byte load per two 16-byte stores, as Q8_0's ratio);
+//  * synchronisation costs: an empty launch (a dependent kernel boundary in a
+//    graph) against a grid barrier inside one launch, the cost a persistent
+//    multi-phase kernel would pay instead of each boundary.
 
 #include <hip/hip_runtime.h>
 
@@ -45,7 +48,82 @@ __global__ __launch_bounds__(256) void read_write_kernel(const v4u *__restrict__
     }
 }
 
+__global__ void empty_kernel() {}
+
+// Barrier words: arrivals, finished workgroups, error flag (separate lines).
+struct BarWords {
+    unsigned arrive, pad0[31];
+    unsigned done, pad1[31];
+    int err, pad2[31];
+};
+
+// `rounds` grid barriers.  Workgroups of XCD 0 only (b % 8 == 0: workgroups
+// are dispatched to the 8 XCDs round robin) when xcd0, else all.  mode 0:
+// release add / acquire fence at agent scope (every store before the barrier
+// visible to every load after it, on any XCD: an L2 writeback and an L2
+// invalidate per workgroup); mode 1: relaxed agent-scope add and polls only
+// (the synchronisation without the data visibility).  Every wait is bounded
+// (spin polls, then err = 1 and on); the last workgroup resets the words.
+template <int MODE>
+__global__ void barrier_kernel(BarWords *w, int rounds, int xcd0, int spin) {
+    if (xcd0 && blockIdx.x % 8 != 0) return;
+    const unsigned n = xcd0 ? gridDim.x / 8 : gridDim.x;
+    for (int r = 1; r <= rounds; ++r) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            if (MODE == 0) __hip_atomic_fetch_add(&w->arrive, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            else __hip_atomic_fetch_add(&w->arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            int k = 0;
+            while (__hip_atomic_load(&w->arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (unsigned)r * n) {
+                if (++k >= spin) {
+                    __hip_atomic_store(&w->err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            if (MODE == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const unsigned old = __hip_atomic_fetch_add(&w->done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == n - 1u) {
+            __hip_atomic_store(&w->arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&w->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
 }  // namespace
+
+// An empty kernel of grid x threads.  0 on success.
+extern "C" int exq_bench_empty(int grid, int threads, void *stream) {
+    if (grid < 1 || grid > 65536 || threads < 64 || threads > 1024) return 1;
+    hipLaunchKernelGGL(empty_kernel, dim3((unsigned)grid), dim3((unsigned)threads), 0, (hipStream_t)stream);
+    return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+// Bytes of the barrier words (zeroed by the caller once).
+extern "C" long long exq_bench_barrier_words(void) { return (long long)sizeof(BarWords); }
+
+// One launch of `rounds` grid barriers over grid workgroups of `threads`
+// (one per CU at 1024 threads: grid <= the CU count keeps every workgroup
+// resident, which the barrier needs).  0 on success; the error flag sits at
+// byte 256 of the words.
+extern "C" int exq_bench_barrier(void *words, int grid, int threads, int rounds, int mode, int xcd0, void *stream) {
+    if (words == nullptr || grid < 8 || grid > 256 || threads < 64 || threads > 1024 || rounds < 1 || rounds > 1000 ||
+        (mode != 0 && mode != 1))
+        return 1;
+    constexpr int kSpin = 1 << 18;
+    if (mode == 0)
+        hipLaunchKernelGGL(barrier_kernel<0>, dim3((unsigned)grid), dim3((unsigned)threads), 0, (hipStream_t)stream,
+                           static_cast<BarWords *>(words), rounds, xcd0, kSpin);
+    else
+        hipLaunchKernelGGL(barrier_kernel<1>, dim3((unsigned)grid), dim3((unsigned)threads), 0, (hipStream_t)stream,
+                           static_cast<BarWords *>(words), rounds, xcd0, kSpin);
+    return hipGetLastError() == hipSuccess ? 0 : 2;
+}
 
 // Writes bytes (a multiple of 16, dst 16-byte aligned) with grid workgroups
 // of 256 threads.  0 on success.
