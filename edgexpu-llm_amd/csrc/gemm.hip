@@ -588,7 +588,10 @@ bool gemm_q8_supported(int type, int n_out, int K, int m) {
 
 size_t gemm_q4k_pack_bytes(int m, int K) { return (size_t)(K / kQKK) * pack_tblocks(m) * kPkBlk; }
 
-static int gemm_split(int ntiles, int nblk) { return gemm_split_for(ntiles, nblk, kMaxSplit); }
+static int gemm_split(int ntiles, int nblk) {
+    static const int max_split = tuning_knob("EXQ_GEMM_SPLIT", kMaxSplit);  // sweep builds only
+    return gemm_split_for(ntiles, nblk, max_split < 1 ? 1 : (max_split > kMaxSplit ? kMaxSplit : max_split));
+}
 
 static int gemm_tiles(int m, int n_out) { return ((n_out + kRowsB - 1) / kRowsB) * pack_tblocks(m); }
 

@@ -75,57 +75,64 @@ struct WSrc {
     size_t row_bytes;
 };
 
+// v_cvt_i32_f32 on a value already rounded to an integer: NaN gives 0,
+// out-of-range values saturate (inline assembly: the hardware's result for
+// every input, which a C conversion leaves undefined for NaN).
+__device__ __forceinline__ int cvt_f32_i32(float v) {
+    int r;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+
 // Q8_K quantization of x into LDS (src/gguf_dot_q8.c:360-412) with the
 // arithmetic of quantize_q8_k_kernel.  16 threads per 256-element block, each
 // owning one 16-element group (so its int16 sum needs no reduction); NT/16
 // blocks per round, one round in registers at a time (the register budget of
-// the staging decides the kernel's occupancy).  The first-index signed
-// maximum is the largest |x| of the block, then the smallest
-//   (index << 1) | sign
-// among the elements equal to it (equal magnitudes -> lowest index wins;
-// zeros and NaN never enter, matching the reference's strict '>' from
-// amax = 0).
+// the staging decides the kernel's occupancy).
+//
+// The reference's scale comes from the first element of largest |x| (its
+// strict '>' from amax = 0: NaN never enters, equal magnitudes keep the
+// lowest index), and only that element's sign matters: each thread finds
+// its first element equal to +-amax (a compare and a select per element),
+// and the lowest thread holding one decides.  With iscale finite every
+// |iscale * x| is at most 127 (|x| <= amax) or NaN, so rint and the
+// hardware conversion (NaN -> 0, as lrintf's LONG_MIN truncates to 0) give
+// the reference's codes with no clamp; with iscale infinite (amax below
+// ~3.7e-37) every product is infinite or NaN and every reference code is 0.
+// Codes are packed four to a word with byte permutes and their sums taken
+// with sdot4 against ones.
 template <int NT>
 __device__ __forceinline__ void quantize_q8_k_group(const float (&xs)[16], int blk, int total, int nb, int K,
                                                     int sub, int8_t *lq, float *ld, int16_t *lbs) {
     const bool valid = blk < total;  // uniform over each 16-thread group
-    // this thread's largest |x| (fmaxf skips NaN like the strict '>'), then
-    // the first of its elements that attains it
     float am = 0.0f;
 #pragma unroll
     for (int e = 0; e < 16; ++e) am = fmaxf(am, fabsf(xs[e]));
-    uint32_t first = 15u, neg = 0u;
-#pragma unroll
-    for (int e = 15; e >= 0; --e) {
-        const bool hit = fabsf(xs[e]) == am;
-        first = hit ? (uint32_t)e : first;
-        neg = hit ? (xs[e] < 0.0f ? 1u : 0u) : neg;
-    }
-    // the block's largest |x| over its 16 threads (one DPP row), then, among
-    // the threads holding it, the lowest (element index, sign): the first
-    // element that attains the maximum
     const float amax = row16_max(am);
-    const uint32_t win = row16_min(am == amax && amax > 0.0f ? ((((uint32_t)(16 * sub) + first) << 1) | neg)
-                                                              : 0xffffffffu);
+    float first = 0.0f;  // this thread's first element of magnitude amax (0: none)
+#pragma unroll
+    for (int e = 15; e >= 0; --e) first = fabsf(xs[e]) == amax ? xs[e] : first;
+    const uint32_t win =
+        row16_min(amax > 0.0f && first != 0.0f ? (((uint32_t)sub << 1) | (first < 0.0f ? 1u : 0u)) : 0xffffffffu);
     if (!valid) return;
     const int tok = blk / nb, b = blk - tok * nb;
-    uint32_t words[4] = {0u, 0u, 0u, 0u};
+    const float maxv = (win & 1u) ? -amax : amax;
+    const float iscale = -127.0f / maxv;
+    const bool codes = amax > 0.0f && fabsf(iscale) < INFINITY;  // uniform over the group
+    uint32_t words[4];
     int sum = 0;
-    float d = 0.0f;
-    if (amax > 0.0f) {
-        const float maxv = (win & 1u) ? -amax : amax;
-        const float iscale = -127.0f / maxv;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const float q0 = iscale * xs[e];
-            // lrintf: a NaN or infinite product gives LONG_MIN, whose low 32 bits are 0
-            int q = fabsf(q0) < 2147483648.0f ? (int)rintf(q0) : 0;
-            q = q > 127 ? 127 : (q < -127 ? -127 : q);
-            sum += q;
-            words[e >> 2] |= (uint32_t)(q & 0xff) << (8 * (e & 3));
-        }
-        d = 1.0f / iscale;
+    for (int k = 0; k < 4; ++k) {
+        int q[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) q[e] = cvt_f32_i32(rintf(iscale * xs[4 * k + e]));
+        // bytes q0..q3, low to high
+        const uint32_t lo = __builtin_amdgcn_perm((uint32_t)q[1], (uint32_t)q[0], 0x0c0c0400u);
+        const uint32_t hi = __builtin_amdgcn_perm((uint32_t)q[3], (uint32_t)q[2], 0x04000c0cu);
+        words[k] = codes ? (lo | hi) : 0u;
+        sum = __builtin_amdgcn_sdot4((int)words[k], 0x01010101, sum, false);
     }
+    const float d = amax > 0.0f ? 1.0f / iscale : 0.0f;
     *reinterpret_cast<uint4 *>(lq + (size_t)tok * K + (size_t)b * kQKK + 16 * sub) =
         make_uint4(words[0], words[1], words[2], words[3]);
     lbs[(size_t)tok * (K / 16) + 16 * b + sub] = (int16_t)sum;

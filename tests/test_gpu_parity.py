@@ -797,3 +797,52 @@ def test_linear_group_matches_single(hipdev, ora, qt, n_in, n_outs, m):
         sample = np.arange(min(n, 48))
         S = q8_scales(ora, qt, w[sample], x) + (0 if biases[z] is None else np.abs(biases[z][sample]))
         assert_tol(got[:, sample], want[:, sample], S, f"group matrix {z}")
+
+
+def _staging_edge_blocks(golden, rng):
+    """256-element activation blocks that steer the Q8_K quantizer through
+    every branch: the golden edge cases (zeros, ties of +-amax in either
+    order, halfway rounding, huge, tiny and subnormal maxima whose -127/max
+    overflows), plus +-amax held by different 16-element groups (the earlier
+    group decides), both signs inside the first group holding amax (its
+    first element decides), NaN and infinite elements."""
+    g = golden("quantize")
+    blocks = [np.asarray(x, np.float32) for x in g["x"]]
+
+    def base():
+        return rng.normal(0, 1, 256).astype(np.float32)
+
+    b = base(); b[3 * 16 + 5] = 9.0; b[1 * 16 + 7] = -9.0; blocks.append(b)     # -9 in an earlier group
+    b = base(); b[2 * 16 + 9] = -9.0; b[2 * 16 + 3] = 9.0; blocks.append(b)     # same group, + first
+    b = base(); b[2 * 16 + 3] = -9.0; b[2 * 16 + 9] = 9.0; b[5 * 16] = 9.0; blocks.append(b)  # same group, - first
+    b = base(); b[0] = 9.0; b[15] = -9.0; b[16] = -9.0; blocks.append(b)         # group 0 both, + first
+    b = base(); b[40] = np.nan; b[41] = 5.0; blocks.append(b)                    # NaN never enters amax
+    b = base(); b[77] = np.inf; blocks.append(b)                                 # amax = inf: iscale = -0
+    b = base(); b[100] = -np.inf; b[7] = np.inf; blocks.append(b)                # first infinity decides
+    b = np.zeros(256, np.float32); b[200] = 1e-39; b[201] = -1e-39; blocks.append(b)  # subnormal tie
+    return blocks
+
+
+@pytest.mark.parametrize("qt,n_in", [(12, 4096), (12, 14336), (14, 9728), (14, 2560)])
+def test_fused_staging_quantizer_edge_cases(hipdev, ora, golden, qt, n_in):
+    """The GEMV's in-kernel Q8_K quantizer (one token: the activation is
+    quantized in LDS inside the launch) on every branch of the reference's
+    quantize_row_q8_K: equal bit for bit to quantizing with the standalone
+    kernel (itself bit-exact against the reference's golden vectors) and
+    running the GEMV over those bytes; the standalone codes equal the
+    oracle's.  Shapes: 8-wave, 16-wave (rows split over 4 waves) and 12-wave
+    (3 waves per row) workgroups."""
+    rng = np.random.default_rng(n_in + qt)
+    blocks = _staging_edge_blocks(golden, rng)
+    nb = n_in // 256
+    x = np.concatenate([blocks[i % len(blocks)] for i in range(nb)]).astype(np.float32)[None, :]
+    n_out = 300
+    w = synth.np_weights(qt, n_out, n_in, rng)
+    wd = dev(w)
+    xq = E.quantize_q8_k(dev(x))
+    assert np.array_equal(xq.cpu().numpy(), ora.quantize_q8_k(x[0]))
+    sep = E.gemv_q8(wd, qt, xq, 1, n_out, n_in).cpu().numpy()
+    fused = E.linear_quant_batch(wd, qt, dev(x), n_out, n_in).cpu().numpy()
+    fin = np.isfinite(sep)
+    assert np.array_equal(fin, np.isfinite(fused))
+    assert np.array_equal(bits(fused[fin]), bits(sep[fin]))
