@@ -253,7 +253,25 @@ def main():
                 others[wl]["cpu_baseline"] = cpu_baseline(args, model, 1)
                 del model
             torch.cuda.empty_cache()
+            if wl == "hybrid-4b-q4km-decode":
+                # its configuration spans batch 1-4: the step at 2 and 4 tokens
+                others[wl]["batches"] = {}
+                for mb in (2, 4):
+                    rb = decode_leg(L, E, synth, gen, dev, wl, mb, args.steps, args.warmup, args.kernel_reps,
+                                    per_kernel=False)
+                    others[wl]["batches"][str(mb)] = {k: rb[k] for k in ("ms_per_step", "value", "unit",
+                                                                         "hbm_frac_step")}
+                    torch.cuda.empty_cache()
         extra["workloads"] = others
+        # the decode step with the layer ops on device and every dependency
+        # respected (rmsnorm -> q/k/v, o + residual, rmsnorm -> gate/up ->
+        # silu * up, down + residual, logits), one token, each workload
+        extra["layer_step"] = {}
+        for wl in WORKLOADS:
+            r = layer_step(L, E, synth, gen, dev, WORKLOADS[wl], wl, 1, args.steps, args.warmup, full=False)
+            extra["layer_step"][wl] = {"ms_per_step": r["ms_per_step"]["fused"],
+                                       "weight_GBps": r["weight_GBps"]["fused"], "launches_per_layer": 4}
+            torch.cuda.empty_cache()
 
     cfg = WORKLOADS[args.workload]
     line = {
@@ -574,7 +592,7 @@ def launch_sweep(L, E, synth, gen, dev):
                     "rows_fitted": list(big)}}
 
 
-def layer_step(L, E, synth, gen, dev, cfg, workload, m, steps, warmup):
+def layer_step(L, E, synth, gen, dev, cfg, workload, m, steps, warmup, full=True):
     """The decode step's matrix path with the ops between the projections on
     device (src/native.c:2529-2580; attention itself is not on this path, so
     o reads q):  rmsnorm -> q/k/v, o + residual, rmsnorm -> gate/up,
@@ -659,7 +677,7 @@ def layer_step(L, E, synth, gen, dev, cfg, workload, m, steps, warmup):
             logits(sp)
 
     res = {}
-    for name, fn in (("fused", fused), ("separate", separate)):
+    for name, fn in (("fused", fused), ("separate", separate)) if full else (("fused", fused),):
         g = capture(fn)
         for _ in range(max(1, warmup)):
             g.replay()
@@ -679,7 +697,7 @@ def layer_step(L, E, synth, gen, dev, cfg, workload, m, steps, warmup):
                                                              resid=hidden),
     }
     per = {}
-    for kname, kfn in kinds.items():
+    for kname, kfn in kinds.items() if full else ():
         def body(sp, kfn=kfn):
             for _ in range(4):
                 for lw, (an, fn) in zip(layers0, norms):
