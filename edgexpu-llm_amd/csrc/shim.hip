@@ -61,9 +61,6 @@ hipError_t launch_g32_pack(const float *x, const uint8_t *xq, size_t xq_stride, 
 hipError_t launch_gemm_g32(int type, const uint8_t *rw, int n_out, int K, int m, const uint8_t *pack, float *part,
                            unsigned *cnt, const float *bias, float *out, int ldo, hipStream_t st);
 bool gemv_fused_supported(int type, int K, int m);
-bool gemv_mfma_supported(int type, int K, int m);
-hipError_t launch_gemv_mfma(int type, int nmat, const uint8_t *const *w, const int *n_out, const float *const *bias,
-                            float *const *out, size_t row_bytes, int K, int m, const float *x, hipStream_t st);
 bool gemv_fused_f32_supported(int type, int K);
 bool gemv_fused_pro_supported(int type, int K, int pro);
 hipError_t launch_gemv_fused_layer(int type, int nmat, const uint8_t *const *w, const int *n_out,
@@ -216,14 +213,6 @@ bool stage_in_kernel(uint32_t type, int K, int m) {
     static const int generic = tuning_knob("EXQ_GENERIC", 0);
     if (mode == 0 || generic != 0 || !gemv_fused_supported((int)type, K, m)) return false;
     return mode == 2 || K <= kStageMaxK || (k_family((int)type) && m == 1 && K <= kStageMaxKWide);
-}
-
-// Decode products (1..4 tokens) of Q4_K rows on the int8 matrix cores
-// (gemv_mfma.hip) instead of the lane-per-unit GEMV: off by default (a
-// sweep build turns it on; measured slower so far, see gemv_mfma.hip).
-bool mfma_gemv(uint32_t type, int K, int m) {
-    static const int mode = tuning_knob("EXQ_MFMA_GEMV", 0);
-    return mode != 0 && gemv_mfma_supported((int)type, K, m);
 }
 
 bool split_gemv(uint32_t type, int K, int m) {
@@ -533,9 +522,6 @@ bool run_linear_group(uint32_t type, int nmat, const void *const *w, const int *
                 return false;
         return true;
     }
-    if (mfma_gemv(type, n_in, m))
-        return hip_ok(launch_gemv_mfma((int)type, nmat, (const uint8_t *const *)w, n_out, bias, out, rb, n_in, m, x, st),
-                      "gemv_mfma");
     if (stage_in_kernel(type, n_in, m)) {
         return hip_ok(launch_gemv_fused((int)type, nmat, (const uint8_t *const *)w, n_out, bias, out, rb, n_in, m, x,
                                         nullptr, 0, st),
