@@ -265,18 +265,33 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ s
     }
 }
 
-// Pass 2: one wavefront per row t reduces its nparts partials (at
-// partial + t*stride) to best[t].
-__global__ __launch_bounds__(64) void argmax_finish_kernel(const unsigned long long *__restrict__ partial,
-                                                           int nparts, int stride, uint32_t *__restrict__ best) {
+// Pass 2: one 256-thread workgroup per row t reduces its nparts partials
+// (at partial + t*stride, 1 <= nparts) to best[t].  Each thread issues its
+// first four loads together (clamped indices, so none is conditional): the
+// keys were just written by another kernel and every read misses in L2, so
+// one round trip rather than one per key bounds the pass.
+__global__ __launch_bounds__(256) void argmax_finish_kernel(const unsigned long long *__restrict__ partial,
+                                                            int nparts, int stride, uint32_t *__restrict__ best) {
     const unsigned long long *p = partial + (size_t)blockIdx.x * stride;
-    unsigned long long b = 0ull;
-    for (int i = threadIdx.x; i < nparts; i += 64) b = p[i] > b ? p[i] : b;
+    __shared__ unsigned long long red[4];
+    const int tid = threadIdx.x;
+    unsigned long long v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = p[min(tid + 256 * j, nparts - 1)];
+    unsigned long long b = v[0];
+#pragma unroll
+    for (int j = 1; j < 4; ++j) b = v[j] > b ? v[j] : b;
+    for (int i = tid + 1024; i < nparts; i += 256) b = p[i] > b ? p[i] : b;
     for (int off = 32; off > 0; off >>= 1) {
         const unsigned long long o = __shfl_xor(b, off, 64);
         b = o > b ? o : b;
     }
-    if (threadIdx.x == 0) best[blockIdx.x] = b != 0ull ? ~(uint32_t)(b & 0xffffffffull) : 0u;
+    if ((tid & 63) == 0) red[tid >> 6] = b;
+    __syncthreads();
+    if (tid == 0) {
+        for (int k = 1; k < 4; ++k) b = red[k] > b ? red[k] : b;
+        best[blockIdx.x] = b != 0ull ? ~(uint32_t)(b & 0xffffffffull) : 0u;
+    }
 }
 
 // Greedy argmax of m score rows (row t at s + t*lds, n entries) into best[t];
@@ -289,7 +304,7 @@ hipError_t launch_argmax_rows(const float *s, int m, int n, size_t lds, unsigned
         hipLaunchKernelGGL(argmax_kernel, dim3(grid), dim3(256), 0, st, s + (size_t)t * lds, n,
                            partial + (size_t)t * kArgmaxParts);
     }
-    hipLaunchKernelGGL(argmax_finish_kernel, dim3(m), dim3(64), 0, st, partial, grid, kArgmaxParts, best);
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(m), dim3(256), 0, st, partial, grid, kArgmaxParts, best);
     return hipGetLastError();
 }
 
@@ -297,6 +312,7 @@ hipError_t launch_argmax_rows(const float *s, int m, int n, size_t lds, unsigned
 // by the logits launch's argmax epilogue).
 hipError_t launch_argmax_finish(const unsigned long long *partial, int m, int nparts, int stride, uint32_t *best,
                                 hipStream_t st) {
-    hipLaunchKernelGGL(argmax_finish_kernel, dim3(m), dim3(64), 0, st, partial, nparts, stride, best);
+    if (nparts < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(m), dim3(256), 0, st, partial, nparts, stride, best);
     return hipGetLastError();
 }

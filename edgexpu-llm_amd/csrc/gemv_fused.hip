@@ -49,9 +49,9 @@ bool gemv_fused_f32_supported(int type, int K) {
 namespace {
 // The f32 logits launch with the argmax epilogue: the same shapes and
 // schedules as launch_gemv_fused_f32, one key per workgroup of the grid.
-template <class F, int R, int NW, int LOOP>
+template <class F, int R, int NW, int LOOP, bool STAGE = false>
 hipError_t launch_argmax_fmt(FusedArgs a, hipStream_t st, int *nparts) {
-    const hipError_t e = launch_fused_fmt<F, 1, R, NW, false, LOOP, 16>(a, st);
+    const hipError_t e = launch_fused_fmt<F, 1, R, NW, STAGE, LOOP, 16>(a, st);
     *nparts = fused_last_grid();
     return e;
 }
@@ -97,6 +97,40 @@ hipError_t launch_gemv_fused_f32_argmax(int type, const uint8_t *w, int n_out, c
             return balanced ? launch_argmax_fmt<FmtQ6KF32, 2, 8, 2>(a, st, nparts)
                             : launch_argmax_fmt<FmtQ6KF32, 2, 8, 0>(a, st, nparts);
     }
+}
+
+// One token of f32 activations x, quantized to Q8_0 inside each workgroup,
+// against Q8_0 rows, with the argmax epilogue: the Q8_0 logits product
+// (src/native.c:2317-2319) and its greedy pick's per-workgroup keys in one
+// launch (at least kFusedArgmaxParts keys at amax, *nparts the count).
+hipError_t launch_gemv_fused_q8_0_argmax(const uint8_t *w, int n_out, const float *bias, float *out,
+                                         size_t row_bytes, int K, const float *x, hipStream_t st,
+                                         unsigned long long *amax, int *nparts) {
+    if (!gemv_fused_supported(kTypeQ8_0, K, 1)) return hipErrorInvalidValue;
+    FusedArgs a{};
+    a.amax_cap = kFusedArgmaxParts;
+    a.nmat = 1;
+    a.w[0] = w;
+    a.n_out[0] = n_out;
+    a.bias[0] = bias;
+    a.out[0] = out;
+    a.row_bytes = row_bytes;
+    a.K = K;
+    a.m = 1;
+    a.x = x;
+    a.amax = amax;
+    a.nblk = K / kQK8_0;
+    a.U = a.nblk;
+    if (!pick_fused_shape(a.U, a.G, a.KS) || 8 % a.KS != 0) return hipErrorInvalidValue;
+    // more than two workgroups' worth of tiles per CU: the balanced per-wave
+    // schedule (logits [49152 x 576]: 11.5 us, against 13.8 us for the two
+    // register buffers of the scores-only launch with this epilogue)
+    const int r1 = a.KS == 1 && n_out <= 4096 ? 2 : 4;
+    const int rows_per_tile = (64 / a.G) * r1;
+    const int tiles = (n_out + rows_per_tile - 1) / rows_per_tile;
+    if (a.KS == 1 && tiles > 2 * device_cus() * 8) return launch_argmax_fmt<FmtQ80, 2, 8, 2, true>(a, st, nparts);
+    return r1 == 2 ? launch_argmax_fmt<FmtQ80, 2, 8, 0, true>(a, st, nparts)
+                   : launch_argmax_fmt<FmtQ80, 4, 8, 0, true>(a, st, nparts);
 }
 
 // With amax non-null (at least kFusedArgmaxParts keys) the launch also

@@ -62,12 +62,13 @@ struct FusedArgs {
 // score bits above ~index, so the largest key is the largest score at the
 // lowest index; NaN and -inf give 0 and never win.
 __device__ __forceinline__ unsigned long long score_key(float s, unsigned idx) {
-    if (!(s > -INFINITY)) return 0ull;
+    // selects only (no branch in the store path of the GEMV's epilogue);
     // -0.0 and +0.0 compare equal in the reference's `score > best`, so they
     // share one key (the lower index then wins)
-    uint32_t u = s == 0.0f ? 0u : __float_as_uint(s);
-    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((unsigned long long)u << 32) | (unsigned long long)(~idx);
+    const uint32_t b = s == 0.0f ? 0u : __float_as_uint(s);
+    const uint32_t u = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    const bool wins = s > -INFINITY;
+    return ((unsigned long long)(wins ? u : 0u) << 32) | (unsigned long long)(wins ? ~idx : 0u);
 }
 
 struct WSrc {
@@ -433,11 +434,14 @@ void gemv_fused_kernel(FusedArgs a) {
     }
     const int o_r = o_idx / M, o_t = o_idx - (o_idx / M) * M;
     constexpr bool kArgmax = (PRO & 16) != 0;
-    static_assert(!kArgmax || (M == 1 && (LOOP == 0 || LOOP == 2)), "the argmax epilogue: one token, grid-stride schedules");
-    // argmax epilogue: each lane's running best key lives in LDS, not in
-    // registers (the logits kernels have none to spare)
-    __shared__ unsigned long long lbest[kArgmax ? NW * 64 : 1];
-    if constexpr (kArgmax) lbest[threadIdx.x] = 0ull;
+    static_assert(!kArgmax || (M == 1 && (LOOP == 0 || LOOP == 2)), "the argmax epilogue: one token, one register buffer");
+    // argmax epilogue: each lane's running best key lives in LDS for the
+    // f32-activation formats (the logits kernels have no registers to
+    // spare), in two registers otherwise
+    constexpr bool kKeyLds = sizeof(typename Fmt::Act) >= 128;
+    __shared__ unsigned long long lbest[kArgmax ? (kKeyLds ? NW * 64 : NW) : 1];
+    unsigned long long best_reg = 0ull;
+    if constexpr (kArgmax && kKeyLds) lbest[threadIdx.x] = 0ull;
 
     // Loads of one tile: weights (unconditional: clamped tile, row and unit,
     // so every path issues the same loads), the bias and the residual of
@@ -579,8 +583,12 @@ void gemv_fused_kernel(FusedArgs a) {
                                               live ? (o_t * ct.n_out + row) * 4 : kDeadOffset, 0, 0);
         if constexpr (kArgmax) {
             const unsigned long long k = live ? score_key(o, (unsigned)row) : 0ull;
-            const unsigned long long b = lbest[threadIdx.x];
-            lbest[threadIdx.x] = k > b ? k : b;
+            if constexpr (kKeyLds) {
+                const unsigned long long b = lbest[threadIdx.x];
+                lbest[threadIdx.x] = k > b ? k : b;
+            } else {
+                best_reg = k > best_reg ? k : best_reg;
+            }
         }
     };
 
@@ -683,7 +691,7 @@ void gemv_fused_kernel(FusedArgs a) {
     if constexpr (kArgmax) {
         // the workgroup's best key: each wave over its 64 lanes, then the
         // first wave over the NW wave results; one key per workgroup
-        unsigned long long best_key = lbest[threadIdx.x];
+        unsigned long long best_key = kKeyLds ? lbest[threadIdx.x] : best_reg;
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) {
             const unsigned long long o = __shfl_xor(best_key, off, 64);

@@ -70,6 +70,9 @@ hipError_t launch_gemv_fused_layer(int type, int nmat, const uint8_t *const *w, 
 hipError_t launch_gemv_fused_f32(int type, const uint8_t *w, int n_out, const float *bias, float *out,
                                  size_t row_bytes, int K, const float *xf, const float *xs, hipStream_t st,
                                  unsigned long long *amax = nullptr, int *nparts = nullptr);
+hipError_t launch_gemv_fused_q8_0_argmax(const uint8_t *w, int n_out, const float *bias, float *out,
+                                         size_t row_bytes, int K, const float *x, hipStream_t st,
+                                         unsigned long long *amax, int *nparts);
 hipError_t launch_sample_softmax(float *x, int n, float top_p, double u, uint32_t *out, void *ws, hipStream_t st);
 size_t sample_workspace_bytes(int n);
 hipError_t launch_div_scalar(float *io, long long n, float d, hipStream_t st);
@@ -943,12 +946,32 @@ bool logits_run(float *scores, uint32_t *best_dev, const float *hidden, const vo
     // the chunking, so one launch covers all chunks in row order.
     if (q8_0_family((int)type)) {
         // src/native.c:2317-2319: the Q8_0 family scores rows against the
-        // Q8_0-quantized hidden vector
-        if (!hip_ok(launch_quantize_q8_0(hidden, m, n_embd, n_embd, a.xq, st), "quantize_q8_0")) return false;
-        if (!hip_ok(launch_gemv_q8((int)type, (const uint8_t *)w, rb, vocab, n_embd, m, a.xq,
-                                   act_bytes(type, n_embd), bias, scores, vocab, st),
-                    "logits gemv"))
-            return false;
+        // Q8_0-quantized hidden vector.  One fused launch per hidden vector
+        // quantizes it inside each workgroup (the same quantizer; a row's
+        // score then does not depend on m, as in the reference's per-token
+        // loop); Q8_0 rows also keep the argmax epilogue's keys, reduced by
+        // one small launch.
+        if (stage_in_kernel(type, n_embd, 1)) {
+            const uint8_t *wp = (const uint8_t *)w;
+            const bool keys = best_dev != nullptr && type == (uint32_t)kTypeQ8_0;
+            int nparts = 0;
+            for (int t = 0; t < m; ++t) {
+                float *out = scores + (size_t)t * vocab;
+                const float *ht = hidden + (size_t)t * n_embd;
+                const hipError_t e =
+                    keys ? launch_gemv_fused_q8_0_argmax(wp, vocab, bias, out, rb, n_embd, ht, st,
+                                                         a.keys + (size_t)t * kArgmaxParts, &nparts)
+                         : launch_gemv_fused((int)type, 1, &wp, &vocab, &bias, &out, rb, n_embd, 1, ht, nullptr, 0, st);
+                if (!hip_ok(e, "logits gemv")) return false;
+            }
+            if (keys) return hip_ok(launch_argmax_finish(a.keys, m, nparts, kArgmaxParts, best_dev, st), "argmax");
+        } else {
+            if (!hip_ok(launch_quantize_q8_0(hidden, m, n_embd, n_embd, a.xq, st), "quantize_q8_0")) return false;
+            if (!hip_ok(launch_gemv_q8((int)type, (const uint8_t *)w, rb, vocab, n_embd, m, a.xq,
+                                       act_bytes(type, n_embd), bias, scores, vocab, st),
+                        "logits gemv"))
+                return false;
+        }
     } else {
         // the other formats use the f32-activation dots (src/native.c:445-462);
         // K-quant rows one hidden vector per fused launch (a row's score then

@@ -671,9 +671,10 @@ def test_logits_multi_token(hipdev, ora, qt, n, vocab, m):
     assert np.array_equal(best.cpu().numpy(), np.argmax(got, axis=1))
 
 
-@pytest.mark.parametrize("qt,n,vocab", [(12, 4096, 20000), (14, 2560, 15001), (12, 2560, 3001)])
+@pytest.mark.parametrize("qt,n,vocab", [(12, 4096, 20000), (14, 2560, 15001), (12, 2560, 3001), (8, 576, 49152),
+                                        (8, 2048, 7001)])
 def test_logits_fused_argmax(hipdev, qt, n, vocab):
-    """K-quant logits with the argmax in the GEMV's store: the scores equal the
+    """K-quant and Q8_0 logits with the argmax in the GEMV's store: the scores equal the
     scores-only launch bit for bit, the index is the lowest one of the largest
     score (two rows made equal and largest), and a NaN score never wins."""
     rng = np.random.default_rng(qt * 31 + vocab)
