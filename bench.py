@@ -851,10 +851,14 @@ def sample_leg(L, gen, dev, no_cpu=False, vocab=128256, reps=50):
     """Softmax of a [vocab] f32 score vector in place and one draw
     (edgexpu_hip_sample_softmax_dev), eager launches on one stream (the
     generator's uniform is a kernel argument, so a draw is not replayed from
-    a graph); top_p 1.0 (index-order draw) and 0.9 (bitonic sort of the
-    vocabulary).  Later calls run on the previous call's probabilities: the
-    same launches and bytes.  Beside it, unless no_cpu, the reference's
-    edgexpu_cpu_sample_softmax on one host core over the same scores."""
+    a graph); top_p 1.0 (index-order draw) and 0.9 (radix selection of the
+    kept prefix's end and of the drawn item).  Each call starts from fresh
+    scores (seeded normal x 3.0, copied in before the call; the copy's own
+    time, measured alone, is subtracted).  The top-p draw's work depends on
+    the distribution, so it is also timed on a flat one: calls that run on
+    the previous call's probabilities ("top_p_0.9_flat").  Beside it, unless
+    no_cpu, the reference's edgexpu_cpu_sample_softmax on one host core over
+    the same scores."""
     import torch
 
     base = torch.randn(vocab, generator=gen, device=dev) * 3.0
@@ -863,16 +867,30 @@ def sample_leg(L, gen, dev, no_cpu=False, vocab=128256, reps=50):
     st = C.c_uint64(1)
     sp = torch.cuda.current_stream().cuda_stream
     res = {}
-    for top_p in (1.0, 0.9):
+
+    def copy_in():
         x.copy_(base)
+
+    copy_in()
+    copy_us = timed(copy_in, reps) * 1e3
+    for top_p in (1.0, 0.9):
 
         def run(top_p=top_p):
             if not L.sample_dev(x.data_ptr(), vocab, top_p, C.byref(st), out.data_ptr(), sp):
                 L.check(0, "sample_softmax")
 
-        run()
-        us = timed(run, reps) * 1e3
+        def fresh(run=run):
+            copy_in()
+            run()
+
+        fresh()
+        us = timed(fresh, reps) * 1e3 - copy_us
         res[f"top_p_{top_p}"] = {"us": round(us, 2)}
+        if top_p < 1.0:
+            copy_in()
+            run()
+            res[f"top_p_{top_p}_flat"] = {"us": round(timed(run, reps) * 1e3, 2)}
+    res["copy_us"] = round(copy_us, 2)
     if not no_cpu:
         import oracle as O
 

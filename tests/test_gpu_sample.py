@@ -96,6 +96,33 @@ def test_sample_degenerate_scores(hipdev, ora, n, top_p):
     assert tok == n // 2 and p[n // 2] == 1.0 and np.count_nonzero(p) == 1
 
 
+@pytest.mark.parametrize("n", [128256, 151936])
+@pytest.mark.parametrize("top_p", [0.9, 0.5, 0.05])
+@pytest.mark.parametrize("kind", ["equal", "few_values", "near_uniform", "one_tail"])
+def test_sample_top_p_ties_and_flat(hipdev, ora, n, top_p, kind):
+    """Top-p over large vocabularies whose probabilities tie or crowd: all
+    equal (the draw is the j-th index among n equal items), a few distinct
+    values (tie groups of tens of thousands), nearly equal (the softmax of
+    probabilities: every item in one first digit), and one large value over
+    equal small ones.  The token equals the definition's draw over the
+    device probabilities, over a run of generator states."""
+    rng = np.random.default_rng(n + int(top_p * 100) + len(kind))
+    if kind == "equal":
+        logits = np.zeros(n, np.float32)
+    elif kind == "few_values":
+        logits = rng.integers(0, 3, n).astype(np.float32)
+    elif kind == "near_uniform":
+        logits = ora.softmax((rng.standard_normal(n) * 3.0).astype(np.float32))
+    else:
+        logits = np.zeros(n, np.float32)
+        logits[n // 3] = 12.0
+    seed = 11
+    for _ in range(6):
+        tok, p, s = dev_sample(logits, top_p, seed)
+        assert tok == npref.draw(p, top_p, s), (kind, n, top_p, seed)
+        seed = s
+
+
 @pytest.mark.parametrize("n", [1, 3, 4096, 151936])
 def test_softmax_vs_oracle(hipdev, ora, n):
     rng = np.random.default_rng(n)
