@@ -946,25 +946,29 @@ bool logits_run(float *scores, uint32_t *best_dev, const float *hidden, const vo
     // the chunking, so one launch covers all chunks in row order.
     if (q8_0_family((int)type)) {
         // src/native.c:2317-2319: the Q8_0 family scores rows against the
-        // Q8_0-quantized hidden vector.  One fused launch per hidden vector
-        // quantizes it inside each workgroup (the same quantizer; a row's
-        // score then does not depend on m, as in the reference's per-token
-        // loop); Q8_0 rows also keep the argmax epilogue's keys, reduced by
-        // one small launch.
-        if (stage_in_kernel(type, n_embd, 1)) {
+        // Q8_0-quantized hidden vector.  Fused launches of up to 4 hidden
+        // vectors quantize them inside each workgroup (the same quantizer; a
+        // row's score does not depend on how many vectors share the launch,
+        // as in the reference's per-token loop); one vector of Q8_0 rows
+        // also keeps the argmax epilogue's keys, reduced by one small launch.
+        if (stage_in_kernel(type, n_embd, m < kFusedMaxTokens ? m : kFusedMaxTokens)) {
             const uint8_t *wp = (const uint8_t *)w;
-            const bool keys = best_dev != nullptr && type == (uint32_t)kTypeQ8_0;
-            int nparts = 0;
-            for (int t = 0; t < m; ++t) {
-                float *out = scores + (size_t)t * vocab;
-                const float *ht = hidden + (size_t)t * n_embd;
-                const hipError_t e =
-                    keys ? launch_gemv_fused_q8_0_argmax(wp, vocab, bias, out, rb, n_embd, ht, st,
-                                                         a.keys + (size_t)t * kArgmaxParts, &nparts)
-                         : launch_gemv_fused((int)type, 1, &wp, &vocab, &bias, &out, rb, n_embd, 1, ht, nullptr, 0, st);
-                if (!hip_ok(e, "logits gemv")) return false;
+            if (m == 1 && best_dev != nullptr && type == (uint32_t)kTypeQ8_0) {
+                int nparts = 0;
+                if (!hip_ok(launch_gemv_fused_q8_0_argmax(wp, vocab, bias, scores, rb, n_embd, hidden, st, a.keys,
+                                                          &nparts),
+                            "logits gemv + argmax"))
+                    return false;
+                return hip_ok(launch_argmax_finish(a.keys, 1, nparts, kArgmaxParts, best_dev, st), "argmax");
             }
-            if (keys) return hip_ok(launch_argmax_finish(a.keys, m, nparts, kArgmaxParts, best_dev, st), "argmax");
+            for (int t = 0; t < m; t += kFusedMaxTokens) {
+                const int mt = m - t < kFusedMaxTokens ? m - t : kFusedMaxTokens;
+                float *out = scores + (size_t)t * vocab;
+                if (!hip_ok(launch_gemv_fused((int)type, 1, &wp, &vocab, &bias, &out, rb, n_embd, mt,
+                                              hidden + (size_t)t * n_embd, nullptr, 0, st),
+                            "logits gemv"))
+                    return false;
+            }
         } else {
             if (!hip_ok(launch_quantize_q8_0(hidden, m, n_embd, n_embd, a.xq, st), "quantize_q8_0")) return false;
             if (!hip_ok(launch_gemv_q8((int)type, (const uint8_t *)w, rb, vocab, n_embd, m, a.xq,
