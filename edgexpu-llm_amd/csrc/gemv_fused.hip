@@ -183,6 +183,42 @@ hipError_t launch_gemv_fused_f32(int type, const uint8_t *w, int n_out, const fl
 #undef EXQ_F32_LAUNCH
 }
 
+// Two tokens of f32 activations (xf, xs at token strides K and K / 16)
+// against one K-quant matrix, outputs at out and out + n_out: the weights are
+// read once for both.  Each score equals the one-token launch's bit for bit
+// (the same lane partials, summed by the same reduction tree whichever value
+// slot holds them).
+hipError_t launch_gemv_fused_f32_pair(int type, const uint8_t *w, int n_out, const float *bias, float *out,
+                                      size_t row_bytes, int K, const float *xf, const float *xs, hipStream_t st) {
+    if ((type != kTypeQ4_K && type != kTypeQ6_K) || !gemv_fused_f32_supported(type, K)) return hipErrorInvalidValue;
+    FusedArgs a{};
+    a.nmat = 1;
+    a.w[0] = w;
+    a.n_out[0] = n_out;
+    a.bias[0] = bias;
+    a.out[0] = out;
+    a.row_bytes = row_bytes;
+    a.K = K;
+    a.m = 2;
+    a.xf = xf;
+    a.xs = xs;
+    a.nblk = K / kQKK;
+    a.U = a.nblk * 4;
+    if (!pick_fused_shape(a.U, a.G, a.KS)) return hipErrorInvalidValue;
+    static const int f32_ks3 = tuning_knob("EXQ_FUSED_F32_KS3", 1);
+    if (f32_ks3 != 0 && a.U > 32 && a.U <= 48) {
+        // the one-token launch's split (16-lane slots over three waves), in
+        // 6-wave workgroups: two row groups, at most two waves per SIMD, so
+        // both tokens' activation slices fit the registers
+        a.G = 16;
+        a.KS = 3;
+        return type == kTypeQ4_K ? launch_fused_fmt<FmtQ4KF32, 2, 1, 6, false, 0>(a, st)
+                                 : launch_fused_fmt<FmtQ6KF32, 2, 1, 6, false, 0>(a, st);
+    }
+    return type == kTypeQ4_K ? launch_fused_fmt<FmtQ4KF32, 2, 1, 8, false, 0>(a, st)
+                             : launch_fused_fmt<FmtQ6KF32, 2, 1, 8, false, 0>(a, st);
+}
+
 // nmat matrices of the same type and K, all applied to the same m tokens:
 // f32 x quantized inside the kernel (x != null), or codes already quantized
 // in the reference block layout (xq, token stride xq_stride).

@@ -352,8 +352,8 @@ struct FusedLds {
 template <class Fmt>
 constexpr int fused_occupancy(int r, int m, int loop) {
     // f32-activation formats: the activation slice (32 to 68 floats) stays
-    // in registers
-    if (sizeof(typename Fmt::Act) >= 128) return r <= 1 ? 4 : 3;
+    // in registers, one per token
+    if (sizeof(typename Fmt::Act) >= 128) return m > 1 ? 2 : (r <= 1 ? 4 : 3);
     // two register buffers at 2-4 tokens: one 8-wave workgroup per CU, two
     // waves per SIMD
     if (loop == 1 && m > 1) return 2;

@@ -70,6 +70,8 @@ hipError_t launch_gemv_fused_layer(int type, int nmat, const uint8_t *const *w, 
 hipError_t launch_gemv_fused_f32(int type, const uint8_t *w, int n_out, const float *bias, float *out,
                                  size_t row_bytes, int K, const float *xf, const float *xs, hipStream_t st,
                                  unsigned long long *amax = nullptr, int *nparts = nullptr);
+hipError_t launch_gemv_fused_f32_pair(int type, const uint8_t *w, int n_out, const float *bias, float *out,
+                                      size_t row_bytes, int K, const float *xf, const float *xs, hipStream_t st);
 hipError_t launch_gemv_fused_q8_0_argmax(const uint8_t *w, int n_out, const float *bias, float *out,
                                          size_t row_bytes, int K, const float *x, hipStream_t st,
                                          unsigned long long *amax, int *nparts);
@@ -459,11 +461,19 @@ bool run_f32_product(uint32_t type, const void *w, int n_out, int n_in, int m, c
         return true;
     }
     if (k_family((int)type) && ldo == n_out && gemv_fused_f32_supported((int)type, n_in)) {
-        for (int t = 0; t < m; ++t) {
-            if (!hip_ok(launch_gemv_fused_f32((int)type, (const uint8_t *)w, n_out, bias, out + (size_t)t * ldo, rb,
-                                              n_in, x + (size_t)t * n_in, xs + (size_t)t * (n_in / 16), st),
-                        "gemv_f32 fused"))
-                return false;
+        // tokens in pairs where the format has the two-token launch (the
+        // weights read once per pair), else one at a time
+        const bool pairs = type == (uint32_t)kTypeQ4_K || type == (uint32_t)kTypeQ6_K;
+        for (int t = 0; t < m;) {
+            const int mt = pairs && m - t >= 2 ? 2 : 1;
+            const float *xt = x + (size_t)t * n_in, *st_ = xs + (size_t)t * (n_in / 16);
+            const hipError_t e =
+                mt == 2 ? launch_gemv_fused_f32_pair((int)type, (const uint8_t *)w, n_out, bias, out + (size_t)t * ldo,
+                                                     rb, n_in, xt, st_, st)
+                        : launch_gemv_fused_f32((int)type, (const uint8_t *)w, n_out, bias, out + (size_t)t * ldo, rb,
+                                                n_in, xt, st_, st);
+            if (!hip_ok(e, "gemv_f32 fused")) return false;
+            t += mt;
         }
         return true;
     }
@@ -978,12 +988,14 @@ bool logits_run(float *scores, uint32_t *best_dev, const float *hidden, const vo
         }
     } else {
         // the other formats use the f32-activation dots (src/native.c:445-462);
-        // K-quant rows one hidden vector per fused launch (a row's score then
-        // does not depend on m, as in the reference's per-token loop), whose
-        // store also keeps each wave's greedy-argmax key: one small launch
-        // then reduces those keys instead of re-reading the scores
+        // K-quant rows: one hidden vector in a fused launch whose store also
+        // keeps each wave's greedy-argmax key (one small launch then reduces
+        // those keys instead of re-reading the scores); several in fused
+        // launches of two (the weights read once per pair), then the argmax
+        // over the scores.  A row's score does not depend on m, as in the
+        // reference's per-token loop.
         if (k_family((int)type) && !hip_ok(launch_xsum16(hidden, m, n_embd, a.xs, st), "xsum16")) return false;
-        if (best_dev != nullptr && k_family((int)type) && gemv_fused_f32_supported((int)type, n_embd)) {
+        if (m == 1 && best_dev != nullptr && k_family((int)type) && gemv_fused_f32_supported((int)type, n_embd)) {
             int nparts = 0;
             for (int t = 0; t < m; ++t) {
                 const hipError_t e = launch_gemv_fused_f32(
