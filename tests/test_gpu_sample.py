@@ -123,6 +123,23 @@ def test_sample_top_p_ties_and_flat(hipdev, ora, n, top_p, kind):
         seed = s
 
 
+@pytest.mark.parametrize("n", [1000003, 4194305])
+@pytest.mark.parametrize("kind", ["normal", "near_uniform"])
+def test_sample_top_p_large_vocabulary(hipdev, ora, n, kind):
+    """Top-p over vocabularies far beyond the LDS-resident case, of odd size
+    (gathered keys read from memory, the tied indices gathered into LDS,
+    indices of 20+ bits): the token equals the definition's draw."""
+    rng = np.random.default_rng(n + len(kind))
+    logits = (rng.standard_normal(n) * 3.0).astype(np.float32)
+    if kind == "near_uniform":
+        logits = ora.softmax(logits)
+    seed = 5
+    for top_p in (0.9, 0.3):
+        tok, p, s = dev_sample(logits, top_p, seed)
+        assert tok == npref.draw(p, top_p, s), (kind, n, top_p)
+        seed = s
+
+
 @pytest.mark.parametrize("n", [1, 3, 4096, 151936])
 def test_softmax_vs_oracle(hipdev, ora, n):
     rng = np.random.default_rng(n)
