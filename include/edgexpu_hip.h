@@ -195,7 +195,8 @@ int edgexpu_hip_embed_rows_dev(float *out, const void *table, uint32_t type, lon
  * agree with the reference within a few float ulp (device expf; sums in
  * double in a fixed segment order); the token differs only where the pick
  * falls within that distance of a running sum.  logits 16-byte aligned,
- * 1 <= n <= 2^24. */
+ * 1 <= n <= 2^24.  The library's sampling workspace (8 bytes per entry plus
+ * ~230 KiB) is allocated on the first call of a larger n and reused. */
 int edgexpu_hip_sample_softmax_dev(float *logits, int n, float top_p, uint64_t *rng, uint32_t *out, void *stream);
 /* io[i] = io[i] / d on device, float division: the temperature scaling of
  * the scores before sampling (src/native.c:2339). */
