@@ -160,6 +160,12 @@ __device__ __forceinline__ float row16_max(float v) {
     v = row8_max(v);
     return fmaxf(v, __uint_as_float(dpp_u32<kDppMirror>(__float_as_uint(v))));
 }
+__device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
+    v = max(v, dpp_u32<kDppXor1>(v));
+    v = max(v, dpp_u32<kDppXor2>(v));
+    v = max(v, dpp_u32<kDppHalfMirror>(v));
+    return max(v, dpp_u32<kDppMirror>(v));
+}
 __device__ __forceinline__ uint32_t row16_min(uint32_t v) {
     v = min(v, dpp_u32<kDppXor1>(v));
     v = min(v, dpp_u32<kDppXor2>(v));

@@ -23,33 +23,40 @@ struct Q8KLane {
 
 __device__ __forceinline__ Q8KLane q8k_quantize_lane(const float4 v, int lane) {
     const float xs[4] = {v.x, v.y, v.z, v.w};
-    // First-index signed maximum of |x|: one 64-bit max over keys
-    // (|x| bits << 32) | (~index << 1) | sign -- equal magnitudes -> lowest
-    // index wins; zeros and NaN never enter.
-    unsigned long long key = 0ull;
+    // First-index signed maximum of |x| (zeros and NaN never enter): the
+    // largest magnitude over the wave as bits (non-negative floats order as
+    // their bits), then the first lane holding it (ballot) and its first
+    // element there; the sign is that element's.
+    uint32_t b[4], amax_bits = 0u;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const float av = fabsf(xs[e]);
-        const uint32_t idx = (uint32_t)(lane * 4 + e);
-        unsigned long long k = ((unsigned long long)__float_as_uint(av) << 32) | (((~idx) & 0x7fffffffu) << 1) |
-                               (xs[e] < 0.0f ? 1u : 0u);
-        k = av > 0.0f ? k : 0ull;
-        key = k > key ? k : key;
+        b[e] = av > 0.0f ? __float_as_uint(av) : 0u;
+        amax_bits = max(amax_bits, b[e]);
     }
+    amax_bits = row16_max_u32(amax_bits);
+    amax_bits = max(amax_bits, (uint32_t)__shfl_xor((int)amax_bits, 16, 64));
+    amax_bits = max(amax_bits, (uint32_t)__shfl_xor((int)amax_bits, 32, 64));
+    bool hit = false, neg = false;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const unsigned long long o = __shfl_xor(key, off, 64);
-        key = o > key ? o : key;
+    for (int e = 3; e >= 0; --e) {  // the first element of this lane wins
+        const bool h = amax_bits != 0u && b[e] == amax_bits;
+        neg = h ? xs[e] < 0.0f : neg;
+        hit = hit || h;
     }
+    const unsigned long long hits = __ballot(hit);
+    const int first = hits != 0ull ? __ffsll((long long)hits) - 1 : 0;
+    const bool negative = __shfl((int)neg, first, 64) != 0;
+    (void)lane;
     Q8KLane r;
-    r.zero = key == 0ull;
+    r.zero = amax_bits == 0u;
     r.word = 0u;
     r.sum4 = 0;
     r.d = 0.0f;
     r.q[0] = r.q[1] = r.q[2] = r.q[3] = 0;
     if (r.zero) return r;  // wavefront-uniform
-    const float amax = __uint_as_float((uint32_t)(key >> 32));
-    const float maxv = (key & 1ull) ? -amax : amax;
+    const float amax = __uint_as_float(amax_bits);
+    const float maxv = negative ? -amax : amax;
     const float iscale = -127.0f / maxv;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
