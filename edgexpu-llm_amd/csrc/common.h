@@ -151,6 +151,7 @@ constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
 constexpr int kDppMirror = 0x140;      // row_mirror
+constexpr int kDppRor8 = 0x128;        // row_ror:8 (lane l of a 16-lane row gets lane l ^ 8)
 __device__ __forceinline__ float row8_max(float v) {
     v = fmaxf(v, __uint_as_float(dpp_u32<kDppXor1>(__float_as_uint(v))));
     v = fmaxf(v, __uint_as_float(dpp_u32<kDppXor2>(__float_as_uint(v))));
@@ -202,6 +203,22 @@ __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
     return __shfl_xor(v, mask, 64);
 }
 
+// The partner value l ^ off of a level of group_reduce's plain butterfly:
+// ^ 32 by bpermute, ^ 16 and ^ 4 by swizzle, inside 16-lane rows ^ 8 as the
+// DPP rotation by 8 and ^ 2, ^ 1 as quad permutes.  Every level pairs l with
+// l ^ off, as the transposing levels do, so a value's tree does not depend
+// on how many values a lane reduces (V).
+__device__ __forceinline__ float reduce_partner(float v, int off) {
+    switch (off) {
+        case 1: return __uint_as_float(dpp_u32<kDppXor1>(__float_as_uint(v)));
+        case 2: return __uint_as_float(dpp_u32<kDppXor2>(__float_as_uint(v)));
+        case 4: return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x101f));
+        case 8: return __uint_as_float(dpp_u32<kDppRor8>(__float_as_uint(v)));
+        case 16: return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f));
+        default: return shfl_xor_f(v, off);
+    }
+}
+
 // Sum of V per-lane values over aligned groups of G lanes (G a power of two
 // <= 64).  On return vals[0] in every lane holds the group total of value
 // index vidx(lane), where the indices are distributed over the group's lanes
@@ -229,7 +246,7 @@ __device__ __forceinline__ void group_reduce(float (&vals)[V], int G, int lane) 
     }
     // Plain butterfly for the remaining group bits.
     for (; off > 0; off >>= 1) {
-        vals[0] += shfl_xor_f(vals[0], off);
+        vals[0] += reduce_partner(vals[0], off);
     }
     (void)nv;
 }

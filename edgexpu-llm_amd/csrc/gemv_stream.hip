@@ -1,0 +1,600 @@
+// Streaming decode GEMV for one token of Q4_K rows: edgexpu_cpu_linear_quant_batch
+// (src/cpu_kernel.c:545-644) at m = 1 with the Q4_K x Q8_K block dot
+// (dot_q4_k_q8_k, src/gguf_dot_q8.c:603-666), for the row lengths of the
+// decode steps (K = 2560, 4096, 14336).
+//
+// Every weight row travels HBM -> LDS by DMA (buffer_load ... lds: no
+// registers held while it is in flight), one row per wave step, into a
+// per-wave ring of NB slots.  A slot is refilled as soon as its bytes are in
+// registers, so NB rows per wave stay in flight while the wave computes.
+// Lanes own fixed 64-element units of K (super-block i, quarter j): the
+// activation slice of a lane stays in registers for every row, the Q4_K
+// header's 6-bit scale/min pair is unpacked with lane-constant selectors
+// (v_perm), integer block sums with sdot4 / sdot2, one fp32 combine per unit.
+// A row's total is the fused kernel's butterfly over the lanes (so the two
+// kernels' outputs are equal bit for bit), four rows at a time;
+// step k's total is kept in lane k % 64 and every 64 steps one store per wave
+// writes them with their bias (prefetched at the start), so the only vector
+// memory operations inside the loop are the DMAs and every wait counts
+// exactly the rows still in flight.
+//
+// The activation is quantized to Q8_K inside each workgroup with the
+// arithmetic of quantize_q8_k_kernel (bit-identical to the reference's
+// quantize_row_q8_K, src/gguf_dot_q8.c:360-412), optionally after a staging
+// prologue (RMSNorm, SiLU-mul; src/native.c:2529, 2576-2578), or read from
+// Q8_K block bytes already in memory.  Epilogues: bias, residual
+// (src/native.c:2571-2580), gate/up pairs with silu(gate) * up.
+//
+// The waits on the ring are explicit s_waitcnt counts over the DMAs this
+// wave issued: vector memory loads of one wave complete in issue order, and
+// the loop issues no other vector memory operation.  The staged inputs are
+// read by inline-assembly loads issued before the ring's first rows, so the
+// compiler inserts no wait of its own for them (its count would include the
+// DMAs it cannot see); one explicit wait after the ring's first rows lets
+// only those rows stay in flight.
+#include "gemv_fused_kernel.h"
+
+namespace exq {
+
+namespace {
+
+typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
+
+constexpr int kStreamMaxMats = 4;
+// Rows of 14336 elements take the streaming kernel in the size-based mode
+// from this many weight bytes (2048 rows).
+constexpr long long kStreamMinBytes14336 = 2048ll * 56 * kBytesQ4_K;
+
+struct StreamArgs {
+    int nmat;                              // matrices (pairs: 1, gate = w[0], up = w[1])
+    const uint8_t *w[kStreamMaxMats];
+    const float *bias[kStreamMaxMats];
+    const float *resid[kStreamMaxMats];    // added after the bias (null: none)
+    float *out[kStreamMaxMats];
+    int n_out[kStreamMaxMats];
+    int row_start[kStreamMaxMats + 1];     // first step of each matrix
+    int nrows;                             // steps (rows, or gate/up pairs)
+    const float *x;                        // f32 activation [K] (staged), or
+    const uint8_t *xq;                     // its Q8_K block bytes
+    const float *x2;                       // SiLU-mul: act = silu(x) * x2
+    const float *nw;                       // RMSNorm: act = rmsnorm(x; nw, eps)
+    float eps;
+};
+
+// flags: bits 0-1 prologue (1 RMSNorm, 2 SiLU-mul), 4 residual, 8 gate/up
+// pairs, 16 activation already in Q8_K block bytes
+constexpr int kSRes = 4, kSPair = 8, kSXq = 16;
+
+__device__ __forceinline__ v4u_t s_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    return v4u_t{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, bytes, 0x00020000u};
+}
+
+// One LDS DMA: each lane's 16 bytes at base + soff + voff land at LDS byte
+// address lds + 16 * lane (M0 saved and restored around it).  voff is the
+// range-checked offset: past the buffer the lane reads zeros.
+__device__ __forceinline__ void s_dma16(uint32_t lds, uint32_t voff, const v4u_t &rs, uint32_t soff) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(lds), "v"(voff), "s"(rs), "s"(soff)
+        : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void s_wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+__device__ __forceinline__ uint32_t s_lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// 16 bytes at p (16-byte aligned global address) into registers, no wait.
+__device__ __forceinline__ v4u_t s_load16(const void *p) {
+    v4u_t r;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p) : "memory");
+    return r;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float s_dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+
+// Sum over the 64 lanes, every lane gets it, as group_reduce (common.h)
+// sums a 64-lane group: partners l ^ 32, ^ 16, ^ 8, ^ 4, ^ 2, ^ 1 in that
+// order (bpermute, swizzle, DPP rotation by 8, swizzle, quad DPP).  Each pair
+// adds the same two values, so every lane holds the same total, bit for bit
+// the fused kernel's total for the same lane partials.
+__device__ __forceinline__ float s_wave_total(float a) {
+    a += __shfl_xor(a, 32, 64);
+    a += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, a), 0x401f));  // ^ 16
+    a += s_dpp<0x128>(a);  // ^ 8 (row_ror:8)
+    a += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, a), 0x101f));  // ^ 4
+    a += s_dpp<0x4E>(a);   // ^ 2
+    a += s_dpp<0xB1>(a);   // ^ 1
+    return a;
+}
+
+// Four values per lane summed over the wave with the same tree, the first
+// two levels transposed (as group_reduce does for V = 4): level ^32 leaves
+// rows {0,1} on lanes 0-31 and {2,3} on 32-63, level ^16 one row per lane;
+// every row's pairs (and the order within each pair) are those of
+// s_wave_total, so each total is its s_wave_total bit for bit.  Row r ends on the lanes with bit 5 = r / 2 and
+// bit 4 = r % 2, e.g. lane 16 r.
+__device__ __forceinline__ float s_wave_total4(const float (&v)[4]) {
+    const int lane = threadIdx.x & 63;
+    const bool u32 = (lane & 32) != 0;
+    const float s0 = u32 ? v[0] : v[2], k0 = u32 ? v[2] : v[0];
+    const float s1 = u32 ? v[1] : v[3], k1 = u32 ? v[3] : v[1];
+    const float b0 = k0 + __shfl_xor(s0, 32, 64), b1 = k1 + __shfl_xor(s1, 32, 64);
+    const bool u16 = (lane & 16) != 0;
+    const float s = u16 ? b0 : b1, k = u16 ? b1 : b0;
+    float a = k + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, s), 0x401f));
+    a += s_dpp<0x128>(a);  // ^ 8
+    a += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, a), 0x101f));  // ^ 4
+    a += s_dpp<0x4E>(a);   // ^ 2
+    a += s_dpp<0xB1>(a);   // ^ 1
+    return a;
+}
+
+// Value of lane `src` (wave-uniform) in every lane.
+__device__ __forceinline__ float s_lane(float v, int src) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
+}
+
+// Per-lane selectors of the 6-bit scale/min pair of sub-blocks 2j, 2j+1
+// (get_scale_min_k4, src/gguf_dot_q8.c:112-124): header words y = scales
+// 0..3, z = 4..7, w = 8..11; for j < 2 sc = y[b..b+1] & 63, m = z[b..b+1] & 63;
+// for j >= 2 sc = (w[b..] & 15) | ((y[b..] >> 6) << 4),
+// m = (w[b..] >> 4) | ((z[b..] >> 6) << 4), b = 2 (j & 1).
+struct ScaleSel {
+    uint32_t sel, mT, sU;
+};
+__device__ __forceinline__ ScaleSel scale_sel(int j) {
+    const uint32_t b = 2u * (uint32_t)(j & 1);
+    return ScaleSel{b | ((b + 1u) << 8) | ((b + 4u) << 16) | ((b + 5u) << 24), j < 2 ? 0u : 0x0f0f0f0fu,
+                    j < 2 ? 0u : 2u};
+}
+
+// One unit's contribution, with the roundings of FmtQ4K::dot1: fma(dx*d, isum)
+// then fma(-dx*dmin, imin) (so a row's total is the fused kernel's bit for
+// bit).  |dlo|, |dhi| <= 32 * 15 * 128 < 2^23: the scale products are 24-bit.
+__device__ __forceinline__ float q4k_unit(v4u_t h, v4u_t q0, v4u_t q1, const FmtQ4K::Act &x, const ScaleSel &c) {
+    const uint32_t T = __builtin_amdgcn_perm(h.w >> 4, h.w, c.sel);
+    const uint32_t U = __builtin_amdgcn_perm(h.z, h.y, c.sel);
+    const uint32_t res = ((T & c.mT) | ((U >> c.sU) & ~c.mT)) & 0x3f3f3f3fu;  // sc0, sc1, m0, m1
+    const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    int dlo = 0, dhi = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        dlo = sdot4(qw[k] & 0x0f0f0f0fu, x.q[k], dlo);
+        dhi = sdot4((qw[k] >> 4) & 0x0f0f0f0fu, x.q[8 + k], dhi);
+    }
+    const int sc0 = (int)(res & 0xffu), sc1 = (int)((res >> 8) & 0xffu);
+    const int isum = ((dlo << 8) >> 8) * sc0 + ((dhi << 8) >> 8) * sc1;
+    const int imin = sdot2(__builtin_amdgcn_perm(0u, res, 0x0c030c02u), x.spair, 0);
+    const float dd = x.dx * f16_bits_to_f32(h.x), dm = x.dx * f16_bits_to_f32(h.x >> 16);
+    return fmaf(-dm, (float)imin, fmaf(dd, (float)isum, 0.0f));
+}
+
+// The activation slice of unit u from Q8_K block bytes (292 B per block) in LDS.
+__device__ __forceinline__ void act_from_blocks(const uint8_t *raw, int unit, FmtQ4K::Act &x) {
+    const int i = unit >> 2, j = unit & 3;
+    const uint8_t *blk = raw + (size_t)i * kBytesQ8_K;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) x.q[v] = *reinterpret_cast<const uint32_t *>(blk + 4 + 64 * j + 4 * v);
+    x.dx = *reinterpret_cast<const float *>(blk);
+    const uint32_t b0 = *reinterpret_cast<const uint32_t *>(blk + 260 + 8 * j);
+    const uint32_t b1 = *reinterpret_cast<const uint32_t *>(blk + 264 + 8 * j);
+    const int s0 = (int)(int16_t)(b0 & 0xffffu) + (int)(int16_t)(b0 >> 16);
+    const int s1 = (int)(int16_t)(b1 & 0xffffu) + (int)(int16_t)(b1 >> 16);
+    x.spair = ((uint32_t)s0 & 0xffffu) | ((uint32_t)s1 << 16);
+}
+
+template <int KSB, int NW, int NB, int FL>
+struct StreamGeom {
+    static constexpr int K = KSB * kQKK;
+    static constexpr int U = 4 * KSB;                    // units per row
+    static constexpr int T = (U + 63) / 64;              // units per lane
+    static constexpr int RB = KSB * kBytesQ4_K;          // row bytes
+    static constexpr int RPS = (FL & kSPair) ? 2 : 1;    // rows per step
+    static constexpr int SB = RPS * RB;                  // slot bytes
+    static constexpr int CH = RB / 1024;                 // whole 1 KB chunks per row
+    static constexpr int PL = (RB % 1024) / 16;          // lanes of the partial chunk
+    static constexpr int NI = RPS * (CH + (PL > 0 ? 1 : 0));  // DMA instructions per step
+    static constexpr int NT = NW * 64;
+    static constexpr int ROUNDS = (FL & kSXq) ? 0 : (KSB * 16 + NT - 1) / NT;  // staging rounds
+    static constexpr int QB = (K + 15) & ~15, DB = (KSB * 4 + 15) & ~15, BB = ((K / 16) * 2 + 15) & ~15;
+    static constexpr int XQB = ((KSB * kBytesQ8_K + 1023) / 1024) * 1024;  // raw blocks, whole chunks
+    static constexpr int AREA = (FL & kSXq) ? XQB : QB + DB + BB;
+    static constexpr size_t lds() { return (size_t)AREA + (size_t)NW * NB * SB; }
+    static_assert(RB % 16 == 0, "16-byte DMA lanes");
+    static_assert(NB * NI + 8 * ((FL & 3) ? 2 : 1) <= 63, "vmcnt range");
+    static_assert(AREA % 16 == 0, "slot alignment");
+};
+
+template <int KSB, int NW, int NB, int FL>
+__global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
+    using G = StreamGeom<KSB, NW, NB, FL>;
+    constexpr int PRO = FL & 3;
+    constexpr bool kRes = (FL & kSRes) != 0, kPair = (FL & kSPair) != 0, kXq = (FL & kSXq) != 0;
+    constexpr int kWait = (NB - 1) * G::NI;  // DMAs of the later steps
+    extern __shared__ __align__(16) uint8_t smem[];
+    int8_t *lq = reinterpret_cast<int8_t *>(smem);
+    float *ld = reinterpret_cast<float *>(smem + G::QB);
+    int16_t *lbs = reinterpret_cast<int16_t *>(smem + G::QB + G::DB);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint8_t *ring = smem + G::AREA + wave * (NB * G::SB);
+    const uint32_t ring_lds = s_lds_addr(ring);
+    const int gw = blockIdx.x * NW + wave, TW = gridDim.x * NW;
+    const int last = a.nrows;
+
+    // the matrix of a step and its row (scalar selects over the arguments)
+    struct Mat {
+        const uint8_t *w;
+        int n_out, row;
+    };
+    auto locate = [&](int step) {
+        Mat m{a.w[0], a.n_out[0], step};
+#pragma unroll
+        for (int z = 1; z < kStreamMaxMats; ++z) {
+            const bool in = !kPair && z < a.nmat && step >= a.row_start[z];
+            m.w = in ? a.w[z] : m.w;
+            m.n_out = in ? a.n_out[z] : m.n_out;
+            m.row = in ? step - a.row_start[z] : m.row;
+        }
+        return m;
+    };
+    auto issue = [&](int b, int step) {
+        const bool ok = step < last;
+        const Mat m = locate(ok ? step : 0);
+        const uint32_t so = ok ? (uint32_t)m.row * G::RB : 0u;
+        const uint32_t vo = ok ? (uint32_t)lane * 16u : 0x7ff00000u;
+#pragma unroll
+        for (int r = 0; r < G::RPS; ++r) {
+            const v4u_t rs = s_rsrc(r == 0 ? m.w : a.w[1], (uint32_t)m.n_out * G::RB);
+            const uint32_t dst = ring_lds + b * G::SB + r * G::RB;
+#pragma unroll
+            for (int k = 0; k < G::CH; ++k) s_dma16(dst + k * 1024, vo, rs, so + k * 1024);
+            if constexpr (G::PL > 0) {
+                if (lane < G::PL) s_dma16(dst + G::CH * 1024, vo, rs, so + G::CH * 1024);
+            }
+        }
+    };
+
+    // 1. the inputs of the activation, then the ring's first rows
+    const int tid = threadIdx.x, sub = tid & 15, bl = tid >> 4;
+    constexpr int BPR = G::NT / 16;
+    constexpr int RN = G::ROUNDS > 0 ? G::ROUNDS : 1;
+    v4u_t xr[RN][4], yr[RN][4];
+    if constexpr (kXq) {
+        // Q8_K block bytes into LDS, 1 KB chunks over the waves
+        const v4u_t rsx = s_rsrc(a.xq, (uint32_t)(KSB * kBytesQ8_K));
+        constexpr int XCH = G::XQB / 1024;
+        for (int c = wave; c < XCH; c += NW) s_dma16(s_lds_addr(smem) + c * 1024, lane * 16u, rsx, c * 1024u);
+    } else {
+#pragma unroll
+        for (int r = 0; r < G::ROUNDS; ++r) {
+            const int blk = min(r * BPR + bl, KSB - 1);
+            const float *px = a.x + blk * kQKK + 16 * sub;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) xr[r][k] = s_load16(px + 4 * k);
+            if constexpr (PRO != 0) {
+                const float *py = PRO == 2 ? a.x2 + blk * kQKK + 16 * sub : a.nw + blk * kQKK + 16 * sub;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) yr[r][k] = s_load16(py + 4 * k);
+            }
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) issue(b, gw + b * TW);
+    s_wait_vm<NB * G::NI>();  // the activation inputs have arrived; the ring's rows may not have
+    if constexpr (kXq) {
+        __syncthreads();
+    } else {
+        // the loaded registers are complete only now: every use is ordered after the wait
+#pragma unroll
+        for (int r = 0; r < G::ROUNDS; ++r)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                asm volatile("" : "+v"(xr[r][k]));
+                if constexpr (PRO != 0) asm volatile("" : "+v"(yr[r][k]));
+            }
+        // 2. Q8_K staging (quantize_q8_k_group: the reference's quantizer), after the prologue
+        float xs[RN][16], ys[RN][16];
+#pragma unroll
+        for (int r = 0; r < G::ROUNDS; ++r)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                // whole-vector casts: a bit_cast of one ext-vector element reads element 0 in this clang
+                const float4 f = __builtin_bit_cast(float4, xr[r][k]);
+                xs[r][4 * k] = f.x; xs[r][4 * k + 1] = f.y; xs[r][4 * k + 2] = f.z; xs[r][4 * k + 3] = f.w;
+                const float4 g = __builtin_bit_cast(float4, yr[r][k]);
+                ys[r][4 * k] = g.x; ys[r][4 * k + 1] = g.y; ys[r][4 * k + 2] = g.z; ys[r][4 * k + 3] = g.w;
+            }
+        if constexpr (PRO == 2) {
+#pragma unroll
+            for (int r = 0; r < G::ROUNDS; ++r)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) xs[r][e] = silu_f32(xs[r][e]) * ys[r][e];
+        } else if constexpr (PRO == 1) {
+            // RMSNorm (src/cpu_kernel.c:228-241): squares summed in double over the row (the
+            // lanes of clamped past-the-end blocks add nothing), scale from the mean
+            __shared__ double red[NW];
+            double s = 0.0;
+#pragma unroll
+            for (int r = 0; r < G::ROUNDS; ++r) {
+                double sr = 0.0;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const double v = (double)xs[r][e];
+                    sr += v * v;
+                }
+                s += r * BPR + bl < KSB ? sr : 0.0;
+            }
+            s = wave_sum_f64(s);
+            if (lane == 0) red[wave] = s;
+            __syncthreads();
+            double ss = 0.0;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) ss += red[w];
+            const float scale = rms_scale(ss, G::K, a.eps);
+#pragma unroll
+            for (int r = 0; r < G::ROUNDS; ++r)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const float v = xs[r][e] * scale;
+                    xs[r][e] = v * ys[r][e];
+                }
+        }
+#pragma unroll
+        for (int r = 0; r < G::ROUNDS; ++r) quantize_q8_k_group<G::NT>(xs[r], r * BPR + bl, KSB, KSB, G::K, sub, lq, ld, lbs);
+        __syncthreads();
+    }
+    // the lane's activation slices, scale selectors and row offsets
+    const ActLds act{lq, ld, lbs, G::K, KSB};
+    FmtQ4K::Act xa[G::T];
+    ScaleSel lc[G::T];
+    uint32_t hoff[G::T], qoff[G::T];
+    bool live[G::T];
+#pragma unroll
+    for (int t = 0; t < G::T; ++t) {
+        const int u = lane + 64 * t;
+        live[t] = u < G::U;
+        const int uc = min(u, G::U - 1);
+        if constexpr (kXq) act_from_blocks(smem, uc, xa[t]);
+        else FmtQ4K::load_act_lds(act, uc, 0, xa[t]);
+        lc[t] = scale_sel(uc & 3);
+        hoff[t] = (uint32_t)(uc >> 2) * kBytesQ4_K;
+        qoff[t] = hoff[t] + 16u + 32u * (uint32_t)(uc & 3);
+    }
+
+    // 3. the epilogue words of the lane's step (step first + lane * TW), loaded ahead of use
+    struct Epi {
+        float b0, b1, r;
+    };
+    auto lane_out = [&](int step, float *&out, int &row, const float *&bias, const float *&resid) {
+        out = a.out[0];
+        bias = a.bias[0];
+        resid = a.resid[0];
+        row = step;
+#pragma unroll
+        for (int z = 1; z < kStreamMaxMats; ++z) {
+            const bool in = !kPair && z < a.nmat && step >= a.row_start[z];
+            out = in ? a.out[z] : out;
+            bias = in ? a.bias[z] : bias;
+            resid = in ? a.resid[z] : resid;
+            row = in ? step - a.row_start[z] : row;
+        }
+    };
+    auto load_epi = [&](int first) {
+        const int step = first + lane * TW;
+        const bool ok = step < last;
+        float *out;
+        int row;
+        const float *bias, *resid;
+        lane_out(ok ? step : 0, out, row, bias, resid);
+        Epi e{0.0f, 0.0f, 0.0f};
+        if (ok) {
+            e.b0 = bias != nullptr ? bias[row] : 0.0f;
+            if constexpr (kPair) e.b1 = a.bias[1] != nullptr ? a.bias[1][row] : 0.0f;
+            if constexpr (kRes) e.r = resid != nullptr ? resid[row] : 0.0f;
+        }
+        return e;
+    };
+    float keep0 = 0.0f, keep1 = 0.0f;
+    auto flush = [&](int first, int n, const Epi &e) {
+        const int step = first + lane * TW;
+        float *out;
+        int row;
+        const float *bias, *resid;
+        lane_out(step < last ? step : 0, out, row, bias, resid);
+        if (lane < n && step < last) {
+            // out = resid + (bias + dot) (src/native.c:2571-2580); pairs: silu(gate) * up
+            const float v = e.b0 + keep0;
+            float o = v;
+            if constexpr (kRes) o = resid != nullptr ? e.r + v : v;
+            if constexpr (kPair) o = silu_f32(v) * (e.b1 + keep1);
+            out[row] = o;
+        }
+    };
+    Epi epi = load_epi(gw);
+
+    // 4. one step (a row, or a gate/up pair) per ring slot.  The slot's rows
+    //    into registers, the slot refilled with the step NB ahead, the lane
+    //    partials of each row: per unit pass t, dead units 0.
+    auto step_partials = [&](int b, int step, float (&p)[G::RPS][G::T]) {
+        s_wait_vm<kWait>();
+        const uint8_t *sb = ring + b * G::SB;
+        v4u_t h[G::RPS][G::T], q0[G::RPS][G::T], q1[G::RPS][G::T];
+#pragma unroll
+        for (int r = 0; r < G::RPS; ++r)
+#pragma unroll
+            for (int t = 0; t < G::T; ++t) {
+                h[r][t] = *reinterpret_cast<const v4u_t *>(sb + r * G::RB + hoff[t]);
+                q0[r][t] = *reinterpret_cast<const v4u_t *>(sb + r * G::RB + qoff[t]);
+                q1[r][t] = *reinterpret_cast<const v4u_t *>(sb + r * G::RB + qoff[t] + 16);
+            }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        issue(b, step + NB * TW);
+#pragma unroll
+        for (int r = 0; r < G::RPS; ++r)
+#pragma unroll
+            for (int t = 0; t < G::T; ++t) {
+                const float v = q4k_unit(h[r][t], q0[r][t], q1[r][t], xa[t], lc[t]);
+                p[r][t] = live[t] ? v : 0.0f;
+            }
+    };
+    int k64 = 0, first = gw;
+    auto advance = [&](int n) {
+        k64 += n;
+        if (k64 == 64) {  // uniform
+            s_wait_vm<0>();
+            flush(first, 64, epi);
+            first += 64 * TW;
+            k64 = 0;
+            epi = load_epi(first);
+        }
+    };
+    {
+        for (int t0 = gw; t0 < last; t0 += NB * TW) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                float p[G::RPS][G::T];
+                step_partials(b, t0 + b * TW, p);
+                // a row's total: per unit pass the wave's sum (the fused kernel's waves of a
+                // split row), the passes added in order from 0
+                float acc[G::RPS];
+#pragma unroll
+                for (int r = 0; r < G::RPS; ++r) {
+                    if constexpr (G::T == 1) {
+                        acc[r] = s_wave_total(p[r][0]);
+                    } else if constexpr (G::T == 4) {
+                        const float tot = s_wave_total4(p[r]);
+                        float sum = 0.0f;
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) sum += s_lane(tot, 16 * t);
+                        acc[r] = sum;
+                    } else {
+                        float sum = 0.0f;
+#pragma unroll
+                        for (int t = 0; t < G::T; ++t) sum += s_wave_total(p[r][t]);
+                        acc[r] = sum;
+                    }
+                }
+                keep0 = lane == k64 ? acc[0] : keep0;
+                if constexpr (kPair) keep1 = lane == k64 ? acc[G::RPS - 1] : keep1;
+                advance(1);
+            }
+        }
+    }
+    s_wait_vm<0>();
+    if (k64 > 0) flush(first, k64, epi);
+}
+
+template <int KSB, int NW, int NB, int FL>
+hipError_t launch_stream(const StreamArgs &a, hipStream_t st) {
+    using G = StreamGeom<KSB, NW, NB, FL>;
+    // one workgroup per CU: the grid covers the chip once and every wave strides over the rows
+    const int grid = device_cus();
+    hipLaunchKernelGGL((gemv_stream_q4k<KSB, NW, NB, FL>), dim3(grid), dim3(NW * 64), G::lds(), st, a);
+    return hipGetLastError();
+}
+
+template <int KSB, int NW, int NB>
+hipError_t launch_stream_flags(int fl, const StreamArgs &a, hipStream_t st) {
+    switch (fl) {
+        case 0: return launch_stream<KSB, NW, NB, 0>(a, st);
+        case 1: return launch_stream<KSB, NW, NB, 1>(a, st);
+        case 2: return launch_stream<KSB, NW, NB, 2>(a, st);
+        case kSRes: return launch_stream<KSB, NW, NB, kSRes>(a, st);
+        case 2 | kSRes: return launch_stream<KSB, NW, NB, 2 | kSRes>(a, st);
+        case kSPair: return launch_stream<KSB, NW, NB, kSPair>(a, st);
+        case 1 | kSPair: return launch_stream<KSB, NW, NB, 1 | kSPair>(a, st);
+        case kSXq: return launch_stream<KSB, NW, NB, kSXq>(a, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+// Kernel choice for the one-token Q4_K launches this kernel covers (the
+// library's edgexpu_hip_set_gemv_mode): 0 by launch size, 1 the fused kernel,
+// 2 this one.  Both give the same outputs bit for bit.
+static int g_gemv_mode = 0;
+void set_gemv_stream_mode(int mode) { g_gemv_mode = mode; }
+int gemv_stream_mode() { return g_gemv_mode; }
+
+// True when the streaming GEMV can take (type, K, m): one token of Q4_K rows
+// of 2560, 4096 or 14336 elements.
+bool gemv_stream_supported(int type, int K, int m) {
+    return type == kTypeQ4_K && m == 1 && (K == 2560 || K == 4096 || K == 14336);
+}
+
+// True when the streaming GEMV runs a launch of `rows` rows (pairs: gate and
+// up rows together) of (type, K, m).  By size, as measured on one MI355X
+// (launch sweep over distinct weights, both kernels in one run): K = 2560
+// and 4096 from 1024 rows on (e.g. [28672 x 4096] 14.5 against 16.0 us,
+// [4096 x 4096] 5.5 against 5.7), K = 14336 from 2048 rows (8 MB of rows
+// split four ways per wave: 7.7 against 7.0 us at 1024 rows, 11.0 against
+// 12.4 at 4096).
+bool gemv_stream_take(int type, int K, int m, long long rows) {
+    if (!gemv_stream_supported(type, K, m) || g_gemv_mode == 1) return false;
+    if (g_gemv_mode == 2) return true;
+    const long long bytes = rows * (long long)(K / kQKK) * kBytesQ4_K;
+    return K != 14336 || bytes >= kStreamMinBytes14336;
+}
+
+// nmat Q4_K matrices against one token: x f32 (quantized in the kernel, after
+// the prologue pro: 1 RMSNorm with nw / eps, 2 SiLU-mul with x2) or xq (Q8_K
+// block bytes); resid (per matrix, may be null) added after the bias; pair:
+// nmat = 2 (gate, up), out[0] = silu(gate) * up.
+hipError_t launch_gemv_stream(int nmat, const uint8_t *const *w, const int *n_out, const float *const *bias,
+                              const float *const *resid, float *const *out, int K, const float *x,
+                              const uint8_t *xq, const float *x2, const float *nw, float eps, int pro, bool pair,
+                              hipStream_t st) {
+    if (!gemv_stream_supported(kTypeQ4_K, K, 1) || nmat < 1 || nmat > kStreamMaxMats) return hipErrorInvalidValue;
+    if ((x == nullptr) == (xq == nullptr) || (xq != nullptr && (pro != 0 || pair))) return hipErrorInvalidValue;
+    if (pair && (nmat != 2 || n_out[0] != n_out[1])) return hipErrorInvalidValue;
+    StreamArgs a{};
+    a.nmat = pair ? 1 : nmat;
+    int rows = 0;
+    bool any_res = false;
+    for (int z = 0; z < nmat; ++z) {
+        a.w[z] = w[z];
+        a.bias[z] = bias != nullptr ? bias[z] : nullptr;
+        a.resid[z] = resid != nullptr ? resid[z] : nullptr;
+        a.out[z] = out[z];
+        a.n_out[z] = n_out[z];
+        any_res = any_res || a.resid[z] != nullptr;
+    }
+    for (int z = 0; z < a.nmat; ++z) {
+        a.row_start[z] = rows;
+        rows += n_out[z];
+    }
+    for (int z = a.nmat; z <= kStreamMaxMats; ++z) a.row_start[z] = rows;
+    a.nrows = rows;
+    a.x = x;
+    a.xq = xq;
+    a.x2 = x2;
+    a.nw = nw;
+    a.eps = eps;
+    if (any_res && pair) return hipErrorInvalidValue;
+    const int fl = xq != nullptr ? kSXq : ((pro & 3) | (any_res ? kSRes : 0) | (pair ? kSPair : 0));
+    // measured on the Llama-3-8B / hybrid decode shapes: 8 waves per CU, two
+    // slots per wave, one slot where a row is 8 KB (K = 14336)
+    switch (K) {
+        case 2560: return launch_stream_flags<10, 8, 2>(fl, a, st);
+        case 4096: return launch_stream_flags<16, 8, 2>(fl, a, st);
+        default: return launch_stream_flags<56, 8, 1>(fl, a, st);
+    }
+}
+
+}  // namespace exq

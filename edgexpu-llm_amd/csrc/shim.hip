@@ -84,6 +84,12 @@ hipError_t launch_gemv_fused(int type, int nmat, const uint8_t *const *w, const 
                              float *const *out, size_t row_bytes, int K, int m, const float *x, const uint8_t *xq,
                              size_t xq_stride, hipStream_t st);
 
+// gemv_stream.hip: the decode GEMV kernel choice for one-token Q4_K launches
+namespace exq {
+void set_gemv_stream_mode(int mode);
+int gemv_stream_mode();
+}  // namespace exq
+
 namespace {
 
 constexpr int kGemvMaxTokens = 8;
@@ -637,6 +643,17 @@ int edgexpu_hip_set_prefill_mode(int mode) {
 }
 
 int edgexpu_hip_prefill_mode(void) { return g.prefill_mode; }
+
+int edgexpu_hip_set_gemv_mode(int mode) {
+    if (mode != EDGEXPU_HIP_GEMV_AUTO && mode != EDGEXPU_HIP_GEMV_FUSED && mode != EDGEXPU_HIP_GEMV_STREAM) {
+        set_error(-2, "set_gemv_mode: unknown mode %d", mode);
+        return 0;
+    }
+    set_gemv_stream_mode(mode);
+    return 1;
+}
+
+int edgexpu_hip_gemv_mode(void) { return gemv_stream_mode(); }
 
 int edgexpu_hip_synchronize(void) {
     if (!ensure_init()) return 0;

@@ -65,6 +65,8 @@ class HipLib:
         self.supports_type = _sig(L, "edgexpu_hip_supports_type", C.c_int, [C.c_uint32])
         self.set_prefill_mode = _sig(L, "edgexpu_hip_set_prefill_mode", C.c_int, [C.c_int])
         self.prefill_mode = _sig(L, "edgexpu_hip_prefill_mode", C.c_int, [])
+        self.set_gemv_mode = _sig(L, "edgexpu_hip_set_gemv_mode", C.c_int, [C.c_int])
+        self.gemv_mode = _sig(L, "edgexpu_hip_gemv_mode", C.c_int, [])
         self.synchronize = _sig(L, "edgexpu_hip_synchronize", C.c_int, [])
         self.stream = _sig(L, "edgexpu_hip_stream", _vp, [])
         self.row_bytes = _sig(L, "edgexpu_hip_row_bytes", C.c_size_t, [C.c_uint32, C.c_int])

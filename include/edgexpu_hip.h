@@ -70,6 +70,21 @@ int edgexpu_hip_supports_type(uint32_t type);
 #define EDGEXPU_HIP_PREFILL_F16 1
 int edgexpu_hip_set_prefill_mode(int mode);
 int edgexpu_hip_prefill_mode(void);
+/* Decode GEMV kernel for one token of Q4_K rows of 2560, 4096 or 14336
+ * elements.  No reference counterpart (the reference has one CPU kernel).
+ *  EDGEXPU_HIP_GEMV_AUTO (default): the streaming kernel (weight rows
+ *    through LDS by DMA), except launches of fewer than 2048 rows of 14336
+ *    elements, which take the fused kernel;
+ *  EDGEXPU_HIP_GEMV_FUSED / EDGEXPU_HIP_GEMV_STREAM: always that kernel.
+ * The two give the same outputs bit for bit (same lane partials, same
+ * reduction order), so the setting moves time, never results.  Process-wide
+ * setting of this library.  Returns 1, or 0 (sticky error) for an unknown
+ * mode. */
+#define EDGEXPU_HIP_GEMV_AUTO 0
+#define EDGEXPU_HIP_GEMV_FUSED 1
+#define EDGEXPU_HIP_GEMV_STREAM 2
+int edgexpu_hip_set_gemv_mode(int mode);
+int edgexpu_hip_gemv_mode(void);
 /* Blocks until the library stream is idle. */
 int edgexpu_hip_synchronize(void);
 /* hipStream_t of the library stream. */

@@ -1,0 +1,150 @@
+"""The two decode GEMV kernels for one token of Q4_K rows agree bit for bit.
+
+One token of Q4_K rows of 2560, 4096 or 14336 elements runs on either the
+fused kernel (csrc/gemv_fused_kernel.h) or the streaming kernel
+(csrc/gemv_stream.hip: rows through LDS by DMA), chosen by launch size
+(edgexpu_hip_set_gemv_mode).  Both compute each lane's unit partial with the
+same roundings and sum the lanes with the same xor tree, so every output is
+the same word whichever kernel runs -- the plain projection, grouped
+launches, the RMSNorm and SiLU-mul staging prologues, the residual store,
+gate/up pairs with silu(gate) * up, and activations given as Q8_K block
+bytes.  Each variant is also held to the oracle (the reference's
+edgexpu_cpu_linear_quant_batch, src/cpu_kernel.c:545-644) within the usual
+1e-5 of the conditioning scale, so the agreement is between two correct
+results, not two copies of one mistake.
+"""
+import numpy as np
+import pytest
+import torch
+
+import edgexpu_amd as E
+import npref
+from edgexpu_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+AUTO, FUSED, STREAM = 0, 1, 2
+TOL = 1e-5
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+
+
+def both(L, fn):
+    """fn() under the fused kernel and under the streaming kernel."""
+    out = {}
+    try:
+        for mode in (FUSED, STREAM):
+            assert L.set_gemv_mode(mode) == 1
+            out[mode] = [t.cpu().numpy() for t in fn()]
+    finally:
+        L.set_gemv_mode(AUTO)
+    return out[FUSED], out[STREAM]
+
+
+def cond(ora, w, x):
+    """S_i of each output row: the sum over blocks of |block terms| (float64)."""
+    xq = ora.quantize_q8_k(x[0])
+    return np.array([npref.q8_dot_f64(12, w[i], xq)[1] for i in range(w.shape[0])])[None, :]
+
+
+SHAPES = [(4096, (14336, 14336)), (4096, (4096, 1024, 1024)), (4096, (4096,)), (4096, (33,)),
+          (14336, (4096,)), (14336, (2048,)), (14336, (300,)), (2560, (9728, 9728)), (2560, (4096, 1024, 1024)),
+          (2560, (7,))]
+
+
+@pytest.mark.parametrize("n_in,n_outs", SHAPES)
+def test_plain_group_fused_equals_stream(hipdev, ora, n_in, n_outs):
+    rng = np.random.default_rng(n_in + sum(n_outs))
+    ws = [synth.np_weights(12, n, n_in, rng) for n in n_outs]
+    x = synth.np_activations(1, n_in, rng)
+    biases = [rng.normal(0, 0.3, n).astype(np.float32) if z % 2 == 0 else None for z, n in enumerate(n_outs)]
+    wd = [dev(w) for w in ws]
+    bd = [None if b is None else dev(b) for b in biases]
+    f, s = both(hipdev, lambda: E.linear_quant_group(wd, 12, dev(x), list(n_outs), n_in, biases=bd))
+    for z, n in enumerate(n_outs):
+        assert np.array_equal(bits(f[z]), bits(s[z])), f"matrix {z}"
+        sample = np.arange(min(n, 64))
+        want = ora.linear_quant_batch(x, ws[z][sample], 12, None if biases[z] is None else biases[z][sample], 1,
+                                      len(sample), n_in)
+        S = cond(ora, ws[z][sample], x) + (0 if biases[z] is None else np.abs(biases[z][sample]))
+        assert np.all(np.abs(s[z][:, sample] - want) <= TOL * S), f"matrix {z}"
+
+
+@pytest.mark.parametrize("n_in,n_out", [(4096, 1000), (14336, 2100), (2560, 515)])
+def test_q8k_input_fused_equals_stream(hipdev, ora, n_in, n_out):
+    """Activations already in Q8_K block bytes (edgexpu_hip_gemv_q8_dev): the
+    streaming kernel reads the blocks instead of quantizing, same words."""
+    rng = np.random.default_rng(n_in * 3 + n_out)
+    w = synth.np_weights(12, n_out, n_in, rng)
+    x = synth.np_activations(1, n_in, rng)
+    xq = dev(ora.quantize_q8_k(x[0]))
+    wd = dev(w)
+    f, s = both(hipdev, lambda: [E.gemv_q8(wd, 12, xq, 1, n_out, n_in)])
+    assert np.array_equal(bits(f[0]), bits(s[0]))
+    # and equal to quantizing inside the launch
+    staged = E.linear_quant_batch(wd, 12, dev(x), n_out, n_in).cpu().numpy()
+    assert np.array_equal(bits(staged), bits(s[0]))
+
+
+@pytest.mark.parametrize("n_in,n_outs", [(4096, (4096, 1024, 1024)), (4096, (14336, 14336)), (14336, (4096,)),
+                                         (2560, (4096, 1024, 1024))])
+def test_rmsnorm_prologue_fused_equals_stream(hipdev, ora, n_in, n_outs):
+    rng = np.random.default_rng(n_in + 7 * len(n_outs))
+    ws = [dev(synth.np_weights(12, n, n_in, rng)) for n in n_outs]
+    x = (rng.normal(0, 1, (1, n_in)) * 3).astype(np.float32)
+    nw = dev(rng.normal(1, 0.2, n_in).astype(np.float32))
+    biases = [dev(rng.normal(0, 0.5, n).astype(np.float32)) for n in n_outs]
+    f, s = both(hipdev, lambda: E.layer_linear(ws, 12, dev(x), n_outs, n_in, norm_weight=nw, eps=1e-5, biases=biases))
+    for z in range(len(n_outs)):
+        assert np.array_equal(bits(f[z]), bits(s[z])), f"matrix {z}"
+
+
+@pytest.mark.parametrize("n_in,n_out", [(14336, 4096), (4096, 2560), (2560, 2560)])
+def test_silu_mul_residual_fused_equals_stream(hipdev, ora, n_in, n_out):
+    rng = np.random.default_rng(n_in + n_out)
+    w = dev(synth.np_weights(12, n_out, n_in, rng))
+    g = dev(rng.normal(0, 2, (1, n_in)).astype(np.float32))
+    u = dev(rng.normal(0, 2, (1, n_in)).astype(np.float32))
+    res = rng.normal(0, 4, (1, n_out)).astype(np.float32)
+    f, s = both(hipdev, lambda: E.layer_linear([w], 12, g, (n_out,), n_in, x2=u, residuals=[dev(res)]))
+    assert np.array_equal(bits(f[0]), bits(s[0]))
+
+
+def test_residual_only_fused_equals_stream(hipdev):
+    n_in, n_outs = 4096, (4096, 1024)
+    rng = np.random.default_rng(11)
+    ws = [dev(synth.np_weights(12, n, n_in, rng)) for n in n_outs]
+    x = dev(synth.np_activations(1, n_in, rng))
+    res = dev(rng.normal(0, 4, (1, n_outs[0])).astype(np.float32))
+    bias = [dev(rng.normal(0, 0.5, n).astype(np.float32)) for n in n_outs]
+    f, s = both(hipdev, lambda: E.layer_linear(ws, 12, x, n_outs, n_in, biases=bias, residuals=[res, None]))
+    for z in range(2):
+        assert np.array_equal(bits(f[z]), bits(s[z]))
+
+
+@pytest.mark.parametrize("n_in,n_ff", [(4096, 14336), (2560, 9728), (14336, 4096), (4096, 300)])
+@pytest.mark.parametrize("norm", [True, False])
+def test_gate_up_pairs_fused_equals_stream(hipdev, ora, n_in, n_ff, norm):
+    rng = np.random.default_rng(n_in + n_ff + norm)
+    wg, wu = dev(synth.np_weights(12, n_ff, n_in, rng)), dev(synth.np_weights(12, n_ff, n_in, rng))
+    x = dev((rng.normal(0, 1, (1, n_in)) * 2).astype(np.float32))
+    nw = dev(rng.normal(1, 0.2, n_in).astype(np.float32)) if norm else None
+    bg, bu = dev(rng.normal(0, 0.5, n_ff).astype(np.float32)), dev(rng.normal(0, 0.5, n_ff).astype(np.float32))
+    f, s = both(hipdev, lambda: [E.gate_up_silu(wg, wu, 12, x, n_ff, n_in, norm_weight=nw, b_gate=bg, b_up=bu)])
+    assert np.array_equal(bits(f[0]), bits(s[0]))
+
+
+def test_gemv_mode_switch(hipdev):
+    L = hipdev
+    assert L.gemv_mode() == AUTO
+    assert L.set_gemv_mode(3) == 0
+    code, msg = L.last_error()
+    assert code != 0 and "unknown mode" in msg
+    L.clear_error()
+    assert L.gemv_mode() == AUTO
