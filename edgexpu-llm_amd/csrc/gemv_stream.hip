@@ -32,6 +32,9 @@
 // compiler inserts no wait of its own for them (its count would include the
 // DMAs it cannot see); one explicit wait after the ring's first rows lets
 // only those rows stay in flight.
+#include <type_traits>
+#include <utility>
+
 #include "gemv_fused_kernel.h"
 
 namespace exq {
@@ -197,7 +200,7 @@ __device__ __forceinline__ void act_from_blocks(const uint8_t *raw, int unit, Fm
     x.spair = ((uint32_t)s0 & 0xffffu) | ((uint32_t)s1 << 16);
 }
 
-template <int KSB, int NW, int NB, int FL>
+template <int KSB, int NW, int NB, int FL, bool DEEP>
 struct StreamGeom {
     static constexpr int K = KSB * kQKK;
     static constexpr int U = 4 * KSB;                    // units per row
@@ -213,25 +216,28 @@ struct StreamGeom {
     static constexpr int QB = (K + 15) & ~15, DB = (KSB * 4 + 15) & ~15, BB = ((K / 16) * 2 + 15) & ~15;
     static constexpr int XQB = ((KSB * kBytesQ8_K + 1023) / 1024) * 1024;  // raw blocks, whole chunks
     static constexpr int AREA = (FL & kSXq) ? XQB : QB + DB + BB;
-    static constexpr size_t lds() { return (size_t)AREA + (size_t)NW * NB * SB; }
+    // ring slots: NB steps in flight, NS at the start (DEEP: twice NB)
+    static constexpr int NS = DEEP ? 2 * NB : NB;
+    static constexpr size_t lds() { return (size_t)AREA + (size_t)NW * NS * SB; }
     static_assert(RB % 16 == 0, "16-byte DMA lanes");
-    static_assert(NB * NI + 8 * ((FL & 3) ? 2 : 1) <= 63, "vmcnt range");
+    static_assert(AREA + (size_t)NW * NS * SB + 8 * NW <= 160 * 1024, "the ring and the staging fit the gfx950 LDS");
+    static_assert(NS * NI + 8 * ((FL & 3) ? 2 : 1) <= 63, "vmcnt range");
     static_assert(AREA % 16 == 0, "slot alignment");
 };
 
-template <int KSB, int NW, int NB, int FL>
+template <int KSB, int NW, int NB, int FL, bool DEEP>
 __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
-    using G = StreamGeom<KSB, NW, NB, FL>;
+    using G = StreamGeom<KSB, NW, NB, FL, DEEP>;
     constexpr int PRO = FL & 3;
     constexpr bool kRes = (FL & kSRes) != 0, kPair = (FL & kSPair) != 0, kXq = (FL & kSXq) != 0;
-    constexpr int kWait = (NB - 1) * G::NI;  // DMAs of the later steps
+    constexpr int NS = G::NS;
     extern __shared__ __align__(16) uint8_t smem[];
     int8_t *lq = reinterpret_cast<int8_t *>(smem);
     float *ld = reinterpret_cast<float *>(smem + G::QB);
     int16_t *lbs = reinterpret_cast<int16_t *>(smem + G::QB + G::DB);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    uint8_t *ring = smem + G::AREA + wave * (NB * G::SB);
+    uint8_t *ring = smem + G::AREA + wave * (NS * G::SB);
     const uint32_t ring_lds = s_lds_addr(ring);
     const int gw = blockIdx.x * NW + wave, TW = gridDim.x * NW;
     const int last = a.nrows;
@@ -293,9 +299,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
             }
         }
     }
+    // every slot filled at the start: NS rows per wave in flight while the
+    // activation is quantized, then NB once the steps begin
 #pragma unroll
-    for (int b = 0; b < NB; ++b) issue(b, gw + b * TW);
-    s_wait_vm<NB * G::NI>();  // the activation inputs have arrived; the ring's rows may not have
+    for (int b = 0; b < NS; ++b) issue(b, gw + b * TW);
+    s_wait_vm<NS * G::NI>();  // the activation inputs have arrived; the ring's rows may not have
     if constexpr (kXq) {
         __syncthreads();
     } else {
@@ -427,12 +435,15 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     };
     Epi epi = load_epi(gw);
 
-    // 4. one step (a row, or a gate/up pair) per ring slot.  The slot's rows
-    //    into registers, the slot refilled with the step NB ahead, the lane
-    //    partials of each row: per unit pass t, dead units 0.
-    auto step_partials = [&](int b, int step, float (&p)[G::RPS][G::T]) {
-        s_wait_vm<kWait>();
-        const uint8_t *sb = ring + b * G::SB;
+    // 4. one step (a row, or a gate/up pair) per ring slot.  Step k of the wave
+    //    (row gw + k TW) sits in slot k % NS; once its bytes are in registers
+    //    the slot of step k + NB - NS is free and takes step k + NB (before
+    //    that, steps up to NS - 1 came with the start), then the lane partials
+    //    of each row: per unit pass t, dead units 0.  WAIT: this wave's DMAs
+    //    of later steps that may stay in flight.
+    auto step_partials = [&](auto wait_c, int slot, int k, float (&p)[G::RPS][G::T]) {
+        s_wait_vm<decltype(wait_c)::value>();
+        const uint8_t *sb = ring + slot * G::SB;
         v4u_t h[G::RPS][G::T], q0[G::RPS][G::T], q1[G::RPS][G::T];
 #pragma unroll
         for (int r = 0; r < G::RPS; ++r)
@@ -443,7 +454,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
                 q1[r][t] = *reinterpret_cast<const v4u_t *>(sb + r * G::RB + qoff[t] + 16);
             }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        issue(b, step + NB * TW);
+        if (k + NB >= NS) issue((slot + NB) % NS, gw + (k + NB) * TW);  // uniform; slot == k % NS
 #pragma unroll
         for (int r = 0; r < G::RPS; ++r)
 #pragma unroll
@@ -453,9 +464,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
             }
     };
     int k64 = 0, first = gw;
-    auto advance = [&](int n) {
-        k64 += n;
-        if (k64 == 64) {  // uniform
+    auto advance = [&]() {
+        if (++k64 == 64) {  // uniform
             s_wait_vm<0>();
             flush(first, 64, epi);
             first += 64 * TW;
@@ -463,35 +473,52 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
             epi = load_epi(first);
         }
     };
-    {
-        for (int t0 = gw; t0 < last; t0 += NB * TW) {
+    // a row's total: per unit pass the wave's sum (the fused kernel's waves of
+    // a split row), the passes added in order from 0
+    auto finish = [&](float (&p)[G::RPS][G::T]) {
+        float acc[G::RPS];
 #pragma unroll
-            for (int b = 0; b < NB; ++b) {
+        for (int r = 0; r < G::RPS; ++r) {
+            if constexpr (G::T == 1) {
+                acc[r] = s_wave_total(p[r][0]);
+            } else if constexpr (G::T == 4) {
+                const float tot = s_wave_total4(p[r]);
+                float sum = 0.0f;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) sum += s_lane(tot, 16 * t);
+                acc[r] = sum;
+            } else {
+                float sum = 0.0f;
+#pragma unroll
+                for (int t = 0; t < G::T; ++t) sum += s_wave_total(p[r][t]);
+                acc[r] = sum;
+            }
+        }
+        keep0 = lane == k64 ? acc[0] : keep0;
+        if constexpr (kPair) keep1 = lane == k64 ? acc[G::RPS - 1] : keep1;
+        advance();
+    };
+    // the first NS steps: their rows came with the start, so fewer stay in flight after each
+    bool more = true;
+    [&]<int... K>(std::integer_sequence<int, K...>) {
+        ((more = more && gw + K * TW < last,
+          more ? (void)([&] {
+              float p[G::RPS][G::T];
+              step_partials(std::integral_constant<int, (K < NS - NB ? NS - 1 - K : NB - 1) * G::NI>{}, K, K, p);
+              finish(p);
+          }())
+               : (void)0),
+         ...);
+    }(std::make_integer_sequence<int, NS>{});
+    // then NB in flight: one step per slot in turn (slot indices known at compile time)
+    for (int k0 = NS; more; k0 += NS) {
+#pragma unroll
+        for (int b = 0; b < NS; ++b) {
+            more = more && gw + (k0 + b) * TW < last;
+            if (more) {  // uniform
                 float p[G::RPS][G::T];
-                step_partials(b, t0 + b * TW, p);
-                // a row's total: per unit pass the wave's sum (the fused kernel's waves of a
-                // split row), the passes added in order from 0
-                float acc[G::RPS];
-#pragma unroll
-                for (int r = 0; r < G::RPS; ++r) {
-                    if constexpr (G::T == 1) {
-                        acc[r] = s_wave_total(p[r][0]);
-                    } else if constexpr (G::T == 4) {
-                        const float tot = s_wave_total4(p[r]);
-                        float sum = 0.0f;
-#pragma unroll
-                        for (int t = 0; t < 4; ++t) sum += s_lane(tot, 16 * t);
-                        acc[r] = sum;
-                    } else {
-                        float sum = 0.0f;
-#pragma unroll
-                        for (int t = 0; t < G::T; ++t) sum += s_wave_total(p[r][t]);
-                        acc[r] = sum;
-                    }
-                }
-                keep0 = lane == k64 ? acc[0] : keep0;
-                if constexpr (kPair) keep1 = lane == k64 ? acc[G::RPS - 1] : keep1;
-                advance(1);
+                step_partials(std::integral_constant<int, (NB - 1) * G::NI>{}, b, k0 + b, p);
+                finish(p);
             }
         }
     }
@@ -501,10 +528,23 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
 
 template <int KSB, int NW, int NB, int FL>
 hipError_t launch_stream(const StreamArgs &a, hipStream_t st) {
-    using G = StreamGeom<KSB, NW, NB, FL>;
-    // one workgroup per CU: the grid covers the chip once and every wave strides over the rows
+    // one workgroup per CU: the grid covers the chip once and every wave
+    // strides over the rows.  Launches of at most three steps per wave fill
+    // twice the ring at the start (measured: [4096 x 4096] 5.3 against
+    // 5.5 us, [6144 x 2560] 5.5 against 6.1); longer ones keep NB in flight
+    // from the start ([28672 x 4096] 14.5 against 14.7 us), and 8 KB rows
+    // never take the deep start (12.4 against 11.0 us at [4096 x 14336]).
     const int grid = device_cus();
-    hipLaunchKernelGGL((gemv_stream_q4k<KSB, NW, NB, FL>), dim3(grid), dim3(NW * 64), G::lds(), st, a);
+    const long long steps = ((long long)a.nrows + (long long)grid * NW - 1) / ((long long)grid * NW);
+    if constexpr (KSB <= 16) {
+        if (steps <= 3) {
+            using G = StreamGeom<KSB, NW, NB, FL, true>;
+            hipLaunchKernelGGL((gemv_stream_q4k<KSB, NW, NB, FL, true>), dim3(grid), dim3(NW * 64), G::lds(), st, a);
+            return hipGetLastError();
+        }
+    }
+    using G = StreamGeom<KSB, NW, NB, FL, false>;
+    hipLaunchKernelGGL((gemv_stream_q4k<KSB, NW, NB, FL, false>), dim3(grid), dim3(NW * 64), G::lds(), st, a);
     return hipGetLastError();
 }
 
