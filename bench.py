@@ -448,7 +448,8 @@ def decode_leg(L, E, synth, gen, dev, workload, m, steps, warmup, kernel_reps, p
         traffic, tinfo = traffic_from_profile(workload)
         roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-                    "kernel": f"gemv_fused_kernel ({E.TYPE_NAMES[cfg['wtype']]}, gate+up grouped) "
+                    "kernel": f"{decode_kernel_name(cfg['wtype'], dom['shape'][1], m, dom['shape'][0])} "
+                              f"({E.TYPE_NAMES[cfg['wtype']]}, gate+up grouped) "
                               f"{dom['shape'][0]}x{dom['shape'][1]} m={m}",
                     "us_per_launch": dom["us"], "bytes_per_launch": dom["bytes"]}
         if tinfo is not None:
@@ -464,6 +465,16 @@ def decode_leg(L, E, synth, gen, dev, workload, m, steps, warmup, kernel_reps, p
                          "xin": xin, "step_bytes": step_bytes}
     del model, copy_args
     return out
+
+
+def decode_kernel_name(t, n_in, m, rows):
+    """The kernel the library picks for a decode launch in its default mode
+    (csrc/gemv_stream.hip gemv_stream_take): the streaming kernel for one
+    token of Q4_K rows of 2560 or 4096, and of 14336 from 2048 rows on; the
+    fused kernel otherwise."""
+    if t == 12 and m == 1 and (n_in in (2560, 4096) or (n_in == 14336 and rows >= 2048)):
+        return "gemv_stream_q4k"
+    return "gemv_fused_kernel"
 
 
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
@@ -1090,8 +1101,10 @@ def cpu_baseline(args, model, m):
     """The reference's CPU path on the same decode step:
     every layer's projections through edgexpu_cpu_linear_quant_batch of the
     reference built from its own sources (oracle/_ref), the logits through
-    the oracle's restatement of the chunked loop (src/native.c:2292-2401,
-    OpenMP rows, the reference's row dots), on this host's cores.  The
+    src/native.c's greedy chunked loop (2292-2401: Q8_0 hidden state for the
+    Q8_0 family, OpenMP rows, per-thread argmax) over the same build's row
+    dots (oracle/ref_logits.c), on this host's cores; where the reference was
+    never built, both through the oracle's restatements.  The
     weights are copied to host memory (the whole step: beyond the LLC), the
     step is timed over a bounded number of repetitions, twice:
       (a) OpenMP threads = the host's share of cores (OMP_NUM_THREADS, else
@@ -1127,7 +1140,7 @@ def cpu_baseline(args, model, m):
     for c_host, c_wout in rot:
         cl = [(lin._lin, (ys[name].ctypes.data_as(f32p), x[src].ctypes.data_as(f32p), lw[name].ctypes.data_as(u8p), t,
                           None, m, n_out, n_in)) for lw in c_host for name, t, n_out, n_in, src in projs]
-        cl += [(ora._logits, (scores.ctypes.data_as(f32p), x["h"][tok].ctypes.data_as(f32p),
+        cl += [(lin._logits, (scores.ctypes.data_as(f32p), x["h"][tok].ctypes.data_as(f32p),
                               c_wout.ctypes.data_as(u8p), cfg["logits_type"], None, cfg["vocab"], cfg["hidden"],
                               cfg["logits_chunk"])) for tok in range(m)]
         calls.append(cl)
@@ -1186,8 +1199,10 @@ def cpu_baseline(args, model, m):
            "sample": f"the whole {model['workload']} step m={m} ({len(host)} layers x "
                      f"{len(projs)} projections through "
                      f"{'the reference build' if kind == 'reference' else 'the oracle'}'s "
-                     f"edgexpu_cpu_linear_quant_batch + [{cfg['vocab']} x {cfg['hidden']}] logits through the "
-                     f"oracle's chunked loop), {reps} steps over {len(rot)} distinct host cop"
+                     f"edgexpu_cpu_linear_quant_batch + [{cfg['vocab']} x {cfg['hidden']}] logits through "
+                     f"src/native.c's chunked greedy loop on "
+                     f"{'that build' if kind == 'reference' else 'the oracle'}'s row dots), {reps} steps over "
+                     f"{len(rot)} distinct host cop"
                      f"{'y' if len(rot) == 1 else 'ies'} of {one >> 20} MiB",
            "omp": {"OMP_NUM_THREADS": share, "OMP_PROC_BIND": os.environ.get("OMP_PROC_BIND"),
                    "OMP_PLACES": os.environ.get("OMP_PLACES")},

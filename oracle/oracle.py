@@ -249,6 +249,9 @@ class Reference(_Lib, _Elementwise):
         self._df32 = L("edgexpu_gguf_dot_quant", C.c_float, [C.c_uint32, _u8p, _f32p, C.c_int])
         self._lin = L("edgexpu_cpu_linear_quant_batch", None,
                       [_f32p, _f32p, _u8p, C.c_uint32, _f32p, C.c_int, C.c_int, C.c_int])
+        # oracle/ref_logits.c: src/native.c's greedy logits loop over the row kernels above
+        self._logits = L("edgexpu_refdrv_logits", C.c_uint32,
+                         [_f32p, _f32p, _u8p, C.c_uint32, _f32p, C.c_int, C.c_int, C.c_size_t])
         self._self = L("edgexpu_gguf_quant_selftest", C.c_int, [C.c_char_p, C.c_size_t])
         _ew_setup(self, "edgexpu_cpu_rmsnorm", "edgexpu_cpu_silu", "edgexpu_cpu_mul", "edgexpu_cpu_add")
         _sample_setup(self, "edgexpu_cpu_softmax", "edgexpu_cpu_sample_softmax")
@@ -290,6 +293,15 @@ class Reference(_Lib, _Elementwise):
         out = np.zeros((m, n_out), dtype=np.float32)
         self._lin(_p(out, _f32p), _p(x, _f32p), _p(w, _u8p), qtype, _p(b, _f32p), m, n_out, n_in)
         return out
+
+    def logits(self, hidden, w, qtype, bias, vocab, n_embd, chunk_rows=0):
+        hidden = np.ascontiguousarray(hidden, dtype=np.float32)
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        scores = np.zeros(vocab, dtype=np.float32)
+        best = self._logits(_p(scores, _f32p), _p(hidden, _f32p), _p(w, _u8p), qtype, _p(b, _f32p),
+                            vocab, n_embd, chunk_rows)
+        return scores, int(best)
 
     def selftest(self):
         buf = C.create_string_buffer(256)

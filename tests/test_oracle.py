@@ -273,6 +273,26 @@ def test_logits_argmax_rules(ora):
     assert np.array_equal(bits(scores), bits(s3)) and b3 == best
 
 
+@pytest.mark.parametrize("qt", [8, 12, 14] + MORE)
+def test_logits_equal_reference_loop(ora, ref, qt):
+    """The oracle's logits product against src/native.c's greedy loop run on
+    the reference's own row kernels (oracle/ref_logits.c): every score word
+    and the argmax, with and without the output bias, in chunks of 256 rows
+    (parallel) and of 100 rows (below the loop's 256-row parallel threshold),
+    and with the 48 MiB default."""
+    rng = np.random.default_rng(40 + qt)
+    vocab, n = 1000, 512
+    w = synth.np_weights(qt, vocab, n, rng)
+    h = rng.normal(0, 1, n).astype(np.float32)
+    bias = rng.normal(0, 0.5, vocab).astype(np.float32)
+    for b in (None, bias):
+        for chunk in (0, 256, 100):
+            so, bo = ora.logits(h, w, qt, b, vocab, n, chunk)
+            sr, br = ref.logits(h, w, qt, b, vocab, n, chunk)
+            assert np.array_equal(bits(so), bits(sr)), (qt, chunk)
+            assert bo == br == int(np.argmax(sr))
+
+
 # ------------------------------------------------------------ mutations
 
 
