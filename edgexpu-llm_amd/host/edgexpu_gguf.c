@@ -8,7 +8,8 @@
  *   "GGUF" | u32 version | u64 tensor_count | u64 kv_count
  *   kv_count x { string key | u32 value type | value }
  *   tensor_count x { string name | u32 n_dims | u64 dims[n_dims] | u32 type | u64 offset }
- *   padding to general.alignment (32 when absent) | data section
+ *   padding to a multiple of 32 (src/gguf.c:595; general.alignment is
+ *   reported, not used) | data section
  * where a string is u64 length + bytes, and a value is a scalar, a string, or
  * an array (u32 element type | u64 count | elements, arrays nesting).
  */
@@ -137,17 +138,34 @@ void edgexpu_gguf_up_table_free(edgexpu_gguf_up_table *table) {
     memset(table, 0, sizeof(*table));
 }
 
-static uint64_t tensor_nbytes(const edgexpu_gguf_up_tensor *t) {
+/* The element count of t (the product of its dims), or 0 when the product
+ * does not fit 64 bits; *ok = 0 then. */
+static uint64_t tensor_elements(const edgexpu_gguf_up_tensor *t, int *ok) {
     uint64_t n = 1;
     uint32_t d;
-    size_t bs = edgexpu_gguf_type_block_size(t->type);
-    size_t bb = edgexpu_gguf_type_block_bytes(t->type);
-    if (bs == 0 || bb == 0) return 0;
+    *ok = 1;
     for (d = 0; d < t->n_dims; d++) {
-        if (t->dims[d] != 0 && n > UINT64_MAX / t->dims[d]) return 0;
+        if (t->dims[d] != 0 && n > UINT64_MAX / t->dims[d]) {
+            *ok = 0;
+            return 0;
+        }
         n *= t->dims[d];
     }
-    if (n % bs != 0) return 0;
+    return n;
+}
+
+/* Byte size of t's blocks: elements / block size * block bytes; 0 for a type
+ * without a block layout here, an element count that is not whole blocks, or
+ * a size that does not fit 64 bits (*ok = 0 for the last). */
+static uint64_t tensor_nbytes(const edgexpu_gguf_up_tensor *t, int *ok) {
+    size_t bs = edgexpu_gguf_type_block_size(t->type);
+    size_t bb = edgexpu_gguf_type_block_bytes(t->type);
+    uint64_t n = tensor_elements(t, ok);
+    if (!*ok || bs == 0 || bb == 0 || n % bs != 0) return 0;
+    if (n / bs > UINT64_MAX / bb) {
+        *ok = 0;
+        return 0;
+    }
     return n / bs * bb;
 }
 
@@ -194,14 +212,7 @@ int edgexpu_gguf_up_read_table(const char *path, edgexpu_gguf_up_table *table, c
         uint32_t t;
         if (!rd_string(&r, key, sizeof(key)) || !rd_u32(&r, &t)) break;
         if (strcmp(key, "general.alignment") == 0 && t == GV_U32) {
-            uint32_t a;
-            if (!rd_u32(&r, &a)) break;
-            if (a == 0 || (a & (a - 1)) != 0) {
-                fclose(r.f);
-                set_msg(error, error_size, "GGUF table: general.alignment is not a power of two");
-                return 0;
-            }
-            table->alignment = a;
+            if (!rd_u32(&r, &table->alignment)) break; /* reported only */
         } else if (!rd_skip_value(&r, t, 0)) {
             break;
         }
@@ -239,7 +250,16 @@ int edgexpu_gguf_up_read_table(const char *path, edgexpu_gguf_up_table *table, c
             if (!rd_u64(&r, &t->dims[d])) break;
         }
         if (!rd_u32(&r, &t->type) || !rd_u64(&r, &t->offset)) break;
-        t->nbytes = tensor_nbytes(t);
+        {
+            int ok;
+            t->nbytes = tensor_nbytes(t, &ok);
+            if (!ok) {
+                fclose(r.f);
+                edgexpu_gguf_up_table_free(table);
+                set_msg(error, error_size, "GGUF table: a tensor's element count or byte size overflows 64 bits");
+                return 0;
+            }
+        }
         table->n_tensors++;
     }
     fclose(r.f);
@@ -248,7 +268,9 @@ int edgexpu_gguf_up_read_table(const char *path, edgexpu_gguf_up_table *table, c
         set_msg(error, error_size, "GGUF table: truncated tensor infos");
         return 0;
     }
-    table->data_offset = (r.pos + table->alignment - 1) / table->alignment * table->alignment;
+    /* src/gguf.c:595: the data section starts at the end of the infos
+     * rounded up to 32, whatever general.alignment says */
+    table->data_offset = (r.pos + 31u) & ~(uint64_t)31u;
     for (i = 0; i < table->n_tensors; i++) {
         const edgexpu_gguf_up_tensor *t = &table->tensors[i];
         const uint64_t avail = table->data_offset <= r.size ? r.size - table->data_offset : 0;
@@ -335,22 +357,33 @@ const void *edgexpu_gguf_device_tensor(const edgexpu_gguf_device *d, const char 
 edgexpu_hip_weight *edgexpu_gguf_device_weight(const edgexpu_gguf_device *d, const char *name, int n_out, int n_in,
                                                char *error, size_t error_size) {
     const edgexpu_gguf_up_tensor *t = d != NULL ? edgexpu_gguf_up_find(&d->table, name) : NULL;
-    uint64_t n = 1;
-    uint32_t k;
+    uint64_t n;
+    size_t rb;
+    int ok;
     if (t == NULL || d->dev == NULL || n_out <= 0 || n_in <= 0) {
         if (error != NULL && error_size > 0)
             snprintf(error, error_size, "GGUF weight: missing tensor or bad shape: %s", name != NULL ? name : "");
         return NULL;
     }
-    for (k = 0; k < t->n_dims; k++) n *= t->dims[k];
-    if (n != (uint64_t)n_out * (uint64_t)n_in) {
+    n = tensor_elements(t, &ok);
+    if (!ok || n != (uint64_t)n_out * (uint64_t)n_in) {
         if (error != NULL && error_size > 0)
             snprintf(error, error_size, "GGUF weight: shape mismatch: %s (have %llu want %d*%d)", name,
                      (unsigned long long)n, n_out, n_in);
         return NULL;
     }
-    if (edgexpu_gguf_row_bytes(t->type, n_in) == 0) {
+    rb = edgexpu_gguf_row_bytes(t->type, n_in);
+    if (rb == 0) {
         if (error != NULL && error_size > 0) snprintf(error, error_size, "GGUF weight: unsupported type: %s", name);
+        return NULL;
+    }
+    /* load_qweight's size check (src/native.c:624-633): the blocks the
+     * handle reads, n_out rows of rb bytes, are exactly the tensor's bytes,
+     * which the table already bounded by the file */
+    if (t->nbytes == 0 || t->nbytes != (uint64_t)n_out * rb) {
+        if (error != NULL && error_size > 0)
+            snprintf(error, error_size, "GGUF weight: byte size mismatch: %s (have %llu want %d rows of %zu)", name,
+                     (unsigned long long)t->nbytes, n_out, rb);
         return NULL;
     }
     return edgexpu_hip_weight_wrap((const uint8_t *)d->dev + t->offset, t->type, n_out, n_in, NULL);

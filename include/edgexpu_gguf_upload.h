@@ -10,9 +10,10 @@
  *   - edgexpu_gguf_up_read_table reads the file's GGUF v3 tensor directory
  *     (the table edgexpu_gguf_load builds in src/gguf.c:359-610): header,
  *     every metadata key/value skipped by type, the tensor infos, and the
- *     data section offset, which is the end of the infos rounded up to the
- *     file's general.alignment (32 when the key is absent -- the value
- *     src/gguf.c:595 always uses);
+ *     data section offset, which is the end of the infos rounded up to 32
+ *     as src/gguf.c:595 computes it (a general.alignment key is reported in
+ *     the table but, as in the reference, not applied: a file whose writer
+ *     padded to 64 is read where the reference reads it);
  *   - edgexpu_gguf_device_upload copies the whole data section to the GPU
  *     once (one allocation holding the file's own bytes, so tensor t lives at
  *     base + t.offset, unchanged from the file), and
@@ -49,7 +50,7 @@ typedef struct edgexpu_gguf_up_tensor {
 
 typedef struct edgexpu_gguf_up_table {
     uint32_t version;
-    uint32_t alignment;     /* general.alignment, 32 when absent */
+    uint32_t alignment;     /* general.alignment as declared (32 when absent); not applied */
     uint64_t tensor_count;
     uint64_t kv_count;
     uint64_t data_offset;   /* file offset of the data section */
@@ -60,8 +61,9 @@ typedef struct edgexpu_gguf_up_table {
 
 /* Reads the tensor table of the GGUF v3 file at path.  1 on success; 0 and a
  * message in error otherwise (not a GGUF file, unsupported version, a
- * truncated header or table, more than 4 dims, a tensor whose bytes lie past
- * the end of the file).  Free with edgexpu_gguf_up_table_free. */
+ * truncated header or table, more than 4 dims, a tensor whose element count
+ * or byte size overflows 64 bits, a tensor whose bytes lie past the end of
+ * the file).  Free with edgexpu_gguf_up_table_free. */
 int edgexpu_gguf_up_read_table(const char *path, edgexpu_gguf_up_table *table, char *error, size_t error_size);
 void edgexpu_gguf_up_table_free(edgexpu_gguf_up_table *table);
 /* The tensor with this exact name, or NULL (edgexpu_gguf_find_tensor). */
@@ -78,8 +80,9 @@ const edgexpu_gguf_up_table *edgexpu_gguf_device_table(const edgexpu_gguf_device
 const void *edgexpu_gguf_device_tensor(const edgexpu_gguf_device *d, const char *name);
 /* A weight handle (edgexpu_hip_weight_wrap; not owning) over a tensor used as
  * an [n_out x n_in] matrix: NULL and a message when the name is unknown, the
- * element count is not n_out * n_in, or rows of n_in have no block layout
- * (the checks of load_qweight, src/native.c:611-640).  Free the handle with
+ * element count is not n_out * n_in, rows of n_in have no block layout, or
+ * the tensor's byte size is 0 or not n_out rows of n_in (the checks of
+ * load_qweight, src/native.c:611-644).  Free the handle with
  * edgexpu_hip_weight_free before edgexpu_gguf_device_free. */
 edgexpu_hip_weight *edgexpu_gguf_device_weight(const edgexpu_gguf_device *d, const char *name, int n_out, int n_in,
                                                char *error, size_t error_size);

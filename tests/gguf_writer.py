@@ -33,7 +33,8 @@ def write_gguf(path, kvs, tensors, alignment: int | None = None, version: int = 
     """kvs: [(key, type, value)] (ARRAY value: (element type, items));
     tensors: [(name, dims, type, bytes)].  Tensor data is laid out in order,
     each start padded to the alignment (32 unless given; given values are
-    also written as general.alignment).  Returns (data_offset, offsets)."""
+    also written as general.alignment).  Returns (data_offset, offsets,
+    info_end), info_end the file offset where the tensor infos end."""
     align = alignment or 32
     kv = list(kvs)
     if alignment is not None:
@@ -55,7 +56,7 @@ def write_gguf(path, kvs, tensors, alignment: int | None = None, version: int = 
             fh.write(bytes(data))
             pad = -(-len(data) // align) * align - len(data)
             fh.write(b"\0" * pad)
-    return data_offset, offsets
+    return data_offset, offsets, len(head)
 
 
 def as_bytes(a: np.ndarray) -> bytes:

@@ -2,8 +2,9 @@
 written from the format's definition (tests/gguf_writer.py): the directory the
 reference's loader builds (src/gguf.c:359-610) -- names, dims, types,
 offsets relative to the data section, the data section at the end of the
-infos rounded up to the alignment (32, src/gguf.c:595, or general.alignment)
--- and the loader's refusals.  No GPU."""
+infos rounded up to 32 whatever general.alignment declares (src/gguf.c:595
+never reads that key) -- and the loader's refusals, including element counts
+and byte sizes that overflow 64 bits.  No GPU."""
 import numpy as np
 import pytest
 
@@ -33,19 +34,28 @@ KVS = [("general.architecture", G.STRING, "llama"), ("general.name", G.STRING, "
        ("flag", G.BOOL, 1), ("i64", G.I64, -5), ("f64", G.F64, 2.5), ("u8", G.U8, 7), ("i16", G.I16, -3)]
 
 
-@pytest.mark.parametrize("alignment", [None, 64])
+@pytest.mark.parametrize("alignment", [None, 32, 64])
 def test_table_matches_the_written_file(gg, tmp_path, alignment):
     rng = np.random.default_rng(1 + (alignment or 0))
     tensors = _model(rng)
     path = str(tmp_path / "m.gguf")
-    data_offset, offsets = G.write_gguf(path, KVS, [(n, d, t, G.as_bytes(a)) for n, d, t, a in tensors],
-                                        alignment=alignment)
+    kvs = KVS if alignment != 64 else KVS + [("pad", G.STRING, "p" * 39)]
+    data_offset, offsets, info_end = G.write_gguf(path, kvs, [(n, d, t, G.as_bytes(a)) for n, d, t, a in tensors],
+                                                  alignment=alignment)
     tab = gg.read_table(path)
     assert tab["version"] == 3
     assert tab["alignment"] == (alignment or 32)
-    assert tab["kv_count"] == len(KVS) + (alignment is not None)
+    assert tab["kv_count"] == len(kvs) + (alignment is not None)
     assert tab["tensor_count"] == len(tensors)
-    assert tab["data_offset"] == data_offset and data_offset % (alignment or 32) == 0
+    # the reference's data offset: the end of the infos rounded up to 32
+    assert tab["data_offset"] == -(-info_end // 32) * 32
+    if alignment == 64:
+        # a file laid out for 64 whose infos end in the first half of a
+        # 64-byte line: the data the writer put at the next 64 lies 32 bytes
+        # past where the reference (and this reader) start the section
+        assert info_end % 64 < 32 and data_offset == tab["data_offset"] + 32
+        return
+    assert tab["data_offset"] == data_offset
     for (name, dims, t, arr), off, got in zip(tensors, offsets, tab["tensors"]):
         assert got["name"] == name and got["dims"] == dims and got["type"] == t and got["offset"] == off
         assert got["nbytes"] == arr.nbytes
@@ -69,7 +79,7 @@ def test_long_names_are_truncated_like_the_reference(gg, tmp_path):
 
 
 @pytest.mark.parametrize("case", ["magic", "version", "truncated_kv", "truncated_infos", "dims", "past_end",
-                                  "bad_alignment", "missing"])
+                                  "overflow_elements", "overflow_bytes", "missing"])
 def test_refusals(gg, tmp_path, case):
     rng = np.random.default_rng(4)
     w = synth.np_weights(E.Q4_K, 4, 256, rng)
@@ -83,9 +93,12 @@ def test_refusals(gg, tmp_path, case):
         with pytest.raises(ValueError, match="more than 4 dims"):
             gg.read_table(path)
         return
-    if case == "bad_alignment":
-        G.write_gguf(path, [("general.alignment", G.U32, 48)], [("t", [256, 4], E.Q4_K, G.as_bytes(w))])
-        with pytest.raises(ValueError, match="power of two"):
+    if case in ("overflow_elements", "overflow_bytes"):
+        # Q4_K dims whose product wraps to 256 in 64 bits, and F32 dims whose
+        # element count fits but whose byte size (x 4) does not
+        dims = [2 ** 56 + 1, 256] if case == "overflow_elements" else [2 ** 31, 2 ** 31]
+        G.write_gguf(path, [], [("t", dims, E.Q4_K if case == "overflow_elements" else E.F32, G.as_bytes(w))])
+        with pytest.raises(ValueError, match="overflows 64 bits"):
             gg.read_table(path)
         return
     if case == "version":
@@ -93,7 +106,7 @@ def test_refusals(gg, tmp_path, case):
         with pytest.raises(ValueError, match="version 3"):
             gg.read_table(path)
         return
-    data_offset, _ = G.write_gguf(path, KVS, [("t", [256, 4], E.Q4_K, G.as_bytes(w))])
+    data_offset, _, _ = G.write_gguf(path, KVS, [("t", [256, 4], E.Q4_K, G.as_bytes(w))])
     raw = bytearray(open(path, "rb").read())
     if case == "magic":
         raw[0:4] = b"GGML"
