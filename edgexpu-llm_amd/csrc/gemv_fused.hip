@@ -9,7 +9,7 @@ namespace exq {
 // gemv_fused_more.hip: plain projections of Q4_0 / Q5_0 / Q5_K rows
 hipError_t launch_gemv_fused_more(int type, const FusedArgs &a, bool stage, hipStream_t st);
 // gemv_stream.hip: one token of Q4_K rows at the decode row lengths
-bool gemv_stream_take(int type, int K, int m, long long rows);
+bool gemv_stream_take(int type, int K, int m, long long rows, int nmat, const uint8_t *const *w);
 hipError_t launch_gemv_stream(int nmat, const uint8_t *const *w, const int *n_out, const float *const *bias,
                               const float *const *resid, float *const *out, int K, const float *x,
                               const uint8_t *xq, const float *x2, const float *nw, float eps, int pro, bool pair,
@@ -296,7 +296,7 @@ hipError_t launch_gemv_fused_layer(int type, int nmat, const uint8_t *const *w, 
     // staged or Q8_K input), whose rows equal this kernel's bit for bit
     long long rows = 0;
     for (int z = 0; z < nmat; ++z) rows += n_out[z];
-    if (gemv_stream_take(type, K, m, rows))
+    if (gemv_stream_take(type, K, m, rows, nmat, w))
         return launch_gemv_stream(nmat, w, n_out, bias, resid, out, K, x, xq, x2, nw, eps, pro, pair, st);
     a.nblk = q8_0_family(type) ? K / kQK8_0 : K / kQKK;
     a.U = q8_0_family(type) ? a.nblk : a.nblk * 4;

@@ -581,12 +581,16 @@ bool gemv_stream_supported(int type, int K, int m) {
 // True when the streaming GEMV runs a launch of `rows` rows (pairs: gate and
 // up rows together) of (type, K, m).  By size, as measured on one MI355X
 // (launch sweep over distinct weights, both kernels in one run): K = 2560
-// and 4096 from 1024 rows on (e.g. [28672 x 4096] 14.5 against 16.0 us,
-// [4096 x 4096] 5.5 against 5.7), K = 14336 from 2048 rows (8 MB of rows
-// split four ways per wave: 7.7 against 7.0 us at 1024 rows, 11.0 against
-// 12.4 at 4096).
-bool gemv_stream_take(int type, int K, int m, long long rows) {
+// and 4096 at every size swept, 1024 rows up (e.g. [28672 x 4096] 14.5
+// against 16.0 us, [4096 x 4096] 5.2 against 5.7, [1024 x 4096] 4.4 against
+// 5.0), K = 14336 from 2048 rows (7.7 against 7.0 us at 1024 rows, 8.8
+// against 8.8 at 2048, 11.2 against 12.4 at 4096).
+// The rows go to LDS as 16-byte DMA transfers from 16-byte-aligned
+// addresses, so every matrix must start at one; others take the fused kernel.
+bool gemv_stream_take(int type, int K, int m, long long rows, int nmat, const uint8_t *const *w) {
     if (!gemv_stream_supported(type, K, m) || g_gemv_mode == 1) return false;
+    for (int z = 0; z < nmat; ++z)
+        if (((uintptr_t)w[z] & 15u) != 0) return false;
     if (g_gemv_mode == 2) return true;
     const long long bytes = rows * (long long)(K / kQKK) * kBytesQ4_K;
     return K != 14336 || bytes >= kStreamMinBytes14336;
@@ -603,6 +607,8 @@ hipError_t launch_gemv_stream(int nmat, const uint8_t *const *w, const int *n_ou
     if (!gemv_stream_supported(kTypeQ4_K, K, 1) || nmat < 1 || nmat > kStreamMaxMats) return hipErrorInvalidValue;
     if ((x == nullptr) == (xq == nullptr) || (xq != nullptr && (pro != 0 || pair))) return hipErrorInvalidValue;
     if (pair && (nmat != 2 || n_out[0] != n_out[1])) return hipErrorInvalidValue;
+    for (int z = 0; z < nmat; ++z)
+        if (((uintptr_t)w[z] & 15u) != 0) return hipErrorInvalidValue;
     StreamArgs a{};
     a.nmat = pair ? 1 : nmat;
     int rows = 0;

@@ -329,10 +329,20 @@ void *gemm_ws(size_t bytes) {
 // Formats with an exact matrix-core prefill GEMM: Q4_K straight from its
 // blocks (gemm.hip), Q5_K and Q6_K over a per-call repack (gemm_kq.hip), and
 // Q8_0 / Q4_0 / Q5_0 over a per-call repack against Q8_0 activations
-// (gemm_g32.hip).
-bool exact_gemm_type(uint32_t type, int n_out, int n_in, int m) {
-    return gemm_q8_supported((int)type, n_out, n_in, m) || gemm_kq_supported((int)type, n_out, n_in, m) ||
-           gemm_g32_supported((int)type, n_out, n_in, m);
+// (gemm_g32.hip).  The GEMMs also need their weight pointers aligned: Q4_K
+// rows are read as 16-byte vectors (and by the fp16 mode's GEMM likewise),
+// the repacks read 2-byte scale words.  Blocks at other addresses (a GGUF
+// data section may place a tensor at any offset its writer chose) take the
+// GEMV path, which reads bytes at any alignment.
+bool exact_gemm_type(uint32_t type, int nmat, const void *const *w, const int *n_out, int n_in, int m) {
+    const uintptr_t need = type == (uint32_t)kTypeQ4_K ? 15u : 1u;
+    for (int z = 0; z < nmat; ++z) {
+        if (!(gemm_q8_supported((int)type, n_out[z], n_in, m) || gemm_kq_supported((int)type, n_out[z], n_in, m) ||
+              gemm_g32_supported((int)type, n_out[z], n_in, m)))
+            return false;
+        if (((uintptr_t)w[z] & need) != 0) return false;
+    }
+    return true;
 }
 
 // Exact prefill GEMM of nmat matrices over one input: f32 activations
@@ -392,9 +402,9 @@ bool run_gemm_exact(uint32_t type, int nmat, const void *const *w, const int *n_
     return true;
 }
 
-bool use_exact_gemm(uint32_t type, int n_out, int n_in, int m) {
+bool use_exact_gemm(uint32_t type, int nmat, const void *const *w, const int *n_out, int n_in, int m) {
     return m >= gemm_min_tokens(type) && g.prefill_mode == EDGEXPU_HIP_PREFILL_EXACT_INT8 &&
-           exact_gemm_type(type, n_out, n_in, m);
+           exact_gemm_type(type, nmat, w, n_out, n_in, m);
 }
 
 // Workspace carve-up for m tokens of K elements.
@@ -441,6 +451,22 @@ bool check_linear_args(const void *out, const void *x, const void *w, uint32_t t
     }
     if ((size_t)n_in % unit_elems(type) != 0) {
         set_error(-2, "%s: n_in=%d is not a multiple of %zu for type %u", who, n_in, unit_elems(type), type);
+        return false;
+    }
+    return true;
+}
+
+// Device blocks of the formats whose blocks are an even but not a 4-byte
+// multiple long (Q8_0 34, Q4_0 18, Q5_0 22, Q6_K 210 bytes) are read as
+// aligned 32-bit words joined by byte shifts that assume an even block
+// address, so their device pointers must be even.  File-backed weights always
+// are: GGUF places tensors at multiples of the file's alignment (8 or more)
+// after a data section that starts at a multiple of 32 (src/gguf.c:595), and
+// device allocations start at 256.  Weights given as host memory are copied
+// to the device first and are not affected.
+bool check_weight_align(const void *w, uint32_t type, const char *who) {
+    if (((uintptr_t)w & 1u) != 0 && (q8_0_family((int)type) || type == (uint32_t)kTypeQ6_K)) {
+        set_error(-2, "%s: type-%u blocks must start at an even device address (got %p)", who, type, w);
         return false;
     }
     return true;
@@ -499,7 +525,7 @@ bool run_q8_product(uint32_t type, const void *w, int n_out, int n_in, int m, co
                     float *out, int ldo, hipStream_t st) {
     const size_t rb = edgexpu_hip_row_bytes(type, n_in);
     const size_t ab = act_bytes(type, n_in);
-    if (m >= gemm_min_tokens(type) && exact_gemm_type(type, n_out, n_in, m)) {
+    if (m >= gemm_min_tokens(type) && exact_gemm_type(type, 1, &w, &n_out, n_in, m)) {
         if (g.prefill_mode == EDGEXPU_HIP_PREFILL_F16 && gemm_q8_supported((int)type, n_out, n_in, m)) {
             void *ws = f16ws(gemm_f16_workspace(m, n_out, n_in));
             if (ws == nullptr) return false;
@@ -546,7 +572,7 @@ bool run_linear_group(uint32_t type, int nmat, const void *const *w, const int *
                                         nullptr, 0, st),
                       "gemv_fused");
     }
-    if (use_exact_gemm(type, n_out[0], n_in, m))  // the GEMM quantizes x into its own operand layout
+    if (use_exact_gemm(type, nmat, w, n_out, n_in, m))  // the GEMM quantizes x into its own operand layout
         return run_gemm_exact(type, nmat, w, n_out, n_in, m, x, nullptr, 0, bias, out, n_out, st);
     ActWs a;
     if (!act_ws(type, m, n_in, a)) return false;
@@ -779,7 +805,9 @@ int edgexpu_hip_weight_n_in(const edgexpu_hip_weight *w) { return w ? w->n_in : 
 int edgexpu_hip_linear_quant_batch_dev(float *out, const float *x, const void *w, uint32_t type, const float *bias,
                                        int m, int n_out, int n_in, void *stream) {
     if (!ensure_init()) return 0;
-    if (!check_linear_args(out, x, w, type, m, n_out, n_in, "linear_quant_batch")) return 0;
+    if (!check_linear_args(out, x, w, type, m, n_out, n_in, "linear_quant_batch") ||
+        !check_weight_align(w, type, "linear_quant_batch"))
+        return 0;
     if (!aligned16(x)) {
         set_error(-2, "linear_quant_batch: x must be 16-byte aligned");
         return 0;
@@ -797,7 +825,9 @@ int edgexpu_hip_linear_quant_group_dev(int nmat, float *const *out, const float 
         return 0;
     }
     for (int z = 0; z < nmat; ++z) {
-        if (!check_linear_args(out[z], x, w[z], type, m, n_out[z], n_in, "linear_quant_group")) return 0;
+        if (!check_linear_args(out[z], x, w[z], type, m, n_out[z], n_in, "linear_quant_group") ||
+            !check_weight_align(w[z], type, "linear_quant_group"))
+            return 0;
     }
     if (!aligned16(x)) {
         set_error(-2, "linear_quant_group: x must be 16-byte aligned");
@@ -820,7 +850,9 @@ int edgexpu_hip_layer_linear_dev(int nmat, float *const *out, const float *x, co
         return 0;
     }
     for (int z = 0; z < nmat; ++z) {
-        if (!check_linear_args(out[z], x, w[z], type, m, n_out[z], n_in, "layer_linear")) return 0;
+        if (!check_linear_args(out[z], x, w[z], type, m, n_out[z], n_in, "layer_linear") ||
+            !check_weight_align(w[z], type, "layer_linear"))
+            return 0;
     }
     if (!aligned16(x) || (x2 != nullptr && !aligned16(x2)) || (norm_weight != nullptr && !aligned16(norm_weight))) {
         set_error(-2, "layer_linear: x, x2 and norm_weight must be 16-byte aligned");
@@ -885,7 +917,8 @@ int edgexpu_hip_gate_up_silu_dev(float *act, const float *x, const float *norm_w
                                  int n_ff, int n_in, void *stream) {
     if (!ensure_init()) return 0;
     if (!check_linear_args(act, x, w_gate, type, m, n_ff, n_in, "gate_up_silu") ||
-        !check_linear_args(act, x, w_up, type, m, n_ff, n_in, "gate_up_silu"))
+        !check_linear_args(act, x, w_up, type, m, n_ff, n_in, "gate_up_silu") ||
+        !check_weight_align(w_gate, type, "gate_up_silu") || !check_weight_align(w_up, type, "gate_up_silu"))
         return 0;
     if (!aligned16(x) || (norm_weight != nullptr && !aligned16(norm_weight))) {
         set_error(-2, "gate_up_silu: x and norm_weight must be 16-byte aligned");
@@ -926,7 +959,8 @@ int edgexpu_hip_gate_up_silu_dev(float *act, const float *x, const float *norm_w
 int edgexpu_hip_gemv_q8_dev(float *out, const uint8_t *xq, const void *w, uint32_t type, const float *bias, int m,
                             int n_out, int n_in, void *stream) {
     if (!ensure_init()) return 0;
-    if (!check_linear_args(out, xq, w, type, m, n_out, n_in, "gemv_q8")) return 0;
+    if (!check_linear_args(out, xq, w, type, m, n_out, n_in, "gemv_q8") || !check_weight_align(w, type, "gemv_q8"))
+        return 0;
     if (plain_type(type)) {
         set_error(-3, "gemv_q8: F16 and F32 rows have no quantized-activation dot (src/gguf_dot_q8.c:414-434)");
         return 0;
@@ -946,7 +980,8 @@ namespace {
 
 bool check_logits_args(float *scores, const float *hidden, const void *w, uint32_t type, int m, int vocab,
                        int n_embd, int chunk_rows, const char *who) {
-    if (!check_linear_args(scores, hidden, w, type, m, vocab, n_embd, who)) return false;
+    if (!check_linear_args(scores, hidden, w, type, m, vocab, n_embd, who) || !check_weight_align(w, type, who))
+        return false;
     if (m > kGemvMaxTokens) {
         set_error(-2, "%s: at most %d hidden vectors per call (m=%d)", who, kGemvMaxTokens, m);
         return false;
@@ -1086,6 +1121,7 @@ int edgexpu_hip_dequantize_dev(const void *src, uint32_t type, uint64_t n_elemen
         set_error(-2, "dequantize: dst must be 16-byte aligned");
         return 0;
     }
+    if (!check_weight_align(src, type, "dequantize")) return 0;
     return hip_ok(launch_dequantize((const uint8_t *)src, (int)type, n_elements, dst, pick_stream(stream)),
                   "dequantize")
                ? 1
@@ -1110,6 +1146,7 @@ int edgexpu_hip_embed_rows_dev(float *out, const void *table, uint32_t type, lon
                   embed_unit(type), type);
         return 0;
     }
+    if (!check_weight_align(table, type, "embed_rows")) return 0;
     return hip_ok(launch_dequantize_rows((const uint8_t *)table, (int)type, n_rows, n_embd, ids, n_ids, out, bad,
                                          pick_stream(stream)),
                   "embed_rows")

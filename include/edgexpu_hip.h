@@ -121,7 +121,12 @@ int edgexpu_hip_weight_n_out(const edgexpu_hip_weight *w);
 int edgexpu_hip_weight_n_in(const edgexpu_hip_weight *w);
 
 /* ---- device-pointer entry points (all buffers in device memory; work is
- * queued on `stream` and not waited for) ---- */
+ * queued on `stream` and not waited for).  Weight blocks may start at any
+ * address except that Q8_0, Q4_0, Q5_0 and Q6_K blocks (34, 18, 22 and 210
+ * bytes) must start at an even one: an odd one is refused with error -2.
+ * GGUF tensors in a device copy of a file's data section always qualify.
+ * Q4_K at 16-byte addresses takes the streaming and matrix-core kernels,
+ * elsewhere the fused GEMV, with the same results. ---- */
 
 /* out[t*n_out + o] = bias[o] + dot(W[o], q8(x[t]))  for t < m.
  * Replaces edgexpu_cpu_linear_quant_batch (include/edgexpu/cpu_kernel.h:71-80,
