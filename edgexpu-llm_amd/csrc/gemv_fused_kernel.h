@@ -347,8 +347,11 @@ struct FusedLds {
 };
 
 // Waves per SIMD the register allocator is held to: enough for the whole
-// weight matrix to be requested by one generation of workgroups, without
-// spilling (checked with -Rpass-analysis=kernel-resource-usage).
+// weight matrix to be requested by one generation of workgroups.  The
+// figures for the wide Q6_K weight registers and the staging prologues are
+// capped in fused_occupancy_pro so that no instantiation spills (every
+// instantiation in this library reports 0 bytes of scratch under
+// -Rpass-analysis=kernel-resource-usage).
 template <class Fmt>
 constexpr int fused_occupancy(int r, int m, int loop) {
     // f32-activation formats: the activation slice (32 to 68 floats) stays
@@ -369,13 +372,24 @@ constexpr int fused_occupancy(int r, int m, int loop) {
 // STAGE: quantize a.x into LDS inside the kernel; otherwise read the codes
 // of a.xq (quantized by an earlier launch) straight from global memory.
 // A staging prologue holds its second input (16 more registers) and its
-// arithmetic beside the first tile: one wave per SIMD fewer where the plain
-// kernel runs at more than 5 (4 for the Q6_K rows), so that nothing spills.
+// arithmetic beside the first tile, the RMSNorm one its sums too.  Caps
+// found with -Rpass-analysis=kernel-resource-usage, each the highest
+// occupancy at which that shape spills nothing:
+//   Q4_K rows, RMSNorm prologue: 4;  other prologues: 5;
+//   Q6_K rows (56 bytes of weight registers per unit): 4 for one or two rows
+//   per slot; four rows per slot: 2 under a prologue or a gate/up pair
+//   (whose two rows per slot hold twice the weights).
 template <class Fmt>
 constexpr int fused_occupancy_pro(int r, int m, int loop, int pro) {
-    const int occ = fused_occupancy<Fmt>(r, m, loop);
-    const int cap = sizeof(typename Fmt::W) > 48 ? 4 : 5;
-    return (pro & 3) != 0 && occ > cap ? cap : occ;
+    const bool wide = sizeof(typename Fmt::W) > 48;
+    int occ = fused_occupancy<Fmt>(r, m, loop);
+    int cap = (pro & 3) == 1 ? 4 : (pro & 3) != 0 ? 5 : 8;
+    if (wide) {
+        cap = cap < 4 ? cap : 4;
+        const int rows = r * ((pro & 8) != 0 ? 2 : 1);  // a pair's slot holds gate and up rows
+        if (rows >= 4 && ((pro & 3) != 0 || (pro & 8) != 0)) cap = 2;
+    }
+    return occ > cap ? cap : occ;
 }
 
 // PRO bits 0-1: staging prologue (0 none, 1 RMSNorm, 2 SiLU-mul; STAGE
@@ -725,7 +739,7 @@ static int device_cus() {
 // EXQ_FUSED_PIPE / EXQ_FUSED_DYN / EXQ_FUSED_BIG (tile schedule).
 
 // Grid of the most recent launch_fused_fmt (the argmax epilogue's key count).
-static int &fused_last_grid() {
+static inline int &fused_last_grid() {
     static int g = 0;
     return g;
 }
@@ -804,7 +818,10 @@ static hipError_t launch_fused_m(FusedArgs a, int r1, int loop, hipStream_t st) 
             }
             if (loop == 1) {
                 if (r1 == 1) return launch_fused_fmt<Fmt, 1, 1, NW, STAGE, 1>(a, st);
-                if (r1 == 4) return launch_fused_fmt<Fmt, 1, 4, NW, STAGE, 1>(a, st);
+                // two buffers of four Q6_K rows exceed the 256 registers a
+                // wave of an 8-wave workgroup can hold: two rows instead
+                if constexpr (sizeof(typename Fmt::W) <= 48)
+                    if (r1 == 4) return launch_fused_fmt<Fmt, 1, 4, NW, STAGE, 1>(a, st);
                 return launch_fused_fmt<Fmt, 1, 2, NW, STAGE, 1>(a, st);
             }
             if (r1 == 1) return launch_fused_fmt<Fmt, 1, 1, NW, STAGE, 0>(a, st);
