@@ -349,9 +349,9 @@ struct FusedLds {
 // Waves per SIMD the register allocator is held to: enough for the whole
 // weight matrix to be requested by one generation of workgroups.  The
 // figures for the wide Q6_K weight registers and the staging prologues are
-// capped in fused_occupancy_pro so that no instantiation spills (every
-// instantiation in this library reports 0 bytes of scratch under
-// -Rpass-analysis=kernel-resource-usage).
+// capped in fused_occupancy_pro so that no instantiation spills (under
+// -Rpass-analysis=kernel-resource-usage every instantiation in this library
+// reports 0 bytes of scratch but one, named there).
 template <class Fmt>
 constexpr int fused_occupancy(int r, int m, int loop) {
     // f32-activation formats: the activation slice (32 to 68 floats) stays
@@ -379,9 +379,14 @@ constexpr int fused_occupancy(int r, int m, int loop) {
 //   Q6_K rows (56 bytes of weight registers per unit): 4 for one or two rows
 //   per slot; four rows per slot: 2 under a prologue or a gate/up pair
 //   (whose two rows per slot hold twice the weights).
+// One exception is deliberate: the Q4_K logits kernel with the argmax
+// epilogue (f32 activation, two rows per slot) runs at 4 with 16 bytes of
+// scratch per lane rather than at 3 without (77.9 against 82.4 us for the
+// [128256 x 4096] product); at 3 its two workgroups per CU no longer fit.
 template <class Fmt>
 constexpr int fused_occupancy_pro(int r, int m, int loop, int pro) {
     const bool wide = sizeof(typename Fmt::W) > 48;
+    if ((pro & 16) != 0 && sizeof(typename Fmt::Act) >= 128 && !wide && m == 1 && r <= 2) return 4;
     int occ = fused_occupancy<Fmt>(r, m, loop);
     int cap = (pro & 3) == 1 ? 4 : (pro & 3) != 0 ? 5 : 8;
     if (wide) {
@@ -598,8 +603,9 @@ void gemv_fused_kernel(FusedArgs a) {
         if constexpr (kArgmax) {
             const unsigned long long k = live ? score_key(o, (unsigned)row) : 0ull;
             if constexpr (kKeyLds) {
-                const unsigned long long b = lbest[threadIdx.x];
-                lbest[threadIdx.x] = k > b ? k : b;
+                // the LDS unit keeps the maximum (ds_max_u64; each lane owns
+                // its slot): no register holds the old key
+                __hip_atomic_fetch_max(&lbest[threadIdx.x], k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
             } else {
                 best_reg = k > best_reg ? k : best_reg;
             }
