@@ -57,7 +57,7 @@ struct StreamArgs {
     int n_out[kStreamMaxMats];
     int row_start[kStreamMaxMats + 1];     // first step of each matrix
     int nrows;                             // steps (rows, or gate/up pairs)
-    const float *x;                        // f32 activation [K] (staged), or
+    const float *x;                        // f32 activation [m][K] (staged), or
     const uint8_t *xq;                     // its Q8_K block bytes
     const float *x2;                       // SiLU-mul: act = silu(x) * x2
     const float *nw;                       // RMSNorm: act = rmsnorm(x; nw, eps)
@@ -216,7 +216,7 @@ __device__ __forceinline__ void act_from_blocks(const uint8_t *raw, int unit, Fm
     x.spair = ((uint32_t)s0 & 0xffffu) | ((uint32_t)s1 << 16);
 }
 
-template <int KSB, int NW, int NB, int FL, bool DEEP>
+template <int KSB, int NW, int NB, int FL, bool DEEP, int M = 1>
 struct StreamGeom {
     static constexpr int K = KSB * kQKK;
     static constexpr int U = 4 * KSB;                    // units per row
@@ -228,8 +228,9 @@ struct StreamGeom {
     static constexpr int PL = (RB % 1024) / 16;          // lanes of the partial chunk
     static constexpr int NI = RPS * (CH + (PL > 0 ? 1 : 0));  // DMA instructions per step
     static constexpr int NT = NW * 64;
-    static constexpr int ROUNDS = (FL & kSXq) ? 0 : (KSB * 16 + NT - 1) / NT;  // staging rounds
-    static constexpr int QB = (K + 15) & ~15, DB = (KSB * 4 + 15) & ~15, BB = ((K / 16) * 2 + 15) & ~15;
+    static constexpr int ROUNDS = (FL & kSXq) ? 0 : (M * KSB * 16 + NT - 1) / NT;  // staging rounds
+    // staged activations of the M tokens: codes, block scales, 16-element sums
+    static constexpr int QB = (M * K + 15) & ~15, DB = (M * KSB * 4 + 15) & ~15, BB = (M * (K / 16) * 2 + 15) & ~15;
     static constexpr int XQB = ((KSB * kBytesQ8_K + 1023) / 1024) * 1024;  // raw blocks, whole chunks
     static constexpr int AREA = (FL & kSXq) ? XQB : QB + DB + BB;
     // ring slots: NB steps in flight, NS at the start (DEEP: twice NB)
@@ -237,13 +238,15 @@ struct StreamGeom {
     static constexpr size_t lds() { return (size_t)AREA + (size_t)NW * NS * SB; }
     static_assert(RB % 16 == 0, "16-byte DMA lanes");
     static_assert(AREA + (size_t)NW * NS * SB + 8 * NW <= 160 * 1024, "the ring and the staging fit the gfx950 LDS");
+    static_assert(ROUNDS <= 2, "the staging loads of at most two rounds are in flight at the start");
     static_assert(NS * NI + 8 * ((FL & 3) ? 2 : 1) <= 63, "vmcnt range");
     static_assert(AREA % 16 == 0, "slot alignment");
+    static_assert(M == 1 || FL == 0, "several tokens: plain projections of staged activations");
 };
 
-template <int KSB, int NW, int NB, int FL, bool DEEP>
+template <int KSB, int NW, int NB, int FL, bool DEEP, int M = 1>
 __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
-    using G = StreamGeom<KSB, NW, NB, FL, DEEP>;
+    using G = StreamGeom<KSB, NW, NB, FL, DEEP, M>;
     constexpr int PRO = FL & 3;
     constexpr bool kRes = (FL & kSRes) != 0, kPair = (FL & kSPair) != 0, kXq = (FL & kSXq) != 0;
     constexpr int NS = G::NS;
@@ -304,7 +307,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     } else {
 #pragma unroll
         for (int r = 0; r < G::ROUNDS; ++r) {
-            const int blk = min(r * BPR + bl, KSB - 1);
+            // block blk of the M tokens' [M][K] activation (token blk / KSB)
+            const int blk = min(r * BPR + bl, M * KSB - 1);
             const float *px = a.x + blk * kQKK + 16 * sub;
 #pragma unroll
             for (int k = 0; k < 4; ++k) xr[r][k] = s_load16(px + 4 * k);
@@ -379,12 +383,13 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
                 }
         }
 #pragma unroll
-        for (int r = 0; r < G::ROUNDS; ++r) quantize_q8_k_group<G::NT>(xs[r], r * BPR + bl, KSB, KSB, G::K, sub, lq, ld, lbs);
+        for (int r = 0; r < G::ROUNDS; ++r)
+            quantize_q8_k_group<G::NT>(xs[r], r * BPR + bl, M * KSB, KSB, G::K, sub, lq, ld, lbs);
         __syncthreads();
     }
     // the lane's activation slices, scale selectors and row offsets
     const ActLds act{lq, ld, lbs, G::K, KSB};
-    FmtQ4K::Act xa[G::T];
+    FmtQ4K::Act xa[M][G::T];
     ScaleSel lc[G::T];
     uint32_t hoff[G::T], qoff[G::T];
     bool live[G::T];
@@ -393,8 +398,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
         const int u = lane + 64 * t;
         live[t] = u < G::U;
         const int uc = min(u, G::U - 1);
-        if constexpr (kXq) act_from_blocks(smem, uc, xa[t]);
-        else FmtQ4K::load_act_lds(act, uc, 0, xa[t]);
+        if constexpr (kXq) {
+            act_from_blocks(smem, uc, xa[0][t]);
+        } else {
+#pragma unroll
+            for (int m = 0; m < M; ++m) FmtQ4K::load_act_lds(act, uc, m, xa[m][t]);
+        }
         lc[t] = scale_sel(uc & 3);
         hoff[t] = (uint32_t)(uc >> 2) * kBytesQ4_K;
         qoff[t] = hoff[t] + 16u + 32u * (uint32_t)(uc & 3);
@@ -404,11 +413,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     struct Epi {
         float b0, b1, r;
     };
-    auto lane_out = [&](int step, float *&out, int &row, const float *&bias, const float *&resid) {
+    auto lane_out = [&](int step, float *&out, int &row, const float *&bias, const float *&resid, int &n_out) {
         out = a.out[0];
         bias = a.bias[0];
         resid = a.resid[0];
         row = step;
+        n_out = a.n_out[0];
 #pragma unroll
         for (int z = 1; z < kStreamMaxMats; ++z) {
             const bool in = !kPair && z < a.nmat && step >= a.row_start[z];
@@ -416,15 +426,16 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
             bias = in ? a.bias[z] : bias;
             resid = in ? a.resid[z] : resid;
             row = in ? step - a.row_start[z] : row;
+            n_out = in ? a.n_out[z] : n_out;
         }
     };
     auto load_epi = [&](int first) {
         const int step = first + lane * TW;
         const bool ok = step < last;
         float *out;
-        int row;
+        int row, n_out;
         const float *bias, *resid;
-        lane_out(ok ? step : 0, out, row, bias, resid);
+        lane_out(ok ? step : 0, out, row, bias, resid, n_out);
         Epi e{0.0f, 0.0f, 0.0f};
         if (ok) {
             e.b0 = bias != nullptr ? bias[row] : 0.0f;
@@ -433,20 +444,26 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
         }
         return e;
     };
-    float keep0 = 0.0f, keep1 = 0.0f;
+    // keep[m]: token m's total of step k (k % 64 = this lane); keep1: up's
+    float keep[M], keep1 = 0.0f;
+#pragma unroll
+    for (int m = 0; m < M; ++m) keep[m] = 0.0f;
     auto flush = [&](int first, int n, const Epi &e) {
         const int step = first + lane * TW;
         float *out;
-        int row;
+        int row, n_out;
         const float *bias, *resid;
-        lane_out(step < last ? step : 0, out, row, bias, resid);
+        lane_out(step < last ? step : 0, out, row, bias, resid, n_out);
         if (lane < n && step < last) {
             // out = resid + (bias + dot) (src/native.c:2571-2580); pairs: silu(gate) * up
-            const float v = e.b0 + keep0;
-            float o = v;
-            if constexpr (kRes) o = resid != nullptr ? e.r + v : v;
-            if constexpr (kPair) o = silu_f32(v) * (e.b1 + keep1);
-            out[row] = o;
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const float v = e.b0 + keep[m];
+                float o = v;
+                if constexpr (kRes) o = resid != nullptr ? e.r + v : v;
+                if constexpr (kPair) o = silu_f32(v) * (e.b1 + keep1);
+                out[(size_t)m * n_out + row] = o;
+            }
         }
     };
     Epi epi = load_epi(gw);
@@ -457,7 +474,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     //    that, steps up to NS - 1 came with the start), then the lane partials
     //    of each row: per unit pass t, dead units 0.  WAIT: this wave's DMAs
     //    of later steps that may stay in flight.
-    auto step_partials = [&](auto wait_c, int slot, int k, float (&p)[G::RPS][G::T]) {
+    auto step_partials = [&](auto wait_c, int slot, int k, float (&p)[M][G::RPS][G::T]) {
         s_wait_vm<decltype(wait_c)::value>();
         const uint8_t *sb = ring + slot * G::SB;
         v4u_t h[G::RPS][G::T], q0[G::RPS][G::T], q1[G::RPS][G::T];
@@ -472,12 +489,14 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         if (k + NB >= NS) issue((slot + NB) % NS, gw + (k + NB) * TW);  // uniform; slot == k % NS
 #pragma unroll
-        for (int r = 0; r < G::RPS; ++r)
+        for (int m = 0; m < M; ++m)
 #pragma unroll
-            for (int t = 0; t < G::T; ++t) {
-                const float v = q4k_unit(h[r][t], q0[r][t], q1[r][t], xa[t], lc[t]);
-                p[r][t] = live[t] ? v : 0.0f;
-            }
+            for (int r = 0; r < G::RPS; ++r)
+#pragma unroll
+                for (int t = 0; t < G::T; ++t) {
+                    const float v = q4k_unit(h[r][t], q0[r][t], q1[r][t], xa[m][t], lc[t]);
+                    p[m][r][t] = live[t] ? v : 0.0f;
+                }
     };
     int k64 = 0, first = gw;
     auto advance = [&]() {
@@ -491,27 +510,38 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     };
     // a row's total: per unit pass the wave's sum (the fused kernel's waves of
     // a split row), the passes added in order from 0
-    auto finish = [&](float (&p)[G::RPS][G::T]) {
-        float acc[G::RPS];
+    auto finish = [&](float (&p)[M][G::RPS][G::T]) {
+        float acc[M][G::RPS];
+        if constexpr (M == 4 && G::T == 1) {
+            // four tokens' rows in one tree (each total is its s_wave_total bit for bit)
+            const float v4[4] = {p[0][0][0], p[1][0][0], p[2][0][0], p[3][0][0]};
+            const float tot = s_wave_total4(v4);
 #pragma unroll
-        for (int r = 0; r < G::RPS; ++r) {
-            if constexpr (G::T == 1) {
-                acc[r] = s_wave_total(p[r][0]);
-            } else if constexpr (G::T == 4) {
-                const float tot = s_wave_total4(p[r]);
-                float sum = 0.0f;
+            for (int m = 0; m < 4; ++m) acc[m][0] = s_lane(tot, 16 * m);
+        } else {
 #pragma unroll
-                for (int t = 0; t < 4; ++t) sum += s_lane(tot, 16 * t);
-                acc[r] = sum;
-            } else {
-                float sum = 0.0f;
+            for (int m = 0; m < M; ++m)
 #pragma unroll
-                for (int t = 0; t < G::T; ++t) sum += s_wave_total(p[r][t]);
-                acc[r] = sum;
-            }
+                for (int r = 0; r < G::RPS; ++r) {
+                    if constexpr (G::T == 1) {
+                        acc[m][r] = s_wave_total(p[m][r][0]);
+                    } else if constexpr (G::T == 4) {
+                        const float tot = s_wave_total4(p[m][r]);
+                        float sum = 0.0f;
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) sum += s_lane(tot, 16 * t);
+                        acc[m][r] = sum;
+                    } else {
+                        float sum = 0.0f;
+#pragma unroll
+                        for (int t = 0; t < G::T; ++t) sum += s_wave_total(p[m][r][t]);
+                        acc[m][r] = sum;
+                    }
+                }
         }
-        keep0 = lane == k64 ? acc[0] : keep0;
-        if constexpr (kPair) keep1 = lane == k64 ? acc[G::RPS - 1] : keep1;
+#pragma unroll
+        for (int m = 0; m < M; ++m) keep[m] = lane == k64 ? acc[m][0] : keep[m];
+        if constexpr (kPair) keep1 = lane == k64 ? acc[0][G::RPS - 1] : keep1;
         advance();
     };
     // the first NS steps: their rows came with the start, so fewer stay in flight after each
@@ -519,7 +549,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     [&]<int... K>(std::integer_sequence<int, K...>) {
         ((more = more && gw + K * TW < last,
           more ? (void)([&] {
-              float p[G::RPS][G::T];
+              float p[M][G::RPS][G::T];
               step_partials(std::integral_constant<int, (K < NS - NB ? NS - 1 - K : NB - 1) * G::NI>{}, K, K, p);
               finish(p);
           }())
@@ -532,7 +562,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
         for (int b = 0; b < NS; ++b) {
             more = more && gw + (k0 + b) * TW < last;
             if (more) {  // uniform
-                float p[G::RPS][G::T];
+                float p[M][G::RPS][G::T];
                 step_partials(std::integral_constant<int, (NB - 1) * G::NI>{}, b, k0 + b, p);
                 finish(p);
             }
@@ -542,7 +572,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     if (k64 > 0) flush(first, k64, epi);
 }
 
-template <int KSB, int NW, int NB, int FL>
+template <int KSB, int NW, int NB, int FL, int M = 1>
 hipError_t launch_stream(const StreamArgs &a, hipStream_t st) {
     // one workgroup per CU: the grid covers the chip once and every wave
     // strides over the rows.  Launches of at most three steps per wave fill
@@ -554,14 +584,26 @@ hipError_t launch_stream(const StreamArgs &a, hipStream_t st) {
     const long long steps = ((long long)a.nrows + (long long)grid * NW - 1) / ((long long)grid * NW);
     if constexpr (KSB <= 16) {
         if (steps <= 3) {
-            using G = StreamGeom<KSB, NW, NB, FL, true>;
-            hipLaunchKernelGGL((gemv_stream_q4k<KSB, NW, NB, FL, true>), dim3(grid), dim3(NW * 64), G::lds(), st, a);
+            using G = StreamGeom<KSB, NW, NB, FL, true, M>;
+            hipLaunchKernelGGL((gemv_stream_q4k<KSB, NW, NB, FL, true, M>), dim3(grid), dim3(NW * 64), G::lds(), st,
+                               a);
             return hipGetLastError();
         }
     }
-    using G = StreamGeom<KSB, NW, NB, FL, false>;
-    hipLaunchKernelGGL((gemv_stream_q4k<KSB, NW, NB, FL, false>), dim3(grid), dim3(NW * 64), G::lds(), st, a);
+    using G = StreamGeom<KSB, NW, NB, FL, false, M>;
+    hipLaunchKernelGGL((gemv_stream_q4k<KSB, NW, NB, FL, false, M>), dim3(grid), dim3(NW * 64), G::lds(), st, a);
     return hipGetLastError();
+}
+
+// Plain projections of m = 2..4 staged tokens (rows of 2560 or 4096).
+template <int KSB>
+hipError_t launch_stream_tokens(int m, const StreamArgs &a, hipStream_t st) {
+    switch (m) {
+        case 2: return launch_stream<KSB, 8, 2, 0, 2>(a, st);
+        case 3: return launch_stream<KSB, 8, 2, 0, 3>(a, st);
+        case 4: return launch_stream<KSB, 8, 2, 0, 4>(a, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 template <int KSB, int NW, int NB>
@@ -590,8 +632,11 @@ int gemv_stream_mode() { return g_gemv_mode; }
 
 // True when the streaming GEMV can take (type, K, m): one token of Q4_K rows
 // of 2560, 4096 or 14336 elements.
-bool gemv_stream_supported(int type, int K, int m) {
-    return type == kTypeQ4_K && m == 1 && (K == 2560 || K == 4096 || K == 14336);
+// m = 2..4 tokens: rows of 2560 or 4096, plain projections of f32 tokens.
+bool gemv_stream_supported(int type, int K, int m, bool plain_staged) {
+    if (type != kTypeQ4_K) return false;
+    if (m == 1) return K == 2560 || K == 4096 || K == 14336;
+    return m >= 2 && m <= 4 && plain_staged && (K == 2560 || K == 4096);
 }
 
 // True when the streaming GEMV runs a launch of `rows` rows (pairs: gate and
@@ -603,8 +648,9 @@ bool gemv_stream_supported(int type, int K, int m) {
 // against 8.8 at 2048, 11.2 against 12.4 at 4096).
 // The rows go to LDS as 16-byte DMA transfers from 16-byte-aligned
 // addresses, so every matrix must start at one; others take the fused kernel.
-bool gemv_stream_take(int type, int K, int m, long long rows, int nmat, const uint8_t *const *w) {
-    if (!gemv_stream_supported(type, K, m) || g_gemv_mode == 1) return false;
+// plain_staged: f32 tokens, no prologue, residual or pairs.
+bool gemv_stream_take(int type, int K, int m, long long rows, int nmat, const uint8_t *const *w, bool plain_staged) {
+    if (!gemv_stream_supported(type, K, m, plain_staged) || g_gemv_mode == 1) return false;
     for (int z = 0; z < nmat; ++z)
         if (((uintptr_t)w[z] & 15u) != 0) return false;
     if (g_gemv_mode == 2) return true;
@@ -612,15 +658,20 @@ bool gemv_stream_take(int type, int K, int m, long long rows, int nmat, const ui
     return K != 14336 || bytes >= kStreamMinBytes14336;
 }
 
-// nmat Q4_K matrices against one token: x f32 (quantized in the kernel, after
+// nmat Q4_K matrices against one token (m = 1) or the plain projection of
+// m = 2..4 tokens ([m][K] f32 x; out[z] is [m][n_out[z]]): x f32 (quantized in the kernel, after
 // the prologue pro: 1 RMSNorm with nw / eps, 2 SiLU-mul with x2) or xq (Q8_K
 // block bytes); resid (per matrix, may be null) added after the bias; pair:
 // nmat = 2 (gate, up), out[0] = silu(gate) * up.
 hipError_t launch_gemv_stream(int nmat, const uint8_t *const *w, const int *n_out, const float *const *bias,
-                              const float *const *resid, float *const *out, int K, const float *x,
+                              const float *const *resid, float *const *out, int K, int m, const float *x,
                               const uint8_t *xq, const float *x2, const float *nw, float eps, int pro, bool pair,
                               hipStream_t st) {
-    if (!gemv_stream_supported(kTypeQ4_K, K, 1) || nmat < 1 || nmat > kStreamMaxMats) return hipErrorInvalidValue;
+    bool any_resid = false;
+    for (int z = 0; z < nmat && resid != nullptr; ++z) any_resid = any_resid || resid[z] != nullptr;
+    const bool plain_staged = x != nullptr && pro == 0 && !pair && !any_resid;
+    if (!gemv_stream_supported(kTypeQ4_K, K, m, plain_staged) || nmat < 1 || nmat > kStreamMaxMats)
+        return hipErrorInvalidValue;
     if ((x == nullptr) == (xq == nullptr) || (xq != nullptr && (pro != 0 || pair))) return hipErrorInvalidValue;
     if (pair && (nmat != 2 || n_out[0] != n_out[1])) return hipErrorInvalidValue;
     for (int z = 0; z < nmat; ++z)
@@ -650,6 +701,7 @@ hipError_t launch_gemv_stream(int nmat, const uint8_t *const *w, const int *n_ou
     a.eps = eps;
     if (any_res && pair) return hipErrorInvalidValue;
     const int fl = xq != nullptr ? kSXq : ((pro & 3) | (any_res ? kSRes : 0) | (pair ? kSPair : 0));
+    if (m > 1) return K == 2560 ? launch_stream_tokens<10>(m, a, st) : launch_stream_tokens<16>(m, a, st);
     // measured on the Llama-3-8B / hybrid decode shapes: 8 waves per CU, two
     // slots per wave, one slot where a row is 8 KB (K = 14336: two, 12.7
     // against 10.9 us at [4096 x 14336])
