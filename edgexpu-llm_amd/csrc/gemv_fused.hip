@@ -9,11 +9,12 @@ namespace exq {
 // gemv_fused_more.hip: plain projections of Q4_0 / Q5_0 / Q5_K rows
 hipError_t launch_gemv_fused_more(int type, const FusedArgs &a, bool stage, hipStream_t st);
 // gemv_stream.hip: one to four tokens of Q4_K rows at the decode row lengths
-bool gemv_stream_take(int type, int K, int m, long long rows, int nmat, const uint8_t *const *w, bool plain_staged);
-hipError_t launch_gemv_stream(int nmat, const uint8_t *const *w, const int *n_out, const float *const *bias,
-                              const float *const *resid, float *const *out, int K, int m, const float *x,
-                              const uint8_t *xq, const float *x2, const float *nw, float eps, int pro, bool pair,
-                              hipStream_t st);
+bool gemv_stream_take(int type, int K, int m, long long rows, int nmat, const uint8_t *const *w, int code,
+                      bool staged);
+hipError_t launch_gemv_stream(int type, int nmat, const uint8_t *const *w, const int *n_out,
+                              const float *const *bias, const float *const *resid, float *const *out, int K, int m,
+                              const float *x, const uint8_t *xq, const float *x2, const float *nw, float eps, int pro,
+                              bool pair, hipStream_t st);
 }  // namespace exq
 
 using namespace exq;
@@ -293,12 +294,12 @@ hipError_t launch_gemv_fused_layer(int type, int nmat, const uint8_t *const *w, 
         return hipErrorInvalidValue;
     // Q4_K rows at the decode lengths: the streaming kernel (one token: every
     // variant -- plain, prologues, residual, pairs, staged or Q8_K input;
-    // two to four tokens: plain projections of staged tokens), whose rows
-    // equal this kernel's bit for bit
+    // two to four tokens: plain projections of staged tokens), and one staged
+    // token of Q6_K rows of 9728; its rows equal this kernel's bit for bit
     long long rows = 0;
     for (int z = 0; z < nmat; ++z) rows += n_out[z];
-    if (gemv_stream_take(type, K, m, rows, nmat, w, x != nullptr && code == 0))
-        return launch_gemv_stream(nmat, w, n_out, bias, resid, out, K, m, x, xq, x2, nw, eps, pro, pair, st);
+    if (gemv_stream_take(type, K, m, rows, nmat, w, code, x != nullptr))
+        return launch_gemv_stream(type, nmat, w, n_out, bias, resid, out, K, m, x, xq, x2, nw, eps, pro, pair, st);
     a.nblk = q8_0_family(type) ? K / kQK8_0 : K / kQKK;
     a.U = q8_0_family(type) ? a.nblk : a.nblk * 4;
     // three waves per row: one-token K-quant launches (Q4_K, Q6_K)

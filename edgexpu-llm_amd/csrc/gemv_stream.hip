@@ -104,6 +104,19 @@ __device__ __forceinline__ void s_dma16_nt(uint32_t lds, uint32_t voff, const v4
         : "memory");
 }
 
+// One LDS DMA of 4 bytes per lane (lane L's dword lands at lds + 4 * L), non-temporal.
+__device__ __forceinline__ void s_dma4_nt(uint32_t lds, uint32_t voff, const v4u_t &rs, uint32_t soff) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "buffer_load_dword %2, %3, %4 offen nt lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(lds), "v"(voff), "s"(rs), "s"(soff)
+        : "memory");
+}
+
 template <int N>
 __device__ __forceinline__ void s_wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
@@ -216,17 +229,70 @@ __device__ __forceinline__ void act_from_blocks(const uint8_t *raw, int unit, Fm
     x.spair = ((uint32_t)s0 & 0xffffu) | ((uint32_t)s1 << 16);
 }
 
-template <int KSB, int NW, int NB, int FL, bool DEEP, int M = 1>
+// Q6_K rows in LDS: a row of 210-byte super-blocks starts 4-byte aligned in
+// its slot, so a super-block starts 2 mod 4 when its index is odd.  The
+// fields of a unit (16-byte quarter-rows A, B of the low nibbles, H of the
+// high bits, the 8 scale bytes of its half, d) share that offset.  Reads
+// take aligned dwords and join them with v_alignbyte (sh = 0 or 2 bytes).
+__device__ __forceinline__ uint32_t lds_u32(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
+__device__ __forceinline__ v4u_t lds16_a2(const uint8_t *q, uint32_t sh) {  // q 4-byte aligned
+    const uint32_t w0 = lds_u32(q), w1 = lds_u32(q + 4), w2 = lds_u32(q + 8), w3 = lds_u32(q + 12),
+                   w4 = lds_u32(q + 16);
+    return v4u_t{__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh),
+                 __builtin_amdgcn_alignbyte(w3, w2, sh), __builtin_amdgcn_alignbyte(w4, w3, sh)};
+}
+
+// One Q6_K unit's contribution with the roundings of FmtQ6K::dot1 from a
+// zero accumulator: fma(dx * d, isum, 0), isum = sum_k sc_k (dot_k - 32
+// bsum_k) exact in int32 (src/gguf_dot_q8.c:897-963).
+__device__ __forceinline__ float q6k_unit(v4u_t A4, v4u_t B4, v4u_t H4, uint32_t scx, uint32_t scy, uint32_t dbits,
+                                          int p, const FmtQ6K::Act &xa) {
+    const float d = f16_bits_to_f32(dbits);
+    int sc[4];
+    sc[0] = (int)(int8_t)((scx >> (8 * p)) & 0xffu);
+    sc[1] = (int)(int8_t)((scx >> (8 * (2 + p))) & 0xffu);
+    sc[2] = (int)(int8_t)((scy >> (8 * p)) & 0xffu);
+    sc[3] = (int)(int8_t)((scy >> (8 * (2 + p))) & 0xffu);
+    const uint32_t A[4] = {A4.x, A4.y, A4.z, A4.w};
+    const uint32_t B[4] = {B4.x, B4.y, B4.z, B4.w};
+    const uint32_t H[4] = {H4.x, H4.y, H4.z, H4.w};
+    uint32_t c[4][4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        c[0][v] = (A[v] & 0x0f0f0f0fu) | ((H[v] << 4) & 0x30303030u);
+        c[1][v] = (B[v] & 0x0f0f0f0fu) | ((H[v] << 2) & 0x30303030u);
+        c[2][v] = ((A[v] >> 4) & 0x0f0f0f0fu) | (H[v] & 0x30303030u);
+        c[3][v] = ((B[v] >> 4) & 0x0f0f0f0fu) | ((H[v] >> 2) & 0x30303030u);
+    }
+    int isum = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        int dk = 0;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) dk = sdot4(c[k][v], xa.q[4 * k + v], dk);
+        isum += sc[k] * (dk - xa.bs32[k]);
+    }
+    return fmaf(xa.dx * d, (float)isum, 0.0f);
+}
+
+template <int KSB, int NW, int NB, int FL, bool DEEP, int M = 1, int TYPE = kTypeQ4_K>
 struct StreamGeom {
+    static constexpr bool Q6 = TYPE == kTypeQ6_K;
     static constexpr int K = KSB * kQKK;
     static constexpr int U = 4 * KSB;                    // units per row
     static constexpr int T = (U + 63) / 64;              // units per lane
-    static constexpr int RB = KSB * kBytesQ4_K;          // row bytes
+    static constexpr int RB = KSB * (Q6 ? kBytesQ6_K : kBytesQ4_K);  // row bytes
     static constexpr int RPS = (FL & kSPair) ? 2 : 1;    // rows per step
-    static constexpr int SB = RPS * RB;                  // slot bytes
-    static constexpr int CH = RB / 1024;                 // whole 1 KB chunks per row
-    static constexpr int PL = (RB % 1024) / 16;          // lanes of the partial chunk
-    static constexpr int NI = RPS * (CH + (PL > 0 ? 1 : 0));  // DMA instructions per step
+    // Q4_K rows are whole 16-byte transfers.  A Q6_K row starts s = 0, 4, 8
+    // or 12 bytes past a 16-byte boundary: its slot takes the 16-byte
+    // transfers from that boundary that end inside the row (F of them, F
+    // depending on s), then 4-byte transfers of the rest; the row starts s
+    // bytes into its slot.
+    static constexpr int F_MIN = RB / 16, F_MAX = (RB + 12) / 16;
+    static constexpr int SB = Q6 ? ((RB + 16 + 15) & ~15) : RPS * RB;  // slot bytes
+    static constexpr int CH = (Q6 ? F_MIN * 16 : RB) / 1024;          // whole 1 KB chunks per row
+    static constexpr int PL = (RB % 1024) / 16;          // Q4_K: lanes of the partial chunk
+    static constexpr int NI = Q6 ? CH + 2 : RPS * (CH + (PL > 0 ? 1 : 0));  // DMA instructions per step
     static constexpr int NT = NW * 64;
     static constexpr int ROUNDS = (FL & kSXq) ? 0 : (M * KSB * 16 + NT - 1) / NT;  // staging rounds
     // staged activations of the M tokens: codes, block scales, 16-element sums
@@ -236,7 +302,10 @@ struct StreamGeom {
     // ring slots: NB steps in flight, NS at the start (DEEP: twice NB)
     static constexpr int NS = DEEP ? 2 * NB : NB;
     static constexpr size_t lds() { return (size_t)AREA + (size_t)NW * NS * SB; }
-    static_assert(RB % 16 == 0, "16-byte DMA lanes");
+    static_assert(Q6 ? (RB % 4 == 0 && F_MIN - 64 * CH >= 1 && F_MAX - 64 * CH <= 64)
+                     : RB % 16 == 0,
+                  "16-byte DMA lanes; Q6_K: one partial chunk of at least one lane");
+    static_assert(!Q6 || (FL & (kSPair | kSXq)) == 0, "Q6_K rows: staged activations, no pairs");
     static_assert(AREA + (size_t)NW * NS * SB + 8 * NW <= 160 * 1024, "the ring and the staging fit the gfx950 LDS");
     static_assert(ROUNDS <= 2, "the staging loads of at most two rounds are in flight at the start");
     static_assert(NS * NI + 8 * ((FL & 3) ? 2 : 1) <= 63, "vmcnt range");
@@ -244,9 +313,10 @@ struct StreamGeom {
     static_assert(M == 1 || FL == 0, "several tokens: plain projections of staged activations");
 };
 
-template <int KSB, int NW, int NB, int FL, bool DEEP, int M = 1>
+template <int KSB, int NW, int NB, int FL, bool DEEP, int M = 1, int TYPE = kTypeQ4_K>
 __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
-    using G = StreamGeom<KSB, NW, NB, FL, DEEP, M>;
+    using G = StreamGeom<KSB, NW, NB, FL, DEEP, M, TYPE>;
+    constexpr bool Q6 = G::Q6;
     constexpr int PRO = FL & 3;
     constexpr bool kRes = (FL & kSRes) != 0, kPair = (FL & kSPair) != 0, kXq = (FL & kSXq) != 0;
     constexpr int NS = G::NS;
@@ -282,6 +352,23 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
         const Mat m = locate(ok ? step : 0);
         const uint32_t so = ok ? (uint32_t)m.row * G::RB : 0u;
         const uint32_t vo = ok ? (uint32_t)lane * 16u : 0x7ff00000u;
+        if constexpr (Q6) {
+            // every transfer lies inside the row or the rows before it
+            const uint32_t sh = so & 15u, a0 = so - sh, end = sh + (uint32_t)G::RB;
+            const int F = (int)(end >> 4), tail = (int)((end & 15u) >> 2);
+            const v4u_t rs = s_rsrc(m.w, (uint32_t)m.n_out * G::RB);
+            const uint32_t dst = ring_lds + b * G::SB;
+#pragma unroll
+            for (int k = 0; k < G::CH; ++k) s_dma16_nt(dst + k * 1024, vo, rs, a0 + k * 1024);
+            if (lane < F - 64 * G::CH) s_dma16_nt(dst + G::CH * 1024, vo, rs, a0 + G::CH * 1024);
+            // the row's last 0-12 bytes as dwords; none left: lane 0 reloads the
+            // last dword of the 16-byte transfers past them (an issued
+            // instruction either way, so every wait counts NI per step)
+            const uint32_t t0 = 16u * (uint32_t)F;
+            const uint32_t vo4 = ok ? (uint32_t)lane * 4u : 0x7ff00000u;
+            if (lane < (tail > 0 ? tail : 1)) s_dma4_nt(dst + t0, vo4, rs, tail > 0 ? a0 + t0 : a0 + t0 - 4u);
+            return;
+        }
 #pragma unroll
         for (int r = 0; r < G::RPS; ++r) {
             const v4u_t rs = s_rsrc(r == 0 ? m.w : a.w[1], (uint32_t)m.n_out * G::RB);
@@ -389,9 +476,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     }
     // the lane's activation slices, scale selectors and row offsets
     const ActLds act{lq, ld, lbs, G::K, KSB};
-    FmtQ4K::Act xa[M][G::T];
+    using Act = std::conditional_t<Q6, FmtQ6K::Act, FmtQ4K::Act>;
+    Act xa[M][G::T];
     ScaleSel lc[G::T];
-    uint32_t hoff[G::T], qoff[G::T];
+    uint32_t hoff[G::T], qoff[G::T];  // Q6_K: the unit's aligned byte offset, its shift (0 or 2)
     bool live[G::T];
 #pragma unroll
     for (int t = 0; t < G::T; ++t) {
@@ -400,13 +488,21 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
         const int uc = min(u, G::U - 1);
         if constexpr (kXq) {
             act_from_blocks(smem, uc, xa[0][t]);
+        } else if constexpr (Q6) {
+            FmtQ6K::load_act_lds(act, uc, 0, xa[0][t]);
         } else {
 #pragma unroll
             for (int m = 0; m < M; ++m) FmtQ4K::load_act_lds(act, uc, m, xa[m][t]);
         }
-        lc[t] = scale_sel(uc & 3);
-        hoff[t] = (uint32_t)(uc >> 2) * kBytesQ4_K;
-        qoff[t] = hoff[t] + 16u + 32u * (uint32_t)(uc & 3);
+        if constexpr (Q6) {
+            const uint32_t sb = (uint32_t)(uc >> 2) * kBytesQ6_K;  // the unit's fields sit at sb + 4-byte multiples
+            hoff[t] = sb & ~3u;
+            qoff[t] = sb & 3u;  // v_alignbyte shift, bytes
+        } else {
+            lc[t] = scale_sel(uc & 3);
+            hoff[t] = (uint32_t)(uc >> 2) * kBytesQ4_K;
+            qoff[t] = hoff[t] + 16u + 32u * (uint32_t)(uc & 3);
+        }
     }
 
     // 3. the epilogue words of the lane's step (step first + lane * TW), loaded ahead of use
@@ -476,27 +572,59 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     //    of later steps that may stay in flight.
     auto step_partials = [&](auto wait_c, int slot, int k, float (&p)[M][G::RPS][G::T]) {
         s_wait_vm<decltype(wait_c)::value>();
-        const uint8_t *sb = ring + slot * G::SB;
-        v4u_t h[G::RPS][G::T], q0[G::RPS][G::T], q1[G::RPS][G::T];
-#pragma unroll
-        for (int r = 0; r < G::RPS; ++r)
+        if constexpr (Q6) {
+            // the row starts (row * RB) & 15 bytes into its slot
+            const int step = gw + k * TW;
+            const Mat m = locate(step < last ? step : 0);
+            const uint8_t *rb = ring + slot * G::SB + (((uint32_t)m.row * G::RB) & 15u);
+            v4u_t A[G::T], B[G::T], H[G::T];
+            uint32_t s0[G::T], s1[G::T], s2[G::T], dw[G::T];
 #pragma unroll
             for (int t = 0; t < G::T; ++t) {
-                h[r][t] = *reinterpret_cast<const v4u_t *>(sb + r * G::RB + hoff[t]);
-                q0[r][t] = *reinterpret_cast<const v4u_t *>(sb + r * G::RB + qoff[t]);
-                q1[r][t] = *reinterpret_cast<const v4u_t *>(sb + r * G::RB + qoff[t] + 16);
+                const int u = min(lane + 64 * t, G::U - 1), h = (u >> 1) & 1, pp = u & 1;
+                const uint8_t *q = rb + hoff[t];
+                A[t] = lds16_a2(q + 64 * h + 16 * pp, qoff[t]);
+                B[t] = lds16_a2(q + 64 * h + 32 + 16 * pp, qoff[t]);
+                H[t] = lds16_a2(q + 128 + 32 * h + 16 * pp, qoff[t]);
+                s0[t] = lds_u32(q + 192 + 8 * h);
+                s1[t] = lds_u32(q + 196 + 8 * h);
+                s2[t] = lds_u32(q + 200 + 8 * h);
+                dw[t] = lds_u32(q + 208);
             }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (k + NB >= NS) issue((slot + NB) % NS, gw + (k + NB) * TW);  // uniform; slot == k % NS
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (k + NB >= NS) issue((slot + NB) % NS, gw + (k + NB) * TW);  // uniform; slot == k % NS
 #pragma unroll
-        for (int m = 0; m < M; ++m)
+            for (int t = 0; t < G::T; ++t) {
+                const int u = min(lane + 64 * t, G::U - 1);
+                const uint32_t scx = __builtin_amdgcn_alignbyte(s1[t], s0[t], qoff[t]);
+                const uint32_t scy = __builtin_amdgcn_alignbyte(s2[t], s1[t], qoff[t]);
+                const uint32_t db = (dw[t] >> (8u * qoff[t])) & 0xffffu;
+                const float v = q6k_unit(A[t], B[t], H[t], scx, scy, db, u & 1, xa[0][t]);
+                p[0][0][t] = live[t] ? v : 0.0f;
+            }
+        } else {
+            const uint8_t *sb = ring + slot * G::SB;
+            v4u_t h[G::RPS][G::T], q0[G::RPS][G::T], q1[G::RPS][G::T];
 #pragma unroll
             for (int r = 0; r < G::RPS; ++r)
 #pragma unroll
                 for (int t = 0; t < G::T; ++t) {
-                    const float v = q4k_unit(h[r][t], q0[r][t], q1[r][t], xa[m][t], lc[t]);
-                    p[m][r][t] = live[t] ? v : 0.0f;
+                    h[r][t] = *reinterpret_cast<const v4u_t *>(sb + r * G::RB + hoff[t]);
+                    q0[r][t] = *reinterpret_cast<const v4u_t *>(sb + r * G::RB + qoff[t]);
+                    q1[r][t] = *reinterpret_cast<const v4u_t *>(sb + r * G::RB + qoff[t] + 16);
                 }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (k + NB >= NS) issue((slot + NB) % NS, gw + (k + NB) * TW);  // uniform; slot == k % NS
+#pragma unroll
+            for (int m = 0; m < M; ++m)
+#pragma unroll
+                for (int r = 0; r < G::RPS; ++r)
+#pragma unroll
+                    for (int t = 0; t < G::T; ++t) {
+                        const float v = q4k_unit(h[r][t], q0[r][t], q1[r][t], xa[m][t], lc[t]);
+                        p[m][r][t] = live[t] ? v : 0.0f;
+                    }
+        }
     };
     int k64 = 0, first = gw;
     auto advance = [&]() {
@@ -572,7 +700,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     if (k64 > 0) flush(first, k64, epi);
 }
 
-template <int KSB, int NW, int NB, int FL, int M = 1>
+template <int KSB, int NW, int NB, int FL, int M = 1, int TYPE = kTypeQ4_K>
 hipError_t launch_stream(const StreamArgs &a, hipStream_t st) {
     // one workgroup per CU: the grid covers the chip once and every wave
     // strides over the rows.  Launches of at most three steps per wave fill
@@ -584,15 +712,29 @@ hipError_t launch_stream(const StreamArgs &a, hipStream_t st) {
     const long long steps = ((long long)a.nrows + (long long)grid * NW - 1) / ((long long)grid * NW);
     if constexpr (KSB <= 16) {
         if (steps <= 3) {
-            using G = StreamGeom<KSB, NW, NB, FL, true, M>;
-            hipLaunchKernelGGL((gemv_stream_q4k<KSB, NW, NB, FL, true, M>), dim3(grid), dim3(NW * 64), G::lds(), st,
-                               a);
+            using G = StreamGeom<KSB, NW, NB, FL, true, M, TYPE>;
+            hipLaunchKernelGGL((gemv_stream_q4k<KSB, NW, NB, FL, true, M, TYPE>), dim3(grid), dim3(NW * 64), G::lds(),
+                               st, a);
             return hipGetLastError();
         }
     }
-    using G = StreamGeom<KSB, NW, NB, FL, false, M>;
-    hipLaunchKernelGGL((gemv_stream_q4k<KSB, NW, NB, FL, false, M>), dim3(grid), dim3(NW * 64), G::lds(), st, a);
+    using G = StreamGeom<KSB, NW, NB, FL, false, M, TYPE>;
+    hipLaunchKernelGGL((gemv_stream_q4k<KSB, NW, NB, FL, false, M, TYPE>), dim3(grid), dim3(NW * 64), G::lds(), st,
+                       a);
     return hipGetLastError();
+}
+
+// Q6_K rows: one token, staged activations; prologues and the residual as for Q4_K.
+template <int KSB, int NW, int NB>
+hipError_t launch_stream_q6k(int fl, const StreamArgs &a, hipStream_t st) {
+    switch (fl) {
+        case 0: return launch_stream<KSB, NW, NB, 0, 1, kTypeQ6_K>(a, st);
+        case 1: return launch_stream<KSB, NW, NB, 1, 1, kTypeQ6_K>(a, st);
+        case 2: return launch_stream<KSB, NW, NB, 2, 1, kTypeQ6_K>(a, st);
+        case kSRes: return launch_stream<KSB, NW, NB, kSRes, 1, kTypeQ6_K>(a, st);
+        case 2 | kSRes: return launch_stream<KSB, NW, NB, 2 | kSRes, 1, kTypeQ6_K>(a, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 // Plain projections of m = 2..4 staged tokens (rows of 2560 or 4096).
@@ -632,11 +774,18 @@ int gemv_stream_mode() { return g_gemv_mode; }
 
 // True when the streaming GEMV can take (type, K, m): one token of Q4_K rows
 // of 2560, 4096 or 14336 elements.
-// m = 2..4 tokens: rows of 2560 or 4096, plain projections of f32 tokens.
-bool gemv_stream_supported(int type, int K, int m, bool plain_staged) {
-    if (type != kTypeQ4_K) return false;
-    if (m == 1) return K == 2560 || K == 4096 || K == 14336;
-    return m >= 2 && m <= 4 && plain_staged && (K == 2560 || K == 4096);
+// code: prologue (bits 0-1), residual (4), gate/up pairs (8); staged: f32
+// tokens (not Q8_K block bytes).  Q4_K: one token of rows of 2560, 4096 or
+// 14336, or plain projections of m = 2..4 staged tokens of rows of 2560 or
+// 4096.  Q6_K: one staged token of rows of 9728 (the hybrid ~4B down
+// projection), no pairs.
+bool gemv_stream_supported(int type, int K, int m, int code, bool staged) {
+    if (type == kTypeQ4_K) {
+        if (m == 1) return K == 2560 || K == 4096 || K == 14336;
+        return m >= 2 && m <= 4 && staged && code == 0 && (K == 2560 || K == 4096);
+    }
+    if (type == kTypeQ6_K) return m == 1 && staged && (code & 8) == 0 && K == 9728;
+    return false;
 }
 
 // True when the streaming GEMV runs a launch of `rows` rows (pairs: gate and
@@ -648,12 +797,15 @@ bool gemv_stream_supported(int type, int K, int m, bool plain_staged) {
 // against 8.8 at 2048, 11.2 against 12.4 at 4096).
 // The rows go to LDS as 16-byte DMA transfers from 16-byte-aligned
 // addresses, so every matrix must start at one; others take the fused kernel.
-// plain_staged: f32 tokens, no prologue, residual or pairs.
-bool gemv_stream_take(int type, int K, int m, long long rows, int nmat, const uint8_t *const *w, bool plain_staged) {
-    if (!gemv_stream_supported(type, K, m, plain_staged) || g_gemv_mode == 1) return false;
+bool gemv_stream_take(int type, int K, int m, long long rows, int nmat, const uint8_t *const *w, int code,
+                      bool staged) {
+    if (!gemv_stream_supported(type, K, m, code, staged) || g_gemv_mode == 1) return false;
     for (int z = 0; z < nmat; ++z)
         if (((uintptr_t)w[z] & 15u) != 0) return false;
     if (g_gemv_mode == 2) return true;
+    // Q6_K rows of 9728 from 2048 rows (measured: 10.2 against 11.4 us at
+    // 2560 rows, 18.9 against 25.1 at 9728; 7.4 against 6.5 at 1024)
+    if (type == kTypeQ6_K) return rows >= 2048;
     const long long bytes = rows * (long long)(K / kQKK) * kBytesQ4_K;
     return K != 14336 || bytes >= kStreamMinBytes14336;
 }
@@ -663,14 +815,14 @@ bool gemv_stream_take(int type, int K, int m, long long rows, int nmat, const ui
 // the prologue pro: 1 RMSNorm with nw / eps, 2 SiLU-mul with x2) or xq (Q8_K
 // block bytes); resid (per matrix, may be null) added after the bias; pair:
 // nmat = 2 (gate, up), out[0] = silu(gate) * up.
-hipError_t launch_gemv_stream(int nmat, const uint8_t *const *w, const int *n_out, const float *const *bias,
-                              const float *const *resid, float *const *out, int K, int m, const float *x,
-                              const uint8_t *xq, const float *x2, const float *nw, float eps, int pro, bool pair,
-                              hipStream_t st) {
+hipError_t launch_gemv_stream(int type, int nmat, const uint8_t *const *w, const int *n_out,
+                              const float *const *bias, const float *const *resid, float *const *out, int K, int m,
+                              const float *x, const uint8_t *xq, const float *x2, const float *nw, float eps, int pro,
+                              bool pair, hipStream_t st) {
     bool any_resid = false;
     for (int z = 0; z < nmat && resid != nullptr; ++z) any_resid = any_resid || resid[z] != nullptr;
-    const bool plain_staged = x != nullptr && pro == 0 && !pair && !any_resid;
-    if (!gemv_stream_supported(kTypeQ4_K, K, m, plain_staged) || nmat < 1 || nmat > kStreamMaxMats)
+    const int code = (pro & 3) | (any_resid ? kSRes : 0) | (pair ? kSPair : 0);
+    if (!gemv_stream_supported(type, K, m, code, x != nullptr) || nmat < 1 || nmat > kStreamMaxMats)
         return hipErrorInvalidValue;
     if ((x == nullptr) == (xq == nullptr) || (xq != nullptr && (pro != 0 || pair))) return hipErrorInvalidValue;
     if (pair && (nmat != 2 || n_out[0] != n_out[1])) return hipErrorInvalidValue;
@@ -701,6 +853,10 @@ hipError_t launch_gemv_stream(int nmat, const uint8_t *const *w, const int *n_ou
     a.eps = eps;
     if (any_res && pair) return hipErrorInvalidValue;
     const int fl = xq != nullptr ? kSXq : ((pro & 3) | (any_res ? kSRes : 0) | (pair ? kSPair : 0));
+    // Q6_K rows of 9728 (8 KB): one slot per wave, no deep start (measured on
+    // [2560 x 9728]: 10.2 us; a deep start 11.6, two slots 11.9, 12 waves
+    // per CU 10.2 but 13.2 at 4096 rows)
+    if (type == kTypeQ6_K) return launch_stream_q6k<38, 8, 1>(fl, a, st);
     if (m > 1) return K == 2560 ? launch_stream_tokens<10>(m, a, st) : launch_stream_tokens<16>(m, a, st);
     // measured on the Llama-3-8B / hybrid decode shapes: 8 waves per CU, two
     // slots per wave, one slot where a row is 8 KB (K = 14336: two, 12.7

@@ -1,7 +1,8 @@
 """The two decode GEMV kernels for one token of Q4_K rows agree bit for bit.
 
 One token of Q4_K rows of 2560, 4096 or 14336 elements (or two to four
-tokens of rows of 2560 or 4096, plain projections) runs on either the
+tokens of rows of 2560 or 4096, plain projections), or of Q6_K rows of 9728,
+runs on either the
 fused kernel (csrc/gemv_fused_kernel.h) or the streaming kernel
 (csrc/gemv_stream.hip: rows through LDS by DMA), chosen by launch size
 (edgexpu_hip_set_gemv_mode).  Both compute each lane's unit partial with the
@@ -169,6 +170,53 @@ def test_tokens_fused_equals_stream(hipdev, ora, n_in, n_outs, m):
         if biases[z] is not None:
             S = S + np.abs(biases[z][sample])[None, :]
         assert np.all(np.abs(s[z][:, sample] - want) <= TOL * S), f"matrix {z}"
+
+
+def cond6(ora, w, x):
+    """S_i of Q6_K rows against one token's Q8_K codes (float64)."""
+    xq = ora.quantize_q8_k(x[0])
+    return np.array([npref.q8_dot_f64(14, w[i], xq)[1] for i in range(w.shape[0])])[None, :]
+
+
+@pytest.mark.parametrize("n_outs", [(2560,), (2560, 2560), (77,), (1, 3000), (4097,)])
+def test_q6k_fused_equals_stream(hipdev, ora, n_outs):
+    """One token of Q6_K rows of 9728 (the hybrid ~4B down projection): rows
+    of 210-byte super-blocks start 4-byte aligned in the stream's slots and
+    are read with byte shifts; every output equals the fused kernel's bit for
+    bit and the oracle's within 1e-5 of its conditioning scale."""
+    n_in = 9728
+    rng = np.random.default_rng(6000 + sum(n_outs))
+    ws = [synth.np_weights(14, n, n_in, rng) for n in n_outs]
+    x = synth.np_activations(1, n_in, rng)
+    biases = [rng.normal(0, 0.3, n).astype(np.float32) if z % 2 == 0 else None for z, n in enumerate(n_outs)]
+    wd = [dev(w) for w in ws]
+    bd = [None if b is None else dev(b) for b in biases]
+    f, s = both(hipdev, lambda: E.linear_quant_group(wd, 14, dev(x), list(n_outs), n_in, biases=bd))
+    for z, n in enumerate(n_outs):
+        assert np.array_equal(bits(f[z]), bits(s[z])), f"matrix {z}"
+        sample = np.unique(np.concatenate([np.arange(min(n, 40)), np.arange(max(0, n - 8), n)]))
+        want = ora.linear_quant_batch(x, ws[z][sample], 14, None if biases[z] is None else biases[z][sample], 1,
+                                      len(sample), n_in)
+        S = cond6(ora, ws[z][sample], x) + (0 if biases[z] is None else np.abs(biases[z][sample]))
+        assert np.all(np.abs(s[z][:, sample] - want) <= TOL * S), f"matrix {z}"
+
+
+@pytest.mark.parametrize("pro", ["rmsnorm", "silu_mul", "silu_mul_residual", "residual"])
+def test_q6k_layer_variants_fused_equals_stream(hipdev, ora, pro):
+    """The Q6_K down projection as a layer issues it (SiLU-mul prologue and
+    residual) and the other staging variants: the two kernels agree."""
+    n_in, n_out = 9728, 2560
+    rng = np.random.default_rng(6100 + len(pro))
+    w = dev(synth.np_weights(14, n_out, n_in, rng))
+    x = dev((rng.normal(0, 1, (1, n_in)) * 2).astype(np.float32))
+    x2 = dev(rng.normal(0, 2, (1, n_in)).astype(np.float32))
+    nw = dev(rng.normal(1, 0.2, n_in).astype(np.float32))
+    res = dev(rng.normal(0, 4, (1, n_out)).astype(np.float32))
+    bias = [dev(rng.normal(0, 0.5, n_out).astype(np.float32))]
+    kw = {"rmsnorm": dict(norm_weight=nw, eps=1e-5), "silu_mul": dict(x2=x2),
+          "silu_mul_residual": dict(x2=x2, residuals=[res]), "residual": dict(residuals=[res])}[pro]
+    f, s = both(hipdev, lambda: E.layer_linear([w], 14, x, (n_out,), n_in, biases=bias, **kw))
+    assert np.array_equal(bits(f[0]), bits(s[0]))
 
 
 def test_gemv_mode_switch(hipdev):
