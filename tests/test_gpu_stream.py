@@ -172,6 +172,27 @@ def test_tokens_fused_equals_stream(hipdev, ora, n_in, n_outs, m):
         assert np.all(np.abs(s[z][:, sample] - want) <= TOL * S), f"matrix {z}"
 
 
+@pytest.mark.parametrize("m", [1, 2])
+def test_more_than_64_steps_per_wave(hipdev, ora, m):
+    """A launch long enough that every wave takes more than 64 rows: the
+    totals kept in lanes are flushed every 64 steps and the bias prefetched
+    again, then a partial flush at the end (131 849 rows of 2560: 64 full
+    steps of the 2048 waves of 256 CUs, and 777 rows more)."""
+    n_in, n_out = 2560, 2048 * 64 + 777
+    rng = np.random.default_rng(64 + m)
+    w = synth.np_weights(12, n_out, n_in, rng)
+    x = synth.np_activations(m, n_in, rng)
+    bias = rng.normal(0, 0.3, n_out).astype(np.float32)
+    wd, bd = dev(w), dev(bias)
+    f, s = both(hipdev, lambda: [E.linear_quant_batch(wd, 12, dev(x), n_out, n_in, bias=bd)])
+    assert np.array_equal(bits(f[0]), bits(s[0]))
+    sample = np.unique(np.concatenate([np.arange(0, n_out, 997), np.arange(n_out - 40, n_out),
+                                       np.arange(2048 * 63, 2048 * 63 + 40), np.arange(2048 * 64 - 20, 2048 * 64 + 20)]))
+    want = ora.linear_quant_batch(x, w[sample], 12, bias[sample], m, len(sample), n_in)
+    S = np.stack([cond(ora, w[sample], x[t:t + 1])[0] for t in range(m)]) + np.abs(bias[sample])[None, :]
+    assert np.all(np.abs(s[0][:, sample] - want) <= TOL * S)
+
+
 def cond6(ora, w, x):
     """S_i of Q6_K rows against one token's Q8_K codes (float64)."""
     xq = ora.quantize_q8_k(x[0])
