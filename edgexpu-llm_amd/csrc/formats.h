@@ -35,7 +35,6 @@ struct GemvArgs {
     const uint8_t *xq;
     size_t xq_stride;
     const float *xf;         // [m][K] f32 activations (f32 path)
-    const float *xs;         // [m][K/16] 16-element sums of x (f32 path)
     const float *bias;       // [n_out] or null
     float *out;              // [m][ldo]
     int ldo;
@@ -444,6 +443,16 @@ struct FmtQ5K {
 
 // ------------------------------------------------------------ f32 activations
 
+// Sum of 16 consecutive activation floats in a fixed order: four pairs of
+// pairs, accumulated from 0 (the 16-element sums the f32 K-quant dots take
+// for their min / offset terms).
+__device__ __forceinline__ float sum16(const float *x) {
+    float s = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) s += (x[4 * v] + x[4 * v + 1]) + (x[4 * v + 2] + x[4 * v + 3]);
+    return s;
+}
+
 // Q4_K weights against f32 activations (logits path, dot_q4_k).
 // Unit = (super-block i, 64-chunk j); the activation slice is 64 floats.
 struct FmtQ4KF32 {
@@ -452,7 +461,7 @@ struct FmtQ4KF32 {
         float x[64];
         float sx0, sx1;   // sums of x over sub-blocks 2j and 2j+1
     };
-    template <class A>  // GemvArgs or FusedArgs: a.xf, a.xs, a.K
+    template <class A>  // GemvArgs or FusedArgs: a.xf, a.K
     __device__ static void load_act(const A &a, int unit, int tk, Act &x) {
         const int i = unit >> 2, j = unit & 3;
         const float4 *p = reinterpret_cast<const float4 *>(a.xf + (size_t)tk * a.K + 256 * i + 64 * j);
@@ -461,9 +470,8 @@ struct FmtQ4KF32 {
             const float4 t = p[v];
             x.x[4 * v] = t.x; x.x[4 * v + 1] = t.y; x.x[4 * v + 2] = t.z; x.x[4 * v + 3] = t.w;
         }
-        const float *s = a.xs + (size_t)tk * (a.K / 16) + 16 * i + 4 * j;
-        x.sx0 = s[0] + s[1];
-        x.sx1 = s[2] + s[3];
+        x.sx0 = sum16(x.x) + sum16(x.x + 16);
+        x.sx1 = sum16(x.x + 32) + sum16(x.x + 48);
     }
     using W = FmtQ4K::W;
     template <class A>
@@ -518,7 +526,7 @@ struct FmtQ6KF32 {
         float x[64];      // [k][16]
         float sx[4];      // sums of x per sub-block 8h+2k+p
     };
-    template <class A>  // GemvArgs or FusedArgs: a.xf, a.xs, a.K
+    template <class A>  // GemvArgs or FusedArgs: a.xf, a.K
     __device__ static void load_act(const A &a, int unit, int tk, Act &x) {
         const int i = unit >> 2, h = (unit >> 1) & 1, p = unit & 1;
         const float *base = a.xf + (size_t)tk * a.K + 256 * i + 128 * h + 16 * p;
@@ -532,9 +540,8 @@ struct FmtQ6KF32 {
                 x.x[16 * k + 4 * v + 2] = t.z; x.x[16 * k + 4 * v + 3] = t.w;
             }
         }
-        const float *s = a.xs + (size_t)tk * (a.K / 16) + 16 * i + 8 * h + p;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) x.sx[k] = s[2 * k];
+        for (int k = 0; k < 4; ++k) x.sx[k] = sum16(x.x + 16 * k);
     }
     using W = FmtQ6K::W;
     template <class A>
@@ -586,7 +593,7 @@ struct FmtQ80F32 {
     struct Act {
         float x[32];
     };
-    template <class A>  // GemvArgs or FusedArgs: a.xf, a.xs, a.K
+    template <class A>  // GemvArgs or FusedArgs: a.xf, a.K
     __device__ static void load_act(const A &a, int unit, int tk, Act &x) {
         const float4 *p = reinterpret_cast<const float4 *>(a.xf + (size_t)tk * a.K + 32 * unit);
 #pragma unroll

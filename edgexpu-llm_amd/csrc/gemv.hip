@@ -179,11 +179,9 @@ hipError_t launch_gemv_q8(int type, const uint8_t *w, size_t row_bytes, int n_ou
 }
 
 // f32-activation GEMV over m <= 8 rows of x (logits path, F16 rows, the
-// per-row f32 dots).  xs holds the 16-element sums of x ([m][K/16]); read
-// only by the K-quant formats.  F16 rows need K % 32 == 0.
+// per-row f32 dots).  F16 rows need K % 32 == 0.
 hipError_t launch_gemv_f32(int type, const uint8_t *w, size_t row_bytes, int n_out, int K, int m,
-                           const float *xf, const float *xs, const float *bias, float *out, int ldo,
-                           hipStream_t st) {
+                           const float *xf, const float *bias, float *out, int ldo, hipStream_t st) {
     GemvArgs a{};
     a.w = w;
     a.row_bytes = row_bytes;
@@ -191,7 +189,6 @@ hipError_t launch_gemv_f32(int type, const uint8_t *w, size_t row_bytes, int n_o
     a.K = K;
     a.m = m;
     a.xf = xf;
-    a.xs = xs;
     a.bias = bias;
     a.out = out;
     a.ldo = ldo;
@@ -205,28 +202,6 @@ hipError_t launch_gemv_f32(int type, const uint8_t *w, size_t row_bytes, int n_o
         case kTypeQ6_K: a.nblk = K / kQKK; return launch_m<FmtQ6KF32>(a, st);
         default: return hipErrorInvalidValue;
     }
-}
-
-// 16-element sums of f32 activations: xs[t][g] = sum_{e<16} x[t][16g+e].
-__global__ __launch_bounds__(256) void xsum16_kernel(const float *__restrict__ x, int m, int K,
-                                                     float *__restrict__ xs) {
-    const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long total = (long long)m * (K / 16);
-    if (g >= total) return;
-    const float4 *p = reinterpret_cast<const float4 *>(x + g * 16);
-    float s = 0.0f;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        const float4 t = p[v];
-        s += (t.x + t.y) + (t.z + t.w);
-    }
-    xs[g] = s;
-}
-
-hipError_t launch_xsum16(const float *x, int m, int K, float *xs, hipStream_t st) {
-    const long long total = (long long)m * (K / 16);
-    hipLaunchKernelGGL(xsum16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, x, m, K, xs);
-    return hipGetLastError();
 }
 
 // Greedy argmax over scores with the reference's rules (src/native.c:2355-2396):

@@ -50,8 +50,7 @@ bool gemv_fused_f32_supported(int type, int K) {
     return L.total() <= 64 * 1024;
 }
 
-// One token of f32 activations xf (with 16-element sums xs for the K-quants)
-// against one matrix: the logits product (src/native.c:445-462).  Rows per
+// One token of f32 activations xf against one matrix: the logits product (src/native.c:445-462).  Rows per
 // slot R = 1 or 2 (the activation slice takes the registers of larger R).
 namespace {
 // The f32 logits launch with the argmax epilogue: the same shapes and
@@ -65,7 +64,7 @@ hipError_t launch_argmax_fmt(FusedArgs a, hipStream_t st, int *nparts) {
 }  // namespace
 
 hipError_t launch_gemv_fused_f32_argmax(int type, const uint8_t *w, int n_out, const float *bias, float *out,
-                                        size_t row_bytes, int K, const float *xf, const float *xs, hipStream_t st,
+                                        size_t row_bytes, int K, const float *xf, hipStream_t st,
                                         unsigned long long *amax, int *nparts) {
     FusedArgs a{};
     a.amax_cap = kFusedArgmaxParts;
@@ -78,7 +77,6 @@ hipError_t launch_gemv_fused_f32_argmax(int type, const uint8_t *w, int n_out, c
     a.K = K;
     a.m = 1;
     a.xf = xf;
-    a.xs = xs;
     a.amax = amax;
     a.nblk = type == kTypeQ8_0 ? K / kQK8_0 : K / kQKK;
     a.U = type == kTypeQ8_0 ? a.nblk : a.nblk * 4;
@@ -143,11 +141,10 @@ hipError_t launch_gemv_fused_q8_0_argmax(const uint8_t *w, int n_out, const floa
 // With amax non-null (at least kFusedArgmaxParts keys) the launch also
 // writes one greedy-argmax key per workgroup there and *nparts the count.
 hipError_t launch_gemv_fused_f32(int type, const uint8_t *w, int n_out, const float *bias, float *out,
-                                 size_t row_bytes, int K, const float *xf, const float *xs, hipStream_t st,
-                                 unsigned long long *amax, int *nparts) {
+                                 size_t row_bytes, int K, const float *xf, hipStream_t st, unsigned long long *amax,
+                                 int *nparts) {
     if (!gemv_fused_f32_supported(type, K)) return hipErrorInvalidValue;
-    if (amax != nullptr) return launch_gemv_fused_f32_argmax(type, w, n_out, bias, out, row_bytes, K, xf, xs, st, amax,
-                                                             nparts);
+    if (amax != nullptr) return launch_gemv_fused_f32_argmax(type, w, n_out, bias, out, row_bytes, K, xf, st, amax, nparts);
     FusedArgs a{};
     a.nmat = 1;
     a.w[0] = w;
@@ -158,7 +155,6 @@ hipError_t launch_gemv_fused_f32(int type, const uint8_t *w, int n_out, const fl
     a.K = K;
     a.m = 1;
     a.xf = xf;
-    a.xs = xs;
     a.nblk = type == kTypeQ8_0 ? K / kQK8_0 : K / kQKK;
     a.U = type == kTypeQ8_0 ? a.nblk : a.nblk * 4;
     if (!pick_fused_shape(a.U, a.G, a.KS)) return hipErrorInvalidValue;
@@ -190,13 +186,12 @@ hipError_t launch_gemv_fused_f32(int type, const uint8_t *w, int n_out, const fl
 #undef EXQ_F32_LAUNCH
 }
 
-// Two tokens of f32 activations (xf, xs at token strides K and K / 16)
-// against one K-quant matrix, outputs at out and out + n_out: the weights are
+// Two tokens of f32 activations (xf, token stride K) against one K-quant matrix, outputs at out and out + n_out: the weights are
 // read once for both.  Each score equals the one-token launch's bit for bit
 // (the same lane partials, summed by the same reduction tree whichever value
 // slot holds them).
 hipError_t launch_gemv_fused_f32_pair(int type, const uint8_t *w, int n_out, const float *bias, float *out,
-                                      size_t row_bytes, int K, const float *xf, const float *xs, hipStream_t st) {
+                                      size_t row_bytes, int K, const float *xf, hipStream_t st) {
     if ((type != kTypeQ4_K && type != kTypeQ6_K) || !gemv_fused_f32_supported(type, K)) return hipErrorInvalidValue;
     FusedArgs a{};
     a.nmat = 1;
@@ -208,7 +203,6 @@ hipError_t launch_gemv_fused_f32_pair(int type, const uint8_t *w, int n_out, con
     a.K = K;
     a.m = 2;
     a.xf = xf;
-    a.xs = xs;
     a.nblk = K / kQKK;
     a.U = a.nblk * 4;
     if (!pick_fused_shape(a.U, a.G, a.KS)) return hipErrorInvalidValue;

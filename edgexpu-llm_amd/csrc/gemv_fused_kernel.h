@@ -49,7 +49,6 @@ struct FusedArgs {
     const uint8_t *xq;     // or: activations already quantized, reference block bytes
     size_t xq_stride;      //     (Q8_0: 34 B per 32, Q8_K: 292 B per 256), token t at xq + t*xq_stride
     const float *xf;       // or (f32-activation formats): x [m][K] f32
-    const float *xs;       //     and its 16-element sums [m][K/16]
     const float *resid[kFusedMaxMats];  // added to each output after its bias ([m][n_out[z]]; null: none)
     const float *x2;       // SiLU-mul prologue: the staged activation is silu(x) * x2
     const float *nw;       // RMSNorm prologue: the staged activation is rmsnorm(x; nw, eps)

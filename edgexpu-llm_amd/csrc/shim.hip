@@ -24,10 +24,9 @@ hipError_t launch_dequantize_rows(const uint8_t *table, int type, long long n_ro
 hipError_t launch_gemv_q8(int type, const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const uint8_t *xq,
                           size_t xq_stride, const float *bias, float *out, int ldo, hipStream_t st);
 hipError_t launch_gemv_f32(int type, const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const float *xf,
-                           const float *xs, const float *bias, float *out, int ldo, hipStream_t st);
+                           const float *bias, float *out, int ldo, hipStream_t st);
 hipError_t launch_gemv_plain(int type, const uint8_t *w, size_t row_bytes, int n_out, int K, int m, const float *x,
                              int ldx, const float *bias, bool bias_f64, float *out, int ldo, hipStream_t st);
-hipError_t launch_xsum16(const float *x, int m, int K, float *xs, hipStream_t st);
 hipError_t launch_rmsnorm(const float *x, const float *w, float *out, int m, int n, float eps, hipStream_t st);
 hipError_t launch_elementwise(const float *a, const float *b, float *out, long long n, int kind, hipStream_t st);
 hipError_t launch_argmax_rows(const float *s, int m, int n, size_t lds, unsigned long long *partial, uint32_t *best,
@@ -68,10 +67,10 @@ hipError_t launch_gemv_fused_layer(int type, int nmat, const uint8_t *const *w, 
                                    size_t row_bytes, int K, int m, const float *x, const float *x2, const float *nw,
                                    float eps, int pro, const uint8_t *xq, size_t xq_stride, hipStream_t st);
 hipError_t launch_gemv_fused_f32(int type, const uint8_t *w, int n_out, const float *bias, float *out,
-                                 size_t row_bytes, int K, const float *xf, const float *xs, hipStream_t st,
+                                 size_t row_bytes, int K, const float *xf, hipStream_t st,
                                  unsigned long long *amax = nullptr, int *nparts = nullptr);
 hipError_t launch_gemv_fused_f32_pair(int type, const uint8_t *w, int n_out, const float *bias, float *out,
-                                      size_t row_bytes, int K, const float *xf, const float *xs, hipStream_t st);
+                                      size_t row_bytes, int K, const float *xf, hipStream_t st);
 hipError_t launch_gemv_fused_q8_0_argmax(const uint8_t *w, int n_out, const float *bias, float *out,
                                          size_t row_bytes, int K, const float *x, hipStream_t st,
                                          unsigned long long *amax, int *nparts);
@@ -134,7 +133,7 @@ struct State {
 State g;
 
 // Fixed device scratch of edgexpu_hip_logits_noalloc_dev: the quantized
-// hidden vectors, their 16-element sums and the argmax partial keys of up to
+// hidden vectors and the argmax partial keys of up to
 // kGemvMaxTokens vectors of kScratchMaxEmbd elements (each GPU the library
 // runs on holds its own copy until the process ends).  Host code never hands
 // `scratch` itself to a kernel: its device address comes from
@@ -142,7 +141,6 @@ State g;
 constexpr int kScratchMaxEmbd = 16384;
 constexpr size_t kScratchBytes =
     ((size_t)kGemvMaxTokens * (kScratchMaxEmbd / kQKK) * kBytesQ8_K + 255) / 256 * 256 +  // Q8_K (> Q8_0) codes
-    (size_t)kGemvMaxTokens * (kScratchMaxEmbd / 16) * sizeof(float) +                    // 16-element sums
     (size_t)kGemvMaxTokens * kArgmaxParts * sizeof(unsigned long long);                  // argmax keys
 static_assert(kScratchBytes <= 512 * 1024, "a modest fixed scratch");
 constexpr int kMaxDevices = 64;
@@ -410,30 +408,27 @@ bool use_exact_gemm(uint32_t type, int nmat, const void *const *w, const int *n_
 // Workspace carve-up for m tokens of K elements.
 struct ActWs {
     uint8_t *xq;               // m * act_bytes   quantized activations
-    float *xs;                 // m * K/16        16-element sums of f32 x (f32 logits path)
     unsigned long long *keys;  // m * 4096        argmax partials
 };
 
-// Byte sizes of the three parts, each a multiple of 256.
-void act_ws_sizes(uint32_t type, int m, int K, size_t &qb, size_t &sb, size_t &kb) {
+// Byte sizes of the two parts, each a multiple of 256.
+void act_ws_sizes(uint32_t type, int m, int K, size_t &qb, size_t &kb) {
     qb = align_up((size_t)m * act_bytes(type, K), 256);
-    sb = align_up((size_t)m * (K / 16) * sizeof(float), 256);
     kb = align_up((size_t)m * kArgmaxParts * sizeof(unsigned long long), 256);
 }
 
-// The three parts carved out of base (256-byte aligned).
+// The two parts carved out of base (256-byte aligned).
 void act_ws_carve(uint32_t type, int m, int K, uint8_t *base, ActWs &a) {
-    size_t qb, sb, kb;
-    act_ws_sizes(type, m, K, qb, sb, kb);
+    size_t qb, kb;
+    act_ws_sizes(type, m, K, qb, kb);
     a.xq = base;
-    a.xs = (float *)(base + qb);
-    a.keys = (unsigned long long *)(base + qb + sb);
+    a.keys = (unsigned long long *)(base + qb);
 }
 
 bool act_ws(uint32_t type, int m, int K, ActWs &a) {
-    size_t qb, sb, kb;
-    act_ws_sizes(type, m, K, qb, sb, kb);
-    uint8_t *base = (uint8_t *)workspace(qb + sb + kb);
+    size_t qb, kb;
+    act_ws_sizes(type, m, K, qb, kb);
+    uint8_t *base = (uint8_t *)workspace(qb + kb);
     if (base == nullptr) return false;
     act_ws_carve(type, m, K, base, a);
     return true;
@@ -475,12 +470,11 @@ bool check_weight_align(const void *w, uint32_t type, const char *who) {
 // f32-activation products (F16 and F32 rows in the batch driver; every type
 // in the per-row f32 dot and the logits of the non-Q8_0 formats): at most
 // kGemvMaxTokens tokens per launch of the generic kernels, or the fused
-// kernel one token at a time for the K-quant formats it covers.  xs: the
-// tokens' 16-element sums of x (K-quants only).  bias_f64: F32 rows add the
+// kernel one token at a time for the K-quant formats it covers.  bias_f64: F32 rows add the
 // bias in double before the final rounding (the one-token linear of
 // src/cpu_kernel.c:566-569, 462-523).
-bool run_f32_product(uint32_t type, const void *w, int n_out, int n_in, int m, const float *x, const float *xs,
-                     const float *bias, float *out, int ldo, hipStream_t st, bool bias_f64 = false) {
+bool run_f32_product(uint32_t type, const void *w, int n_out, int n_in, int m, const float *x, const float *bias,
+                     float *out, int ldo, hipStream_t st, bool bias_f64 = false) {
     const size_t rb = edgexpu_hip_row_bytes(type, n_in);
     if (type == (uint32_t)kTypeF32 || (type == (uint32_t)kTypeF16 && n_in % 32 != 0)) {
         for (int t0 = 0; t0 < m; t0 += kGemvMaxTokens) {
@@ -498,12 +492,12 @@ bool run_f32_product(uint32_t type, const void *w, int n_out, int n_in, int m, c
         const bool pairs = type == (uint32_t)kTypeQ4_K || type == (uint32_t)kTypeQ6_K;
         for (int t = 0; t < m;) {
             const int mt = pairs && m - t >= 2 ? 2 : 1;
-            const float *xt = x + (size_t)t * n_in, *st_ = xs + (size_t)t * (n_in / 16);
+            const float *xt = x + (size_t)t * n_in;
             const hipError_t e =
                 mt == 2 ? launch_gemv_fused_f32_pair((int)type, (const uint8_t *)w, n_out, bias, out + (size_t)t * ldo,
-                                                     rb, n_in, xt, st_, st)
+                                                     rb, n_in, xt, st)
                         : launch_gemv_fused_f32((int)type, (const uint8_t *)w, n_out, bias, out + (size_t)t * ldo, rb,
-                                                n_in, xt, st_, st);
+                                                n_in, xt, st);
             if (!hip_ok(e, "gemv_f32 fused")) return false;
             t += mt;
         }
@@ -511,8 +505,7 @@ bool run_f32_product(uint32_t type, const void *w, int n_out, int n_in, int m, c
     }
     for (int t0 = 0; t0 < m; t0 += kGemvMaxTokens) {
         const int mt = m - t0 < kGemvMaxTokens ? m - t0 : kGemvMaxTokens;
-        if (!hip_ok(launch_gemv_f32((int)type, (const uint8_t *)w, rb, n_out, n_in, mt, x + (size_t)t0 * n_in,
-                                    xs != nullptr ? xs + (size_t)t0 * (n_in / 16) : nullptr, bias,
+        if (!hip_ok(launch_gemv_f32((int)type, (const uint8_t *)w, rb, n_out, n_in, mt, x + (size_t)t0 * n_in, bias,
                                     out + (size_t)t0 * ldo, ldo, st),
                     "gemv_f32"))
             return false;
@@ -562,7 +555,7 @@ bool run_linear_group(uint32_t type, int nmat, const void *const *w, const int *
         // whose sum starts at the bias in double
         const bool f64 = type == (uint32_t)kTypeF32 && m == 1;
         for (int z = 0; z < nmat; ++z)
-            if (!run_f32_product(type, w[z], n_out[z], n_in, m, x, nullptr, bias != nullptr ? bias[z] : nullptr,
+            if (!run_f32_product(type, w[z], n_out[z], n_in, m, x, bias != nullptr ? bias[z] : nullptr,
                                  out[z], n_out[z], st, f64))
                 return false;
         return true;
@@ -1046,20 +1039,17 @@ bool logits_run(float *scores, uint32_t *best_dev, const float *hidden, const vo
         // launches of two (the weights read once per pair), then the argmax
         // over the scores.  A row's score does not depend on m, as in the
         // reference's per-token loop.
-        if (k_family((int)type) && !hip_ok(launch_xsum16(hidden, m, n_embd, a.xs, st), "xsum16")) return false;
         if (m == 1 && best_dev != nullptr && k_family((int)type) && gemv_fused_f32_supported((int)type, n_embd)) {
             int nparts = 0;
             for (int t = 0; t < m; ++t) {
                 const hipError_t e = launch_gemv_fused_f32(
                     (int)type, (const uint8_t *)w, vocab, bias, scores + (size_t)t * vocab, rb, n_embd,
-                    hidden + (size_t)t * n_embd, a.xs + (size_t)t * (n_embd / 16), st, a.keys + (size_t)t * kArgmaxParts,
-                    &nparts);
+                    hidden + (size_t)t * n_embd, st, a.keys + (size_t)t * kArgmaxParts, &nparts);
                 if (!hip_ok(e, "logits gemv + argmax")) return false;
             }
             return hip_ok(launch_argmax_finish(a.keys, m, nparts, kArgmaxParts, best_dev, st), "argmax");
         }
-        if (!run_f32_product(type, w, vocab, n_embd, m, hidden, k_family((int)type) ? a.xs : nullptr, bias, scores,
-                             vocab, st))
+        if (!run_f32_product(type, w, vocab, n_embd, m, hidden, bias, scores, vocab, st))
             return false;
     }
     if (best_dev != nullptr &&
@@ -1090,9 +1080,9 @@ int edgexpu_hip_logits_noalloc_dev(float *scores, uint32_t *best_dev, const floa
         return 0;
     }
     if (!check_logits_args(scores, hidden, w, type, m, vocab, n_embd, chunk_rows, "logits_noalloc")) return 0;
-    size_t qb, sb, kb;
-    act_ws_sizes(type, m, n_embd, qb, sb, kb);
-    if (n_embd > kScratchMaxEmbd || qb + sb + kb > kScratchBytes) {
+    size_t qb, kb;
+    act_ws_sizes(type, m, n_embd, qb, kb);
+    if (n_embd > kScratchMaxEmbd || qb + kb > kScratchBytes) {
         set_error(-2, "logits_noalloc: m=%d x n_embd=%d exceeds the fixed scratch (n_embd <= %d, m <= %d)", m,
                   n_embd, kScratchMaxEmbd, kGemvMaxTokens);
         return 0;
@@ -1403,14 +1393,7 @@ int edgexpu_hip_dot_f32_rows(float *out, const uint8_t *w, uint32_t type, const 
     if (!hip_ok(hipMemcpyAsync(dx, x, (size_t)n * sizeof(float), hipMemcpyHostToDevice, g.stream), "H2D x")) return 0;
     // the f32-activation dot for every type (edgexpu_gguf_dot_quant never
     // quantizes x, src/gguf_quant.c:894-918)
-    float *xs = nullptr;
-    if (k_family((int)type)) {
-        ActWs a;
-        if (!act_ws(type, 1, n, a)) return 0;
-        xs = a.xs;
-        if (!hip_ok(launch_xsum16(dx, 1, n, xs, g.stream), "xsum16")) return 0;
-    }
-    if (!run_f32_product(type, d, rows, n, 1, dx, xs, nullptr, dout, rows, g.stream)) return 0;
+    if (!run_f32_product(type, d, rows, n, 1, dx, nullptr, dout, rows, g.stream)) return 0;
     if (!hip_ok(hipMemcpyAsync(out, dout, (size_t)rows * sizeof(float), hipMemcpyDeviceToHost, g.stream), "D2H"))
         return 0;
     return hip_ok(hipStreamSynchronize(g.stream), "sync") ? 1 : 0;

@@ -178,8 +178,8 @@ int edgexpu_hip_logits_dev(float *scores, uint32_t *best_dev, const float *hidde
  * cannot allocate device memory: code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc.  No counterpart in the reference.
  * Same arguments, checks and results (bit for bit) as edgexpu_hip_logits_dev.
- * Its scratch (quantized hidden vectors, 16-element sums, argmax partial
- * keys) is one fixed device array of about 430 KiB per GPU, held until the
+ * Its scratch (quantized hidden vectors, argmax partial keys) is one fixed
+ * device array of 402 KiB per GPU, held until the
  * process ends: m <= 8 and n_embd <= 16384, larger calls are refused.
  * edgexpu_hip_init must have run on the device first.  Every call on a GPU
  * shares that GPU's array, which keeps the last call's contents (every part

@@ -916,15 +916,17 @@ def _staging_edge_blocks(golden, rng):
     return blocks
 
 
+@pytest.mark.parametrize("gemv_mode", [1, 2])
 @pytest.mark.parametrize("qt,n_in", [(12, 4096), (12, 14336), (14, 9728), (14, 2560)])
-def test_fused_staging_quantizer_edge_cases(hipdev, ora, golden, qt, n_in):
+def test_fused_staging_quantizer_edge_cases(hipdev, ora, golden, qt, n_in, gemv_mode):
     """The GEMV's in-kernel Q8_K quantizer (one token: the activation is
     quantized in LDS inside the launch) on every branch of the reference's
     quantize_row_q8_K: equal bit for bit to quantizing with the standalone
     kernel (itself bit-exact against the reference's golden vectors) and
     running the GEMV over those bytes; the standalone codes equal the
     oracle's.  Shapes: 8-wave, 16-wave (rows split over 4 waves) and 12-wave
-    (3 waves per row) workgroups."""
+    (3 waves per row) workgroups; the fused kernel's staging and the
+    streaming kernel's (gemv_mode 2, where it covers the shape)."""
     rng = np.random.default_rng(n_in + qt)
     blocks = _staging_edge_blocks(golden, rng)
     nb = n_in // 256
@@ -934,8 +936,13 @@ def test_fused_staging_quantizer_edge_cases(hipdev, ora, golden, qt, n_in):
     wd = dev(w)
     xq = E.quantize_q8_k(dev(x))
     assert np.array_equal(xq.cpu().numpy(), ora.quantize_q8_k(x[0]))
-    sep = E.gemv_q8(wd, qt, xq, 1, n_out, n_in).cpu().numpy()
-    fused = E.linear_quant_batch(wd, qt, dev(x), n_out, n_in).cpu().numpy()
+    L = hipdev
+    try:
+        assert L.set_gemv_mode(gemv_mode) == 1
+        sep = E.gemv_q8(wd, qt, xq, 1, n_out, n_in).cpu().numpy()
+        fused = E.linear_quant_batch(wd, qt, dev(x), n_out, n_in).cpu().numpy()
+    finally:
+        L.set_gemv_mode(0)
     fin = np.isfinite(sep)
     assert np.array_equal(fin, np.isfinite(fused))
     assert np.array_equal(bits(fused[fin]), bits(sep[fin]))
