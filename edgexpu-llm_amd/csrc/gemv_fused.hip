@@ -8,7 +8,7 @@
 namespace exq {
 // gemv_fused_more.hip: plain projections of Q4_0 / Q5_0 / Q5_K rows
 hipError_t launch_gemv_fused_more(int type, const FusedArgs &a, bool stage, hipStream_t st);
-// gemv_stream.hip: one to four tokens of Q4_K rows at the decode row lengths
+// gemv_stream.hip: one to four tokens of Q4_K / Q6_K rows at the decode row lengths
 bool gemv_stream_take(int type, int K, int m, long long rows, int nmat, const uint8_t *const *w, int code,
                       bool staged);
 hipError_t launch_gemv_stream(int type, int nmat, const uint8_t *const *w, const int *n_out,
@@ -288,8 +288,8 @@ hipError_t launch_gemv_fused_layer(int type, int nmat, const uint8_t *const *w, 
         return hipErrorInvalidValue;
     // Q4_K rows at the decode lengths: the streaming kernel (one token: every
     // variant -- plain, prologues, residual, pairs, staged or Q8_K input;
-    // two to four tokens: plain projections of staged tokens), and one staged
-    // token of Q6_K rows of 9728; its rows equal this kernel's bit for bit
+    // two to four tokens: plain projections of staged tokens), and staged
+    // tokens of Q6_K rows of 9728; its rows equal this kernel's bit for bit
     long long rows = 0;
     for (int z = 0; z < nmat; ++z) rows += n_out[z];
     if (gemv_stream_take(type, K, m, rows, nmat, w, code, x != nullptr))

@@ -1,14 +1,17 @@
-// Streaming decode GEMV for one token of Q4_K rows: edgexpu_cpu_linear_quant_batch
-// (src/cpu_kernel.c:545-644) at m = 1 with the Q4_K x Q8_K block dot
-// (dot_q4_k_q8_k, src/gguf_dot_q8.c:603-666), for the row lengths of the
-// decode steps (K = 2560, 4096, 14336).
+// Streaming decode GEMV for one to four tokens of Q4_K or Q6_K rows:
+// edgexpu_cpu_linear_quant_batch (src/cpu_kernel.c:545-644) at m <= 4 with
+// the Q4_K x Q8_K and Q6_K x Q8_K block dots (dot_q4_k_q8_k,
+// src/gguf_dot_q8.c:603-666; dot_q6_k_q8_k, 897-963), for the row lengths of
+// the decode steps (Q4_K: K = 2560, 4096, 14336; Q6_K: 9728).
 //
 // Every weight row travels HBM -> LDS by DMA (buffer_load ... lds: no
 // registers held while it is in flight), one row per wave step, into a
 // per-wave ring of NB slots.  A slot is refilled as soon as its bytes are in
 // registers, so NB rows per wave stay in flight while the wave computes.
 // Lanes own fixed 64-element units of K (super-block i, quarter j): the
-// activation slice of a lane stays in registers for every row, the Q4_K
+// activation slices of a lane stay in registers for every row (where the
+// tokens' slices would take more than 160 registers, each row reads them
+// from LDS), the Q4_K
 // header's 6-bit scale/min pair is unpacked with lane-constant selectors
 // (v_perm), integer block sums with sdot4 / sdot2, one fp32 combine per unit.
 // A row's total is the fused kernel's butterfly over the lanes (so the two
@@ -295,6 +298,10 @@ struct StreamGeom {
     static constexpr int NI = Q6 ? CH + 2 : RPS * (CH + (PL > 0 ? 1 : 0));  // DMA instructions per step
     static constexpr int NT = NW * 64;
     static constexpr int ROUNDS = (FL & kSXq) ? 0 : (M * KSB * 16 + NT - 1) / NT;  // staging rounds
+    // the lane's activation slices (M tokens x T units) stay in registers when
+    // they take at most 160 of them; otherwise each step reads them from LDS
+    static constexpr int ACT_DW = Q6 ? 21 : 18;          // registers of one slice
+    static constexpr bool XREG = M * T * ACT_DW <= 160;
     // staged activations of the M tokens: codes, block scales, 16-element sums
     static constexpr int QB = (M * K + 15) & ~15, DB = (M * KSB * 4 + 15) & ~15, BB = (M * (K / 16) * 2 + 15) & ~15;
     static constexpr int XQB = ((KSB * kBytesQ8_K + 1023) / 1024) * 1024;  // raw blocks, whole chunks
@@ -307,10 +314,11 @@ struct StreamGeom {
                   "16-byte DMA lanes; Q6_K: one partial chunk of at least one lane");
     static_assert(!Q6 || (FL & (kSPair | kSXq)) == 0, "Q6_K rows: staged activations, no pairs");
     static_assert(AREA + (size_t)NW * NS * SB + 8 * NW <= 160 * 1024, "the ring and the staging fit the gfx950 LDS");
-    static_assert(ROUNDS <= 2, "the staging loads of at most two rounds are in flight at the start");
-    static_assert(NS * NI + 8 * ((FL & 3) ? 2 : 1) <= 63, "vmcnt range");
+    static_assert(ROUNDS <= 8, "the staging loads of every round are in flight at the start");
+    static_assert(NS * NI + 4 * ROUNDS * ((FL & 3) ? 2 : 1) <= 63, "vmcnt range");
     static_assert(AREA % 16 == 0, "slot alignment");
     static_assert(M == 1 || FL == 0, "several tokens: plain projections of staged activations");
+    static_assert(XREG || (FL & kSXq) == 0, "Q8_K block input: the slices in registers");
 };
 
 template <int KSB, int NW, int NB, int FL, bool DEEP, int M = 1, int TYPE = kTypeQ4_K>
@@ -477,7 +485,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     // the lane's activation slices, scale selectors and row offsets
     const ActLds act{lq, ld, lbs, G::K, KSB};
     using Act = std::conditional_t<Q6, FmtQ6K::Act, FmtQ4K::Act>;
-    Act xa[M][G::T];
+    using Fmt = std::conditional_t<Q6, FmtQ6K, FmtQ4K>;
+    Act xa[G::XREG ? M : 1][G::XREG ? G::T : 1];
     ScaleSel lc[G::T];
     uint32_t hoff[G::T], qoff[G::T];  // Q6_K: the unit's aligned byte offset, its shift (0 or 2)
     bool live[G::T];
@@ -488,11 +497,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
         const int uc = min(u, G::U - 1);
         if constexpr (kXq) {
             act_from_blocks(smem, uc, xa[0][t]);
-        } else if constexpr (Q6) {
-            FmtQ6K::load_act_lds(act, uc, 0, xa[0][t]);
-        } else {
+        } else if constexpr (G::XREG) {
 #pragma unroll
-            for (int m = 0; m < M; ++m) FmtQ4K::load_act_lds(act, uc, m, xa[m][t]);
+            for (int m = 0; m < M; ++m) Fmt::load_act_lds(act, uc, m, xa[m][t]);
         }
         if constexpr (Q6) {
             const uint32_t sb = (uint32_t)(uc >> 2) * kBytesQ6_K;  // the unit's fields sit at sb + 4-byte multiples
@@ -504,6 +511,17 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
             qoff[t] = hoff[t] + 16u + 32u * (uint32_t)(uc & 3);
         }
     }
+
+    // token m's activation slice of unit pass t
+    auto xslice = [&](int m, int t) -> Act {
+        if constexpr (G::XREG) {
+            return xa[m][t];
+        } else {
+            Act x;
+            Fmt::load_act_lds(act, min(lane + 64 * t, G::U - 1), m, x);
+            return x;
+        }
+    };
 
     // 3. the epilogue words of the lane's step (step first + lane * TW), loaded ahead of use
     struct Epi {
@@ -599,8 +617,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
                 const uint32_t scx = __builtin_amdgcn_alignbyte(s1[t], s0[t], qoff[t]);
                 const uint32_t scy = __builtin_amdgcn_alignbyte(s2[t], s1[t], qoff[t]);
                 const uint32_t db = (dw[t] >> (8u * qoff[t])) & 0xffffu;
-                const float v = q6k_unit(A[t], B[t], H[t], scx, scy, db, u & 1, xa[0][t]);
-                p[0][0][t] = live[t] ? v : 0.0f;
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const float v = q6k_unit(A[t], B[t], H[t], scx, scy, db, u & 1, xslice(m, t));
+                    p[m][0][t] = live[t] ? v : 0.0f;
+                }
             }
         } else {
             const uint8_t *sb = ring + slot * G::SB;
@@ -621,7 +642,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
                 for (int r = 0; r < G::RPS; ++r)
 #pragma unroll
                     for (int t = 0; t < G::T; ++t) {
-                        const float v = q4k_unit(h[r][t], q0[r][t], q1[r][t], xa[m][t], lc[t]);
+                        const float v = q4k_unit(h[r][t], q0[r][t], q1[r][t], xslice(m, t), lc[t]);
                         p[m][r][t] = live[t] ? v : 0.0f;
                     }
         }
@@ -737,13 +758,13 @@ hipError_t launch_stream_q6k(int fl, const StreamArgs &a, hipStream_t st) {
     }
 }
 
-// Plain projections of m = 2..4 staged tokens (rows of 2560 or 4096).
-template <int KSB>
+// Plain projections of m = 2..4 staged tokens.
+template <int KSB, int NB, int TYPE = kTypeQ4_K>
 hipError_t launch_stream_tokens(int m, const StreamArgs &a, hipStream_t st) {
     switch (m) {
-        case 2: return launch_stream<KSB, 8, 2, 0, 2>(a, st);
-        case 3: return launch_stream<KSB, 8, 2, 0, 3>(a, st);
-        case 4: return launch_stream<KSB, 8, 2, 0, 4>(a, st);
+        case 2: return launch_stream<KSB, 8, NB, 0, 2, TYPE>(a, st);
+        case 3: return launch_stream<KSB, 8, NB, 0, 3, TYPE>(a, st);
+        case 4: return launch_stream<KSB, 8, NB, 0, 4, TYPE>(a, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -772,19 +793,18 @@ static int g_gemv_mode = 0;
 void set_gemv_stream_mode(int mode) { g_gemv_mode = mode; }
 int gemv_stream_mode() { return g_gemv_mode; }
 
-// True when the streaming GEMV can take (type, K, m): one token of Q4_K rows
-// of 2560, 4096 or 14336 elements.
+// True when the streaming GEMV can take (type, K, m).
 // code: prologue (bits 0-1), residual (4), gate/up pairs (8); staged: f32
 // tokens (not Q8_K block bytes).  Q4_K: one token of rows of 2560, 4096 or
-// 14336, or plain projections of m = 2..4 staged tokens of rows of 2560 or
-// 4096.  Q6_K: one staged token of rows of 9728 (the hybrid ~4B down
-// projection), no pairs.
+// 14336, or plain projections of m = 2..4 staged tokens of those rows.
+// Q6_K: staged tokens of rows of 9728 (the hybrid ~4B down projection), one
+// (any variant but pairs) or two to four (plain projections).
 bool gemv_stream_supported(int type, int K, int m, int code, bool staged) {
     if (type == kTypeQ4_K) {
         if (m == 1) return K == 2560 || K == 4096 || K == 14336;
-        return m >= 2 && m <= 4 && staged && code == 0 && (K == 2560 || K == 4096);
+        return m >= 2 && m <= 4 && staged && code == 0 && (K == 2560 || K == 4096 || K == 14336);
     }
-    if (type == kTypeQ6_K) return m == 1 && staged && (code & 8) == 0 && K == 9728;
+    if (type == kTypeQ6_K) return K == 9728 && staged && (m == 1 ? (code & 8) == 0 : m <= 4 && code == 0);
     return false;
 }
 
@@ -804,10 +824,15 @@ bool gemv_stream_take(int type, int K, int m, long long rows, int nmat, const ui
         if (((uintptr_t)w[z] & 15u) != 0) return false;
     if (g_gemv_mode == 2) return true;
     // Q6_K rows of 9728 from 2048 rows (measured: 10.2 against 11.4 us at
-    // 2560 rows, 18.9 against 25.1 at 9728; 7.4 against 6.5 at 1024)
+    // 2560 rows, 18.9 against 25.1 at 9728; 7.4 against 6.5 at 1024; two /
+    // three / four tokens of 2560 rows 12.8 / 15.6 / 18.2 against 17.9 /
+    // 17.9 / 18.9 us for a quantize launch and the fused kernel)
     if (type == kTypeQ6_K) return rows >= 2048;
+    // Q4_K rows of 14336 from 2048 rows (two / three tokens of 4096 rows:
+    // 13.8 / 17.1 against 18.2 / 21.1 us), four tokens at any size (the other
+    // path there is the generic GEMV: 15.0 against 22.5 us at 1024 rows)
     const long long bytes = rows * (long long)(K / kQKK) * kBytesQ4_K;
-    return K != 14336 || bytes >= kStreamMinBytes14336;
+    return K != 14336 || bytes >= kStreamMinBytes14336 || m == 4;
 }
 
 // nmat Q4_K matrices against one token (m = 1) or the plain projection of
@@ -856,8 +881,15 @@ hipError_t launch_gemv_stream(int type, int nmat, const uint8_t *const *w, const
     // Q6_K rows of 9728 (8 KB): one slot per wave, no deep start (measured on
     // [2560 x 9728]: 10.2 us; a deep start 11.6, two slots 11.9, 12 waves
     // per CU 10.2 but 13.2 at 4096 rows)
-    if (type == kTypeQ6_K) return launch_stream_q6k<38, 8, 1>(fl, a, st);
-    if (m > 1) return K == 2560 ? launch_stream_tokens<10>(m, a, st) : launch_stream_tokens<16>(m, a, st);
+    if (type == kTypeQ6_K)
+        return m > 1 ? launch_stream_tokens<38, 1, kTypeQ6_K>(m, a, st) : launch_stream_q6k<38, 8, 1>(fl, a, st);
+    if (m > 1) {
+        switch (K) {
+            case 2560: return launch_stream_tokens<10, 2>(m, a, st);
+            case 4096: return launch_stream_tokens<16, 2>(m, a, st);
+            default: return launch_stream_tokens<56, 1>(m, a, st);
+        }
+    }
     // measured on the Llama-3-8B / hybrid decode shapes: 8 waves per CU, two
     // slots per wave, one slot where a row is 8 KB (K = 14336: two, 12.7
     // against 10.9 us at [4096 x 14336])

@@ -87,6 +87,8 @@ hipError_t launch_gemv_fused(int type, int nmat, const uint8_t *const *w, const 
 namespace exq {
 void set_gemv_stream_mode(int mode);
 int gemv_stream_mode();
+bool gemv_stream_take(int type, int K, int m, long long rows, int nmat, const uint8_t *const *w, int code,
+                      bool staged);
 }  // namespace exq
 
 namespace {
@@ -560,7 +562,15 @@ bool run_linear_group(uint32_t type, int nmat, const void *const *w, const int *
                 return false;
         return true;
     }
-    if (stage_in_kernel(type, n_in, m)) {
+    // two to four tokens of the rows the streaming GEMV takes are quantized
+    // inside its workgroups too; other long rows quantize once in their own
+    // launch
+    long long rows = 0;
+    for (int z = 0; z < nmat; ++z) rows += n_out[z];
+    const bool stream_staged =
+        m > 1 && m <= kFusedMaxTokens &&
+        gemv_stream_take((int)type, n_in, m, rows, nmat, (const uint8_t *const *)w, 0, true);
+    if (stream_staged || stage_in_kernel(type, n_in, m)) {
         return hip_ok(launch_gemv_fused((int)type, nmat, (const uint8_t *const *)w, n_out, bias, out, rb, n_in, m, x,
                                         nullptr, 0, st),
                       "gemv_fused");
