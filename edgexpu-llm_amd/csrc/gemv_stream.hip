@@ -721,6 +721,14 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     if (k64 > 0) flush(first, k64, epi);
 }
 
+template <int KSB, int NW, int NB, int FL, bool DEEP, int M, int TYPE>
+hipError_t launch_stream_geom(const StreamArgs &a, hipStream_t st) {
+    using G = StreamGeom<KSB, NW, NB, FL, DEEP, M, TYPE>;
+    hipLaunchKernelGGL((gemv_stream_q4k<KSB, NW, NB, FL, DEEP, M, TYPE>), dim3(device_cus()), dim3(NW * 64), G::lds(),
+                       st, a);
+    return hipGetLastError();
+}
+
 template <int KSB, int NW, int NB, int FL, int M = 1, int TYPE = kTypeQ4_K>
 hipError_t launch_stream(const StreamArgs &a, hipStream_t st) {
     // one workgroup per CU: the grid covers the chip once and every wave
@@ -732,17 +740,9 @@ hipError_t launch_stream(const StreamArgs &a, hipStream_t st) {
     const int grid = device_cus();
     const long long steps = ((long long)a.nrows + (long long)grid * NW - 1) / ((long long)grid * NW);
     if constexpr (KSB <= 16) {
-        if (steps <= 3) {
-            using G = StreamGeom<KSB, NW, NB, FL, true, M, TYPE>;
-            hipLaunchKernelGGL((gemv_stream_q4k<KSB, NW, NB, FL, true, M, TYPE>), dim3(grid), dim3(NW * 64), G::lds(),
-                               st, a);
-            return hipGetLastError();
-        }
+        if (steps <= 3) return launch_stream_geom<KSB, NW, NB, FL, true, M, TYPE>(a, st);
     }
-    using G = StreamGeom<KSB, NW, NB, FL, false, M, TYPE>;
-    hipLaunchKernelGGL((gemv_stream_q4k<KSB, NW, NB, FL, false, M, TYPE>), dim3(grid), dim3(NW * 64), G::lds(), st,
-                       a);
-    return hipGetLastError();
+    return launch_stream_geom<KSB, NW, NB, FL, false, M, TYPE>(a, st);
 }
 
 // Q6_K rows: one token, staged activations; prologues and the residual as for Q4_K.
@@ -758,9 +758,24 @@ hipError_t launch_stream_q6k(int fl, const StreamArgs &a, hipStream_t st) {
     }
 }
 
-// Plain projections of m = 2..4 staged tokens.
+// Plain projections of m = 2..4 staged tokens.  Rows of 4096 in launches
+// of at most three steps per wave keep one row per wave in flight (measured,
+// q+k+v [6144 x 4096] at 2 / 3 / 4 tokens: 6.5 / 7.9 / 8.5 us, against 7.3 /
+// 8.1 / 9.1 with two slots filled twice at the start; o [4096 x 4096] 5.7 /
+// 6.8 / 7.5 against 5.8 / 7.0 / 7.7); longer launches two.
 template <int KSB, int NB, int TYPE = kTypeQ4_K>
 hipError_t launch_stream_tokens(int m, const StreamArgs &a, hipStream_t st) {
+    if constexpr (KSB == 16 && NB == 2) {
+        const long long per_gen = (long long)device_cus() * 8;
+        if (((long long)a.nrows + per_gen - 1) / per_gen <= 3) {
+            switch (m) {
+                case 2: return launch_stream_geom<KSB, 8, 1, 0, false, 2, TYPE>(a, st);
+                case 3: return launch_stream_geom<KSB, 8, 1, 0, false, 3, TYPE>(a, st);
+                case 4: return launch_stream_geom<KSB, 8, 1, 0, false, 4, TYPE>(a, st);
+                default: return hipErrorInvalidValue;
+            }
+        }
+    }
     switch (m) {
         case 2: return launch_stream<KSB, 8, NB, 0, 2, TYPE>(a, st);
         case 3: return launch_stream<KSB, 8, NB, 0, 3, TYPE>(a, st);
