@@ -476,9 +476,17 @@ struct FmtQ4KF32 {
     using W = FmtQ4K::W;
     template <class A>
     __device__ static void load_w(const A &a, int row, int unit, W &w) { FmtQ4K::load_w(a, row, unit, w); }
-    __device__ static void dot1(const W &w, int unit, const Act &xa, float &acc) {
+    // Every token's dot with the unit's weights, each weight converted once.
+    // The 4-bit codes go to f32 as fp8 (E4M3) bytes: a byte q < 16 is the
+    // subnormal or first-binade value q * 2^-9 exactly (one conversion per
+    // pair of codes), and the sub-block scales carry the 2^9 back (d * 512 *
+    // sc is exact: 11 + 6 significant bits).  Every product and partial sum
+    // is the one of (float)q * x scaled by 2^-9 exactly, so the roundings are
+    // those of the plain loop unless a partial sum falls below 2^-117.
+    template <int M>
+    __device__ static void dotm(const W &w, int unit, const Act (&xa)[M], float *acc) {
         const int j = unit & 3;
-        const float d = f16_bits_to_f32(w.h.x & 0xffffu);
+        const float d = f16_bits_to_f32(w.h.x & 0xffffu) * 512.0f;
         const float dmin = f16_bits_to_f32(w.h.x >> 16);
         const int sh = 16 * (j & 1);
         uint32_t scp, mp;
@@ -492,29 +500,36 @@ struct FmtQ4KF32 {
         const float d1 = d * (float)(scp & 0xffu), d2 = d * (float)(scp >> 8);
         const float m1 = dmin * (float)(mp & 0xffu), m2 = dmin * (float)(mp >> 8);
         const uint32_t qw[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
-        {
-            float qlo = 0.0f, qhi = 0.0f;
+        float qlo[M], qhi[M];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                uint32_t lo = qw[k] & 0x0f0f0f0fu;
-                uint32_t hi = (qw[k] >> 4) & 0x0f0f0f0fu;
-                // opaque to the compiler: it would otherwise fold each byte
-                // extraction back into a 4-bit field extract of qw, where one
-                // v_cvt_f32_ubyte{0..3} per byte of the masked word suffices
-                asm volatile("" : "+v"(lo), "+v"(hi));
-                qlo = fmaf((float)(lo & 0xffu), xa.x[4 * k + 0], qlo);
-                qlo = fmaf((float)((lo >> 8) & 0xffu), xa.x[4 * k + 1], qlo);
-                qlo = fmaf((float)((lo >> 16) & 0xffu), xa.x[4 * k + 2], qlo);
-                qlo = fmaf((float)(lo >> 24), xa.x[4 * k + 3], qlo);
-                qhi = fmaf((float)(hi & 0xffu), xa.x[32 + 4 * k + 0], qhi);
-                qhi = fmaf((float)((hi >> 8) & 0xffu), xa.x[32 + 4 * k + 1], qhi);
-                qhi = fmaf((float)((hi >> 16) & 0xffu), xa.x[32 + 4 * k + 2], qhi);
-                qhi = fmaf((float)(hi >> 24), xa.x[32 + 4 * k + 3], qhi);
+        for (int t = 0; t < M; ++t) qlo[t] = qhi[t] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int lo = (int)(qw[k] & 0x0f0f0f0fu), hi = (int)((qw[k] >> 4) & 0x0f0f0f0fu);
+            const auto l01 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false), l23 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+            const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false), h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+#pragma unroll
+            for (int t = 0; t < M; ++t) {
+                qlo[t] = fmaf(l01[0], xa[t].x[4 * k + 0], qlo[t]);
+                qlo[t] = fmaf(l01[1], xa[t].x[4 * k + 1], qlo[t]);
+                qlo[t] = fmaf(l23[0], xa[t].x[4 * k + 2], qlo[t]);
+                qlo[t] = fmaf(l23[1], xa[t].x[4 * k + 3], qlo[t]);
+                qhi[t] = fmaf(h01[0], xa[t].x[32 + 4 * k + 0], qhi[t]);
+                qhi[t] = fmaf(h01[1], xa[t].x[32 + 4 * k + 1], qhi[t]);
+                qhi[t] = fmaf(h23[0], xa[t].x[32 + 4 * k + 2], qhi[t]);
+                qhi[t] = fmaf(h23[1], xa[t].x[32 + 4 * k + 3], qhi[t]);
             }
-            float r = d1 * qlo - m1 * xa.sx0;
-            r += d2 * qhi - m2 * xa.sx1;
-            acc += r;
         }
+#pragma unroll
+        for (int t = 0; t < M; ++t) {
+            float r = d1 * qlo[t] - m1 * xa[t].sx0;
+            r += d2 * qhi[t] - m2 * xa[t].sx1;
+            acc[t] += r;
+        }
+    }
+    static constexpr bool kTokensShareW = true;  // dotm: M tokens per weight conversion
+    __device__ static void dot1(const W &w, int unit, const Act &xa, float &acc) {
+        dotm<1>(w, unit, reinterpret_cast<const Act(&)[1]>(xa), &acc);
     }
 };
 

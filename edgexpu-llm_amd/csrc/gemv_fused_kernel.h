@@ -21,6 +21,8 @@
 
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "formats.h"
 
 namespace exq {
@@ -402,6 +404,12 @@ constexpr int fused_occupancy_pro(int r, int m, int loop, int pro) {
 // greedy-argmax epilogue (one matrix, one token): every stored score also
 // enters its lane's running best key, and each workgroup writes its best to
 // a.amax at the end.
+// Formats whose dotm<M> takes M tokens per conversion of the weights.
+template <class F, class = void>
+struct tokens_share_w : std::false_type {};
+template <class F>
+struct tokens_share_w<F, std::void_t<decltype(F::kTokensShareW)>> : std::bool_constant<F::kTokensShareW> {};
+
 template <class Fmt, int M, int R, int NW, bool STAGE, int LOOP, int PRO = 0>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(fused_occupancy_pro<Fmt>(R, M, LOOP, PRO))))
 void gemv_fused_kernel(FusedArgs a) {
@@ -551,13 +559,19 @@ void gemv_fused_kernel(FusedArgs a) {
     auto dot = [&](const typename Fmt::W (&w_)[R], float (&vals)[V]) {
 #pragma unroll
         for (int k = 0; k < V; ++k) vals[k] = 0.0f;
+        if constexpr (M > 1 && tokens_share_w<Fmt>::value) {
+            // every token's dot from one conversion of the weights
 #pragma unroll
-        for (int t = 0; t < M; ++t) {
-            typename Fmt::Act x;
-            if constexpr (M == 1) x = x1;
-            else x = xr[t];
+            for (int r = 0; r < R; ++r) Fmt::template dotm<M>(w_[r], u, xr, &vals[r * M]);
+        } else {
 #pragma unroll
-            for (int r = 0; r < R; ++r) Fmt::dot1(w_[r], u, x, vals[r * M + t]);
+            for (int t = 0; t < M; ++t) {
+                typename Fmt::Act x;
+                if constexpr (M == 1) x = x1;
+                else x = xr[t];
+#pragma unroll
+                for (int r = 0; r < R; ++r) Fmt::dot1(w_[r], u, x, vals[r * M + t]);
+            }
         }
 #pragma unroll
         for (int k = 0; k < V; ++k) vals[k] = unit_live ? vals[k] : 0.0f;

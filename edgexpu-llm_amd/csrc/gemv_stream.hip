@@ -65,11 +65,13 @@ struct StreamArgs {
     const float *x2;                       // SiLU-mul: act = silu(x) * x2
     const float *nw;                       // RMSNorm: act = rmsnorm(x; nw, eps)
     float eps;
+    unsigned long long *amax;              // argmax epilogue: one key per workgroup, at blockIdx.x
 };
 
 // flags: bits 0-1 prologue (1 RMSNorm, 2 SiLU-mul), 4 residual, 8 gate/up
-// pairs, 16 activation already in Q8_K block bytes
-constexpr int kSRes = 4, kSPair = 8, kSXq = 16;
+// pairs, 16 activation already in Q8_K block bytes, 32 f32 activation (the
+// f32-activation dot of the logits, not quantized), 64 greedy-argmax keys
+constexpr int kSRes = 4, kSPair = 8, kSXq = 16, kSF32 = 32, kSArgmax = 64;
 
 __device__ __forceinline__ v4u_t s_rsrc(const void *base, uint32_t bytes) {
     const uint64_t a = (uint64_t)(uintptr_t)base;
@@ -297,15 +299,16 @@ struct StreamGeom {
     static constexpr int PL = (RB % 1024) / 16;          // Q4_K: lanes of the partial chunk
     static constexpr int NI = Q6 ? CH + 2 : RPS * (CH + (PL > 0 ? 1 : 0));  // DMA instructions per step
     static constexpr int NT = NW * 64;
-    static constexpr int ROUNDS = (FL & kSXq) ? 0 : (M * KSB * 16 + NT - 1) / NT;  // staging rounds
+    static constexpr bool F32 = (FL & kSF32) != 0;       // f32 activation slices, loaded by each lane
+    static constexpr int ROUNDS = (FL & (kSXq | kSF32)) ? 0 : (M * KSB * 16 + NT - 1) / NT;  // staging rounds
     // the lane's activation slices (M tokens x T units) stay in registers when
     // they take at most 160 of them; otherwise each step reads them from LDS
-    static constexpr int ACT_DW = Q6 ? 21 : 18;          // registers of one slice
+    static constexpr int ACT_DW = F32 ? 66 : Q6 ? 21 : 18;  // registers of one slice
     static constexpr bool XREG = M * T * ACT_DW <= 160;
     // staged activations of the M tokens: codes, block scales, 16-element sums
     static constexpr int QB = (M * K + 15) & ~15, DB = (M * KSB * 4 + 15) & ~15, BB = (M * (K / 16) * 2 + 15) & ~15;
     static constexpr int XQB = ((KSB * kBytesQ8_K + 1023) / 1024) * 1024;  // raw blocks, whole chunks
-    static constexpr int AREA = (FL & kSXq) ? XQB : QB + DB + BB;
+    static constexpr int AREA = (FL & kSXq) ? XQB : F32 ? 0 : QB + DB + BB;
     // ring slots: NB steps in flight, NS at the start (DEEP: twice NB)
     static constexpr int NS = DEEP ? 2 * NB : NB;
     static constexpr size_t lds() { return (size_t)AREA + (size_t)NW * NS * SB; }
@@ -315,9 +318,11 @@ struct StreamGeom {
     static_assert(!Q6 || (FL & (kSPair | kSXq)) == 0, "Q6_K rows: staged activations, no pairs");
     static_assert(AREA + (size_t)NW * NS * SB + 8 * NW <= 160 * 1024, "the ring and the staging fit the gfx950 LDS");
     static_assert(ROUNDS <= 8, "the staging loads of every round are in flight at the start");
-    static_assert(NS * NI + 4 * ROUNDS * ((FL & 3) ? 2 : 1) <= 63, "vmcnt range");
+    static_assert(NS * NI + 4 * ROUNDS * ((FL & 3) ? 2 : 1) + (F32 ? 16 * M * T : 0) <= 63, "vmcnt range");
+    static_assert(!F32 || (!Q6 && (FL & ~(kSF32 | kSArgmax)) == 0 && XREG), "f32 activations: plain Q4_K rows, slices in registers");
+    static_assert(!(FL & kSArgmax) || (F32 && M == 1), "argmax keys: one f32 token");
     static_assert(AREA % 16 == 0, "slot alignment");
-    static_assert(M == 1 || FL == 0, "several tokens: plain projections of staged activations");
+    static_assert(M == 1 || (FL & ~kSF32) == 0, "several tokens: plain projections");
     static_assert(XREG || (FL & kSXq) == 0, "Q8_K block input: the slices in registers");
 };
 
@@ -327,6 +332,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     constexpr bool Q6 = G::Q6;
     constexpr int PRO = FL & 3;
     constexpr bool kRes = (FL & kSRes) != 0, kPair = (FL & kSPair) != 0, kXq = (FL & kSXq) != 0;
+    constexpr bool kF32 = G::F32, kArgmax = (FL & kSArgmax) != 0;
     constexpr int NS = G::NS;
     extern __shared__ __align__(16) uint8_t smem[];
     int8_t *lq = reinterpret_cast<int8_t *>(smem);
@@ -394,7 +400,18 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     constexpr int BPR = G::NT / 16;
     constexpr int RN = G::ROUNDS > 0 ? G::ROUNDS : 1;
     v4u_t xr[RN][4], yr[RN][4];
-    if constexpr (kXq) {
+    // f32 activations: each lane's 64 floats of every unit pass and token
+    v4u_t fr[kF32 ? M : 1][kF32 ? G::T : 1][16];
+    if constexpr (kF32) {
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int t = 0; t < G::T; ++t) {
+                const float *px = a.x + (size_t)m * G::K + 64 * min(lane + 64 * t, G::U - 1);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) fr[m][t][v] = s_load16(px + 4 * v);
+            }
+    } else if constexpr (kXq) {
         // Q8_K block bytes into LDS, 1 KB chunks over the waves
         const v4u_t rsx = s_rsrc(a.xq, (uint32_t)(KSB * kBytesQ8_K));
         constexpr int XCH = G::XQB / 1024;
@@ -421,6 +438,13 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     s_wait_vm<NS * G::NI>();  // the activation inputs have arrived; the ring's rows may not have
     if constexpr (kXq) {
         __syncthreads();
+    } else if constexpr (kF32) {
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int t = 0; t < G::T; ++t)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) asm volatile("" : "+v"(fr[m][t][v]));
     } else {
         // the loaded registers are complete only now: every use is ordered after the wait
 #pragma unroll
@@ -484,7 +508,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     }
     // the lane's activation slices, scale selectors and row offsets
     const ActLds act{lq, ld, lbs, G::K, KSB};
-    using Act = std::conditional_t<Q6, FmtQ6K::Act, FmtQ4K::Act>;
+    using Act = std::conditional_t<kF32, FmtQ4KF32::Act, std::conditional_t<Q6, FmtQ6K::Act, FmtQ4K::Act>>;
     using Fmt = std::conditional_t<Q6, FmtQ6K, FmtQ4K>;
     Act xa[G::XREG ? M : 1][G::XREG ? G::T : 1];
     ScaleSel lc[G::T];
@@ -497,6 +521,19 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
         const int uc = min(u, G::U - 1);
         if constexpr (kXq) {
             act_from_blocks(smem, uc, xa[0][t]);
+        } else if constexpr (kF32) {
+            // FmtQ4KF32::load_act's slice and sums
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const float4 f = __builtin_bit_cast(float4, fr[m][t][v]);
+                    xa[m][t].x[4 * v] = f.x; xa[m][t].x[4 * v + 1] = f.y;
+                    xa[m][t].x[4 * v + 2] = f.z; xa[m][t].x[4 * v + 3] = f.w;
+                }
+                xa[m][t].sx0 = sum16(xa[m][t].x) + sum16(xa[m][t].x + 16);
+                xa[m][t].sx1 = sum16(xa[m][t].x + 32) + sum16(xa[m][t].x + 48);
+            }
         } else if constexpr (G::XREG) {
 #pragma unroll
             for (int m = 0; m < M; ++m) Fmt::load_act_lds(act, uc, m, xa[m][t]);
@@ -560,6 +597,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     };
     // keep[m]: token m's total of step k (k % 64 = this lane); keep1: up's
     float keep[M], keep1 = 0.0f;
+    unsigned long long best = 0ull;  // argmax: the lane's best key (score_key) so far
 #pragma unroll
     for (int m = 0; m < M; ++m) keep[m] = 0.0f;
     auto flush = [&](int first, int n, const Epi &e) {
@@ -577,6 +615,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
                 if constexpr (kRes) o = resid != nullptr ? e.r + v : v;
                 if constexpr (kPair) o = silu_f32(v) * (e.b1 + keep1);
                 out[(size_t)m * n_out + row] = o;
+                if constexpr (kArgmax) {
+                    const unsigned long long key = score_key(o, (unsigned)row);
+                    best = key > best ? key : best;
+                }
             }
         }
     };
@@ -636,15 +678,38 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
                 }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             if (k + NB >= NS) issue((slot + NB) % NS, gw + (k + NB) * TW);  // uniform; slot == k % NS
-#pragma unroll
-            for (int m = 0; m < M; ++m)
+            if constexpr (kF32) {
+                // the f32-activation dot of every token from one conversion of
+                // the unit's weights, from a zero sum (as the fused kernel)
 #pragma unroll
                 for (int r = 0; r < G::RPS; ++r)
 #pragma unroll
                     for (int t = 0; t < G::T; ++t) {
-                        const float v = q4k_unit(h[r][t], q0[r][t], q1[r][t], xslice(m, t), lc[t]);
-                        p[m][r][t] = live[t] ? v : 0.0f;
+                        const FmtQ4K::W w{uint4{h[r][t][0], h[r][t][1], h[r][t][2], h[r][t][3]},
+                                          uint4{q0[r][t][0], q0[r][t][1], q0[r][t][2], q0[r][t][3]},
+                                          uint4{q1[r][t][0], q1[r][t][1], q1[r][t][2], q1[r][t][3]}};
+                        Act xm[M];
+                        float acc[M];
+#pragma unroll
+                        for (int m = 0; m < M; ++m) {
+                            xm[m] = xa[m][t];
+                            acc[m] = 0.0f;
+                        }
+                        FmtQ4KF32::dotm<M>(w, min(lane + 64 * t, G::U - 1), xm, acc);
+#pragma unroll
+                        for (int m = 0; m < M; ++m) p[m][r][t] = live[t] ? acc[m] : 0.0f;
                     }
+            } else {
+#pragma unroll
+                for (int m = 0; m < M; ++m)
+#pragma unroll
+                    for (int r = 0; r < G::RPS; ++r)
+#pragma unroll
+                        for (int t = 0; t < G::T; ++t) {
+                            const float v = q4k_unit(h[r][t], q0[r][t], q1[r][t], xslice(m, t), lc[t]);
+                            p[m][r][t] = live[t] ? v : 0.0f;
+                        }
+            }
         }
     };
     int k64 = 0, first = gw;
@@ -719,6 +784,22 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     }
     s_wait_vm<0>();
     if (k64 > 0) flush(first, k64, epi);
+    if constexpr (kArgmax) {
+        // the workgroup's best key: each wave over its lanes, then the first
+        // lane over the waves; one key per workgroup (at blockIdx.x)
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const unsigned long long o = __shfl_xor(best, off, 64);
+            best = o > best ? o : best;
+        }
+        __shared__ unsigned long long wbest[NW];
+        if (lane == 0) wbest[wave] = best;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int k = 1; k < NW; ++k) best = wbest[k] > best ? wbest[k] : best;
+            a.amax[blockIdx.x] = best;
+        }
+    }
 }
 
 template <int KSB, int NW, int NB, int FL, bool DEEP, int M, int TYPE>
@@ -801,7 +882,7 @@ hipError_t launch_stream_flags(int fl, const StreamArgs &a, hipStream_t st) {
 
 }  // namespace
 
-// Kernel choice for the one-token Q4_K launches this kernel covers (the
+// Kernel choice for the launches this kernel covers (the
 // library's edgexpu_hip_set_gemv_mode): 0 by launch size, 1 the fused kernel,
 // 2 this one.  Both give the same outputs bit for bit.
 static int g_gemv_mode = 0;
@@ -913,6 +994,44 @@ hipError_t launch_gemv_stream(int type, int nmat, const uint8_t *const *w, const
         case 4096: return launch_stream_flags<16, 8, 2>(fl, a, st);
         default: return launch_stream_flags<56, 8, 1>(fl, a, st);
     }
+}
+
+// True when the streaming GEMV runs the f32-activation product (the logits
+// dot, src/native.c:445-462) of m tokens against Q4_K rows at w: rows of 4096,
+// one or two tokens, the matrix 16-byte aligned.  Measured on [128256 x
+// 4096] against the fused kernel: one token 57.6 against 70.7 us (61.5
+// against 71.9 with the argmax keys and their reduction), two tokens 78.1
+// against 113.8; both kernels give the same words.
+bool gemv_stream_f32_take(int type, int K, int m, const uint8_t *w) {
+    if (g_gemv_mode == 1 || type != kTypeQ4_K || K != 4096 || m < 1 || m > 2) return false;
+    return ((uintptr_t)w & 15u) == 0;
+}
+
+// scores[t][row] = bias[row] + the f32-activation dot of token t (xf [m][K])
+// with Q4_K row `row`; amax (one token): each workgroup's greedy-argmax key
+// (score_key) at amax[blockIdx.x], *nparts keys.
+hipError_t launch_gemv_stream_f32(int K, int m, const uint8_t *w, int n_out, const float *bias, float *out,
+                                  const float *xf, unsigned long long *amax, int *nparts, hipStream_t st) {
+    if (K != 4096 || m < 1 || m > 2 || (amax != nullptr && m != 1) || ((uintptr_t)w & 15u) != 0 || n_out < 1)
+        return hipErrorInvalidValue;
+    StreamArgs a{};
+    a.nmat = 1;
+    a.w[0] = w;
+    a.bias[0] = bias;
+    a.out[0] = out;
+    a.n_out[0] = n_out;
+    for (int z = 1; z <= kStreamMaxMats; ++z) a.row_start[z] = n_out;
+    a.nrows = n_out;
+    a.x = xf;
+    a.amax = amax;
+    if (nparts != nullptr) *nparts = device_cus();
+    // one token: 16 waves per CU, one row each in flight (the f32 dot's
+    // arithmetic wants the waves; measured 57.6 us against 59.2-65.0 with 8
+    // waves and two to four slots); two tokens (two activation slices per
+    // lane): 8 waves, three slots (78.1 against 81.2 with two)
+    if (amax != nullptr) return launch_stream_geom<16, 16, 1, kSF32 | kSArgmax, false, 1, kTypeQ4_K>(a, st);
+    return m == 1 ? launch_stream_geom<16, 16, 1, kSF32, false, 1, kTypeQ4_K>(a, st)
+                  : launch_stream<16, 8, 3, kSF32, 2>(a, st);
 }
 
 }  // namespace exq
