@@ -561,7 +561,9 @@ struct FmtQ6KF32 {
     using W = FmtQ6K::W;
     template <class A>
     __device__ static void load_w(const A &a, int row, int unit, W &w) { FmtQ6K::load_w(a, row, unit, w); }
-    __device__ static void dot1(const W &w, int unit, const Act &xa, float &acc) {
+    // Every token's dot with the unit's weights, each code converted once.
+    template <int M>
+    __device__ static void dotm(const W &w, int unit, const Act (&xa)[M], float *acc) {
         const int p = unit & 1;
         const float d = f16_bits_to_f32(w.d);
         float ds[4];
@@ -580,24 +582,37 @@ struct FmtQ6KF32 {
             c[2][v] = ((A[v] >> 4) & 0x0f0f0f0fu) | (H[v] & 0x30303030u);
             c[3][v] = ((B[v] >> 4) & 0x0f0f0f0fu) | ((H[v] >> 2) & 0x30303030u);
         }
-        {
-            float r = 0.0f;
+        float r[M];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                float s = 0.0f;
+        for (int t = 0; t < M; ++t) r[t] = 0.0f;
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const uint32_t cv = c[k][v];
-                    s = fmaf((float)(cv & 0xffu), xa.x[16 * k + 4 * v + 0], s);
-                    s = fmaf((float)((cv >> 8) & 0xffu), xa.x[16 * k + 4 * v + 1], s);
-                    s = fmaf((float)((cv >> 16) & 0xffu), xa.x[16 * k + 4 * v + 2], s);
-                    s = fmaf((float)(cv >> 24), xa.x[16 * k + 4 * v + 3], s);
+        for (int k = 0; k < 4; ++k) {
+            float s[M];
+#pragma unroll
+            for (int t = 0; t < M; ++t) s[t] = 0.0f;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const uint32_t cv = c[k][v];
+                const float f0 = (float)(cv & 0xffu), f1 = (float)((cv >> 8) & 0xffu);
+                const float f2 = (float)((cv >> 16) & 0xffu), f3 = (float)(cv >> 24);
+#pragma unroll
+                for (int t = 0; t < M; ++t) {
+                    s[t] = fmaf(f0, xa[t].x[16 * k + 4 * v + 0], s[t]);
+                    s[t] = fmaf(f1, xa[t].x[16 * k + 4 * v + 1], s[t]);
+                    s[t] = fmaf(f2, xa[t].x[16 * k + 4 * v + 2], s[t]);
+                    s[t] = fmaf(f3, xa[t].x[16 * k + 4 * v + 3], s[t]);
                 }
-                // sum (q-32)*x = sum q*x - 32*sum x
-                r = fmaf(ds[k], fmaf(-32.0f, xa.sx[k], s), r);
             }
-            acc += r;
+            // sum (q-32)*x = sum q*x - 32*sum x
+#pragma unroll
+            for (int t = 0; t < M; ++t) r[t] = fmaf(ds[k], fmaf(-32.0f, xa[t].sx[k], s[t]), r[t]);
         }
+#pragma unroll
+        for (int t = 0; t < M; ++t) acc[t] += r[t];
+    }
+    static constexpr bool kTokensShareW = true;  // dotm: M tokens per weight conversion
+    __device__ static void dot1(const W &w, int unit, const Act &xa, float &acc) {
+        dotm<1>(w, unit, reinterpret_cast<const Act(&)[1]>(xa), &acc);
     }
 };
 

@@ -180,6 +180,23 @@ __device__ __forceinline__ float s_wave_total4(const float (&v)[4]) {
     return a;
 }
 
+// The row total of 33-48 units as the fused kernel's f32-activation launches
+// form it (16-lane slots over three waves, src/native.c:445-462 rows of
+// 2112-3072): lanes 16k..16k+15 summed by the last four levels of
+// s_wave_total (^ 8, ^ 4, ^ 2, ^ 1), then the three group totals added in
+// order from 0, as the fused kernel adds its waves' partials.
+__device__ __forceinline__ float s_wave_total_3x16(float a) {
+    a += s_dpp<0x128>(a);  // ^ 8 (row_ror:8)
+    a += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, a), 0x101f));  // ^ 4
+    a += s_dpp<0x4E>(a);   // ^ 2
+    a += s_dpp<0xB1>(a);   // ^ 1
+    float t = 0.0f;
+    t += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 0));
+    t += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 16));
+    t += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 32));
+    return t;
+}
+
 // Value of lane `src` (wave-uniform) in every lane.
 __device__ __forceinline__ float s_lane(float v, int src) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
@@ -303,7 +320,7 @@ struct StreamGeom {
     static constexpr int ROUNDS = (FL & (kSXq | kSF32)) ? 0 : (M * KSB * 16 + NT - 1) / NT;  // staging rounds
     // the lane's activation slices (M tokens x T units) stay in registers when
     // they take at most 160 of them; otherwise each step reads them from LDS
-    static constexpr int ACT_DW = F32 ? 66 : Q6 ? 21 : 18;  // registers of one slice
+    static constexpr int ACT_DW = F32 ? (Q6 ? 68 : 66) : Q6 ? 21 : 18;  // registers of one slice
     static constexpr bool XREG = M * T * ACT_DW <= 160;
     // staged activations of the M tokens: codes, block scales, 16-element sums
     static constexpr int QB = (M * K + 15) & ~15, DB = (M * KSB * 4 + 15) & ~15, BB = (M * (K / 16) * 2 + 15) & ~15;
@@ -319,7 +336,7 @@ struct StreamGeom {
     static_assert(AREA + (size_t)NW * NS * SB + 8 * NW <= 160 * 1024, "the ring and the staging fit the gfx950 LDS");
     static_assert(ROUNDS <= 8, "the staging loads of every round are in flight at the start");
     static_assert(NS * NI + 4 * ROUNDS * ((FL & 3) ? 2 : 1) + (F32 ? 16 * M * T : 0) <= 63, "vmcnt range");
-    static_assert(!F32 || (!Q6 && (FL & ~(kSF32 | kSArgmax)) == 0 && XREG), "f32 activations: plain Q4_K rows, slices in registers");
+    static_assert(!F32 || ((FL & ~(kSF32 | kSArgmax)) == 0 && XREG), "f32 activations: plain rows, slices in registers");
     static_assert(!(FL & kSArgmax) || (F32 && M == 1), "argmax keys: one f32 token");
     static_assert(AREA % 16 == 0, "slot alignment");
     static_assert(M == 1 || (FL & ~kSF32) == 0, "several tokens: plain projections");
@@ -401,15 +418,24 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     constexpr int RN = G::ROUNDS > 0 ? G::ROUNDS : 1;
     v4u_t xr[RN][4], yr[RN][4];
     // f32 activations: each lane's 64 floats of every unit pass and token
+    // (Q4_K unit 4i+j: elements 256i+64j..+63; Q6_K unit (i, h, p): four
+    // runs of 16 at 256i+128h+16p+32k, k = 0..3)
     v4u_t fr[kF32 ? M : 1][kF32 ? G::T : 1][16];
     if constexpr (kF32) {
 #pragma unroll
         for (int m = 0; m < M; ++m)
 #pragma unroll
             for (int t = 0; t < G::T; ++t) {
-                const float *px = a.x + (size_t)m * G::K + 64 * min(lane + 64 * t, G::U - 1);
+                const int uc = min(lane + 64 * t, G::U - 1);
+                if constexpr (Q6) {
+                    const float *px = a.x + (size_t)m * G::K + 256 * (uc >> 2) + 128 * ((uc >> 1) & 1) + 16 * (uc & 1);
 #pragma unroll
-                for (int v = 0; v < 16; ++v) fr[m][t][v] = s_load16(px + 4 * v);
+                    for (int v = 0; v < 16; ++v) fr[m][t][v] = s_load16(px + 32 * (v >> 2) + 4 * (v & 3));
+                } else {
+                    const float *px = a.x + (size_t)m * G::K + 64 * uc;
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) fr[m][t][v] = s_load16(px + 4 * v);
+                }
             }
     } else if constexpr (kXq) {
         // Q8_K block bytes into LDS, 1 KB chunks over the waves
@@ -508,7 +534,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     }
     // the lane's activation slices, scale selectors and row offsets
     const ActLds act{lq, ld, lbs, G::K, KSB};
-    using Act = std::conditional_t<kF32, FmtQ4KF32::Act, std::conditional_t<Q6, FmtQ6K::Act, FmtQ4K::Act>>;
+    using ActF32 = std::conditional_t<Q6, FmtQ6KF32::Act, FmtQ4KF32::Act>;
+    using Act = std::conditional_t<kF32, ActF32, std::conditional_t<Q6, FmtQ6K::Act, FmtQ4K::Act>>;
     using Fmt = std::conditional_t<Q6, FmtQ6K, FmtQ4K>;
     Act xa[G::XREG ? M : 1][G::XREG ? G::T : 1];
     ScaleSel lc[G::T];
@@ -522,7 +549,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
         if constexpr (kXq) {
             act_from_blocks(smem, uc, xa[0][t]);
         } else if constexpr (kF32) {
-            // FmtQ4KF32::load_act's slice and sums
+            // the slice and sums of FmtQ4KF32::load_act / FmtQ6KF32::load_act
 #pragma unroll
             for (int m = 0; m < M; ++m) {
 #pragma unroll
@@ -531,8 +558,13 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
                     xa[m][t].x[4 * v] = f.x; xa[m][t].x[4 * v + 1] = f.y;
                     xa[m][t].x[4 * v + 2] = f.z; xa[m][t].x[4 * v + 3] = f.w;
                 }
-                xa[m][t].sx0 = sum16(xa[m][t].x) + sum16(xa[m][t].x + 16);
-                xa[m][t].sx1 = sum16(xa[m][t].x + 32) + sum16(xa[m][t].x + 48);
+                if constexpr (Q6) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) xa[m][t].sx[k] = sum16(xa[m][t].x + 16 * k);
+                } else {
+                    xa[m][t].sx0 = sum16(xa[m][t].x) + sum16(xa[m][t].x + 16);
+                    xa[m][t].sx1 = sum16(xa[m][t].x + 32) + sum16(xa[m][t].x + 48);
+                }
             }
         } else if constexpr (G::XREG) {
 #pragma unroll
@@ -659,10 +691,26 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
                 const uint32_t scx = __builtin_amdgcn_alignbyte(s1[t], s0[t], qoff[t]);
                 const uint32_t scy = __builtin_amdgcn_alignbyte(s2[t], s1[t], qoff[t]);
                 const uint32_t db = (dw[t] >> (8u * qoff[t])) & 0xffffu;
+                if constexpr (kF32) {
+                    // the f32-activation dot of every token, from a zero sum (as the fused kernel)
+                    const FmtQ6K::W w{uint4{A[t][0], A[t][1], A[t][2], A[t][3]}, uint4{B[t][0], B[t][1], B[t][2], B[t][3]},
+                                      uint4{H[t][0], H[t][1], H[t][2], H[t][3]}, uint2{scx, scy}, db};
+                    Act xm[M];
+                    float acc[M];
 #pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    const float v = q6k_unit(A[t], B[t], H[t], scx, scy, db, u & 1, xslice(m, t));
-                    p[m][0][t] = live[t] ? v : 0.0f;
+                    for (int m = 0; m < M; ++m) {
+                        xm[m] = xa[m][t];
+                        acc[m] = 0.0f;
+                    }
+                    FmtQ6KF32::dotm<M>(w, u, xm, acc);
+#pragma unroll
+                    for (int m = 0; m < M; ++m) p[m][0][t] = live[t] ? acc[m] : 0.0f;
+                } else {
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        const float v = q6k_unit(A[t], B[t], H[t], scx, scy, db, u & 1, xslice(m, t));
+                        p[m][0][t] = live[t] ? v : 0.0f;
+                    }
                 }
             }
         } else {
@@ -737,7 +785,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
             for (int m = 0; m < M; ++m)
 #pragma unroll
                 for (int r = 0; r < G::RPS; ++r) {
-                    if constexpr (G::T == 1) {
+                    if constexpr (G::F32 && G::T == 1 && G::U > 32 && G::U <= 48) {
+                        acc[m][r] = s_wave_total_3x16(p[m][r][0]);
+                    } else if constexpr (G::T == 1) {
                         acc[m][r] = s_wave_total(p[m][r][0]);
                     } else if constexpr (G::T == 4) {
                         const float tot = s_wave_total4(p[m][r]);
@@ -997,22 +1047,25 @@ hipError_t launch_gemv_stream(int type, int nmat, const uint8_t *const *w, const
 }
 
 // True when the streaming GEMV runs the f32-activation product (the logits
-// dot, src/native.c:445-462) of m tokens against Q4_K rows at w: rows of 4096,
-// one or two tokens, the matrix 16-byte aligned.  Measured on [128256 x
-// 4096] against the fused kernel: one token 57.6 against 70.7 us (61.5
-// against 71.9 with the argmax keys and their reduction), two tokens 78.1
-// against 113.8; both kernels give the same words.
+// dot, src/native.c:445-462) of m tokens against the rows at w: Q4_K rows of
+// 4096 or Q6_K rows of 2560, one or two tokens, the matrix 16-byte aligned.
+// Measured on [128256 x 4096] Q4_K against the fused kernel: one token 57.6
+// against 70.7 us (61.5 against 71.9 with the argmax keys and their
+// reduction), two tokens 78.1 against 113.8; both kernels give the same
+// words.
 bool gemv_stream_f32_take(int type, int K, int m, const uint8_t *w) {
-    if (g_gemv_mode == 1 || type != kTypeQ4_K || K != 4096 || m < 1 || m > 2) return false;
+    if (g_gemv_mode == 1 || m < 1 || m > 2) return false;
+    if (!(type == kTypeQ4_K && K == 4096) && !(type == kTypeQ6_K && K == 2560)) return false;
     return ((uintptr_t)w & 15u) == 0;
 }
 
 // scores[t][row] = bias[row] + the f32-activation dot of token t (xf [m][K])
 // with Q4_K row `row`; amax (one token): each workgroup's greedy-argmax key
 // (score_key) at amax[blockIdx.x], *nparts keys.
-hipError_t launch_gemv_stream_f32(int K, int m, const uint8_t *w, int n_out, const float *bias, float *out,
-                                  const float *xf, unsigned long long *amax, int *nparts, hipStream_t st) {
-    if (K != 4096 || m < 1 || m > 2 || (amax != nullptr && m != 1) || ((uintptr_t)w & 15u) != 0 || n_out < 1)
+hipError_t launch_gemv_stream_f32(int type, int K, int m, const uint8_t *w, int n_out, const float *bias,
+                                  float *out, const float *xf, unsigned long long *amax, int *nparts, hipStream_t st) {
+    if (!(type == kTypeQ4_K && K == 4096) && !(type == kTypeQ6_K && K == 2560)) return hipErrorInvalidValue;
+    if (m < 1 || m > 2 || (amax != nullptr && m != 1) || ((uintptr_t)w & 15u) != 0 || n_out < 1)
         return hipErrorInvalidValue;
     StreamArgs a{};
     a.nmat = 1;
@@ -1029,6 +1082,14 @@ hipError_t launch_gemv_stream_f32(int K, int m, const uint8_t *w, int n_out, con
     // arithmetic wants the waves; measured 57.6 us against 59.2-65.0 with 8
     // waves and two to four slots); two tokens (two activation slices per
     // lane): 8 waves, three slots (78.1 against 81.2 with two)
+    // Q6_K rows of 2560 ([151936 x 2560]): one token 16 waves, one slot (77.8
+    // - 80.5 us against 86.5 - 87.5 fused; 8 waves 89.0 - 95.2); two tokens
+    // 8 waves, two slots (108.9 against 147.9)
+    if (type == kTypeQ6_K) {
+        if (amax != nullptr) return launch_stream_geom<10, 16, 1, kSF32 | kSArgmax, false, 1, kTypeQ6_K>(a, st);
+        return m == 1 ? launch_stream_geom<10, 16, 1, kSF32, false, 1, kTypeQ6_K>(a, st)
+                      : launch_stream_geom<10, 8, 2, kSF32, false, 2, kTypeQ6_K>(a, st);
+    }
     if (amax != nullptr) return launch_stream_geom<16, 16, 1, kSF32 | kSArgmax, false, 1, kTypeQ4_K>(a, st);
     return m == 1 ? launch_stream_geom<16, 16, 1, kSF32, false, 1, kTypeQ4_K>(a, st)
                   : launch_stream<16, 8, 3, kSF32, 2>(a, st);

@@ -258,35 +258,36 @@ def test_q6k_tokens_fused_equals_stream(hipdev, ora, n_outs, m):
         assert np.all(np.abs(s[z][:, sample] - want) <= TOL * S), f"matrix {z}"
 
 
-def f32_scales(w, h):
-    """S_i of the f32-activation dot of Q4_K rows with h (float64)."""
-    return np.array([npref.f32_dot_f64(12, w[i], h)[1] for i in range(w.shape[0])])
+def f32_scales(qt, w, h):
+    """S_i of the f32-activation dot of the rows of w with h (float64)."""
+    return np.array([npref.f32_dot_f64(qt, w[i], h)[1] for i in range(w.shape[0])])
 
 
+@pytest.mark.parametrize("qt,n", [(12, 4096), (14, 2560)])
 @pytest.mark.parametrize("vocab,m,with_bias", [(20000, 1, True), (3001, 1, False), (2048 * 64 + 5, 1, False),
                                                (20000, 2, True), (3001, 3, False)])
-def test_logits_q4k_fused_equals_stream(hipdev, ora, vocab, m, with_bias):
-    """The f32-activation logits of Q4_K rows of 4096 (one hidden vector with
-    the greedy-argmax keys, or several in launches of two): scores and greedy
-    indices equal the fused kernel's bit for bit, every score within 1e-5 of
-    its row's scale of the oracle's (src/native.c:445-462, 2355-2396).  Sizes:
-    a few rows per wave, fewer than three, and more than 64 (the kept totals
-    flushed, the argmax keys carried across flushes)."""
-    n = 4096
-    rng = np.random.default_rng(7000 + vocab + m)
-    w = synth.np_weights(12, vocab, n, rng)
+def test_logits_f32_fused_equals_stream(hipdev, ora, qt, n, vocab, m, with_bias):
+    """The f32-activation logits of Q4_K rows of 4096 and Q6_K rows of 2560
+    (one hidden vector with the greedy-argmax keys, or several in launches
+    of two): scores and greedy indices equal the fused kernel's bit for bit,
+    every score within 1e-5 of its row's scale of the oracle's
+    (src/native.c:445-462, 2355-2396).  Sizes: a few rows per wave, fewer
+    than three, and more than 64 (the kept totals flushed, the argmax keys
+    carried across flushes)."""
+    rng = np.random.default_rng(7000 + vocab + m + qt)
+    w = synth.np_weights(qt, vocab, n, rng)
     h = rng.normal(0, 1, (m, n)).astype(np.float32)
     bias = rng.normal(0, 0.01, vocab).astype(np.float32) if with_bias else None
     wd, hd, bd = dev(w), dev(h), None if bias is None else dev(bias)
-    f, s = both(hipdev, lambda: E.logits(wd, 12, hd, vocab, n, bias=bd))
+    f, s = both(hipdev, lambda: E.logits(wd, qt, hd, vocab, n, bias=bd))
     assert np.array_equal(bits(f[0]), bits(s[0]))
     assert np.array_equal(f[1], s[1])
     for t in range(m):
         assert int(s[1][t]) == int(np.argmax(s[0][t]))
     rows = np.unique(np.concatenate([np.arange(40), np.arange(vocab - 40, vocab), rng.integers(0, vocab, 200)]))
     for t in range(m):
-        want, _ = ora.logits(h[t], w[rows], 12, None if bias is None else bias[rows], len(rows), n, 0)
-        S = f32_scales(w[rows], h[t]) + (0 if bias is None else np.abs(bias[rows]))
+        want, _ = ora.logits(h[t], w[rows], qt, None if bias is None else bias[rows], len(rows), n, 0)
+        S = f32_scales(qt, w[rows], h[t]) + (0 if bias is None else np.abs(bias[rows]))
         assert np.all(np.abs(s[0][t][rows] - want) <= TOL * S), f"token {t}"
 
 
