@@ -777,7 +777,10 @@ def sync_costs(dev):
     launch in a HIP graph, against a grid barrier of one workgroup per CU
     (all 256, or the 32 of XCD 0) with agent-scope release/acquire (every
     store visible to every later load on any XCD) or with relaxed atomics
-    only (no data visibility).  Barrier cost = (launch of 101 barriers -
+    only (no data visibility); and a hierarchical barrier (per-XCD arrival
+    counters and release words, relaxed atomics), alone and with a phase's
+    data exchanged through write-through atomic stores and loads (no L2
+    writeback or invalidate).  Barrier cost = (launch of 101 barriers -
     launch of 1) / 100."""
     import torch
 
@@ -797,21 +800,22 @@ def sync_costs(dev):
         g = capture(empties)
         res["empty_launch_us"][f"{grid}x{threads}"] = round(min(timed(g.replay, 3) for _ in range(2)) * 1e3 / 200, 3)
         del g
-    for xcd0 in (0, 1):
-        for mode in (0, 1):
-            per = {}
-            for rounds in (1, 101):
-                def barriers(sp, rounds=rounds):
-                    for _ in range(20):
-                        if lib.exq_bench_barrier(words.data_ptr(), cus, 1024, rounds, mode, xcd0, sp) != 0:
-                            raise RuntimeError("exq_bench_barrier failed")
+    for xcd0, mode in ((0, 0), (0, 1), (1, 0), (1, 1), (0, 2), (0, 3)):
+        per = {}
+        for rounds in (1, 101):
+            def barriers(sp, rounds=rounds, mode=mode, xcd0=xcd0):
+                for _ in range(20):
+                    if lib.exq_bench_barrier(words.data_ptr(), cus, 1024, rounds, mode, xcd0, sp) != 0:
+                        raise RuntimeError("exq_bench_barrier failed")
 
-                g = capture(barriers)
-                per[rounds] = min(timed(g.replay, 2) for _ in range(2)) * 1e3 / 20
-                del g
-            key = ("xcd0_32wg" if xcd0 else f"all_{cus}wg") + ("_release_acquire" if mode == 0 else "_relaxed")
-            res["barrier_us"][key] = {"launch_1_barrier": round(per[1], 3),
-                                      "per_barrier": round((per[101] - per[1]) / 100, 3)}
+            g = capture(barriers)
+            per[rounds] = min(timed(g.replay, 2) for _ in range(2)) * 1e3 / 20
+            del g
+        key = ("xcd0_32wg" if xcd0 else f"all_{cus}wg") + {0: "_release_acquire", 1: "_relaxed",
+                                                           2: "_per_xcd_relaxed",
+                                                           3: "_per_xcd_relaxed_write_through_data"}[mode]
+        res["barrier_us"][key] = {"launch_1_barrier": round(per[1], 3),
+                                  "per_barrier": round((per[101] - per[1]) / 100, 3)}
     torch.cuda.synchronize()
     err = int(words.view(-1)[64].item())
     if err != 0:

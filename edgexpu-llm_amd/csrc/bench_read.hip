@@ -50,11 +50,17 @@ __global__ __launch_bounds__(256) void read_write_kernel(const v4u *__restrict__
 
 __global__ void empty_kernel() {}
 
-// Barrier words: arrivals, finished workgroups, error flag (separate lines).
+// Barrier words: arrivals, finished workgroups, error flag (separate lines);
+// per-XCD arrival counters and release words (one line each) and a phase
+// buffer of 16 words per workgroup for the hierarchical barriers.
 struct BarWords {
     unsigned arrive, pad0[31];
     unsigned done, pad1[31];
     int err, pad2[31];
+    unsigned xcd[8][32];
+    unsigned go[8][32];
+    unsigned data[256 * 16];
+    unsigned sink[256];
 };
 
 // `rounds` grid barriers.  Workgroups of XCD 0 only (b % 8 == 0: workgroups
@@ -95,6 +101,68 @@ __global__ void barrier_kernel(BarWords *w, int rounds, int xcd0, int spin) {
     }
 }
 
+// `rounds` hierarchical grid barriers over all workgroups (gridDim.x a
+// multiple of 8, one per CU): each workgroup arrives on its XCD's counter
+// (workgroup b runs on XCD b % 8), the last arrival of an XCD on the global
+// counter, and the last of those releases every XCD through its own word, so
+// at most gridDim.x / 8 workgroups poll one word.  Relaxed agent-scope
+// atomics only.  MODE 3 also exchanges data the way a persistent kernel's
+// phases would without fences: before arriving, threads 0-15 store the
+// workgroup's 16 words with agent-scope atomic stores (written through to
+// the device-coherent level, no L2 writeback needed); after the barrier every
+// thread reads 4 of the 256 x 16 words with agent-scope atomic loads (no L2
+// invalidate needed) and folds them into a word it stores at the end.  Every
+// wait is bounded as in barrier_kernel; the last workgroup resets the words.
+template <int MODE>
+__global__ __launch_bounds__(1024) void xcd_barrier_kernel(BarWords *w, int rounds, int spin) {
+    const unsigned nx = gridDim.x / 8u;
+    const unsigned xc = blockIdx.x % 8u;
+    unsigned acc = 0u;
+    for (int r = 1; r <= rounds; ++r) {
+        if (MODE == 3 && threadIdx.x < 16)
+            __hip_atomic_store(&w->data[blockIdx.x * 16 + threadIdx.x], (unsigned)r ^ blockIdx.x, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const unsigned old = __hip_atomic_fetch_add(&w->xcd[xc][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (old == (unsigned)r * nx - 1u) {
+                const unsigned g = __hip_atomic_fetch_add(&w->arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (g == (unsigned)r * 8u - 1u)
+                    for (int k = 0; k < 8; ++k)
+                        __hip_atomic_store(&w->go[k][0], (unsigned)r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            int k = 0;
+            while (__hip_atomic_load(&w->go[xc][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (unsigned)r) {
+                if (++k >= spin) {
+                    __hip_atomic_store(&w->err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        __syncthreads();
+        if (MODE == 3) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc ^= __hip_atomic_load(&w->data[(threadIdx.x * 4 + j) % (gridDim.x * 16)], __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (MODE == 3 && threadIdx.x == 0) w->sink[blockIdx.x] = acc;
+    if (threadIdx.x == 0) {
+        const unsigned old = __hip_atomic_fetch_add(&w->done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == gridDim.x - 1u) {
+            __hip_atomic_store(&w->arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int k = 0; k < 8; ++k) {
+                __hip_atomic_store(&w->xcd[k][0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&w->go[k][0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __hip_atomic_store(&w->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
 }  // namespace
 
 // An empty kernel of grid x threads.  0 on success.
@@ -111,11 +179,22 @@ extern "C" long long exq_bench_barrier_words(void) { return (long long)sizeof(Ba
 // (one per CU at 1024 threads: grid <= the CU count keeps every workgroup
 // resident, which the barrier needs).  0 on success; the error flag sits at
 // byte 256 of the words.
+// mode 2 / 3: the hierarchical barrier (xcd_barrier_kernel, all workgroups,
+// grid a multiple of 8, xcd0 ignored), 3 with its data exchange.
 extern "C" int exq_bench_barrier(void *words, int grid, int threads, int rounds, int mode, int xcd0, void *stream) {
     if (words == nullptr || grid < 8 || grid > 256 || threads < 64 || threads > 1024 || rounds < 1 || rounds > 1000 ||
-        (mode != 0 && mode != 1))
+        mode < 0 || mode > 3 || (mode >= 2 && grid % 8 != 0))
         return 1;
     constexpr int kSpin = 1 << 18;
+    if (mode == 2 || mode == 3) {
+        if (mode == 2)
+            hipLaunchKernelGGL(xcd_barrier_kernel<2>, dim3((unsigned)grid), dim3((unsigned)threads), 0,
+                               (hipStream_t)stream, static_cast<BarWords *>(words), rounds, kSpin);
+        else
+            hipLaunchKernelGGL(xcd_barrier_kernel<3>, dim3((unsigned)grid), dim3((unsigned)threads), 0,
+                               (hipStream_t)stream, static_cast<BarWords *>(words), rounds, kSpin);
+        return hipGetLastError() == hipSuccess ? 0 : 2;
+    }
     if (mode == 0)
         hipLaunchKernelGGL(barrier_kernel<0>, dim3((unsigned)grid), dim3((unsigned)threads), 0, (hipStream_t)stream,
                            static_cast<BarWords *>(words), rounds, xcd0, kSpin);

@@ -9,7 +9,7 @@ namespace exq {
 // gemv_fused_more.hip: plain projections of Q4_0 / Q5_0 / Q5_K rows
 hipError_t launch_gemv_fused_more(int type, const FusedArgs &a, bool stage, hipStream_t st);
 // gemv_stream.hip: one to four tokens of Q4_K / Q6_K rows at the decode row lengths
-bool gemv_stream_f32_take(int type, int K, int m, const uint8_t *w);
+bool gemv_stream_f32_take(int type, int K, int m, const uint8_t *w, int n_out);
 hipError_t launch_gemv_stream_f32(int type, int K, int m, const uint8_t *w, int n_out, const float *bias,
                                   float *out, const float *xf, unsigned long long *amax, int *nparts, hipStream_t st);
 bool gemv_stream_take(int type, int K, int m, long long rows, int nmat, const uint8_t *const *w, int code,
@@ -147,7 +147,7 @@ hipError_t launch_gemv_fused_f32(int type, const uint8_t *w, int n_out, const fl
                                  size_t row_bytes, int K, const float *xf, hipStream_t st, unsigned long long *amax,
                                  int *nparts) {
     if (!gemv_fused_f32_supported(type, K)) return hipErrorInvalidValue;
-    if (gemv_stream_f32_take(type, K, 1, w))
+    if (gemv_stream_f32_take(type, K, 1, w, n_out))
         return launch_gemv_stream_f32(type, K, 1, w, n_out, bias, out, xf, amax, nparts, st);
     if (amax != nullptr) return launch_gemv_fused_f32_argmax(type, w, n_out, bias, out, row_bytes, K, xf, st, amax, nparts);
     FusedArgs a{};
@@ -198,7 +198,7 @@ hipError_t launch_gemv_fused_f32(int type, const uint8_t *w, int n_out, const fl
 hipError_t launch_gemv_fused_f32_pair(int type, const uint8_t *w, int n_out, const float *bias, float *out,
                                       size_t row_bytes, int K, const float *xf, hipStream_t st) {
     if ((type != kTypeQ4_K && type != kTypeQ6_K) || !gemv_fused_f32_supported(type, K)) return hipErrorInvalidValue;
-    if (gemv_stream_f32_take(type, K, 2, w))
+    if (gemv_stream_f32_take(type, K, 2, w, n_out))
         return launch_gemv_stream_f32(type, K, 2, w, n_out, bias, out, xf, nullptr, nullptr, st);
     FusedArgs a{};
     a.nmat = 1;

@@ -968,6 +968,8 @@ bool gemv_stream_take(int type, int K, int m, long long rows, int nmat, const ui
     if (!gemv_stream_supported(type, K, m, code, staged) || g_gemv_mode == 1) return false;
     for (int z = 0; z < nmat; ++z)
         if (((uintptr_t)w[z] & 15u) != 0) return false;
+    // a matrix's rows are addressed by 32-bit buffer offsets
+    if (rows * (long long)(K / kQKK) * (type == kTypeQ6_K ? kBytesQ6_K : kBytesQ4_K) >= (1ll << 32)) return false;
     if (g_gemv_mode == 2) return true;
     // Q6_K rows of 9728 from 2048 rows (measured: 10.2 against 11.4 us at
     // 2560 rows, 18.9 against 25.1 at 9728; 7.4 against 6.5 at 1024; two /
@@ -997,8 +999,10 @@ hipError_t launch_gemv_stream(int type, int nmat, const uint8_t *const *w, const
         return hipErrorInvalidValue;
     if ((x == nullptr) == (xq == nullptr) || (xq != nullptr && (pro != 0 || pair))) return hipErrorInvalidValue;
     if (pair && (nmat != 2 || n_out[0] != n_out[1])) return hipErrorInvalidValue;
+    const long long rb = (long long)(K / kQKK) * (type == kTypeQ6_K ? kBytesQ6_K : kBytesQ4_K);
     for (int z = 0; z < nmat; ++z)
-        if (((uintptr_t)w[z] & 15u) != 0) return hipErrorInvalidValue;
+        if (((uintptr_t)w[z] & 15u) != 0 || n_out[z] < 0 || (long long)n_out[z] * rb >= (1ll << 32))
+            return hipErrorInvalidValue;
     StreamArgs a{};
     a.nmat = pair ? 1 : nmat;
     int rows = 0;
@@ -1053,10 +1057,12 @@ hipError_t launch_gemv_stream(int type, int nmat, const uint8_t *const *w, const
 // against 70.7 us (61.5 against 71.9 with the argmax keys and their
 // reduction), two tokens 78.1 against 113.8; both kernels give the same
 // words.
-bool gemv_stream_f32_take(int type, int K, int m, const uint8_t *w) {
+bool gemv_stream_f32_take(int type, int K, int m, const uint8_t *w, int n_out) {
     if (g_gemv_mode == 1 || m < 1 || m > 2) return false;
     if (!(type == kTypeQ4_K && K == 4096) && !(type == kTypeQ6_K && K == 2560)) return false;
-    return ((uintptr_t)w & 15u) == 0;
+    // rows addressed by 32-bit buffer offsets
+    const long long rb = (long long)(K / kQKK) * (type == kTypeQ6_K ? kBytesQ6_K : kBytesQ4_K);
+    return ((uintptr_t)w & 15u) == 0 && n_out >= 1 && (long long)n_out * rb < (1ll << 32);
 }
 
 // scores[t][row] = bias[row] + the f32-activation dot of token t (xf [m][K])
@@ -1065,7 +1071,8 @@ bool gemv_stream_f32_take(int type, int K, int m, const uint8_t *w) {
 hipError_t launch_gemv_stream_f32(int type, int K, int m, const uint8_t *w, int n_out, const float *bias,
                                   float *out, const float *xf, unsigned long long *amax, int *nparts, hipStream_t st) {
     if (!(type == kTypeQ4_K && K == 4096) && !(type == kTypeQ6_K && K == 2560)) return hipErrorInvalidValue;
-    if (m < 1 || m > 2 || (amax != nullptr && m != 1) || ((uintptr_t)w & 15u) != 0 || n_out < 1)
+    if (m < 1 || m > 2 || (amax != nullptr && m != 1) || ((uintptr_t)w & 15u) != 0 || n_out < 1 ||
+        (long long)n_out * (K / kQKK) * (type == kTypeQ6_K ? kBytesQ6_K : kBytesQ4_K) >= (1ll << 32))
         return hipErrorInvalidValue;
     StreamArgs a{};
     a.nmat = 1;
