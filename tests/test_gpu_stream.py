@@ -291,6 +291,26 @@ def test_logits_f32_fused_equals_stream(hipdev, ora, qt, n, vocab, m, with_bias)
         assert np.all(np.abs(s[0][t][rows] - want) <= TOL * S), f"token {t}"
 
 
+@pytest.mark.parametrize("qt,n,off", [(12, 4096, 8), (12, 4096, 4), (14, 2560, 2), (14, 2560, 6)])
+@pytest.mark.parametrize("m", [1, 2])
+def test_logits_at_unaligned_weights_take_the_fused_kernel(hipdev, qt, n, off, m):
+    """The streaming logits read 16-byte transfers from 16-byte-aligned rows;
+    a matrix at another address takes the fused kernel, whose words are the
+    same: scores and greedy indices equal those of the aligned copy."""
+    vocab = 9001
+    rng = np.random.default_rng(7100 + qt + off + m)
+    w = synth.np_weights(qt, vocab, n, rng)
+    h = dev(rng.normal(0, 1, (m, n)).astype(np.float32))
+    buf = torch.zeros(w.nbytes + 256, dtype=torch.uint8, device="cuda:0")
+    wu = buf[off:off + w.nbytes].view(w.shape)
+    wu.copy_(dev(w))
+    assert wu.data_ptr() % 16 == off % 16
+    s_al, b_al = E.logits(dev(w), qt, h, vocab, n)
+    s_un, b_un = E.logits(wu, qt, h, vocab, n)
+    assert np.array_equal(bits(s_al.cpu().numpy()), bits(s_un.cpu().numpy()))
+    assert np.array_equal(b_al.cpu().numpy(), b_un.cpu().numpy())
+
+
 @pytest.mark.parametrize("pro", ["rmsnorm", "silu_mul", "silu_mul_residual", "residual"])
 def test_q6k_layer_variants_fused_equals_stream(hipdev, ora, pro):
     """The Q6_K down projection as a layer issues it (SiLU-mul prologue and
