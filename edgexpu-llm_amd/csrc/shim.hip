@@ -1043,12 +1043,13 @@ bool logits_run(float *scores, uint32_t *best_dev, const float *hidden, const vo
         }
     } else {
         // the other formats use the f32-activation dots (src/native.c:445-462);
-        // K-quant rows: one hidden vector in a fused launch whose store also
-        // keeps each wave's greedy-argmax key (one small launch then reduces
-        // those keys instead of re-reading the scores); several in fused
-        // launches of two (the weights read once per pair), then the argmax
-        // over the scores.  A row's score does not depend on m, as in the
-        // reference's per-token loop.
+        // K-quant rows: one hidden vector in a launch (the streaming kernel for
+        // Q4_K rows of 4096 and Q6_K rows of 2560 at 16-byte addresses, the
+        // fused one otherwise, same words) that also keeps each workgroup's
+        // greedy-argmax key (one small launch then reduces those keys instead
+        // of re-reading the scores); several in launches of two (the weights
+        // read once per pair), then the argmax over the scores.  A row's score
+        // does not depend on m, as in the reference's per-token loop.
         if (m == 1 && best_dev != nullptr && k_family((int)type) && gemv_fused_f32_supported((int)type, n_embd)) {
             int nparts = 0;
             for (int t = 0; t < m; ++t) {

@@ -71,18 +71,24 @@ int edgexpu_hip_supports_type(uint32_t type);
 int edgexpu_hip_set_prefill_mode(int mode);
 int edgexpu_hip_prefill_mode(void);
 /* Decode GEMV kernel for the launches both kernels cover: one token of Q4_K
- * rows of 2560, 4096 or 14336 elements; plain projections of 2-4 tokens of
- * Q4_K rows of 2560 or 4096; one token of Q6_K rows of 9728 (activations
- * given as f32).  No reference counterpart (the reference has one CPU
- * kernel).
+ * rows of 2560, 4096 or 14336 elements or of Q6_K rows of 9728 (every
+ * variant), plain projections of 2-4 tokens of those rows (activations
+ * given as f32), and the f32-activation logits of one or two tokens against
+ * Q4_K rows of 4096 or Q6_K rows of 2560.  No reference counterpart (the
+ * reference has one CPU kernel).
  *  EDGEXPU_HIP_GEMV_AUTO (default): the streaming kernel (weight rows
- *    through LDS by DMA), except launches of fewer than 2048 rows of 14336
- *    Q4_K or 9728 Q6_K elements, which take the fused kernel;
- *  EDGEXPU_HIP_GEMV_FUSED / EDGEXPU_HIP_GEMV_STREAM: always that kernel.
+ *    through LDS by DMA), except launches of fewer than 2048 rows of 9728
+ *    Q6_K elements or of 14336 Q4_K elements at 1-3 tokens, which take the
+ *    fused kernel;
+ *  EDGEXPU_HIP_GEMV_FUSED / EDGEXPU_HIP_GEMV_STREAM: always that kernel
+ *    (FUSED at four tokens of 14336 elements, whose codes exceed the fused
+ *    kernel's LDS: a quantize launch and the generic GEMV).
  * The two give the same outputs bit for bit (same lane partials, same
- * reduction order), so the setting moves time, never results.  Process-wide
- * setting of this library.  Returns 1, or 0 (sticky error) for an unknown
- * mode. */
+ * reduction order), so the setting moves time, never results -- except four
+ * tokens of 14336 elements, where the generic GEMV's summation order differs
+ * (both within 1e-5 of each row's conditioning scale of the reference).
+ * Process-wide setting of this library.  Returns 1, or 0 (sticky error) for
+ * an unknown mode. */
 #define EDGEXPU_HIP_GEMV_AUTO 0
 #define EDGEXPU_HIP_GEMV_FUSED 1
 #define EDGEXPU_HIP_GEMV_STREAM 2
@@ -128,9 +134,9 @@ int edgexpu_hip_weight_n_in(const edgexpu_hip_weight *w);
  * address except that Q8_0, Q4_0, Q5_0 and Q6_K blocks (34, 18, 22 and 210
  * bytes) must start at an even one: an odd one is refused with error -2.
  * GGUF tensors in a device copy of a file's data section always qualify.
- * Blocks at 16-byte addresses can take the streaming GEMV (Q4_K, Q6_K) and
- * the matrix-core prefill (Q4_K; the others need even addresses); blocks
- * elsewhere take the fused GEMV, with the same results. ---- */
+ * Blocks at 16-byte addresses can take the streaming GEMV and logits (Q4_K,
+ * Q6_K) and the matrix-core prefill (Q4_K; the others need even addresses);
+ * blocks elsewhere take the fused GEMV, with the same results. ---- */
 
 /* out[t*n_out + o] = bias[o] + dot(W[o], q8(x[t]))  for t < m.
  * Replaces edgexpu_cpu_linear_quant_batch (include/edgexpu/cpu_kernel.h:71-80,
