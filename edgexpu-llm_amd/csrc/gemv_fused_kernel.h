@@ -352,7 +352,7 @@ struct FusedLds {
 // figures for the wide Q6_K weight registers and the staging prologues are
 // capped in fused_occupancy_pro so that no instantiation spills (under
 // -Rpass-analysis=kernel-resource-usage every instantiation in this library
-// reports 0 bytes of scratch but one, named there).
+// reports 0 bytes of scratch).
 template <class Fmt>
 constexpr int fused_occupancy(int r, int m, int loop) {
     // f32-activation formats: the activation slice (32 to 68 floats) stays
@@ -380,10 +380,11 @@ constexpr int fused_occupancy(int r, int m, int loop) {
 //   Q6_K rows (56 bytes of weight registers per unit): 4 for one or two rows
 //   per slot; four rows per slot: 2 under a prologue or a gate/up pair
 //   (whose two rows per slot hold twice the weights).
-// One exception is deliberate: the Q4_K logits kernel with the argmax
-// epilogue (f32 activation, two rows per slot) runs at 4 with 16 bytes of
-// scratch per lane rather than at 3 without (77.9 against 82.4 us for the
-// [128256 x 4096] product); at 3 its two workgroups per CU no longer fit.
+// The Q4_K logits kernel with the argmax epilogue (f32 activation, two rows
+// per slot) is held to 4, not the 3 of the other f32 shapes: at 3 its two
+// workgroups per CU no longer fit (77.9 against 82.4 us for the [128256 x
+// 4096] product, when it still needed 16 bytes of scratch per lane at 4;
+// since the codes convert two at a time it fits 4 without any).
 template <class Fmt>
 constexpr int fused_occupancy_pro(int r, int m, int loop, int pro) {
     const bool wide = sizeof(typename Fmt::W) > 48;
