@@ -192,13 +192,6 @@ __device__ __forceinline__ float rms_scale(double ss, int n, float eps) {
     return 1.0f / sqrtf(mean + eps);
 }
 
-// Sum of a double over the 64 lanes of a wave (every lane gets the total).
-__device__ __forceinline__ double wave_sum_f64(double s) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-    return s;
-}
-
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
     return __shfl_xor(v, mask, 64);
 }
@@ -217,6 +210,21 @@ __device__ __forceinline__ float reduce_partner(float v, int off) {
         case 16: return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f));
         default: return shfl_xor_f(v, off);
     }
+}
+
+// Sum of a double over the 64 lanes of a wave (every lane gets the total):
+// partners l ^ 32, ^ 16, ..., ^ 1 in that order, each double moved as its
+// two words by reduce_partner (bpermute for ^ 32, swizzles and DPP below),
+// so every lane adds the same pairs in the same order.
+__device__ __forceinline__ double wave_sum_f64(double s) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint64_t b = __builtin_bit_cast(uint64_t, s);
+        const uint32_t lo = __float_as_uint(reduce_partner(__uint_as_float((uint32_t)b), off));
+        const uint32_t hi = __float_as_uint(reduce_partner(__uint_as_float((uint32_t)(b >> 32)), off));
+        s += __builtin_bit_cast(double, (uint64_t)lo | ((uint64_t)hi << 32));
+    }
+    return s;
 }
 
 // Sum of V per-lane values over aligned groups of G lanes (G a power of two
