@@ -265,7 +265,7 @@ def f32_scales(qt, w, h):
 
 @pytest.mark.parametrize("qt,n", [(12, 4096), (14, 2560)])
 @pytest.mark.parametrize("vocab,m,with_bias", [(20000, 1, True), (3001, 1, False), (2048 * 64 + 5, 1, False),
-                                               (20000, 2, True), (3001, 3, False)])
+                                               (20000, 2, True), (3001, 3, False), (1, 1, True), (7, 2, False)])
 def test_logits_f32_fused_equals_stream(hipdev, ora, qt, n, vocab, m, with_bias):
     """The f32-activation logits of Q4_K rows of 4096 and Q6_K rows of 2560
     (one hidden vector with the greedy-argmax keys, or several in launches
@@ -284,7 +284,8 @@ def test_logits_f32_fused_equals_stream(hipdev, ora, qt, n, vocab, m, with_bias)
     assert np.array_equal(f[1], s[1])
     for t in range(m):
         assert int(s[1][t]) == int(np.argmax(s[0][t]))
-    rows = np.unique(np.concatenate([np.arange(40), np.arange(vocab - 40, vocab), rng.integers(0, vocab, 200)]))
+    rows = np.unique(np.concatenate([np.arange(min(vocab, 40)), np.arange(max(0, vocab - 40), vocab),
+                                     rng.integers(0, vocab, 200)]))
     for t in range(m):
         want, _ = ora.logits(h[t], w[rows], qt, None if bias is None else bias[rows], len(rows), n, 0)
         S = f32_scales(qt, w[rows], h[t]) + (0 if bias is None else np.abs(bias[rows]))
