@@ -70,8 +70,9 @@ struct StreamArgs {
 
 // flags: bits 0-1 prologue (1 RMSNorm, 2 SiLU-mul), 4 residual, 8 gate/up
 // pairs, 16 activation already in Q8_K block bytes, 32 f32 activation (the
-// f32-activation dot of the logits, not quantized), 64 greedy-argmax keys
-constexpr int kSRes = 4, kSPair = 8, kSXq = 16, kSF32 = 32, kSArgmax = 64;
+// f32-activation dot of the logits, not quantized), 64 greedy-argmax keys,
+// 128 two adjacent rows of one matrix per step
+constexpr int kSRes = 4, kSPair = 8, kSXq = 16, kSF32 = 32, kSArgmax = 64, kSRow2 = 128;
 
 __device__ __forceinline__ v4u_t s_rsrc(const void *base, uint32_t bytes) {
     const uint64_t a = (uint64_t)(uintptr_t)base;
@@ -304,7 +305,7 @@ struct StreamGeom {
     static constexpr int U = 4 * KSB;                    // units per row
     static constexpr int T = (U + 63) / 64;              // units per lane
     static constexpr int RB = KSB * (Q6 ? kBytesQ6_K : kBytesQ4_K);  // row bytes
-    static constexpr int RPS = (FL & kSPair) ? 2 : 1;    // rows per step
+    static constexpr int RPS = (FL & (kSPair | kSRow2)) ? 2 : 1;  // rows per step
     // Q4_K rows are whole 16-byte transfers.  A Q6_K row starts s = 0, 4, 8
     // or 12 bytes past a 16-byte boundary: its slot takes the 16-byte
     // transfers from that boundary that end inside the row (F of them, F
@@ -341,6 +342,8 @@ struct StreamGeom {
     static_assert(AREA % 16 == 0, "slot alignment");
     static_assert(M == 1 || (FL & ~kSF32) == 0, "several tokens: plain projections");
     static_assert(XREG || (FL & kSXq) == 0, "Q8_K block input: the slices in registers");
+    static_assert(!(FL & kSRow2) || ((FL & ~(kSRow2 | 1)) == 0 && M == 1 && !Q6),
+                  "row pairs: one token of Q4_K projections, RMSNorm prologue or none");
 };
 
 template <int KSB, int NW, int NB, int FL, bool DEEP, int M = 1, int TYPE = kTypeQ4_K>
@@ -349,7 +352,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     constexpr bool Q6 = G::Q6;
     constexpr int PRO = FL & 3;
     constexpr bool kRes = (FL & kSRes) != 0, kPair = (FL & kSPair) != 0, kXq = (FL & kSXq) != 0;
-    constexpr bool kF32 = G::F32, kArgmax = (FL & kSArgmax) != 0;
+    constexpr bool kF32 = G::F32, kArgmax = (FL & kSArgmax) != 0, kRow2 = (FL & kSRow2) != 0;
     constexpr int NS = G::NS;
     extern __shared__ __align__(16) uint8_t smem[];
     int8_t *lq = reinterpret_cast<int8_t *>(smem);
@@ -381,7 +384,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     auto issue = [&](int b, int step) {
         const bool ok = step < last;
         const Mat m = locate(ok ? step : 0);
-        const uint32_t so = ok ? (uint32_t)m.row * G::RB : 0u;
+        // row pairs: step row r of the matrix is rows 2r and 2r + 1
+        const uint32_t so = ok ? (uint32_t)m.row * (kRow2 ? 2u : 1u) * G::RB : 0u;
         const uint32_t vo = ok ? (uint32_t)lane * 16u : 0x7ff00000u;
         if constexpr (Q6) {
             // every transfer lies inside the row or the rows before it
@@ -402,12 +406,13 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
         }
 #pragma unroll
         for (int r = 0; r < G::RPS; ++r) {
-            const v4u_t rs = s_rsrc(r == 0 ? m.w : a.w[1], (uint32_t)m.n_out * G::RB);
+            const v4u_t rs = s_rsrc(r == 0 || kRow2 ? m.w : a.w[1], (uint32_t)m.n_out * G::RB);
             const uint32_t dst = ring_lds + b * G::SB + r * G::RB;
+            const uint32_t sr = so + (kRow2 ? (uint32_t)r * G::RB : 0u);
 #pragma unroll
-            for (int k = 0; k < G::CH; ++k) s_dma16_nt(dst + k * 1024, vo, rs, so + k * 1024);
+            for (int k = 0; k < G::CH; ++k) s_dma16_nt(dst + k * 1024, vo, rs, sr + k * 1024);
             if constexpr (G::PL > 0) {
-                if (lane < G::PL) s_dma16_nt(dst + G::CH * 1024, vo, rs, so + G::CH * 1024);
+                if (lane < G::PL) s_dma16_nt(dst + G::CH * 1024, vo, rs, sr + G::CH * 1024);
             }
         }
     };
@@ -621,7 +626,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
         lane_out(ok ? step : 0, out, row, bias, resid, n_out);
         Epi e{0.0f, 0.0f, 0.0f};
         if (ok) {
-            e.b0 = bias != nullptr ? bias[row] : 0.0f;
+            if constexpr (kRow2) {
+                e.b0 = bias != nullptr ? bias[2 * row] : 0.0f;
+                e.b1 = bias != nullptr ? bias[2 * row + 1] : 0.0f;
+            } else {
+                e.b0 = bias != nullptr ? bias[row] : 0.0f;
+            }
             if constexpr (kPair) e.b1 = a.bias[1] != nullptr ? a.bias[1][row] : 0.0f;
             if constexpr (kRes) e.r = resid != nullptr ? resid[row] : 0.0f;
         }
@@ -646,6 +656,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
                 float o = v;
                 if constexpr (kRes) o = resid != nullptr ? e.r + v : v;
                 if constexpr (kPair) o = silu_f32(v) * (e.b1 + keep1);
+                if constexpr (kRow2) {
+                    out[2 * row] = o;
+                    out[2 * row + 1] = e.b1 + keep1;
+                    continue;
+                }
                 out[(size_t)m * n_out + row] = o;
                 if constexpr (kArgmax) {
                     const unsigned long long key = score_key(o, (unsigned)row);
@@ -805,7 +820,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
         }
 #pragma unroll
         for (int m = 0; m < M; ++m) keep[m] = lane == k64 ? acc[m][0] : keep[m];
-        if constexpr (kPair) keep1 = lane == k64 ? acc[0][G::RPS - 1] : keep1;
+        if constexpr (kPair || kRow2) keep1 = lane == k64 ? acc[0][G::RPS - 1] : keep1;
         advance();
     };
     // the first NS steps: their rows came with the start, so fewer stay in flight after each
@@ -926,8 +941,13 @@ hipError_t launch_stream_flags(int fl, const StreamArgs &a, hipStream_t st) {
         case kSPair: return launch_stream<KSB, NW, NB, kSPair>(a, st);
         case 1 | kSPair: return launch_stream<KSB, NW, NB, 1 | kSPair>(a, st);
         case kSXq: return launch_stream<KSB, NW, NB, kSXq>(a, st);
-        default: return hipErrorInvalidValue;
+        default: break;
     }
+    if constexpr (KSB == 10 && NB == 1) {
+        if (fl == kSRow2) return launch_stream<KSB, NW, NB, kSRow2>(a, st);
+        if (fl == (1 | kSRow2)) return launch_stream<KSB, NW, NB, 1 | kSRow2>(a, st);
+    }
+    return hipErrorInvalidValue;
 }
 
 }  // namespace
@@ -1003,6 +1023,20 @@ hipError_t launch_gemv_stream(int type, int nmat, const uint8_t *const *w, const
     for (int z = 0; z < nmat; ++z)
         if (((uintptr_t)w[z] & 15u) != 0 || n_out[z] < 0 || (long long)n_out[z] * rb >= (1ll << 32))
             return hipErrorInvalidValue;
+    // one token of rows of 2560, no residual, long launches: two adjacent
+    // rows of a matrix per step (the steps and row_start count row pairs)
+    // where every wave takes at least four pairs and the longest wave takes
+    // no more rows than with single rows
+    bool row2 = type == kTypeQ4_K && K == 2560 && m == 1 && !pair && !any_resid && xq == nullptr && (pro & 3) <= 1;
+    long long all_rows = 0;
+    for (int z = 0; z < nmat; ++z) {
+        row2 = row2 && n_out[z] % 2 == 0;
+        all_rows += n_out[z];
+    }
+    if (row2) {
+        const long long waves = (long long)device_cus() * 8, pairs = all_rows / 2;
+        row2 = pairs >= 4 * waves && 2 * ((pairs + waves - 1) / waves) <= (all_rows + waves - 1) / waves;
+    }
     StreamArgs a{};
     a.nmat = pair ? 1 : nmat;
     int rows = 0;
@@ -1017,7 +1051,7 @@ hipError_t launch_gemv_stream(int type, int nmat, const uint8_t *const *w, const
     }
     for (int z = 0; z < a.nmat; ++z) {
         a.row_start[z] = rows;
-        rows += n_out[z];
+        rows += row2 ? n_out[z] / 2 : n_out[z];
     }
     for (int z = a.nmat; z <= kStreamMaxMats; ++z) a.row_start[z] = rows;
     a.nrows = rows;
@@ -1042,9 +1076,14 @@ hipError_t launch_gemv_stream(int type, int nmat, const uint8_t *const *w, const
     }
     // measured on the Llama-3-8B / hybrid decode shapes: 8 waves per CU, two
     // slots per wave, one slot where a row is 8 KB (K = 14336: two, 12.7
-    // against 10.9 us at [4096 x 14336])
+    // against 10.9 us at [4096 x 14336]).  Row pairs of 2560 (2880 bytes a
+    // step) take one slot: gate+up [19456 x 2560] 8.07 against 8.9 us with
+    // single rows (two slots of pairs 8.27, three 8.8); pairs of rows of
+    // 4096 were no faster ([28672 x 4096] 12.8-13.1 against 12.8 us).
     switch (K) {
-        case 2560: return launch_stream_flags<10, 8, 2>(fl, a, st);
+        case 2560:
+            if (row2) return launch_stream_flags<10, 8, 1>(fl | kSRow2, a, st);
+            return launch_stream_flags<10, 8, 2>(fl, a, st);
         case 4096: return launch_stream_flags<16, 8, 2>(fl, a, st);
         default: return launch_stream_flags<56, 8, 1>(fl, a, st);
     }

@@ -8,8 +8,9 @@ fused kernel (csrc/gemv_fused_kernel.h) or the streaming kernel
 same roundings and sum the lanes with the same xor tree, so every output is
 the same word whichever kernel runs -- the plain projection, grouped
 launches, the RMSNorm and SiLU-mul staging prologues, the residual store,
-gate/up pairs with silu(gate) * up, and activations given as Q8_K block
-bytes.  Each variant is also held to the oracle (the reference's
+gate/up pairs with silu(gate) * up, activations given as Q8_K block bytes,
+and (one token of rows of 2560 or 4096 in long launches, every matrix of an
+even row count) two adjacent rows per step.  Each variant is also held to the oracle (the reference's
 edgexpu_cpu_linear_quant_batch, src/cpu_kernel.c:545-644) within the usual
 1e-5 of the conditioning scale, so the agreement is between two correct
 results, not two copies of one mistake.
@@ -56,7 +57,7 @@ def cond(ora, w, x):
 
 SHAPES = [(4096, (14336, 14336)), (4096, (4096, 1024, 1024)), (4096, (4096,)), (4096, (33,)),
           (14336, (4096,)), (14336, (2048,)), (14336, (300,)), (2560, (9728, 9728)), (2560, (4096, 1024, 1024)),
-          (2560, (7,))]
+          (2560, (7,)), (2560, (2, 18430, 6)), (4096, (2, 18430, 6)), (2560, (4, 1031))]
 
 
 @pytest.mark.parametrize("n_in,n_outs", SHAPES)
@@ -181,22 +182,25 @@ def test_tokens_fused_equals_stream(hipdev, ora, n_in, n_outs, m):
         assert np.all(np.abs(s[z][:, sample] - want) <= TOL * S), f"matrix {z}"
 
 
-@pytest.mark.parametrize("m", [1, 2])
-def test_more_than_64_steps_per_wave(hipdev, ora, m):
-    """A launch long enough that every wave takes more than 64 rows: the
+@pytest.mark.parametrize("m,pairs", [(1, False), (2, False), (1, True)])
+def test_more_than_64_steps_per_wave(hipdev, ora, m, pairs):
+    """A launch long enough that every wave takes more than 64 steps: the
     totals kept in lanes are flushed every 64 steps and the bias prefetched
     again, then a partial flush at the end (131 849 rows of 2560: 64 full
-    steps of the 2048 waves of 256 CUs, and 777 rows more)."""
-    n_in, n_out = 2560, 2048 * 64 + 777
-    rng = np.random.default_rng(64 + m)
+    steps of the 2048 waves of 256 CUs, and 777 rows more; an even count of
+    rows, one token: 131 849 steps of two adjacent rows)."""
+    n_in, n_out = 2560, (2048 * 64 + 777) * (2 if pairs else 1)
+    rng = np.random.default_rng(64 + m + 10 * pairs)
     w = synth.np_weights(12, n_out, n_in, rng)
     x = synth.np_activations(m, n_in, rng)
     bias = rng.normal(0, 0.3, n_out).astype(np.float32)
     wd, bd = dev(w), dev(bias)
     f, s = both(hipdev, lambda: [E.linear_quant_batch(wd, 12, dev(x), n_out, n_in, bias=bd)])
     assert np.array_equal(bits(f[0]), bits(s[0]))
+    r = 2 if pairs else 1
     sample = np.unique(np.concatenate([np.arange(0, n_out, 997), np.arange(n_out - 40, n_out),
-                                       np.arange(2048 * 63, 2048 * 63 + 40), np.arange(2048 * 64 - 20, 2048 * 64 + 20)]))
+                                       np.arange(r * 2048 * 63, r * 2048 * 63 + 40),
+                                       np.arange(r * 2048 * 64 - 20, r * 2048 * 64 + 20)]))
     want = ora.linear_quant_batch(x, w[sample], 12, bias[sample], m, len(sample), n_in)
     S = np.stack([cond(ora, w[sample], x[t:t + 1])[0] for t in range(m)]) + np.abs(bias[sample])[None, :]
     assert np.all(np.abs(s[0][:, sample] - want) <= TOL * S)
