@@ -82,98 +82,180 @@ constexpr int kMaxSplit = 4;
 
 // --------------------------------------------------------------- packing
 
-constexpr int kPackTokensPerWave = 1;
-constexpr int kPackWaves = 8;  // consecutive tokens of one super-block per workgroup
+constexpr int kPackWaves = 8;  // workgroup of the pack kernels
 constexpr int kPackThreads = 64 * kPackWaves;
+constexpr int kPackF32Tokens = 4;  // tokens per wavefront of the f32 pack
 
-// The pack kernel: one wavefront per (super-block, token), 8 wavefronts (8
-// consecutive tokens, whose 16-byte vectors fill 128-byte lines) per
-// workgroup, everything in registers.  Per token the wave quantizes the
-// block (Q8_K, bit-identical to quantize_q8_k_kernel) or reads its Q8_K
-// bytes; lane l then holds elements 4l .. 4l+3.  The 16-byte code vector of
-// (half hf, K-step s, lane half h) holds elements 64 j + 4 s .. + 3 (low
-// nibble positions, lane 16 j + s) and 64 j + 32 + 4 s .. + 3 (high, lane
-// 16 j + 8 + s) with j = 2 h + hf, so lane 16 j + s writes it after one
-// exchange with lane 16 j + s + 8.  Tokens past m get zero codes and d = 0.
-template <bool F32IN>
-__global__ __launch_bounds__(kPackThreads) void q8k_pack_kernel(const float *__restrict__ x, int ldx,
-                                                       const uint8_t *__restrict__ xq, size_t xq_stride, int m,
-                                                       int K, int ntb, uint8_t *__restrict__ pack) {
+// Code vectors of the pack: the 16-byte vector of (half hf, K-step s, lane
+// half h) holds elements 64 j + 4 s .. + 3 (the low nibble positions of qs
+// bytes 32 j + 4 s .. + 3) and 64 j + 32 + 4 s .. + 3 (their high nibbles)
+// with j = 2 h + hf, as fp16 [lo 0, lo 2, hi 0, hi 2, lo 1, lo 3, hi 1, hi 3].
+// Tokens past m get zero codes and d = 0.
+
+// The f32 pack kernel: one wavefront per (super-block, 4 consecutive
+// tokens), 8 wavefronts (32 tokens, one MFMA token tile) per workgroup,
+// everything in registers.  The 16 lanes 16 t4 + 4 j + q of token t4 hold
+// its elements 64 j + 8 q .. + 7 and 64 j + 32 + 8 q .. + 7: the code vectors
+// of K-steps 2 q and 2 q + 1 of half j & 1, lane half j >> 1, with no
+// exchange.  The Q8_K quantization (src/gguf_dot_q8.c:360-412) runs over a
+// 16-lane row: the largest |x| (zeros and NaN never enter) by a row max, the
+// sign of its first element by a row min over (index, sign) keys, then
+// iscale = -127 / max and each code as quantize_q8_k_kernel forms it, so
+// every code, d, bsum and sum |q| is that kernel's.
+__global__ __launch_bounds__(kPackThreads) void q8k_pack_f32_kernel(const float *__restrict__ x, int ldx, int m,
+                                                                    int K, int ntb, uint8_t *__restrict__ pack) {
     const int nb = K / kQKK;
     const int sb = (int)blockIdx.x % nb, tg = (int)blockIdx.x / nb;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int tbase = (tg * kPackWaves + wave) * kPackTokensPerWave;
-    // all the wave's loads first
-    float4 xv[kPackTokensPerWave];
-    uint32_t qw[kPackTokensPerWave], dw[kPackTokensPerWave], bw[kPackTokensPerWave];
-#pragma unroll
-    for (int i = 0; i < kPackTokensPerWave; ++i) {
-        const int t = tbase + i;
-        if (F32IN) {
-            xv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (t < m) xv[i] = *reinterpret_cast<const float4 *>(x + (size_t)t * ldx + (size_t)sb * kQKK + lane * 4);
-        } else {
-            qw[i] = dw[i] = bw[i] = 0u;
-            if (t < m) {
-                const uint8_t *blk = xq + (size_t)t * xq_stride + (size_t)sb * kBytesQ8_K;
-                qw[i] = ldg4(blk + 4 + 4 * lane);
-                dw[i] = ldg4(blk);
-                bw[i] = ldg4(blk + 260 + 4 * (lane >> 3));  // bsums 2k, 2k+1 of k = lane >> 2
-            }
+    const int t4 = lane >> 4, r = lane & 15, j = r >> 2, q = r & 3;
+    const int t = (tg * kPackWaves + wave) * kPackF32Tokens + t4;
+    // xs[i] = element 64 j + 8 q + i, xs[8 + i] = element 64 j + 32 + 8 q + i
+    float xs[16];
+    {
+        float4 v[4] = {};
+        if (t < m) {
+            const float *src = x + (size_t)t * ldx + (size_t)sb * kQKK + 64 * j + 8 * q;
+            v[0] = *reinterpret_cast<const float4 *>(src);
+            v[1] = *reinterpret_cast<const float4 *>(src + 4);
+            v[2] = *reinterpret_cast<const float4 *>(src + 32);
+            v[3] = *reinterpret_cast<const float4 *>(src + 36);
         }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            xs[4 * k] = v[k].x;
+            xs[4 * k + 1] = v[k].y;
+            xs[4 * k + 2] = v[k].z;
+            xs[4 * k + 3] = v[k].w;
+        }
+    }
+    uint32_t bb[16], amax_bits = 0u;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float av = fabsf(xs[i]);
+        bb[i] = av > 0.0f ? __float_as_uint(av) : 0u;  // non-negative floats order as their bits
+        amax_bits = max(amax_bits, bb[i]);
+    }
+    amax_bits = row16_max_u32(amax_bits);
+    // the lane's first element holding the maximum (its elements ascend with
+    // i), as the key 2 * index + sign; the row's smallest key is the block's
+    uint32_t key = 0xffffffffu;
+    const uint32_t base = 2u * (uint32_t)(64 * j + 8 * q);
+#pragma unroll
+    for (int i = 15; i >= 0; --i) {
+        const uint32_t off = 2u * (uint32_t)(i < 8 ? i : 24 + i);
+        key = bb[i] == amax_bits ? base + off + (xs[i] < 0.0f ? 1u : 0u) : key;
+    }
+    key = row16_min(key);
+    const bool zero = amax_bits == 0u;
+    const float amax = __uint_as_float(amax_bits);
+    const float maxv = (key & 1u) != 0u ? -amax : amax;
+    const float iscale = -127.0f / maxv;
+    int qv[16], lo8 = 0, hi8 = 0, sq = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float pv = iscale * xs[i];
+        // lrintf: a NaN or infinite product gives LONG_MIN, whose low 32 bits are 0
+        int c = fabsf(pv) < 2147483648.0f ? (int)rintf(pv) : 0;
+        c = c > 127 ? 127 : (c < -127 ? -127 : c);
+        c = zero ? 0 : c;
+        qv[i] = c;
+        if (i < 8)
+            lo8 += c;
+        else
+            hi8 += c;
+        sq += abs(c);
+    }
+    const float d = zero ? 0.0f : 1.0f / iscale;
+    // bsums: lanes q and q ^ 1 share the 16-element groups 4 j + q / 2 (low)
+    // and 4 j + 2 + q / 2 (high); lane q = 0 then takes groups 4 j + 1 and
+    // 4 j + 3 from lane q = 2
+    lo8 += (int)dpp_u32<kDppXor1>((uint32_t)lo8);
+    hi8 += (int)dpp_u32<kDppXor1>((uint32_t)hi8);
+    const int lo_n = (int)dpp_u32<kDppXor2>((uint32_t)lo8), hi_n = (int)dpp_u32<kDppXor2>((uint32_t)hi8);
+    sq += (int)dpp_u32<kDppXor1>((uint32_t)sq);
+    sq += (int)dpp_u32<kDppXor2>((uint32_t)sq);
+    sq += (int)dpp_u32<kDppHalfMirror>((uint32_t)sq);
+    sq += (int)dpp_u32<kDppMirror>((uint32_t)sq);
+
+    const int tb = t / kTokB, tt = (t % kTokB) / 32, tl = t % 32;
+    const int h = j >> 1, hf = j & 1;
+    uint8_t *blk = pack + ((size_t)sb * ntb + tb) * kPkBlk;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int s = 2 * q + u;
+        v4u o;
+        o[0] = h2_bits(qv[4 * u], qv[4 * u + 2]);
+        o[1] = h2_bits(qv[8 + 4 * u], qv[8 + 4 * u + 2]);
+        o[2] = h2_bits(qv[4 * u + 1], qv[4 * u + 3]);
+        o[3] = h2_bits(qv[8 + 4 * u + 1], qv[8 + 4 * u + 3]);
+        *reinterpret_cast<v4u *>(blk + hf * kPkHalf + (s * kTiles + tt) * 1024 + (tl + 32 * h) * 16) = o;
+    }
+    // min-term vector of lane half h: bsums 8 h .. 8 h + 7 as fp16 pairs; this
+    // row's groups 4 j .. 4 j + 3 are its bytes 8 hf .. 8 hf + 7
+    if (q == 0) {
+        uint2 o;
+        o.x = h2_bits(lo8, lo_n);
+        o.y = h2_bits(hi8, hi_n);
+        *reinterpret_cast<uint2 *>(blk + kPkCodes + tt * 1024 + (tl + 32 * h) * 16 + 8 * hf) = o;
+    }
+    if (r == 0) {
+        *reinterpret_cast<float *>(blk + kPkCodes + kPkMn + 4 * (32 * tt + tl)) = d;
+        *reinterpret_cast<int *>(blk + kPkCodes + kPkMn + kPkDx + 4 * (32 * tt + tl)) = sq;
+    }
+}
+
+// The Q8_K-block pack kernel: one wavefront per (super-block, token), 8
+// wavefronts (8 consecutive tokens, whose 16-byte vectors fill 128-byte
+// lines) per workgroup.  Lane l reads the codes of elements 4 l .. 4 l + 3,
+// so lane 16 j + s writes the code vector of K-step s of half j & 1, lane
+// half j >> 1 after one exchange with lane 16 j + s + 8.
+__global__ __launch_bounds__(kPackThreads) void q8k_pack_blocks_kernel(const uint8_t *__restrict__ xq,
+                                                                       size_t xq_stride, int m, int K, int ntb,
+                                                                       uint8_t *__restrict__ pack) {
+    const int nb = K / kQKK;
+    const int sb = (int)blockIdx.x % nb, tg = (int)blockIdx.x / nb;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = tg * kPackWaves + wave;
+    uint32_t word = 0u, dw = 0u, bw = 0u;
+    if (t < m) {
+        const uint8_t *blk = xq + (size_t)t * xq_stride + (size_t)sb * kBytesQ8_K;
+        word = ldg4(blk + 4 + 4 * lane);
+        dw = ldg4(blk);
+        bw = ldg4(blk + 260 + 4 * (lane >> 3));  // bsums 2k, 2k+1 of k = lane >> 2
     }
     const int j = lane >> 4, s8 = lane & 7;
     const int h = j >> 1, hf = j & 1;
+    const int tb = t / kTokB, tt = (t % kTokB) / 32, tl = t % 32;
+    uint8_t *blk = pack + ((size_t)sb * ntb + tb) * kPkBlk;
+    int q[4];
 #pragma unroll
-    for (int i = 0; i < kPackTokensPerWave; ++i) {
-        const int t = tbase + i;
-        const int tb = t / kTokB, tt = (t % kTokB) / 32, tl = t % 32;
-        uint8_t *blk = pack + ((size_t)sb * ntb + tb) * kPkBlk;
-        int q[4];
-        int bsum;
-        float d;
-        uint32_t word;
-        if (F32IN) {
-            const Q8KLane r = q8k_quantize_lane(xv[i], lane);
+    for (int e = 0; e < 4; ++e) q[e] = sbyte(word, e);
+    const float d = __uint_as_float(dw);
+    const int bsum = (int)(int16_t)((bw >> (16 * ((lane >> 2) & 1))) & 0xffffu);
+    const int sq = wave_sum(abs(q[0]) + abs(q[1]) + abs(q[2]) + abs(q[3]));
+    const uint32_t hiw = (uint32_t)__shfl_xor((int)word, 8, 64);
+    if ((lane & 8) == 0) {
+        v4u o;
+        o[0] = h2_bits(sbyte(word, 0), sbyte(word, 2));
+        o[1] = h2_bits(sbyte(hiw, 0), sbyte(hiw, 2));
+        o[2] = h2_bits(sbyte(word, 1), sbyte(word, 3));
+        o[3] = h2_bits(sbyte(hiw, 1), sbyte(hiw, 3));
+        *reinterpret_cast<v4u *>(blk + hf * kPkHalf + (s8 * kTiles + tt) * 1024 + (tl + 32 * h) * 16) = o;
+    }
+    // min-term vector of lane half hh = lane (lanes 0, 1): bsums 8 hh .. 8 hh + 7,
+    // held by lanes 32 hh + 4 k
+    int bv[8];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) q[e] = r.q[e];
-            word = r.word;
-            d = r.d;
-            bsum = r.sum4;
-            bsum += __shfl_xor(bsum, 1, 64);
-            bsum += __shfl_xor(bsum, 2, 64);
-        } else {
-            word = qw[i];
+    for (int k = 0; k < 8; ++k) bv[k] = __shfl(bsum, 32 * (lane & 1) + 4 * k, 64);
+    if (lane < 2) {
+        v4u o;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) q[e] = sbyte(word, e);
-            d = __uint_as_float(dw[i]);
-            bsum = (int)(int16_t)((bw[i] >> (16 * ((lane >> 2) & 1))) & 0xffffu);
-        }
-        const int sq = wave_sum(abs(q[0]) + abs(q[1]) + abs(q[2]) + abs(q[3]));
-        const uint32_t hiw = (uint32_t)__shfl_xor((int)word, 8, 64);
-        if ((lane & 8) == 0) {
-            v4u o;
-            o[0] = h2_bits(sbyte(word, 0), sbyte(word, 2));
-            o[1] = h2_bits(sbyte(hiw, 0), sbyte(hiw, 2));
-            o[2] = h2_bits(sbyte(word, 1), sbyte(word, 3));
-            o[3] = h2_bits(sbyte(hiw, 1), sbyte(hiw, 3));
-            *reinterpret_cast<v4u *>(blk + hf * kPkHalf + (s8 * kTiles + tt) * 1024 + (tl + 32 * h) * 16) = o;
-        }
-        // min-term vector of lane half hh = lane (lanes 0, 1): bsums 8 hh .. 8 hh + 7,
-        // held by lanes 32 hh + 4 k
-        int bv[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) bv[k] = __shfl(bsum, 32 * (lane & 1) + 4 * k, 64);
-        if (lane < 2) {
-            v4u o;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) o[k] = h2_bits(bv[2 * k], bv[2 * k + 1]);
-            *reinterpret_cast<v4u *>(blk + kPkCodes + tt * 1024 + (tl + 32 * lane) * 16) = o;
-        }
-        if (lane == 0) {
-            *reinterpret_cast<float *>(blk + kPkCodes + kPkMn + 4 * (32 * tt + tl)) = d;
-            *reinterpret_cast<int *>(blk + kPkCodes + kPkMn + kPkDx + 4 * (32 * tt + tl)) = sq;
-        }
+        for (int k = 0; k < 4; ++k) o[k] = h2_bits(bv[2 * k], bv[2 * k + 1]);
+        *reinterpret_cast<v4u *>(blk + kPkCodes + tt * 1024 + (tl + 32 * lane) * 16) = o;
+    }
+    if (lane == 0) {
+        *reinterpret_cast<float *>(blk + kPkCodes + kPkMn + 4 * (32 * tt + tl)) = d;
+        *reinterpret_cast<int *>(blk + kPkCodes + kPkMn + kPkDx + 4 * (32 * tt + tl)) = sq;
     }
 }
 
@@ -605,17 +687,15 @@ size_t gemm_q4k_counter_bytes() { return kGemmCounters * sizeof(unsigned); }
 
 hipError_t launch_q8k_pack_f32(const float *x, int m, int K, int ldx, uint8_t *pack, hipStream_t st) {
     const int ntb = pack_tblocks(m);
-    const unsigned grid = (unsigned)((K / kQKK) * ntb * (kTokB / (kPackWaves * kPackTokensPerWave)));
-    hipLaunchKernelGGL(q8k_pack_kernel<true>, dim3(grid), dim3(kPackThreads), 0, st, x, ldx, nullptr, (size_t)0, m,
-                       K, ntb, pack);
+    const unsigned grid = (unsigned)((K / kQKK) * ntb * (kTokB / (kPackWaves * kPackF32Tokens)));
+    hipLaunchKernelGGL(q8k_pack_f32_kernel, dim3(grid), dim3(kPackThreads), 0, st, x, ldx, m, K, ntb, pack);
     return hipGetLastError();
 }
 
 hipError_t launch_q8k_pack_q8k(const uint8_t *xq, size_t xq_stride, int m, int K, uint8_t *pack, hipStream_t st) {
     const int ntb = pack_tblocks(m);
-    const unsigned grid = (unsigned)((K / kQKK) * ntb * (kTokB / (kPackWaves * kPackTokensPerWave)));
-    hipLaunchKernelGGL(q8k_pack_kernel<false>, dim3(grid), dim3(kPackThreads), 0, st, nullptr, 0, xq, xq_stride, m,
-                       K, ntb, pack);
+    const unsigned grid = (unsigned)((K / kQKK) * ntb * (kTokB / kPackWaves));
+    hipLaunchKernelGGL(q8k_pack_blocks_kernel, dim3(grid), dim3(kPackThreads), 0, st, xq, xq_stride, m, K, ntb, pack);
     return hipGetLastError();
 }
 

@@ -659,6 +659,50 @@ def test_prefill_gemm_two_chains(hipdev, ora):
     assert_tol(got[:4], want, S[:4], "two chains vs oracle")
 
 
+@pytest.mark.parametrize("qt", [12, 13, 14])
+def test_prefill_pack_special_blocks(hipdev, ora, qt):
+    """The f32 activation pack of the K-quant prefill GEMMs (four tokens per
+    wavefront) quantizes as the reference's quantize_row_q8_K does
+    (src/gguf_dot_q8.c:360-412): the GEMM over it equals, bit for bit, the
+    GEMM over the oracle's Q8_K bytes of the same activations.  Blocks: all
+    zero, the largest magnitude twice with opposite signs (negative first,
+    positive first, in one lane and in lanes far apart), NaN elements, -0.0
+    and subnormals, codes at exact .5 ties, a block whose maximum is its last
+    element, and a token count that leaves a wavefront's last tokens past m."""
+    rng = np.random.default_rng(4242 + qt)
+    n_in, n_out, m = 1024, 96, 37
+    x = synth.np_activations(m, n_in, rng)
+    x[0, 0:256] = 0.0                                   # all-zero block
+    x[1, 256:512] = -0.0
+    x[1, 256 + 77] = np.float32(1e-40)                  # only a subnormal
+    x[2, 0:256] = rng.uniform(-1, 1, 256)
+    x[2, 10], x[2, 200] = -3.0, 3.0                      # tie, negative first (lanes apart)
+    x[3, 0:256] = rng.uniform(-1, 1, 256)
+    x[3, 40], x[3, 41] = 2.5, -2.5                       # tie, positive first (one lane)
+    x[4, 0:256] = rng.uniform(-1, 1, 256)
+    x[4, 3] = np.nan
+    x[4, 250] = np.nan                                  # NaN never the maximum
+    x[5, 0:256] = rng.uniform(-1, 1, 256)
+    x[5, 255] = -5.0                                    # the maximum is the last element
+    x[6, 0] = -127.0                                    # iscale = 1: the codes are x itself,
+    x[6, 1:256] = (np.arange(255) - 127) * 0.5          # .5 ties round to even
+    x[6, 256:512] = rng.uniform(-1, 1, 256) * 1e-38      # subnormal-range block
+    x[7, 512:768] = 0.0
+    x[7, 512 + 100] = -7.0                              # one element, negative
+    x[8, 768:1024] = x[8, 768:1024] * 1e6
+    x = x.astype(np.float32)
+    w = synth.np_weights(qt, n_out, n_in, rng)
+    bias = rng.normal(0, 0.5, n_out).astype(np.float32)
+    got = E.linear_quant_batch(dev(w), qt, dev(x), n_out, n_in, bias=dev(bias)).cpu().numpy()
+    xq = _q8k_rows(ora, x)
+    want = E.gemv_q8(dev(w), qt, dev(xq), m, n_out, n_in, bias=dev(bias)).cpu().numpy()
+    assert np.array_equal(bits(got), bits(want))
+    finite = np.isfinite(x).all(axis=1)
+    ref = ora.linear_quant_batch(x[finite], w, qt, bias, int(finite.sum()), n_out, n_in)
+    S = q8_scales(ora, qt, w, x[finite]) + np.abs(bias)[None, :]
+    assert_tol(got[finite], ref, S, "pack special blocks vs oracle")
+
+
 def test_prefill_gemm_q8k_input_and_repeat(hipdev, ora):
     """The GEMM over Q8_K block bytes already in memory (edgexpu_hip_gemv_q8_dev)
     equals the GEMM over the f32 activations bit for bit (same codes, same
