@@ -469,10 +469,13 @@ def decode_leg(L, E, synth, gen, dev, workload, m, steps, warmup, kernel_reps, p
 
 def decode_kernel_name(t, n_in, m, rows):
     """The kernel the library picks for a decode launch in its default mode
-    (csrc/gemv_stream.hip gemv_stream_take): the streaming kernel for one
-    token of Q4_K rows of 2560 or 4096, and of 14336 from 2048 rows on; the
+    (csrc/gemv_stream.hip gemv_stream_take): the streaming kernel for one to
+    four tokens of Q4_K rows of 2560 or 4096, of 14336 from 2048 rows on (four
+    tokens at any size), and of Q6_K rows of 9728 from 2048 rows on; the
     fused kernel otherwise."""
-    if t == 12 and m == 1 and (n_in in (2560, 4096) or (n_in == 14336 and rows >= 2048)):
+    if t == 12 and 1 <= m <= 4 and (n_in in (2560, 4096) or (n_in == 14336 and (rows >= 2048 or m == 4))):
+        return "gemv_stream_q4k"
+    if t == 14 and 1 <= m <= 4 and n_in == 9728 and rows >= 2048:
         return "gemv_stream_q4k"
     return "gemv_fused_kernel"
 
