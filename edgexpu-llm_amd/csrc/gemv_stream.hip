@@ -5,8 +5,9 @@
 // the decode steps (Q4_K: K = 2560, 4096, 14336; Q6_K: 9728).
 //
 // Every weight row travels HBM -> LDS by DMA (buffer_load ... lds: no
-// registers held while it is in flight), one row per wave step, into a
-// per-wave ring of NB slots.  A slot is refilled as soon as its bytes are in
+// registers held while it is in flight), one row per wave step (two adjacent
+// rows for one token of rows of 2560 in long launches), into a per-wave ring
+// of NB slots.  A slot is refilled as soon as its bytes are in
 // registers, so NB rows per wave stay in flight while the wave computes.
 // Lanes own fixed 64-element units of K (super-block i, quarter j): the
 // activation slices of a lane stay in registers for every row (where the
@@ -59,7 +60,7 @@ struct StreamArgs {
     float *out[kStreamMaxMats];
     int n_out[kStreamMaxMats];
     int row_start[kStreamMaxMats + 1];     // first step of each matrix
-    int nrows;                             // steps (rows, or gate/up pairs)
+    int nrows;                             // steps (rows, gate/up pairs or row pairs)
     const float *x;                        // f32 activation [m][K] (staged), or
     const uint8_t *xq;                     // its Q8_K block bytes
     const float *x2;                       // SiLU-mul: act = silu(x) * x2
