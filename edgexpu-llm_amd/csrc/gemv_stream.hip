@@ -67,6 +67,8 @@ struct StreamArgs {
     const float *nw;                       // RMSNorm: act = rmsnorm(x; nw, eps)
     float eps;
     unsigned long long *amax;              // argmax epilogue: one key per workgroup, at blockIdx.x
+    int cu_major;                          // 1: wave w of workgroup g is wave w * G + g of the grid (G
+                                           // workgroups), else g * NW + w
 };
 
 // flags: bits 0-1 prologue (1 RMSNorm, 2 SiLU-mul), 4 residual, 8 gate/up
@@ -363,7 +365,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     uint8_t *ring = smem + G::AREA + wave * (NS * G::SB);
     const uint32_t ring_lds = s_lds_addr(ring);
-    const int gw = blockIdx.x * NW + wave, TW = gridDim.x * NW;
+    // the wave's index in the grid: workgroup-major (a workgroup takes NW
+    // adjacent rows of each step) or wave-major (adjacent rows go to adjacent
+    // workgroups, so the rows of a last partial step spread over every CU)
+    const int gw = a.cu_major ? wave * (int)gridDim.x + (int)blockIdx.x : (int)blockIdx.x * NW + wave;
+    const int TW = gridDim.x * NW;
     const int last = a.nrows;
 
     // the matrix of a step and its row (scalar selects over the arguments)
@@ -1056,6 +1062,11 @@ hipError_t launch_gemv_stream(int type, int nmat, const uint8_t *const *w, const
     }
     for (int z = a.nmat; z <= kStreamMaxMats; ++z) a.row_start[z] = rows;
     a.nrows = rows;
+    // rows of 8 KB whose last step leaves waves idle: wave-major, so every
+    // CU streams the same bytes ([2560 x 9728] Q6_K: 9.1 against 10.1 us;
+    // shorter rows measured no faster: [1024 x 2560] 3.61 against 3.49,
+    // [9728 x 2560] 6.3 against 6.15)
+    a.cu_major = rb >= 4096 && rows % (device_cus() * 8) != 0;
     a.x = x;
     a.xq = xq;
     a.x2 = x2;
