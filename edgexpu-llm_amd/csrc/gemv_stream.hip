@@ -343,10 +343,10 @@ struct StreamGeom {
     static_assert(!F32 || ((FL & ~(kSF32 | kSArgmax)) == 0 && XREG), "f32 activations: plain rows, slices in registers");
     static_assert(!(FL & kSArgmax) || (F32 && M == 1), "argmax keys: one f32 token");
     static_assert(AREA % 16 == 0, "slot alignment");
-    static_assert(M == 1 || (FL & ~kSF32) == 0, "several tokens: plain projections");
+    static_assert(M == 1 || (FL & ~(kSF32 | kSRow2)) == 0, "several tokens: plain projections");
     static_assert(XREG || (FL & kSXq) == 0, "Q8_K block input: the slices in registers");
-    static_assert(!(FL & kSRow2) || ((FL & ~(kSRow2 | 1)) == 0 && M == 1 && !Q6),
-                  "row pairs: one token of Q4_K projections, RMSNorm prologue or none");
+    static_assert(!(FL & kSRow2) || ((FL & ~(kSRow2 | 1)) == 0 && !Q6),
+                  "row pairs: Q4_K projections, RMSNorm prologue (one token) or none");
 };
 
 template <int KSB, int NW, int NB, int FL, bool DEEP, int M = 1, int TYPE = kTypeQ4_K>
@@ -644,11 +644,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
         }
         return e;
     };
-    // keep[m]: token m's total of step k (k % 64 = this lane); keep1: up's
-    float keep[M], keep1 = 0.0f;
+    // keep[m]: token m's total of step k (k % 64 = this lane); keep1[m]: the
+    // step's second row (up of a pair, or the odd row of a row pair)
+    float keep[M], keep1[M];
     unsigned long long best = 0ull;  // argmax: the lane's best key (score_key) so far
 #pragma unroll
-    for (int m = 0; m < M; ++m) keep[m] = 0.0f;
+    for (int m = 0; m < M; ++m) keep[m] = keep1[m] = 0.0f;
     auto flush = [&](int first, int n, const Epi &e) {
         const int step = first + lane * TW;
         float *out;
@@ -662,10 +663,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
                 const float v = e.b0 + keep[m];
                 float o = v;
                 if constexpr (kRes) o = resid != nullptr ? e.r + v : v;
-                if constexpr (kPair) o = silu_f32(v) * (e.b1 + keep1);
+                if constexpr (kPair) o = silu_f32(v) * (e.b1 + keep1[m]);
                 if constexpr (kRow2) {
-                    out[2 * row] = o;
-                    out[2 * row + 1] = e.b1 + keep1;
+                    out[(size_t)m * n_out + 2 * row] = o;
+                    out[(size_t)m * n_out + 2 * row + 1] = e.b1 + keep1[m];
                     continue;
                 }
                 out[(size_t)m * n_out + row] = o;
@@ -798,10 +799,13 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
         float acc[M][G::RPS];
         if constexpr (M == 4 && G::T == 1) {
             // four tokens' rows in one tree (each total is its s_wave_total bit for bit)
-            const float v4[4] = {p[0][0][0], p[1][0][0], p[2][0][0], p[3][0][0]};
-            const float tot = s_wave_total4(v4);
 #pragma unroll
-            for (int m = 0; m < 4; ++m) acc[m][0] = s_lane(tot, 16 * m);
+            for (int r = 0; r < G::RPS; ++r) {
+                const float v4[4] = {p[0][r][0], p[1][r][0], p[2][r][0], p[3][r][0]};
+                const float tot = s_wave_total4(v4);
+#pragma unroll
+                for (int m = 0; m < 4; ++m) acc[m][r] = s_lane(tot, 16 * m);
+            }
         } else {
 #pragma unroll
             for (int m = 0; m < M; ++m)
@@ -827,7 +831,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
         }
 #pragma unroll
         for (int m = 0; m < M; ++m) keep[m] = lane == k64 ? acc[m][0] : keep[m];
-        if constexpr (kPair || kRow2) keep1 = lane == k64 ? acc[0][G::RPS - 1] : keep1;
+        if constexpr (kPair || kRow2) {
+#pragma unroll
+            for (int m = 0; m < M; ++m) keep1[m] = lane == k64 ? acc[m][G::RPS - 1] : keep1[m];
+        }
         advance();
     };
     // the first NS steps: their rows came with the start, so fewer stay in flight after each
@@ -916,7 +923,7 @@ hipError_t launch_stream_q6k(int fl, const StreamArgs &a, hipStream_t st) {
 // q+k+v [6144 x 4096] at 2 / 3 / 4 tokens: 6.5 / 7.9 / 8.5 us, against 7.3 /
 // 8.1 / 9.1 with two slots filled twice at the start; o [4096 x 4096] 5.7 /
 // 6.8 / 7.5 against 5.8 / 7.0 / 7.7); longer launches two.
-template <int KSB, int NB, int TYPE = kTypeQ4_K>
+template <int KSB, int NB, int TYPE = kTypeQ4_K, int FL = 0>
 hipError_t launch_stream_tokens(int m, const StreamArgs &a, hipStream_t st) {
     if constexpr (KSB == 16 && NB == 2) {
         const long long per_gen = (long long)device_cus() * 8;
@@ -930,9 +937,9 @@ hipError_t launch_stream_tokens(int m, const StreamArgs &a, hipStream_t st) {
         }
     }
     switch (m) {
-        case 2: return launch_stream<KSB, 8, NB, 0, 2, TYPE>(a, st);
-        case 3: return launch_stream<KSB, 8, NB, 0, 3, TYPE>(a, st);
-        case 4: return launch_stream<KSB, 8, NB, 0, 4, TYPE>(a, st);
+        case 2: return launch_stream<KSB, 8, NB, FL, 2, TYPE>(a, st);
+        case 3: return launch_stream<KSB, 8, NB, FL, 3, TYPE>(a, st);
+        case 4: return launch_stream<KSB, 8, NB, FL, 4, TYPE>(a, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -1030,11 +1037,11 @@ hipError_t launch_gemv_stream(int type, int nmat, const uint8_t *const *w, const
     for (int z = 0; z < nmat; ++z)
         if (((uintptr_t)w[z] & 15u) != 0 || n_out[z] < 0 || (long long)n_out[z] * rb >= (1ll << 32))
             return hipErrorInvalidValue;
-    // one token of rows of 2560, no residual, long launches: two adjacent
-    // rows of a matrix per step (the steps and row_start count row pairs)
+    // rows of 2560, no residual, long launches: two adjacent rows of a
+    // matrix per step (the steps and row_start count row pairs)
     // where every wave takes at least four pairs and the longest wave takes
     // no more rows than with single rows
-    bool row2 = type == kTypeQ4_K && K == 2560 && m == 1 && !pair && !any_resid && xq == nullptr && (pro & 3) <= 1;
+    bool row2 = type == kTypeQ4_K && K == 2560 && !pair && !any_resid && xq == nullptr && (pro & 3) <= 1;
     long long all_rows = 0;
     for (int z = 0; z < nmat; ++z) {
         row2 = row2 && n_out[z] % 2 == 0;
@@ -1081,7 +1088,9 @@ hipError_t launch_gemv_stream(int type, int nmat, const uint8_t *const *w, const
         return m > 1 ? launch_stream_tokens<38, 1, kTypeQ6_K>(m, a, st) : launch_stream_q6k<38, 8, 1>(fl, a, st);
     if (m > 1) {
         switch (K) {
-            case 2560: return launch_stream_tokens<10, 2>(m, a, st);
+            case 2560:
+                if (row2) return launch_stream_tokens<10, 1, kTypeQ4_K, kSRow2>(m, a, st);
+                return launch_stream_tokens<10, 2>(m, a, st);
             case 4096: return launch_stream_tokens<16, 2>(m, a, st);
             default: return launch_stream_tokens<56, 1>(m, a, st);
         }
