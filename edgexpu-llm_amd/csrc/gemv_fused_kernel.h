@@ -86,23 +86,28 @@ __device__ __forceinline__ int cvt_f32_i32(float v) {
     return r;
 }
 
-// Q8_K quantization of x into LDS (src/gguf_dot_q8.c:360-412) with the
-// arithmetic of quantize_q8_k_kernel.  16 threads per 256-element block, each
-// owning one 16-element group (so its int16 sum needs no reduction); NT/16
-// blocks per round, one round in registers at a time (the register budget of
-// the staging decides the kernel's occupancy).
+// Q8_K quantization of x into LDS (src/gguf_dot_q8.c:360-412) for the
+// GEMV's own use.  16 threads per 256-element block, each owning one
+// 16-element group (so its int16 sum needs no reduction); NT/16 blocks per
+// round, one round in registers at a time (the register budget of the
+// staging decides the kernel's occupancy).
 //
-// The reference's scale comes from the first element of largest |x| (its
-// strict '>' from amax = 0: NaN never enters, equal magnitudes keep the
-// lowest index), and only that element's sign matters: each thread finds
-// its first element equal to +-amax (a compare and a select per element),
-// and the lowest thread holding one decides.  With iscale finite every
-// |iscale * x| is at most 127 (|x| <= amax) or NaN, so rint and the
-// hardware conversion (NaN -> 0, as lrintf's LONG_MIN truncates to 0) give
-// the reference's codes with no clamp; with iscale infinite (amax below
-// ~3.7e-37) every product is infinite or NaN and every reference code is 0.
-// Codes are packed four to a word with byte permutes and their sums taken
-// with sdot4 against ones.
+// The reference's scale is iscale = -127 / max with max the first element
+// of largest |x|, sign included.  Here max is |max| for every block: a block
+// whose first largest element is negative gets the negated codes, bsums and
+// d of the reference's block (rint and the clamp are odd functions, and
+// 1 / -iscale = -d), and every use of the block in a dot product is a
+// product of d with an integer sum of codes (dot_q4_k_q8_k / dot_q6_k_q8_k
+// and the other K-quant dots), unchanged word for word when both factors
+// change sign.  So the outputs are the reference's; only the sign search
+// (a compare and a select per element, a 16-lane minimum per block) is gone.
+// quantize_q8_k_kernel, whose bytes leave the kernel, keeps the reference's
+// signs.  With iscale finite every |iscale * x| is at most 127 (|x| <= amax)
+// or NaN, so rint and the hardware conversion (NaN -> 0, as lrintf's
+// LONG_MIN truncates to 0) give the codes with no clamp; with iscale
+// infinite (amax below ~3.7e-37) every product is infinite or NaN and every
+// code is 0.  Codes are packed four to a word with byte permutes and their
+// sums taken with sdot4 against ones.
 template <int NT>
 __device__ __forceinline__ void quantize_q8_k_group(const float (&xs)[16], int blk, int total, int nb, int K,
                                                     int sub, int8_t *lq, float *ld, int16_t *lbs) {
@@ -111,15 +116,9 @@ __device__ __forceinline__ void quantize_q8_k_group(const float (&xs)[16], int b
 #pragma unroll
     for (int e = 0; e < 16; ++e) am = fmaxf(am, fabsf(xs[e]));
     const float amax = row16_max(am);
-    float first = 0.0f;  // this thread's first element of magnitude amax (0: none)
-#pragma unroll
-    for (int e = 15; e >= 0; --e) first = fabsf(xs[e]) == amax ? xs[e] : first;
-    const uint32_t win =
-        row16_min(amax > 0.0f && first != 0.0f ? (((uint32_t)sub << 1) | (first < 0.0f ? 1u : 0u)) : 0xffffffffu);
     if (!valid) return;
     const int tok = blk / nb, b = blk - tok * nb;
-    const float maxv = (win & 1u) ? -amax : amax;
-    const float iscale = -127.0f / maxv;
+    const float iscale = -127.0f / amax;
     const bool codes = amax > 0.0f && fabsf(iscale) < INFINITY;  // uniform over the group
     uint32_t words[4];
     int sum = 0;

@@ -23,9 +23,10 @@
 // exactly the rows still in flight.
 //
 // The activation is quantized to Q8_K inside each workgroup with the
-// arithmetic of quantize_q8_k_kernel (bit-identical to the reference's
-// quantize_row_q8_K, src/gguf_dot_q8.c:360-412), optionally after a staging
-// prologue (RMSNorm, SiLU-mul; src/native.c:2529, 2576-2578), or read from
+// fused kernel's staging (quantize_q8_k_group: the reference's
+// quantize_row_q8_K, src/gguf_dot_q8.c:360-412, up to the sign of each
+// block's codes and scale, which cancels in every dot), optionally after a
+// staging prologue (RMSNorm, SiLU-mul; src/native.c:2529, 2576-2578), or read from
 // Q8_K block bytes already in memory.  Epilogues: bias, residual
 // (src/native.c:2571-2580), gate/up pairs with silu(gate) * up.
 //
@@ -492,7 +493,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
                 asm volatile("" : "+v"(xr[r][k]));
                 if constexpr (PRO != 0) asm volatile("" : "+v"(yr[r][k]));
             }
-        // 2. Q8_K staging (quantize_q8_k_group: the reference's quantizer), after the prologue
+        // 2. Q8_K staging (quantize_q8_k_group), after the prologue
         float xs[RN][16], ys[RN][16];
 #pragma unroll
         for (int r = 0; r < G::ROUNDS; ++r)

@@ -527,3 +527,56 @@ def test_g32_gemm_f64_restatement_vs_rows_and_oracle(ora, qt):
         assert np.allclose(S[t], s1, rtol=1e-12)
     want = ora.linear_quant_batch(x, w, qt, None, m, n_out, n_in)
     assert np.all(np.abs(want - val) <= 1e-5 * S)
+
+
+def _sign_free_q8k(x):
+    """Q8_K blocks with the scale -127/amax for every block (numpy, float32
+    arithmetic): the GEMVs' in-kernel staging."""
+    out = []
+    for blk in x.reshape(-1, 256):
+        amax = np.float32(np.abs(blk).max())
+        if amax == 0:
+            out.append(np.zeros(292, np.uint8))
+            continue
+        iscale = np.float32(-127.0) / amax
+        q = np.rint((iscale * blk).astype(np.float32)).astype(np.int32)
+        bs = q.reshape(16, 16).sum(axis=1).astype(np.int16)
+        d = np.float32(1.0) / iscale
+        out.append(np.concatenate([np.frombuffer(np.float32(d).tobytes(), np.uint8), q.astype(np.int8).view(np.uint8),
+                                   bs.view(np.uint8)]))
+    return np.concatenate(out)
+
+
+@pytest.mark.parametrize("qt", [12, 13, 14])
+def test_q8k_block_sign_cancels_in_dots(ora, ref, qt):
+    """The GEMVs' in-kernel Q8_K staging scales every block by -127/amax,
+    whatever the sign of its first largest element.  Where that element is
+    negative, the staged block is the reference's (quantize_row_q8_K,
+    src/gguf_dot_q8.c:360-412) with codes, bsums and d negated, and every
+    K-quant dot of the reference build (dot_q4_k_q8_k, dot_q5_k_q8_k,
+    dot_q6_k_q8_k: products of d with integer sums of codes) gives the same
+    word for both blocks; so does the oracle's."""
+    rng = np.random.default_rng(31 + qt)
+    n, rows = 2048, 24
+    w = synth.np_weights(qt, rows, n, rng)
+    x = (rng.normal(0, 1, n) * rng.uniform(0.01, 100.0)).astype(np.float32)
+    for b in range(n // 256):  # the largest element negative in even blocks, positive in odd ones
+        blk = x[256 * b:256 * (b + 1)]
+        blk[rng.integers(0, 256)] = (1.5 if b % 2 else -1.5) * np.abs(blk).max()
+    xr = ora.quantize_q8_k(x)
+    assert np.array_equal(xr, ref.quantize_q8_k(x))
+    xs = _sign_free_q8k(x)
+    blocks_r, blocks_s = xr.reshape(-1, 292), xs.reshape(-1, 292)
+    d_r = blocks_r[:, :4].copy().view(np.float32)[:, 0]
+    flip = d_r > 0  # the blocks whose first largest element is negative
+    assert np.array_equal(flip, np.arange(n // 256) % 2 == 0)
+    neg = blocks_r.copy()
+    neg[flip, :4] = (-d_r[flip]).astype(np.float32).view(np.uint8).reshape(-1, 4)
+    neg[flip, 4:260] = (-blocks_r[flip, 4:260].view(np.int8)).astype(np.int8).view(np.uint8)
+    neg[flip, 260:] = (-blocks_r[flip, 260:].copy().view(np.int16)).astype(np.int16).view(np.uint8)
+    assert np.array_equal(neg, blocks_s)  # the staged blocks are the negated reference blocks
+    for i in range(rows):
+        for lib in (ora, ref):
+            a = np.float32(lib.dot_q8k(qt, w[i], xr, n))
+            s = np.float32(lib.dot_q8k(qt, w[i], xs, n))
+            assert a.view(np.uint32) == s.view(np.uint32), (i, a, s)
