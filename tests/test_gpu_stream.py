@@ -9,8 +9,8 @@ same roundings and sum the lanes with the same xor tree, so every output is
 the same word whichever kernel runs -- the plain projection, grouped
 launches, the RMSNorm and SiLU-mul staging prologues, the residual store,
 gate/up pairs with silu(gate) * up, activations given as Q8_K block bytes,
-and (rows of 2560 in long launches, every matrix of an even row count) two
-adjacent rows per step.  Each variant is also held to the oracle (the reference's
+and (rows of 2560, or of 4096 at two to four tokens, in long launches,
+every matrix of an even row count) two adjacent rows per step.  Each variant is also held to the oracle (the reference's
 edgexpu_cpu_linear_quant_batch, src/cpu_kernel.c:545-644) within the usual
 1e-5 of the conditioning scale, so the agreement is between two correct
 results, not two copies of one mistake.
@@ -144,7 +144,7 @@ def test_gate_up_pairs_fused_equals_stream(hipdev, ora, n_in, n_ff, norm):
 
 TOKEN_SHAPES = [(4096, (4096, 1024, 1024)), (4096, (14336, 14336)), (4096, (4096,)), (4096, (301,)),
                 (2560, (4096, 1024, 1024)), (2560, (9728, 9728)), (2560, (2560,)), (2560, (77,)),
-                (14336, (4096,)), (14336, (2048, 300))]
+                (14336, (4096,)), (14336, (2048, 300)), (4096, (2, 18430, 6))]
 
 
 def fused_stages(m, n_in):
