@@ -6,8 +6,8 @@
 //
 // Every weight row travels HBM -> LDS by DMA (buffer_load ... lds: no
 // registers held while it is in flight), one row per wave step (two adjacent
-// rows for one token of rows of 2560 in long launches), into a per-wave ring
-// of NB slots.  A slot is refilled as soon as its bytes are in
+// rows in long launches of rows of 2560, and of rows of 4096 at 2-4 tokens),
+// into a per-wave ring of NB slots.  A slot is refilled as soon as its bytes are in
 // registers, so NB rows per wave stay in flight while the wave computes.
 // Lanes own fixed 64-element units of K (super-block i, quarter j): the
 // activation slices of a lane stay in registers for every row (where the
