@@ -897,7 +897,9 @@ hipError_t launch_stream(const StreamArgs &a, hipStream_t st) {
     // twice the ring at the start (measured: [4096 x 4096] 5.3 against
     // 5.5 us, [6144 x 2560] 5.5 against 6.1); longer ones keep NB in flight
     // from the start ([28672 x 4096] 14.5 against 14.7 us), and 8 KB rows
-    // never take the deep start (12.4 against 11.0 us at [4096 x 14336]).
+    // never take the deep start (12.4 against 11.0 us at [4096 x 14336];
+    // measured again with the current staging: 10.8 against 9.6 us, and the
+    // Q6_K [2560 x 9728] 9.8 against 8.9).
     const int grid = device_cus();
     const long long steps = ((long long)a.nrows + (long long)grid * NW - 1) / ((long long)grid * NW);
     if constexpr (KSB <= 16) {
