@@ -75,8 +75,9 @@ struct StreamArgs {
 // flags: bits 0-1 prologue (1 RMSNorm, 2 SiLU-mul), 4 residual, 8 gate/up
 // pairs, 16 activation already in Q8_K block bytes, 32 f32 activation (the
 // f32-activation dot of the logits, not quantized), 64 greedy-argmax keys,
-// 128 two adjacent rows of one matrix per step
-constexpr int kSRes = 4, kSPair = 8, kSXq = 16, kSF32 = 32, kSArgmax = 64, kSRow2 = 128;
+// 128 two adjacent rows of one matrix per step, 256 three adjacent rows per
+// step (Q6_K f32 rows of 2560, their 120 units over two passes of 64 lanes)
+constexpr int kSRes = 4, kSPair = 8, kSXq = 16, kSF32 = 32, kSArgmax = 64, kSRow2 = 128, kSRow3 = 256;
 
 __device__ __forceinline__ v4u_t s_rsrc(const void *base, uint32_t bytes) {
     const uint64_t a = (uint64_t)(uintptr_t)base;
@@ -307,16 +308,19 @@ struct StreamGeom {
     static constexpr bool Q6 = TYPE == kTypeQ6_K;
     static constexpr int K = KSB * kQKK;
     static constexpr int U = 4 * KSB;                    // units per row
-    static constexpr int T = (U + 63) / 64;              // units per lane
+    static constexpr int R3 = (FL & kSRow3) ? 3 : 1;     // Q6_K f32 row triples: rows per step
+    static constexpr int UT = R3 * U;                    // units per step
+    static constexpr int T = (UT + 63) / 64;             // units per lane
     static constexpr int RB = KSB * (Q6 ? kBytesQ6_K : kBytesQ4_K);  // row bytes
-    static constexpr int RPS = (FL & (kSPair | kSRow2)) ? 2 : 1;  // rows per step
+    static constexpr int SPAN = R3 * RB;                 // bytes of a step's rows (Q6_K)
+    static constexpr int RPS = (FL & (kSPair | kSRow2)) ? 2 : R3;  // rows per step
     // Q4_K rows are whole 16-byte transfers.  A Q6_K row starts s = 0, 4, 8
     // or 12 bytes past a 16-byte boundary: its slot takes the 16-byte
     // transfers from that boundary that end inside the row (F of them, F
     // depending on s), then 4-byte transfers of the rest; the row starts s
     // bytes into its slot.
-    static constexpr int F_MIN = RB / 16, F_MAX = (RB + 12) / 16;
-    static constexpr int SB = Q6 ? ((RB + 16 + 15) & ~15) : RPS * RB;  // slot bytes
+    static constexpr int F_MIN = SPAN / 16, F_MAX = (SPAN + 12) / 16;
+    static constexpr int SB = Q6 ? ((SPAN + 16 + 15) & ~15) : RPS * RB;  // slot bytes
     static constexpr int CH = (Q6 ? F_MIN * 16 : RB) / 1024;          // whole 1 KB chunks per row
     static constexpr int PL = (RB % 1024) / 16;          // Q4_K: lanes of the partial chunk
     static constexpr int NI = Q6 ? CH + 2 : RPS * (CH + (PL > 0 ? 1 : 0));  // DMA instructions per step
@@ -341,7 +345,8 @@ struct StreamGeom {
     static_assert(AREA + (size_t)NW * NS * SB + 8 * NW <= 160 * 1024, "the ring and the staging fit the gfx950 LDS");
     static_assert(ROUNDS <= 8, "the staging loads of every round are in flight at the start");
     static_assert(NS * NI + 4 * ROUNDS * ((FL & 3) ? 2 : 1) + (F32 ? 16 * M * T : 0) <= 63, "vmcnt range");
-    static_assert(!F32 || ((FL & ~(kSF32 | kSArgmax)) == 0 && XREG), "f32 activations: plain rows, slices in registers");
+    static_assert(!F32 || ((FL & ~(kSF32 | kSArgmax | kSRow3)) == 0 && XREG), "f32 activations: plain rows, slices in registers");
+    static_assert(!(FL & kSRow3) || (Q6 && F32 && M == 1), "row triples: one token of Q6_K f32 logits");
     static_assert(!(FL & kSArgmax) || (F32 && M == 1), "argmax keys: one f32 token");
     static_assert(AREA % 16 == 0, "slot alignment");
     static_assert(M == 1 || (FL & ~(kSF32 | kSRow2)) == 0, "several tokens: plain projections");
@@ -357,6 +362,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     constexpr int PRO = FL & 3;
     constexpr bool kRes = (FL & kSRes) != 0, kPair = (FL & kSPair) != 0, kXq = (FL & kSXq) != 0;
     constexpr bool kF32 = G::F32, kArgmax = (FL & kSArgmax) != 0, kRow2 = (FL & kSRow2) != 0;
+    constexpr bool kRow3 = (FL & kSRow3) != 0;
     constexpr int NS = G::NS;
     extern __shared__ __align__(16) uint8_t smem[];
     int8_t *lq = reinterpret_cast<int8_t *>(smem);
@@ -393,14 +399,27 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
         const bool ok = step < last;
         const Mat m = locate(ok ? step : 0);
         // row pairs: step row r of the matrix is rows 2r and 2r + 1
-        const uint32_t so = ok ? (uint32_t)m.row * (kRow2 ? 2u : 1u) * G::RB : 0u;
+        const uint32_t so = ok ? (uint32_t)m.row * (kRow2 ? 2u : 1u) * (uint32_t)G::SPAN : 0u;
         const uint32_t vo = ok ? (uint32_t)lane * 16u : 0x7ff00000u;
         if constexpr (Q6) {
             // every transfer lies inside the row or the rows before it
-            const uint32_t sh = so & 15u, a0 = so - sh, end = sh + (uint32_t)G::RB;
+            const uint32_t sh = so & 15u, a0 = so - sh, end = sh + (uint32_t)G::SPAN;
             const int F = (int)(end >> 4), tail = (int)((end & 15u) >> 2);
             const v4u_t rs = s_rsrc(m.w, (uint32_t)m.n_out * G::RB);
             const uint32_t dst = ring_lds + b * G::SB;
+            if constexpr (kRow3) {
+                // the last triple may pass the matrix end: the offsets go in the
+                // range-checked VGPR offset (bytes past n_out rows read 0)
+                const uint32_t t0 = 16u * (uint32_t)F;
+#pragma unroll
+                for (int k = 0; k < G::CH; ++k)
+                    s_dma16_nt(dst + k * 1024, ok ? a0 + k * 1024u + (uint32_t)lane * 16u : 0x7ff00000u, rs, 0u);
+                if (lane < F - 64 * G::CH)
+                    s_dma16_nt(dst + G::CH * 1024, ok ? a0 + G::CH * 1024u + (uint32_t)lane * 16u : 0x7ff00000u, rs, 0u);
+                const uint32_t v4 = tail > 0 ? a0 + t0 + (uint32_t)lane * 4u : a0 + t0 - 4u;
+                if (lane < (tail > 0 ? tail : 1)) s_dma4_nt(dst + t0, ok ? v4 : 0x7ff00000u, rs, 0u);
+                return;
+            }
 #pragma unroll
             for (int k = 0; k < G::CH; ++k) s_dma16_nt(dst + k * 1024, vo, rs, a0 + k * 1024);
             if (lane < F - 64 * G::CH) s_dma16_nt(dst + G::CH * 1024, vo, rs, a0 + G::CH * 1024);
@@ -439,7 +458,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
         for (int m = 0; m < M; ++m)
 #pragma unroll
             for (int t = 0; t < G::T; ++t) {
-                const int uc = min(lane + 64 * t, G::U - 1);
+                const int uc = min(lane + 64 * t, G::UT - 1) % G::U;
                 if constexpr (Q6) {
                     const float *px = a.x + (size_t)m * G::K + 256 * (uc >> 2) + 128 * ((uc >> 1) & 1) + 16 * (uc & 1);
 #pragma unroll
@@ -554,11 +573,15 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     ScaleSel lc[G::T];
     uint32_t hoff[G::T], qoff[G::T];  // Q6_K: the unit's aligned byte offset, its shift (0 or 2)
     bool live[G::T];
+    int unit[G::T], prow[G::T];  // the lane's unit of each pass and its row in the step
 #pragma unroll
     for (int t = 0; t < G::T; ++t) {
         const int u = lane + 64 * t;
-        live[t] = u < G::U;
-        const int uc = min(u, G::U - 1);
+        live[t] = u < G::UT;
+        const int gl = min(u, G::UT - 1);
+        const int uc = gl % G::U;
+        unit[t] = uc;
+        prow[t] = gl / G::U;
         if constexpr (kXq) {
             act_from_blocks(smem, uc, xa[0][t]);
         } else if constexpr (kF32) {
@@ -584,7 +607,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
             for (int m = 0; m < M; ++m) Fmt::load_act_lds(act, uc, m, xa[m][t]);
         }
         if constexpr (Q6) {
-            const uint32_t sb = (uint32_t)(uc >> 2) * kBytesQ6_K;  // the unit's fields sit at sb + 4-byte multiples
+            // the unit's fields sit at sb + 4-byte multiples
+            const uint32_t sb = (uint32_t)prow[t] * (uint32_t)G::RB + (uint32_t)(uc >> 2) * kBytesQ6_K;
             hoff[t] = sb & ~3u;
             qoff[t] = sb & 3u;  // v_alignbyte shift, bytes
         } else {
@@ -600,14 +624,14 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
             return xa[m][t];
         } else {
             Act x;
-            Fmt::load_act_lds(act, min(lane + 64 * t, G::U - 1), m, x);
+            Fmt::load_act_lds(act, unit[t], m, x);
             return x;
         }
     };
 
     // 3. the epilogue words of the lane's step (step first + lane * TW), loaded ahead of use
     struct Epi {
-        float b0, b1, r;
+        float b0, b1, r, b2;
     };
     auto lane_out = [&](int step, float *&out, int &row, const float *&bias, const float *&resid, int &n_out) {
         out = a.out[0];
@@ -632,9 +656,13 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
         int row, n_out;
         const float *bias, *resid;
         lane_out(ok ? step : 0, out, row, bias, resid, n_out);
-        Epi e{0.0f, 0.0f, 0.0f};
+        Epi e{0.0f, 0.0f, 0.0f, 0.0f};
         if (ok) {
-            if constexpr (kRow2) {
+            if constexpr (kRow3) {
+                e.b0 = bias != nullptr ? bias[3 * row] : 0.0f;
+                e.b1 = bias != nullptr && 3 * row + 1 < n_out ? bias[3 * row + 1] : 0.0f;
+                e.b2 = bias != nullptr && 3 * row + 2 < n_out ? bias[3 * row + 2] : 0.0f;
+            } else if constexpr (kRow2) {
                 e.b0 = bias != nullptr ? bias[2 * row] : 0.0f;
                 e.b1 = bias != nullptr ? bias[2 * row + 1] : 0.0f;
             } else {
@@ -647,10 +675,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
     };
     // keep[m]: token m's total of step k (k % 64 = this lane); keep1[m]: the
     // step's second row (up of a pair, or the odd row of a row pair)
-    float keep[M], keep1[M];
+    float keep[M], keep1[M], keep2[M];
     unsigned long long best = 0ull;  // argmax: the lane's best key (score_key) so far
 #pragma unroll
-    for (int m = 0; m < M; ++m) keep[m] = keep1[m] = 0.0f;
+    for (int m = 0; m < M; ++m) keep[m] = keep1[m] = keep2[m] = 0.0f;
     auto flush = [&](int first, int n, const Epi &e) {
         const int step = first + lane * TW;
         float *out;
@@ -668,6 +696,21 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
                 if constexpr (kRow2) {
                     out[(size_t)m * n_out + 2 * row] = o;
                     out[(size_t)m * n_out + 2 * row + 1] = e.b1 + keep1[m];
+                    continue;
+                }
+                if constexpr (kRow3) {
+                    const float o3[3] = {o, e.b1 + keep1[m], e.b2 + keep2[m]};
+#pragma unroll
+                    for (int r = 0; r < 3; ++r) {
+                        const int ro = 3 * row + r;
+                        if (ro < n_out) {
+                            out[ro] = o3[r];
+                            if constexpr (kArgmax) {
+                                const unsigned long long key = score_key(o3[r], (unsigned)ro);
+                                best = key > best ? key : best;
+                            }
+                        }
+                    }
                     continue;
                 }
                 out[(size_t)m * n_out + row] = o;
@@ -692,12 +735,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
             // the row starts (row * RB) & 15 bytes into its slot
             const int step = gw + k * TW;
             const Mat m = locate(step < last ? step : 0);
-            const uint8_t *rb = ring + slot * G::SB + (((uint32_t)m.row * G::RB) & 15u);
+            const uint8_t *rb = ring + slot * G::SB + (((uint32_t)m.row * G::SPAN) & 15u);
             v4u_t A[G::T], B[G::T], H[G::T];
             uint32_t s0[G::T], s1[G::T], s2[G::T], dw[G::T];
 #pragma unroll
             for (int t = 0; t < G::T; ++t) {
-                const int u = min(lane + 64 * t, G::U - 1), h = (u >> 1) & 1, pp = u & 1;
+                const int u = unit[t], h = (u >> 1) & 1, pp = u & 1;
                 const uint8_t *q = rb + hoff[t];
                 A[t] = lds16_a2(q + 64 * h + 16 * pp, qoff[t]);
                 B[t] = lds16_a2(q + 64 * h + 32 + 16 * pp, qoff[t]);
@@ -711,7 +754,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
             if (k + NB >= NS) issue((slot + NB) % NS, gw + (k + NB) * TW);  // uniform; slot == k % NS
 #pragma unroll
             for (int t = 0; t < G::T; ++t) {
-                const int u = min(lane + 64 * t, G::U - 1);
+                const int u = unit[t];
                 const uint32_t scx = __builtin_amdgcn_alignbyte(s1[t], s0[t], qoff[t]);
                 const uint32_t scy = __builtin_amdgcn_alignbyte(s2[t], s1[t], qoff[t]);
                 const uint32_t db = (dw[t] >> (8u * qoff[t])) & 0xffffu;
@@ -728,7 +771,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
                     }
                     FmtQ6KF32::dotm<M>(w, u, xm, acc);
 #pragma unroll
-                    for (int m = 0; m < M; ++m) p[m][0][t] = live[t] ? acc[m] : 0.0f;
+                    for (int m = 0; m < M; ++m) {
+                        p[m][0][t] = live[t] ? acc[m] : 0.0f;  // row triples: the rows are sorted out in finish
+#pragma unroll
+                        for (int r = 1; r < G::RPS; ++r) p[m][r][t] = 0.0f;
+                    }
                 } else {
 #pragma unroll
                     for (int m = 0; m < M; ++m) {
@@ -812,7 +859,24 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
             for (int m = 0; m < M; ++m)
 #pragma unroll
                 for (int r = 0; r < G::RPS; ++r) {
-                    if constexpr (G::F32 && G::T == 1 && G::U > 32 && G::U <= 48) {
+                    if constexpr (kRow3) {
+                        // unit j of each row to lane j (the lanes of pass 0 hold
+                        // units 0-39 of row 0 and 0-23 of row 1, those of pass 1
+                        // units 24-39 of row 1 and 0-39 of row 2), then the tree
+                        // of one row of 40 units: the words of one row per step
+                        const float a0 = p[m][0][0], a1 = p[m][0][1];
+                        float v;
+                        if (r == 0) {
+                            v = lane < 40 ? a0 : 0.0f;
+                        } else if (r == 1) {
+                            const float x0 = __shfl(a0, (lane + 40) & 63, 64), x1 = __shfl(a1, (lane + 40) & 63, 64);
+                            v = lane < 24 ? x0 : (lane < 40 ? x1 : 0.0f);
+                        } else {
+                            const float x2 = __shfl(a1, (lane + 16) & 63, 64);
+                            v = lane < 40 ? x2 : 0.0f;
+                        }
+                        acc[m][r] = s_wave_total_3x16(v);
+                    } else if constexpr (G::F32 && G::T == 1 && G::U > 32 && G::U <= 48) {
                         acc[m][r] = s_wave_total_3x16(p[m][r][0]);
                     } else if constexpr (G::T == 1) {
                         acc[m][r] = s_wave_total(p[m][r][0]);
@@ -832,9 +896,13 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_q4k(StreamArgs a) {
         }
 #pragma unroll
         for (int m = 0; m < M; ++m) keep[m] = lane == k64 ? acc[m][0] : keep[m];
-        if constexpr (kPair || kRow2) {
+        if constexpr (kPair || kRow2 || kRow3) {
 #pragma unroll
-            for (int m = 0; m < M; ++m) keep1[m] = lane == k64 ? acc[m][G::RPS - 1] : keep1[m];
+            for (int m = 0; m < M; ++m) keep1[m] = lane == k64 ? acc[m][1] : keep1[m];
+        }
+        if constexpr (kRow3) {
+#pragma unroll
+            for (int m = 0; m < M; ++m) keep2[m] = lane == k64 ? acc[m][2] : keep2[m];
         }
         advance();
     };
@@ -1156,9 +1224,22 @@ hipError_t launch_gemv_stream_f32(int type, int K, int m, const uint8_t *w, int 
     // arithmetic wants the waves; measured 57.6 us against 59.2-65.0 with 8
     // waves and two to four slots); two tokens (two activation slices per
     // lane): 8 waves, three slots (78.1 against 81.2 with two)
-    // Q6_K rows of 2560 ([151936 x 2560]): one token 16 waves, one slot (77.8
-    // - 80.5 us against 86.5 - 87.5 fused; 8 waves 89.0 - 95.2); two tokens
-    // 8 waves, two slots (108.9 against 147.9)
+    // Q6_K rows of 2560 ([151936 x 2560]) at one token: three rows per step,
+    // their 120 units in two passes of 64 lanes (one row per step leaves 24
+    // of 64 lanes idle on every row), 8 waves per CU (two activation slices
+    // per lane); with the argmax keys one slot per wave, 69-72 against 84-86
+    // us for 16 waves of one row per step; scores only two slots, 75-77
+    // against 96-97 (one row per step: 77.8-80.5 against 86.5-87.5 fused in
+    // the bench's step; it stays for a matrix whose last triple would pass
+    // the 32-bit offset range).  Two tokens: 8 waves, two slots (108.9
+    // against 147.9).
+    const long long rb6 = (long long)(K / kQKK) * kBytesQ6_K;
+    if (type == kTypeQ6_K && m == 1 && (long long)n_out * rb6 + 3 * rb6 < (1ll << 32)) {
+        a.nrows = (n_out + 2) / 3;
+        for (int z = 1; z <= kStreamMaxMats; ++z) a.row_start[z] = a.nrows;
+        if (amax != nullptr) return launch_stream_geom<10, 8, 1, kSF32 | kSArgmax | kSRow3, false, 1, kTypeQ6_K>(a, st);
+        return launch_stream_geom<10, 8, 2, kSF32 | kSRow3, false, 1, kTypeQ6_K>(a, st);
+    }
     if (type == kTypeQ6_K) {
         if (amax != nullptr) return launch_stream_geom<10, 16, 1, kSF32 | kSArgmax, false, 1, kTypeQ6_K>(a, st);
         return m == 1 ? launch_stream_geom<10, 16, 1, kSF32, false, 1, kTypeQ6_K>(a, st)
