@@ -296,6 +296,36 @@ def test_logits_f32_fused_equals_stream(hipdev, ora, qt, n, vocab, m, with_bias)
         assert np.all(np.abs(s[0][t][rows] - want) <= TOL * S), f"token {t}"
 
 
+def test_q6k_logits_row_triples_more_than_64_steps(hipdev, ora):
+    """One token of Q6_K logits rows of 2560 runs three rows per step over
+    two passes of 64 lanes: a vocabulary long enough that every wave takes
+    more than 64 steps (the kept totals flushed and the argmax keys carried
+    across flushes) and ends in a triple of one row (the rows past the matrix
+    read as zeros and are never stored): scores and the greedy index equal
+    the fused kernel's bit for bit, and sampled rows (every flush boundary,
+    the last triple) the oracle's within 1e-5 of their scale."""
+    n = 2560
+    vocab = 2048 * 3 * 65 + 1          # 65 steps for every wave, then one row
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(7321)
+    wd = synth.torch_weights_bulk(14, vocab, n, gen, "cuda:0")
+    hd = torch.randn((1, n), generator=gen, device="cuda:0")
+    bd = torch.randn((vocab,), generator=gen, device="cuda:0") * 0.01
+    f, s = both(hipdev, lambda: E.logits(wd, 14, hd, vocab, n, bias=bd))
+    assert np.array_equal(bits(f[0]), bits(s[0]))
+    assert np.array_equal(f[1], s[1])
+    assert int(s[1][0]) == int(np.argmax(s[0][0]))
+    edge = 2048 * 3 * 64
+    rows = np.unique(np.concatenate([np.arange(12), np.arange(edge - 6, edge + 6), np.arange(vocab - 8, vocab),
+                                     np.random.default_rng(5).integers(0, vocab, 64)]))
+    w = wd[torch.from_numpy(rows).to("cuda:0")].cpu().numpy()
+    h = hd.cpu().numpy()[0]
+    b = bd.cpu().numpy()[rows]
+    want, _ = ora.logits(h, w, 14, b, len(rows), n, 0)
+    S = f32_scales(14, w, h) + np.abs(b)
+    assert np.all(np.abs(s[0][0][rows] - want) <= TOL * S)
+
+
 @pytest.mark.parametrize("qt,n,off", [(12, 4096, 8), (12, 4096, 4), (14, 2560, 2), (14, 2560, 6)])
 @pytest.mark.parametrize("m", [1, 2])
 def test_logits_at_unaligned_weights_take_the_fused_kernel(hipdev, qt, n, off, m):
