@@ -98,10 +98,13 @@ constexpr int kPackF32Tokens = 4;  // tokens per wavefront of the f32 pack
 // its elements 64 j + 8 q .. + 7 and 64 j + 32 + 8 q .. + 7: the code vectors
 // of K-steps 2 q and 2 q + 1 of half j & 1, lane half j >> 1, with no
 // exchange.  The Q8_K quantization (src/gguf_dot_q8.c:360-412) runs over a
-// 16-lane row: the largest |x| (zeros and NaN never enter) by a row max, the
-// sign of its first element by a row min over (index, sign) keys, then
-// iscale = -127 / max and each code as quantize_q8_k_kernel forms it, so
-// every code, d, bsum and sum |q| is that kernel's.
+// 16-lane row: the largest |x| (zeros and NaN never enter) by a row max,
+// then iscale = -127 / max|x| and each code as quantize_q8_k_kernel forms
+// it.  The reference's max carries the sign of the first element of largest
+// |x|; where that is negative, this block is the reference's with codes,
+// bsums and d negated, which every product of the GEMM, dx * (C d - mn dmin)
+// with C and mn integer sums of the codes, leaves word for word (sum |q| is
+// the same either way).
 __global__ __launch_bounds__(kPackThreads) void q8k_pack_f32_kernel(const float *__restrict__ x, int ldx, int m,
                                                                     int K, int ntb, uint8_t *__restrict__ pack) {
     const int nb = K / kQKK;
@@ -136,20 +139,8 @@ __global__ __launch_bounds__(kPackThreads) void q8k_pack_f32_kernel(const float 
         amax_bits = max(amax_bits, bb[i]);
     }
     amax_bits = row16_max_u32(amax_bits);
-    // the lane's first element holding the maximum (its elements ascend with
-    // i), as the key 2 * index + sign; the row's smallest key is the block's
-    uint32_t key = 0xffffffffu;
-    const uint32_t base = 2u * (uint32_t)(64 * j + 8 * q);
-#pragma unroll
-    for (int i = 15; i >= 0; --i) {
-        const uint32_t off = 2u * (uint32_t)(i < 8 ? i : 24 + i);
-        key = bb[i] == amax_bits ? base + off + (xs[i] < 0.0f ? 1u : 0u) : key;
-    }
-    key = row16_min(key);
     const bool zero = amax_bits == 0u;
-    const float amax = __uint_as_float(amax_bits);
-    const float maxv = (key & 1u) != 0u ? -amax : amax;
-    const float iscale = -127.0f / maxv;
+    const float iscale = -127.0f / __uint_as_float(amax_bits);
     int qv[16], lo8 = 0, hi8 = 0, sq = 0;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {

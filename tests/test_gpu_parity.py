@@ -663,8 +663,9 @@ def test_prefill_gemm_two_chains(hipdev, ora):
 def test_prefill_pack_special_blocks(hipdev, ora, qt):
     """The f32 activation pack of the K-quant prefill GEMMs (four tokens per
     wavefront) quantizes as the reference's quantize_row_q8_K does
-    (src/gguf_dot_q8.c:360-412): the GEMM over it equals, bit for bit, the
-    GEMM over the oracle's Q8_K bytes of the same activations.  Blocks: all
+    (src/gguf_dot_q8.c:360-412) up to the sign of a block's codes and scale,
+    which cancels in the GEMM: the GEMM over it equals, bit for bit, the GEMM
+    over the oracle's Q8_K bytes of the same activations.  Blocks: all
     zero, the largest magnitude twice with opposite signs (negative first,
     positive first, in one lane and in lanes far apart), NaN elements, -0.0
     and subnormals, codes at exact .5 ties, a block whose maximum is its last
